@@ -1,0 +1,183 @@
+/*
+ * latchmoe.h — C ABI of liblatchmoe_hip.so, the MI355X (gfx950) kernels of
+ * the slot-indexed fused-MoE hot path.
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers, sizes and a
+ * hipStream_t, never throws, allocates nothing, and returns an int status:
+ *   0                      success
+ *   1 .. 999               a hipError_t from the launch or copy
+ *   LMOE_ERR_* (>= 1000)   an argument error detected on the host before any
+ *                          device work was queued
+ * lmoe_status_string() names a status.  All launches are asynchronous on the
+ * given stream and are legal inside hipStreamBeginCapture/EndCapture (no
+ * allocation, no host synchronisation, no memset node).
+ *
+ * Tensor conventions (row-major, element types in brackets):
+ *   x         [T, H]        bf16   hidden states (T tokens)
+ *   logits    [T, E]        bf16 or f32
+ *   ids       [T, k]        i32    logical expert ids, flat pair p = t*k + j
+ *   w13_slots [P, 2I, H]    bf16   slot bank, rows 0..I-1 gate, I..2I-1 up
+ *   w2_slots  [P, H, I]     bf16   slot bank, down projection
+ *   log2phy   [E_total]     i32    logical expert -> physical slot, -1 = none
+ *
+ * Reference interfaces replaced (paths relative to the LatchMoE repository):
+ *   lmoe_router_gate   gate(hidden) in ops/fused_moe/moe_router_op.py:228-231
+ *   lmoe_router_topk   select_experts (moe_router_op.py:108-124) with the
+ *                      renorm contract of patches/patch_fused_moe.py:597-632
+ *   lmoe_permute       log2phy remap moe_offload/slot_mapping.py:116-140 and
+ *                      npu_moe_init_routing_v2, patch_fused_moe.py:668-701
+ *                      (stable sort by slot, expanded_row_idx, count histogram)
+ *   lmoe_gather_rows   expanded_x output of the same init-routing call
+ *   lmoe_grouped_mlp   npu_grouped_matmul x2 + npu_swiglu (_apply_mlp,
+ *                      patch_fused_moe.py:3772-3774, hooks :4249-4302)
+ *   lmoe_combine       npu_moe_token_unpermute, patch_fused_moe.py:3363-3366,
+ *                      and the single native combine of :3342-3379
+ *   lmoe_fused_moe_decode  GMM1+swiglu+GMM2+unpermute of the decode
+ *                      fused_experts call (patch_fused_moe.py:3946-4009)
+ *   lmoe_stage_copy    TransferEngine.load_many_async H2D batch + ready event,
+ *                      moe_offload/transfer_engine.py:139-187, 205-228
+ */
+#ifndef LATCHMOE_H
+#define LATCHMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LMOE_ABI_VERSION 1
+
+enum {
+  LMOE_OK = 0,
+  LMOE_ERR_ARG = 1000,         /* null pointer or negative size */
+  LMOE_ERR_SHAPE = 1001,       /* a dimension the kernels do not support */
+  LMOE_ERR_WORKSPACE = 1002,   /* workspace smaller than required */
+  LMOE_ERR_UNSUPPORTED = 1003  /* an option combination with no kernel */
+};
+
+/* Scoring functions of lmoe_router_topk. */
+enum { LMOE_SCORING_SOFTMAX = 0, LMOE_SCORING_SIGMOID = 1 };
+
+/* Kernel-path selectors of lmoe_grouped_mlp. */
+enum { LMOE_PATH_AUTO = 0, LMOE_PATH_GEMV = 1, LMOE_PATH_MFMA = 2 };
+
+/* Slots of the meta[] output of lmoe_permute. */
+enum {
+  LMOE_META_ACTIVE = 0,  /* number of slots with at least one pair          */
+  LMOE_META_PAIRS = 1,   /* number of pairs placed in the sorted order      */
+  LMOE_META_ERRORS = 2,  /* pairs dropped because their id did not map      */
+  LMOE_META_TILES = 3,   /* sum over slots of ceil(count / block_m)         */
+  LMOE_META_COUNT = 4
+};
+
+const char* lmoe_status_string(int status);
+int lmoe_abi_version(void);
+
+/* Gate linear: logits[t][e] = sum_h x[t][h] * wg[e][h], f32 accumulation,
+ * stored as bf16 (round to nearest even) or f32.  Replaces the gate matmul of
+ * moe_router_op.py:228-231. */
+int lmoe_router_gate(const void* x, const void* wg, int T, int H, int E,
+                     void* logits, int logits_f32, hipStream_t stream);
+
+/* Expert selection.  scoring = LMOE_SCORING_SOFTMAX: f32 softmax over E, the
+ * k largest probabilities.  scoring = LMOE_SCORING_SIGMOID: s = sigmoid(l),
+ * selection score s + bias (bias may be NULL), n_group contiguous groups
+ * ranked by the sum of their two largest selection scores, the topk_group best
+ * groups kept, k largest selection scores inside the kept groups, weights = s.
+ * Ties break toward the lower expert (or group) id.  Output order is the
+ * selection order (descending score).  If renorm, w /= max(sum(w), FLT_EPSILON)
+ * (sum in selection order); then w *= routed_scale.  w_f32 may be NULL.
+ * E <= 512, k <= 16, n_group <= 64.  Replaces select_experts
+ * (moe_router_op.py:108-124, patch_fused_moe.py:597-632). */
+int lmoe_router_topk(const void* logits, int logits_f32, int T, int E, int k,
+                     int scoring, const float* bias, int n_group,
+                     int topk_group, int renorm, float routed_scale,
+                     float* w_f32, uint16_t* w_bf16, int32_t* ids,
+                     hipStream_t stream);
+
+/* Bytes of device workspace lmoe_permute needs for n_pairs pairs, n_slots. */
+size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);
+
+/* Slot remap, count histogram and stable counting sort of the flat pairs.
+ * slot(p) = log2phy ? log2phy[ids[p]] : ids[p].  A pair whose id is outside
+ * [0, n_log2phy) or whose slot is outside [0, n_slots) is left out of the
+ * sorted order; it is counted in meta[LMOE_META_ERRORS] unless skip_unmapped
+ * is set and the slot is -1 or the id lies outside the table (a pair of
+ * another wave).
+ * Outputs: counts[s]; offsets[s] = exclusive prefix of counts (offsets[P] =
+ * placed pairs); sorted_pairs[offsets[s] + r] = the r-th pair of slot s in
+ * flat order; row_idx[p] = sorted position of pair p or -1; active[a] = a-th
+ * slot with count > 0 (ascending); tile_off[s] = sum over s' < s of
+ * ceil(counts[s'] / block_m); meta[LMOE_META_COUNT].
+ * Replaces slot_mapping.py:116-140 + npu_moe_init_routing_v2
+ * (patch_fused_moe.py:668-701: expert_capacity=-1, drop_pad_mode=0,
+ * expert_tokens_num_type=1). */
+int lmoe_permute(const int32_t* ids, int n_pairs, const int32_t* log2phy,
+                 int n_log2phy, int n_slots, int skip_unmapped, int block_m,
+                 int32_t* counts, int32_t* offsets, int32_t* sorted_pairs,
+                 int32_t* row_idx, int32_t* active, int32_t* tile_off,
+                 int32_t* meta, void* workspace, size_t workspace_bytes,
+                 hipStream_t stream);
+
+/* expanded_x: x_sorted[pos] = x[sorted_pairs[pos] / k] for pos < n_pairs
+ * (positions past meta[LMOE_META_PAIRS] are left untouched). */
+int lmoe_gather_rows(const void* x, int H, int k, const int32_t* sorted_pairs,
+                     const int32_t* meta, int n_pairs, void* x_sorted,
+                     hipStream_t stream);
+
+/* Grouped SwiGLU MLP over the permuted pairs, reading weights only through
+ * the slot bank.  For each placed pair p in slot s (token t = p / k):
+ *   act[pos]  = silu(W13_s[0:I] x_t) * (W13_s[I:2I] x_t)    bf16, f32 math
+ *   y[p]      = W2_s act[pos]                                 bf16, f32 acc.
+ * act is a [n_pairs, I] bf16 workspace in sorted order; y is [T*k, H] bf16
+ * indexed by flat pair (rows of unplaced pairs are left untouched).
+ * path = LMOE_PATH_GEMV (weight-streaming, small slot groups),
+ * LMOE_PATH_MFMA (bf16 MFMA tiles, block_m must equal the block_m given to
+ * lmoe_permute) or LMOE_PATH_AUTO.  H % 8 == 0, I % 64 == 0. */
+int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
+                     const void* w13_slots, const void* w2_slots, int n_slots,
+                     const int32_t* offsets, const int32_t* sorted_pairs,
+                     const int32_t* active, const int32_t* tile_off,
+                     const int32_t* meta, int n_pairs, int block_m, int path,
+                     void* act, void* y, hipStream_t stream);
+
+/* Weighted combine: out[t] = sum_{j<k} w[t][j] * y[t*k+j], f32 accumulation
+ * in j order, one rounding to bf16.  y is [T*k, H] bf16 indexed by flat pair
+ * (as lmoe_grouped_mlp writes it, over one or several waves); row_idx (may be
+ * NULL) masks pairs: a pair with row_idx[p] < 0 contributes nothing.  add (may be NULL) is a
+ * [T, H] bf16 term added before rounding (resident shared expert).  Replaces
+ * npu_moe_token_unpermute (patch_fused_moe.py:3363-3366, semantics
+ * phase_split.py:1649-1656) and the single native combine (:3342-3379). */
+int lmoe_combine(const void* y, const int32_t* row_idx, const uint16_t* w,
+                 int T, int k, int H, const void* add, void* out,
+                 hipStream_t stream);
+
+/* Decode MoE for small pair counts: gate_up GEMV + SiLU*mul into act (sorted
+ * order), then down GEMV fused with the weighted combine:
+ *   out[t] = (add ? add[t] : 0) + sum_j w[t][j] * W2_s(t,j) act[pos(t,j)].
+ * Needs T*k <= 1024.  Permutation arrays as produced by lmoe_permute. */
+int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
+                          const void* w13_slots, const void* w2_slots,
+                          int n_slots, const uint16_t* w,
+                          const int32_t* offsets, const int32_t* sorted_pairs,
+                          const int32_t* row_idx, const int32_t* active,
+                          const int32_t* meta, const void* add, void* act,
+                          void* out, hipStream_t stream);
+
+/* Batched host->device (or device->device) expert copies on a transfer
+ * stream: optionally wait on wait_event, then for i < n copy bytes[i] from
+ * src[i] to dst[i] with hipMemcpyAsync, then record done_event (may be NULL).
+ * Replaces TransferEngine.load_many_async (transfer_engine.py:139-187) with
+ * the contiguous-run batching of :205-228 done by the caller. */
+int lmoe_stage_copy(void* const* dst, const void* const* src,
+                    const size_t* bytes, int n, hipStream_t transfer_stream,
+                    hipEvent_t wait_event, hipEvent_t done_event);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LATCHMOE_H */

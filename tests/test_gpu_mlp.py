@@ -1,0 +1,171 @@
+"""GPU parity of the grouped expert MLP and combine against the oracle.
+
+Tolerance (floating point): max-abs error <= 2e-2 x RMS of the oracle output,
+the bf16 bar of the tier; kernels accumulate in f32.  Integer side outputs are
+exact.  Wave splitting followed by one combine is checked bit for bit against
+the single-pass layer on the GPU itself.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mlp as omlp
+from oracle import permute as operm
+from oracle.bf16 import bf16_to_f32, normal_bf16
+from tests._util import OUT_TOL, from_dev_bf16, rel_max_err, to_dev_bf16, to_dev_i32, ulp_mismatch_stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _native():
+    from vllm_moe_offload_amd import native
+
+    return native
+
+
+def _case(seed, T, k, E, P, H, I, *, mapped=True):
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    used = np.unique(ids)
+    if mapped:
+        if used.size > P:
+            raise ValueError("test case needs more slots")
+        log2phy = np.full(E, -1, dtype=np.int32)
+        log2phy[used] = rng.permutation(P)[: used.size]
+    else:
+        log2phy = None
+    x = normal_bf16(rng, (T, H), 1.0)
+    w13 = normal_bf16(rng, (P, 2 * I, H), 0.02)
+    w2 = normal_bf16(rng, (P, H, I), 0.02)
+    wts = rng.random((T, k)).astype(np.float32)
+    wts = (wts / wts.sum(axis=1, keepdims=True)).astype(np.float32)
+    from oracle.bf16 import f32_to_bf16
+
+    return ids, log2phy, x, w13, w2, f32_to_bf16(wts)
+
+
+def _dev(ids, log2phy, x, w13, w2, wb):
+    return (to_dev_i32(ids), None if log2phy is None else to_dev_i32(log2phy), to_dev_bf16(x),
+            to_dev_bf16(w13), to_dev_bf16(w2), to_dev_bf16(wb))
+
+
+@pytest.mark.parametrize("T,k,E,P,H,I", [
+    (1, 8, 128, 16, 2048, 768),
+    (4, 8, 128, 32, 2048, 768),
+    (16, 8, 64, 64, 1024, 256),
+    (3, 2, 16, 16, 512, 128),
+    (1, 8, 256, 8, 7168, 2048),
+])
+def test_fused_decode_matches_oracle(T, k, E, P, H, I):
+    native = _native()
+    print(f"case fused-decode T={T} k={k} E={E} P={P} H={H} I={I}", flush=True)
+    ids, l2p, x, w13, w2, wb = _case(T * 100 + H, T, k, E, P, H, I)
+    d_ids, d_l2p, d_x, d_w13, d_w2, d_w = _dev(ids, l2p, x, w13, w2, wb)
+    perm = native.Permutation.allocate(T * k, P, "cuda")
+    native.permute(d_ids, perm, log2phy=d_l2p)
+    act = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    native.fused_moe_decode(d_x, d_w, d_w13, d_w2, perm, act, out)
+    torch.cuda.synchronize()
+    ref = omlp.moe_layer(x, ids, wb, l2p, w13, w2)
+    err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
+    print(f"  rel max err {err:.3e}", flush=True)
+    assert err <= OUT_TOL
+
+
+@pytest.mark.parametrize("path", ["gemv", "mfma"])
+@pytest.mark.parametrize("T,k,E,P,H,I", [
+    (8, 8, 128, 64, 2048, 768),
+    (96, 4, 32, 32, 1024, 512),
+    (600, 8, 64, 64, 2048, 768),
+])
+def test_grouped_mlp_and_combine_match_oracle(path, T, k, E, P, H, I):
+    native = _native()
+    if path == "gemv" and T * k > 1024:
+        pytest.skip("gemv path case list kept small")
+    print(f"case grouped-mlp {path} T={T} k={k} E={E} P={P} H={H} I={I}", flush=True)
+    ids, l2p, x, w13, w2, wb = _case(T + 7 * H + k, T, k, E, P, H, I)
+    d_ids, d_l2p, d_x, d_w13, d_w2, d_w = _dev(ids, l2p, x, w13, w2, wb)
+    perm = native.Permutation.allocate(T * k, P, "cuda")
+    native.permute(d_ids, perm, log2phy=d_l2p)
+    act = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((T * k, H), dtype=torch.bfloat16, device="cuda")
+    p = native.LMOE_PATH_GEMV if path == "gemv" else native.LMOE_PATH_MFMA
+    native.grouped_mlp(d_x, k, d_w13, d_w2, perm, act, y, path=p)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    native.combine(y, d_w, out)
+    torch.cuda.synchronize()
+    slot = operm.remap(ids, l2p, P)
+    y_ref = omlp.grouped_mlp(x, slot, k, w13, w2)
+    # y (GMM2 output, bf16 on both sides): accumulation-order noise flips the
+    # bf16 rounding of a few elements by one ulp; near-zero elements (sums
+    # that cancel) carry absolute noise, bounded by 2^-8 RMS(y)
+    rms_y = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
+    frac, max_ulps = ulp_mismatch_stats(bf16_to_f32(from_dev_bf16(y)), y_ref, abs_floor=rms_y / 256)
+    out_ref = omlp.combine(y_ref, wb, round_output=False)
+    err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), out_ref)
+    print(f"  y: frac>1ulp {frac:.2e} max {max_ulps:.2f} ulp; out rel max err {err:.3e}", flush=True)
+    assert frac <= 1e-3 and max_ulps <= 2.0
+    assert err <= OUT_TOL
+
+
+def test_wave_split_is_bitwise_equal_to_single_pass():
+    """Pairs split over waves (each its own slot numbering) then one combine."""
+    native = _native()
+    T, k, E, H, I = 64, 8, 64, 1024, 256
+    rng = np.random.default_rng(123)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    x = normal_bf16(rng, (T, H), 1.0)
+    w13_all = normal_bf16(rng, (E, 2 * I, H), 0.02)
+    w2_all = normal_bf16(rng, (E, H, I), 0.02)
+    wts = rng.random((T, k)).astype(np.float32)
+    from oracle.bf16 import f32_to_bf16
+
+    wb = f32_to_bf16(wts / wts.sum(1, keepdims=True))
+    d_ids, d_x, d_w = to_dev_i32(ids), to_dev_bf16(x), to_dev_bf16(wb)
+    for path in (native.LMOE_PATH_GEMV, native.LMOE_PATH_MFMA):
+        # single pass, identity log2phy over E slots
+        perm = native.Permutation.allocate(T * k, E, "cuda")
+        native.permute(d_ids, perm)
+        act = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
+        y1 = torch.zeros((T * k, H), dtype=torch.bfloat16, device="cuda")
+        native.grouped_mlp(d_x, k, to_dev_bf16(w13_all), to_dev_bf16(w2_all), perm, act, y1, path=path)
+        out1 = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        native.combine(y1, d_w, out1)
+        # three waves of <= 24 experts staged into a 24-slot stage bank
+        waves = [np.arange(0, 24), np.arange(24, 48), np.arange(48, 64)]
+        S = 24
+        y2 = torch.zeros((T * k, H), dtype=torch.bfloat16, device="cuda")
+        for wv in waves:
+            l2p = np.full(E, -1, dtype=np.int32)
+            l2p[wv] = np.arange(wv.size)
+            w13_stage = np.zeros((S, 2 * I, H), dtype=np.uint16)
+            w2_stage = np.zeros((S, H, I), dtype=np.uint16)
+            w13_stage[: wv.size] = w13_all[wv]
+            w2_stage[: wv.size] = w2_all[wv]
+            pw = native.Permutation.allocate(T * k, S, "cuda")
+            native.permute(d_ids, pw, log2phy=to_dev_i32(l2p), skip_unmapped=True)
+            native.grouped_mlp(d_x, k, to_dev_bf16(w13_stage), to_dev_bf16(w2_stage), pw, act, y2, path=path)
+        out2 = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        native.combine(y2, d_w, out2)
+        torch.cuda.synchronize()
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+        assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+
+
+def test_combine_masks_unplaced_pairs_and_adds_shared():
+    native = _native()
+    rng = np.random.default_rng(4)
+    T, k, H = 5, 3, 64
+    y = normal_bf16(rng, (T * k, H), 1.0)
+    from oracle.bf16 import f32_to_bf16
+
+    wb = f32_to_bf16(rng.random((T, k)).astype(np.float32))
+    add = normal_bf16(rng, (T, H), 1.0)
+    mask = np.array([0, -1, 2, 3, 4, 5, -1, -1, 8, 9, 10, 11, 12, 13, -1], dtype=np.int32)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    native.combine(to_dev_bf16(y), to_dev_bf16(wb), out, row_mask=to_dev_i32(mask), add=to_dev_bf16(add))
+    torch.cuda.synchronize()
+    ref = omlp.combine(bf16_to_f32(y), wb, mask=mask, add=bf16_to_f32(add))
+    assert rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref) <= 1e-2

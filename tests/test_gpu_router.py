@@ -1,0 +1,131 @@
+"""GPU parity of the router kernels against the oracle.
+
+Selection (ids) and weights (bf16 and f32) are bit-exact against
+oracle.router on the same logits tensor; the gate GEMV/GEMM is within one
+bf16 ulp of the exact product (its f32 accumulation order differs).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import router as orc
+from oracle.bf16 import bf16_to_f32, f32_to_bf16, normal_bf16
+from tests._util import bf16_ulp, from_dev_bf16, to_dev_bf16, ulp_mismatch_stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _native():
+    from vllm_moe_offload_amd import native
+
+    return native
+
+
+def _tied_logits(rng, T, E, step=0.25):
+    """bf16 logits on a coarse grid so equal values (ties) are common."""
+    v = np.round(rng.standard_normal((T, E)) / step) * step
+    return f32_to_bf16(v.astype(np.float32))
+
+
+@pytest.mark.parametrize("T,E,k,dtype", [
+    (1, 128, 8, "bf16"),
+    (16, 128, 8, "bf16"),
+    (257, 128, 8, "bf16"),
+    (64, 60, 4, "bf16"),
+    (33, 256, 8, "f32"),
+    (8, 512, 16, "bf16"),
+    (5, 8, 2, "f32"),
+])
+def test_softmax_topk_bit_exact(T, E, k, dtype):
+    native = _native()
+    print(f"case softmax T={T} E={E} k={k} {dtype}", flush=True)
+    rng = np.random.default_rng(1000 + T * 7 + E)
+    bits = _tied_logits(rng, T, E)
+    lg32 = bf16_to_f32(bits)
+    if dtype == "bf16":
+        dev = to_dev_bf16(bits)
+    else:
+        lg32 = (lg32 + rng.standard_normal(lg32.shape).astype(np.float32) * 1e-3).astype(np.float32)
+        dev = torch.from_numpy(lg32).cuda()
+    w_f32 = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    w, ids, _ = native.router_topk(dev, k, w_f32=w_f32)
+    torch.cuda.synchronize()
+    r_ids, r_w, r_wb = orc.softmax_topk(lg32, k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
+    np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
+    np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
+
+
+def test_softmax_ties_break_to_lower_id():
+    native = _native()
+    T, E, k = 4, 128, 8
+    lg = np.zeros((T, E), dtype=np.float32)
+    lg[1, [100, 3, 77, 5]] = 1.0          # 4 tied winners, then 124 tied zeros
+    lg[2, ::2] = 0.5                      # every even expert tied
+    lg[3] = -np.arange(E, dtype=np.float32) * 0  # all equal
+    dev = to_dev_bf16(f32_to_bf16(lg))
+    _, ids, _ = native.router_topk(dev, k)
+    got = ids.cpu().numpy()
+    np.testing.assert_array_equal(got[0], np.arange(8))
+    np.testing.assert_array_equal(got[1], [3, 5, 77, 100, 0, 1, 2, 4])
+    np.testing.assert_array_equal(got[2], [0, 2, 4, 6, 8, 10, 12, 14])
+    np.testing.assert_array_equal(got[3], np.arange(8))
+
+
+@pytest.mark.parametrize("T,E,G,TG,k,scale", [
+    (1, 256, 8, 4, 8, 2.5),
+    (32, 256, 8, 4, 8, 2.5),
+    (2048, 256, 8, 4, 8, 2.5),
+    (7, 64, 4, 2, 6, 1.0),
+    (9, 160, 1, 1, 8, 1.0),
+])
+def test_grouped_sigmoid_bit_exact(T, E, G, TG, k, scale):
+    native = _native()
+    print(f"case sigmoid T={T} E={E} G={G}", flush=True)
+    rng = np.random.default_rng(77 + T)
+    bits = _tied_logits(rng, T, E, step=0.125)
+    lg32 = bf16_to_f32(bits)
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    w_f32 = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    w, ids, _ = native.router_topk(
+        to_dev_bf16(bits), k, scoring="sigmoid", bias=torch.from_numpy(bias).cuda(),
+        num_expert_group=G, topk_group=TG, renormalize=True, routed_scaling_factor=scale, w_f32=w_f32,
+    )
+    torch.cuda.synchronize()
+    r_ids, r_w, r_wb = orc.grouped_sigmoid_topk(lg32, k, bias=bias, n_group=G, topk_group=TG, scale=scale)
+    np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
+    np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
+    np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
+
+
+@pytest.mark.parametrize("T,H,E", [(1, 2048, 128), (16, 2048, 128), (64, 7168, 256), (300, 2048, 128), (1000, 7168, 256)])
+def test_gate_within_one_bf16_ulp(T, H, E):
+    native = _native()
+    print(f"case gate T={T} H={H} E={E}", flush=True)
+    rng = np.random.default_rng(5 + T)
+    x = normal_bf16(rng, (T, H), 1.0)
+    wg = normal_bf16(rng, (E, H), 0.02)
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device="cuda")
+    native.router_gate(to_dev_bf16(x), to_dev_bf16(wg), logits)
+    torch.cuda.synchronize()
+    got = bf16_to_f32(from_dev_bf16(logits))
+    ref = orc.gate_logits(x, wg)
+    # bound: one bf16 ulp of rounding plus the f32 accumulation error of a
+    # K-term sum, |err| <= 4 sqrt(K) 2^-24 sum_h |x_h w_h| (cancellation aware)
+    absdot = np.abs(bf16_to_f32(x)).astype(np.float64) @ np.abs(bf16_to_f32(wg)).astype(np.float64).T
+    bound = bf16_ulp(ref) + 4.0 * np.sqrt(H) * 2.0 ** -24 * absdot
+    assert np.all(np.abs(got - ref) <= bound)
+    frac, _ = ulp_mismatch_stats(got, ref)
+    assert frac < 1e-3
+
+
+def test_gate_f32_output():
+    native = _native()
+    rng = np.random.default_rng(9)
+    x = normal_bf16(rng, (4, 2048), 1.0)
+    wg = normal_bf16(rng, (128, 2048), 0.02)
+    logits = torch.empty((4, 128), dtype=torch.float32, device="cuda")
+    native.router_gate(to_dev_bf16(x), to_dev_bf16(wg), logits)
+    exact = orc.gate_logits(x, wg, out_f32=True)
+    np.testing.assert_allclose(logits.cpu().numpy(), exact, rtol=1e-5, atol=1e-5)

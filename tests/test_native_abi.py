@@ -1,0 +1,57 @@
+"""The C-ABI library loads on the CPU host and exports exactly what
+include/latchmoe.h declares; host-side argument checks fail before any
+device work (no GPU needed)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "latchmoe.h").read_text()
+    return sorted(set(re.findall(r"\b(lmoe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    from vllm_moe_offload_amd import native
+
+    assert sorted(native.EXPORTED_SYMBOLS) == _declared()
+
+
+def test_library_exports_every_declared_symbol():
+    from vllm_moe_offload_amd import native
+
+    lib = native.load_library()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.lmoe_abi_version() == 1
+    assert lib.lmoe_status_string(1001) == b"unsupported shape"
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    from vllm_moe_offload_amd import native
+
+    lib = native.load_library()
+    # null outputs / bad sizes are rejected on the host
+    assert lib.lmoe_router_topk(None, 0, 1, 128, 8, 0, None, 1, 1, 1, 1.0, None, None, None, None) == 1000
+    assert lib.lmoe_router_topk(ctypes.c_void_p(16), 0, 1, 1024, 8, 0, None, 1, 1, 1, 1.0, None,
+                                ctypes.c_void_p(16), ctypes.c_void_p(16), None) == 1001
+    assert lib.lmoe_permute(None, 4, None, 0, 0, 0, 128, *([None] * 7), None, 0, None) == 1000
+    assert lib.lmoe_grouped_mlp(*([ctypes.c_void_p(16)] * 1), 1, 2048, 100, 8, *([ctypes.c_void_p(16)] * 2), 4,
+                                *([ctypes.c_void_p(16)] * 5), 8, 128, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == 1001
+    assert lib.lmoe_permute_workspace_bytes(1024, 64) == 0
+    assert lib.lmoe_permute_workspace_bytes(32768, 48) > 0
+    assert lib.lmoe_stage_copy(None, None, None, 0, None, None, None) == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from vllm_moe_offload_amd import native
+
+    monkeypatch.setattr(native, "_LIB", None)
+    monkeypatch.setenv("LATCHMOE_HIP_LIB", str(tmp_path / "absent.so"))
+    with pytest.raises(native.NativeLibraryMissing, match="no CPU or PyTorch fallback"):
+        native.load_library()

@@ -1,0 +1,363 @@
+"""Slot-indexed fused-MoE execution on the gfx950 kernels.
+
+fused_experts() is the body of the reference's fused-experts call with the
+slot bank in place of the expert weights: lmoe_permute remaps the top-k ids
+through log2phy and sorts the pairs by slot, then either
+
+  * lmoe_fused_moe_decode (<= 1024 pairs): gate_up GEMV + SiLU*mul, then the
+    down GEMV fused with the weighted combine — 3 kernels per layer; or
+  * lmoe_grouped_mlp (GEMV or bf16 MFMA) into a flat-pair buffer y, then
+    lmoe_combine.
+
+Every buffer comes from a shape-keyed workspace cache, so repeated calls (and
+hipGraph replays) see the same addresses and allocate nothing.
+
+run_wave_prefill() executes an active expert union larger than the slot
+capacity as canonical waves staged through the runtime's double-buffered
+stage banks, and finishes with ONE combine over the original top-k weights
+(the result is identical, bit for bit, to the unsplit layer).
+run_full_layer() is the blocking reference fallback.
+
+Reference: patches/patch_fused_moe.py — fused_experts hook :3946-4009,
+_maybe_apply_moe_offload_plan :2101-2128, _with_prepared_slot_weights
+:2039-2099, _run_b2_wave_prefill :2443-3470 (one native combine :3342-3379),
+_run_b2_full_layer_reference :3472-3650; MoEFusedExpertsInput fields
+:2051-2099 and result fields :3462-3470.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from time import perf_counter
+
+import torch
+
+from vllm_moe_offload_amd import native
+from vllm_moe_offload_amd.moe_offload import phase_split
+from vllm_moe_offload_amd.moe_offload.runtime import MoeOffloadRuntime
+from vllm_moe_offload_amd.moe_offload.slot_mapping import PreparedSlotWeights
+
+
+# ---------------------------------------------------------------------------
+# workspaces (fixed addresses per shape)
+# ---------------------------------------------------------------------------
+@dataclass
+class MoEWorkspace:
+    perm: native.Permutation
+    act: torch.Tensor   # [N, I] bf16, sorted order
+    y: torch.Tensor     # [N, H] bf16, flat pair order
+    out: torch.Tensor   # [T, H] bf16
+
+
+_WORKSPACES: dict[tuple, MoEWorkspace] = {}
+
+
+def get_workspace(T: int, k: int, P: int, H: int, I: int, device, *, tag: str = "") -> MoEWorkspace:
+    key = (int(T), int(k), int(P), int(H), int(I), str(device), tag)
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        N = T * k
+        ws = MoEWorkspace(
+            perm=native.Permutation.allocate(N, P, device),
+            act=torch.empty((max(N, 1), I), dtype=torch.bfloat16, device=device),
+            y=torch.empty((max(N, 1), H), dtype=torch.bfloat16, device=device),
+            out=torch.empty((max(T, 1), H), dtype=torch.bfloat16, device=device),
+        )
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def clear_workspaces() -> None:
+    _WORKSPACES.clear()
+
+
+# ---------------------------------------------------------------------------
+# router
+# ---------------------------------------------------------------------------
+@dataclass
+class RouterSpec:
+    """Routing scalars of one MoE layer (moe_router_op.py:72-86 arguments)."""
+
+    top_k: int
+    scoring_func: str = "softmax"
+    renormalize: bool = True
+    use_grouped_topk: bool = False
+    num_expert_group: int = 1
+    topk_group: int = 1
+    routed_scaling_factor: float = 1.0
+    e_score_correction_bias: torch.Tensor | None = None
+
+
+def route(hidden: torch.Tensor, gate_weight: torch.Tensor | None, spec: RouterSpec, *,
+          router_logits: torch.Tensor | None = None, logits_out: torch.Tensor | None = None,
+          w_out: torch.Tensor | None = None, ids_out: torch.Tensor | None = None):
+    """Gate (if gate_weight is given) then expert selection on the GPU.
+    Returns (topk_weights bf16 [T,k], topk_ids int32 [T,k], logits)."""
+    if gate_weight is not None:
+        T = hidden.shape[0]
+        E = gate_weight.shape[0]
+        if logits_out is None:
+            logits_out = torch.empty((T, E), dtype=hidden.dtype, device=hidden.device)
+        router_logits = native.router_gate(hidden, gate_weight, logits_out)
+    if router_logits is None:
+        raise ValueError("route() needs router_logits or a gate weight")
+    grouped = bool(spec.use_grouped_topk)
+    w, ids, _ = native.router_topk(
+        router_logits, int(spec.top_k), scoring=spec.scoring_func,
+        bias=spec.e_score_correction_bias,
+        num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
+        topk_group=int(spec.topk_group or 1) if grouped else 1,
+        renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
+        w_bf16=w_out, ids=ids_out,
+    )
+    return w, ids, router_logits
+
+
+# ---------------------------------------------------------------------------
+# one pass over the slot bank
+# ---------------------------------------------------------------------------
+def fused_experts(
+    hidden: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    w13_slots: torch.Tensor,
+    w2_slots: torch.Tensor,
+    log2phy: torch.Tensor | None,
+    *,
+    add: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    path: int = native.LMOE_PATH_AUTO,
+    workspace: MoEWorkspace | None = None,
+) -> torch.Tensor:
+    """out[t] = add[t] + sum_j w[t,j] * MLP_{slot(ids[t,j])}(x_t)."""
+    T, H = hidden.shape
+    k = int(topk_ids.shape[1])
+    P = int(w13_slots.shape[0])
+    I = int(w13_slots.shape[1]) // 2
+    ws = workspace or get_workspace(T, k, P, H, I, hidden.device)
+    native.permute(topk_ids, ws.perm, log2phy=log2phy)
+    dst = out if out is not None else ws.out[:T]
+    if T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA:
+        native.fused_moe_decode(hidden, topk_weights, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add)
+    else:
+        native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
+        native.combine(ws.y[: T * k], topk_weights, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
+    return dst
+
+
+def check_placed(ws: MoEWorkspace) -> None:
+    """Host validation (synchronising): fail if a pair mapped to no slot."""
+    meta = ws.perm.meta.cpu().tolist()
+    if meta[native.META_ERRORS]:
+        raise RuntimeError(f"topk_ids contain experts without ready slots: {meta[native.META_ERRORS]} pairs")
+
+
+# ---------------------------------------------------------------------------
+# the fused-experts extension hook
+# ---------------------------------------------------------------------------
+@dataclass
+class MoEWeights:
+    w1: torch.Tensor
+    w2: torch.Tensor
+
+
+@dataclass
+class MoERoutingParams:
+    log2phy: torch.Tensor | None = None
+    physical_expert_count: int | None = None
+
+
+@dataclass
+class MoEOffloadParams:
+    enabled: bool = False
+    layer_id: int = -1
+    num_logical_experts: int = 0
+    expected_device_type: str = "cuda"
+
+
+@dataclass
+class MoEFusedExpertsInput:
+    hidden_states: torch.Tensor
+    topk_weights: torch.Tensor
+    topk_ids: torch.Tensor
+    weights: MoEWeights
+    routing: MoERoutingParams = field(default_factory=MoERoutingParams)
+    offload: MoEOffloadParams = field(default_factory=MoEOffloadParams)
+    shared_output: torch.Tensor | None = None
+
+
+@dataclass
+class FusedExpertsResult:
+    routed_out: torch.Tensor
+    group_list_type: int = 1
+    expert_tokens: torch.Tensor | None = None
+
+
+class MoECommMethod:
+    """World-size-1 fused-experts method over the slot bank."""
+
+    def __init__(self, runtime: MoeOffloadRuntime) -> None:
+        self.runtime = runtime
+        self._slot_compute_handle = None
+
+    def _with_prepared_slot_weights(self, inp: MoEFusedExpertsInput, prepared: PreparedSlotWeights) -> MoEFusedExpertsInput:
+        self._slot_compute_handle = self.runtime.begin_slot_compute(prepared)
+        return MoEFusedExpertsInput(
+            hidden_states=inp.hidden_states,
+            topk_weights=inp.topk_weights,
+            topk_ids=inp.topk_ids,
+            weights=MoEWeights(prepared.w1, prepared.w2),
+            routing=MoERoutingParams(prepared.log2phy, prepared.physical_expert_count),
+            offload=inp.offload,
+            shared_output=inp.shared_output,
+        )
+
+    def _maybe_apply_moe_offload_plan(self, inp: MoEFusedExpertsInput) -> MoEFusedExpertsInput:
+        if not inp.offload.enabled:
+            return inp
+        prepared = self.runtime.capture_safe_slot_weights(layer_id=int(inp.offload.layer_id))
+        if prepared is None:
+            raise RuntimeError(f"fixed-slot MoE layer {inp.offload.layer_id} is not registered")
+        prepared.validate_backend_ready(expected_device_type=inp.offload.expected_device_type)
+        return self._with_prepared_slot_weights(inp, prepared)
+
+    def fused_experts(self, inp: MoEFusedExpertsInput) -> FusedExpertsResult:
+        inp = self._maybe_apply_moe_offload_plan(inp)
+        try:
+            out = fused_experts(
+                inp.hidden_states, inp.topk_weights, inp.topk_ids, inp.weights.w1, inp.weights.w2,
+                inp.routing.log2phy, add=inp.shared_output,
+            )
+        finally:
+            self.runtime.end_slot_compute(self._slot_compute_handle)
+            self._slot_compute_handle = None
+        return FusedExpertsResult(routed_out=out)
+
+
+# ---------------------------------------------------------------------------
+# capacity-bounded waves with one combine
+# ---------------------------------------------------------------------------
+@dataclass
+class WaveRunReport:
+    waves: tuple[tuple[int, ...], ...]
+    compute_order: tuple[int, ...]
+    h2d_bytes: int = 0
+    d2d_bytes: int = 0
+    issue_log: list = field(default_factory=list)
+    seconds: float = 0.0
+
+
+def run_wave_prefill(
+    runtime: MoeOffloadRuntime,
+    *,
+    layer_id: int,
+    hidden: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    num_logical_experts: int,
+    add: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    token_counts_by_expert: dict[int, int] | None = None,
+    path: int = native.LMOE_PATH_AUTO,
+) -> tuple[torch.Tensor, WaveRunReport]:
+    """Overflow execution: plan waves, stage each into a stage buffer (or run
+    it from the main bank when all its experts are resident), compute every
+    wave's pairs into one flat-pair y, then ONE combine."""
+    t0 = perf_counter()
+    cfg = runtime.config
+    T, H = hidden.shape
+    k = int(topk_ids.shape[1])
+    bank = runtime.slot_bank(layer_id)
+    if bank is None:
+        raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
+    P = bank.physical_expert_count
+    I = int(bank.w13_slots.shape[1]) // 2
+    if token_counts_by_expert is None:
+        token_counts_by_expert = runtime.consume_prefill_route_stats(layer_id=layer_id, topk_ids=topk_ids)
+    if token_counts_by_expert is None:
+        token_counts_by_expert = phase_split.count_routed_tokens_by_expert(topk_ids)  # D2H
+    routed = runtime.routed_expert_count_for_layer(layer_id=layer_id, fallback=num_logical_experts)
+    counts = {e: c for e, c in token_counts_by_expert.items() if 0 <= e < routed}
+    plan = phase_split.plan_balanced_b2_waves(counts, int(cfg.num_slots))
+    if not plan.waves:
+        raise phase_split.B2WaveFallback("no routed pairs to execute")
+    readiness = runtime.slot_readiness_for_experts(layer_id=layer_id, expert_ids=tuple(counts))
+    per_expert = runtime.cached_layer_expert_weight_bytes(layer_id=layer_id)
+    h2d = {i: per_expert * sum(1 for e in w if not readiness.get(e, False)) for i, w in enumerate(plan.waves)}
+    cost = {i: float(plan.wave_tokens(w)) for i, w in enumerate(plan.waves)}
+    sched = phase_split.plan_b2_prefill_async_schedule(
+        plan.waves, slot_readiness=readiness,
+        prefetch_depth=cfg.effective_prefill_prefetch_depth, buffer_count=cfg.effective_prefill_buffer_count,
+        h2d_bytes_by_wave=h2d, compute_cost_by_wave=cost, transfer_aware=cfg.transfer_aware_wave_schedule,
+    )
+    ws = get_workspace(T, k, P, H, I, hidden.device, tag="waves")
+    report = WaveRunReport(plan.waves, sched.compute_order)
+    staged: dict[int, tuple] = {}
+    total_logical = runtime.total_logical_expert_count_for_layer(layer_id=layer_id, fallback=num_logical_experts)
+    # pairs of a pinned shared suffix (ids >= routed) run with the first
+    # computed wave only; later waves' tables stop at the routed ids
+    shared_pairs = int((topk_ids >= routed).sum().item()) if total_logical > routed else 0
+    first = True
+    for kind, w, buf in phase_split.iterate_b2_schedule(sched):
+        report.issue_log.append((kind, w))
+        if kind == "issue_stage":
+            prepared, ready, payload = runtime.prepare_prefill_stage_plan(
+                layer_id=layer_id, active_experts=plan.waves[w], num_logical_experts=total_logical,
+                device=hidden.device, buffer_index=buf, async_load=True,
+            )
+            report.h2d_bytes += int(payload["h2d_bytes"])
+            report.d2d_bytes += int(payload["d2d_bytes"])
+            staged[w] = (prepared, ready, buf)
+        elif kind == "issue_hit":
+            prepared = runtime.prepare_ready_slot_plan(
+                layer_id=layer_id, active_experts=plan.waves[w], num_logical_experts=total_logical,
+                device=hidden.device,
+            )
+            staged[w] = (prepared, None, None)
+        else:
+            prepared, ready, buf = staged.pop(w)
+            runtime.wait_prefill_stage_plan(ready)
+            handle = runtime.begin_slot_compute(prepared)
+            try:
+                native.permute(topk_ids, ws.perm, log2phy=prepared.log2phy, skip_unmapped=True,
+                               table_len=total_logical if first else routed)
+                first = False
+                native.grouped_mlp(hidden, k, prepared.w1, prepared.w2, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
+            finally:
+                runtime.end_slot_compute(handle)
+            if buf is not None:
+                ev = torch.cuda.Event()
+                ev.record(torch.cuda.current_stream())
+                runtime.remember_prefill_stage_buffer_release(layer_id=layer_id, buffer_index=buf, event=ev)
+    if plan.total_pairs + shared_pairs != T * k:
+        raise phase_split.B2WaveFallback(
+            "B2 wave pair coverage does not match the original top-k routing: "
+            f"covered={plan.total_pairs + shared_pairs} expected={T * k}"
+        )
+    dst = out if out is not None else ws.out[:T]
+    native.combine(ws.y[: T * k], topk_weights, dst, add=add)
+    report.seconds = perf_counter() - t0
+    return dst, report
+
+
+def run_full_layer(
+    runtime: MoeOffloadRuntime,
+    *,
+    layer_id: int,
+    hidden: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    num_logical_experts: int,
+    add: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    path: int = native.LMOE_PATH_AUTO,
+) -> torch.Tensor:
+    """Blocking fallback: stage the whole layer, one pass, one combine."""
+    prepared, _ = runtime.prepare_full_layer_prefill_plan(
+        layer_id=layer_id, num_logical_experts=num_logical_experts, device=hidden.device,
+    )
+    T, H = hidden.shape
+    k = int(topk_ids.shape[1])
+    ws = get_workspace(T, k, prepared.physical_expert_count, H, int(prepared.w1.shape[1]) // 2, hidden.device, tag="full")
+    return fused_experts(hidden, topk_weights, topk_ids, prepared.w1, prepared.w2, prepared.log2phy,
+                         add=add, out=out, path=path, workspace=ws)

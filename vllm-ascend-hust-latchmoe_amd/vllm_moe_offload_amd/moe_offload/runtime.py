@@ -1,0 +1,1137 @@
+"""Staging controller: fixed-slot decode staging, prefill stage banks and the
+compute-protected slot lifecycle, on HIP streams and events.
+
+Decode (per offloaded layer, eager, between the captured router piece and the
+captured MLP piece): de-duplicate the routed experts, let a placement-plan
+provider reorder them, drain in-flight work if any slot is LOADING or
+COMPUTING, then in order: a READY resident expert is a hit (touched); a miss
+reserves a slot (first EMPTY, else LRU READY) and joins one async batch on the
+transfer stream; the compute stream waits on the batch's event BEFORE the
+persistent log2phy is updated (only changed entries are written; inactive
+entries are kept).  The log2phy tensor and the slot banks never move, so a
+hipGraph captured against them stays valid; their addresses are fingerprinted
+at capture and re-checked before every staging.
+
+Prefill overflow waves stage into layout-scoped double-buffered stage banks
+(slot i = i-th expert of the wave), D2D from the main bank for hits and H2D
+from the host store for misses, each buffer reused only after the compute
+stream's release event for it.
+
+Reference: moe_offload/runtime.py — MoeOffloadRuntime :262; register
+:591-693; drain/leases :863-1108; prepare_fixed_slot_plan_into_log2phy
+:1636-1936; prepare_ready_slot_plan :1938-2033; prepare_prefill_stage_plan
+:2035-2258; full-layer plan :2260-2370; waits :2372-2398; stage pool
+:2400-2575; stage_fixed_slot_plan / capture_safe_slot_weights / address
+lock :2652-2790; full residency :2792-2862; log2phy update :3068-3101.
+"""
+
+from __future__ import annotations
+
+import itertools
+import os
+import threading
+from contextlib import contextmanager
+from dataclasses import dataclass
+from time import perf_counter
+
+import torch
+
+from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+from vllm_moe_offload_amd.moe_offload.expert_key import ExpertKey
+from vllm_moe_offload_amd.moe_offload.host_store import HostExpertStore
+from vllm_moe_offload_amd.moe_offload.placement_plan import PlacementPlanProvider, resolve_placement_plan
+from vllm_moe_offload_amd.moe_offload.slot_bank import ExpertSlotBank, SlotLease, SlotState
+from vllm_moe_offload_amd.moe_offload.slot_mapping import (
+    ExpertSlotMapping,
+    PreparedSlotWeights,
+    dedupe_preserve_order,
+)
+from vllm_moe_offload_amd.moe_offload.transfer_engine import TransferEngine
+
+
+def _nbytes(t: torch.Tensor) -> int:
+    return int(t.numel()) * int(t.element_size())
+
+
+def _is_current_graph_capturing() -> bool:
+    try:
+        return bool(torch.cuda.is_available() and torch.cuda.is_current_stream_capturing())
+    except Exception:
+        return False
+
+
+@dataclass(frozen=True)
+class MoeOffloadMemoryLedger:
+    registered_layers: int
+    host_experts: int
+    original_expert_weight_bytes: int
+    host_store_bytes: int
+    slot_bank_bytes: int
+    prefill_stage_bank_count: int = 0
+    prefill_stage_bank_bytes: int = 0
+    prefill_stage_mapping_bytes: int = 0
+    full_layer_prefill_bank_count: int = 0
+    full_layer_prefill_bank_bytes: int = 0
+    full_layer_prefill_mapping_bytes: int = 0
+    pinned_shared_lane_bytes: int = 0
+
+    @property
+    def total_device_slot_bytes(self) -> int:
+        return (
+            self.slot_bank_bytes
+            + self.pinned_shared_lane_bytes
+            + self.prefill_stage_bank_bytes
+            + self.prefill_stage_mapping_bytes
+            + self.full_layer_prefill_bank_bytes
+            + self.full_layer_prefill_mapping_bytes
+        )
+
+    # name kept for callers of the reference ledger
+    total_npu_slot_bytes = total_device_slot_bytes
+
+    def to_jsonable(self) -> dict[str, int]:
+        d = {k: int(getattr(self, k)) for k in self.__dataclass_fields__}
+        d["total_device_slot_bytes"] = int(self.total_device_slot_bytes)
+        return d
+
+
+@dataclass(frozen=True)
+class MoePrefillRouteStats:
+    layer_id: int
+    topk_cache_key: tuple
+    token_counts_by_expert: dict[int, int]
+    active_experts: tuple[int, ...]
+    num_tokens: int
+    top_k: int
+    pair_offsets_by_expert: dict[int, tuple[int, ...]] | None = None
+
+
+@dataclass(frozen=True)
+class SlotComputeHandle:
+    layer_id: int
+    slot_ids: tuple[int, ...]
+    leases: tuple[SlotLease, ...]
+
+
+@dataclass(frozen=True)
+class SlotAddressFingerprint:
+    w13_data_ptr: int
+    w2_data_ptr: int
+    log2phy_data_ptr: int
+    w13_shape: tuple[int, ...]
+    w2_shape: tuple[int, ...]
+    log2phy_shape: tuple[int, ...]
+    device: str
+    dtype: str
+
+    def to_jsonable(self) -> dict[str, object]:
+        return {k: (list(v) if isinstance(v, tuple) else v) for k, v in self.__dict__.items()}
+
+
+@dataclass(frozen=True)
+class FusedSharedLaneLayout:
+    """Routed ids [0, routed) live in dynamic slots; shared ids follow as a
+    pinned suffix of the physical bank."""
+
+    routed_expert_count: int
+    shared_expert_count: int
+    pinned_logical_ids: tuple[int, ...]
+
+    @property
+    def total_logical_expert_count(self) -> int:
+        return int(self.routed_expert_count + self.shared_expert_count)
+
+
+class MoeOffloadRuntime:
+    def __init__(self, config: MoeOffloadConfig | None = None) -> None:
+        self.config = config if config is not None else MoeOffloadConfig.from_env()
+        self._step_counter = itertools.count()
+        self._host_store = HostExpertStore()
+        self._slot_banks: dict[int, ExpertSlotBank] = {}
+        self._fused_shared_lane_layouts: dict[int, FusedSharedLaneLayout] = {}
+        self._prefill_stage_pool: dict[tuple, list[ExpertSlotBank]] = {}
+        self._prefill_stage_banks: dict[int, list[ExpertSlotBank]] = {}
+        self._prefill_stage_pool_release_events: dict[tuple, object] = {}
+        self._prefill_stage_log2phy: dict[tuple, torch.Tensor] = {}
+        self._full_layer_prefill_pool: dict[tuple, ExpertSlotBank] = {}
+        self._full_layer_prefill_log2phy: dict[tuple, torch.Tensor] = {}
+        self._original_expert_weight_bytes_by_layer: dict[int, int] = {}
+        self._expert_weight_bytes_by_layer: dict[int, int] = {}
+        self._log2phy_buffers: dict[int, torch.Tensor] = {}
+        self._log2phy_slot_by_expert: dict[int, dict[int, int]] = {}
+        self._graph_slot_address_fingerprints: dict[int, SlotAddressFingerprint] = {}
+        self._graph_slot_address_evidence: set[int] = set()
+        self._slot_generation_protection_evidence: set[int] = set()
+        self._transfer_engine = TransferEngine()
+        self._profile_events: list[dict[str, object]] = []
+        self._prefill_route_stats_by_layer: dict[int, MoePrefillRouteStats] = {}
+        self._active_slot_ids_by_layer: dict[int, tuple[int, ...]] = {}
+        self._slot_compute_done_events: dict[tuple[int, int, int], object] = {}
+        self._placement_plan_provider: PlacementPlanProvider | None = None
+        self._fixed_slot_execution_state = threading.local()
+        self._memory_ledger_cache: MoeOffloadMemoryLedger | None = None
+
+    # ------------------------------------------------------------------ misc
+    @property
+    def transfer_engine(self) -> TransferEngine:
+        return self._transfer_engine
+
+    @property
+    def host_store(self) -> HostExpertStore:
+        return self._host_store
+
+    def slot_bank(self, layer_id: int) -> ExpertSlotBank | None:
+        return self._slot_banks.get(int(layer_id))
+
+    def set_placement_plan_provider(self, provider: PlacementPlanProvider | None) -> None:
+        """Install an external ordering provider (it never sees slot storage)."""
+        self._placement_plan_provider = provider
+
+    def next_step_id(self) -> int:
+        return int(next(self._step_counter))
+
+    def _step(self, step_id: int | None) -> int:
+        return int(step_id) if step_id is not None and int(step_id) >= 0 else self.next_step_id()
+
+    def _record_profile_event(self, name: str, *, layer_id: int | None, start: float,
+                              payload: dict[str, object] | None = None) -> None:
+        ev: dict[str, object] = {
+            "name": name,
+            "layer_id": layer_id,
+            "seconds": perf_counter() - start,
+            "memory_ledger": self.memory_ledger().to_jsonable(),
+        }
+        if payload is not None:
+            ev["payload"] = payload
+        self._profile_events.append(ev)
+
+    def profiling_summary(self) -> dict[str, object]:
+        return {"events": list(self._profile_events), "memory_ledger": self.memory_ledger().to_jsonable()}
+
+    # --------------------------------------------------------- predicates
+    @property
+    def should_use_fixed_slots(self) -> bool:
+        return self.config.enabled and not self.config.trace_only and self.config.num_slots > 0
+
+    def is_resident_layer(self, layer_id: int) -> bool:
+        return self.config.is_resident_layer(int(layer_id))
+
+    @contextmanager
+    def suspend_fixed_slot_execution(self):
+        """Temporarily route the current thread through the native path."""
+        st = self._fixed_slot_execution_state
+        depth = int(getattr(st, "suspend_depth", 0))
+        st.suspend_depth = depth + 1
+        try:
+            yield
+        finally:
+            st.suspend_depth = depth
+
+    def should_use_fixed_slot_plan_for_layer(self, layer_id: int) -> bool:
+        if int(getattr(self._fixed_slot_execution_state, "suspend_depth", 0)) > 0:
+            return False
+        return self.should_use_fixed_slots and not self.is_resident_layer(int(layer_id))
+
+    def is_static_residency_regime(self, num_logical_experts: int) -> bool:
+        """Regime A: every routed expert owns a slot, log2phy never changes."""
+        return int(self.config.num_slots) >= int(num_logical_experts)
+
+    def is_static_residency_regime_for_layer(self, *, layer_id: int, fallback_routed_expert_count: int) -> bool:
+        return self.is_static_residency_regime(
+            self.routed_expert_count_for_layer(layer_id=layer_id, fallback=fallback_routed_expert_count)
+        )
+
+    def should_use_b2_wave_prefill(self, *, layer_id: int, active_expert_count: int, is_prefill: bool) -> bool:
+        if not self.config.b2_wave_prefill or not is_prefill:
+            return False
+        if not self.should_use_fixed_slot_plan_for_layer(int(layer_id)):
+            return False
+        return int(active_expert_count) > int(self.config.num_slots)
+
+    def should_use_b2_pair_waves(self, *, layer_id: int, active_expert_count: int) -> bool:
+        if not self.config.b2_wave_prefill:
+            return False
+        if not self.should_use_fixed_slot_plan_for_layer(int(layer_id)):
+            return False
+        return int(active_expert_count) > int(self.config.num_slots)
+
+    def is_layer_registered(self, layer_id: int) -> bool:
+        return int(layer_id) in self._slot_banks
+
+    def fused_shared_lane_layout(self, layer_id: int) -> FusedSharedLaneLayout | None:
+        return self._fused_shared_lane_layouts.get(int(layer_id))
+
+    def routed_expert_count_for_layer(self, *, layer_id: int, fallback: int) -> int:
+        lay = self.fused_shared_lane_layout(layer_id)
+        return int(lay.routed_expert_count) if lay is not None else int(fallback)
+
+    def total_logical_expert_count_for_layer(self, *, layer_id: int, fallback: int) -> int:
+        lay = self.fused_shared_lane_layout(layer_id)
+        return int(lay.total_logical_expert_count) if lay is not None else int(fallback)
+
+    def _resolve_fused_shared_counts(self, *, layer_id: int, requested_logical_expert_count: int) -> tuple[int, int]:
+        req = int(requested_logical_expert_count)
+        lay = self.fused_shared_lane_layout(layer_id)
+        if lay is None:
+            return req, req
+        routed, total = int(lay.routed_expert_count), int(lay.total_logical_expert_count)
+        if req not in (routed, total):
+            raise RuntimeError(
+                f"fused shared lane logical count mismatch: layer={int(layer_id)} requested={req} "
+                f"routed={routed} total={total}"
+            )
+        return routed, total
+
+    # --------------------------------------------------------- registration
+    def register_layer_for_fixed_slots(self, layer: torch.nn.Module, *, slot_device: torch.device | None = None) -> None:
+        """Host-store the routed experts, build the slot bank and log2phy."""
+        layer_id = int(getattr(layer, "layer_id", -1))
+        if layer_id < 0:
+            raise ValueError("layer.layer_id is required for fixed-slot registration")
+        if layer_id in self._graph_slot_address_fingerprints:
+            raise RuntimeError(
+                f"layer {layer_id} fixed-slot addresses are already captured; "
+                "re-registering would invalidate a graph replay"
+            )
+        start = perf_counter()
+        w13, w2 = layer.w13_weight, layer.w2_weight
+        if int(w13.shape[0]) != int(w2.shape[0]):
+            raise ValueError("w13_weight and w2_weight must have the same number of experts")
+        total = int(w13.shape[0])
+        shared = int(getattr(layer, "n_shared_experts", 0) or 0) if bool(getattr(layer, "mix_placement", False)) else 0
+        if shared > total:
+            raise ValueError(f"fused shared expert count exceeds materialized expert rows: shared={shared}, total={total}")
+        routed = total - shared
+        if routed <= 0:
+            raise ValueError(f"fused mix-placement requires at least one routed expert; total={total}, shared={shared}")
+        pinned_ids = tuple(range(routed, total))
+        report = self._host_store.register_layer(
+            layer,
+            pin_memory=self.config.should_pin_host_memory,
+            clone_tensors=not bool(getattr(layer, "_cpu_first_expert_weights", False)),
+            routed_expert_count=routed,
+        )
+        self._original_expert_weight_bytes_by_layer[layer_id] = _nbytes(w13) + _nbytes(w2)
+        self._expert_weight_bytes_by_layer[layer_id] = _nbytes(w13[0]) + _nbytes(w2[0])
+        device = slot_device if slot_device is not None else w13.device
+        bank = ExpertSlotBank(
+            self.config.num_slots,
+            tuple(int(d) for d in w13.shape[1:]),
+            tuple(int(d) for d in w2.shape[1:]),
+            dtype=w13.dtype,
+            device=device,
+            pinned_logical_ids=pinned_ids,
+        )
+        self._slot_banks[layer_id] = bank
+        if pinned_ids:
+            bank.install_pinned_weights(w13[routed:], w2[routed:])
+            self._fused_shared_lane_layouts[layer_id] = FusedSharedLaneLayout(routed, shared, pinned_ids)
+        else:
+            self._fused_shared_lane_layouts.pop(layer_id, None)
+        self._prefill_stage_banks.pop(layer_id, None)
+        table = torch.full((total,), -1, dtype=torch.int32, device=device)
+        bank.install_pinned_log2phy(table)
+        self._log2phy_buffers[layer_id] = table
+        self._log2phy_slot_by_expert[layer_id] = {}
+        self._memory_ledger_cache = None
+        self._record_profile_event(
+            "register_layer_for_fixed_slots",
+            layer_id=layer_id,
+            start=start,
+            payload={
+                "host_store": report.to_jsonable(),
+                "routed_expert_count": routed,
+                "pinned_shared_expert_count": shared,
+                "pinned_shared_logical_ids": list(pinned_ids),
+            },
+        )
+
+    # ----------------------------------------------------------- queries
+    def slot_readiness_and_ready_slot_ids_for_experts(self, *, layer_id: int, expert_ids) -> tuple[dict[int, bool], dict[int, int]]:
+        bank = self._slot_banks.get(int(layer_id))
+        if bank is None:
+            return {int(e): False for e in expert_ids}, {}
+        ready: dict[int, bool] = {}
+        ids: dict[int, int] = {}
+        for e in expert_ids:
+            slot = bank.lookup_expert_id(int(e))
+            ok = slot is not None and slot.state == SlotState.READY
+            ready[int(e)] = ok
+            if ok:
+                ids[int(e)] = int(slot.slot_id)
+        return ready, ids
+
+    def slot_readiness_for_experts(self, *, layer_id: int, expert_ids) -> dict[int, bool]:
+        return self.slot_readiness_and_ready_slot_ids_for_experts(layer_id=layer_id, expert_ids=expert_ids)[0]
+
+    def ready_slot_ids_for_experts(self, *, layer_id: int, expert_ids) -> dict[int, int]:
+        return self.slot_readiness_and_ready_slot_ids_for_experts(layer_id=layer_id, expert_ids=expert_ids)[1]
+
+    def estimate_expert_weight_bytes(self, *, layer_id: int, expert_id: int) -> int:
+        return int(self._host_store.get(int(layer_id), int(expert_id)).nbytes)
+
+    def cached_layer_expert_weight_bytes(self, *, layer_id: int) -> int:
+        return int(self._expert_weight_bytes_by_layer.get(int(layer_id), 0))
+
+    def log2phy_buffer(self, layer_id: int) -> torch.Tensor | None:
+        """The persistent, fixed-address log2phy table of a layer."""
+        return self._log2phy_buffers.get(int(layer_id))
+
+    # ------------------------------------------------------ memory ledger
+    def memory_ledger(self) -> MoeOffloadMemoryLedger:
+        if self._memory_ledger_cache is not None:
+            return self._memory_ledger_cache
+        stage_banks = {id(b): b for banks in self._prefill_stage_pool.values() for b in banks}
+        full_banks = {id(b): b for b in self._full_layer_prefill_pool.values()}
+        ledger = MoeOffloadMemoryLedger(
+            registered_layers=len(self._slot_banks),
+            host_experts=len(self._host_store),
+            original_expert_weight_bytes=sum(self._original_expert_weight_bytes_by_layer.values()),
+            host_store_bytes=int(self._host_store.total_bytes),
+            slot_bank_bytes=sum(b.dynamic_bytes for b in self._slot_banks.values()),
+            prefill_stage_bank_count=len(stage_banks),
+            prefill_stage_bank_bytes=sum(b.total_bytes for b in stage_banks.values()),
+            prefill_stage_mapping_bytes=sum(_nbytes(t) for t in self._prefill_stage_log2phy.values()),
+            full_layer_prefill_bank_count=len(full_banks),
+            full_layer_prefill_bank_bytes=sum(b.total_bytes for b in full_banks.values()),
+            full_layer_prefill_mapping_bytes=sum(_nbytes(t) for t in self._full_layer_prefill_log2phy.values()),
+            pinned_shared_lane_bytes=sum(b.pinned_bytes for b in self._slot_banks.values()),
+        )
+        self._memory_ledger_cache = ledger
+        return ledger
+
+    # ----------------------------------------------------- slot lifecycle
+    def _allocate_slot_with_loading_fallback(self, bank: ExpertSlotBank, key: ExpertKey, *, step_id: int):
+        try:
+            return bank.allocate_for(key, step_id=step_id)
+        except RuntimeError:
+            if not any(s.state in (SlotState.LOADING, SlotState.COMPUTING) for s in bank.slots):
+                raise
+            self._drain_slot_bank_inflight_work(bank)
+            return bank.allocate_for(key, step_id=step_id)
+
+    def _drain_slot_bank_inflight_work(self, bank: ExpertSlotBank) -> None:
+        """Finish every in-flight copy and compute touching this bank."""
+        if any(s.state == SlotState.LOADING for s in bank.slots):
+            self._transfer_engine.synchronize()
+            still = [s.slot_id for s in bank.slots if s.state == SlotState.LOADING]
+            if still:
+                raise RuntimeError(f"H2D synchronization completed without a matching ready event for slots {still}")
+        computing = [s for s in bank.slots if s.state == SlotState.COMPUTING]
+        leases = [s.lease() for s in computing]
+        events: list[object] = []
+        seen: set[int] = set()
+        for lease in leases:
+            ev = self._slot_compute_done_events.pop((int(lease.expert_key.layer_id), int(lease.slot_id), int(lease.version)), None)
+            if ev is None:
+                raise RuntimeError(
+                    f"computing slot has no completion event: layer={lease.expert_key.layer_id} "
+                    f"slot={lease.slot_id} version={lease.version}"
+                )
+            if id(ev) not in seen:
+                seen.add(id(ev))
+                events.append(ev)
+        for ev in events:
+            _synchronize_event(ev)
+        for slot, lease in zip(computing, leases):
+            if not slot.matches_lease(lease):
+                raise RuntimeError(f"slot {lease.slot_id} ownership changed while compute was in flight")
+            if slot.state == SlotState.COMPUTING:
+                slot.state = SlotState.READY
+        for layer_id in sorted({int(l.expert_key.layer_id) for l in leases} - self._slot_generation_protection_evidence):
+            mine = [l for l in leases if int(l.expert_key.layer_id) == layer_id]
+            self._slot_generation_protection_evidence.add(layer_id)
+            self._record_profile_event(
+                "slot_generation_protected_until_compute_complete",
+                layer_id=layer_id,
+                start=perf_counter(),
+                payload={
+                    "slot_ids": [int(l.slot_id) for l in mine],
+                    "generations": [int(l.version) for l in mine],
+                    "expert_ids": [int(l.expert_key.expert_id) for l in mine],
+                    "completion_events_synchronized": len(events),
+                    "leases_still_match": True,
+                },
+            )
+
+    @staticmethod
+    def _release_allocated_loads(bank: ExpertSlotBank, loads) -> None:
+        for _, slot in loads:
+            if getattr(slot, "state", None) == SlotState.LOADING:
+                bank.clear_slot(int(slot.slot_id), force=True)
+
+    def begin_slot_compute(self, prepared: PreparedSlotWeights) -> SlotComputeHandle | None:
+        """Mark the main-bank slots of a plan COMPUTING while kernels read them."""
+        layer_id = int(prepared.mapping.layer_id)
+        bank = self._slot_banks.get(layer_id)
+        if bank is None or prepared.w1.data_ptr() != bank.w13_slots.data_ptr():
+            return None
+        slot_ids = tuple(sorted({int(s) for s in prepared.mapping.active_slot_ids}))
+        if not slot_ids:
+            slot_ids = tuple(int(s) for s in self._active_slot_ids_by_layer.get(layer_id, ()))
+        if not slot_ids:
+            return None
+        capturing = _is_current_graph_capturing()
+        leases: list[SlotLease] = []
+        for sid in slot_ids:
+            slot = bank.slots[sid]
+            if sid >= len(prepared.mapping.slot_to_expert):
+                raise RuntimeError(f"prepared slot mapping has no owner entry for slot {sid}")
+            owner = prepared.mapping.slot_to_expert[sid]
+            expected = ExpertKey(layer_id, int(owner)) if owner is not None else None
+            if slot.expert_key != expected:
+                raise RuntimeError(f"prepared mapping owner mismatch for slot {sid}: expected {expected}, found {slot.expert_key}")
+            if slot.state == SlotState.COMPUTING and capturing:
+                # capture follows the preceding eager compute on the same
+                # device stream order; hand its completion record over
+                # instead of synchronising the host inside capture
+                lease = slot.lease()
+                if self._slot_compute_done_events.pop((layer_id, sid, int(lease.version)), None) is None:
+                    raise RuntimeError(
+                        "capturing slot has no completion event from the preceding eager compute: "
+                        f"layer={layer_id} slot={sid} version={lease.version}"
+                    )
+                slot.state = SlotState.READY
+            if slot.state != SlotState.READY:
+                raise RuntimeError(f"prepared slot {sid} is not ready for compute: {slot.state.value}")
+            leases.append(slot.lease())
+        for sid in slot_ids:
+            bank.mark_computing(sid)
+        return SlotComputeHandle(layer_id, slot_ids, tuple(leases))
+
+    def end_slot_compute(self, handle: SlotComputeHandle | None) -> None:
+        """Record the compute stream's completion event for the leased slots."""
+        if handle is None:
+            return
+        bank = self._slot_banks.get(int(handle.layer_id))
+        if bank is None:
+            return
+        for lease in handle.leases:
+            slot = bank.slots[int(lease.slot_id)]
+            if not slot.matches_lease(lease):
+                raise RuntimeError(f"slot {lease.slot_id} ownership changed before compute completed")
+            if slot.state != SlotState.COMPUTING:
+                raise RuntimeError(f"slot {lease.slot_id} is not computing at compute completion: {slot.state.value}")
+        ev = self._record_current_stream_event_or_none()
+        for lease in handle.leases:
+            slot = bank.slots[int(lease.slot_id)]
+            if ev is None:
+                slot.state = SlotState.READY
+            else:
+                self._slot_compute_done_events[(int(handle.layer_id), int(lease.slot_id), int(lease.version))] = ev
+
+    # ------------------------------------------------------ decode staging
+    def _record_current_stream_event_or_none(self):
+        """Completion event of the compute stream (None for host-only banks)."""
+        if not any(b.w13_slots.device.type == "cuda" for b in self._slot_banks.values()):
+            return None
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream())
+        return ev
+
+    def prepare_fixed_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int,
+                                device: torch.device | None = None, step_id: int | None = None,
+                                record_stage_profile: bool = False) -> PreparedSlotWeights:
+        """Stage into the main bank and return a mapping in a fresh log2phy."""
+        bank = self._slot_banks.get(int(layer_id))
+        if bank is None:
+            raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
+        _, total = self._resolve_fused_shared_counts(layer_id=layer_id, requested_logical_expert_count=num_logical_experts)
+        table = torch.full((total,), -1, dtype=torch.int32, device=device if device is not None else bank.w13_slots.device)
+        bank.install_pinned_log2phy(table)
+        saved = self._log2phy_slot_by_expert.get(int(layer_id))
+        self._log2phy_slot_by_expert[int(layer_id)] = {}
+        try:
+            return self.prepare_fixed_slot_plan_into_log2phy(
+                layer_id=layer_id, active_experts=active_experts, num_logical_experts=num_logical_experts,
+                log2phy=table, step_id=step_id, record_stage_profile=record_stage_profile,
+            )
+        finally:
+            self._log2phy_slot_by_expert[int(layer_id)] = saved if saved is not None else {}
+
+    def prepare_fixed_slot_plan_into_log2phy(self, *, layer_id: int, active_experts, num_logical_experts: int,
+                                             log2phy: torch.Tensor, step_id: int | None = None,
+                                             record_stage_profile: bool = False) -> PreparedSlotWeights:
+        """Decode hot path: hit/miss, one async H2D batch, consumer wait, then
+        an in-place update of the changed log2phy entries."""
+        if not self.should_use_fixed_slots:
+            raise RuntimeError("fixed-slot plan requested while moe offload fixed slots are disabled")
+        layer_id = int(layer_id)
+        if self.is_resident_layer(layer_id):
+            raise RuntimeError(f"fixed-slot plan must not run on resident layer {layer_id}; use the original expert weights")
+        routed, total = self._resolve_fused_shared_counts(layer_id=layer_id, requested_logical_expert_count=num_logical_experts)
+        active = dedupe_preserve_order(active_experts)
+        _validate_active_expert_ids(layer_id=layer_id, active_experts=active, num_logical_experts=routed)
+        if len(active) > self.config.num_slots:
+            raise RuntimeError(f"active expert working set size {len(active)} exceeds num_slots={self.config.num_slots}")
+        if int(log2phy.numel()) != total:
+            raise RuntimeError(f"log2phy buffer for layer {layer_id} has size {int(log2phy.numel())}, expected {total}")
+        bank = self._slot_banks.get(layer_id)
+        if bank is None:
+            raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
+        if any(s.state in (SlotState.LOADING, SlotState.COMPUTING) for s in bank.slots):
+            self._drain_slot_bank_inflight_work(bank)
+        step_id = self._step(step_id)
+        t0 = perf_counter()
+        hits: list[int] = []
+        misses: list[int] = []
+        async_loads = []
+        sync_loads = []
+        slot_ids: list[int] = []
+        owners: list[int | None] = [None] * bank.physical_expert_count
+        for logical_id in bank.pinned_logical_ids:
+            owners[int(bank.pinned_slot_for_logical_id(logical_id))] = int(logical_id)
+        for e in active:
+            key = ExpertKey(layer_id, e)
+            slot = bank.lookup(key)
+            if slot is not None and slot.state != SlotState.READY:
+                self._drain_slot_bank_inflight_work(bank)
+                slot = bank.lookup(key)
+            if slot is not None and slot.state == SlotState.READY:
+                slot.last_used_step = step_id
+                hits.append(e)
+            else:
+                misses.append(e)
+                try:
+                    slot = self._allocate_slot_with_loading_fallback(bank, key, step_id=step_id)
+                except RuntimeError as exc:
+                    raise RuntimeError(
+                        f"failed to allocate expert slot for layer {layer_id} expert {e} with "
+                        f"num_slots={self.config.num_slots}; async_load={self.config.async_load}"
+                    ) from exc
+                bundle = self._host_store.get(layer_id, e)
+                (async_loads if self.config.async_load else sync_loads).append((bundle, slot))
+            slot_ids.append(int(slot.slot_id))
+        if sync_loads:
+            try:
+                self._transfer_engine.load_many_sync(sync_loads, validate_layout=False)
+            except Exception:
+                self._release_allocated_loads(bank, sync_loads)
+                raise
+        ready = None
+        if async_loads:
+            try:
+                ready = self._transfer_engine.load_many_async(async_loads, record_event=True, validate_layout=False)
+            except Exception:
+                self._release_allocated_loads(bank, async_loads)
+                raise
+        # order the copies before the consumer, THEN publish the mapping
+        if ready is not None:
+            self._wait_transfer_event(ready)
+        upd_e, upd_s = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=tuple(slot_ids))
+        if upd_e:
+            _update_log2phy_entries(log2phy, expert_ids=upd_e, slot_ids=upd_s)
+            self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd_e, slot_ids=upd_s)
+        for e, sid in zip(active, slot_ids):
+            owners[sid] = e
+        mapping = ExpertSlotMapping(layer_id, active, log2phy, tuple(owners), tuple(slot_ids))
+        self._active_slot_ids_by_layer[layer_id] = tuple(slot_ids)
+        if record_stage_profile and (self.config.profile_path or os.environ.get("LATCHMOE_PROFILE")):
+            per = int(self._expert_weight_bytes_by_layer.get(layer_id, 0))
+            self._record_profile_event(
+                "decode_fixed_slot_stage",
+                layer_id=layer_id,
+                start=t0,
+                payload={
+                    "n_active": len(active),
+                    "n_hits": len(hits),
+                    "n_misses": len(misses),
+                    "hit_rate": round(len(hits) / len(active), 6) if active else 0.0,
+                    "h2d_bytes": per * len(misses),
+                    "step_id": step_id,
+                    "num_slots": int(self.config.num_slots),
+                    "mapping_mode": "persistent_log2phy",
+                    "log2phy_update_count": len(upd_e),
+                    "stage_mode": "main_slot_hit" if not misses else ("async_decode_load_many" if async_loads else "sync_decode_load"),
+                    "consumer_dependency_installed": True,
+                    "mapping_published_after_ready": True,
+                    "active_experts": list(active),
+                    "hit_experts": hits,
+                    "miss_experts": misses,
+                },
+            )
+        return PreparedSlotWeights.from_slot_bank(slot_bank=bank, mapping=mapping)
+
+    def _changed_log2phy_entries(self, *, layer_id: int, expert_ids, slot_ids) -> tuple[tuple[int, ...], tuple[int, ...]]:
+        if len(expert_ids) != len(slot_ids):
+            raise ValueError(f"expert_ids and slot_ids length mismatch: {len(expert_ids)} != {len(slot_ids)}")
+        cached = self._log2phy_slot_by_expert.setdefault(int(layer_id), {})
+        pairs = [(int(e), int(s)) for e, s in zip(expert_ids, slot_ids) if cached.get(int(e)) != int(s)]
+        return tuple(p[0] for p in pairs), tuple(p[1] for p in pairs)
+
+    def _remember_log2phy_entries(self, *, layer_id: int, expert_ids, slot_ids) -> None:
+        cached = self._log2phy_slot_by_expert.setdefault(int(layer_id), {})
+        for e, s in zip(expert_ids, slot_ids):
+            cached[int(e)] = int(s)
+
+    def stage_fixed_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int) -> PreparedSlotWeights:
+        """Eager pre-replay staging into the persistent log2phy (never inside capture)."""
+        if _is_current_graph_capturing():
+            raise RuntimeError(
+                "stage_fixed_slot_plan must run eager (outside graph capture); it performs host decision + H2D staging"
+            )
+        active = resolve_placement_plan(
+            self._placement_plan_provider,
+            layer_id=int(layer_id),
+            routed_experts=tuple(int(e) for e in active_experts),
+            num_logical_experts=int(num_logical_experts),
+        )
+        self._assert_locked_slot_addresses(int(layer_id))
+        buf = self._log2phy_buffers[int(layer_id)]
+        prepared = self.prepare_fixed_slot_plan_into_log2phy(
+            layer_id=int(layer_id), active_experts=active, num_logical_experts=int(num_logical_experts),
+            log2phy=buf, record_stage_profile=True,
+        )
+        return PreparedSlotWeights(prepared.w1, prepared.w2, buf, prepared.physical_expert_count, prepared.mapping)
+
+    def stage_full_residency_slot_plan(self, *, layer_id: int) -> bool:
+        """Regime A: stage every routed expert once, before capture."""
+        layer_id = int(layer_id)
+        if not (self.should_use_fixed_slots and self.config.graph_compatible_offload):
+            return False
+        if self.is_resident_layer(layer_id) or not self.is_layer_registered(layer_id):
+            return False
+        buf = self._log2phy_buffers.get(layer_id)
+        if buf is None:
+            return False
+        if _is_current_graph_capturing():
+            if bool((buf < 0).all().item()):
+                raise RuntimeError(
+                    f"stage_full_residency_slot_plan called during graph capture for layer {layer_id} but its "
+                    "log2phy buffer is still all -1; staging must run eager before capture"
+                )
+            return False
+        routed, total = self._resolve_fused_shared_counts(layer_id=layer_id, requested_logical_expert_count=int(buf.numel()))
+        if not self.is_static_residency_regime(routed):
+            self._record_profile_event(
+                "skip_full_residency_slot_plan", layer_id=layer_id, start=perf_counter(),
+                payload={"reason": "regime_b_num_slots_lt_logical_experts", "num_slots": int(self.config.num_slots),
+                         "routed_expert_count": routed},
+            )
+            return False
+        self.stage_fixed_slot_plan(layer_id=layer_id, active_experts=tuple(range(routed)), num_logical_experts=total)
+        return True
+
+    def capture_safe_slot_weights(self, *, layer_id: int) -> PreparedSlotWeights | None:
+        """Fixed slot tensors + fixed log2phy, no host sync, no copy: what a
+        captured graph records.  Locks the address fingerprint."""
+        layer_id = int(layer_id)
+        bank = self._slot_banks.get(layer_id)
+        buf = self._log2phy_buffers.get(layer_id)
+        if bank is None or buf is None:
+            return None
+        self._lock_graph_slot_addresses(layer_id)
+        owners: list[int | None] = [int(s.expert_key.expert_id) if s.expert_key is not None else None for s in bank.slots]
+        owners.extend(int(e) for e in bank.pinned_logical_ids)
+        mapping = ExpertSlotMapping(layer_id, (), buf, tuple(owners), ())
+        return PreparedSlotWeights.from_slot_bank(slot_bank=bank, mapping=mapping)
+
+    def _slot_address_fingerprint(self, layer_id: int) -> SlotAddressFingerprint:
+        bank = self._slot_banks.get(int(layer_id))
+        buf = self._log2phy_buffers.get(int(layer_id))
+        if bank is None or buf is None:
+            raise RuntimeError(f"layer {layer_id} has no fixed-slot tensors to fingerprint")
+        return SlotAddressFingerprint(
+            int(bank.w13_slots.data_ptr()), int(bank.w2_slots.data_ptr()), int(buf.data_ptr()),
+            tuple(int(d) for d in bank.w13_slots.shape), tuple(int(d) for d in bank.w2_slots.shape),
+            tuple(int(d) for d in buf.shape), str(bank.w13_slots.device), str(bank.w13_slots.dtype),
+        )
+
+    def _lock_graph_slot_addresses(self, layer_id: int) -> None:
+        start = perf_counter()
+        fp = self._slot_address_fingerprint(layer_id)
+        old = self._graph_slot_address_fingerprints.get(int(layer_id))
+        if old is None:
+            self._graph_slot_address_fingerprints[int(layer_id)] = fp
+            self._record_profile_event("graph_slot_address_lock", layer_id=int(layer_id), start=start, payload=fp.to_jsonable())
+            return
+        if old != fp:
+            raise RuntimeError(f"fixed-slot address fingerprint changed for captured layer {layer_id}")
+        if not _is_current_graph_capturing() and int(layer_id) not in self._graph_slot_address_evidence:
+            self._graph_slot_address_evidence.add(int(layer_id))
+            self._record_profile_event(
+                "graph_slot_address_validate", layer_id=int(layer_id), start=start,
+                payload={**fp.to_jsonable(), "matches_capture_fingerprint": True},
+            )
+
+    def _assert_locked_slot_addresses(self, layer_id: int) -> None:
+        if int(layer_id) in self._graph_slot_address_fingerprints:
+            self._lock_graph_slot_addresses(int(layer_id))
+
+    def _wait_transfer_event(self, ready_event) -> None:
+        if ready_event is None:
+            return
+        install = getattr(ready_event, "install_consumer_dependency", None)
+        if callable(install):
+            install(_current_stream_for(ready_event))
+            return
+        ev = getattr(ready_event, "event", ready_event)
+        if isinstance(ev, torch.cuda.Event):
+            torch.cuda.current_stream().wait_event(ev)
+        mark = getattr(ready_event, "mark_ready", None)
+        if callable(mark):
+            mark()
+
+    def wait_prefill_stage_plan(self, ready_event) -> None:
+        self._wait_transfer_event(ready_event)
+
+    # ---------------------------------------------------- prefill waves
+    def _validate_prefill_buffer_index(self, buffer_index: int) -> None:
+        cap = self.config.effective_prefill_buffer_count
+        if int(buffer_index) < 0 or int(buffer_index) >= cap:
+            raise RuntimeError(
+                f"prefill stage buffer index {int(buffer_index)} is outside prefill_buffer_count={cap}"
+            )
+
+    @staticmethod
+    def _pool_key(bank: ExpertSlotBank) -> tuple:
+        return (
+            str(bank.w13_slots.device), str(bank.w13_slots.dtype), len(bank.slots),
+            tuple(bank.pinned_logical_ids), tuple(int(d) for d in bank.w13_slots.shape[1:]),
+            tuple(int(d) for d in bank.w2_slots.shape[1:]),
+        )
+
+    def _get_prefill_stage_bank(self, *, layer_id: int, buffer_index: int, template_bank: ExpertSlotBank) -> ExpertSlotBank:
+        self._validate_prefill_buffer_index(buffer_index)
+        banks = self._prefill_stage_pool.setdefault(self._pool_key(template_bank), [])
+        self._prefill_stage_banks[int(layer_id)] = banks
+        while len(banks) <= int(buffer_index):
+            start = perf_counter()
+            nb = ExpertSlotBank(
+                len(template_bank.slots),
+                tuple(int(d) for d in template_bank.w13_slots.shape[1:]),
+                tuple(int(d) for d in template_bank.w2_slots.shape[1:]),
+                dtype=template_bank.w13_slots.dtype,
+                device=template_bank.w13_slots.device,
+                pinned_logical_ids=template_bank.pinned_logical_ids,
+            )
+            nb.copy_pinned_weights_from(template_bank)
+            banks.append(nb)
+            self._memory_ledger_cache = None
+            self._record_profile_event(
+                "prefill_stage_bank_allocate", layer_id=int(layer_id), start=start,
+                payload={"buffer_index": len(banks) - 1, "bank_bytes": int(nb.total_bytes)},
+            )
+        return banks[int(buffer_index)]
+
+    def _get_prefill_stage_log2phy_buffer(self, *, template_bank: ExpertSlotBank, buffer_index: int,
+                                          num_logical_experts: int, device) -> torch.Tensor:
+        key = (self._pool_key(template_bank), int(buffer_index), int(num_logical_experts), str(device))
+        buf = self._prefill_stage_log2phy.get(key)
+        if buf is None:
+            buf = torch.full((int(num_logical_experts),), -1, dtype=torch.int32, device=device)
+            self._prefill_stage_log2phy[key] = buf
+            self._memory_ledger_cache = None
+        return buf
+
+    def prefill_stage_buffer_release_event(self, *, layer_id: int, buffer_index: int) -> object | None:
+        self._validate_prefill_buffer_index(buffer_index)
+        bank = self._slot_banks.get(int(layer_id))
+        if bank is None:
+            return None
+        return self._prefill_stage_pool_release_events.get((self._pool_key(bank), int(buffer_index)))
+
+    def remember_prefill_stage_buffer_release(self, *, layer_id: int, buffer_index: int, event: object | None) -> None:
+        self._validate_prefill_buffer_index(buffer_index)
+        if event is None:
+            return
+        bank = self._slot_banks.get(int(layer_id))
+        if bank is not None:
+            self._prefill_stage_pool_release_events[(self._pool_key(bank), int(buffer_index))] = event
+
+    def prepare_ready_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int, device,
+                                step_id: int | None = None, build_log2phy: bool = True, **_: object) -> PreparedSlotWeights:
+        """Zero-copy plan for a wave whose experts are all READY in the main
+        bank; any miss fails closed."""
+        if not self.should_use_fixed_slots:
+            raise RuntimeError("ready-slot plan requested while fixed slots are disabled")
+        layer_id = int(layer_id)
+        if self.is_resident_layer(layer_id):
+            raise RuntimeError(f"ready-slot plan must not run on resident layer {layer_id}")
+        routed, total = self._resolve_fused_shared_counts(layer_id=layer_id, requested_logical_expert_count=num_logical_experts)
+        active = dedupe_preserve_order(active_experts)
+        _validate_active_expert_ids(layer_id=layer_id, active_experts=active, num_logical_experts=routed)
+        if len(active) > self.config.num_slots:
+            raise RuntimeError(f"ready expert working set size {len(active)} exceeds num_slots={self.config.num_slots}")
+        bank = self._slot_banks.get(layer_id)
+        if bank is None:
+            raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
+        step_id = self._step(step_id)
+        missing: list[int] = []
+        slot_ids: list[int] = []
+        for e in active:
+            slot = bank.lookup(ExpertKey(layer_id, e))
+            if slot is None or slot.state != SlotState.READY:
+                missing.append(e)
+                continue
+            slot.last_used_step = step_id
+            slot_ids.append(int(slot.slot_id))
+        if missing:
+            raise RuntimeError(f"ready-slot plan requested for non-ready experts in layer {layer_id}: {missing}")
+        if build_log2phy:
+            mapping = ExpertSlotMapping.from_slot_bank(
+                layer_id=layer_id, active_experts=active, num_logical_experts=total, slot_bank=bank, device=device
+            )
+        else:
+            owners: list[int | None] = [None] * bank.physical_expert_count
+            for logical_id in bank.pinned_logical_ids:
+                owners[int(bank.pinned_slot_for_logical_id(logical_id))] = int(logical_id)
+            for s in bank.slots:
+                if s.expert_key is not None:
+                    owners[s.slot_id] = int(s.expert_key.expert_id)
+            mapping = ExpertSlotMapping(
+                layer_id, active, torch.empty(0, dtype=torch.int32, device=device), tuple(owners), tuple(slot_ids),
+                log2phy_valid=False,
+            )
+        return PreparedSlotWeights.from_slot_bank(slot_bank=bank, mapping=mapping)
+
+    def prepare_prefill_stage_plan(self, *, layer_id: int, active_experts, num_logical_experts: int, device,
+                                   buffer_index: int, async_load: bool, wait_event=None, step_id: int | None = None,
+                                   build_log2phy: bool = True, known_miss: bool = False):
+        """Stage one wave into stage buffer `buffer_index`: slot i <- i-th
+        expert (D2D for main-bank hits, H2D for misses).  Returns
+        (prepared, ready_event or None, payload)."""
+        if not self.should_use_fixed_slots:
+            raise RuntimeError("prefill stage plan requested while fixed slots are disabled")
+        self._validate_prefill_buffer_index(int(buffer_index))
+        layer_id = int(layer_id)
+        if self.is_resident_layer(layer_id):
+            raise RuntimeError(f"prefill stage plan must not run on resident layer {layer_id}")
+        routed, total = self._resolve_fused_shared_counts(layer_id=layer_id, requested_logical_expert_count=num_logical_experts)
+        active = dedupe_preserve_order(active_experts)
+        _validate_active_expert_ids(layer_id=layer_id, active_experts=active, num_logical_experts=routed)
+        if len(active) > self.config.num_slots:
+            raise RuntimeError(f"prefill wave size {len(active)} exceeds num_slots={self.config.num_slots}")
+        src = self._slot_banks.get(layer_id)
+        if src is None:
+            raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
+        stage = self._get_prefill_stage_bank(layer_id=layer_id, buffer_index=int(buffer_index), template_bank=src)
+        if wait_event is None:
+            wait_event = self.prefill_stage_buffer_release_event(layer_id=layer_id, buffer_index=int(buffer_index))
+        table = self._get_prefill_stage_log2phy_buffer(
+            template_bank=src, buffer_index=int(buffer_index), num_logical_experts=total, device=device
+        )
+        step_id = self._step(step_id)
+        hits: list[int] = []
+        misses: list[int] = []
+        loads = []
+        if build_log2phy:
+            values = [-1] * total
+            for logical_id in stage.pinned_logical_ids:
+                values[logical_id] = int(stage.pinned_slot_for_logical_id(logical_id))
+        for i, e in enumerate(active):
+            key = ExpertKey(layer_id, e)
+            slot = (stage.assign_transient_slot if known_miss else stage.assign_slot)(i, key, step_id=step_id)
+            if build_log2phy:
+                values[e] = i
+            hit = None if known_miss else src.lookup(key)
+            if hit is not None and hit.state == SlotState.READY:
+                hits.append(e)
+                loads.append((hit.as_bundle(), slot))
+            else:
+                misses.append(e)
+                loads.append((self._host_store.get(layer_id, e), slot))
+        if build_log2phy:
+            table.copy_(torch.tensor(values, dtype=torch.int32), non_blocking=False)
+        ready = None
+        if loads:
+            if async_load:
+                try:
+                    ready = self._transfer_engine.load_many_async(loads, wait_event=wait_event, record_event=True, validate_layout=False)
+                except Exception:
+                    self._release_allocated_loads(stage, loads)
+                    raise
+            else:
+                if wait_event is not None:
+                    _synchronize_event(getattr(wait_event, "event", wait_event))
+                try:
+                    self._transfer_engine.load_many_sync(loads, validate_layout=False)
+                except Exception:
+                    self._release_allocated_loads(stage, loads)
+                    raise
+        for sid in range(len(active), len(stage.slots)):
+            stage.clear_slot(sid)
+        if async_load and ready is None:
+            ready = wait_event
+        owners: list[int | None] = [None] * stage.physical_expert_count
+        for logical_id in stage.pinned_logical_ids:
+            owners[int(stage.pinned_slot_for_logical_id(logical_id))] = int(logical_id)
+        for i, e in enumerate(active):
+            owners[i] = e
+        mapping = ExpertSlotMapping(layer_id, active, table, tuple(owners), tuple(range(len(active))), log2phy_valid=build_log2phy)
+        per = int(self._expert_weight_bytes_by_layer.get(layer_id, 0))
+        payload = {
+            "buffer_index": int(buffer_index),
+            "hit_experts": hits,
+            "miss_experts": misses,
+            "h2d_bytes": per * len(misses),
+            "d2d_bytes": per * len(hits),
+            "log2phy_built": bool(build_log2phy),
+            "known_miss": bool(known_miss),
+        }
+        return PreparedSlotWeights.from_slot_bank(slot_bank=stage, mapping=mapping), ready, payload
+
+    def prepare_full_layer_prefill_plan(self, *, layer_id: int, num_logical_experts: int, device,
+                                        step_id: int | None = None):
+        """Blocking reference plan: the whole layer in one layout-shared bank
+        with identity log2phy (the recoverable-fallback path)."""
+        if not self.should_use_fixed_slots:
+            raise RuntimeError("full-layer prefill plan requested while fixed slots are disabled")
+        layer_id = int(layer_id)
+        routed, total = self._resolve_fused_shared_counts(layer_id=layer_id, requested_logical_expert_count=num_logical_experts)
+        if self.is_resident_layer(layer_id):
+            raise RuntimeError(f"full-layer prefill plan must not run on resident layer {layer_id}")
+        tmpl = self._slot_banks.get(layer_id)
+        if tmpl is None:
+            raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
+        buf = self._host_store.get_layer_buffer(layer_id)
+        if int(buf.num_experts) != routed:
+            raise RuntimeError(f"host expert count for layer {layer_id} is {buf.num_experts}, expected {routed}")
+        key = (*self._pool_key(tmpl)[:2], routed, *self._pool_key(tmpl)[3:])
+        reused = key in self._full_layer_prefill_pool
+        bank = self._full_layer_prefill_pool.get(key)
+        if bank is None:
+            bank = ExpertSlotBank(
+                routed, tuple(int(d) for d in tmpl.w13_slots.shape[1:]), tuple(int(d) for d in tmpl.w2_slots.shape[1:]),
+                dtype=tmpl.w13_slots.dtype, device=tmpl.w13_slots.device, pinned_logical_ids=tmpl.pinned_logical_ids,
+            )
+            self._full_layer_prefill_pool[key] = bank
+            self._memory_ledger_cache = None
+        table = self._full_layer_prefill_log2phy.get(key)
+        if table is None:
+            values = list(range(routed)) + [int(bank.pinned_slot_for_logical_id(e)) for e in bank.pinned_logical_ids]
+            table = torch.tensor(values, dtype=torch.int32, device=device)
+            self._full_layer_prefill_log2phy[key] = table
+            self._memory_ledger_cache = None
+        step_id = self._step(step_id)
+        for e in range(routed):
+            bank.assign_transient_slot(e, ExpertKey(layer_id, e), step_id=step_id)
+        start = perf_counter()
+        try:
+            bank.w13_slots[:routed].copy_(buf.w13)
+            bank.w2_slots[:routed].copy_(buf.w2)
+            bank.copy_pinned_weights_from(tmpl)
+        except Exception:
+            for sid in range(routed):
+                bank.clear_slot(sid, force=True)
+            raise
+        for sid in range(routed):
+            bank.mark_ready(sid)
+        all_experts = tuple(range(routed))
+        owners: list[int | None] = list(all_experts) + [int(e) for e in bank.pinned_logical_ids]
+        mapping = ExpertSlotMapping(layer_id, all_experts, table, tuple(owners), all_experts)
+        prepared = PreparedSlotWeights.from_slot_bank(slot_bank=bank, mapping=mapping)
+        payload = {
+            "execution_mode": "reference_full_layer",
+            "num_logical_experts": total,
+            "routed_expert_count": routed,
+            "pinned_shared_expert_count": len(bank.pinned_logical_ids),
+            "physical_expert_count": int(prepared.physical_expert_count),
+            "h2d_bytes": int(buf.total_bytes),
+            "stage_ms": round((perf_counter() - start) * 1000.0, 3),
+            "pool_reused": bool(reused),
+        }
+        return prepared, payload
+
+    # ------------------------------------------------------ route stats
+    @staticmethod
+    def _route_stats_key(*, layer_id: int, topk_ids: torch.Tensor) -> tuple:
+        try:
+            version = int(topk_ids._version)
+        except RuntimeError:
+            version = 0
+        return (
+            int(layer_id), str(topk_ids.device), str(topk_ids.dtype), tuple(int(d) for d in topk_ids.shape),
+            tuple(int(s) for s in topk_ids.stride()), int(topk_ids.storage_offset()), int(topk_ids.numel()),
+            int(topk_ids.data_ptr()), version,
+        )
+
+    def cache_prefill_route_stats(self, *, layer_id: int, topk_ids: torch.Tensor, token_counts_by_expert: dict[int, int],
+                                  pair_offsets_by_expert=None) -> MoePrefillRouteStats:
+        """Remember the histogram the stage seam already paid a D2H for."""
+        counts = {int(e): int(c) for e, c in token_counts_by_expert.items() if int(c) > 0}
+        offs = None
+        if pair_offsets_by_expert is not None:
+            offs = {int(e): tuple(int(o) for o in v) for e, v in pair_offsets_by_expert.items() if int(e) in counts}
+        stats = MoePrefillRouteStats(
+            layer_id=int(layer_id),
+            topk_cache_key=self._route_stats_key(layer_id=layer_id, topk_ids=topk_ids),
+            token_counts_by_expert=counts,
+            active_experts=tuple(sorted(counts)),
+            num_tokens=int(topk_ids.shape[0]) if topk_ids.ndim > 0 else 0,
+            top_k=int(topk_ids.shape[1]) if topk_ids.ndim > 1 else 1,
+            pair_offsets_by_expert=offs,
+        )
+        self._prefill_route_stats_by_layer[int(layer_id)] = stats
+        return stats
+
+    def consume_prefill_route_stats_record(self, *, layer_id: int, topk_ids: torch.Tensor) -> MoePrefillRouteStats | None:
+        stats = self._prefill_route_stats_by_layer.pop(int(layer_id), None)
+        if stats is None or stats.topk_cache_key != self._route_stats_key(layer_id=layer_id, topk_ids=topk_ids):
+            return None
+        return stats
+
+    def consume_prefill_route_stats(self, *, layer_id: int, topk_ids: torch.Tensor) -> dict[int, int] | None:
+        stats = self.consume_prefill_route_stats_record(layer_id=layer_id, topk_ids=topk_ids)
+        return None if stats is None else dict(stats.token_counts_by_expert)
+
+
+# ---------------------------------------------------------------------------
+def _synchronize_event(ev: object) -> None:
+    sync = getattr(ev, "synchronize", None)
+    if callable(sync):
+        sync()
+        return
+    wait = getattr(ev, "wait", None)
+    if callable(wait):
+        wait()
+
+
+def _current_stream_for(ready_event):
+    ev = getattr(ready_event, "event", None)
+    if isinstance(ev, torch.cuda.Event) and torch.cuda.is_available():
+        return torch.cuda.current_stream()
+    return _NullStream()
+
+
+class _NullStream:
+    def wait_event(self, _event) -> None:  # host-only slot banks need no ordering
+        return None
+
+
+def _validate_active_expert_ids(*, layer_id: int, active_experts, num_logical_experts: int) -> None:
+    bad = [int(e) for e in active_experts if int(e) < 0 or int(e) >= int(num_logical_experts)]
+    if bad:
+        raise ValueError(
+            f"fixed-slot active expert id out of range: layer_id={int(layer_id)}, "
+            f"num_logical_experts={int(num_logical_experts)}, expert_ids={bad}"
+        )
+
+
+def _update_log2phy_entries(log2phy: torch.Tensor, *, expert_ids, slot_ids) -> None:
+    """Write the changed entries of a persistent log2phy in one tensor op."""
+    if len(expert_ids) != len(slot_ids):
+        raise ValueError(f"expert_ids and slot_ids length mismatch: {len(expert_ids)} != {len(slot_ids)}")
+    if not expert_ids:
+        return
+    if len(expert_ids) == 1:
+        log2phy[int(expert_ids[0])] = int(slot_ids[0])
+        return
+    idx = torch.tensor([int(e) for e in expert_ids], dtype=torch.long).to(log2phy.device, non_blocking=False)
+    val = torch.tensor([int(s) for s in slot_ids], dtype=log2phy.dtype).to(log2phy.device, non_blocking=False)
+    log2phy.index_copy_(0, idx, val)
+
+
+_runtime: MoeOffloadRuntime | None = None
+
+
+def get_moe_offload_runtime() -> MoeOffloadRuntime:
+    global _runtime
+    if _runtime is None:
+        _runtime = MoeOffloadRuntime()
+    return _runtime
+
+
+def reset_moe_offload_runtime() -> None:
+    global _runtime
+    _runtime = None

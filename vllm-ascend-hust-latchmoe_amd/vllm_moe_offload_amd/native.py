@@ -1,0 +1,450 @@
+"""ctypes binding of liblatchmoe_hip.so (the gfx950 hot-path kernels).
+
+Every wrapper takes torch tensors that already live on the GPU, checks shape,
+dtype and contiguity on the host, and launches on the current torch stream
+(or the stream given).  Nothing here falls back to a CPU or PyTorch
+implementation: if the library is missing the import of a wrapper raises.
+
+The C declarations live in include/latchmoe.h; `EXPORTED_SYMBOLS` lists them.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "liblatchmoe_hip.so"
+
+LMOE_SCORING_SOFTMAX = 0
+LMOE_SCORING_SIGMOID = 1
+LMOE_PATH_AUTO = 0
+LMOE_PATH_GEMV = 1
+LMOE_PATH_MFMA = 2
+META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
+META_COUNT = 4
+MFMA_BLOCK_M = 128
+FUSED_DECODE_MAX_PAIRS = 1024
+
+EXPORTED_SYMBOLS = (
+    "lmoe_status_string",
+    "lmoe_abi_version",
+    "lmoe_router_gate",
+    "lmoe_router_topk",
+    "lmoe_permute_workspace_bytes",
+    "lmoe_permute",
+    "lmoe_gather_rows",
+    "lmoe_grouped_mlp",
+    "lmoe_combine",
+    "lmoe_fused_moe_decode",
+    "lmoe_stage_copy",
+)
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+_SIGNATURES = {
+    "lmoe_status_string": (ctypes.c_char_p, [_i]),
+    "lmoe_abi_version": (_i, []),
+    "lmoe_router_gate": (_i, [_vp, _vp, _i, _i, _i, _vp, _i, _vp]),
+    "lmoe_router_topk": (
+        _i,
+        [_vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp],
+    ),
+    "lmoe_permute_workspace_bytes": (_sz, [_i, _i]),
+    "lmoe_permute": (
+        _i,
+        [_vp, _i, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "lmoe_gather_rows": (_i, [_vp, _i, _i, _vp, _vp, _i, _vp, _vp]),
+    "lmoe_grouped_mlp": (
+        _i,
+        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp],
+    ),
+    "lmoe_combine": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "lmoe_fused_moe_decode": (
+        _i,
+        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
+    "lmoe_stage_copy": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    """liblatchmoe_hip.so is not built; there is no fallback path."""
+
+
+def library_path() -> Path:
+    override = os.environ.get("LATCHMOE_HIP_LIB")
+    return Path(override) if override else LIB_PATH
+
+
+def load_library() -> ctypes.CDLL:
+    """Load (once) and return the HIP kernel library, raising if absent."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not path.exists():
+        raise NativeLibraryMissing(
+            f"{path} is missing: build it with "
+            "`python vllm-ascend-hust-latchmoe_amd/build_native.py` "
+            "(the slot-indexed MoE path has no CPU or PyTorch fallback)"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _LIB = lib
+    return lib
+
+
+def _check(status: int, fn: str) -> None:
+    if status != 0:
+        msg = load_library().lmoe_status_string(int(status))
+        raise RuntimeError(f"{fn} failed with status {status}: {msg.decode()}")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else int(t.data_ptr())
+
+
+def _stream(stream: torch.cuda.Stream | None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device tensor, got {t.device}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
+# ---------------------------------------------------------------------------
+# router
+# ---------------------------------------------------------------------------
+def router_gate(x: torch.Tensor, wg: torch.Tensor, logits: torch.Tensor, *, stream=None) -> torch.Tensor:
+    """logits = x . wg^T with f32 accumulation (bf16 or f32 output)."""
+    lib = load_library()
+    T, H = x.shape
+    E = wg.shape[0]
+    _need(x, "x", torch.bfloat16)
+    _need(wg, "wg", torch.bfloat16, (E, H))
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("logits must be bf16 or f32")
+    _need(logits, "logits", logits.dtype, (T, E))
+    _check(
+        lib.lmoe_router_gate(_ptr(x), _ptr(wg), T, H, E, _ptr(logits),
+                             int(logits.dtype == torch.float32), _stream(stream)),
+        "lmoe_router_gate",
+    )
+    return logits
+
+
+def router_topk(
+    logits: torch.Tensor,
+    top_k: int,
+    *,
+    scoring: str = "softmax",
+    bias: torch.Tensor | None = None,
+    num_expert_group: int = 1,
+    topk_group: int = 1,
+    renormalize: bool = True,
+    routed_scaling_factor: float = 1.0,
+    w_bf16: torch.Tensor | None = None,
+    ids: torch.Tensor | None = None,
+    w_f32: torch.Tensor | None = None,
+    stream=None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """Select top_k experts per token; returns (w_bf16 [T,k], ids int32 [T,k], w_f32)."""
+    lib = load_library()
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("logits must be bf16 or f32")
+    _need(logits, "logits", logits.dtype)
+    T, E = logits.shape
+    if scoring == "softmax":
+        mode = LMOE_SCORING_SOFTMAX
+    elif scoring == "sigmoid":
+        mode = LMOE_SCORING_SIGMOID
+    else:
+        raise ValueError(f"unsupported scoring function {scoring!r}")
+    if bias is not None:
+        _need(bias, "e_score_correction_bias", torch.float32, (E,))
+    dev = logits.device
+    if w_bf16 is None:
+        w_bf16 = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
+    if ids is None:
+        ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    _need(w_bf16, "topk_weights", torch.bfloat16, (T, top_k))
+    _need(ids, "topk_ids", torch.int32, (T, top_k))
+    if w_f32 is not None:
+        _need(w_f32, "w_f32", torch.float32, (T, top_k))
+    _check(
+        lib.lmoe_router_topk(
+            _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), mode,
+            _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
+            int(bool(renormalize)), float(routed_scaling_factor),
+            _ptr(w_f32), _ptr(w_bf16), _ptr(ids), _stream(stream),
+        ),
+        "lmoe_router_topk",
+    )
+    return w_bf16, ids, w_f32
+
+
+# ---------------------------------------------------------------------------
+# permutation
+# ---------------------------------------------------------------------------
+@dataclass
+class Permutation:
+    """Device outputs of lmoe_permute for one (n_pairs, n_slots) shape.
+
+    Buffers are allocated once and reused (fixed addresses, graph safe).
+    """
+
+    n_pairs: int
+    n_slots: int
+    counts: torch.Tensor        # [P] i32 histogram (expert_tokens, count type)
+    offsets: torch.Tensor       # [P+1] i32
+    sorted_pairs: torch.Tensor  # [N] i32 flat pair at each sorted position
+    row_idx: torch.Tensor       # [N] i32 sorted position of each pair (expanded_row_idx) or -1
+    active: torch.Tensor        # [P] i32 slots with count > 0, ascending
+    tile_off: torch.Tensor      # [P+1] i32 MFMA tile prefix
+    meta: torch.Tensor          # [4] i32
+    workspace: torch.Tensor     # int8 scratch for the multi-block path
+
+    @classmethod
+    def allocate(cls, n_pairs: int, n_slots: int, device) -> "Permutation":
+        lib = load_library()
+        ws = int(lib.lmoe_permute_workspace_bytes(int(n_pairs), int(n_slots)))
+        i32 = dict(dtype=torch.int32, device=device)
+        return cls(
+            n_pairs=int(n_pairs),
+            n_slots=int(n_slots),
+            counts=torch.zeros(n_slots, **i32),
+            offsets=torch.zeros(n_slots + 1, **i32),
+            sorted_pairs=torch.zeros(max(1, n_pairs), **i32),
+            row_idx=torch.zeros(max(1, n_pairs), **i32),
+            active=torch.zeros(n_slots, **i32),
+            tile_off=torch.zeros(n_slots + 1, **i32),
+            meta=torch.zeros(META_COUNT, **i32),
+            workspace=torch.empty(max(ws, 1), dtype=torch.int8, device=device),
+        )
+
+
+def permute(
+    ids: torch.Tensor,
+    perm: Permutation,
+    *,
+    log2phy: torch.Tensor | None = None,
+    skip_unmapped: bool = False,
+    table_len: int | None = None,
+    block_m: int = MFMA_BLOCK_M,
+    stream=None,
+) -> Permutation:
+    """Remap ids through log2phy and stable-sort the flat pairs by slot.
+
+    table_len (<= log2phy.numel()) limits the ids the table covers; with
+    skip_unmapped, ids past it are left to another pass."""
+    lib = load_library()
+    _need(ids, "topk_ids", torch.int32)
+    n = int(ids.numel())
+    if n != perm.n_pairs:
+        raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {n}")
+    n_table = 0
+    if log2phy is not None:
+        _need(log2phy, "log2phy", torch.int32)
+        n_table = int(log2phy.numel()) if table_len is None else min(int(table_len), int(log2phy.numel()))
+    _check(
+        lib.lmoe_permute(
+            _ptr(ids), n, _ptr(log2phy), n_table,
+            perm.n_slots, int(bool(skip_unmapped)), int(block_m),
+            _ptr(perm.counts), _ptr(perm.offsets), _ptr(perm.sorted_pairs),
+            _ptr(perm.row_idx), _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta),
+            _ptr(perm.workspace), int(perm.workspace.numel()), _stream(stream),
+        ),
+        "lmoe_permute",
+    )
+    return perm
+
+
+def gather_rows(x: torch.Tensor, top_k: int, perm: Permutation, out: torch.Tensor | None = None,
+                *, stream=None) -> torch.Tensor:
+    """expanded_x: out[pos] = x[sorted_pairs[pos] // top_k]."""
+    lib = load_library()
+    _need(x, "x", torch.bfloat16)
+    H = x.shape[1]
+    if out is None:
+        out = torch.empty((perm.n_pairs, H), dtype=torch.bfloat16, device=x.device)
+    _need(out, "x_sorted", torch.bfloat16, (perm.n_pairs, H))
+    _check(
+        lib.lmoe_gather_rows(_ptr(x), H, int(top_k), _ptr(perm.sorted_pairs), _ptr(perm.meta),
+                             perm.n_pairs, _ptr(out), _stream(stream)),
+        "lmoe_gather_rows",
+    )
+    return out
+
+
+# ---------------------------------------------------------------------------
+# expert MLP and combine
+# ---------------------------------------------------------------------------
+def _check_bank(w13: torch.Tensor, w2: torch.Tensor, H: int) -> tuple[int, int]:
+    _need(w13, "w13_slots", torch.bfloat16)
+    _need(w2, "w2_slots", torch.bfloat16)
+    if w13.dim() != 3 or w2.dim() != 3:
+        raise ValueError("slot banks must be [P, 2I, H] and [P, H, I]")
+    P, two_i, h = w13.shape
+    if h != H or two_i % 2 != 0:
+        raise ValueError(f"w13_slots shape {tuple(w13.shape)} does not match H={H}")
+    I = two_i // 2
+    if tuple(w2.shape) != (P, H, I):
+        raise ValueError(f"w2_slots shape {tuple(w2.shape)} != {(P, H, I)}")
+    return P, I
+
+
+def grouped_mlp(
+    x: torch.Tensor,
+    top_k: int,
+    w13_slots: torch.Tensor,
+    w2_slots: torch.Tensor,
+    perm: Permutation,
+    act: torch.Tensor,
+    y: torch.Tensor,
+    *,
+    path: int = LMOE_PATH_AUTO,
+    stream=None,
+) -> torch.Tensor:
+    """y[pair] = W2_s . (silu(W13_s[:I] x) * W13_s[I:] x) for the placed pairs."""
+    lib = load_library()
+    _need(x, "x", torch.bfloat16)
+    T, H = x.shape
+    P, I = _check_bank(w13_slots, w2_slots, H)
+    if P != perm.n_slots:
+        raise ValueError(f"slot bank has {P} slots, permutation {perm.n_slots}")
+    if perm.n_pairs != T * top_k:
+        raise ValueError("permutation does not match T * top_k pairs")
+    _need(act, "act", torch.bfloat16, (perm.n_pairs, I))
+    _need(y, "y", torch.bfloat16, (perm.n_pairs, H))
+    _check(
+        lib.lmoe_grouped_mlp(
+            _ptr(x), T, H, I, int(top_k), _ptr(w13_slots), _ptr(w2_slots), P,
+            _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.active), _ptr(perm.tile_off),
+            _ptr(perm.meta), perm.n_pairs, MFMA_BLOCK_M, int(path), _ptr(act), _ptr(y),
+            _stream(stream),
+        ),
+        "lmoe_grouped_mlp",
+    )
+    return y
+
+
+def combine(
+    y: torch.Tensor,
+    topk_weights: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    row_mask: torch.Tensor | None = None,
+    add: torch.Tensor | None = None,
+    stream=None,
+) -> torch.Tensor:
+    """out[t] = add[t] + sum_j w[t,j] * y[t*k+j] (pairs with row_mask < 0 skipped)."""
+    lib = load_library()
+    _need(topk_weights, "topk_weights", torch.bfloat16)
+    T, k = topk_weights.shape
+    _need(y, "y", torch.bfloat16)
+    H = y.shape[1]
+    if y.shape[0] < T * k:
+        raise ValueError("y has fewer rows than pairs")
+    _need(out, "out", torch.bfloat16, (T, H))
+    if row_mask is not None:
+        _need(row_mask, "row_mask", torch.int32)
+    if add is not None:
+        _need(add, "add", torch.bfloat16, (T, H))
+    _check(
+        lib.lmoe_combine(_ptr(y), _ptr(row_mask), _ptr(topk_weights), T, k, H, _ptr(add),
+                         _ptr(out), _stream(stream)),
+        "lmoe_combine",
+    )
+    return out
+
+
+def fused_moe_decode(
+    x: torch.Tensor,
+    topk_weights: torch.Tensor,
+    w13_slots: torch.Tensor,
+    w2_slots: torch.Tensor,
+    perm: Permutation,
+    act: torch.Tensor,
+    out: torch.Tensor,
+    *,
+    add: torch.Tensor | None = None,
+    stream=None,
+) -> torch.Tensor:
+    """Decode layer body: gate_up GEMV, then down GEMV fused with the combine."""
+    lib = load_library()
+    _need(x, "x", torch.bfloat16)
+    T, H = x.shape
+    _need(topk_weights, "topk_weights", torch.bfloat16)
+    k = topk_weights.shape[1]
+    P, I = _check_bank(w13_slots, w2_slots, H)
+    if perm.n_pairs != T * k or perm.n_slots != P:
+        raise ValueError("permutation does not match the batch or the slot bank")
+    if T * k > FUSED_DECODE_MAX_PAIRS:
+        raise ValueError(f"fused decode supports at most {FUSED_DECODE_MAX_PAIRS} pairs")
+    _need(act, "act", torch.bfloat16, (perm.n_pairs, I))
+    _need(out, "out", torch.bfloat16, (T, H))
+    if add is not None:
+        _need(add, "add", torch.bfloat16, (T, H))
+    _check(
+        lib.lmoe_fused_moe_decode(
+            _ptr(x), T, H, I, k, _ptr(w13_slots), _ptr(w2_slots), P, _ptr(topk_weights),
+            _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.row_idx), _ptr(perm.active),
+            _ptr(perm.meta), _ptr(add), _ptr(act), _ptr(out), _stream(stream),
+        ),
+        "lmoe_fused_moe_decode",
+    )
+    return out
+
+
+# ---------------------------------------------------------------------------
+# staging
+# ---------------------------------------------------------------------------
+def stage_copy(
+    copies: list[tuple[int, int, int]],
+    transfer_stream: torch.cuda.Stream,
+    *,
+    wait_event: torch.cuda.Event | None = None,
+    done_event: torch.cuda.Event | None = None,
+) -> None:
+    """Queue (dst_ptr, src_ptr, nbytes) copies on transfer_stream.
+
+    The stream first waits for wait_event (slot release) and done_event is
+    recorded after the batch; both are torch events, ordered through torch so
+    their lazily created handles stay valid.
+    """
+    lib = load_library()
+    if wait_event is not None:
+        transfer_stream.wait_event(wait_event)
+    n = len(copies)
+    dst = (ctypes.c_void_p * max(n, 1))(*[c[0] for c in copies])
+    src = (ctypes.c_void_p * max(n, 1))(*[c[1] for c in copies])
+    nbytes = (ctypes.c_size_t * max(n, 1))(*[c[2] for c in copies])
+    _check(
+        lib.lmoe_stage_copy(dst, src, nbytes, n, int(transfer_stream.cuda_stream), None, None),
+        "lmoe_stage_copy",
+    )
+    if done_event is not None:
+        done_event.record(transfer_stream)
