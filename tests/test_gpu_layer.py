@@ -1,0 +1,168 @@
+"""End-to-end slot-bank MoE layer on the GPU: routing, eager staging (H2D on
+the transfer stream, event-ordered), slot-bank MLP, capacity waves with one
+combine, hipGraph replay with fixed slot addresses, and the DeepSeek-style
+grouped router with a pinned shared expert.  Checked against the oracle
+(routing bit-exact on the same logits; outputs within 2e-2 x RMS)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mlp as omlp
+from oracle import router as orouter
+from oracle.bf16 import bf16_to_f32, f32_to_bf16, normal_bf16
+from tests._util import OUT_TOL, from_dev_bf16, rel_max_err, to_dev_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _mods():
+    from vllm_moe_offload_amd import fused_moe
+    from vllm_moe_offload_amd.layer import SlotMoELayer
+    from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+    from vllm_moe_offload_amd.moe_offload.runtime import MoeOffloadRuntime
+
+    return fused_moe, SlotMoELayer, MoeOffloadConfig, MoeOffloadRuntime
+
+
+def _weights(rng, E, H, I):
+    return normal_bf16(rng, (E, 2 * I, H), 0.02), normal_bf16(rng, (E, H, I), 0.02), normal_bf16(rng, (E, H), 0.02)
+
+
+def _oracle_layer(x, ids, wb, w13, w2, shared=None):
+    return omlp.moe_layer(x, ids, wb, None, w13, w2, shared=shared)
+
+
+def test_decode_steps_with_lru_staging_match_oracle():
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(11)
+    E, H, I, k, B, slots = 64, 1024, 256, 8, 4, 32  # 32 >= B*k distinct experts
+    w13, w2, wg = _weights(rng, E, H, I)
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True, graph_compatible_offload=True))
+    layer = SlotMoELayer(layer_id=0, runtime=rt, gate_weight=to_dev_bf16(wg), w13_weight=torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16),
+                         w2_weight=torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16), top_k=k)
+    layer.register()
+    assert rt.host_store.get_layer_buffer(0).w13.is_pinned()
+    total_misses = 0
+    for step in range(12):
+        print(f"case decode-step {step}", flush=True)
+        x = normal_bf16(rng, (B, H), 1.0)
+        dx = to_dev_bf16(x)
+        logits = torch.empty((B, E), dtype=torch.bfloat16, device="cuda")
+        w, ids, _ = fused_moe.route(dx, layer.gate_weight, layer.router_spec, logits_out=logits)
+        out = layer.forward(dx).clone()
+        torch.cuda.synchronize()
+        r_ids, _, r_wb = orouter.softmax_topk(bf16_to_f32(from_dev_bf16(logits)), k)
+        np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
+        np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
+        ref = _oracle_layer(x, r_ids, r_wb, w13, w2)
+        assert rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref) <= OUT_TOL
+        total_misses += rt.transfer_engine.copies_issued
+    assert rt.transfer_engine.bytes_issued > 0
+
+
+def test_wave_prefill_equals_full_layer_bitwise_and_oracle():
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(12)
+    E, H, I, k, T, slots = 64, 1024, 256, 8, 384, 16
+    w13, w2, wg = _weights(rng, E, H, I)
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True, b2_wave_prefill=True))
+    layer = SlotMoELayer(layer_id=1, runtime=rt, gate_weight=to_dev_bf16(wg), w13_weight=torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16),
+                         w2_weight=torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16), top_k=k)
+    layer.register()
+    x = normal_bf16(rng, (T, H), 1.0)
+    dx = to_dev_bf16(x)
+    w, ids, logits = fused_moe.route(dx, layer.gate_weight, layer.router_spec)
+    out_w, report = fused_moe.run_wave_prefill(rt, layer_id=1, hidden=dx, topk_weights=w, topk_ids=ids, num_logical_experts=E)
+    out_w = out_w.clone()
+    out_f = fused_moe.run_full_layer(rt, layer_id=1, hidden=dx, topk_weights=w, topk_ids=ids, num_logical_experts=E).clone()
+    torch.cuda.synchronize()
+    print(f"waves {len(report.waves)} h2d {report.h2d_bytes} issue {report.issue_log[:6]}", flush=True)
+    assert len(report.waves) == 4 and report.h2d_bytes > 0
+    ndiff = int((out_w.view(torch.int16) != out_f.view(torch.int16)).sum().item())
+    print(f"wave vs full-layer differing elements: {ndiff}", flush=True)
+    assert ndiff == 0
+    ref = _oracle_layer(x, ids.cpu().numpy(), from_dev_bf16(w), w13, w2)
+    assert rel_max_err(bf16_to_f32(from_dev_bf16(out_w)), ref) <= OUT_TOL
+    # the seam path defers the overflow and runs the same waves
+    out_seam = layer.forward(dx, phase=1).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(out_seam.view(torch.int16), out_w.view(torch.int16))
+
+
+def test_graph_replay_keeps_slot_addresses_and_follows_restaging():
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(13)
+    E, H, I, k, B, slots = 32, 512, 128, 4, 2, 8
+    w13, w2, wg = _weights(rng, E, H, I)
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True, graph_compatible_offload=True))
+    layer = SlotMoELayer(layer_id=2, runtime=rt, gate_weight=to_dev_bf16(wg), w13_weight=torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16),
+                         w2_weight=torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16), top_k=k)
+    layer.register()
+    static_x = torch.zeros((B, H), dtype=torch.bfloat16, device="cuda")
+    static_w = torch.zeros((B, k), dtype=torch.bfloat16, device="cuda")
+    static_ids = torch.zeros((B, k), dtype=torch.int32, device="cuda")
+    static_out = torch.zeros((B, H), dtype=torch.bfloat16, device="cuda")
+    prepared = rt.capture_safe_slot_weights(layer_id=2)
+    ws = fused_moe.get_workspace(B, k, prepared.physical_expert_count, H, I, "cuda", tag="graph")
+
+    def piece2():
+        fused_moe.fused_experts(static_x, static_w, static_ids, prepared.w1, prepared.w2, prepared.log2phy, out=static_out, workspace=ws)
+
+    # stage once so the capture run is valid, warm up, capture
+    x0 = to_dev_bf16(normal_bf16(rng, (B, H), 1.0))
+    w0, ids0, _ = fused_moe.route(x0, layer.gate_weight, layer.router_spec)
+    rt.stage_fixed_slot_plan(layer_id=2, active_experts=tuple(sorted(set(ids0.cpu().flatten().tolist()))), num_logical_experts=E)
+    static_x.copy_(x0), static_w.copy_(w0), static_ids.copy_(ids0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        piece2()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        piece2()
+    fp = rt._slot_address_fingerprint(2)
+    for step in range(6):
+        x = normal_bf16(rng, (B, H), 1.0)
+        dx = to_dev_bf16(x)
+        w, ids, _ = fused_moe.route(dx, layer.gate_weight, layer.router_spec)
+        rt.stage_fixed_slot_plan(layer_id=2, active_experts=tuple(sorted(set(ids.cpu().flatten().tolist()))), num_logical_experts=E)
+        static_x.copy_(dx), static_w.copy_(w), static_ids.copy_(ids)
+        g.replay()
+        torch.cuda.synchronize()
+        assert rt._slot_address_fingerprint(2) == fp
+        ref = _oracle_layer(x, ids.cpu().numpy(), from_dev_bf16(w), w13, w2)
+        err = rel_max_err(bf16_to_f32(from_dev_bf16(static_out)), ref)
+        print(f"replay {step} err {err:.3e}", flush=True)
+        assert err <= OUT_TOL
+
+
+def test_deepseek_style_grouped_router_with_pinned_shared_expert():
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(14)
+    E, H, I, k, B, slots, G, TG = 64, 1024, 256, 8, 3, 32, 8, 4
+    w13, w2, wg = _weights(rng, E, H, I)
+    s13 = normal_bf16(rng, (2 * I, H), 0.02)
+    s2 = normal_bf16(rng, (H, I), 0.02)
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True))
+    tb = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+    layer = SlotMoELayer(layer_id=3, runtime=rt, gate_weight=to_dev_bf16(wg), w13_weight=tb(w13), w2_weight=tb(w2), top_k=k,
+                         scoring_func="sigmoid", use_grouped_topk=True, num_expert_group=G, topk_group=TG,
+                         routed_scaling_factor=2.5, e_score_correction_bias=torch.from_numpy(bias).cuda(),
+                         shared_w13=tb(s13), shared_w2=tb(s2))
+    layer.register()
+    assert layer.mix_placement and rt.slot_bank(3).pinned_slot_ids == (slots,)
+    x = normal_bf16(rng, (B, H), 1.0)
+    dx = to_dev_bf16(x)
+    logits = torch.empty((B, E), dtype=torch.bfloat16, device="cuda")
+    fused_moe.route(dx, layer.gate_weight, layer.router_spec, logits_out=logits)
+    out = layer.forward(dx).clone()
+    torch.cuda.synchronize()
+    r_ids, _, r_wb = orouter.grouped_sigmoid_topk(bf16_to_f32(from_dev_bf16(logits)), k, bias=bias, n_group=G,
+                                                  topk_group=TG, scale=2.5)
+    ref = _oracle_layer(x, r_ids, r_wb, w13, w2, shared=(s13, s2))
+    err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
+    print(f"deepseek-style err {err:.3e}", flush=True)
+    assert err <= OUT_TOL

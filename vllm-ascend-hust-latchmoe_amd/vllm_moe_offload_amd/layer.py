@@ -129,9 +129,9 @@ class SlotMoELayer(torch.nn.Module):
 
     def stage(self, topk_ids: torch.Tensor, phase: int = PHASE_DECODE) -> None:
         """Eager seam between the pieces."""
-        from vllm_moe_offload_amd.ops.fused_moe.moe_offload_stage_op import _moe_offload_stage_impl
+        from vllm_moe_offload_amd.ops.fused_moe.moe_offload_stage_op import stage_topk_for_layer
 
-        _moe_offload_stage_impl(topk_ids, self.layer_id, self.num_logical_experts, int(phase))
+        stage_topk_for_layer(self.runtime, topk_ids, self.layer_id, self.num_logical_experts, int(phase))
 
     def shared_expert_forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.shared_w13 is None:

@@ -78,9 +78,16 @@ def count_active_experts_from_cpu_topk(flat_topk_ids: torch.Tensor, *, num_logic
 
 
 def _moe_offload_stage_impl(topk_ids: torch.Tensor, layer_id: int, num_logical_experts: int, phase: int) -> None:
-    from vllm_moe_offload_amd.moe_offload.runtime import _is_current_graph_capturing, get_moe_offload_runtime
+    from vllm_moe_offload_amd.moe_offload.runtime import get_moe_offload_runtime
 
-    runtime = get_moe_offload_runtime()
+    stage_topk_for_layer(get_moe_offload_runtime(), topk_ids, layer_id, num_logical_experts, phase)
+
+
+def stage_topk_for_layer(runtime, topk_ids: torch.Tensor, layer_id: int, num_logical_experts: int, phase: int) -> None:
+    """The seam's staging decision for one layer of the given runtime."""
+    from vllm_moe_offload_amd.moe_offload import runtime as runtime_mod
+
+    _is_current_graph_capturing = runtime_mod._is_current_graph_capturing
     layer_id = int(layer_id)
     routed = runtime.routed_expert_count_for_layer(layer_id=layer_id, fallback=int(num_logical_experts))
     total = runtime.total_logical_expert_count_for_layer(layer_id=layer_id, fallback=int(num_logical_experts))
