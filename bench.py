@@ -1,0 +1,774 @@
+#!/usr/bin/env python3
+"""Benchmark of the slot-indexed fused-MoE hot path on one MI355X.
+
+Headline (value): Qwen3-30B-A3B-shaped decode, 48 MoE layers, 64 slots per
+layer, batch 1 — MoE-layer microseconds per token per layer, measured as the
+hipGraph replay of the 48-layer decode compute (router -> permute -> gate_up
+GEMV -> down GEMV + combine per layer) after the step's eager staging has
+made every routed expert resident.  Also reported in the same JSON line:
+
+  decode[B]   B in --batches: graph-replayed layer us/token, layer HBM GB/s,
+              slot-miss rate of the Zipf-skewed router, and the eager
+              staging-inclusive step time (D2H of the ids, LRU, H2D)
+  roofline    dominant kernel (gate_up GEMV + SiLU*mul at B=1), timed with
+              HIP events over launches rotating through the 48 layers
+  prefill     4096 tokens, 48 slots, uniform router: capacity waves with one
+              combine (compute TFLOP/s and MFMA fraction; staged wall time;
+              H2D GB/s), against the blocking full layer
+  staging     forced k misses per layer per step (k in 1, 4, 8): H2D GB/s on
+              the transfer stream and the fraction of compute overlapped,
+              with per-layer graph replays and stable slot addresses
+  deepseek    DeepSeek-V3-style layer (H 7168, E 256, I 2048, grouped
+              sigmoid router, pinned shared expert): decode us/token
+  cpu_baseline  the numpy oracle of the same layer on the host cores
+
+Synthetic data: weights N(0, 0.02) bf16 and hidden states N(0, 1) from fixed
+seeds.  To bound page-locked host memory the 48 layers share one 128-expert
+pinned host store (1.2 GB); every miss still moves its full 9,437,184 bytes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "vllm-ascend-hust-latchmoe_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+
+H, E, I, K = 2048, 128, 768, 8  # Qwen3-30B-A3B MoE layer
+EXPERT_BYTES = 3 * H * I * 2    # 9,437,184
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def zipf_bias(seed: int, n: int = E, s: float = 1.1) -> list[float]:
+    """Seeded Zipf(s) rank permutation mapped linearly onto [-2, +2] logits."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    ranks = rng.permutation(n) + 1
+    logp = -s * np.log(ranks.astype(np.float64))
+    lo, hi = -s * math.log(n), 0.0
+    return list((-2.0 + 4.0 * (logp - lo) / (hi - lo)).astype(np.float32))
+
+
+class Timer:
+    """HIP-event timer on a stream."""
+
+    def __init__(self, stream=None):
+        import torch
+
+        self.stream = stream or torch.cuda.current_stream()
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def __enter__(self):
+        self.a.record(self.stream)
+        return self
+
+    def __exit__(self, *exc):
+        self.b.record(self.stream)
+
+    def ms(self) -> float:
+        self.b.synchronize()
+        return float(self.a.elapsed_time(self.b))
+
+
+# ---------------------------------------------------------------------------
+# C2: 48-layer decode
+# ---------------------------------------------------------------------------
+class DecodeModel:
+    def __init__(self, n_layers: int, num_slots: int, host_w13, host_w2, seed: int = 1):
+        import torch
+
+        from vllm_moe_offload_amd.fused_moe import RouterSpec
+        from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+        from vllm_moe_offload_amd.moe_offload.runtime import MoeOffloadRuntime
+
+        self.L = n_layers
+        self.rt = MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=num_slots, async_load=True,
+                                                     graph_compatible_offload=True, b2_wave_prefill=True))
+        dev = torch.device("cuda")
+        g = torch.Generator(device=dev)
+        self.gates, self.specs = [], []
+        for l in range(n_layers):
+            g.manual_seed(seed * 1000 + l)
+            self.gates.append((torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+            bias = torch.tensor(zipf_bias(seed * 7919 + l), dtype=torch.float32, device=dev)
+            self.specs.append(RouterSpec(top_k=K, scoring_func="softmax", renormalize=True, e_score_correction_bias=bias))
+            self.rt.register_host_buffers(layer_id=l, w13_host=host_w13, w2_host=host_w2, slot_device=dev)
+
+    def bank(self, l):
+        return self.rt.slot_bank(l)
+
+
+def _route(x, model, l, w_out, ids_out, logits_out):
+    from vllm_moe_offload_amd import native
+
+    native.router_gate(x, model.gates[l], logits_out)
+    native.router_topk(logits_out, K, bias=model.specs[l].e_score_correction_bias, w_bf16=w_out, ids=ids_out)
+
+
+def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int, budget_s: float) -> dict:
+    """B tokens per step through the 48 layers.  Per step: eager routing of
+    every layer, one D2H of the ids, LRU staging of every layer (the seam),
+    then the captured 48-layer compute is replayed and timed with HIP events.
+    A step whose working set exceeds the slots of some layer runs eager, with
+    capacity waves for those layers (timed apart: graphs are not replayed
+    for it)."""
+    import torch
+
+    from vllm_moe_offload_amd import fused_moe
+
+    dev = torch.device("cuda")
+    L = model.L
+    rt = model.rt
+    gx = torch.Generator(device=dev)
+    gx.manual_seed(seed + B)
+    n_inputs = steps + warmup
+    xs = torch.randn((n_inputs, B, H), generator=gx, device=dev).to(torch.bfloat16)
+    static_x = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
+    logits = [torch.empty((B, E), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    ws_w = [torch.empty((B, K), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    ws_ids = [torch.empty((B, K), dtype=torch.int32, device=dev) for _ in range(L)]
+    outs = [torch.empty((B, H), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    P = model.bank(0).physical_expert_count
+    ws = fused_moe.get_workspace(B, K, P, H, I, dev, tag=f"bench{B}")
+
+    def compute_layer(l):
+        _route(static_x, model, l, ws_w[l], ws_ids[l], logits[l])
+        bank = model.bank(l)
+        fused_moe.fused_experts(static_x, ws_w[l], ws_ids[l], bank.w13_slots, bank.w2_slots,
+                                rt.log2phy_buffer(l), out=outs[l], workspace=ws)
+
+    def compute_all():
+        for l in range(L):
+            compute_layer(l)
+
+    def route_all(i: int) -> list[tuple[int, ...]]:
+        static_x.copy_(xs[i])
+        for l in range(L):
+            _route(static_x, model, l, ws_w[l], ws_ids[l], logits[l])
+        ids_host = torch.stack(ws_ids).cpu()  # one D2H for all layers' ids
+        return [tuple(sorted(set(ids_host[l].flatten().tolist()))) for l in range(L)]
+
+    stats = {"hits": 0, "misses": 0}
+
+    def stage(l, active):
+        rt.stage_fixed_slot_plan(layer_id=l, active_experts=active, num_logical_experts=E)
+        h, m = rt.last_stage_stats
+        stats["hits"] += h
+        stats["misses"] += m
+
+    def overflow_step(active_sets):
+        for l in range(L):
+            if len(active_sets[l]) <= rt.config.num_slots:
+                stage(l, active_sets[l])
+                compute_layer(l)
+            else:
+                fused_moe.run_wave_prefill(rt, layer_id=l, hidden=static_x, topk_weights=ws_w[l],
+                                           topk_ids=ws_ids[l], num_logical_experts=E, out=outs[l])
+            rt.record_layer_compute(l)
+
+    def fits(active_sets):
+        return all(len(a) <= rt.config.num_slots for a in active_sets)
+
+    # warm up (fills the slot banks), then capture the 48-layer compute
+    captured = False
+    graph = torch.cuda.CUDAGraph()
+    t_begin = time.perf_counter()
+    for i in range(warmup):
+        a = route_all(i)
+        if fits(a):
+            for l in range(L):
+                stage(l, a[l])
+            compute_all()
+            if not captured:
+                torch.cuda.synchronize()
+                for l in range(L):
+                    rt.capture_safe_slot_weights(layer_id=l)  # lock slot addresses
+                s = torch.cuda.Stream()
+                s.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(s):
+                    compute_all()
+                torch.cuda.current_stream().wait_stream(s)
+                with torch.cuda.graph(graph):
+                    compute_all()
+                captured = True
+        else:
+            overflow_step(a)
+    torch.cuda.synchronize()
+    fp0 = [rt._slot_address_fingerprint(l) for l in range(L)]
+    stats["hits"] = stats["misses"] = 0
+    replay_ms, overflow_ms, stage_ms, U = [], [], [], []
+    done = 0
+    for i in range(warmup, warmup + steps):
+        if time.perf_counter() - t_begin > budget_s and done >= 8:
+            break
+        t0 = time.perf_counter()
+        a = route_all(i)
+        U.append(sum(len(x) for x in a) / L)
+        if captured and fits(a):
+            for l in range(L):
+                stage(l, a[l])
+            torch.cuda.synchronize()
+            stage_ms.append((time.perf_counter() - t0) * 1000.0)
+            with Timer() as t:
+                graph.replay()
+            for l in range(L):
+                rt.record_layer_compute(l)
+            replay_ms.append(t.ms())
+        else:
+            with Timer() as t:
+                overflow_step(a)
+            overflow_ms.append(t.ms())
+        done += 1
+    torch.cuda.synchronize()
+    assert fp0 == [rt._slot_address_fingerprint(l) for l in range(L)], "slot addresses moved"
+    res: dict = {"B": B, "steps_run": done, "steps_graph": len(replay_ms), "steps_overflow_waves": len(overflow_ms)}
+    res["slot_miss_rate"] = round(stats["misses"] / max(1, stats["hits"] + stats["misses"]), 4)
+    u = sum(U) / max(1, len(U))
+    res["distinct_experts_per_layer"] = round(u, 2)
+    layer_bytes = u * EXPERT_BYTES + E * H * 2 + 2 * B * H * 2
+    res["algorithmic_bytes_per_layer"] = int(layer_bytes)
+    if replay_ms:
+        ms = sorted(replay_ms)
+        mean = sum(ms) / len(ms)
+        us_layer = mean * 1000.0 / L
+        res.update(
+            graph_ms_per_step_mean=round(mean, 4),
+            graph_ms_per_step_median=round(ms[len(ms) // 2], 4),
+            graph_ms_p10=round(ms[len(ms) // 10], 4),
+            graph_ms_p90=round(ms[(9 * len(ms)) // 10], 4),
+            us_per_layer=round(us_layer, 3),
+            us_per_token_per_layer=round(us_layer / B, 3),
+            layer_hbm_gbs=round(layer_bytes / (us_layer * 1e-6) / 1e9, 1),
+        )
+        res["layer_hbm_frac"] = round(res["layer_hbm_gbs"] / HBM_PEAK_GBS, 4)
+        res["eager_stage_ms_per_step"] = round(sum(stage_ms) / len(stage_ms), 3)
+    if overflow_ms:
+        res["overflow_eager_ms_per_step"] = round(sum(overflow_ms) / len(overflow_ms), 3)
+    res["_state"] = (ws_ids, static_x)
+    return res
+
+
+def bench_gateup_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
+    """Dominant decode kernel at B=1: gate_up GEMV + SiLU*mul, 48*reps
+    launches rotating through the 48 layers' slot banks (29 GB, far beyond
+    the 256 MB MALL), captured in one graph so they run back to back, timed
+    with HIP events on the stream they are launched on."""
+    import torch
+
+    from vllm_moe_offload_amd import native
+
+    ws_ids, x = state
+    L = model.L
+    dev = torch.device("cuda")
+    B = x.shape[0]
+    P = model.bank(0).physical_expert_count
+    perms, acts = [], []
+    for l in range(L):
+        p = native.Permutation.allocate(B * K, P, dev)
+        native.permute(ws_ids[l], p, log2phy=model.rt.log2phy_buffer(l))
+        perms.append(p)
+        acts.append(torch.empty((B * K, I), dtype=torch.bfloat16, device=dev))
+    torch.cuda.synchronize()
+    U = [int(perms[l].meta[native.META_ACTIVE].item()) for l in range(L)]
+
+    def launches():
+        for _ in range(reps):
+            for l in range(L):
+                native.gateup_silu(x, K, model.bank(l).w13_slots, perms[l], acts[l], path=native.LMOE_PATH_GEMV)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launches()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launches()
+    g.replay()
+    stream = torch.cuda.current_stream()
+    with Timer(stream) as t:
+        g.replay()
+    ms = t.ms()
+    n = reps * L
+    avg_us = ms * 1000.0 / n
+    u = sum(U) / L
+    bytes_per_launch = u * (2 * I * H * 2) + B * H * 2 + B * K * I * 2
+    return {
+        "kernel": "gateup_gemv_kernel",
+        "avg_launch_us": round(avg_us, 3),
+        "bytes_per_launch": int(bytes_per_launch),
+        "distinct_slots_per_launch": round(u, 2),
+        "achieved_gbs": round(bytes_per_launch / (avg_us * 1e-6) / 1e9, 1),
+        "launches": n,
+    }
+
+
+# ---------------------------------------------------------------------------
+# C3: multi-wave prefill
+# ---------------------------------------------------------------------------
+def bench_prefill(host_w13, host_w2, T: int = 4096, slots: int = 48, reps: int = 5) -> dict:
+    import torch
+
+    from vllm_moe_offload_amd import fused_moe, native
+    from vllm_moe_offload_amd.fused_moe import RouterSpec, route
+    from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+    from vllm_moe_offload_amd.moe_offload.runtime import MoeOffloadRuntime
+
+    dev = torch.device("cuda")
+    rt = MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=slots, async_load=True, b2_wave_prefill=True))
+    rt.register_host_buffers(layer_id=0, w13_host=host_w13, w2_host=host_w2, slot_device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4096)
+    gate = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+    spec = RouterSpec(top_k=K)
+    w, ids, _ = route(x, gate, spec)
+    torch.cuda.synchronize()
+    pairs = T * K
+    flops = 2.0 * pairs * 3 * H * I
+    router_flops = 2.0 * T * H * E
+    res: dict = {"T": T, "slots": slots, "algorithmic_gflop": round((flops + router_flops) / 1e9, 2)}
+
+    # staged multi-wave layer (H2D from the pinned host store each call)
+    fused_moe.run_wave_prefill(rt, layer_id=0, hidden=x, topk_weights=w, topk_ids=ids, num_logical_experts=E)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    nrep = 2
+    for _ in range(nrep):
+        out_w, rep = fused_moe.run_wave_prefill(rt, layer_id=0, hidden=x, topk_weights=w, topk_ids=ids, num_logical_experts=E)
+    torch.cuda.synchronize()
+    staged_ms = (time.perf_counter() - t0) * 1000.0 / nrep
+    res.update(waves=len(rep.waves), wave_sizes=[len(v) for v in rep.waves], staged_wave_ms=round(staged_ms, 2),
+               staged_h2d_gb=round(rep.h2d_bytes / 1e9, 3),
+               staged_effective_h2d_gbs=round(rep.h2d_bytes / (staged_ms * 1e-3) / 1e9, 1))
+
+    # compute-only: all waves' experts resident in per-wave banks
+    full, _ = rt.prepare_full_layer_prefill_plan(layer_id=0, num_logical_experts=E, device=dev)
+    torch.cuda.synchronize()
+    wave_banks = []
+    for wv in rep.waves:
+        idx = torch.tensor(wv, dtype=torch.long, device=dev)
+        w13 = full.w1.index_select(0, idx).contiguous()
+        w2 = full.w2.index_select(0, idx).contiguous()
+        l2p = torch.full((E,), -1, dtype=torch.int32, device=dev)
+        l2p[idx] = torch.arange(len(wv), dtype=torch.int32, device=dev)
+        wave_banks.append((w13, w2, l2p))
+    perm = native.Permutation.allocate(pairs, max(len(v) for v in rep.waves), dev)
+    perms_w = [native.Permutation.allocate(pairs, wb[0].shape[0], dev) for wb in wave_banks]
+    act = torch.empty((pairs, I), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((pairs, H), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+
+    def waves_compute():
+        for (w13, w2, l2p), pw in zip(wave_banks, perms_w):
+            native.permute(ids, pw, log2phy=l2p, skip_unmapped=True)
+            native.grouped_mlp(x, K, w13, w2, pw, act, y, path=native.LMOE_PATH_MFMA)
+        native.combine(y, w, out)
+
+    ws_full = fused_moe.get_workspace(T, K, E, H, I, dev, tag="bench-full")
+
+    def full_compute():
+        fused_moe.fused_experts(x, w, ids, full.w1, full.w2, full.log2phy, path=native.LMOE_PATH_MFMA, workspace=ws_full)
+
+    def gemm_only():
+        for (w13, w2, l2p), pw in zip(wave_banks, perms_w):
+            native.grouped_mlp(x, K, w13, w2, pw, act, y, path=native.LMOE_PATH_MFMA)
+
+    for fn in (waves_compute, full_compute):
+        fn()
+    torch.cuda.synchronize()
+    for name, fn in (("waves_compute", waves_compute), ("full_layer_compute", full_compute), ("grouped_gemm_only", gemm_only)):
+        with Timer() as t:
+            for _ in range(reps):
+                fn()
+        ms = t.ms() / reps
+        tf = flops / (ms * 1e-3) / 1e12
+        res[f"{name}_ms"] = round(ms, 3)
+        res[f"{name}_tflops"] = round(tf, 1)
+        res[f"{name}_mfma_frac"] = round(tf / BF16_PEAK_TFLOPS, 4)
+    torch.cuda.synchronize()
+    same = torch.equal(out.view(torch.int16), ws_full.out[:T].view(torch.int16))
+    res["waves_equal_full_layer_bitwise"] = bool(same)
+    return res
+
+
+# ---------------------------------------------------------------------------
+# C4: staging stress with prefetch under per-layer graph replay
+# ---------------------------------------------------------------------------
+def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int = 99) -> dict:
+    """Per step and layer, exactly k experts that are not resident plus 8-k
+    resident ones.  Pipelined: layer l+1's miss copies are queued on the
+    transfer stream (prefetch) before layer l's graph is replayed; the
+    compute stream waits for them (complete) right before layer l+1."""
+    import numpy as np
+    import torch
+
+    from vllm_moe_offload_amd import fused_moe
+
+    dev = torch.device("cuda")
+    L = model.L
+    rt = model.rt
+    engine = rt.transfer_engine
+    rng = np.random.default_rng(seed)
+    B = 1
+    x = torch.randn((B, H), device=dev).to(torch.bfloat16)
+    w_all = torch.full((L, B, K), 1.0 / K, dtype=torch.bfloat16, device=dev)
+    ids_all = torch.zeros((L, B, K), dtype=torch.int32, device=dev)
+    ids_host = torch.zeros((L, B, K), dtype=torch.int32, pin_memory=True)
+    out_l = [torch.empty((B, H), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    P = model.bank(0).physical_expert_count
+    ws = fused_moe.get_workspace(B, K, P, H, I, dev, tag="bench-stage")
+
+    def resident(l):
+        return [s.expert_key.expert_id for s in model.bank(l).slots if s.expert_key is not None]
+
+    for l in range(L):
+        ids_all[l, 0].copy_(torch.tensor(resident(l)[:K], dtype=torch.int32))
+    graphs = []
+    for l in range(L):
+        bank = model.bank(l)
+
+        def piece(l=l, bank=bank):
+            fused_moe.fused_experts(x, w_all[l], ids_all[l], bank.w13_slots, bank.w2_slots, rt.log2phy_buffer(l),
+                                    out=out_l[l], workspace=ws)
+
+        piece()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            piece()
+        graphs.append(g)
+
+    def plan_step(k: int):
+        plan = []
+        for l in range(L):
+            res = resident(l)
+            non = sorted(set(range(E)) - set(res))
+            miss = list(rng.choice(non, size=k, replace=False))
+            hit = list(rng.choice(res, size=K - k, replace=False)) if K - k > 0 else []
+            plan.append(tuple(int(e) for e in miss + hit))
+        return plan
+
+    def load_ids(plan):
+        ids_host.copy_(torch.tensor(plan, dtype=torch.int32).view(L, B, K))
+        ids_all.copy_(ids_host, non_blocking=True)
+
+    compute = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    tc = []
+    for _ in range(3):
+        with Timer(compute) as t:
+            for g in graphs:
+                g.replay()
+        tc.append(t.ms())
+    tc_ms = min(tc)
+    fp = [rt._slot_address_fingerprint(l) for l in range(L)]
+    out: dict = {"compute_only_ms_per_step": round(tc_ms, 3)}
+    for k in ks:
+        # (a) copies alone: all layers prefetched back to back on the transfer stream
+        plan = plan_step(k)
+        torch.cuda.synchronize()
+        b0 = engine.bytes_issued
+        t0 = time.perf_counter()
+        pend = [rt.prefetch_fixed_slot_plan(layer_id=l, active_experts=plan[l], num_logical_experts=E) for l in range(L)]
+        host_issue_ms = (time.perf_counter() - t0) * 1000.0
+        engine.stream.synchronize()
+        th_ms = (time.perf_counter() - t0) * 1000.0
+        h2d_bytes = engine.bytes_issued - b0
+        for l in range(L):
+            rt.complete_fixed_slot_plan(pend[l])
+        torch.cuda.synchronize()
+        # (b) pipelined under per-layer graph replays
+        tb, nb, host_ms = [], 0, []
+        for _ in range(steps):
+            plan = plan_step(k)
+            torch.cuda.synchronize()
+            b0 = engine.bytes_issued
+            t0 = time.perf_counter()
+            load_ids(plan)
+            pending = rt.prefetch_fixed_slot_plan(layer_id=0, active_experts=plan[0], num_logical_experts=E)
+            for l in range(L):
+                rt.complete_fixed_slot_plan(pending)
+                nxt = None
+                if l + 1 < L:
+                    nxt = rt.prefetch_fixed_slot_plan(layer_id=l + 1, active_experts=plan[l + 1], num_logical_experts=E)
+                graphs[l].replay()
+                rt.record_layer_compute(l)
+                pending = nxt
+            host_ms.append((time.perf_counter() - t0) * 1000.0)
+            torch.cuda.synchronize()
+            tb.append((time.perf_counter() - t0) * 1000.0)
+            nb += engine.bytes_issued - b0
+        tb_ms = sum(tb) / len(tb)
+        assert fp == [rt._slot_address_fingerprint(l) for l in range(L)], "slot addresses moved"
+        hidden = (tc_ms + th_ms - tb_ms) / max(1e-9, min(tc_ms, th_ms))
+        out[f"k{k}"] = {
+            "h2d_bytes_per_step": int(h2d_bytes),
+            "h2d_only_ms": round(th_ms, 3),
+            "h2d_gbs": round(h2d_bytes / (th_ms * 1e-3) / 1e9, 2),
+            "host_issue_ms": round(host_issue_ms, 3),
+            "pipelined_step_ms": round(tb_ms, 3),
+            "pipelined_host_ms": round(sum(host_ms) / len(host_ms), 3),
+            "pipelined_h2d_gbs": round(nb / steps / (tb_ms * 1e-3) / 1e9, 2),
+            "compute_hidden_frac": round(max(0.0, min(1.0, hidden)), 4),
+            "steps": steps,
+        }
+    out["slot_addresses_stable_across_replays"] = True
+    return out
+
+
+# ---------------------------------------------------------------------------
+# C5: DeepSeek-V3-style layer (compute, resident slots)
+# ---------------------------------------------------------------------------
+def bench_deepseek(batches=(1, 8, 32), prefill_tokens: int = 2048, reps: int = 20) -> dict:
+    """DeepSeek-V3-style layer with every routed expert resident: 64 slots
+    hold the 256 routed ids round-robin (the weights are synthetic, so the
+    bytes and flops are those of a real layer) plus the shared expert as a
+    pinned suffix slot, appended to every token's top-8 with weight 1."""
+    import torch
+
+    from vllm_moe_offload_amd import fused_moe, native
+
+    dev = torch.device("cuda")
+    Hd, Ed, Id, Kd, P = 7168, 256, 2048, 8, 64
+    g = torch.Generator(device=dev)
+    g.manual_seed(7168)
+    w13 = (torch.randn((P + 1, 2 * Id, Hd), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn((P + 1, Hd, Id), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    gate = (torch.randn((Ed, Hd), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    bias = (torch.randn((Ed,), generator=g, device=dev) * 0.01).float()
+    l2p = torch.cat([torch.arange(Ed, dtype=torch.int32, device=dev) % P,
+                     torch.tensor([P], dtype=torch.int32, device=dev)])
+    res: dict = {}
+    per_expert = 3 * Hd * Id * 2
+
+    def make_step(B, path):
+        x = torch.randn((B, Hd), generator=g, device=dev).to(torch.bfloat16)
+        logits = torch.empty((B, Ed), dtype=torch.bfloat16, device=dev)
+        wk = torch.empty((B, Kd), dtype=torch.bfloat16, device=dev)
+        idk = torch.empty((B, Kd), dtype=torch.int32, device=dev)
+        wv = torch.ones((B, Kd + 1), dtype=torch.bfloat16, device=dev)
+        idv = torch.full((B, Kd + 1), Ed, dtype=torch.int32, device=dev)
+        ws = fused_moe.get_workspace(B, Kd + 1, P + 1, Hd, Id, dev, tag=f"ds{B}")
+        out = torch.empty((B, Hd), dtype=torch.bfloat16, device=dev)
+
+        def step():
+            native.router_gate(x, gate, logits)
+            native.router_topk(logits, Kd, scoring="sigmoid", bias=bias, num_expert_group=8, topk_group=4,
+                               routed_scaling_factor=2.5, w_bf16=wk, ids=idk)
+            wv[:, :Kd].copy_(wk)
+            idv[:, :Kd].copy_(idk)
+            fused_moe.fused_experts(x, wv, idv, w13, w2, l2p, out=out, workspace=ws, path=path)
+
+        return step, ws
+
+    def timed(step, n):
+        step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        with torch.cuda.graph(graph):
+            step()
+        graph.replay()
+        with Timer() as t:
+            for _ in range(n):
+                graph.replay()
+        return t.ms() / n
+
+    for B in batches:
+        step, ws = make_step(B, native.LMOE_PATH_AUTO)
+        ms = timed(step, reps)
+        U = int(ws.perm.meta[native.META_ACTIVE].item())
+        byts = U * per_expert + Ed * Hd * 2 + 2 * B * Hd * 2
+        res[f"decode_B{B}"] = {"us_per_layer": round(ms * 1000, 2), "us_per_token": round(ms * 1000 / B, 2),
+                               "distinct_slots": U, "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+                               "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    T = prefill_tokens
+    step, ws = make_step(T, native.LMOE_PATH_MFMA)
+    ms = timed(step, 5)
+    flops = 2.0 * T * (Kd + 1) * 3 * Hd * Id + 2.0 * T * Hd * Ed
+    tf = flops / (ms * 1e-3) / 1e12
+    res[f"prefill_T{T}"] = {"ms": round(ms, 3), "tflops": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+    del w13, w2
+    fused_moe.clear_workspaces()
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle of one layer on the host cores
+# ---------------------------------------------------------------------------
+def bench_cpu_baseline(budget_s: float = 15.0) -> dict:
+    """The numpy oracle of one Qwen3-shaped layer at decode B=1: gate,
+    softmax top-8, the 8 experts' SwiGLU MLP with f32 accumulation, combine.
+    Expert weights are generated lazily outside the timed region."""
+    import numpy as np
+
+    from oracle import mlp as omlp
+    from oracle import router as orouter
+    from oracle.bf16 import normal_bf16
+
+    rng = np.random.default_rng(5)
+    wg = normal_bf16(rng, (E, H), 0.02)
+    experts: dict[int, tuple] = {}
+    t_total, tokens = 0.0, 0
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or tokens < 3:
+        x = normal_bf16(rng, (1, H), 1.0)
+        t0 = time.perf_counter()
+        ids, _, wb = orouter.softmax_topk(orouter.gate_logits(x, wg), K)
+        t_route = time.perf_counter() - t0
+        for e in ids[0]:
+            if int(e) not in experts:
+                experts[int(e)] = (normal_bf16(rng, (2 * I, H), 0.02), normal_bf16(rng, (H, I), 0.02))
+        w13 = np.stack([experts[int(e)][0] for e in ids[0]])
+        w2 = np.stack([experts[int(e)][1] for e in ids[0]])
+        t1 = time.perf_counter()
+        omlp.moe_layer(x, np.arange(K, dtype=np.int32)[None, :], wb, None, w13, w2)
+        t_total += t_route + (time.perf_counter() - t1)
+        tokens += 1
+    cores = int(os.environ.get("OMP_NUM_THREADS") or (os.cpu_count() or 1))
+    return {"value": round(t_total / tokens * 1e6, 1), "unit": "us/token/layer (decode B=1)",
+            "cores": cores, "kind": "port",
+            "sample": f"{tokens} single-token decode passes of one Qwen3-shaped MoE layer through the numpy "
+                      f"oracle (gate, softmax top-8, 8 f32-accumulated SwiGLU experts, combine), "
+                      f"{budget_s:.0f} s budget; BLAS threads up to {cores}"}
+
+
+# ---------------------------------------------------------------------------
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode steps per batch size")
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--batches", default="1,4,16,64")
+    ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--slots", type=int, default=64)
+    ap.add_argument("--skip", default="", help="comma list of: prefill,staging,deepseek,cpu")
+    ap.add_argument("--budget-s", type=float, default=30.0, help="wall-clock cap per decode batch size")
+    ap.add_argument("--stage-steps", type=int, default=16)
+    ap.add_argument("--out", default="")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it"}))
+        return 2
+    skip = set(x for x in args.skip.split(",") if x)
+
+    import torch
+
+    from vllm_moe_offload_amd import native
+
+    native.load_library()
+    dev = torch.device("cuda")
+    torch.manual_seed(0)
+    t_setup = time.perf_counter()
+    # shared 128-expert pinned host store (checkpoint layout)
+    host_w13 = torch.empty((E, 2 * I, H), dtype=torch.bfloat16, pin_memory=True)
+    host_w2 = torch.empty((E, H, I), dtype=torch.bfloat16, pin_memory=True)
+    g = torch.Generator(device=dev)
+    g.manual_seed(128)
+    for e in range(E):
+        host_w13[e].copy_((torch.randn((2 * I, H), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+        host_w2[e].copy_((torch.randn((H, I), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    model = DecodeModel(args.layers, args.slots, host_w13, host_w2)
+    log(f"setup {time.perf_counter() - t_setup:.1f}s")
+
+    decode = {}
+    roof = None
+    t_run0 = time.perf_counter()
+    for B in [int(b) for b in args.batches.split(",") if b]:
+        t0 = time.perf_counter()
+        r = bench_decode(model, B, args.steps, args.warmup, seed=17, budget_s=args.budget_s)
+        state = r.pop("_state")
+        if B == 1:
+            roof = bench_gateup_roofline(model, state)
+        decode[f"B{B}"] = r
+        log(f"decode B={B}: {r} ({time.perf_counter() - t0:.1f}s)")
+    t_decode = time.perf_counter() - t_run0
+    prefill = staging = deepseek = cpu = None
+    if "prefill" not in skip:
+        t0 = time.perf_counter()
+        prefill = bench_prefill(host_w13, host_w2)
+        log(f"prefill: {prefill} ({time.perf_counter() - t0:.1f}s)")
+    if "staging" not in skip:
+        t0 = time.perf_counter()
+        staging = bench_staging(model, steps=args.stage_steps)
+        log(f"staging: {staging} ({time.perf_counter() - t0:.1f}s)")
+    del model
+    torch.cuda.empty_cache()
+    if "deepseek" not in skip:
+        t0 = time.perf_counter()
+        deepseek = bench_deepseek()
+        log(f"deepseek: {deepseek} ({time.perf_counter() - t0:.1f}s)")
+    if "cpu" not in skip:
+        cpu = bench_cpu_baseline()
+        log(f"cpu baseline: {cpu}")
+
+    b1 = decode.get("B1", {})
+    value = b1.get("us_per_token_per_layer")
+    steps_ms = b1.get("graph_ms_per_step_mean")
+    line = {
+        "metric": "MoE-layer us/token decode (HBM GB/s %peak); prefill TFLOP/s; H2D GB/s",
+        "value": value,
+        "unit": "us/token/layer (decode, B=1, 48-layer hipGraph replay)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": steps_ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (weights N(0,0.02) bf16, hidden N(0,1), Zipf(1.1) router bias from fixed seeds)",
+        "config": {"workload": "C2 Qwen3-30B-A3B-shaped decode: 48 MoE layers, hidden 2048, 128 experts, top-8, "
+                               "intermediate 768, 64 slots/layer, pinned host store, hipGraph-captured step",
+                   "layers": args.layers, "slots": args.slots, "batch": 1},
+        "roofline": None,
+        "cpu_baseline": cpu,
+        "decode": decode,
+        "prefill": prefill,
+        "staging": staging,
+        "deepseek_v3_style": deepseek,
+    }
+    if roof is not None:
+        line["roofline"] = {"bound": "hbm", "achieved": roof["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(roof["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": roof["kernel"], "avg_launch_us": roof["avg_launch_us"],
+                            "bytes_per_launch": roof["bytes_per_launch"],
+                            "distinct_slots_per_launch": roof["distinct_slots_per_launch"]}
+        traffic_file = ROOT / "profiles" / "gateup_gemv_decode_b1_traffic.json"
+        if traffic_file.exists():
+            try:
+                line["roofline"]["traffic"] = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+            except Exception:
+                pass
+    text = json.dumps(line)
+    print(text, flush=True)
+    if args.out:
+        Path(args.out).write_text(text + "\n")
+    log(f"decode phase {t_decode:.1f}s total")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -82,8 +82,9 @@ int lmoe_abi_version(void);
 int lmoe_router_gate(const void* x, const void* wg, int T, int H, int E,
                      void* logits, int logits_f32, hipStream_t stream);
 
-/* Expert selection.  scoring = LMOE_SCORING_SOFTMAX: f32 softmax over E, the
- * k largest probabilities.  scoring = LMOE_SCORING_SIGMOID: s = sigmoid(l),
+/* Expert selection.  scoring = LMOE_SCORING_SOFTMAX: f32 softmax over E of
+ * l + bias (bias may be NULL: an additive per-expert logit bias), the k
+ * largest probabilities.  scoring = LMOE_SCORING_SIGMOID: s = sigmoid(l),
  * selection score s + bias (bias may be NULL), n_group contiguous groups
  * ranked by the sum of their two largest selection scores, the topk_group best
  * groups kept, k largest selection scores inside the kept groups, weights = s.
@@ -143,6 +144,21 @@ int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
                      const int32_t* active, const int32_t* tile_off,
                      const int32_t* meta, int n_pairs, int block_m, int path,
                      void* act, void* y, hipStream_t stream);
+
+/* The two halves of lmoe_grouped_mlp, callable on their own (same argument
+ * meaning): GMM1 + SwiGLU into act, and GMM2 from act into y.  Replace the
+ * separate npu_grouped_matmul + npu_swiglu and npu_grouped_matmul calls of
+ * _apply_mlp (patch_fused_moe.py:3772-3774). */
+int lmoe_gateup_silu(const void* x, int T, int H, int I, int k,
+                     const void* w13_slots, int n_slots, const int32_t* offsets,
+                     const int32_t* sorted_pairs, const int32_t* active,
+                     const int32_t* tile_off, const int32_t* meta, int n_pairs,
+                     int block_m, int path, void* act, hipStream_t stream);
+int lmoe_down(const void* act, int H, int I, const void* w2_slots, int n_slots,
+              const int32_t* offsets, const int32_t* sorted_pairs,
+              const int32_t* active, const int32_t* tile_off,
+              const int32_t* meta, int n_pairs, int block_m, int path, void* y,
+              hipStream_t stream);
 
 /* Weighted combine: out[t] = sum_{j<k} w[t][j] * y[t*k+j], f32 accumulation
  * in j order, one rounding to bf16.  y is [T*k, H] bf16 indexed by flat pair

@@ -125,10 +125,14 @@ def _finish(sel_w: np.ndarray, renorm: bool, scale: float) -> tuple[np.ndarray, 
 
 
 def softmax_topk(
-    logits: np.ndarray, k: int, *, renorm: bool = True, scale: float = 1.0
+    logits: np.ndarray, k: int, *, renorm: bool = True, scale: float = 1.0, bias: np.ndarray | None = None
 ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
-    """Returns (ids int32 [T,k], w_f32 [T,k], w_bf16 bits [T,k])."""
-    p = softmax_probs(logits)
+    """Returns (ids int32 [T,k], w_f32 [T,k], w_bf16 bits [T,k]).  bias is an
+    additive per-expert logit bias applied (one f32 rounding) before softmax."""
+    lg = np.asarray(logits, dtype=np.float32)
+    if bias is not None:
+        lg = (lg + np.asarray(bias, dtype=np.float32)[None, :]).astype(np.float32)
+    p = softmax_probs(lg)
     T, E = p.shape
     ids = np.empty((T, k), dtype=np.int32)
     sel = np.empty((T, k), dtype=np.float32)

@@ -57,6 +57,21 @@ def test_softmax_topk_bit_exact(T, E, k, dtype):
     np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
 
 
+def test_softmax_with_logit_bias_bit_exact():
+    native = _native()
+    rng = np.random.default_rng(21)
+    T, E, k = 64, 128, 8
+    bits = _tied_logits(rng, T, E)
+    bias = (rng.standard_normal(E) * 0.7).astype(np.float32)
+    w_f32 = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    w, ids, _ = native.router_topk(to_dev_bf16(bits), k, bias=torch.from_numpy(bias).cuda(), w_f32=w_f32)
+    torch.cuda.synchronize()
+    r_ids, r_w, r_wb = orc.softmax_topk(bf16_to_f32(bits), k, bias=bias)
+    np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
+    np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
+    np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
+
+
 def test_softmax_ties_break_to_lower_id():
     native = _native()
     T, E, k = 4, 128, 8

@@ -226,7 +226,7 @@ def test_decode_waits_before_publishing_async_mapping(monkeypatch):  # :1491-154
     pending, observed = [], []
 
     def fake_async(loads, *, wait_event=None, record_event=True, validate_layout=True):
-        assert wait_event is None and record_event and validate_layout is False
+        assert wait_event is None and record_event and validate_layout is False  # no compute recorded yet
         pending.extend(loads)
         for b, s in loads:
             s.w13.copy_(b.w13)
@@ -488,3 +488,60 @@ def test_runtime_stages_in_placement_plan_order():
     p = rt.stage_fixed_slot_plan(layer_id=7, active_experts=(0, 1, 2), num_logical_experts=4)
     assert p.mapping.active_experts == (2, 0, 1) and p.mapping.active_slot_ids == (0, 1, 2)
     assert rt.log2phy_buffer(7).tolist() == [1, 2, 0, -1]
+
+
+def test_prefetch_then_complete_publishes_after_wait_and_orders_after_layer_compute(monkeypatch):
+    """Split decode staging: copies are queued at prefetch (waiting on the
+    layer's last recorded compute), the mapping is published only at
+    complete, after the consumer wait."""
+    rt = _rt(num_slots=2, graph_compatible_offload=True, async_load=True)
+    rt.register_layer_for_fixed_slots(TinyLayer(), slot_device=CPU)
+    calls, observed = [], []
+    release = object()
+    rt._layer_release_events[7] = release
+
+    def fake_async(loads, *, wait_event=None, record_event=True, validate_layout=True):
+        calls.append(wait_event)
+        for b, s in loads:
+            s.w13.copy_(b.w13)
+            s.w2.copy_(b.w2)
+            s.state = SlotState.LOADING
+        return ("ready", tuple(s for _, s in loads))
+
+    def wait(ready):
+        observed.append(rt.log2phy_buffer(7).tolist())
+        for s in ready[1]:
+            s.state = SlotState.READY
+
+    monkeypatch.setattr(rt._transfer_engine, "load_many_async", fake_async)
+    monkeypatch.setattr(rt, "_wait_transfer_event", wait)
+    pending = rt.prefetch_fixed_slot_plan(layer_id=7, active_experts=(2, 0), num_logical_experts=4)
+    assert calls == [release]
+    assert pending.misses == (2, 0) and rt.log2phy_buffer(7).tolist() == [-1, -1, -1, -1]
+    p = rt.complete_fixed_slot_plan(pending)
+    assert observed == [[-1, -1, -1, -1]]
+    assert p.log2phy.data_ptr() == rt.log2phy_buffer(7).data_ptr()
+    assert rt.log2phy_buffer(7).tolist() == [1, -1, 0, -1]
+    assert rt.last_stage_stats == (0, 2)
+    # all hits: no copy, nothing to wait for
+    p = rt.complete_fixed_slot_plan(rt.prefetch_fixed_slot_plan(layer_id=7, active_experts=(0,), num_logical_experts=4))
+    assert len(calls) == 1 and rt.last_stage_stats == (1, 0)
+    assert torch.equal(p.w1[1], TinyLayer().w13_weight.detach()[0])
+
+
+def test_register_host_buffers_uses_buffers_in_place():
+    """CPU-first registration: the host tensors become the store as they are."""
+    rt = _rt(num_slots=2, graph_compatible_offload=True)
+    w13 = torch.arange(4 * 2 * 3, dtype=torch.float32).reshape(4, 2, 3)
+    w2 = torch.arange(4 * 3 * 2, dtype=torch.float32).reshape(4, 3, 2) + 100
+    rt.register_host_buffers(layer_id=5, w13_host=w13, w2_host=w2, slot_device=CPU)
+    buf = rt.host_store.get_layer_buffer(5)
+    assert buf.w13.data_ptr() == w13.data_ptr() and buf.w2.data_ptr() == w2.data_ptr()
+    assert rt.log2phy_buffer(5).tolist() == [-1] * 4
+    assert rt.cached_layer_expert_weight_bytes(layer_id=5) == (6 + 6) * 4
+    p = rt.stage_fixed_slot_plan(layer_id=5, active_experts=(3, 1), num_logical_experts=4)
+    assert rt.log2phy_buffer(5).tolist() == [-1, 1, -1, 0]
+    assert torch.equal(p.w1[0], w13[3]) and torch.equal(p.w2[1], w2[1])
+    rt.capture_safe_slot_weights(layer_id=5)
+    with pytest.raises(RuntimeError, match="already captured"):
+        rt.register_host_buffers(layer_id=5, w13_host=w13, w2_host=w2, slot_device=CPU)

@@ -298,38 +298,82 @@ using namespace lmoe;
 static long long slot_elems_w13(int H, int I) { return 2LL * I * H; }
 static long long slot_elems_w2(int H, int I) { return 1LL * H * I; }
 
-extern "C" int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
-                                const void* w13_slots, const void* w2_slots,
-                                int n_slots, const int32_t* offsets,
-                                const int32_t* sorted_pairs,
+static int check_mlp_args(int T, int H, int I, int k, int n_slots, int n_pairs) {
+  if (T < 0 || H <= 0 || I <= 0 || k <= 0 || n_slots <= 0 || n_pairs < 0) return LMOE_ERR_ARG;
+  if (H % 8 != 0 || I % 64 != 0 || I > 8192 || H > 8192) return LMOE_ERR_SHAPE;
+  return LMOE_OK;
+}
+
+static int resolve_path(int path, int n_pairs) {
+  return path == LMOE_PATH_AUTO ? (n_pairs <= 256 ? LMOE_PATH_GEMV : LMOE_PATH_MFMA) : path;
+}
+
+extern "C" int lmoe_gateup_silu(const void* x, int T, int H, int I, int k,
+                                const void* w13_slots, int n_slots,
+                                const int32_t* offsets, const int32_t* sorted_pairs,
                                 const int32_t* active, const int32_t* tile_off,
                                 const int32_t* meta, int n_pairs, int block_m,
-                                int path, void* act, void* y,
-                                hipStream_t stream) {
-  if (x == nullptr || w13_slots == nullptr || w2_slots == nullptr ||
-      offsets == nullptr || sorted_pairs == nullptr || active == nullptr ||
-      meta == nullptr || act == nullptr || y == nullptr)
+                                int path, void* act, hipStream_t stream) {
+  if (x == nullptr || w13_slots == nullptr || offsets == nullptr || sorted_pairs == nullptr ||
+      active == nullptr || meta == nullptr || act == nullptr)
     return LMOE_ERR_ARG;
-  if (T < 0 || H <= 0 || I <= 0 || k <= 0 || n_slots <= 0 || n_pairs < 0)
-    return LMOE_ERR_ARG;
-  if (H % 8 != 0 || I % 64 != 0 || I > 8192 || H > 8192) return LMOE_ERR_SHAPE;
+  int st = check_mlp_args(T, H, I, k, n_slots, n_pairs);
+  if (st != LMOE_OK) return st;
   if (n_pairs == 0) return LMOE_OK;
-  if (path == LMOE_PATH_AUTO) path = (n_pairs <= 256) ? LMOE_PATH_GEMV : LMOE_PATH_MFMA;
-  const uint16_t* xb = static_cast<const uint16_t*>(x);
-  const uint16_t* w13 = static_cast<const uint16_t*>(w13_slots);
-  const uint16_t* w2 = static_cast<const uint16_t*>(w2_slots);
-  uint16_t* actb = static_cast<uint16_t*>(act);
-  uint16_t* yb = static_cast<uint16_t*>(y);
+  path = resolve_path(path, n_pairs);
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
   if (path == LMOE_PATH_GEMV) {
-    int st = launch_gateup_gemv(xb, H, I, k, w13, offsets, sorted_pairs, active,
-                                meta, max_active, actb, stream);
+    st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
+                            static_cast<const uint16_t*>(w13_slots), offsets, sorted_pairs,
+                            active, meta, max_active, static_cast<uint16_t*>(act), stream);
     if (st != LMOE_OK) return st;
+    LMOE_RETURN_LAUNCH();
+  }
+  if (path != LMOE_PATH_MFMA) return LMOE_ERR_UNSUPPORTED;
+  if (tile_off == nullptr) return LMOE_ERR_ARG;
+  if (block_m != kBM) return LMOE_ERR_UNSUPPORTED;
+  GemmArgs g{};
+  g.topk = k;
+  g.offsets = offsets;
+  g.sorted_pairs = sorted_pairs;
+  g.tile_off = tile_off;
+  g.meta = meta;
+  g.P = n_slots;
+  g.a = static_cast<const uint16_t*>(x);
+  g.w = static_cast<const uint16_t*>(w13_slots);
+  g.w_slot_stride = slot_elems_w13(H, I);
+  g.N = I;
+  g.K = H;
+  g.I = I;
+  g.out = act;
+  const int ub_tiles = n_pairs / kBM + max_active + 1;
+  hipLaunchKernelGGL(grouped_gemm_kernel<kGateUp>, dim3(ub_tiles, (I + 63) / 64), dim3(256), 0,
+                     stream, g);
+  LMOE_RETURN_LAUNCH();
+}
+
+extern "C" int lmoe_down(const void* act, int H, int I, const void* w2_slots, int n_slots,
+                         const int32_t* offsets, const int32_t* sorted_pairs,
+                         const int32_t* active, const int32_t* tile_off,
+                         const int32_t* meta, int n_pairs, int block_m, int path,
+                         void* y, hipStream_t stream) {
+  if (act == nullptr || w2_slots == nullptr || offsets == nullptr || sorted_pairs == nullptr ||
+      active == nullptr || meta == nullptr || y == nullptr)
+    return LMOE_ERR_ARG;
+  int st = check_mlp_args(1, H, I, 1, n_slots, n_pairs);
+  if (st != LMOE_OK) return st;
+  if (n_pairs == 0) return LMOE_OK;
+  path = resolve_path(path, n_pairs);
+  const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
+  const uint16_t* actb = static_cast<const uint16_t*>(act);
+  const uint16_t* w2 = static_cast<const uint16_t*>(w2_slots);
+  uint16_t* yb = static_cast<uint16_t*>(y);
+  if (path == LMOE_PATH_GEMV) {
     dim3 grid((H + 15) / 16, max_active);
     const int nu = nu_for(I);
-#define LMOE_DN(NU)                                                          \
-  hipLaunchKernelGGL(down_gemv_kernel<NU>, grid, dim3(256), 0, stream, actb, I, \
-                     H, w2, offsets, sorted_pairs, active, meta, yb)
+#define LMOE_DN(NU)                                                            \
+  hipLaunchKernelGGL(down_gemv_kernel<NU>, grid, dim3(256), 0, stream, actb, I, H, \
+                     w2, offsets, sorted_pairs, active, meta, yb)
     if (nu <= 3) LMOE_DN(3);
     else if (nu <= 4) LMOE_DN(4);
     else if (nu <= 8) LMOE_DN(8);
@@ -341,34 +385,39 @@ extern "C" int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
   if (path != LMOE_PATH_MFMA) return LMOE_ERR_UNSUPPORTED;
   if (tile_off == nullptr) return LMOE_ERR_ARG;
   if (block_m != kBM) return LMOE_ERR_UNSUPPORTED;
-  const int ub_tiles = n_pairs / kBM + max_active + 1;
   GemmArgs g{};
-  g.topk = k;
+  g.topk = 1;
   g.offsets = offsets;
   g.sorted_pairs = sorted_pairs;
   g.tile_off = tile_off;
   g.meta = meta;
   g.P = n_slots;
-  // gate_up + SiLU*mul -> act (sorted order)
-  g.a = xb;
-  g.w = w13;
-  g.w_slot_stride = slot_elems_w13(H, I);
-  g.N = I;
-  g.K = H;
-  g.I = I;
-  g.out = actb;
-  hipLaunchKernelGGL(grouped_gemm_kernel<kGateUp>, dim3(ub_tiles, (I + 63) / 64),
-                     dim3(256), 0, stream, g);
-  // down -> y (flat pair order)
   g.a = actb;
   g.w = w2;
   g.w_slot_stride = slot_elems_w2(H, I);
   g.N = H;
   g.K = I;
   g.out = yb;
-  hipLaunchKernelGGL(grouped_gemm_kernel<kDown>, dim3(ub_tiles, (H + 127) / 128),
-                     dim3(256), 0, stream, g);
+  const int ub_tiles = n_pairs / kBM + max_active + 1;
+  hipLaunchKernelGGL(grouped_gemm_kernel<kDown>, dim3(ub_tiles, (H + 127) / 128), dim3(256), 0,
+                     stream, g);
   LMOE_RETURN_LAUNCH();
+}
+
+extern "C" int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
+                                const void* w13_slots, const void* w2_slots,
+                                int n_slots, const int32_t* offsets,
+                                const int32_t* sorted_pairs,
+                                const int32_t* active, const int32_t* tile_off,
+                                const int32_t* meta, int n_pairs, int block_m,
+                                int path, void* act, void* y,
+                                hipStream_t stream) {
+  if (w2_slots == nullptr || y == nullptr) return LMOE_ERR_ARG;
+  int st = lmoe_gateup_silu(x, T, H, I, k, w13_slots, n_slots, offsets, sorted_pairs, active,
+                            tile_off, meta, n_pairs, block_m, path, act, stream);
+  if (st != LMOE_OK) return st;
+  return lmoe_down(act, H, I, w2_slots, n_slots, offsets, sorted_pairs, active, tile_off, meta,
+                   n_pairs, block_m, path, y, stream);
 }
 
 extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,

@@ -108,6 +108,14 @@ __global__ __launch_bounds__(256) void topk_kernel(
   float wgt[kMaxEPL];   // weight carried by a selected expert
   bool elig[kMaxEPL];
   if (scoring == LMOE_SCORING_SOFTMAX) {
+    if (bias != nullptr) {
+      // additive per-expert logit bias (rounded once, before the softmax)
+#pragma unroll
+      for (int j = 0; j < kMaxEPL; ++j) {
+        const int e = j * kWave + lane;
+        if (e < E) lg[j] = lg[j] + bias[e];
+      }
+    }
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kMaxEPL; ++j) m = fmaxf(m, lg[j]);

@@ -120,7 +120,8 @@ def _host_copy(t: torch.Tensor, *, clone: bool, pin: bool) -> tuple[torch.Tensor
     host = src.cpu() if src.device.type != "cpu" else src
     if clone or src.device.type != "cpu":
         host = host.clone()
-    return host.contiguous(), False, None
+    host = host.contiguous()
+    return host, bool(host.is_pinned()) if host.device.type == "cpu" else False, None
 
 
 class HostExpertStore:

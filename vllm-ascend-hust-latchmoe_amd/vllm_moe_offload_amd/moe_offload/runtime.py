@@ -113,6 +113,22 @@ class SlotComputeHandle:
     leases: tuple[SlotLease, ...]
 
 
+@dataclass
+class PendingFixedSlotStage:
+    """A decode staging whose copies are queued but not yet published."""
+
+    layer_id: int
+    active: tuple[int, ...]
+    slot_ids: tuple[int, ...]
+    owners: list
+    ready: object | None
+    hits: tuple[int, ...]
+    misses: tuple[int, ...]
+    log2phy: torch.Tensor
+    step_id: int
+    started: float
+
+
 @dataclass(frozen=True)
 class SlotAddressFingerprint:
     w13_data_ptr: int
@@ -167,6 +183,7 @@ class MoeOffloadRuntime:
         self._prefill_route_stats_by_layer: dict[int, MoePrefillRouteStats] = {}
         self._active_slot_ids_by_layer: dict[int, tuple[int, ...]] = {}
         self._slot_compute_done_events: dict[tuple[int, int, int], object] = {}
+        self._layer_release_events: dict[int, object] = {}
         self._placement_plan_provider: PlacementPlanProvider | None = None
         self._fixed_slot_execution_state = threading.local()
         self._memory_ledger_cache: MoeOffloadMemoryLedger | None = None
@@ -346,6 +363,32 @@ class MoeOffloadRuntime:
             },
         )
 
+    def register_host_buffers(self, *, layer_id: int, w13_host: torch.Tensor, w2_host: torch.Tensor,
+                              slot_device: torch.device) -> None:
+        """Register a layer whose routed experts already sit in host buffers
+        ([E, 2I, H] / [E, H, I], ideally page-locked): no device copy of the
+        full layer is ever made, the buffers become the host store as they are
+        (the CPU-first loading path, cpu_first_loader.py:40-177)."""
+        layer_id = int(layer_id)
+        if layer_id in self._graph_slot_address_fingerprints:
+            raise RuntimeError(f"layer {layer_id} fixed-slot addresses are already captured")
+        holder = torch.nn.Module()
+        holder.layer_id = layer_id
+        holder.w13_weight = w13_host
+        holder.w2_weight = w2_host
+        holder._cpu_first_expert_weights = True
+        E = int(w13_host.shape[0])
+        self._host_store.register_layer(holder, pin_memory=False, clone_tensors=False, routed_expert_count=E)
+        self._original_expert_weight_bytes_by_layer[layer_id] = 0
+        self._expert_weight_bytes_by_layer[layer_id] = _nbytes(w13_host[0]) + _nbytes(w2_host[0])
+        bank = ExpertSlotBank(self.config.num_slots, tuple(int(d) for d in w13_host.shape[1:]),
+                              tuple(int(d) for d in w2_host.shape[1:]), dtype=w13_host.dtype, device=slot_device)
+        self._slot_banks[layer_id] = bank
+        self._fused_shared_lane_layouts.pop(layer_id, None)
+        self._log2phy_buffers[layer_id] = torch.full((E,), -1, dtype=torch.int32, device=slot_device)
+        self._log2phy_slot_by_expert[layer_id] = {}
+        self._memory_ledger_cache = None
+
     # ----------------------------------------------------------- queries
     def slot_readiness_and_ready_slot_ids_for_experts(self, *, layer_id: int, expert_ids) -> tuple[dict[int, bool], dict[int, int]]:
         bank = self._slot_banks.get(int(layer_id))
@@ -513,12 +556,24 @@ class MoeOffloadRuntime:
             if slot.state != SlotState.COMPUTING:
                 raise RuntimeError(f"slot {lease.slot_id} is not computing at compute completion: {slot.state.value}")
         ev = self._record_current_stream_event_or_none()
+        if ev is not None:
+            self._layer_release_events[int(handle.layer_id)] = ev
         for lease in handle.leases:
             slot = bank.slots[int(lease.slot_id)]
             if ev is None:
                 slot.state = SlotState.READY
             else:
                 self._slot_compute_done_events[(int(handle.layer_id), int(lease.slot_id), int(lease.version))] = ev
+
+    def record_layer_compute(self, layer_id: int) -> None:
+        """Record, on the current stream, the end of compute the caller has
+        queued that reads this layer's slot bank (e.g. a graph replay, which
+        bypasses begin/end_slot_compute).  The next miss copies into the bank
+        wait for it on the GPU, so no slot still read by that compute is
+        overwritten."""
+        ev = self._record_current_stream_event_or_none()
+        if ev is not None:
+            self._layer_release_events[int(layer_id)] = ev
 
     # ------------------------------------------------------ decode staging
     def _record_current_stream_event_or_none(self):
@@ -554,6 +609,32 @@ class MoeOffloadRuntime:
                                              record_stage_profile: bool = False) -> PreparedSlotWeights:
         """Decode hot path: hit/miss, one async H2D batch, consumer wait, then
         an in-place update of the changed log2phy entries."""
+        pending = self._reserve_and_issue(layer_id=layer_id, active_experts=active_experts,
+                                          num_logical_experts=num_logical_experts, log2phy=log2phy, step_id=step_id)
+        return self._publish(pending, record_stage_profile=record_stage_profile)
+
+    def prefetch_fixed_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int) -> PendingFixedSlotStage:
+        """Reserve slots and queue the miss copies on the transfer stream now;
+        publish later with complete_fixed_slot_plan (after the previous layer's
+        kernels are queued), so the copies overlap that compute."""
+        if _is_current_graph_capturing():
+            raise RuntimeError("prefetch_fixed_slot_plan must run eager (outside graph capture)")
+        active = resolve_placement_plan(
+            self._placement_plan_provider, layer_id=int(layer_id),
+            routed_experts=tuple(int(e) for e in active_experts), num_logical_experts=int(num_logical_experts),
+        )
+        self._assert_locked_slot_addresses(int(layer_id))
+        return self._reserve_and_issue(layer_id=layer_id, active_experts=active, num_logical_experts=num_logical_experts,
+                                       log2phy=self._log2phy_buffers[int(layer_id)], step_id=None)
+
+    def complete_fixed_slot_plan(self, pending: PendingFixedSlotStage) -> PreparedSlotWeights:
+        """Order the prefetched copies before the current stream, then publish."""
+        prepared = self._publish(pending, record_stage_profile=True)
+        buf = self._log2phy_buffers[int(pending.layer_id)]
+        return PreparedSlotWeights(prepared.w1, prepared.w2, buf, prepared.physical_expert_count, prepared.mapping)
+
+    def _reserve_and_issue(self, *, layer_id: int, active_experts, num_logical_experts: int, log2phy: torch.Tensor,
+                           step_id: int | None) -> PendingFixedSlotStage:
         if not self.should_use_fixed_slots:
             raise RuntimeError("fixed-slot plan requested while moe offload fixed slots are disabled")
         layer_id = int(layer_id)
@@ -611,43 +692,55 @@ class MoeOffloadRuntime:
         ready = None
         if async_loads:
             try:
-                ready = self._transfer_engine.load_many_async(async_loads, record_event=True, validate_layout=False)
+                ready = self._transfer_engine.load_many_async(
+                    async_loads, wait_event=self._layer_release_events.get(layer_id), record_event=True,
+                    validate_layout=False,
+                )
             except Exception:
                 self._release_allocated_loads(bank, async_loads)
                 raise
+        return PendingFixedSlotStage(layer_id, active, tuple(slot_ids), owners, ready, tuple(hits), tuple(misses),
+                                     log2phy, step_id, t0)
+
+    def _publish(self, pending: PendingFixedSlotStage, *, record_stage_profile: bool) -> PreparedSlotWeights:
+        layer_id = pending.layer_id
+        bank = self._slot_banks[layer_id]
         # order the copies before the consumer, THEN publish the mapping
-        if ready is not None:
-            self._wait_transfer_event(ready)
-        upd_e, upd_s = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=tuple(slot_ids))
+        if pending.ready is not None:
+            self._wait_transfer_event(pending.ready)
+        active, slot_ids, owners = pending.active, pending.slot_ids, pending.owners
+        upd_e, upd_s = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=slot_ids)
         if upd_e:
-            _update_log2phy_entries(log2phy, expert_ids=upd_e, slot_ids=upd_s)
+            _update_log2phy_entries(pending.log2phy, expert_ids=upd_e, slot_ids=upd_s)
             self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd_e, slot_ids=upd_s)
         for e, sid in zip(active, slot_ids):
             owners[sid] = e
-        mapping = ExpertSlotMapping(layer_id, active, log2phy, tuple(owners), tuple(slot_ids))
+        mapping = ExpertSlotMapping(layer_id, active, pending.log2phy, tuple(owners), tuple(slot_ids))
         self._active_slot_ids_by_layer[layer_id] = tuple(slot_ids)
+        self.last_stage_stats = (len(pending.hits), len(pending.misses))
         if record_stage_profile and (self.config.profile_path or os.environ.get("LATCHMOE_PROFILE")):
             per = int(self._expert_weight_bytes_by_layer.get(layer_id, 0))
             self._record_profile_event(
                 "decode_fixed_slot_stage",
                 layer_id=layer_id,
-                start=t0,
+                start=pending.started,
                 payload={
                     "n_active": len(active),
-                    "n_hits": len(hits),
-                    "n_misses": len(misses),
-                    "hit_rate": round(len(hits) / len(active), 6) if active else 0.0,
-                    "h2d_bytes": per * len(misses),
-                    "step_id": step_id,
+                    "n_hits": len(pending.hits),
+                    "n_misses": len(pending.misses),
+                    "hit_rate": round(len(pending.hits) / len(active), 6) if active else 0.0,
+                    "h2d_bytes": per * len(pending.misses),
+                    "step_id": pending.step_id,
                     "num_slots": int(self.config.num_slots),
                     "mapping_mode": "persistent_log2phy",
                     "log2phy_update_count": len(upd_e),
-                    "stage_mode": "main_slot_hit" if not misses else ("async_decode_load_many" if async_loads else "sync_decode_load"),
+                    "stage_mode": "main_slot_hit" if not pending.misses else (
+                        "async_decode_load_many" if pending.ready is not None else "sync_decode_load"),
                     "consumer_dependency_installed": True,
                     "mapping_published_after_ready": True,
                     "active_experts": list(active),
-                    "hit_experts": hits,
-                    "miss_experts": misses,
+                    "hit_experts": list(pending.hits),
+                    "miss_experts": list(pending.misses),
                 },
             )
         return PreparedSlotWeights.from_slot_bank(slot_bank=bank, mapping=mapping)
@@ -1117,9 +1210,16 @@ def _update_log2phy_entries(log2phy: torch.Tensor, *, expert_ids, slot_ids) -> N
     if len(expert_ids) == 1:
         log2phy[int(expert_ids[0])] = int(slot_ids[0])
         return
-    idx = torch.tensor([int(e) for e in expert_ids], dtype=torch.long).to(log2phy.device, non_blocking=False)
-    val = torch.tensor([int(s) for s in slot_ids], dtype=log2phy.dtype).to(log2phy.device, non_blocking=False)
-    log2phy.index_copy_(0, idx, val)
+    n = len(expert_ids)
+    if log2phy.device.type != "cuda":
+        idx = torch.tensor([int(e) for e in expert_ids], dtype=torch.long)
+        log2phy.index_copy_(0, idx, torch.tensor([int(v) for v in slot_ids], dtype=log2phy.dtype))
+        return
+    # one page-locked staging tensor and an asynchronous copy: no host sync
+    # (the caching host allocator keeps it alive until the copy has run)
+    host = torch.tensor([int(e) for e in expert_ids] + [int(v) for v in slot_ids], dtype=torch.int32).pin_memory()
+    dev = host.to(log2phy.device, non_blocking=True)
+    log2phy.index_copy_(0, dev[:n].long(), dev[n:].to(log2phy.dtype))
 
 
 _runtime: MoeOffloadRuntime | None = None

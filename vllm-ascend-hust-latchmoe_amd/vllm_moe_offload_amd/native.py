@@ -38,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "lmoe_permute",
     "lmoe_gather_rows",
     "lmoe_grouped_mlp",
+    "lmoe_gateup_silu",
+    "lmoe_down",
     "lmoe_combine",
     "lmoe_fused_moe_decode",
     "lmoe_stage_copy",
@@ -66,6 +68,11 @@ _SIGNATURES = {
         _i,
         [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp],
     ),
+    "lmoe_gateup_silu": (
+        _i,
+        [_vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp],
+    ),
+    "lmoe_down": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "lmoe_combine": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "lmoe_fused_moe_decode": (
         _i,
@@ -347,6 +354,49 @@ def grouped_mlp(
             _stream(stream),
         ),
         "lmoe_grouped_mlp",
+    )
+    return y
+
+
+def gateup_silu(x: torch.Tensor, top_k: int, w13_slots: torch.Tensor, perm: Permutation, act: torch.Tensor,
+                *, path: int = LMOE_PATH_AUTO, stream=None) -> torch.Tensor:
+    """act[pos] = silu(W13_s[:I] x) * (W13_s[I:] x) for the placed pairs (GMM1 + SwiGLU)."""
+    lib = load_library()
+    _need(x, "x", torch.bfloat16)
+    _need(w13_slots, "w13_slots", torch.bfloat16)
+    T, H = x.shape
+    P, two_i, h = w13_slots.shape
+    if h != H or P != perm.n_slots:
+        raise ValueError("w13_slots does not match x or the permutation")
+    I = two_i // 2
+    _need(act, "act", torch.bfloat16, (perm.n_pairs, I))
+    _check(
+        lib.lmoe_gateup_silu(
+            _ptr(x), T, H, I, int(top_k), _ptr(w13_slots), P, _ptr(perm.offsets), _ptr(perm.sorted_pairs),
+            _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta), perm.n_pairs, MFMA_BLOCK_M, int(path),
+            _ptr(act), _stream(stream),
+        ),
+        "lmoe_gateup_silu",
+    )
+    return act
+
+
+def down(act: torch.Tensor, w2_slots: torch.Tensor, perm: Permutation, y: torch.Tensor,
+         *, path: int = LMOE_PATH_AUTO, stream=None) -> torch.Tensor:
+    """y[pair] = W2_s act[pos] for the placed pairs (GMM2)."""
+    lib = load_library()
+    _need(w2_slots, "w2_slots", torch.bfloat16)
+    P, H, I = w2_slots.shape
+    if P != perm.n_slots:
+        raise ValueError("w2_slots does not match the permutation")
+    _need(act, "act", torch.bfloat16, (perm.n_pairs, I))
+    _need(y, "y", torch.bfloat16, (perm.n_pairs, H))
+    _check(
+        lib.lmoe_down(
+            _ptr(act), H, I, _ptr(w2_slots), P, _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.active),
+            _ptr(perm.tile_off), _ptr(perm.meta), perm.n_pairs, MFMA_BLOCK_M, int(path), _ptr(y), _stream(stream),
+        ),
+        "lmoe_down",
     )
     return y
 
