@@ -3,14 +3,15 @@
 
 Headline (value): Qwen3-30B-A3B-shaped decode, 48 MoE layers, 64 slots per
 layer, batch 1 — MoE-layer microseconds per token per layer, measured as the
-hipGraph replay of the 48-layer decode compute (router -> permute -> gate_up
-GEMV -> down GEMV + combine per layer) after the step's eager staging has
-made every routed expert resident.  Also reported in the same JSON line:
+hipGraph replay of the 48-layer decode compute (per layer: one router launch
+= gate + top-k, one layer-body launch = slot remap + grouping + gate_up +
+SiLU*mul + down + combine) after the step's eager staging has made every
+routed expert resident.  Also reported in the same JSON line:
 
   decode[B]   B in --batches: graph-replayed layer us/token, layer HBM GB/s,
               slot-miss rate of the Zipf-skewed router, and the eager
               staging-inclusive step time (D2H of the ids, LRU, H2D)
-  roofline    dominant kernel (gate_up GEMV + SiLU*mul at B=1), timed with
+  roofline    dominant kernel (the layer-body launch at B=1), timed with
               HIP events over launches rotating through the 48 layers
   prefill     4096 tokens, 48 slots, uniform router: capacity waves with one
               combine (compute TFLOP/s and MFMA fraction; staged wall time;
@@ -115,10 +116,15 @@ class DecodeModel:
 
 
 def _route(x, model, l, w_out, ids_out, logits_out):
-    from vllm_moe_offload_amd import native
+    """Gate + selection: one launch up to 16 tokens, two beyond."""
+    from vllm_moe_offload_amd import fused_moe, native
 
-    native.router_gate(x, model.gates[l], logits_out)
-    native.router_topk(logits_out, K, bias=model.specs[l].e_score_correction_bias, w_bf16=w_out, ids=ids_out)
+    if x.shape[0] <= native.ROUTE_DECODE_MAX_TOKENS:
+        native.router_decode(x, model.gates[l], K, fused_moe.route_sync(x.device),
+                             bias=model.specs[l].e_score_correction_bias, logits=logits_out, w_bf16=w_out, ids=ids_out)
+    else:
+        native.router_gate(x, model.gates[l], logits_out)
+        native.router_topk(logits_out, K, bias=model.specs[l].e_score_correction_bias, w_bf16=w_out, ids=ids_out)
 
 
 def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int, budget_s: float) -> dict:
@@ -260,37 +266,39 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
         res["eager_stage_ms_per_step"] = round(sum(stage_ms) / len(stage_ms), 3)
     if overflow_ms:
         res["overflow_eager_ms_per_step"] = round(sum(overflow_ms) / len(overflow_ms), 3)
-    res["_state"] = (ws_ids, static_x)
+    res["_state"] = (ws_w, ws_ids, static_x)
     return res
 
 
-def bench_gateup_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
-    """Dominant decode kernel at B=1: gate_up GEMV + SiLU*mul, 48*reps
-    launches rotating through the 48 layers' slot banks (29 GB, far beyond
-    the 256 MB MALL), captured in one graph so they run back to back, timed
-    with HIP events on the stream they are launched on."""
+def bench_decode_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
+    """Dominant decode kernel at B=1: the one-launch layer body
+    (moe_decode_kernel: remap, grouping, gate_up + SiLU*mul, down, combine),
+    48*reps launches rotating through the 48 layers' slot banks (29 GB, far
+    beyond the 256 MB MALL), captured in one graph so they run back to back,
+    timed with HIP events on the stream they are launched on."""
     import torch
 
-    from vllm_moe_offload_amd import native
+    from vllm_moe_offload_amd import fused_moe, native
 
-    ws_ids, x = state
+    ws_w, ws_ids, x = state
     L = model.L
     dev = torch.device("cuda")
     B = x.shape[0]
     P = model.bank(0).physical_expert_count
-    perms, acts = [], []
+    ws = fused_moe.get_workspace(B, K, P, H, I, dev, tag="roofline")
+    out = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
+    U = []
     for l in range(L):
-        p = native.Permutation.allocate(B * K, P, dev)
-        native.permute(ws_ids[l], p, log2phy=model.rt.log2phy_buffer(l))
-        perms.append(p)
-        acts.append(torch.empty((B * K, I), dtype=torch.bfloat16, device=dev))
-    torch.cuda.synchronize()
-    U = [int(perms[l].meta[native.META_ACTIVE].item()) for l in range(L)]
+        native.moe_decode(x, ws_w[l], ws_ids[l], model.bank(l).w13_slots, model.bank(l).w2_slots,
+                          model.rt.log2phy_buffer(l), out, ws.act, ws.y, ws.sync, ws.meta)
+        torch.cuda.synchronize()
+        U.append(int(ws.meta[native.META_ACTIVE].item()))
 
     def launches():
         for _ in range(reps):
             for l in range(L):
-                native.gateup_silu(x, K, model.bank(l).w13_slots, perms[l], acts[l], path=native.LMOE_PATH_GEMV)
+                native.moe_decode(x, ws_w[l], ws_ids[l], model.bank(l).w13_slots, model.bank(l).w2_slots,
+                                  model.rt.log2phy_buffer(l), out, ws.act, ws.y, ws.sync, ws.meta)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -305,12 +313,15 @@ def bench_gateup_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
     with Timer(stream) as t:
         g.replay()
     ms = t.ms()
+    torch.cuda.synchronize()
+    assert int(ws.meta[native.META_STALLS].item()) == 0
     n = reps * L
     avg_us = ms * 1000.0 / n
     u = sum(U) / L
-    bytes_per_launch = u * (2 * I * H * 2) + B * H * 2 + B * K * I * 2
+    # weights of the distinct slots + ids/log2phy/x/w in + act, y out and back + out
+    bytes_per_launch = u * EXPERT_BYTES + B * H * 2 + B * K * (I + H) * 2 * 2 + B * H * 2
     return {
-        "kernel": "gateup_gemv_kernel",
+        "kernel": "moe_decode_kernel",
         "avg_launch_us": round(avg_us, 3),
         "bytes_per_launch": int(bytes_per_launch),
         "distinct_slots_per_launch": round(u, 2),
@@ -701,7 +712,7 @@ def main() -> int:
         r = bench_decode(model, B, args.steps, args.warmup, seed=17, budget_s=args.budget_s)
         state = r.pop("_state")
         if B == 1:
-            roof = bench_gateup_roofline(model, state)
+            roof = bench_decode_roofline(model, state)
         decode[f"B{B}"] = r
         log(f"decode B={B}: {r} ({time.perf_counter() - t0:.1f}s)")
     t_decode = time.perf_counter() - t_run0
@@ -756,7 +767,7 @@ def main() -> int:
                             "kernel": roof["kernel"], "avg_launch_us": roof["avg_launch_us"],
                             "bytes_per_launch": roof["bytes_per_launch"],
                             "distinct_slots_per_launch": roof["distinct_slots_per_launch"]}
-        traffic_file = ROOT / "profiles" / "gateup_gemv_decode_b1_traffic.json"
+        traffic_file = ROOT / "profiles" / "moe_decode_b1_traffic.json"
         if traffic_file.exists():
             try:
                 line["roofline"]["traffic"] = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")

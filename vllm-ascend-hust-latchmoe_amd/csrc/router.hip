@@ -7,15 +7,12 @@
 // (w / w.sum().clamp_min(eps)), grouped sigmoid as configured for the
 // DeepSeek-V3-style layer (bias for selection only, sum of the two best scores
 // per group, keep topk_group groups, renormalise, then scale).
-#include <float.h>
-
 #include "gemm_mfma.h"
+#include "select.h"
 
 namespace lmoe {
 
 constexpr int kGateMaxChunks = 16;  // H <= 16 * 512 = 8192 in the GEMV path
-constexpr int kMaxEPL = 8;          // E <= 8 * 64 = 512 experts per token
-constexpr int kMaxK = 16;
 
 // logits[t][e] for e = 4*blockIdx.x + wave, tokens [t0, t1).  The expert row
 // stays in registers (one 16-byte chunk per 512 columns per lane) while the
@@ -60,190 +57,106 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
   }
 }
 
-// (value desc, id asc) ordering used by every selection step.
-__device__ __forceinline__ bool better(float v, int e, float v2, int e2) {
-  return (v > v2) || (v == v2 && e < e2);
-}
-
-// Wave-wide arg-best: all lanes return the winning (value, id).
-__device__ __forceinline__ void wave_argbest(float& v, int& e) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    const float v2 = __shfl_xor(v, o, kWave);
-    const int e2 = __shfl_xor(e, o, kWave);
-    if (better(v2, e2, v, e)) {
-      v = v2;
-      e = e2;
-    }
-  }
-}
-
-// One wave per token; lane l holds experts e = j*64 + l, j < kMaxEPL.
+// One wave per token.
 __global__ __launch_bounds__(256) void topk_kernel(
-    const void* __restrict__ logits, int logits_f32, int T, int E, int k,
-    int scoring, const float* __restrict__ bias, int n_group, int topk_group,
-    int renorm, float routed_scale, float* __restrict__ w_f32,
-    uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids) {
-  __shared__ float sel_lds[4][kMaxEPL * kWave];
+    const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
+    float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16,
+    int32_t* __restrict__ ids) {
+  __shared__ SelectLds lds[4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
-  const bool token_ok = t < T;
-  const int tt = token_ok ? t : 0;
-
   float lg[kMaxEPL];
-#pragma unroll
-  for (int j = 0; j < kMaxEPL; ++j) {
-    const int e = j * kWave + lane;
-    float v = -INFINITY;
-    if (e < E) {
-      const size_t o = static_cast<size_t>(tt) * E + e;
-      v = logits_f32 ? reinterpret_cast<const float*>(logits)[o]
-                     : bf16_to_f32(reinterpret_cast<const uint16_t*>(logits)[o]);
-    }
-    lg[j] = v;
-  }
-
-  float sel[kMaxEPL];   // selection score
-  float wgt[kMaxEPL];   // weight carried by a selected expert
-  bool elig[kMaxEPL];
-  if (scoring == LMOE_SCORING_SOFTMAX) {
-    if (bias != nullptr) {
-      // additive per-expert logit bias (rounded once, before the softmax)
-#pragma unroll
-      for (int j = 0; j < kMaxEPL; ++j) {
-        const int e = j * kWave + lane;
-        if (e < E) lg[j] = lg[j] + bias[e];
-      }
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kMaxEPL; ++j) m = fmaxf(m, lg[j]);
-    m = wave_max(m);
-    float ex[kMaxEPL];
-    float local = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxEPL; ++j) {
-      const int e = j * kWave + lane;
-      ex[j] = (e < E) ? exp_nonpos(lg[j] - m) : 0.0f;
-      local = (j == 0) ? ex[0] : local + ex[j];
-    }
-    const float s = wave_sum(local);
-#pragma unroll
-    for (int j = 0; j < kMaxEPL; ++j) {
-      const int e = j * kWave + lane;
-      const float p = ex[j] / s;
-      sel[j] = p;
-      wgt[j] = p;
-      elig[j] = e < E;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < kMaxEPL; ++j) {
-      const int e = j * kWave + lane;
-      const float sg = sigmoid_det(lg[j]);
-      const float sb = (e < E && bias != nullptr) ? sg + bias[e] : sg;
-      sel[j] = sb;
-      wgt[j] = sg;
-      elig[j] = e < E;
-    }
-    if (n_group > 1) {
-      const int gs = E / n_group;
-#pragma unroll
-      for (int j = 0; j < kMaxEPL; ++j) {
-        const int e = j * kWave + lane;
-        if (e < E) sel_lds[wave][e] = sel[j];
-      }
-      __syncthreads();
-      // group score = best + second best selection score of the group
-      float gscore = -INFINITY;
-      if (lane < n_group) {
-        float m1 = -INFINITY, m2 = -INFINITY;
-        for (int i = 0; i < gs; ++i) {
-          const float v = sel_lds[wave][lane * gs + i];
-          if (v > m1) {
-            m2 = m1;
-            m1 = v;
-          } else if (v > m2) {
-            m2 = v;
-          }
-        }
-        gscore = m1 + m2;
-      }
-      uint64_t kept = 0ull;
-      bool gtaken = false;
-      for (int it = 0; it < topk_group; ++it) {
-        float v = (lane < n_group && !gtaken) ? gscore : -INFINITY;
-        int g = (lane < n_group && !gtaken) ? lane : 0x7fffffff;
-        wave_argbest(v, g);
-        if (g >= 0 && g < 64) kept |= 1ull << g;
-        if (lane == g) gtaken = true;
-      }
-#pragma unroll
-      for (int j = 0; j < kMaxEPL; ++j) {
-        const int e = j * kWave + lane;
-        elig[j] = (e < E) && ((kept >> (e / gs)) & 1ull);
-      }
-    }
-  }
-
-  // k rounds of wave arg-best; lane-local candidates scanned in ascending j,
-  // i.e. ascending expert id, so the first maximum is the lowest id.
-  uint32_t taken = 0u;
-  int sel_e[kMaxK];
-  float sel_w[kMaxK];
-#pragma unroll
-  for (int it = 0; it < kMaxK; ++it) {
-    sel_e[it] = 0;
-    sel_w[it] = 0.0f;
-    if (it < k) {
-      float bv = -INFINITY;
-      int be = 0x7fffffff;
-      float bw = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kMaxEPL; ++j) {
-        const int e = j * kWave + lane;
-        if (elig[j] && !((taken >> j) & 1u) && better(sel[j], e, bv, be)) {
-          bv = sel[j];
-          be = e;
-          bw = wgt[j];
-        }
-      }
-      float v = bv;
-      int e = be;
-      wave_argbest(v, e);
-      const bool found = e >= 0 && e < E;
-      const int owner = found ? (e & 63) : 0;
-      const float w = __shfl(bw, owner, kWave);
-      if (found && lane == owner) taken |= 1u << (e >> 6);
-      if (!found) e = -1;  // no eligible expert left: an id no table maps
-      sel_e[it] = e;
-      sel_w[it] = w;
-    }
-  }
-
-  float sum = sel_w[0];
-#pragma unroll
-  for (int it = 1; it < kMaxK; ++it)
-    if (it < k) sum = sum + sel_w[it];
-  const float denom = fmaxf(sum, FLT_EPSILON);
-
-  if (token_ok && lane < k) {
-    int my_e = 0;
-    float my_w = 0.0f;
-#pragma unroll
-    for (int it = 0; it < kMaxK; ++it) {
-      if (lane == it) {
-        my_e = sel_e[it];
-        my_w = sel_w[it];
-      }
-    }
-    float w = renorm ? my_w / denom : my_w;
-    w = w * routed_scale;
-    const size_t o = static_cast<size_t>(t) * k + lane;
-    ids[o] = my_e;
+  load_logits(logits, logits_f32, t < T ? t : 0, sp.E, lg);
+  int e;
+  float w;
+  select_token(sp, lg, lds[wave], e, w);
+  if (t < T && lane < sp.k) {
+    const size_t o = static_cast<size_t>(t) * sp.k + lane;
+    ids[o] = e;
     w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
     if (w_f32 != nullptr) w_f32[o] = w;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode router: gate + selection in one launch.  Block b's 8 waves compute
+// the logits of experts 8b .. 8b+7 for all T tokens (expert row in
+// registers); the last block to finish (device-scope counter, reset by that
+// block) selects the experts of every token, 8 tokens at a time.  No block
+// ever waits for another, so the launch cannot stall.
+// ---------------------------------------------------------------------------
+constexpr int kRouteDecodeMaxT = 16;
+constexpr int kRouteWaves = 8;
+
+template <int NC>
+__global__ __launch_bounds__(512) void route_decode_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T,
+    int H, SelectParams sp, void* __restrict__ logits, int logits_f32,
+    float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16,
+    int32_t* __restrict__ ids, int32_t* __restrict__ sync) {
+  __shared__ SelectLds lds[kRouteWaves];
+  __shared__ int is_last;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int E = sp.E;
+  const int e = blockIdx.x * kRouteWaves + wave;
+  if (e < E) {
+    const uint16_t* wrow = wg + static_cast<size_t>(e) * H;
+    uint4 w[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int h = c * 512 + lane * 8;
+      w[c] = (h < H) ? *reinterpret_cast<const uint4*>(wrow + h)
+                     : make_uint4(0u, 0u, 0u, 0u);
+    }
+    for (int t = 0; t < T; ++t) {
+      const uint16_t* xr = x + static_cast<size_t>(t) * H;
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int h = c * 512 + lane * 8;
+        if (h < H) acc = dot8(*reinterpret_cast<const uint4*>(xr + h), w[c], acc);
+      }
+      acc = wave_sum(acc);
+      if (lane == 0) {
+        const size_t o = static_cast<size_t>(t) * E + e;
+        if (logits_f32) {
+          reinterpret_cast<float*>(logits)[o] = acc;
+        } else {
+          reinterpret_cast<uint16_t*>(logits)[o] =
+              static_cast<uint16_t>(f32_to_bf16_bits(acc));
+        }
+      }
+    }
+  }
+  // publish this block's logits, then count it
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int done = __hip_atomic_fetch_add(sync, 1, __ATOMIC_ACQ_REL,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    is_last = done == static_cast<int>(gridDim.x) - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  for (int t0 = 0; t0 < T; t0 += kRouteWaves) {
+    const int t = t0 + wave;
+    float lg[kMaxEPL];
+    load_logits(logits, logits_f32, t < T ? t : 0, E, lg);
+    int se;
+    float sw;
+    select_token(sp, lg, lds[wave], se, sw);
+    if (t < T && lane < sp.k) {
+      const size_t o = static_cast<size_t>(t) * sp.k + lane;
+      ids[o] = se;
+      w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(sw));
+      if (w_f32 != nullptr) w_f32[o] = sw;
+    }
+  }
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -283,6 +196,35 @@ extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
   LMOE_RETURN_LAUNCH();
 }
 
+static int check_select(int T, int E, int k, int scoring, int n_group,
+                        int topk_group) {
+  if (T < 0 || E <= 0 || k <= 0) return LMOE_ERR_ARG;
+  if (E > kMaxE || k > kMaxK || k > E) return LMOE_ERR_SHAPE;
+  if (scoring != LMOE_SCORING_SOFTMAX && scoring != LMOE_SCORING_SIGMOID)
+    return LMOE_ERR_UNSUPPORTED;
+  if (scoring == LMOE_SCORING_SIGMOID && n_group > 1) {
+    if (n_group > 64 || E % n_group != 0 || E / n_group < 2) return LMOE_ERR_SHAPE;
+    if (topk_group <= 0 || topk_group > n_group) return LMOE_ERR_SHAPE;
+    if (k > topk_group * (E / n_group)) return LMOE_ERR_SHAPE;
+  }
+  return LMOE_OK;
+}
+
+static SelectParams make_select(int E, int k, int scoring, const float* bias,
+                                int n_group, int topk_group, int renorm,
+                                float routed_scale) {
+  SelectParams sp;
+  sp.E = E;
+  sp.k = k;
+  sp.scoring = scoring;
+  sp.bias = bias;
+  sp.n_group = scoring == LMOE_SCORING_SIGMOID ? (n_group > 1 ? n_group : 1) : 1;
+  sp.topk_group = topk_group;
+  sp.renorm = renorm;
+  sp.routed_scale = routed_scale;
+  return sp;
+}
+
 extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
                                 int E, int k, int scoring, const float* bias,
                                 int n_group, int topk_group, int renorm,
@@ -291,20 +233,48 @@ extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
                                 hipStream_t stream) {
   if (logits == nullptr || w_bf16 == nullptr || ids == nullptr)
     return LMOE_ERR_ARG;
-  if (T < 0 || E <= 0 || k <= 0) return LMOE_ERR_ARG;
-  if (E > kMaxEPL * kWave || k > kMaxK || k > E) return LMOE_ERR_SHAPE;
-  if (scoring != LMOE_SCORING_SOFTMAX && scoring != LMOE_SCORING_SIGMOID)
-    return LMOE_ERR_UNSUPPORTED;
-  if (scoring == LMOE_SCORING_SIGMOID && n_group > 1) {
-    if (n_group > 64 || E % n_group != 0 || E / n_group < 2) return LMOE_ERR_SHAPE;
-    if (topk_group <= 0 || topk_group > n_group) return LMOE_ERR_SHAPE;
-    if (k > topk_group * (E / n_group)) return LMOE_ERR_SHAPE;
-  }
+  const int st = check_select(T, E, k, scoring, n_group, topk_group);
+  if (st != LMOE_OK) return st;
   if (T == 0) return LMOE_OK;
-  dim3 grid((T + 3) / 4);
-  hipLaunchKernelGGL(topk_kernel, grid, dim3(256), 0, stream, logits,
-                     logits_f32, T, E, k, scoring, bias,
-                     scoring == LMOE_SCORING_SIGMOID ? n_group : 1, topk_group,
-                     renorm, routed_scale, w_f32, w_bf16, ids);
+  const SelectParams sp =
+      make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, stream,
+                     logits, logits_f32, T, sp, w_f32, w_bf16, ids);
+  LMOE_RETURN_LAUNCH();
+}
+
+extern "C" int lmoe_router_decode(const void* x, const void* wg, int T, int H,
+                                  int E, int k, int scoring, const float* bias,
+                                  int n_group, int topk_group, int renorm,
+                                  float routed_scale, void* logits,
+                                  int logits_f32, float* w_f32,
+                                  uint16_t* w_bf16, int32_t* ids,
+                                  int32_t* sync, hipStream_t stream) {
+  if (x == nullptr || wg == nullptr || logits == nullptr || w_bf16 == nullptr ||
+      ids == nullptr || sync == nullptr)
+    return LMOE_ERR_ARG;
+  if (H <= 0) return LMOE_ERR_ARG;
+  const int st = check_select(T, E, k, scoring, n_group, topk_group);
+  if (st != LMOE_OK) return st;
+  if (T > kRouteDecodeMaxT || H % 8 != 0 || H > kGateMaxChunks * 512)
+    return LMOE_ERR_SHAPE;
+  if (T == 0) return LMOE_OK;
+  const SelectParams sp =
+      make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  const dim3 grid((E + kRouteWaves - 1) / kRouteWaves);
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint16_t* wb = static_cast<const uint16_t*>(wg);
+  const int nc = (H + 511) / 512;
+  if (nc <= 4) {
+    hipLaunchKernelGGL(route_decode_kernel<4>, grid, dim3(512), 0, stream, xb, wb,
+                       T, H, sp, logits, logits_f32, w_f32, w_bf16, ids, sync);
+  } else if (nc <= 8) {
+    hipLaunchKernelGGL(route_decode_kernel<8>, grid, dim3(512), 0, stream, xb, wb,
+                       T, H, sp, logits, logits_f32, w_f32, w_bf16, ids, sync);
+  } else {
+    hipLaunchKernelGGL(route_decode_kernel<16>, grid, dim3(512), 0, stream, xb,
+                       wb, T, H, sp, logits, logits_f32, w_f32, w_bf16, ids,
+                       sync);
+  }
   LMOE_RETURN_LAUNCH();
 }

@@ -44,9 +44,12 @@ from vllm_moe_offload_amd.moe_offload.slot_mapping import PreparedSlotWeights
 @dataclass
 class MoEWorkspace:
     perm: native.Permutation
-    act: torch.Tensor   # [N, I] bf16, sorted order
+    act: torch.Tensor   # [N, I] bf16 (sorted order; flat pair order in moe_decode)
     y: torch.Tensor     # [N, H] bf16, flat pair order
     out: torch.Tensor   # [T, H] bf16
+    sync: torch.Tensor  # int32 counters of moe_decode, zero between launches
+    meta: torch.Tensor  # int32 [META_COUNT] of moe_decode
+    last_meta: torch.Tensor | None = None  # meta written by the last fused_experts call
 
 
 _WORKSPACES: dict[tuple, MoEWorkspace] = {}
@@ -57,11 +60,14 @@ def get_workspace(T: int, k: int, P: int, H: int, I: int, device, *, tag: str = 
     ws = _WORKSPACES.get(key)
     if ws is None:
         N = T * k
+        words = native.moe_decode_sync_words(N, P, H, I) if 0 < N <= native.MOE_DECODE_MAX_PAIRS else 1
         ws = MoEWorkspace(
             perm=native.Permutation.allocate(N, P, device),
             act=torch.empty((max(N, 1), I), dtype=torch.bfloat16, device=device),
             y=torch.empty((max(N, 1), H), dtype=torch.bfloat16, device=device),
             out=torch.empty((max(T, 1), H), dtype=torch.bfloat16, device=device),
+            sync=torch.zeros(max(words, 1), dtype=torch.int32, device=device),
+            meta=torch.zeros(native.META_COUNT, dtype=torch.int32, device=device),
         )
         _WORKSPACES[key] = ws
     return ws
@@ -69,6 +75,22 @@ def get_workspace(T: int, k: int, P: int, H: int, I: int, device, *, tag: str = 
 
 def clear_workspaces() -> None:
     _WORKSPACES.clear()
+    _ROUTE_SYNC.clear()
+
+
+_ROUTE_SYNC: dict[str, torch.Tensor] = {}
+
+
+def route_sync(device) -> torch.Tensor:
+    """The per-device counter of the one-launch decode router (zero between
+    launches).  Launches that share it must not run concurrently: route on
+    one stream, or pass each concurrent caller its own zeroed int32."""
+    key = str(torch.device(device))
+    t = _ROUTE_SYNC.get(key)
+    if t is None:
+        t = torch.zeros(1, dtype=torch.int32, device=device)
+        _ROUTE_SYNC[key] = t
+    return t
 
 
 # ---------------------------------------------------------------------------
@@ -90,9 +112,22 @@ class RouterSpec:
 
 def route(hidden: torch.Tensor, gate_weight: torch.Tensor | None, spec: RouterSpec, *,
           router_logits: torch.Tensor | None = None, logits_out: torch.Tensor | None = None,
-          w_out: torch.Tensor | None = None, ids_out: torch.Tensor | None = None):
+          w_out: torch.Tensor | None = None, ids_out: torch.Tensor | None = None,
+          sync: torch.Tensor | None = None):
     """Gate (if gate_weight is given) then expert selection on the GPU.
-    Returns (topk_weights bf16 [T,k], topk_ids int32 [T,k], logits)."""
+    Returns (topk_weights bf16 [T,k], topk_ids int32 [T,k], logits).  Up to
+    16 tokens with a gate weight run as one launch (gate + selection)."""
+    grouped = bool(spec.use_grouped_topk)
+    if gate_weight is not None and hidden.shape[0] <= native.ROUTE_DECODE_MAX_TOKENS and router_logits is None:
+        w, ids, logits = native.router_decode(
+            hidden, gate_weight, int(spec.top_k), sync if sync is not None else route_sync(hidden.device),
+            scoring=spec.scoring_func, bias=spec.e_score_correction_bias,
+            num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
+            topk_group=int(spec.topk_group or 1) if grouped else 1,
+            renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
+            logits=logits_out, w_bf16=w_out, ids=ids_out,
+        )
+        return w, ids, logits
     if gate_weight is not None:
         T = hidden.shape[0]
         E = gate_weight.shape[0]
@@ -101,7 +136,6 @@ def route(hidden: torch.Tensor, gate_weight: torch.Tensor | None, spec: RouterSp
         router_logits = native.router_gate(hidden, gate_weight, logits_out)
     if router_logits is None:
         raise ValueError("route() needs router_logits or a gate weight")
-    grouped = bool(spec.use_grouped_topk)
     w, ids, _ = native.router_topk(
         router_logits, int(spec.top_k), scoring=spec.scoring_func,
         bias=spec.e_score_correction_bias,
@@ -129,15 +163,24 @@ def fused_experts(
     path: int = native.LMOE_PATH_AUTO,
     workspace: MoEWorkspace | None = None,
 ) -> torch.Tensor:
-    """out[t] = add[t] + sum_j w[t,j] * MLP_{slot(ids[t,j])}(x_t)."""
+    """out[t] = add[t] + sum_j w[t,j] * MLP_{slot(ids[t,j])}(x_t).
+
+    AUTO: up to 512 pairs run as one decode launch (remap, grouping, both
+    GEMVs, combine); more pairs permute and run the grouped MFMA GEMM (or
+    the GEMV kernels when path is GEMV) and the combine."""
     T, H = hidden.shape
     k = int(topk_ids.shape[1])
     P = int(w13_slots.shape[0])
     I = int(w13_slots.shape[1]) // 2
     ws = workspace or get_workspace(T, k, P, H, I, hidden.device)
-    native.permute(topk_ids, ws.perm, log2phy=log2phy)
     dst = out if out is not None else ws.out[:T]
-    if T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA:
+    if path == native.LMOE_PATH_AUTO and 0 < T * k <= native.MOE_DECODE_MAX_PAIRS:
+        ws.last_meta = ws.meta
+        return native.moe_decode(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2phy, dst,
+                                 ws.act, ws.y, ws.sync, ws.meta, add=add)
+    native.permute(topk_ids, ws.perm, log2phy=log2phy)
+    ws.last_meta = ws.perm.meta
+    if T * k <= native.FUSED_DECODE_MAX_PAIRS and path == native.LMOE_PATH_GEMV:
         native.fused_moe_decode(hidden, topk_weights, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add)
     else:
         native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
@@ -147,7 +190,7 @@ def fused_experts(
 
 def check_placed(ws: MoEWorkspace) -> None:
     """Host validation (synchronising): fail if a pair mapped to no slot."""
-    meta = ws.perm.meta.cpu().tolist()
+    meta = (ws.last_meta if ws.last_meta is not None else ws.perm.meta).cpu().tolist()
     if meta[native.META_ERRORS]:
         raise RuntimeError(f"topk_ids contain experts without ready slots: {meta[native.META_ERRORS]} pairs")
 
