@@ -219,7 +219,7 @@ def test_moe_decode_matches_oracle(T, k, E, P, H, I):
 def test_moe_decode_unmapped_pairs_add_term_and_identity_table():
     native = _native()
     rng = np.random.default_rng(808)
-    T, k, E, P, H, I = 6, 4, 32, 16, 1024, 256
+    T, k, E, P, H, I = 6, 4, 32, 24, 1024, 256
     ids, l2p, x, w13, w2, wb = _case(808, T, k, E, P, H, I)
     l2p = l2p.copy()
     dropped = np.unique(ids)[:3]
