@@ -54,6 +54,7 @@ def grouped_mlp(
     referenced are converted).
     """
     x = bf16_to_f32(x_bf16)
+    slot_of_pair = np.asarray(slot_of_pair).reshape(-1)  # flat pair order
     N = slot_of_pair.size
     H = x.shape[1]
     y = np.zeros((N, H), dtype=np.float32)
