@@ -3,16 +3,16 @@
 
 Headline (value): Qwen3-30B-A3B-shaped decode, 48 MoE layers, 64 slots per
 layer, batch 1 — MoE-layer microseconds per token per layer, measured as the
-hipGraph replay of the 48-layer decode compute (per layer: one router launch
-= gate + top-k, one layer-body launch = slot remap + grouping + gate_up +
-SiLU*mul + down + combine) after the step's eager staging has made every
-routed expert resident.  Also reported in the same JSON line:
+hipGraph replay of the 48-layer decode compute (per layer: gate GEMV, top-k,
+gate_up + SiLU*mul, down + combine; slot remap and grouping inside the last
+two) after the step's eager staging has made every routed expert resident.  Also reported in the same JSON line:
 
   decode[B]   B in --batches: graph-replayed layer us/token, layer HBM GB/s,
               slot-miss rate of the Zipf-skewed router, and the eager
               staging-inclusive step time (D2H of the ids, LRU, H2D)
-  roofline    dominant kernel (the layer-body launch at B=1), timed with
-              HIP events over launches rotating through the 48 layers
+  roofline    dominant work (the layer body lmoe_moe_decode at B=1: its
+              gate_up and down + combine kernels), timed with HIP events
+              over calls rotating through the 48 layers
   prefill     4096 tokens, 48 slots, uniform router: capacity waves with one
               combine (compute TFLOP/s and MFMA fraction; staged wall time;
               H2D GB/s), against the blocking full layer
@@ -116,15 +116,11 @@ class DecodeModel:
 
 
 def _route(x, model, l, w_out, ids_out, logits_out):
-    """Gate + selection: one launch up to 16 tokens, two beyond."""
-    from vllm_moe_offload_amd import fused_moe, native
+    """Gate GEMV then top-k selection (two launches)."""
+    from vllm_moe_offload_amd import native
 
-    if x.shape[0] <= native.ROUTE_DECODE_MAX_TOKENS:
-        native.router_decode(x, model.gates[l], K, fused_moe.route_sync(x.device),
-                             bias=model.specs[l].e_score_correction_bias, logits=logits_out, w_bf16=w_out, ids=ids_out)
-    else:
-        native.router_gate(x, model.gates[l], logits_out)
-        native.router_topk(logits_out, K, bias=model.specs[l].e_score_correction_bias, w_bf16=w_out, ids=ids_out)
+    native.router_gate(x, model.gates[l], logits_out)
+    native.router_topk(logits_out, K, bias=model.specs[l].e_score_correction_bias, w_bf16=w_out, ids=ids_out)
 
 
 def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int, budget_s: float) -> dict:
@@ -271,11 +267,11 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
 
 
 def bench_decode_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
-    """Dominant decode kernel at B=1: the one-launch layer body
-    (moe_decode_kernel: remap, grouping, gate_up + SiLU*mul, down, combine),
-    48*reps launches rotating through the 48 layers' slot banks (29 GB, far
-    beyond the 256 MB MALL), captured in one graph so they run back to back,
-    timed with HIP events on the stream they are launched on."""
+    """Dominant decode work at B=1: the layer body lmoe_moe_decode (its
+    gate_up kernel and its down + combine kernel, remap and grouping inside
+    both), 48*reps calls rotating through the 48 layers' slot banks (29 GB,
+    far beyond the 256 MB MALL), captured in one graph so they run back to
+    back, timed with HIP events on the stream they are launched on."""
     import torch
 
     from vllm_moe_offload_amd import fused_moe, native
@@ -290,7 +286,7 @@ def bench_decode_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
     U = []
     for l in range(L):
         native.moe_decode(x, ws_w[l], ws_ids[l], model.bank(l).w13_slots, model.bank(l).w2_slots,
-                          model.rt.log2phy_buffer(l), out, ws.act, ws.y, ws.sync, ws.meta)
+                          model.rt.log2phy_buffer(l), out, ws.act, ws.meta)
         torch.cuda.synchronize()
         U.append(int(ws.meta[native.META_ACTIVE].item()))
 
@@ -298,7 +294,7 @@ def bench_decode_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
         for _ in range(reps):
             for l in range(L):
                 native.moe_decode(x, ws_w[l], ws_ids[l], model.bank(l).w13_slots, model.bank(l).w2_slots,
-                                  model.rt.log2phy_buffer(l), out, ws.act, ws.y, ws.sync, ws.meta)
+                                  model.rt.log2phy_buffer(l), out, ws.act, ws.meta)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -314,14 +310,14 @@ def bench_decode_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
         g.replay()
     ms = t.ms()
     torch.cuda.synchronize()
-    assert int(ws.meta[native.META_STALLS].item()) == 0
+    assert int(ws.meta[native.META_ERRORS].item()) == 0
     n = reps * L
     avg_us = ms * 1000.0 / n
     u = sum(U) / L
-    # weights of the distinct slots + ids/log2phy/x/w in + act, y out and back + out
-    bytes_per_launch = u * EXPERT_BYTES + B * H * 2 + B * K * (I + H) * 2 * 2 + B * H * 2
+    # weights of the distinct slots + x in + act out and back + out
+    bytes_per_launch = u * EXPERT_BYTES + B * H * 2 + B * K * I * 2 * 2 + B * H * 2
     return {
-        "kernel": "moe_decode_kernel",
+        "kernel": "lmoe_moe_decode = moe_decode_gateup_kernel + moe_decode_down_kernel",
         "avg_launch_us": round(avg_us, 3),
         "bytes_per_launch": int(bytes_per_launch),
         "distinct_slots_per_launch": round(u, 2),

@@ -34,12 +34,11 @@
  *                      and the single native combine of :3342-3379
  *   lmoe_fused_moe_decode  GMM1+swiglu+GMM2+unpermute of the decode
  *                      fused_experts call (patch_fused_moe.py:3946-4009)
- *   lmoe_router_decode gate + select_experts in one launch (moe_router_op.py:
- *                      191-278, the captured router piece of the decode seam)
  *   lmoe_moe_decode    remap + init-routing + GMM1 + swiglu + GMM2 + unpermute
- *                      of the decode fused_experts call in one launch
- *                      (slot_mapping.py:116-140, patch_fused_moe.py:668-701,
- *                      :3772-3774, :3363-3366, :3946-4009)
+ *                      of the decode fused_experts call, straight from the
+ *                      router output (slot_mapping.py:116-140,
+ *                      patch_fused_moe.py:668-701, :3772-3774, :3363-3366,
+ *                      :3946-4009)
  *   lmoe_stage_copy    TransferEngine.load_many_async H2D batch + ready event,
  *                      moe_offload/transfer_engine.py:139-187, 205-228
  */
@@ -76,9 +75,7 @@ enum {
   LMOE_META_PAIRS = 1,   /* number of pairs placed in the sorted order      */
   LMOE_META_ERRORS = 2,  /* pairs dropped because their id did not map      */
   LMOE_META_TILES = 3,   /* sum over slots of ceil(count / block_m)         */
-  LMOE_META_STALLS = 4,  /* bounded in-kernel waits that timed out (lmoe_moe_decode;
-                            accumulates, never reset by the library: 0 = healthy) */
-  LMOE_META_COUNT = 8
+  LMOE_META_COUNT = 4
 };
 
 const char* lmoe_status_string(int status);
@@ -106,17 +103,6 @@ int lmoe_router_topk(const void* logits, int logits_f32, int T, int E, int k,
                      int topk_group, int renorm, float routed_scale,
                      float* w_f32, uint16_t* w_bf16, int32_t* ids,
                      hipStream_t stream);
-
-/* lmoe_router_gate + lmoe_router_topk in one launch, for T <= 16 tokens
- * (same arguments and results; logits are written too).  sync is one int32
- * of device memory that must be zero before the first call; every call
- * leaves it zero (calls sharing it must not overlap).  H <= 8192. */
-int lmoe_router_decode(const void* x, const void* wg, int T, int H, int E,
-                       int k, int scoring, const float* bias, int n_group,
-                       int topk_group, int renorm, float routed_scale,
-                       void* logits, int logits_f32, float* w_f32,
-                       uint16_t* w_bf16, int32_t* ids, int32_t* sync,
-                       hipStream_t stream);
 
 /* Bytes of device workspace lmoe_permute needs for n_pairs pairs, n_slots. */
 size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);
@@ -202,10 +188,7 @@ int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                           const int32_t* meta, const void* add, void* act,
                           void* out, hipStream_t stream);
 
-/* Number of int32 words of the sync workspace lmoe_moe_decode needs. */
-size_t lmoe_moe_decode_sync_words(int n_pairs, int n_slots, int H, int I);
-
-/* Decode MoE layer body in one launch, straight from the router output:
+/* Decode MoE layer body from the router output (two launches on stream):
  *   slot(p) = log2phy ? log2phy[ids[p]] : ids[p]   (p = t*k + j)
  *   act[p]  = silu(W13_s[0:I] x_t) * (W13_s[I:2I] x_t)   bf16 (GMM1 bf16)
  *   y[p]    = W2_s act[p]                                 bf16
@@ -214,17 +197,15 @@ size_t lmoe_moe_decode_sync_words(int n_pairs, int n_slots, int H, int I);
  * A pair whose id is outside [0, n_log2phy) or whose slot is outside
  * [0, n_slots) contributes nothing and is counted in meta[LMOE_META_ERRORS];
  * meta[ACTIVE] = distinct slots, meta[PAIRS] = placed pairs.  act [T*k, I]
- * and y [T*k, H] are bf16 workspaces indexed by flat pair.  sync
- * (lmoe_moe_decode_sync_words int32) must be zero before the first call and
- * is left zero by every call; calls sharing sync must not overlap.
- * T*k <= 512, n_slots <= 8192, H % 8 == 0, I % 8 == 0, H <= 8192,
- * I <= 4096; x, weights, act and y 16-byte aligned. */
+ * is a bf16 workspace indexed by flat pair.  T*k <= 512, n_slots <= 8192,
+ * H % 8 == 0, I % 8 == 0, H <= 8192, I <= 4096; x, weights and act 16-byte
+ * aligned.  Replaces the decode fused_experts call
+ * (patch_fused_moe.py:3946-4009) including its remap and init-routing. */
 int lmoe_moe_decode(const void* x, int T, int H, int I, int k,
                     const int32_t* ids, const int32_t* log2phy, int n_log2phy,
                     const void* w13_slots, const void* w2_slots, int n_slots,
                     const uint16_t* w, const void* add, void* out, void* act,
-                    void* y, int32_t* sync, size_t sync_words, int32_t* meta,
-                    hipStream_t stream);
+                    int32_t* meta, hipStream_t stream);
 
 /* Batched host->device (or device->device) expert copies on a transfer
  * stream: optionally wait on wait_event, then for i < n copy bytes[i] from

@@ -171,18 +171,15 @@ def test_combine_masks_unplaced_pairs_and_adds_shared():
     assert rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref) <= 1e-2
 
 
-def _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None, sync=None, table_len=None):
+def _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None, table_len=None):
     T, H = d_x.shape
     k = d_ids.shape[1]
-    P, I = d_w13.shape[0], d_w13.shape[1] // 2
-    if sync is None:
-        sync = torch.zeros(native.moe_decode_sync_words(T * k, P, H, I), dtype=torch.int32, device="cuda")
+    I = d_w13.shape[1] // 2
     meta = torch.zeros(native.META_COUNT, dtype=torch.int32, device="cuda")
     act = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
-    y = torch.empty((T * k, H), dtype=torch.bfloat16, device="cuda")
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
-    native.moe_decode(d_x, d_w, d_ids, d_w13, d_w2, d_l2p, out, act, y, sync, meta, add=add, table_len=table_len)
-    return out, meta, sync
+    native.moe_decode(d_x, d_w, d_ids, d_w13, d_w2, d_l2p, out, act, meta, add=add, table_len=table_len)
+    return out, meta
 
 
 @pytest.mark.parametrize("T,k,E,P,H,I", [
@@ -202,13 +199,12 @@ def test_moe_decode_matches_oracle(T, k, E, P, H, I):
     ids, l2p, x, w13, w2, wb = _case(T * 31 + H + k, T, k, E, P, H, I)
     d = _dev(ids, l2p, x, w13, w2, wb)
     d_ids, d_l2p, d_x, d_w13, d_w2, d_w = d
-    out, meta, sync = _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
-    out2, meta2, _ = _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, sync=sync)
+    out, meta = _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
+    out2, _ = _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
     torch.cuda.synchronize()
     m = meta.cpu().tolist()
     assert m[native.META_ACTIVE] == np.unique(ids).size
-    assert m[native.META_PAIRS] == T * k and m[native.META_ERRORS] == 0 and m[native.META_STALLS] == 0
-    assert int(sync.abs().sum().item()) == 0, "counters must be back at zero"
+    assert m[native.META_PAIRS] == T * k and m[native.META_ERRORS] == 0
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
     ref = omlp.moe_layer(x, ids, wb, l2p, w13, w2)
     err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
@@ -227,7 +223,7 @@ def test_moe_decode_unmapped_pairs_add_term_and_identity_table():
     ids[0, 0] = E + 5                                   # outside the table
     add = normal_bf16(rng, (T, H), 0.5)
     d_ids, d_l2p, d_x, d_w13, d_w2, d_w = _dev(ids, l2p, x, w13, w2, wb)
-    out, meta, _ = _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, add=to_dev_bf16(add))
+    out, meta = _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, add=to_dev_bf16(add))
     torch.cuda.synchronize()
     ok = (ids >= 0) & (ids < E)
     ok[ok] &= l2p[ids[ok]] >= 0
@@ -241,13 +237,13 @@ def test_moe_decode_unmapped_pairs_add_term_and_identity_table():
     assert err <= OUT_TOL
     # every pair unmapped: out = add exactly
     none = np.full(E, -1, dtype=np.int32)
-    out0, meta0, _ = _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, to_dev_i32(none), add=to_dev_bf16(add))
+    out0, meta0 = _moe_decode(native, d_x, d_w, d_ids, d_w13, d_w2, to_dev_i32(none), add=to_dev_bf16(add))
     torch.cuda.synchronize()
     assert meta0[native.META_ACTIVE].item() == 0
     assert np.array_equal(from_dev_bf16(out0), add)
     # no table: ids are slots
     sid = np.stack([rng.permutation(P)[:k] for _ in range(T)]).astype(np.int32)
-    out1, _, _ = _moe_decode(native, d_x, d_w, to_dev_i32(sid), d_w13, d_w2, None)
+    out1, _ = _moe_decode(native, d_x, d_w, to_dev_i32(sid), d_w13, d_w2, None)
     torch.cuda.synchronize()
     ref1 = omlp.moe_layer(x, sid, wb, None, w13, w2)
     assert rel_max_err(bf16_to_f32(from_dev_bf16(out1)), ref1) <= OUT_TOL
@@ -255,7 +251,7 @@ def test_moe_decode_unmapped_pairs_add_term_and_identity_table():
 
 def test_moe_decode_graph_replays_with_changing_routes():
     """Captured once; routes and tables change between replays (eager work in
-    between), every replay matches the oracle and leaves the counters zero."""
+    between), every replay matches the oracle."""
     native = _native()
     rng = np.random.default_rng(4242)
     T, k, E, P, H, I = 4, 8, 128, 64, 2048, 768
@@ -266,14 +262,12 @@ def test_moe_decode_graph_replays_with_changing_routes():
     w = torch.zeros((T, k), dtype=torch.bfloat16, device="cuda")
     ids = torch.zeros((T, k), dtype=torch.int32, device="cuda")
     l2p = torch.full((E,), -1, dtype=torch.int32, device="cuda")
-    sync = torch.zeros(native.moe_decode_sync_words(T * k, P, H, I), dtype=torch.int32, device="cuda")
     meta = torch.zeros(native.META_COUNT, dtype=torch.int32, device="cuda")
     act = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
-    y = torch.empty((T * k, H), dtype=torch.bfloat16, device="cuda")
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
 
     def body():
-        native.moe_decode(x, w, ids, d_w13, d_w2, l2p, out, act, y, sync, meta)
+        native.moe_decode(x, w, ids, d_w13, d_w2, l2p, out, act, meta)
 
     def load(seed):
         r = np.random.default_rng(seed)
@@ -306,6 +300,6 @@ def test_moe_decode_graph_replays_with_changing_routes():
         err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
         print(f"  replay {rep}: rel max err {err:.3e}", flush=True)
         assert err <= OUT_TOL
-        assert int(sync.abs().sum().item()) == 0 and meta[native.META_STALLS].item() == 0
+        assert meta[native.META_ERRORS].item() == 0
         body()  # eager launch between replays
         torch.cuda.synchronize()

@@ -144,87 +144,3 @@ def test_gate_f32_output():
     native.router_gate(to_dev_bf16(x), to_dev_bf16(wg), logits)
     exact = orc.gate_logits(x, wg, out_f32=True)
     np.testing.assert_allclose(logits.cpu().numpy(), exact, rtol=1e-5, atol=1e-5)
-
-
-@pytest.mark.parametrize("T,H,E,k,scoring,G,TG", [
-    (1, 2048, 128, 8, "softmax", 1, 1),
-    (4, 2048, 128, 8, "softmax", 1, 1),
-    (16, 2048, 128, 8, "softmax", 1, 1),
-    (3, 1024, 60, 4, "softmax", 1, 1),
-    (1, 7168, 256, 8, "sigmoid", 8, 4),
-    (16, 7168, 256, 8, "sigmoid", 8, 4),
-    (5, 4096, 512, 16, "softmax", 1, 1),
-])
-def test_router_decode_equals_gate_plus_topk_and_oracle(T, H, E, k, scoring, G, TG):
-    """One-launch decode router: logits bit-identical to lmoe_router_gate,
-    selection bit-exact against the oracle on those logits; the counter is
-    left at zero so repeated calls agree."""
-    native = _native()
-    print(f"case router-decode T={T} H={H} E={E} k={k} {scoring}", flush=True)
-    rng = np.random.default_rng(31 + T + E)
-    x = normal_bf16(rng, (T, H), 1.0)
-    wg = normal_bf16(rng, (E, H), 0.02)
-    bias = (rng.standard_normal(E) * (0.01 if scoring == "sigmoid" else 0.5)).astype(np.float32)
-    dx, dwg, dbias = to_dev_bf16(x), to_dev_bf16(wg), torch.from_numpy(bias).cuda()
-    kw = dict(scoring=scoring, bias=dbias, num_expert_group=G, topk_group=TG,
-              routed_scaling_factor=2.5 if scoring == "sigmoid" else 1.0)
-    sync = torch.zeros(1, dtype=torch.int32, device="cuda")
-    w_f32 = torch.empty((T, k), dtype=torch.float32, device="cuda")
-    w, ids, logits = native.router_decode(dx, dwg, k, sync, w_f32=w_f32, **kw)
-    ref_logits = torch.empty((T, E), dtype=torch.bfloat16, device="cuda")
-    native.router_gate(dx, dwg, ref_logits)
-    w2_, ids2, _ = native.router_topk(ref_logits, k, **kw)
-    w3, ids3, _ = native.router_decode(dx, dwg, k, sync, **kw)
-    torch.cuda.synchronize()
-    assert int(sync.item()) == 0
-    assert torch.equal(logits.view(torch.int16), ref_logits.view(torch.int16))
-    lg32 = bf16_to_f32(from_dev_bf16(logits))
-    if scoring == "softmax":
-        r_ids, r_w, r_wb = orc.softmax_topk(lg32, k, bias=bias)
-    else:
-        r_ids, r_w, r_wb = orc.grouped_sigmoid_topk(lg32, k, bias=bias, n_group=G, topk_group=TG, scale=2.5)
-    np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
-    np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
-    np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
-    for a, b in ((ids2, ids), (ids3, ids)):
-        assert torch.equal(a, b)
-    for a, b in ((w2_, w), (w3, w)):
-        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
-
-
-def test_router_decode_graph_replays():
-    native = _native()
-    rng = np.random.default_rng(5150)
-    T, H, E, k = 4, 2048, 128, 8
-    wg = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
-    sync = torch.zeros(1, dtype=torch.int32, device="cuda")
-    x = torch.zeros((T, H), dtype=torch.bfloat16, device="cuda")
-    w = torch.empty((T, k), dtype=torch.bfloat16, device="cuda")
-    ids = torch.empty((T, k), dtype=torch.int32, device="cuda")
-    logits = torch.empty((T, E), dtype=torch.bfloat16, device="cuda")
-    x.copy_(to_dev_bf16(normal_bf16(rng, (T, H), 1.0)))
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        native.router_decode(x, wg, k, sync, logits=logits, w_bf16=w, ids=ids)
-    torch.cuda.current_stream().wait_stream(s)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        native.router_decode(x, wg, k, sync, logits=logits, w_bf16=w, ids=ids)
-    for rep in range(4):
-        xs = normal_bf16(rng, (T, H), 1.0)
-        x.copy_(to_dev_bf16(xs))
-        g.replay()
-        torch.cuda.synchronize()
-        got_lg = bf16_to_f32(from_dev_bf16(logits))
-        wgb = from_dev_bf16(wg)
-        exact = orc.gate_logits(xs, wgb)
-        absdot = np.abs(bf16_to_f32(xs)).astype(np.float64) @ np.abs(bf16_to_f32(wgb)).astype(np.float64).T
-        assert np.all(np.abs(got_lg - exact) <= bf16_ulp(exact) + 4.0 * np.sqrt(H) * 2.0 ** -24 * absdot)
-        ref_ids, _, ref_wb = orc.softmax_topk(got_lg, k)
-        np.testing.assert_array_equal(ids.cpu().numpy(), ref_ids)
-        np.testing.assert_array_equal(from_dev_bf16(w), ref_wb)
-        # eager work between replays
-        e_w, e_ids, _ = native.router_decode(x, wg, k, sync)
-        torch.cuda.synchronize()
-        assert torch.equal(e_ids, ids) and int(sync.item()) == 0

@@ -1,23 +1,18 @@
-// Decode MoE layer body in one launch: slot remap + grouping of the pairs by
-// slot, gate_up GEMV + SiLU*mul, down GEMV, weighted combine.
+// Decode MoE layer body straight from the router output, in two launches
+// with no cross-block synchronisation inside either:
+//   1. gate_up GEMV + SiLU*mul  -> act [T*k, I] (flat pair order)
+//   2. down GEMV + weighted combine -> out [T, H]
+// Both derive the slot grouping of the pairs themselves from ids + log2phy
+// (an LDS bitmap of the used slots ranked by popcount prefix: active slot a
+// is the a-th smallest used slot id; each slot's pairs in flat order), which
+// costs two dependent L2 reads per block and replaces a permutation launch.
+// Each expert's weights are read from HBM once per launch, however many of
+// the T tokens chose it.
 //
-// Work units are handed out in launch order by a device-scope ticket
-// counter: first every gate_up unit (slot-major: all units of the first
-// active slot, then the next ...), then every down unit.  A down unit loads
-// its W2 rows first, then waits until all gate_up units of its slot have
-// published their act rows.  Every unit it can wait for holds a smaller
-// ticket, so it is already resident and never waits itself: the launch
-// always drains.  The wait is also bounded (about a second); a timeout is
-// counted in meta[LMOE_META_STALLS] instead of spinning on.  The last down
-// unit of each output column tile (per-tile counter) combines the tokens of
-// that tile.  All counters are returned to zero by the launch itself (the
-// last unit to finish resets the shared ones), so the workspace needs to be
-// zeroed once, at allocation, and never again: graph replays need no memset.
-//
-// Every block derives the slot grouping itself from ids + log2phy (an LDS
-// bitmap of the slots, ranked by popcount prefix, so active slot a is the
-// a-th smallest slot id, and each slot's pairs in flat order), which costs
-// two dependent L2 reads and replaces a separate permutation launch.
+// (Cross-block hand-off inside one launch would need agent-scope release /
+// acquire fences; on this part they write back / invalidate a whole XCD L2
+// each and cost far more than a kernel boundary, which in a captured graph
+// is back to back.)
 //
 // Rounding points follow the reference: gate and up leave GMM1 as bf16, the
 // SwiGLU output is bf16, y = GMM2 output is bf16, the combine accumulates in
@@ -35,7 +30,7 @@ namespace lmoe {
 constexpr int kDecMaxPairs = 512;
 constexpr int kDecMaxSlots = 8192;
 constexpr int kDecWords = kDecMaxSlots / 32;
-constexpr int kDecSpinLimit = 1 << 22;  // x s_sleep(8) ~ 2e9 cycles
+constexpr int kDnMaxRows = 4;  // output rows per down block (at most)
 
 struct DecodeArgs {
   const uint16_t* x;
@@ -50,19 +45,13 @@ struct DecodeArgs {
   const uint16_t* add;
   uint16_t* out;
   uint16_t* act;  // [N, I] by flat pair
-  uint16_t* y;    // [N, H] by flat pair
-  int32_t* sync;  // [2 + max_active + dn_per_slot], zero between launches
   int32_t* meta;
-  int max_active;
-  int gu_per_slot;
-  int dn_per_slot;
 };
 
 // Sum V values per lane over the lanes that differ in bits LO..HI of the lane
 // id, leaving ONE total per lane: the first log2(V) steps exchange halves of
 // the value set (a reduce-scatter), the rest are plain butterfly adds.  On
-// return, the lane holds value index
-//   sum_{b < log2 V} ((lane >> (HI - b)) & 1) << (log2 V - 1 - b).
+// return, the lane holds value index scatter_index<HI, LO, log2 V>(lane).
 template <int V, int HI, int LO>
 __device__ __forceinline__ float reduce_scatter(float (&v)[V], int lane) {
   constexpr int L = (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
@@ -102,42 +91,30 @@ __device__ __forceinline__ uint4 load_stream16(const uint16_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-__device__ __forceinline__ void release_agent() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-}
-__device__ __forceinline__ void acquire_agent() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-}
+// Slot grouping of the pairs: s_slot[p] = slot of pair p (-1 if it does not
+// map), s_bits = bitmap of the used slots, s_wpre = exclusive popcount prefix
+// per 32-slot word.
+struct Grouping {
+  int s_slot[kDecMaxPairs];
+  uint32_t s_bits[kDecWords];
+  int s_wpre[kDecWords];
+  int s_scan[8];
+  int na, err, placed;
+};
 
-// GNC: 512-column chunks of an H row (gate_up); GR: row pairs per wave.
-// DNC: 256-column chunks of an I row (down, one row per half wave);
-// DS: row steps per wave (2 rows per step).
-template <int GNC, int GR, int DNC, int DS>
-__global__ __launch_bounds__(256) void moe_decode_kernel(DecodeArgs a) {
-  __shared__ int s_slot[kDecMaxPairs];
-  __shared__ uint32_t s_bits[kDecWords];
-  __shared__ int s_wpre[kDecWords];
-  __shared__ int s_list[kDecMaxPairs];
-  __shared__ int s_scan[8];
-  __shared__ int s_ticket, s_na, s_err, s_placed, s_myslot, s_n, s_last;
-
+// Every thread of a 256-thread block calls it.
+__device__ void build_grouping(const DecodeArgs& a, Grouping& g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int N = a.T * a.k;
-  const int I = a.I;
-  const int H = a.H;
-
-  if (tid == 0) {
-    s_ticket = __hip_atomic_fetch_add(&a.sync[0], 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-    s_err = 0;
-    s_placed = 0;
-  }
   const int nwords = (a.P + 31) >> 5;
-  for (int w = tid; w < nwords; w += 256) s_bits[w] = 0u;
+  if (tid == 0) {
+    g.err = 0;
+    g.placed = 0;
+  }
+  for (int w = tid; w < nwords; w += 256) g.s_bits[w] = 0u;
   __syncthreads();
-  // ---- slot of every pair, slot bitmap
   int err = 0, placed = 0;
   for (int p = tid; p < N; p += 256) {
     const int id = a.ids[p];
@@ -148,322 +125,336 @@ __global__ __launch_bounds__(256) void moe_decode_kernel(DecodeArgs a) {
       s = id;
     }
     if (s >= 0 && s < a.P) {
-      atomicOr(&s_bits[s >> 5], 1u << (s & 31));
+      atomicOr(&g.s_bits[s >> 5], 1u << (s & 31));
       ++placed;
     } else {
       s = -1;
       ++err;
     }
-    s_slot[p] = s;
+    g.s_slot[p] = s;
   }
-  if (err) atomicAdd(&s_err, err);
-  if (placed) atomicAdd(&s_placed, placed);
+  if (err) atomicAdd(&g.err, err);
+  if (placed) atomicAdd(&g.placed, placed);
   __syncthreads();
-  // ---- exclusive prefix of the word popcounts (nwords <= 256 threads)
-  {
-    const int c = tid < nwords ? __popc(s_bits[tid]) : 0;
-    int inc = c;
+  // exclusive prefix of the word popcounts (nwords <= 256 threads)
+  const int c = tid < nwords ? __popc(g.s_bits[tid]) : 0;
+  int inc = c;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_up(inc, o, kWave);
-      if (lane >= o) inc += t;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) g.s_scan[wave] = inc;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += g.s_scan[w];
+  if (tid < nwords) g.s_wpre[tid] = base + inc - c;
+  if (tid == 255) g.na = base + inc;
+  __syncthreads();
+}
+
+// slot id of active rank r (r < g.na)
+__device__ __forceinline__ int slot_of_rank(const Grouping& g, int nwords, int r) {
+  int lo = 0, hi = nwords - 1;  // largest w with s_wpre[w] <= r
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (g.s_wpre[mid] <= r) lo = mid; else hi = mid - 1;
+  }
+  uint32_t bits = g.s_bits[lo];
+  for (int q = r - g.s_wpre[lo]; q > 0; --q) bits &= bits - 1u;
+  return lo * 32 + (__ffs(bits) - 1);
+}
+
+// ---------------------------------------------------------------------------
+// gate_up + SiLU*mul.  grid (gu_units, max_active): block (sub, a) owns rows
+// i = (4*sub + wave)*GR .. +GR of the a-th active slot; the weight rows stay
+// in registers while that slot's tokens stream past, 4 at a time.
+// GNC: 512-column chunks of an H row; GR: row pairs per wave.
+// ---------------------------------------------------------------------------
+template <int GNC, int GR>
+__global__ __launch_bounds__(256) void moe_decode_gateup_kernel(DecodeArgs a) {
+  __shared__ Grouping g;
+  __shared__ int s_list[kDecMaxPairs];
+  __shared__ int s_n, s_myslot;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int N = a.T * a.k;
+  const int I = a.I;
+  const int H = a.H;
+  const int nwords = (a.P + 31) >> 5;
+  build_grouping(a, g);
+  const int slot_rank = blockIdx.y;
+  if (blockIdx.x == 0 && slot_rank == 0 && tid == 0) {
+    a.meta[LMOE_META_ACTIVE] = g.na;
+    a.meta[LMOE_META_PAIRS] = g.placed;
+    a.meta[LMOE_META_ERRORS] = g.err;
+  }
+  if (slot_rank >= g.na) return;
+  if (tid == 0) s_myslot = slot_of_rank(g, nwords, slot_rank);
+  __syncthreads();
+  const int myslot = s_myslot;
+  if (wave == 0) {
+    int cnt = 0;
+    for (int base = 0; base < N; base += 64) {
+      const int p = base + lane;
+      const bool m = p < N && g.s_slot[p] == myslot;
+      const uint64_t bm = __ballot(m);
+      if (m) s_list[cnt + __popcll(bm & lanemask_lt(lane))] = p;
+      cnt += __popcll(bm);
     }
-    if (lane == 63) s_scan[wave] = inc;
-    __syncthreads();
-    int base = 0;
-    for (int w = 0; w < wave; ++w) base += s_scan[w];
-    if (tid < nwords) s_wpre[tid] = base + inc - c;
-    if (tid == 255) s_na = base + inc;
+    if (lane == 0) s_n = cnt;
   }
   __syncthreads();
-  const int na = s_na;
-  const int ticket = s_ticket;
-  const int n_gu = a.max_active * a.gu_per_slot;
-  const bool is_gu = ticket < n_gu;
-  const int u = is_gu ? ticket : ticket - n_gu;
-  const int slot_rank = is_gu ? u / a.gu_per_slot : u / a.dn_per_slot;
-  const int sub = is_gu ? u % a.gu_per_slot : u % a.dn_per_slot;
-  const bool has_work = slot_rank < na;
+  const int n = s_n;
 
-  if (ticket == 0) {
-    if (tid == 0) {
-      a.meta[LMOE_META_ACTIVE] = na;
-      a.meta[LMOE_META_PAIRS] = s_placed;
-      a.meta[LMOE_META_ERRORS] = s_err;
+  const int i0 = (blockIdx.x * 4 + wave) * GR;
+  const uint16_t* base13 = a.w13 + static_cast<size_t>(myslot) * 2 * I * H;
+  uint4 wg[GR][GNC], wu[GR][GNC];
+#pragma unroll
+  for (int r = 0; r < GR; ++r) {
+    const int i = i0 + r;
+#pragma unroll
+    for (int c = 0; c < GNC; ++c) {
+      const int h = c * 512 + lane * 8;
+      if (i < I && h < H) {
+        wg[r][c] = load_stream16(base13 + static_cast<size_t>(i) * H + h);
+        wu[r][c] = load_stream16(base13 + static_cast<size_t>(I + i) * H + h);
+      } else {
+        wg[r][c] = make_uint4(0u, 0u, 0u, 0u);
+        wu[r][c] = make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   }
-  if (has_work) {
-    // ---- the slot of rank slot_rank and its pairs in flat order
-    if (tid == 0) {
-      int lo = 0, hi = nwords - 1;  // largest w with s_wpre[w] <= slot_rank
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_wpre[mid] <= slot_rank) lo = mid; else hi = mid - 1;
-      }
-      uint32_t bits = s_bits[lo];
-      for (int r = slot_rank - s_wpre[lo]; r > 0; --r) bits &= bits - 1u;
-      s_myslot = lo * 32 + (__ffs(bits) - 1);
-    }
-    __syncthreads();
-    const int myslot = s_myslot;
-    if (wave == 0) {
-      int cnt = 0;
-      for (int base = 0; base < N; base += 64) {
-        const int p = base + lane;
-        const bool m = p < N && s_slot[p] == myslot;
-        const uint64_t bm = __ballot(m);
-        if (m) s_list[cnt + __popcll(bm & lanemask_lt(lane))] = p;
-        cnt += __popcll(bm);
-      }
-      if (lane == 0) s_n = cnt;
-    }
-    __syncthreads();
-    const int n = s_n;
-
-    if (is_gu) {
-      // ================= gate_up rows i0 .. i0+GR-1 of slot myslot
-      const int i0 = (sub * 4 + wave) * GR;
-      const uint16_t* base13 = a.w13 + static_cast<size_t>(myslot) * 2 * I * H;
-      uint4 wg[GR][GNC], wu[GR][GNC];
+  constexpr int V = 2 * GR * 4;
+  constexpr int LV = (V >= 16) ? 4 : (V >= 8) ? 3 : 2;
+  for (int q0 = 0; q0 < n; q0 += 4) {
+    float v[V];
 #pragma unroll
-      for (int r = 0; r < GR; ++r) {
-        const int i = i0 + r;
+    for (int z = 0; z < V; ++z) v[z] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q0 + q < n) {
+        const int t = s_list[q0 + q] / a.k;
+        const uint16_t* xr = a.x + static_cast<size_t>(t) * H;
 #pragma unroll
         for (int c = 0; c < GNC; ++c) {
           const int h = c * 512 + lane * 8;
-          if (i < I && h < H) {
-            wg[r][c] = load_stream16(base13 + static_cast<size_t>(i) * H + h);
-            wu[r][c] = load_stream16(base13 + static_cast<size_t>(I + i) * H + h);
-          } else {
-            wg[r][c] = make_uint4(0u, 0u, 0u, 0u);
-            wu[r][c] = make_uint4(0u, 0u, 0u, 0u);
-          }
-        }
-      }
-      constexpr int V = 2 * GR * 4;
-      constexpr int LV = (V >= 16) ? 4 : (V >= 8) ? 3 : 2;
-      for (int q0 = 0; q0 < n; q0 += 4) {
-        float v[V];
+          if (h < H) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(xr + h);
 #pragma unroll
-        for (int z = 0; z < V; ++z) v[z] = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (q0 + q < n) {
-            const int t = s_list[q0 + q] / a.k;
-            const uint16_t* xr = a.x + static_cast<size_t>(t) * H;
-#pragma unroll
-            for (int c = 0; c < GNC; ++c) {
-              const int h = c * 512 + lane * 8;
-              if (h < H) {
-                const uint4 xv = *reinterpret_cast<const uint4*>(xr + h);
-#pragma unroll
-                for (int r = 0; r < GR; ++r) {
-                  v[r * 4 + q] = dot8(xv, wg[r][c], v[r * 4 + q]);
-                  v[GR * 4 + r * 4 + q] = dot8(xv, wu[r][c], v[GR * 4 + r * 4 + q]);
-                }
-              }
+            for (int r = 0; r < GR; ++r) {
+              v[r * 4 + q] = dot8(xv, wg[r][c], v[r * 4 + q]);
+              v[GR * 4 + r * 4 + q] = dot8(xv, wu[r][c], v[GR * 4 + r * 4 + q]);
             }
           }
         }
-        // value index z = which * (4 GR) + r * 4 + q; after the reduction
-        // lane l holds z = scatter_index(l), "which" is lane bit 5
-        const float tot = reduce_scatter<V, 5, 0>(v, lane);
-        const float other = __shfl_xor(tot, 32, kWave);
-        const int z = scatter_index<5, 0, LV>(lane);
-        const int low_bits = 6 - LV;
-        if ((lane & 32) == 0 && (lane & ((1 << low_bits) - 1)) == 0) {
-          const int r = (z >> 2) % GR;
-          const int q = z & 3;
-          const int i = i0 + r;
-          if (q0 + q < n && i < I) {
-            const int p = s_list[q0 + q];
-            a.act[static_cast<size_t>(p) * I + i] = swiglu_bf16(tot, other);
-          }
-        }
       }
-      release_agent();
-      __syncthreads();
-      if (tid == 0)
-        __hip_atomic_fetch_add(&a.sync[2 + slot_rank], 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      // ================= down rows of tile sub, slot myslot
-      const int half = lane >> 5;
-      const int l5 = lane & 31;
-      const int rows_per_unit = 4 * 2 * DS;
-      const int hbase = sub * rows_per_unit + wave * 2 * DS;
-      const uint16_t* base2 = a.w2 + static_cast<size_t>(myslot) * H * I;
-      uint4 wv[DS][DNC];
+    }
+    // value index z = which * (4 GR) + r * 4 + q; after the reduction lane l
+    // holds z = scatter_index(l): "which" (gate 0 / up 1) is lane bit 5
+    const float tot = reduce_scatter<V, 5, 0>(v, lane);
+    const float other = __shfl_xor(tot, 32, kWave);
+    const int z = scatter_index<5, 0, LV>(lane);
+    constexpr int kLow = 6 - LV;
+    if ((lane & 32) == 0 && (lane & ((1 << kLow) - 1)) == 0) {
+      const int r = (z >> 2) % GR;
+      const int q = z & 3;
+      const int i = i0 + r;
+      if (q0 + q < n && i < I) {
+        const int p = s_list[q0 + q];
+        a.act[static_cast<size_t>(p) * I + i] = swiglu_bf16(tot, other);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// down + weighted combine.  grid ceil(H / R): block b owns output rows
+// h0 = R*b .. R*b+R-1 for EVERY active slot, so its combine needs nothing
+// from other blocks.  Half wave hw (8 per block) takes the active slots
+// a = hw, hw + 8, ...: it holds the slot's R W2 rows (DNC 16-byte chunks per
+// lane and row), with PF also loading the next slot's while it computes,
+// streams the slot's act rows from L2 and leaves y[p][h] (bf16 values) in
+// LDS; then the block combines its R columns of every token in j order.
+// ---------------------------------------------------------------------------
+template <int DNC, int R, bool PF>
+__global__ __launch_bounds__(256) void moe_decode_down_kernel(DecodeArgs a) {
+  constexpr int kDnRows = R;
+  constexpr int V = 4 * R;
+  constexpr int LV = (V >= 16) ? 4 : (V >= 8) ? 3 : 2;
+  __shared__ Grouping g;
+  __shared__ float s_y[kDecMaxPairs * kDnMaxRows];
+  __shared__ int s_list[8][kDecMaxPairs];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int half = lane >> 5;
+  const int l5 = lane & 31;
+  const int hw = wave * 2 + half;
+  const int N = a.T * a.k;
+  const int I = a.I;
+  const int H = a.H;
+  const int nwords = (a.P + 31) >> 5;
+  build_grouping(a, g);
+  const int na = g.na;
+  const int h0 = blockIdx.x * kDnRows;
+
+  uint4 wcur[kDnRows][DNC], wnxt[PF ? kDnRows : 1][PF ? DNC : 1];
+  int rank = hw;
+  int s_cur = rank < na ? slot_of_rank(g, nwords, rank) : -1;
+  if (s_cur >= 0) {
+    const uint16_t* base2 = a.w2 + static_cast<size_t>(s_cur) * H * I;
 #pragma unroll
-      for (int st = 0; st < DS; ++st) {
-        const int h = hbase + st * 2 + half;
+    for (int r = 0; r < kDnRows; ++r) {
+      const int h = h0 + r;
+#pragma unroll
+      for (int c = 0; c < DNC; ++c) {
+        const int col = c * 256 + l5 * 8;
+        wcur[r][c] = (h < H && col < I) ? load_stream16(base2 + static_cast<size_t>(h) * I + col)
+                                        : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
+  // both halves of a wave run the loop together (ballots), each on its own
+  // slot sequence; a half with no slot left idles until the other finishes
+  while (__ballot(s_cur >= 0) != 0ull) {
+    const int nrank = rank + 8;
+    const int s_nxt = (s_cur >= 0 && nrank < na) ? slot_of_rank(g, nwords, nrank) : -1;
+    if (PF && s_nxt >= 0) {
+      const uint16_t* base2 = a.w2 + static_cast<size_t>(s_nxt) * H * I;
+#pragma unroll
+      for (int r = 0; r < kDnRows; ++r) {
+        const int h = h0 + r;
 #pragma unroll
         for (int c = 0; c < DNC; ++c) {
           const int col = c * 256 + l5 * 8;
-          wv[st][c] = (h < H && col < I)
-                          ? load_stream16(base2 + static_cast<size_t>(h) * I + col)
-                          : make_uint4(0u, 0u, 0u, 0u);
+          wnxt[PF ? r : 0][PF ? c : 0] =
+              (h < H && col < I) ? load_stream16(base2 + static_cast<size_t>(h) * I + col)
+                                 : make_uint4(0u, 0u, 0u, 0u);
         }
       }
-      // wait for the act rows of this slot
-      if (tid == 0) {
-        int spins = 0;
-        while (__hip_atomic_load(&a.sync[2 + slot_rank], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT) < a.gu_per_slot) {
-          __builtin_amdgcn_s_sleep(8);
-          if (++spins > kDecSpinLimit) {
-            atomicAdd(&a.meta[LMOE_META_STALLS], 1);
-            break;
-          }
-        }
-      }
-      __syncthreads();
-      acquire_agent();
-      constexpr int V = 4 * DS;
-      constexpr int LV = (V >= 16) ? 4 : (V >= 8) ? 3 : 2;
-      for (int q0 = 0; q0 < n; q0 += 4) {
-        float v[V];
+    }
+    // pairs of s_cur in flat order (per half wave)
+    int* list = s_list[hw];
+    int n = 0;
+    for (int base = 0; base < N; base += 32) {
+      const int p = base + l5;
+      const bool m = s_cur >= 0 && p < N && g.s_slot[p] == s_cur;
+      const uint64_t bm = __ballot(m);
+      const uint32_t mine = static_cast<uint32_t>(half ? (bm >> 32) : bm);
+      if (m) list[n + __popc(mine & ((1u << l5) - 1u))] = p;
+      n += __popc(mine);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int n_other = __shfl_xor(n, 32, kWave);
+    const int n_max = n > n_other ? n : n_other;
+    for (int q0 = 0; q0 < n_max; q0 += 4) {
+      float v[V];
 #pragma unroll
-        for (int z = 0; z < V; ++z) v[z] = 0.0f;
+      for (int z = 0; z < V; ++z) v[z] = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (q0 + q < n) {
-            const uint16_t* ar = a.act + static_cast<size_t>(s_list[q0 + q]) * I;
+      for (int q = 0; q < 4; ++q) {
+        if (q0 + q < n) {
+          const uint16_t* ar = a.act + static_cast<size_t>(list[q0 + q]) * I;
 #pragma unroll
-            for (int c = 0; c < DNC; ++c) {
-              const int col = c * 256 + l5 * 8;
-              if (col < I) {
-                const uint4 av = *reinterpret_cast<const uint4*>(ar + col);
+          for (int c = 0; c < DNC; ++c) {
+            const int col = c * 256 + l5 * 8;
+            if (col < I) {
+              const uint4 av = *reinterpret_cast<const uint4*>(ar + col);
 #pragma unroll
-                for (int st = 0; st < DS; ++st) v[st * 4 + q] = dot8(av, wv[st][c], v[st * 4 + q]);
-              }
+              for (int r = 0; r < kDnRows; ++r) v[r * 4 + q] = dot8(av, wcur[r][c], v[r * 4 + q]);
             }
           }
         }
-        const float tot = reduce_scatter<V, 4, 0>(v, lane);
-        const int z = scatter_index<4, 0, LV>(lane);
-        const int low_bits = 5 - LV;
-        if ((l5 & ((1 << low_bits) - 1)) == 0) {
-          const int st = z >> 2;
-          const int q = z & 3;
-          const int h = hbase + st * 2 + half;
-          if (q0 + q < n && h < H) {
-            const int p = s_list[q0 + q];
-            a.y[static_cast<size_t>(p) * H + h] =
-                static_cast<uint16_t>(f32_to_bf16_bits(tot));
-          }
+      }
+      // reduce over the 32 lanes of each half wave: lane holds z = r*4 + q
+      const float tot = reduce_scatter<V, 4, 0>(v, lane);
+      const int z = scatter_index<4, 0, LV>(lane);
+      if ((l5 & ((1 << (5 - LV)) - 1)) == 0) {
+        const int r = z >> 2;
+        const int q = z & 3;
+        if (q0 + q < n) s_y[list[q0 + q] * kDnRows + r] = round_bf16(tot);  // GMM2 output is bf16
+      }
+    }
+    rank = nrank;
+    s_cur = s_nxt;
+    if (PF) {
+#pragma unroll
+      for (int r = 0; r < kDnRows; ++r)
+#pragma unroll
+        for (int c = 0; c < DNC; ++c) wcur[r][c] = wnxt[PF ? r : 0][PF ? c : 0];
+    } else if (s_cur >= 0) {
+      const uint16_t* base2 = a.w2 + static_cast<size_t>(s_cur) * H * I;
+#pragma unroll
+      for (int r = 0; r < kDnRows; ++r) {
+        const int h = h0 + r;
+#pragma unroll
+        for (int c = 0; c < DNC; ++c) {
+          const int col = c * 256 + l5 * 8;
+          wcur[r][c] = (h < H && col < I) ? load_stream16(base2 + static_cast<size_t>(h) * I + col)
+                                          : make_uint4(0u, 0u, 0u, 0u);
         }
       }
     }
   }
-
-  // ---- combine: the last down unit of each column tile
-  if (!is_gu && slot_rank < (na > 0 ? na : 1)) {
-    release_agent();
-    __syncthreads();
-    if (tid == 0) {
-      const int expect = na > 0 ? na : 1;
-      const int done = __hip_atomic_fetch_add(&a.sync[2 + a.max_active + sub], 1,
-                                              __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = done == expect - 1;
-    }
-    __syncthreads();
-    if (s_last) {
-      acquire_agent();
-      const int R = 4 * 2 * DS;
-      const int h0 = sub * R;
-      for (int qq = tid; qq < a.T * R; qq += 256) {
-        const int t = qq / R;
-        const int h = h0 + qq % R;
-        if (h >= H) continue;
-        float acc = 0.0f;
-        for (int j = 0; j < a.k; ++j) {
-          const int p = t * a.k + j;
-          if (s_slot[p] >= 0)
-            acc += bf16_to_f32(a.wts[p]) * bf16_to_f32(a.y[static_cast<size_t>(p) * H + h]);
-        }
-        if (a.add != nullptr) acc += bf16_to_f32(a.add[static_cast<size_t>(t) * H + h]);
-        a.out[static_cast<size_t>(t) * H + h] = static_cast<uint16_t>(f32_to_bf16_bits(acc));
-      }
-      if (tid == 0)
-        __hip_atomic_store(&a.sync[2 + a.max_active + sub], 0, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-
-  // ---- the last unit to finish returns the shared counters to zero
   __syncthreads();
-  if (tid == 0) {
-    const int fin = __hip_atomic_fetch_add(&a.sync[1], 1, __ATOMIC_ACQ_REL,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-    if (fin == static_cast<int>(gridDim.x) - 1) {
-      for (int i = 0; i < a.max_active; ++i)
-        __hip_atomic_store(&a.sync[2 + i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&a.sync[0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&a.sync[1], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int qq = tid; qq < a.T * kDnRows; qq += 256) {
+    const int t = qq / kDnRows;
+    const int r = qq % kDnRows;
+    const int h = h0 + r;
+    if (h >= H) continue;
+    float acc = 0.0f;
+    for (int j = 0; j < a.k; ++j) {
+      const int p = t * a.k + j;
+      if (g.s_slot[p] >= 0) acc += bf16_to_f32(a.wts[p]) * s_y[p * kDnRows + r];
     }
+    if (a.add != nullptr) acc += bf16_to_f32(a.add[static_cast<size_t>(t) * H + h]);
+    a.out[static_cast<size_t>(t) * H + h] = static_cast<uint16_t>(f32_to_bf16_bits(acc));
   }
-}
-
-struct DecodeShape {
-  int gnc, gr, dnc, ds;
-};
-
-static DecodeShape pick_shape(int H, int I) {
-  DecodeShape s{};
-  const int g = (H + 511) / 512;
-  s.gnc = g <= 4 ? 4 : g <= 8 ? 8 : g <= 14 ? 14 : 16;
-  s.gr = s.gnc <= 4 ? 2 : 1;
-  const int d = (I + 255) / 256;
-  s.dnc = d <= 3 ? 3 : d <= 4 ? 4 : d <= 8 ? 8 : 16;
-  s.ds = s.dnc <= 4 ? 4 : s.dnc <= 8 ? 2 : 1;
-  return s;
-}
-
-static int decode_units(const DecodeShape& s, int H, int I, int* gu, int* dn) {
-  *gu = (I + 4 * s.gr - 1) / (4 * s.gr);
-  *dn = (H + 8 * s.ds - 1) / (8 * s.ds);
-  return 0;
 }
 
 }  // namespace lmoe
 
 using namespace lmoe;
 
-extern "C" size_t lmoe_moe_decode_sync_words(int n_pairs, int n_slots, int H, int I) {
-  if (n_pairs <= 0 || n_slots <= 0 || H <= 0 || I <= 0) return 0;
-  const DecodeShape s = pick_shape(H, I);
-  int gu, dn;
-  decode_units(s, H, I, &gu, &dn);
-  const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
-  return static_cast<size_t>(2 + max_active + dn);
+namespace {
+
+struct DecodeShape {
+  int gnc, gr, dnc;
+};
+
+DecodeShape pick_shape(int H, int I) {
+  DecodeShape s{};
+  const int g = (H + 511) / 512;
+  s.gnc = g <= 4 ? 4 : g <= 8 ? 8 : g <= 14 ? 14 : 16;
+  s.gr = s.gnc <= 4 ? 2 : 1;
+  const int d = (I + 255) / 256;
+  s.dnc = d <= 3 ? 3 : d <= 4 ? 4 : d <= 8 ? 8 : 16;
+  return s;
 }
 
-#define LMOE_DECODE_LAUNCH(G, GR_, D, DS_)                                      \
-  hipLaunchKernelGGL((moe_decode_kernel<G, GR_, D, DS_>), grid, dim3(256), 0,   \
-                     stream, args)
+}  // namespace
 
 extern "C" int lmoe_moe_decode(const void* x, int T, int H, int I, int k,
                                const int32_t* ids, const int32_t* log2phy,
                                int n_log2phy, const void* w13_slots,
                                const void* w2_slots, int n_slots,
                                const uint16_t* w, const void* add, void* out,
-                               void* act, void* y, int32_t* sync,
-                               size_t sync_words, int32_t* meta,
-                               hipStream_t stream) {
+                               void* act, int32_t* meta, hipStream_t stream) {
   if (x == nullptr || ids == nullptr || w13_slots == nullptr ||
       w2_slots == nullptr || w == nullptr || out == nullptr || act == nullptr ||
-      y == nullptr || sync == nullptr || meta == nullptr)
+      meta == nullptr)
     return LMOE_ERR_ARG;
   if (T <= 0 || H <= 0 || I <= 0 || k <= 0 || n_slots <= 0) return LMOE_ERR_ARG;
   if (log2phy != nullptr && n_log2phy <= 0) return LMOE_ERR_ARG;
   const int N = T * k;
   if (N > kDecMaxPairs || n_slots > kDecMaxSlots) return LMOE_ERR_SHAPE;
   if (H % 8 != 0 || I % 8 != 0 || H > 16 * 512 || I > 16 * 256) return LMOE_ERR_SHAPE;
-  if (sync_words < lmoe_moe_decode_sync_words(N, n_slots, H, I)) return LMOE_ERR_WORKSPACE;
   const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w13_slots) |
-                          reinterpret_cast<uintptr_t>(w2_slots) | reinterpret_cast<uintptr_t>(act) |
-                          reinterpret_cast<uintptr_t>(y);
+                          reinterpret_cast<uintptr_t>(w2_slots) | reinterpret_cast<uintptr_t>(act);
   if (align & 15u) return LMOE_ERR_SHAPE;
   const DecodeShape s = pick_shape(H, I);
   DecodeArgs args{};
@@ -482,27 +473,28 @@ extern "C" int lmoe_moe_decode(const void* x, int T, int H, int I, int k,
   args.add = static_cast<const uint16_t*>(add);
   args.out = static_cast<uint16_t*>(out);
   args.act = static_cast<uint16_t*>(act);
-  args.y = static_cast<uint16_t*>(y);
-  args.sync = sync;
   args.meta = meta;
-  args.max_active = N < n_slots ? N : n_slots;
-  decode_units(s, H, I, &args.gu_per_slot, &args.dn_per_slot);
-  const dim3 grid(args.max_active * (args.gu_per_slot + args.dn_per_slot));
-  if (s.gnc == 4 && s.dnc == 3) LMOE_DECODE_LAUNCH(4, 2, 3, 4);
-  else if (s.gnc == 4 && s.dnc == 4) LMOE_DECODE_LAUNCH(4, 2, 4, 4);
-  else if (s.gnc == 4 && s.dnc == 8) LMOE_DECODE_LAUNCH(4, 2, 8, 2);
-  else if (s.gnc == 4) LMOE_DECODE_LAUNCH(4, 2, 16, 1);
-  else if (s.gnc == 8 && s.dnc == 3) LMOE_DECODE_LAUNCH(8, 1, 3, 4);
-  else if (s.gnc == 8 && s.dnc == 4) LMOE_DECODE_LAUNCH(8, 1, 4, 4);
-  else if (s.gnc == 8 && s.dnc == 8) LMOE_DECODE_LAUNCH(8, 1, 8, 2);
-  else if (s.gnc == 8) LMOE_DECODE_LAUNCH(8, 1, 16, 1);
-  else if (s.gnc == 14 && s.dnc == 3) LMOE_DECODE_LAUNCH(14, 1, 3, 4);
-  else if (s.gnc == 14 && s.dnc == 4) LMOE_DECODE_LAUNCH(14, 1, 4, 4);
-  else if (s.gnc == 14 && s.dnc == 8) LMOE_DECODE_LAUNCH(14, 1, 8, 2);
-  else if (s.gnc == 14) LMOE_DECODE_LAUNCH(14, 1, 16, 1);
-  else if (s.dnc == 3) LMOE_DECODE_LAUNCH(16, 1, 3, 4);
-  else if (s.dnc == 4) LMOE_DECODE_LAUNCH(16, 1, 4, 4);
-  else if (s.dnc == 8) LMOE_DECODE_LAUNCH(16, 1, 8, 2);
-  else LMOE_DECODE_LAUNCH(16, 1, 16, 1);
+  const int max_active = N < n_slots ? N : n_slots;
+  const dim3 gu_grid((I + 4 * s.gr - 1) / (4 * s.gr), max_active);
+  switch (s.gnc) {
+    case 4: hipLaunchKernelGGL((moe_decode_gateup_kernel<4, 2>), gu_grid, dim3(256), 0, stream, args); break;
+    case 8: hipLaunchKernelGGL((moe_decode_gateup_kernel<8, 1>), gu_grid, dim3(256), 0, stream, args); break;
+    case 14: hipLaunchKernelGGL((moe_decode_gateup_kernel<14, 1>), gu_grid, dim3(256), 0, stream, args); break;
+    default: hipLaunchKernelGGL((moe_decode_gateup_kernel<16, 1>), gu_grid, dim3(256), 0, stream, args); break;
+  }
+  switch (s.dnc) {
+    case 3:
+      hipLaunchKernelGGL((moe_decode_down_kernel<3, 4, true>), dim3((H + 3) / 4), dim3(256), 0, stream, args);
+      break;
+    case 4:
+      hipLaunchKernelGGL((moe_decode_down_kernel<4, 4, true>), dim3((H + 3) / 4), dim3(256), 0, stream, args);
+      break;
+    case 8:
+      hipLaunchKernelGGL((moe_decode_down_kernel<8, 4, false>), dim3((H + 3) / 4), dim3(256), 0, stream, args);
+      break;
+    default:
+      hipLaunchKernelGGL((moe_decode_down_kernel<16, 2, false>), dim3((H + 1) / 2), dim3(256), 0, stream, args);
+      break;
+  }
   LMOE_RETURN_LAUNCH();
 }

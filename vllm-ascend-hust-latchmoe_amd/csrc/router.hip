@@ -57,7 +57,8 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
   }
 }
 
-// One wave per token.
+// One wave per token; EPL experts per lane (EPL*64 >= E).
+template <int EPL>
 __global__ __launch_bounds__(256) void topk_kernel(
     const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16,
@@ -66,97 +67,16 @@ __global__ __launch_bounds__(256) void topk_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
-  float lg[kMaxEPL];
-  load_logits(logits, logits_f32, t < T ? t : 0, sp.E, lg);
+  float lg[EPL];
+  load_logits<EPL>(logits, logits_f32, t < T ? t : 0, sp.E, lg);
   int e;
   float w;
-  select_token(sp, lg, lds[wave], e, w);
+  select_token<EPL>(sp, lg, lds[wave], e, w);
   if (t < T && lane < sp.k) {
     const size_t o = static_cast<size_t>(t) * sp.k + lane;
     ids[o] = e;
     w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
     if (w_f32 != nullptr) w_f32[o] = w;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Decode router: gate + selection in one launch.  Block b's 8 waves compute
-// the logits of experts 8b .. 8b+7 for all T tokens (expert row in
-// registers); the last block to finish (device-scope counter, reset by that
-// block) selects the experts of every token, 8 tokens at a time.  No block
-// ever waits for another, so the launch cannot stall.
-// ---------------------------------------------------------------------------
-constexpr int kRouteDecodeMaxT = 16;
-constexpr int kRouteWaves = 8;
-
-template <int NC>
-__global__ __launch_bounds__(512) void route_decode_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T,
-    int H, SelectParams sp, void* __restrict__ logits, int logits_f32,
-    float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16,
-    int32_t* __restrict__ ids, int32_t* __restrict__ sync) {
-  __shared__ SelectLds lds[kRouteWaves];
-  __shared__ int is_last;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int E = sp.E;
-  const int e = blockIdx.x * kRouteWaves + wave;
-  if (e < E) {
-    const uint16_t* wrow = wg + static_cast<size_t>(e) * H;
-    uint4 w[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int h = c * 512 + lane * 8;
-      w[c] = (h < H) ? *reinterpret_cast<const uint4*>(wrow + h)
-                     : make_uint4(0u, 0u, 0u, 0u);
-    }
-    for (int t = 0; t < T; ++t) {
-      const uint16_t* xr = x + static_cast<size_t>(t) * H;
-      float acc = 0.0f;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int h = c * 512 + lane * 8;
-        if (h < H) acc = dot8(*reinterpret_cast<const uint4*>(xr + h), w[c], acc);
-      }
-      acc = wave_sum(acc);
-      if (lane == 0) {
-        const size_t o = static_cast<size_t>(t) * E + e;
-        if (logits_f32) {
-          reinterpret_cast<float*>(logits)[o] = acc;
-        } else {
-          reinterpret_cast<uint16_t*>(logits)[o] =
-              static_cast<uint16_t>(f32_to_bf16_bits(acc));
-        }
-      }
-    }
-  }
-  // publish this block's logits, then count it
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int done = __hip_atomic_fetch_add(sync, 1, __ATOMIC_ACQ_REL,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    is_last = done == static_cast<int>(gridDim.x) - 1;
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  for (int t0 = 0; t0 < T; t0 += kRouteWaves) {
-    const int t = t0 + wave;
-    float lg[kMaxEPL];
-    load_logits(logits, logits_f32, t < T ? t : 0, E, lg);
-    int se;
-    float sw;
-    select_token(sp, lg, lds[wave], se, sw);
-    if (t < T && lane < sp.k) {
-      const size_t o = static_cast<size_t>(t) * sp.k + lane;
-      ids[o] = se;
-      w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(sw));
-      if (w_f32 != nullptr) w_f32[o] = sw;
-    }
-  }
-  if (threadIdx.x == 0) {
-    __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -238,43 +158,15 @@ extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
   if (T == 0) return LMOE_OK;
   const SelectParams sp =
       make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
-  hipLaunchKernelGGL(topk_kernel, dim3((T + 3) / 4), dim3(256), 0, stream,
-                     logits, logits_f32, T, sp, w_f32, w_bf16, ids);
-  LMOE_RETURN_LAUNCH();
-}
-
-extern "C" int lmoe_router_decode(const void* x, const void* wg, int T, int H,
-                                  int E, int k, int scoring, const float* bias,
-                                  int n_group, int topk_group, int renorm,
-                                  float routed_scale, void* logits,
-                                  int logits_f32, float* w_f32,
-                                  uint16_t* w_bf16, int32_t* ids,
-                                  int32_t* sync, hipStream_t stream) {
-  if (x == nullptr || wg == nullptr || logits == nullptr || w_bf16 == nullptr ||
-      ids == nullptr || sync == nullptr)
-    return LMOE_ERR_ARG;
-  if (H <= 0) return LMOE_ERR_ARG;
-  const int st = check_select(T, E, k, scoring, n_group, topk_group);
-  if (st != LMOE_OK) return st;
-  if (T > kRouteDecodeMaxT || H % 8 != 0 || H > kGateMaxChunks * 512)
-    return LMOE_ERR_SHAPE;
-  if (T == 0) return LMOE_OK;
-  const SelectParams sp =
-      make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
-  const dim3 grid((E + kRouteWaves - 1) / kRouteWaves);
-  const uint16_t* xb = static_cast<const uint16_t*>(x);
-  const uint16_t* wb = static_cast<const uint16_t*>(wg);
-  const int nc = (H + 511) / 512;
-  if (nc <= 4) {
-    hipLaunchKernelGGL(route_decode_kernel<4>, grid, dim3(512), 0, stream, xb, wb,
-                       T, H, sp, logits, logits_f32, w_f32, w_bf16, ids, sync);
-  } else if (nc <= 8) {
-    hipLaunchKernelGGL(route_decode_kernel<8>, grid, dim3(512), 0, stream, xb, wb,
-                       T, H, sp, logits, logits_f32, w_f32, w_bf16, ids, sync);
+  const dim3 grid((T + 3) / 4);
+  if (E <= 64) {
+    hipLaunchKernelGGL(topk_kernel<1>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
+  } else if (E <= 128) {
+    hipLaunchKernelGGL(topk_kernel<2>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
+  } else if (E <= 256) {
+    hipLaunchKernelGGL(topk_kernel<4>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
   } else {
-    hipLaunchKernelGGL(route_decode_kernel<16>, grid, dim3(512), 0, stream, xb,
-                       wb, T, H, sp, logits, logits_f32, w_f32, w_bf16, ids,
-                       sync);
+    hipLaunchKernelGGL(topk_kernel<8>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
   }
   LMOE_RETURN_LAUNCH();
 }

@@ -69,42 +69,43 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Selects the k experts of one token from its logits lg[j] (expert j*64 +
-// lane, -inf beyond E).  Lane l < k returns the l-th selected expert id
-// (-1 if fewer than k are eligible) and its final f32 weight.
+// lane, -inf beyond E; EPL*64 >= E).  Lane l < k returns the l-th selected
+// expert id (-1 if fewer than k are eligible) and its final f32 weight.
+template <int EPL>
 __device__ __forceinline__ void select_token(const SelectParams& sp,
-                                             float (&lg)[kMaxEPL],
+                                             float (&lg)[EPL],
                                              SelectLds& L, int& out_e,
                                              float& out_w) {
   const int lane = threadIdx.x & 63;
   const int E = sp.E;
   const int k = sp.k;
-  float sel[kMaxEPL];  // selection score
-  float wgt[kMaxEPL];  // weight carried by a selected expert
-  bool elig[kMaxEPL];
+  float sel[EPL];  // selection score
+  float wgt[EPL];  // weight carried by a selected expert
+  bool elig[EPL];
   if (sp.scoring == LMOE_SCORING_SOFTMAX) {
     if (sp.bias != nullptr) {
       // additive per-expert logit bias (rounded once, before the softmax)
 #pragma unroll
-      for (int j = 0; j < kMaxEPL; ++j) {
+      for (int j = 0; j < EPL; ++j) {
         const int e = j * kWave + lane;
         if (e < E) lg[j] = lg[j] + sp.bias[e];
       }
     }
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kMaxEPL; ++j) m = fmaxf(m, lg[j]);
+    for (int j = 0; j < EPL; ++j) m = fmaxf(m, lg[j]);
     m = wave_max(m);
-    float ex[kMaxEPL];
+    float ex[EPL];
     float local = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kMaxEPL; ++j) {
+    for (int j = 0; j < EPL; ++j) {
       const int e = j * kWave + lane;
       ex[j] = (e < E) ? exp_nonpos(lg[j] - m) : 0.0f;
       local = (j == 0) ? ex[0] : local + ex[j];
     }
     const float s = wave_sum(local);
 #pragma unroll
-    for (int j = 0; j < kMaxEPL; ++j) {
+    for (int j = 0; j < EPL; ++j) {
       const int e = j * kWave + lane;
       const float p = ex[j] / s;
       sel[j] = p;
@@ -113,7 +114,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < kMaxEPL; ++j) {
+    for (int j = 0; j < EPL; ++j) {
       const int e = j * kWave + lane;
       const float sg = sigmoid_det(lg[j]);
       const float sb = (e < E && sp.bias != nullptr) ? sg + sp.bias[e] : sg;
@@ -125,7 +126,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
       const int ng = sp.n_group;
       const int gs = E / ng;
 #pragma unroll
-      for (int j = 0; j < kMaxEPL; ++j) {
+      for (int j = 0; j < EPL; ++j) {
         const int e = j * kWave + lane;
         if (e < E) L.c_s[e] = sel[j];
       }
@@ -152,7 +153,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
       for (int g = 0; g < ng; ++g) r += better(L.gsc[g], g, gscore, lane) ? 1 : 0;
       const uint64_t kept = __ballot(lane < ng && r < sp.topk_group);
 #pragma unroll
-      for (int j = 0; j < kMaxEPL; ++j) {
+      for (int j = 0; j < EPL; ++j) {
         const int e = j * kWave + lane;
         elig[j] = (e < E) && ((kept >> (e / gs)) & 1ull);
       }
@@ -164,7 +165,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
   float m = -INFINITY;
   int me = 0x7fffffff;
 #pragma unroll
-  for (int j = 0; j < kMaxEPL; ++j) {
+  for (int j = 0; j < EPL; ++j) {
     const int e = j * kWave + lane;
     if (elig[j] && better(sel[j], e, m, me)) {
       m = sel[j];
@@ -188,7 +189,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
   // 3. compact the candidates, in ascending expert id order
   int C = 0;
 #pragma unroll
-  for (int j = 0; j < kMaxEPL; ++j) {
+  for (int j = 0; j < EPL; ++j) {
     const int e = j * kWave + lane;
     const bool c = elig[j] && sel[j] >= thr;
     const uint64_t bm = __ballot(c);
@@ -230,11 +231,12 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
 }
 
 // Logits of token t in the lane layout (expert j*64 + lane), -inf beyond E.
+template <int EPL>
 __device__ __forceinline__ void load_logits(const void* logits, int logits_f32,
-                                            int t, int E, float (&lg)[kMaxEPL]) {
+                                            int t, int E, float (&lg)[EPL]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < kMaxEPL; ++j) {
+  for (int j = 0; j < EPL; ++j) {
     const int e = j * kWave + lane;
     float v = -INFINITY;
     if (e < E) {

@@ -47,7 +47,6 @@ class MoEWorkspace:
     act: torch.Tensor   # [N, I] bf16 (sorted order; flat pair order in moe_decode)
     y: torch.Tensor     # [N, H] bf16, flat pair order
     out: torch.Tensor   # [T, H] bf16
-    sync: torch.Tensor  # int32 counters of moe_decode, zero between launches
     meta: torch.Tensor  # int32 [META_COUNT] of moe_decode
     last_meta: torch.Tensor | None = None  # meta written by the last fused_experts call
 
@@ -60,13 +59,11 @@ def get_workspace(T: int, k: int, P: int, H: int, I: int, device, *, tag: str = 
     ws = _WORKSPACES.get(key)
     if ws is None:
         N = T * k
-        words = native.moe_decode_sync_words(N, P, H, I) if 0 < N <= native.MOE_DECODE_MAX_PAIRS else 1
         ws = MoEWorkspace(
             perm=native.Permutation.allocate(N, P, device),
             act=torch.empty((max(N, 1), I), dtype=torch.bfloat16, device=device),
             y=torch.empty((max(N, 1), H), dtype=torch.bfloat16, device=device),
             out=torch.empty((max(T, 1), H), dtype=torch.bfloat16, device=device),
-            sync=torch.zeros(max(words, 1), dtype=torch.int32, device=device),
             meta=torch.zeros(native.META_COUNT, dtype=torch.int32, device=device),
         )
         _WORKSPACES[key] = ws
@@ -75,22 +72,6 @@ def get_workspace(T: int, k: int, P: int, H: int, I: int, device, *, tag: str = 
 
 def clear_workspaces() -> None:
     _WORKSPACES.clear()
-    _ROUTE_SYNC.clear()
-
-
-_ROUTE_SYNC: dict[str, torch.Tensor] = {}
-
-
-def route_sync(device) -> torch.Tensor:
-    """The per-device counter of the one-launch decode router (zero between
-    launches).  Launches that share it must not run concurrently: route on
-    one stream, or pass each concurrent caller its own zeroed int32."""
-    key = str(torch.device(device))
-    t = _ROUTE_SYNC.get(key)
-    if t is None:
-        t = torch.zeros(1, dtype=torch.int32, device=device)
-        _ROUTE_SYNC[key] = t
-    return t
 
 
 # ---------------------------------------------------------------------------
@@ -112,22 +93,9 @@ class RouterSpec:
 
 def route(hidden: torch.Tensor, gate_weight: torch.Tensor | None, spec: RouterSpec, *,
           router_logits: torch.Tensor | None = None, logits_out: torch.Tensor | None = None,
-          w_out: torch.Tensor | None = None, ids_out: torch.Tensor | None = None,
-          sync: torch.Tensor | None = None):
+          w_out: torch.Tensor | None = None, ids_out: torch.Tensor | None = None):
     """Gate (if gate_weight is given) then expert selection on the GPU.
-    Returns (topk_weights bf16 [T,k], topk_ids int32 [T,k], logits).  Up to
-    16 tokens with a gate weight run as one launch (gate + selection)."""
-    grouped = bool(spec.use_grouped_topk)
-    if gate_weight is not None and hidden.shape[0] <= native.ROUTE_DECODE_MAX_TOKENS and router_logits is None:
-        w, ids, logits = native.router_decode(
-            hidden, gate_weight, int(spec.top_k), sync if sync is not None else route_sync(hidden.device),
-            scoring=spec.scoring_func, bias=spec.e_score_correction_bias,
-            num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
-            topk_group=int(spec.topk_group or 1) if grouped else 1,
-            renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
-            logits=logits_out, w_bf16=w_out, ids=ids_out,
-        )
-        return w, ids, logits
+    Returns (topk_weights bf16 [T,k], topk_ids int32 [T,k], logits)."""
     if gate_weight is not None:
         T = hidden.shape[0]
         E = gate_weight.shape[0]
@@ -136,6 +104,7 @@ def route(hidden: torch.Tensor, gate_weight: torch.Tensor | None, spec: RouterSp
         router_logits = native.router_gate(hidden, gate_weight, logits_out)
     if router_logits is None:
         raise ValueError("route() needs router_logits or a gate weight")
+    grouped = bool(spec.use_grouped_topk)
     w, ids, _ = native.router_topk(
         router_logits, int(spec.top_k), scoring=spec.scoring_func,
         bias=spec.e_score_correction_bias,
@@ -165,9 +134,9 @@ def fused_experts(
 ) -> torch.Tensor:
     """out[t] = add[t] + sum_j w[t,j] * MLP_{slot(ids[t,j])}(x_t).
 
-    AUTO: up to 512 pairs run as one decode launch (remap, grouping, both
-    GEMVs, combine); more pairs permute and run the grouped MFMA GEMM (or
-    the GEMV kernels when path is GEMV) and the combine."""
+    AUTO: up to 512 pairs run the decode body (remap and grouping inside the
+    gate_up and down+combine launches); more pairs permute and run the
+    grouped MFMA GEMM (or the GEMV kernels when path is GEMV) and combine."""
     T, H = hidden.shape
     k = int(topk_ids.shape[1])
     P = int(w13_slots.shape[0])
@@ -177,7 +146,7 @@ def fused_experts(
     if path == native.LMOE_PATH_AUTO and 0 < T * k <= native.MOE_DECODE_MAX_PAIRS:
         ws.last_meta = ws.meta
         return native.moe_decode(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2phy, dst,
-                                 ws.act, ws.y, ws.sync, ws.meta, add=add)
+                                 ws.act, ws.meta, add=add)
     native.permute(topk_ids, ws.perm, log2phy=log2phy)
     ws.last_meta = ws.perm.meta
     if T * k <= native.FUSED_DECODE_MAX_PAIRS and path == native.LMOE_PATH_GEMV:

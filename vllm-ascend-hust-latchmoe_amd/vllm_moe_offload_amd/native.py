@@ -24,12 +24,11 @@ LMOE_SCORING_SIGMOID = 1
 LMOE_PATH_AUTO = 0
 LMOE_PATH_GEMV = 1
 LMOE_PATH_MFMA = 2
-META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES, META_STALLS = 0, 1, 2, 3, 4
-META_COUNT = 8
+META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
+META_COUNT = 4
 MFMA_BLOCK_M = 128
 FUSED_DECODE_MAX_PAIRS = 1024
 MOE_DECODE_MAX_PAIRS = 512
-ROUTE_DECODE_MAX_TOKENS = 16
 
 EXPORTED_SYMBOLS = (
     "lmoe_status_string",
@@ -44,8 +43,6 @@ EXPORTED_SYMBOLS = (
     "lmoe_down",
     "lmoe_combine",
     "lmoe_fused_moe_decode",
-    "lmoe_router_decode",
-    "lmoe_moe_decode_sync_words",
     "lmoe_moe_decode",
     "lmoe_stage_copy",
 )
@@ -83,14 +80,9 @@ _SIGNATURES = {
         _i,
         [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
-    "lmoe_router_decode": (
-        _i,
-        [_vp, _vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp],
-    ),
-    "lmoe_moe_decode_sync_words": (_sz, [_i, _i, _i, _i]),
     "lmoe_moe_decode": (
         _i,
-        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp],
+        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "lmoe_stage_copy": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
 }
@@ -225,62 +217,6 @@ def router_topk(
         "lmoe_router_topk",
     )
     return w_bf16, ids, w_f32
-
-
-def router_decode(
-    x: torch.Tensor,
-    wg: torch.Tensor,
-    top_k: int,
-    sync: torch.Tensor,
-    *,
-    scoring: str = "softmax",
-    bias: torch.Tensor | None = None,
-    num_expert_group: int = 1,
-    topk_group: int = 1,
-    renormalize: bool = True,
-    routed_scaling_factor: float = 1.0,
-    logits: torch.Tensor | None = None,
-    w_bf16: torch.Tensor | None = None,
-    ids: torch.Tensor | None = None,
-    w_f32: torch.Tensor | None = None,
-    stream=None,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Gate + selection in one launch (T <= 16); returns (w_bf16, ids, logits).
-    sync: one int32 of device memory, zero before the first call (left zero)."""
-    lib = load_library()
-    _need(x, "x", torch.bfloat16)
-    T, H = x.shape
-    E = wg.shape[0]
-    _need(wg, "wg", torch.bfloat16, (E, H))
-    _need(sync, "sync", torch.int32)
-    if scoring not in ("softmax", "sigmoid"):
-        raise ValueError(f"unsupported scoring function {scoring!r}")
-    mode = LMOE_SCORING_SOFTMAX if scoring == "softmax" else LMOE_SCORING_SIGMOID
-    if bias is not None:
-        _need(bias, "e_score_correction_bias", torch.float32, (E,))
-    dev = x.device
-    if logits is None:
-        logits = torch.empty((T, E), dtype=torch.bfloat16, device=dev)
-    if logits.dtype not in (torch.bfloat16, torch.float32):
-        raise ValueError("logits must be bf16 or f32")
-    _need(logits, "logits", logits.dtype, (T, E))
-    if w_bf16 is None:
-        w_bf16 = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
-    if ids is None:
-        ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
-    _need(w_bf16, "topk_weights", torch.bfloat16, (T, top_k))
-    _need(ids, "topk_ids", torch.int32, (T, top_k))
-    if w_f32 is not None:
-        _need(w_f32, "w_f32", torch.float32, (T, top_k))
-    _check(
-        lib.lmoe_router_decode(
-            _ptr(x), _ptr(wg), T, H, E, int(top_k), mode, _ptr(bias), int(num_expert_group or 1),
-            int(topk_group or 1), int(bool(renormalize)), float(routed_scaling_factor), _ptr(logits),
-            int(logits.dtype == torch.float32), _ptr(w_f32), _ptr(w_bf16), _ptr(ids), _ptr(sync), _stream(stream),
-        ),
-        "lmoe_router_decode",
-    )
-    return w_bf16, ids, logits
 
 
 # ---------------------------------------------------------------------------
@@ -539,10 +475,6 @@ def fused_moe_decode(
     return out
 
 
-def moe_decode_sync_words(n_pairs: int, n_slots: int, H: int, I: int) -> int:
-    return int(load_library().lmoe_moe_decode_sync_words(int(n_pairs), int(n_slots), int(H), int(I)))
-
-
 def moe_decode(
     x: torch.Tensor,
     topk_weights: torch.Tensor,
@@ -552,16 +484,15 @@ def moe_decode(
     log2phy: torch.Tensor | None,
     out: torch.Tensor,
     act: torch.Tensor,
-    y: torch.Tensor,
-    sync: torch.Tensor,
     meta: torch.Tensor,
     *,
     add: torch.Tensor | None = None,
     table_len: int | None = None,
     stream=None,
 ) -> torch.Tensor:
-    """Decode layer body in one launch from the router output: slot remap,
-    grouping by slot, gate_up + SiLU*mul, down, combine (T*k <= 512)."""
+    """Decode layer body from the router output (gate_up launch, down +
+    combine launch): slot remap and grouping by slot inside both, each
+    expert's weights read once (T*k <= 512)."""
     lib = load_library()
     _need(x, "x", torch.bfloat16)
     T, H = x.shape
@@ -580,18 +511,15 @@ def moe_decode(
     if add is not None:
         _need(add, "add", torch.bfloat16, (T, H))
     _need(act, "act", torch.bfloat16)
-    _need(y, "y", torch.bfloat16)
-    if act.shape[0] < N or act.shape[1] != I or y.shape[0] < N or y.shape[1] != H:
-        raise ValueError("act / y workspaces are smaller than [T*k, I] / [T*k, H]")
-    _need(sync, "sync", torch.int32)
+    if act.dim() != 2 or act.shape[0] < N or act.shape[1] != I:
+        raise ValueError("act workspace is smaller than [T*k, I]")
     _need(meta, "meta", torch.int32)
     if meta.numel() < META_COUNT:
         raise ValueError(f"meta needs {META_COUNT} int32")
     _check(
         lib.lmoe_moe_decode(
             _ptr(x), T, H, I, k, _ptr(topk_ids), _ptr(log2phy), n_table, _ptr(w13_slots), _ptr(w2_slots), P,
-            _ptr(topk_weights), _ptr(add), _ptr(out), _ptr(act), _ptr(y), _ptr(sync), int(sync.numel()),
-            _ptr(meta), _stream(stream),
+            _ptr(topk_weights), _ptr(add), _ptr(out), _ptr(act), _ptr(meta), _stream(stream),
         ),
         "lmoe_moe_decode",
     )
