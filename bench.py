@@ -4,15 +4,15 @@
 Headline (value): Qwen3-30B-A3B-shaped decode, 48 MoE layers, 64 slots per
 layer, batch 1 — MoE-layer microseconds per token per layer, measured as the
 hipGraph replay of the 48-layer decode compute (per layer: gate GEMV, top-k,
-gate_up + SiLU*mul, down + combine; slot remap and grouping inside the last
-two) after the step's eager staging has made every routed expert resident.  Also reported in the same JSON line:
+slot remap + permutation, gate_up GEMV + SiLU*mul, down GEMV + combine)
+after the step's eager staging has made every routed expert resident.  Also reported in the same JSON line:
 
   decode[B]   B in --batches: graph-replayed layer us/token, layer HBM GB/s,
               slot-miss rate of the Zipf-skewed router, and the eager
               staging-inclusive step time (D2H of the ids, LRU, H2D)
-  roofline    dominant work (the layer body lmoe_moe_decode at B=1: its
-              gate_up and down + combine kernels), timed with HIP events
-              over calls rotating through the 48 layers
+  roofline    dominant kernel (gate_up GEMV + SiLU*mul at B=1; the down
+              GEMV + combine beside it), timed with HIP events over launches
+              rotating through the 48 layers
   prefill     4096 tokens, 48 slots, uniform router: capacity waves with one
               combine (compute TFLOP/s and MFMA fraction; staged wall time;
               H2D GB/s), against the blocking full layer
@@ -267,63 +267,64 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
 
 
 def bench_decode_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
-    """Dominant decode work at B=1: the layer body lmoe_moe_decode (its
-    gate_up kernel and its down + combine kernel, remap and grouping inside
-    both), 48*reps calls rotating through the 48 layers' slot banks (29 GB,
-    far beyond the 256 MB MALL), captured in one graph so they run back to
-    back, timed with HIP events on the stream they are launched on."""
+    """Dominant decode kernel at B=1: the gate_up GEMV + SiLU*mul (two thirds
+    of the layer's bytes), 48*reps launches rotating through the 48 layers'
+    slot banks (29 GB, far beyond the 256 MB MALL), captured in one graph so
+    they run back to back, timed with HIP events on the stream they are
+    launched on.  Same measurement for the down GEMV + combine."""
     import torch
 
-    from vllm_moe_offload_amd import fused_moe, native
+    from vllm_moe_offload_amd import native
 
     ws_w, ws_ids, x = state
     L = model.L
     dev = torch.device("cuda")
     B = x.shape[0]
     P = model.bank(0).physical_expert_count
-    ws = fused_moe.get_workspace(B, K, P, H, I, dev, tag="roofline")
+    perms, acts = [], []
     out = torch.empty((B, H), dtype=torch.bfloat16, device=dev)
-    U = []
     for l in range(L):
-        native.moe_decode(x, ws_w[l], ws_ids[l], model.bank(l).w13_slots, model.bank(l).w2_slots,
-                          model.rt.log2phy_buffer(l), out, ws.act, ws.meta)
-        torch.cuda.synchronize()
-        U.append(int(ws.meta[native.META_ACTIVE].item()))
+        p = native.Permutation.allocate(B * K, P, dev)
+        native.permute(ws_ids[l], p, log2phy=model.rt.log2phy_buffer(l))
+        perms.append(p)
+        acts.append(torch.empty((B * K, I), dtype=torch.bfloat16, device=dev))
+    torch.cuda.synchronize()
+    U = [int(perms[l].meta[native.META_ACTIVE].item()) for l in range(L)]
+    u = sum(U) / L
 
-    def launches():
+    def gateup():
         for _ in range(reps):
             for l in range(L):
-                native.moe_decode(x, ws_w[l], ws_ids[l], model.bank(l).w13_slots, model.bank(l).w2_slots,
-                                  model.rt.log2phy_buffer(l), out, ws.act, ws.meta)
+                native.gateup_silu(x, K, model.bank(l).w13_slots, perms[l], acts[l], path=native.LMOE_PATH_GEMV)
 
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        launches()
-    torch.cuda.current_stream().wait_stream(s)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        launches()
-    g.replay()
-    stream = torch.cuda.current_stream()
-    with Timer(stream) as t:
+    def down():
+        for _ in range(reps):
+            for l in range(L):
+                native.down_combine(acts[l], ws_w[l], model.bank(l).w2_slots, perms[l], out)
+
+    res = {}
+    for name, fn, byts in (
+        ("gateup_gemv_kernel", gateup, u * (2 * I * H * 2) + B * H * 2 + B * K * I * 2),
+        ("down_combine_gemv_kernel", down, u * (H * I * 2) + B * K * I * 2 + B * H * 2),
+    ):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
         g.replay()
-    ms = t.ms()
-    torch.cuda.synchronize()
-    assert int(ws.meta[native.META_ERRORS].item()) == 0
-    n = reps * L
-    avg_us = ms * 1000.0 / n
-    u = sum(U) / L
-    # weights of the distinct slots + x in + act out and back + out
-    bytes_per_launch = u * EXPERT_BYTES + B * H * 2 + B * K * I * 2 * 2 + B * H * 2
-    return {
-        "kernel": "lmoe_moe_decode = moe_decode_gateup_kernel + moe_decode_down_kernel",
-        "avg_launch_us": round(avg_us, 3),
-        "bytes_per_launch": int(bytes_per_launch),
-        "distinct_slots_per_launch": round(u, 2),
-        "achieved_gbs": round(bytes_per_launch / (avg_us * 1e-6) / 1e9, 1),
-        "launches": n,
-    }
+        stream = torch.cuda.current_stream()
+        with Timer(stream) as t:
+            g.replay()
+        ms = t.ms()
+        avg_us = ms * 1000.0 / (reps * L)
+        res[name] = {"avg_launch_us": round(avg_us, 3), "bytes_per_launch": int(byts),
+                     "achieved_gbs": round(byts / (avg_us * 1e-6) / 1e9, 1), "launches": reps * L}
+    res["distinct_slots_per_launch"] = round(u, 2)
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -758,12 +759,14 @@ def main() -> int:
         "deepseek_v3_style": deepseek,
     }
     if roof is not None:
-        line["roofline"] = {"bound": "hbm", "achieved": roof["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(roof["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                            "kernel": roof["kernel"], "avg_launch_us": roof["avg_launch_us"],
-                            "bytes_per_launch": roof["bytes_per_launch"],
-                            "distinct_slots_per_launch": roof["distinct_slots_per_launch"]}
-        traffic_file = ROOT / "profiles" / "moe_decode_b1_traffic.json"
+        gu = roof["gateup_gemv_kernel"]
+        line["roofline"] = {"bound": "hbm", "achieved": gu["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(gu["achieved_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                            "kernel": "gateup_gemv_kernel (decode B=1)", "avg_launch_us": gu["avg_launch_us"],
+                            "bytes_per_launch": gu["bytes_per_launch"],
+                            "distinct_slots_per_launch": roof["distinct_slots_per_launch"],
+                            "down_combine_gemv_kernel": roof["down_combine_gemv_kernel"]}
+        traffic_file = ROOT / "profiles" / "gateup_gemv_decode_b1_traffic.json"
         if traffic_file.exists():
             try:
                 line["roofline"]["traffic"] = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")

@@ -34,11 +34,7 @@
  *                      and the single native combine of :3342-3379
  *   lmoe_fused_moe_decode  GMM1+swiglu+GMM2+unpermute of the decode
  *                      fused_experts call (patch_fused_moe.py:3946-4009)
- *   lmoe_moe_decode    remap + init-routing + GMM1 + swiglu + GMM2 + unpermute
- *                      of the decode fused_experts call, straight from the
- *                      router output (slot_mapping.py:116-140,
- *                      patch_fused_moe.py:668-701, :3772-3774, :3363-3366,
- *                      :3946-4009)
+ *   lmoe_down_combine  GMM2 + unpermute of the same call
  *   lmoe_stage_copy    TransferEngine.load_many_async H2D batch + ready event,
  *                      moe_offload/transfer_engine.py:139-187, 205-228
  */
@@ -176,10 +172,23 @@ int lmoe_combine(const void* y, const int32_t* row_idx, const uint16_t* w,
                  int T, int k, int H, const void* add, void* out,
                  hipStream_t stream);
 
-/* Decode MoE for small pair counts: gate_up GEMV + SiLU*mul into act (sorted
- * order), then down GEMV fused with the weighted combine:
+/* The second half of lmoe_fused_moe_decode on its own: down GEMV from act
+ * (sorted order) fused with the weighted combine into out (same argument
+ * meaning).  Replaces npu_grouped_matmul GMM2 + npu_moe_token_unpermute of
+ * the decode call (patch_fused_moe.py:3772-3774, :3363-3366). */
+int lmoe_down_combine(const void* act, int T, int H, int I, int k,
+                      const void* w2_slots, int n_slots, const uint16_t* w,
+                      const int32_t* offsets, const int32_t* row_idx,
+                      const int32_t* active, const int32_t* meta,
+                      const void* add, void* out, hipStream_t stream);
+
+/* Decode MoE for small pair counts, two launches: gate_up GEMV + SiLU*mul
+ * into act (sorted order), then down GEMV fused with the weighted combine
+ * (each workgroup owns a few output columns of every token):
  *   out[t] = (add ? add[t] : 0) + sum_j w[t][j] * W2_s(t,j) act[pos(t,j)].
- * Needs T*k <= 1024.  Permutation arrays as produced by lmoe_permute. */
+ * Each slot's weights are read once however many tokens chose it.  Needs
+ * T*k <= 1024, H % 8 == 0, I % 64 == 0, I <= 4096, H <= 8192; x, slot banks
+ * and act 16-byte aligned.  Permutation arrays as produced by lmoe_permute. */
 int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                           const void* w13_slots, const void* w2_slots,
                           int n_slots, const uint16_t* w,
@@ -187,25 +196,6 @@ int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                           const int32_t* row_idx, const int32_t* active,
                           const int32_t* meta, const void* add, void* act,
                           void* out, hipStream_t stream);
-
-/* Decode MoE layer body from the router output (two launches on stream):
- *   slot(p) = log2phy ? log2phy[ids[p]] : ids[p]   (p = t*k + j)
- *   act[p]  = silu(W13_s[0:I] x_t) * (W13_s[I:2I] x_t)   bf16 (GMM1 bf16)
- *   y[p]    = W2_s act[p]                                 bf16
- *   out[t]  = (add ? add[t] : 0) + sum_j w[t][j] * y[t*k+j]   f32, one rounding
- * Each expert's weights are read once however many of the T tokens chose it.
- * A pair whose id is outside [0, n_log2phy) or whose slot is outside
- * [0, n_slots) contributes nothing and is counted in meta[LMOE_META_ERRORS];
- * meta[ACTIVE] = distinct slots, meta[PAIRS] = placed pairs.  act [T*k, I]
- * is a bf16 workspace indexed by flat pair.  T*k <= 512, n_slots <= 8192,
- * H % 8 == 0, I % 8 == 0, H <= 8192, I <= 4096; x, weights and act 16-byte
- * aligned.  Replaces the decode fused_experts call
- * (patch_fused_moe.py:3946-4009) including its remap and init-routing. */
-int lmoe_moe_decode(const void* x, int T, int H, int I, int k,
-                    const int32_t* ids, const int32_t* log2phy, int n_log2phy,
-                    const void* w13_slots, const void* w2_slots, int n_slots,
-                    const uint16_t* w, const void* add, void* out, void* act,
-                    int32_t* meta, hipStream_t stream);
 
 /* Batched host->device (or device->device) expert copies on a transfer
  * stream: optionally wait on wait_event, then for i < n copy bytes[i] from

@@ -77,6 +77,51 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Sum V values per lane over the lanes that differ in bits LO..HI of the lane
+// id, leaving ONE total per lane: the first log2(V) steps exchange halves of
+// the value set (a reduce-scatter: V-1 shuffles instead of V*(HI-LO+1)), the
+// rest are plain butterfly adds.  On return, the lane holds value index
+// scatter_index<HI, LO, log2 V>(lane).
+template <int V, int HI, int LO>
+__device__ __forceinline__ float reduce_scatter(float (&v)[V], int lane) {
+  constexpr int L = (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
+  static_assert((1 << L) == V, "V must be a power of two <= 16");
+  static_assert(HI - LO + 1 >= L, "not enough lane bits");
+#pragma unroll
+  for (int b = 0; b < L; ++b) {
+    const int bit = HI - b;
+    const int half = V >> (b + 1);
+    const bool upper = (lane >> bit) & 1;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const float send = upper ? v[i] : v[half + i];
+      const float keep = upper ? v[half + i] : v[i];
+      v[i] = keep + __shfl_xor(send, 1 << bit, kWave);
+    }
+  }
+  float r = v[0];
+#pragma unroll
+  for (int bit = HI - L; bit >= LO; --bit) r += __shfl_xor(r, 1 << bit, kWave);
+  return r;
+}
+
+template <int HI, int LO, int L>
+__device__ __forceinline__ int scatter_index(int lane) {
+  int idx = 0;
+#pragma unroll
+  for (int b = 0; b < L; ++b) idx = (idx << 1) | ((lane >> (HI - b)) & 1);
+  return idx;
+}
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming (non-temporal) load of weights read once per launch:
+// measured 7.1 TB/s on a 4 GiB read against 6.2 TB/s for plain loads.
+__device__ __forceinline__ uint4 load_stream16(const uint16_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }

@@ -1,11 +1,14 @@
 // Grouped SwiGLU expert MLP over the slot bank, and the weighted combine.
 //
 // Decode (few pairs per slot): weight-streaming GEMV kernels.  Every weight
-// row is read from HBM exactly once with 16-byte (gate/up) or 8-byte (down)
-// vector loads, several rows per lane in flight; token rows and act rows come
-// from L1/L2.  The down projection can be fused with the weighted combine
-// (one workgroup owns 4 output columns for every token), so the decode layer
-// is permute + two kernels.
+// row is read from HBM exactly once with 16-byte non-temporal loads, all of a
+// wave's rows in flight at once; token rows and act rows come from L2.  The
+// down projection is fused with the weighted combine (one workgroup owns R
+// output columns for every token), so the decode layer body is permute + two
+// kernels.  (A single launch would need a cross-block hand-off of act; the
+// agent-scope fences that takes write back / invalidate a whole XCD L2 each
+// and cost far more than a kernel boundary, which in a captured graph is
+// back to back.)
 // Prefill (hundreds of pairs per slot): bf16 MFMA grouped GEMM, gemm_mfma.h.
 //
 // Reference behaviour: npu_grouped_matmul (GMM1) + npu_swiglu + GMM2 inside
@@ -18,147 +21,199 @@
 namespace lmoe {
 
 // ---------------------------------------------------------------------------
-// gate_up GEMV + SiLU*mul.  grid (ceil(I/4), max_active), 4 waves; wave w of
-// block (bx, a) owns i = 4*bx + w of the a-th active slot: its gate and up
-// rows stay in registers while the slot's token rows stream past.
+// gate_up GEMV + SiLU*mul.  grid (ceil(I/RPB), max_active), 4 waves.
+// Block (bx, a) serves the a-th active slot (active[] / offsets[] of the
+// permutation).  Without SPLIT each wave owns one row pair i (gate row i and
+// up row I+i, 2*NC 16-byte chunks per lane, loaded non-temporally, RPB = 4);
+// with SPLIT (long rows, NC > 8) waves 2w and 2w+1 own the gate and the up
+// row of one i (RPB = 2) and meet in LDS.  The slot's tokens stream past one
+// at a time (x rows from L2); act is written in sorted order.
 // ---------------------------------------------------------------------------
-template <int NC>
+template <int NC, bool SPLIT>
 __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, int H, int I, int topk,
     const uint16_t* __restrict__ w13, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ active,
     const int32_t* __restrict__ meta, uint16_t* __restrict__ act) {
+  __shared__ float s_up[2];
   const int a = blockIdx.y;
   if (a >= meta[LMOE_META_ACTIVE]) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int i = blockIdx.x * 4 + wave;
-  if (i >= I) return;
   const int s = active[a];
   const int p0 = offsets[s];
   const int n = offsets[s + 1] - p0;
-  const uint16_t* grow = w13 + (static_cast<size_t>(s) * 2 * I + i) * H;
-  const uint16_t* urow = grow + static_cast<size_t>(I) * H;
-
-  uint4 wg[NC], wu[NC];
+  if (!SPLIT) {
+    const int i = blockIdx.x * 4 + wave;
+    if (i >= I) return;
+    const uint16_t* grow = w13 + (static_cast<size_t>(s) * 2 * I + i) * H;
+    const uint16_t* urow = grow + static_cast<size_t>(I) * H;
+    uint4 wg[NC], wu[NC];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int h = c * 512 + lane * 8;
-    if (h < H) {
-      wg[c] = *reinterpret_cast<const uint4*>(grow + h);
-      wu[c] = *reinterpret_cast<const uint4*>(urow + h);
-    } else {
-      wg[c] = make_uint4(0u, 0u, 0u, 0u);
-      wu[c] = make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
-  for (int r0 = 0; r0 < n; r0 += 4) {
-    float ag[4], au[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      ag[q] = 0.0f;
-      au[q] = 0.0f;
-      if (r0 + q < n) {
-        const int t = sorted_pairs[p0 + r0 + q] / topk;
-        const uint16_t* xr = x + static_cast<size_t>(t) * H;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const int h = c * 512 + lane * 8;
-          if (h < H) {
-            const uint4 xv = *reinterpret_cast<const uint4*>(xr + h);
-            ag[q] = dot8(xv, wg[c], ag[q]);
-            au[q] = dot8(xv, wu[c], au[q]);
-          }
-        }
+    for (int c = 0; c < NC; ++c) {
+      const int h = c * 512 + lane * 8;
+      if (h < H) {
+        wg[c] = load_stream16(grow + h);
+        wu[c] = load_stream16(urow + h);
+      } else {
+        wg[c] = make_uint4(0u, 0u, 0u, 0u);
+        wu[c] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
+    for (int r = 0; r < n; ++r) {
+      const int t = sorted_pairs[p0 + r] / topk;
+      const uint16_t* xr = x + static_cast<size_t>(t) * H;
+      float v[2] = {0.0f, 0.0f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      ag[q] = wave_sum(ag[q]);
-      au[q] = wave_sum(au[q]);
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (r0 + q < n) {
-          act[static_cast<size_t>(p0 + r0 + q) * I + i] = swiglu_bf16(ag[q], au[q]);
+      for (int c = 0; c < NC; ++c) {
+        const int h = c * 512 + lane * 8;
+        if (h < H) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xr + h);
+          v[0] = dot8(xv, wg[c], v[0]);
+          v[1] = dot8(xv, wu[c], v[1]);
         }
       }
+      // lanes 0..31 end with the gate total, 32..63 with the up total
+      const float tot = reduce_scatter<2, 5, 0>(v, lane);
+      const float up = __shfl_xor(tot, 32, kWave);
+      if (lane == 0) act[static_cast<size_t>(p0 + r) * I + i] = swiglu_bf16(tot, up);
+    }
+  } else {
+    const int i = blockIdx.x * 2 + (wave >> 1);
+    const int which = wave & 1;  // 0 gate row, 1 up row
+    const bool ok = i < I;
+    const uint16_t* row = w13 + (static_cast<size_t>(s) * 2 * I + which * I + (ok ? i : 0)) * H;
+    uint4 wr[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int h = c * 512 + lane * 8;
+      wr[c] = (ok && h < H) ? load_stream16(row + h) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    for (int r = 0; r < n; ++r) {
+      const int t = sorted_pairs[p0 + r] / topk;
+      const uint16_t* xr = x + static_cast<size_t>(t) * H;
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int h = c * 512 + lane * 8;
+        if (h < H) acc = dot8(*reinterpret_cast<const uint4*>(xr + h), wr[c], acc);
+      }
+      acc = wave_sum(acc);
+      if (which == 1 && lane == 0) s_up[wave >> 1] = acc;
+      __syncthreads();
+      if (ok && which == 0 && lane == 0)
+        act[static_cast<size_t>(p0 + r) * I + i] = swiglu_bf16(acc, s_up[wave >> 1]);
+      __syncthreads();
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// down GEMV fused with the weighted combine (n_pairs <= 1024).  grid
-// ceil(H/4); wave w owns output column h = 4*bx + w for every pair: it walks
-// the active slots G at a time (all G weight rows loaded before use), keeps
-// y[pos][h] in LDS, then the block combines tokens in j order.
+// down GEMV + weighted combine (n_pairs <= 1024).  grid ceil(H/R): block b
+// owns output rows h0 = R*b .. R*b+R-1 for EVERY active slot, so the combine
+// needs nothing from other blocks.  Half wave hw (8 per block) takes the
+// active slots a = hw, hw+8, ...: it holds the slot's R W2 rows (DNC
+// 16-byte chunks per lane and row, non-temporal), with PF also loading the
+// next slot's rows while it computes, streams the slot's act rows one pair at
+// a time (sorted order, from L2) and leaves y[pos][r] (bf16 values) in LDS;
+// then the block
+// combines its R columns of every token in j order.
 // ---------------------------------------------------------------------------
 constexpr int kFusedMaxPairs = 1024;
+constexpr int kDnMaxRows = 4;
 
-template <int NU>
+template <int DNC, int R, bool PF>
 __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     const uint16_t* __restrict__ act, int I, int H, int T, int topk,
     const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ active, const int32_t* __restrict__ meta,
     const int32_t* __restrict__ row_idx, const uint16_t* __restrict__ wts,
     const uint16_t* __restrict__ add, uint16_t* __restrict__ out) {
-  __shared__ float ybuf[kFusedMaxPairs * 4];
-  constexpr int G = 4;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int h = blockIdx.x * 4 + wave;
+  constexpr int LV = (R >= 4) ? 2 : 1;
+  __shared__ float s_y[kFusedMaxPairs * kDnMaxRows];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int l5 = lane & 31;
+  const int half = lane >> 5;
+  const int hw = (tid >> 6) * 2 + half;
   const int na = meta[LMOE_META_ACTIVE];
-  if (h < H) {
-    for (int a0 = 0; a0 < na; a0 += G) {
-      uint2 wv[G][NU];
-      int sl[G];
+  const int h0 = blockIdx.x * R;
+
+  uint4 wcur[R][DNC], wnxt[PF ? R : 1][PF ? DNC : 1];
+  auto load_rows = [&](int s, auto& w) {
+    const uint16_t* base2 = w2 + static_cast<size_t>(s) * H * I;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        sl[g] = (a0 + g < na) ? active[a0 + g] : -1;
-        const uint16_t* row =
-            w2 + (static_cast<size_t>(sl[g] >= 0 ? sl[g] : 0) * H + h) * I;
+    for (int r = 0; r < R; ++r) {
+      const int h = h0 + r;
 #pragma unroll
-        for (int u = 0; u < NU; ++u) {
-          const int e = (u * 64 + lane) * 4;
-          wv[g][u] = (sl[g] >= 0 && e < I) ? *reinterpret_cast<const uint2*>(row + e)
-                                            : make_uint2(0u, 0u);
-        }
+      for (int c = 0; c < DNC; ++c) {
+        const int col = c * 256 + l5 * 8;
+        w[r][c] = (h < H && col < I) ? load_stream16(base2 + static_cast<size_t>(h) * I + col)
+                                     : make_uint4(0u, 0u, 0u, 0u);
       }
+    }
+  };
+  int rank = hw;
+  int s_cur = rank < na ? active[rank] : -1;
+  if (s_cur >= 0) load_rows(s_cur, wcur);
+  // both halves of a wave run the loop together (shuffles span the wave)
+  while (__ballot(s_cur >= 0) != 0ull) {
+    const int nrank = rank + 8;
+    const int s_nxt = (s_cur >= 0 && nrank < na) ? active[nrank] : -1;
+    if constexpr (PF) {
+      if (s_nxt >= 0) load_rows(s_nxt, wnxt);
+    }
+    const int p0 = s_cur >= 0 ? offsets[s_cur] : 0;
+    const int n = s_cur >= 0 ? offsets[s_cur + 1] - p0 : 0;
+    const int n_other = __shfl_xor(n, 32, kWave);
+    const int n_max = n > n_other ? n : n_other;
+    for (int q = 0; q < n_max; ++q) {
+      float v[R];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        if (sl[g] < 0) continue;
-        const int p0 = offsets[sl[g]];
-        const int n = offsets[sl[g] + 1] - p0;
-        for (int r = 0; r < n; ++r) {
-          const int pos = p0 + r;
-          const uint16_t* arow = act + static_cast<size_t>(pos) * I;
-          float acc = 0.0f;
+      for (int r = 0; r < R; ++r) v[r] = 0.0f;
+      if (q < n) {
+        const uint16_t* ar = act + static_cast<size_t>(p0 + q) * I;
 #pragma unroll
-          for (int u = 0; u < NU; ++u) {
-            const int e = (u * 64 + lane) * 4;
-            if (e < I) acc = dot4(*reinterpret_cast<const uint2*>(arow + e), wv[g][u], acc);
+        for (int c = 0; c < DNC; ++c) {
+          const int col = c * 256 + l5 * 8;
+          if (col < I) {
+            const uint4 av = *reinterpret_cast<const uint4*>(ar + col);
+#pragma unroll
+            for (int r = 0; r < R; ++r) v[r] = dot8(av, wcur[r][c], v[r]);
           }
-          acc = wave_sum(acc);
-          if (lane == 0) ybuf[pos * 4 + wave] = round_bf16(acc);  // GMM2 output is bf16
         }
       }
+      // reduce over the 32 lanes of each half wave: lane holds row r
+      const float tot = reduce_scatter<R, 4, 0>(v, lane);
+      const int r = scatter_index<4, 0, LV>(lane);
+      if ((l5 & ((1 << (5 - LV)) - 1)) == 0 && q < n)
+        s_y[(p0 + q) * kDnMaxRows + r] = round_bf16(tot);  // GMM2 output is bf16
+    }
+    rank = nrank;
+    s_cur = s_nxt;
+    if constexpr (PF) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < DNC; ++c) wcur[r][c] = wnxt[r][c];
+    } else {
+      if (s_cur >= 0) load_rows(s_cur, wcur);
     }
   }
   __syncthreads();
-  for (int q = threadIdx.x; q < T * 4; q += blockDim.x) {
-    const int t = q >> 2;
-    const int c = q & 3;
-    const int hh = blockIdx.x * 4 + c;
-    if (hh >= H) continue;
+  for (int qq = tid; qq < T * R; qq += 256) {
+    const int t = qq / R;
+    const int r = qq % R;
+    const int h = h0 + r;
+    if (h >= H) continue;
     float acc = 0.0f;
     for (int j = 0; j < topk; ++j) {
       const int p = t * topk + j;
-      const int r = row_idx[p];
-      if (r >= 0) acc += bf16_to_f32(wts[p]) * ybuf[r * 4 + c];
+      const int pos = row_idx[p];
+      if (pos >= 0) acc += bf16_to_f32(wts[p]) * s_y[pos * kDnMaxRows + r];
     }
-    if (add != nullptr) acc += bf16_to_f32(add[static_cast<size_t>(t) * H + hh]);
-    out[static_cast<size_t>(t) * H + hh] = static_cast<uint16_t>(f32_to_bf16_bits(acc));
+    if (add != nullptr) acc += bf16_to_f32(add[static_cast<size_t>(t) * H + h]);
+    out[static_cast<size_t>(t) * H + h] = static_cast<uint16_t>(f32_to_bf16_bits(acc));
   }
 }
 
@@ -275,15 +330,17 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
                               const int32_t* sorted_pairs, const int32_t* active,
                               const int32_t* meta, int max_active, uint16_t* act,
                               hipStream_t stream) {
-  dim3 grid((I + 3) / 4, max_active);
   const int nc = (H + 511) / 512;
-#define LMOE_GU(NC)                                                            \
-  hipLaunchKernelGGL(gateup_gemv_kernel<NC>, grid, dim3(256), 0, stream, x, H, \
+  const dim3 g4((I + 3) / 4, max_active);
+  const dim3 g2((I + 1) / 2, max_active);
+#define LMOE_GU(NC, SPLIT, G)                                                        \
+  hipLaunchKernelGGL((gateup_gemv_kernel<NC, SPLIT>), G, dim3(256), 0, stream, x, H, \
                      I, topk, w13, offsets, sorted_pairs, active, meta, act)
-  if (nc <= 4) LMOE_GU(4);
-  else if (nc <= 8) LMOE_GU(8);
-  else if (nc <= 14) LMOE_GU(14);
-  else if (nc <= 16) LMOE_GU(16);
+  if (nc <= 2) LMOE_GU(2, false, g4);
+  else if (nc <= 4) LMOE_GU(4, false, g4);
+  else if (nc <= 8) LMOE_GU(8, false, g4);
+  else if (nc <= 14) LMOE_GU(14, true, g2);
+  else if (nc <= 16) LMOE_GU(16, true, g2);
   else return LMOE_ERR_SHAPE;
 #undef LMOE_GU
   return LMOE_OK;
@@ -420,6 +477,36 @@ extern "C" int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
                    n_pairs, block_m, path, y, stream);
 }
 
+extern "C" int lmoe_down_combine(const void* act, int T, int H, int I, int k,
+                                 const void* w2_slots, int n_slots, const uint16_t* w,
+                                 const int32_t* offsets, const int32_t* row_idx,
+                                 const int32_t* active, const int32_t* meta,
+                                 const void* add, void* out, hipStream_t stream) {
+  if (act == nullptr || w2_slots == nullptr || w == nullptr || offsets == nullptr ||
+      row_idx == nullptr || active == nullptr || meta == nullptr || out == nullptr)
+    return LMOE_ERR_ARG;
+  if (T < 0 || H <= 0 || I <= 0 || k <= 0 || n_slots <= 0) return LMOE_ERR_ARG;
+  if (H % 8 != 0 || I % 64 != 0 || I > 4096 || H > 8192) return LMOE_ERR_SHAPE;
+  if (T * k > kFusedMaxPairs) return LMOE_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(w2_slots)) & 15u)
+    return LMOE_ERR_SHAPE;
+  if (T == 0) return LMOE_OK;
+  const int dnc = (I + 255) / 256;
+#define LMOE_DC(DNC, R, PF)                                                                  \
+  hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, PF>), dim3((H + R - 1) / R), dim3(256), \
+                     0, stream, static_cast<const uint16_t*>(act), I, H, T, k,               \
+                     static_cast<const uint16_t*>(w2_slots), offsets, active, meta, row_idx,  \
+                     w, static_cast<const uint16_t*>(add), static_cast<uint16_t*>(out))
+  if (dnc <= 2) LMOE_DC(2, 4, true);
+  else if (dnc <= 3) LMOE_DC(3, 4, true);
+  else if (dnc <= 4) LMOE_DC(4, 4, true);
+  else if (dnc <= 8) LMOE_DC(8, 4, false);
+  else if (dnc <= 16) LMOE_DC(16, 2, false);
+  else return LMOE_ERR_SHAPE;
+#undef LMOE_DC
+  LMOE_RETURN_LAUNCH();
+}
+
 extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                                      const void* w13_slots, const void* w2_slots,
                                      int n_slots, const uint16_t* w,
@@ -437,6 +524,9 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
   if (H % 8 != 0 || I % 64 != 0 || I > 4096 || H > 8192) return LMOE_ERR_SHAPE;
   const int n_pairs = T * k;
   if (n_pairs > kFusedMaxPairs) return LMOE_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w13_slots) |
+       reinterpret_cast<uintptr_t>(w2_slots) | reinterpret_cast<uintptr_t>(act)) & 15u)
+    return LMOE_ERR_SHAPE;
   if (T == 0) return LMOE_OK;
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
   int st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
@@ -444,21 +534,8 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                               sorted_pairs, active, meta, max_active,
                               static_cast<uint16_t*>(act), stream);
   if (st != LMOE_OK) return st;
-  dim3 grid((H + 3) / 4);
-  const int nu = nu_for(I);
-#define LMOE_DC(NU)                                                             \
-  hipLaunchKernelGGL(down_combine_gemv_kernel<NU>, grid, dim3(256), 0, stream,  \
-                     static_cast<const uint16_t*>(act), I, H, T, k,              \
-                     static_cast<const uint16_t*>(w2_slots), offsets, active, meta, \
-                     row_idx, w, static_cast<const uint16_t*>(add),              \
-                     static_cast<uint16_t*>(out))
-  if (nu <= 3) LMOE_DC(3);
-  else if (nu <= 4) LMOE_DC(4);
-  else if (nu <= 8) LMOE_DC(8);
-  else if (nu <= 16) LMOE_DC(16);
-  else return LMOE_ERR_SHAPE;
-#undef LMOE_DC
-  LMOE_RETURN_LAUNCH();
+  return lmoe_down_combine(act, T, H, I, k, w2_slots, n_slots, w, offsets, row_idx, active, meta,
+                           add, out, stream);
 }
 
 extern "C" int lmoe_combine(const void* y, const int32_t* row_idx,

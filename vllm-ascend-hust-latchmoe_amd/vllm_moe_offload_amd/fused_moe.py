@@ -44,11 +44,9 @@ from vllm_moe_offload_amd.moe_offload.slot_mapping import PreparedSlotWeights
 @dataclass
 class MoEWorkspace:
     perm: native.Permutation
-    act: torch.Tensor   # [N, I] bf16 (sorted order; flat pair order in moe_decode)
+    act: torch.Tensor   # [N, I] bf16, sorted order
     y: torch.Tensor     # [N, H] bf16, flat pair order
     out: torch.Tensor   # [T, H] bf16
-    meta: torch.Tensor  # int32 [META_COUNT] of moe_decode
-    last_meta: torch.Tensor | None = None  # meta written by the last fused_experts call
 
 
 _WORKSPACES: dict[tuple, MoEWorkspace] = {}
@@ -64,7 +62,6 @@ def get_workspace(T: int, k: int, P: int, H: int, I: int, device, *, tag: str = 
             act=torch.empty((max(N, 1), I), dtype=torch.bfloat16, device=device),
             y=torch.empty((max(N, 1), H), dtype=torch.bfloat16, device=device),
             out=torch.empty((max(T, 1), H), dtype=torch.bfloat16, device=device),
-            meta=torch.zeros(native.META_COUNT, dtype=torch.int32, device=device),
         )
         _WORKSPACES[key] = ws
     return ws
@@ -134,22 +131,17 @@ def fused_experts(
 ) -> torch.Tensor:
     """out[t] = add[t] + sum_j w[t,j] * MLP_{slot(ids[t,j])}(x_t).
 
-    AUTO: up to 512 pairs run the decode body (remap and grouping inside the
-    gate_up and down+combine launches); more pairs permute and run the
-    grouped MFMA GEMM (or the GEMV kernels when path is GEMV) and combine."""
+    Permute, then: up to 1024 pairs (unless path is MFMA) the decode body
+    (gate_up GEMV, down GEMV fused with the combine); more pairs the grouped
+    GEMM (MFMA unless path is GEMV) and the combine."""
     T, H = hidden.shape
     k = int(topk_ids.shape[1])
     P = int(w13_slots.shape[0])
     I = int(w13_slots.shape[1]) // 2
     ws = workspace or get_workspace(T, k, P, H, I, hidden.device)
     dst = out if out is not None else ws.out[:T]
-    if path == native.LMOE_PATH_AUTO and 0 < T * k <= native.MOE_DECODE_MAX_PAIRS:
-        ws.last_meta = ws.meta
-        return native.moe_decode(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2phy, dst,
-                                 ws.act, ws.meta, add=add)
     native.permute(topk_ids, ws.perm, log2phy=log2phy)
-    ws.last_meta = ws.perm.meta
-    if T * k <= native.FUSED_DECODE_MAX_PAIRS and path == native.LMOE_PATH_GEMV:
+    if T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA:
         native.fused_moe_decode(hidden, topk_weights, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add)
     else:
         native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
@@ -159,7 +151,7 @@ def fused_experts(
 
 def check_placed(ws: MoEWorkspace) -> None:
     """Host validation (synchronising): fail if a pair mapped to no slot."""
-    meta = (ws.last_meta if ws.last_meta is not None else ws.perm.meta).cpu().tolist()
+    meta = ws.perm.meta.cpu().tolist()
     if meta[native.META_ERRORS]:
         raise RuntimeError(f"topk_ids contain experts without ready slots: {meta[native.META_ERRORS]} pairs")
 

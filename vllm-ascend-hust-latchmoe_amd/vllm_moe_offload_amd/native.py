@@ -28,7 +28,6 @@ META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
 META_COUNT = 4
 MFMA_BLOCK_M = 128
 FUSED_DECODE_MAX_PAIRS = 1024
-MOE_DECODE_MAX_PAIRS = 512
 
 EXPORTED_SYMBOLS = (
     "lmoe_status_string",
@@ -43,7 +42,7 @@ EXPORTED_SYMBOLS = (
     "lmoe_down",
     "lmoe_combine",
     "lmoe_fused_moe_decode",
-    "lmoe_moe_decode",
+    "lmoe_down_combine",
     "lmoe_stage_copy",
 )
 
@@ -80,10 +79,7 @@ _SIGNATURES = {
         _i,
         [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
-    "lmoe_moe_decode": (
-        _i,
-        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp],
-    ),
+    "lmoe_down_combine": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "lmoe_stage_copy": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
 }
 
@@ -475,53 +471,34 @@ def fused_moe_decode(
     return out
 
 
-def moe_decode(
-    x: torch.Tensor,
-    topk_weights: torch.Tensor,
-    topk_ids: torch.Tensor,
-    w13_slots: torch.Tensor,
-    w2_slots: torch.Tensor,
-    log2phy: torch.Tensor | None,
-    out: torch.Tensor,
+def down_combine(
     act: torch.Tensor,
-    meta: torch.Tensor,
+    topk_weights: torch.Tensor,
+    w2_slots: torch.Tensor,
+    perm: Permutation,
+    out: torch.Tensor,
     *,
     add: torch.Tensor | None = None,
-    table_len: int | None = None,
     stream=None,
 ) -> torch.Tensor:
-    """Decode layer body from the router output (gate_up launch, down +
-    combine launch): slot remap and grouping by slot inside both, each
-    expert's weights read once (T*k <= 512)."""
+    """Second half of fused_moe_decode: down GEMV fused with the combine."""
     lib = load_library()
-    _need(x, "x", torch.bfloat16)
-    T, H = x.shape
     _need(topk_weights, "topk_weights", torch.bfloat16)
-    _need(topk_ids, "topk_ids", torch.int32, tuple(topk_weights.shape))
-    k = int(topk_ids.shape[1])
-    P, I = _check_bank(w13_slots, w2_slots, H)
-    N = T * k
-    if N > MOE_DECODE_MAX_PAIRS:
-        raise ValueError(f"moe_decode supports at most {MOE_DECODE_MAX_PAIRS} pairs, got {N}")
-    n_table = 0
-    if log2phy is not None:
-        _need(log2phy, "log2phy", torch.int32)
-        n_table = int(log2phy.numel()) if table_len is None else min(int(table_len), int(log2phy.numel()))
+    T, k = topk_weights.shape
+    _need(w2_slots, "w2_slots", torch.bfloat16)
+    P, H, I = w2_slots.shape
+    if perm.n_pairs != T * k or perm.n_slots != P:
+        raise ValueError("permutation does not match the batch or the slot bank")
+    _need(act, "act", torch.bfloat16, (perm.n_pairs, I))
     _need(out, "out", torch.bfloat16, (T, H))
     if add is not None:
         _need(add, "add", torch.bfloat16, (T, H))
-    _need(act, "act", torch.bfloat16)
-    if act.dim() != 2 or act.shape[0] < N or act.shape[1] != I:
-        raise ValueError("act workspace is smaller than [T*k, I]")
-    _need(meta, "meta", torch.int32)
-    if meta.numel() < META_COUNT:
-        raise ValueError(f"meta needs {META_COUNT} int32")
     _check(
-        lib.lmoe_moe_decode(
-            _ptr(x), T, H, I, k, _ptr(topk_ids), _ptr(log2phy), n_table, _ptr(w13_slots), _ptr(w2_slots), P,
-            _ptr(topk_weights), _ptr(add), _ptr(out), _ptr(act), _ptr(meta), _stream(stream),
+        lib.lmoe_down_combine(
+            _ptr(act), T, H, I, k, _ptr(w2_slots), P, _ptr(topk_weights), _ptr(perm.offsets),
+            _ptr(perm.row_idx), _ptr(perm.active), _ptr(perm.meta), _ptr(add), _ptr(out), _stream(stream),
         ),
-        "lmoe_moe_decode",
+        "lmoe_down_combine",
     )
     return out
 
