@@ -164,21 +164,36 @@ __global__ __launch_bounds__(1024) void permute_small_kernel(
   for (int s = threadIdx.x; s < P; s += blockDim.x) hist[s] = 0;
   if (threadIdx.x == 0) err_lds = 0;
   __syncthreads();
-  const int p = threadIdx.x;
-  int s = -1;
-  if (p < N) {
-    s = map_pair(ids, p, log2phy, n_log2phy, P, skip);
-    if (s >= 0) atomicAdd(&hist[s], 1);
-    if (s == -2) atomicAdd(&err_lds, 1);
+  // each thread owns pairs threadIdx.x + c * blockDim.x, c < kSmallChunks
+  constexpr int kSmallChunks = kChunk / 64;
+  int sl[kSmallChunks];
+#pragma unroll
+  for (int c = 0; c < kSmallChunks; ++c) {
+    const int p = threadIdx.x + c * blockDim.x;
+    sl[c] = -1;
+    if (p < N) {
+      const int s = map_pair(ids, p, log2phy, n_log2phy, P, skip);
+      sl[c] = s;
+      if (s >= 0) atomicAdd(&hist[s], 1);
+      if (s == -2) atomicAdd(&err_lds, 1);
+    }
   }
   __syncthreads();
   scan_slots(hist, P, block_m, scan_lds, counts, offsets, active, tile_off, meta);
   if (threadIdx.x == 0) meta[LMOE_META_ERRORS] = err_lds;
   __syncthreads();  // hist now holds offsets: the running base of each slot
-  const int pos = chunk_positions(s >= 0 ? s : -1, key_bits(P), hist);
-  if (p < N) {
-    row_idx[p] = pos;
-    if (pos >= 0) sorted_pairs[pos] = p;
+  const int nb = key_bits(P);
+#pragma unroll
+  for (int c = 0; c < kSmallChunks; ++c) {
+    if (c * static_cast<int>(blockDim.x) < N) {  // uniform across the block
+      const int p = threadIdx.x + c * blockDim.x;
+      const int s = sl[c] >= 0 ? sl[c] : -1;
+      const int pos = chunk_positions(s, nb, hist);  // chunks in pair order: stable
+      if (p < N) {
+        row_idx[p] = pos;
+        if (pos >= 0) sorted_pairs[pos] = p;
+      }
+    }
   }
 }
 
@@ -299,7 +314,12 @@ extern "C" int lmoe_permute(const int32_t* ids, int n_pairs,
   const int skip = skip_unmapped ? 1 : 0;
   const size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
   if (n_pairs <= kChunk) {
-    hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(kChunk), lds, stream,
+    // one block; as few waves as the pairs and the slot scan need (block-wide
+    // barriers are the cost of this kernel, and they grow with the waves)
+    int threads = n_pairs > n_slots / 16 ? n_pairs : n_slots / 16;
+    threads = ((threads + 63) / 64) * 64;
+    threads = threads < 64 ? 64 : (threads > kChunk ? kChunk : threads);
+    hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(threads), lds, stream,
                        ids, n_pairs, log2phy, n_log2phy, n_slots, skip, block_m,
                        counts, offsets, sorted_pairs, row_idx, active, tile_off,
                        meta);

@@ -17,6 +17,7 @@ constexpr int kGateMaxChunks = 16;  // H <= 16 * 512 = 8192 in the GEMV path
 // logits[t][e] for e = 4*blockIdx.x + wave, tokens [t0, t1).  The expert row
 // stays in registers (one 16-byte chunk per 512 columns per lane) while the
 // token rows stream through L1.
+template <int NC>
 __global__ __launch_bounds__(256) void gate_gemv_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T,
     int H, int E, int tokens_per_block, void* __restrict__ logits,
@@ -29,9 +30,9 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
   const int t1 = min(T, t0 + tokens_per_block);
   const uint16_t* wrow = wg + static_cast<size_t>(e) * H;
 
-  uint4 w[kGateMaxChunks];
+  uint4 w[NC];
 #pragma unroll
-  for (int c = 0; c < kGateMaxChunks; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int h = c * 512 + lane * 8;
     w[c] = (h < H) ? *reinterpret_cast<const uint4*>(wrow + h)
                    : make_uint4(0u, 0u, 0u, 0u);
@@ -40,7 +41,7 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
     const uint16_t* xr = x + static_cast<size_t>(t) * H;
     float acc = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kGateMaxChunks; ++c) {
+    for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
       if (h < H) acc = dot8(*reinterpret_cast<const uint4*>(xr + h), w[c], acc);
     }
@@ -109,10 +110,15 @@ extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
   }
   const int tpb = 16;
   dim3 grid((E + 3) / 4, (T + tpb - 1) / tpb);
-  hipLaunchKernelGGL(gate_gemv_kernel, grid, dim3(256), 0, stream,
-                     static_cast<const uint16_t*>(x),
-                     static_cast<const uint16_t*>(wg), T, H, E, tpb, logits,
-                     logits_f32);
+  const int nc = (H + 511) / 512;
+#define LMOE_GATE(NC)                                                              \
+  hipLaunchKernelGGL(gate_gemv_kernel<NC>, grid, dim3(256), 0, stream,             \
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(wg), \
+                     T, H, E, tpb, logits, logits_f32)
+  if (nc <= 4) LMOE_GATE(4);
+  else if (nc <= 8) LMOE_GATE(8);
+  else LMOE_GATE(16);
+#undef LMOE_GATE
   LMOE_RETURN_LAUNCH();
 }
 

@@ -43,13 +43,15 @@ struct SelectParams {
   float routed_scale;
 };
 
-// Per-wave LDS scratch of one selection.
+// Per-wave LDS scratch of one selection.  Score/id pairs are interleaved so
+// one 16-byte LDS read returns two entries; the ranking loops are unrolled
+// so all their reads are in flight together (a rolled loop waits for each
+// read in turn: ~120 cycles x 64).
 struct SelectLds {
-  float lm_s[kWave];
-  int lm_e[kWave];
-  float c_s[kMaxE];  // candidate scores; also the score table of the groups
-  int c_e[kMaxE];
+  float2 lm[kWave];   // (score, id as float bits) of every lane maximum
+  float2 cand[kMaxE]; // (score, id bits) of the candidates
   float c_w[kMaxE];
+  float c_s[kMaxE];   // score table of the groups (grouped sigmoid)
   float gsc[kWave];
   float o_w[kMaxK];
   int o_e[kMaxK];
@@ -135,7 +137,22 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
       float gscore = -INFINITY;
       if (lane < ng) {
         float m1 = -INFINITY, m2 = -INFINITY;
-        for (int i = 0; i < gs; ++i) {
+        int i = 0;
+        for (; i + 4 <= gs; i += 4) {
+          float q[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) q[u] = L.c_s[lane * gs + i + u];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (q[u] > m1) {
+              m2 = m1;
+              m1 = q[u];
+            } else if (q[u] > m2) {
+              m2 = q[u];
+            }
+          }
+        }
+        for (; i < gs; ++i) {
           const float v = L.c_s[lane * gs + i];
           if (v > m1) {
             m2 = m1;
@@ -150,6 +167,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
       wave_lds_sync();
       // keep the topk_group best groups (ties to the lower group id)
       int r = 0;
+#pragma unroll 8
       for (int g = 0; g < ng; ++g) r += better(L.gsc[g], g, gscore, lane) ? 1 : 0;
       const uint64_t kept = __ballot(lane < ng && r < sp.topk_group);
 #pragma unroll
@@ -172,8 +190,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
       me = e;
     }
   }
-  L.lm_s[lane] = m;
-  L.lm_e[lane] = me;
+  L.lm[lane] = make_float2(m, __int_as_float(me));
   if (lane < kMaxK) {
     L.o_e[lane] = -1;
     L.o_w[lane] = 0.0f;
@@ -182,7 +199,15 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
   // 2. threshold: value of the lane maximum of rank k-1 (-inf if fewer than
   //    k lanes hold an eligible expert)
   int r = 0;
-  for (int l = 0; l < kWave; ++l) r += better(L.lm_s[l], L.lm_e[l], m, me) ? 1 : 0;
+  {
+    const float4* lm4 = reinterpret_cast<const float4*>(L.lm);
+#pragma unroll
+    for (int l = 0; l < kWave / 2; ++l) {
+      const float4 q = lm4[l];
+      r += better(q.x, __float_as_int(q.y), m, me) ? 1 : 0;
+      r += better(q.z, __float_as_int(q.w), m, me) ? 1 : 0;
+    }
+  }
   const uint64_t at = __ballot(me != 0x7fffffff && r == k - 1);
   const float thr = at ? __shfl(m, __ffsll(static_cast<long long>(at)) - 1, kWave)
                        : -INFINITY;
@@ -195,30 +220,56 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     const uint64_t bm = __ballot(c);
     if (c) {
       const int idx = C + __popcll(bm & lanemask_lt(lane));
-      L.c_s[idx] = sel[j];
-      L.c_e[idx] = e;
+      L.cand[idx] = make_float2(sel[j], __int_as_float(e));
       L.c_w[idx] = wgt[j];
     }
     C += __popcll(bm);
   }
+  // pad to a multiple of 8 with entries that beat nothing (C <= E <= kMaxE,
+  // a multiple of 8, so the padded range stays inside cand[])
+  const int C8 = (C + 7) >> 3;
+  if (lane < 8 && C + lane < C8 * 8) L.cand[C + lane] = make_float2(-INFINITY, __int_as_float(0x7fffffff));
   wave_lds_sync();
+  const float4* cand4 = reinterpret_cast<const float4*>(L.cand);
   for (int i0 = 0; i0 < C; i0 += kWave) {
     const int i = i0 + lane;
-    if (i < C) {
-      const float cs = L.c_s[i];
-      const int ce = L.c_e[i];
-      int rr = 0;
-      for (int i2 = 0; i2 < C; ++i2) rr += better(L.c_s[i2], L.c_e[i2], cs, ce) ? 1 : 0;
-      if (rr < k) {
-        L.o_e[rr] = ce;
-        L.o_w[rr] = L.c_w[i];
+    const float2 me2 = i < C ? L.cand[i] : make_float2(-INFINITY, __int_as_float(0x7fffffff));
+    const float cs = me2.x;
+    const int ce = __float_as_int(me2.y);
+    int rr = 0;
+    for (int b = 0; b < C8; ++b) {
+      float4 q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) q[u] = cand4[b * 4 + u];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        rr += better(q[u].x, __float_as_int(q[u].y), cs, ce) ? 1 : 0;
+        rr += better(q[u].z, __float_as_int(q[u].w), cs, ce) ? 1 : 0;
       }
+    }
+    if (i < C && rr < k) {
+      L.o_e[rr] = ce;
+      L.o_w[rr] = L.c_w[i];
     }
   }
   wave_lds_sync();
   // renormalise in selection order, scale
-  float sum = L.o_w[0];
-  for (int it = 1; it < k; ++it) sum = sum + L.o_w[it];
+  float ow[kMaxK];
+  {
+    const float4* o4 = reinterpret_cast<const float4*>(L.o_w);
+#pragma unroll
+    for (int u = 0; u < kMaxK / 4; ++u) {
+      const float4 q = o4[u];
+      ow[4 * u] = q.x;
+      ow[4 * u + 1] = q.y;
+      ow[4 * u + 2] = q.z;
+      ow[4 * u + 3] = q.w;
+    }
+  }
+  float sum = ow[0];
+#pragma unroll
+  for (int it = 1; it < kMaxK; ++it)
+    if (it < k) sum = sum + ow[it];
   const float denom = fmaxf(sum, FLT_EPSILON);
   out_e = -1;
   out_w = 0.0f;
