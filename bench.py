@@ -324,6 +324,13 @@ def bench_decode_roofline(model: DecodeModel, state, reps: int = 10) -> dict:
         res[name] = {"avg_launch_us": round(avg_us, 3), "bytes_per_launch": int(byts),
                      "achieved_gbs": round(byts / (avg_us * 1e-6) / 1e9, 1), "launches": reps * L}
     res["distinct_slots_per_launch"] = round(u, 2)
+    # calibration for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE: one device copy
+    # of exactly 64 MiB (read 64 MiB, write 64 MiB)
+    src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    res["calibration_copy_bytes"] = int(src.numel())
     return res
 
 
@@ -496,6 +503,7 @@ def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int =
         t0 = time.perf_counter()
         pend = [rt.prefetch_fixed_slot_plan(layer_id=l, active_experts=plan[l], num_logical_experts=E) for l in range(L)]
         host_issue_ms = (time.perf_counter() - t0) * 1000.0
+        first_misses = sum(len(p_.misses) for p_ in pend)
         engine.stream.synchronize()
         th_ms = (time.perf_counter() - t0) * 1000.0
         h2d_bytes = engine.bytes_issued - b0
@@ -503,7 +511,7 @@ def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int =
             rt.complete_fixed_slot_plan(pend[l])
         torch.cuda.synchronize()
         # (b) pipelined under per-layer graph replays
-        tb, nb, host_ms = [], 0, []
+        tb, nb, host_ms, miss_counts = [], 0, [], []
         for _ in range(steps):
             plan = plan_step(k)
             torch.cuda.synchronize()
@@ -511,7 +519,9 @@ def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int =
             t0 = time.perf_counter()
             load_ids(plan)
             pending = rt.prefetch_fixed_slot_plan(layer_id=0, active_experts=plan[0], num_logical_experts=E)
+            step_misses = 0
             for l in range(L):
+                step_misses += len(pending.misses)
                 rt.complete_fixed_slot_plan(pending)
                 nxt = None
                 if l + 1 < L:
@@ -520,6 +530,7 @@ def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int =
                 rt.record_layer_compute(l)
                 pending = nxt
             host_ms.append((time.perf_counter() - t0) * 1000.0)
+            miss_counts.append(step_misses)
             torch.cuda.synchronize()
             tb.append((time.perf_counter() - t0) * 1000.0)
             nb += engine.bytes_issued - b0
@@ -528,6 +539,7 @@ def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int =
         hidden = (tc_ms + th_ms - tb_ms) / max(1e-9, min(tc_ms, th_ms))
         out[f"k{k}"] = {
             "h2d_bytes_per_step": int(h2d_bytes),
+            "h2d_only_misses": int(first_misses),
             "h2d_only_ms": round(th_ms, 3),
             "h2d_gbs": round(h2d_bytes / (th_ms * 1e-3) / 1e9, 2),
             "host_issue_ms": round(host_issue_ms, 3),
@@ -535,6 +547,7 @@ def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int =
             "pipelined_host_ms": round(sum(host_ms) / len(host_ms), 3),
             "pipelined_h2d_gbs": round(nb / steps / (tb_ms * 1e-3) / 1e9, 2),
             "compute_hidden_frac": round(max(0.0, min(1.0, hidden)), 4),
+            "misses_per_step": sorted(set(miss_counts)),
             "steps": steps,
         }
     out["slot_addresses_stable_across_replays"] = True
@@ -668,7 +681,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256, help="timed decode steps per batch size")
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--batches", default="1,4,16,64")
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--slots", type=int, default=64)
