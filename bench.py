@@ -477,7 +477,9 @@ def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int =
             non = sorted(set(range(E)) - set(res))
             miss = list(rng.choice(non, size=k, replace=False))
             hit = list(rng.choice(res, size=K - k, replace=False)) if K - k > 0 else []
-            plan.append(tuple(int(e) for e in miss + hit))
+            # hits first: staging runs in list order (as the reference's), so a
+            # miss listed before a hit could evict that hit's slot
+            plan.append(tuple(int(e) for e in hit + miss))
         return plan
 
     def load_ids(plan):
