@@ -231,3 +231,52 @@ def test_fused_decode_unmapped_pairs_and_add_term():
     torch.cuda.synchronize()
     assert meta0[native.META_ACTIVE].item() == 0
     assert np.array_equal(from_dev_bf16(out0), add)
+
+
+@pytest.mark.parametrize("T,k,E,P,H,I,skip", [
+    (600, 8, 64, 64, 2048, 768, False),    # ~75 pairs/slot: one partial tile per slot
+    (2048, 8, 32, 32, 2048, 768, False),   # ~512 pairs/slot: full + partial tiles
+    (1024, 8, 64, 24, 2048, 768, True),    # a wave: pairs of unmapped ids skipped
+    (256, 8, 16, 16, 1000, 192, False),    # K = 1000 (not a multiple of 64): 128-row parts
+    (160, 8, 32, 16, 7168, 2048, True),    # DeepSeek-V3 expert shape
+])
+def test_mfma_tile_heights_agree_bitwise(T, k, E, P, H, I, skip):
+    """The 256-row direct-to-LDS kernel against the 128-row kernel: both sum
+    every output's K/16 MFMA steps in the same order, so act and y must agree
+    bit for bit; y is also held to the oracle's tolerance."""
+    native = _native()
+    print(f"case tile-heights T={T} k={k} E={E} P={P} H={H} I={I} skip={skip}", flush=True)
+    rng = np.random.default_rng(T + H + P)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    used = np.unique(ids)
+    l2p = np.full(E, -1, dtype=np.int32)
+    mapped = used if not skip else used[: P]
+    l2p[mapped] = rng.permutation(P)[: mapped.size]
+    x = normal_bf16(rng, (T, H), 1.0)
+    w13 = normal_bf16(rng, (P, 2 * I, H), 0.02)
+    w2 = normal_bf16(rng, (P, H, I), 0.02)
+    d_ids, d_l2p, d_x, d_w13, d_w2 = to_dev_i32(ids), to_dev_i32(l2p), to_dev_bf16(x), to_dev_bf16(w13), to_dev_bf16(w2)
+    outs = {}
+    for bm in (128, 256):
+        perm = native.Permutation.allocate(T * k, P, "cuda")
+        native.permute(d_ids, perm, log2phy=d_l2p, skip_unmapped=skip, block_m=bm)
+        act = torch.zeros((T * k, I), dtype=torch.bfloat16, device="cuda")
+        y = torch.zeros((T * k, H), dtype=torch.bfloat16, device="cuda")
+        native.grouped_mlp(d_x, k, d_w13, d_w2, perm, act, y, path=native.LMOE_PATH_MFMA)
+        torch.cuda.synchronize()
+        n_placed = int(perm.meta[native.META_PAIRS].item())
+        outs[bm] = (act[:n_placed].clone(), y.clone())
+    assert torch.equal(outs[128][0].view(torch.int16), outs[256][0].view(torch.int16))
+    assert torch.equal(outs[128][1].view(torch.int16), outs[256][1].view(torch.int16))
+    slot = operm.remap(ids, l2p, P, skip_unmapped=skip)
+    y_ref = omlp.grouped_mlp(x, slot, k, w13, w2)
+    placed = (slot.reshape(-1) >= 0)
+    got = bf16_to_f32(from_dev_bf16(outs[256][1]))[placed]
+    ref = y_ref[placed]
+    rms_y = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    frac, max_ulps = ulp_mismatch_stats(got, ref, abs_floor=rms_y / 256)
+    print(f"  y vs oracle: frac>1ulp {frac:.2e} max {max_ulps:.2f} ulp", flush=True)
+    # f32 summation-order noise grows with K (7168 for the DeepSeek shape vs
+    # <= 2048 elsewhere): more near-cancelling elements cross one ulp, while
+    # every element stays within 2 x (ulp + cancellation floor)
+    assert frac <= 1e-3 * max(1.0, H / 2048) and max_ulps <= 2.0

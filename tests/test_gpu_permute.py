@@ -33,6 +33,7 @@ def _check(perm, ref, n_pairs):
     assert meta[3] == ref.tile_off[-1]
 
 
+@pytest.mark.parametrize("block_m", [128, 256])
 @pytest.mark.parametrize("T,k,E,P,use_map", [
     (1, 8, 128, 64, True),
     (8, 8, 128, 32, False),
@@ -44,9 +45,9 @@ def _check(perm, ref, n_pairs):
     (2048, 8, 256, 256, False),
     (3, 1, 5, 3, True),
 ])
-def test_permute_matches_oracle(T, k, E, P, use_map):
+def test_permute_matches_oracle(T, k, E, P, use_map, block_m):
     native = _native()
-    print(f"case permute T={T} k={k} E={E} P={P} map={use_map}", flush=True)
+    print(f"case permute T={T} k={k} E={E} P={P} map={use_map} block_m={block_m}", flush=True)
     rng = np.random.default_rng(T * 31 + P)
     ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
     log2phy = None
@@ -55,8 +56,9 @@ def test_permute_matches_oracle(T, k, E, P, use_map):
         chosen = rng.permutation(E)[: min(P, E)]
         log2phy[chosen] = rng.permutation(P)[: chosen.size]
     perm = native.Permutation.allocate(T * k, P, "cuda")
-    native.permute(to_dev_i32(ids), perm, log2phy=None if log2phy is None else to_dev_i32(log2phy))
-    _check(perm, orc.init_routing(ids, P, log2phy=log2phy), T * k)
+    native.permute(to_dev_i32(ids), perm, log2phy=None if log2phy is None else to_dev_i32(log2phy),
+                   block_m=block_m)
+    _check(perm, orc.init_routing(ids, P, log2phy=log2phy, block_m=block_m), T * k)
 
 
 @pytest.mark.parametrize("N,P", [(64, 16), (5000, 40)])
@@ -70,7 +72,7 @@ def test_permute_skip_unmapped_wave_filter(N, P):
     log2phy[np.sort(wave)] = np.arange(P, dtype=np.int32)
     perm = native.Permutation.allocate(N, P, "cuda")
     native.permute(to_dev_i32(ids), perm, log2phy=to_dev_i32(log2phy), skip_unmapped=True)
-    ref = orc.init_routing(ids, P, log2phy=log2phy, skip_unmapped=True)
+    ref = orc.init_routing(ids, P, log2phy=log2phy, skip_unmapped=True, block_m=native.MFMA_BLOCK_M)
     assert ref.errors == 0
     _check(perm, ref, N)
 
@@ -81,7 +83,7 @@ def test_permute_counts_invalid_ids_as_errors():
     log2phy = np.array([0, 1, -1, 2], dtype=np.int32)
     perm = native.Permutation.allocate(6, 3, "cuda")
     native.permute(to_dev_i32(ids), perm, log2phy=to_dev_i32(log2phy))
-    ref = orc.init_routing(ids, 3, log2phy=log2phy)
+    ref = orc.init_routing(ids, 3, log2phy=log2phy, block_m=native.MFMA_BLOCK_M)
     assert ref.errors == 3  # expert 2 unstaged, id 9 and id -3 out of range
     _check(perm, ref, 6)
 
@@ -95,7 +97,7 @@ def test_gather_rows_is_expanded_x():
     perm = native.Permutation.allocate(T * k, E, "cuda")
     native.permute(to_dev_i32(ids), perm)
     out = native.gather_rows(to_dev_bf16(x), k, perm)
-    ref = orc.init_routing(ids, E)
+    ref = orc.init_routing(ids, E, block_m=native.MFMA_BLOCK_M)
     np.testing.assert_array_equal(from_dev_bf16(out), orc.expanded_x(x, ref, k))
 
 

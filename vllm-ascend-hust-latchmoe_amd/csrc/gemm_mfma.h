@@ -46,6 +46,7 @@ struct GemmArgs {
   const int32_t* meta;
   int P;
   int M_dense;            // dense: number of rows
+  int block_m;            // rows per tile of tile_off (a multiple of kBM); grouped modes
   void* out;
   int out_f32;            // dense only
 };
@@ -79,13 +80,16 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(GemmArgs g) {
     if (row0 >= g.M_dense) return;
     rows = min(kBM, g.M_dense - row0);
   } else {
+    // tile_off counts tiles of g.block_m rows; blockIdx.z picks the kBM-row
+    // part of the tile this workgroup computes
     const int tile = blockIdx.x;
     if (tile >= g.meta[LMOE_META_TILES]) return;
     slot = find_tile_slot(g.tile_off, g.P, tile);
     const int p0 = g.offsets[slot];
     const int n = g.offsets[slot + 1] - p0;
-    row0 = p0 + (tile - g.tile_off[slot]) * kBM;
+    row0 = p0 + (tile - g.tile_off[slot]) * g.block_m + blockIdx.z * kBM;
     rows = min(kBM, p0 + n - row0);
+    if (rows <= 0) return;
   }
   const int n0 = blockIdx.y * (MODE == kGateUp ? kBN / 2 : kBN);
 

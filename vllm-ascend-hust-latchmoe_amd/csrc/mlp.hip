@@ -16,7 +16,7 @@
 // w1/w2 = slot bank (PreparedSlotWeights, slot_mapping.py:143-187), then
 // npu_moe_token_unpermute (:3363-3366; out[t] = sum_j w[t,j] y[row(t,j)],
 // phase_split.py:1649-1656).
-#include "gemm_mfma.h"
+#include "gemm_lds.h"
 
 namespace lmoe {
 
@@ -348,6 +348,37 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
 
 static int nu_for(int I) { return (I + 255) / 256; }
 
+// ---------------------------------------------------------------------------
+// grouped MFMA GEMM launch (prefill).  block_m is the tile height the
+// permutation's tile table was built with: 256 runs the direct-to-LDS
+// 256 x 256 kernel (K a multiple of 64, 16-byte aligned operands), else the
+// 128 x 128 register-staged kernel over kBM-row parts of each tile.
+// ---------------------------------------------------------------------------
+using PrefillTile = LdsTile<256, 256, 2, 4, 2>;
+
+template <int MODE>
+static int launch_grouped_mfma(GemmArgs g, int n_pairs, int max_active, int block_m,
+                               hipStream_t stream) {
+  if (block_m != PrefillTile::BM && block_m != kBM) return LMOE_ERR_UNSUPPORTED;
+  const int ub_tiles = n_pairs / block_m + max_active + 1;
+  g.block_m = block_m;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.w) |
+                         reinterpret_cast<uintptr_t>(g.out)) & 15u) == 0;
+  if (!aligned) return LMOE_ERR_SHAPE;
+  if (block_m == PrefillTile::BM && g.K % PrefillTile::BK == 0 && g.N % 8 == 0) {
+    const int col_tile = (MODE == kGateUp) ? PrefillTile::BN / 2 : PrefillTile::BN;
+    const int grid = lds_gemm_grid(ub_tiles, (g.N + col_tile - 1) / col_tile);
+    hipLaunchKernelGGL((grouped_gemm_lds_kernel<MODE, PrefillTile>), dim3(grid),
+                       dim3(PrefillTile::THREADS), 0, stream, g);
+    return LMOE_OK;
+  }
+  const int col_tile = (MODE == kGateUp) ? kBN / 2 : kBN;
+  hipLaunchKernelGGL(grouped_gemm_kernel<MODE>,
+                     dim3(ub_tiles, (g.N + col_tile - 1) / col_tile, block_m / kBM), dim3(256),
+                     0, stream, g);
+  return LMOE_OK;
+}
+
 }  // namespace lmoe
 
 using namespace lmoe;
@@ -388,7 +419,6 @@ extern "C" int lmoe_gateup_silu(const void* x, int T, int H, int I, int k,
   }
   if (path != LMOE_PATH_MFMA) return LMOE_ERR_UNSUPPORTED;
   if (tile_off == nullptr) return LMOE_ERR_ARG;
-  if (block_m != kBM) return LMOE_ERR_UNSUPPORTED;
   GemmArgs g{};
   g.topk = k;
   g.offsets = offsets;
@@ -403,9 +433,8 @@ extern "C" int lmoe_gateup_silu(const void* x, int T, int H, int I, int k,
   g.K = H;
   g.I = I;
   g.out = act;
-  const int ub_tiles = n_pairs / kBM + max_active + 1;
-  hipLaunchKernelGGL(grouped_gemm_kernel<kGateUp>, dim3(ub_tiles, (I + 63) / 64), dim3(256), 0,
-                     stream, g);
+  st = launch_grouped_mfma<kGateUp>(g, n_pairs, max_active, block_m, stream);
+  if (st != LMOE_OK) return st;
   LMOE_RETURN_LAUNCH();
 }
 
@@ -441,7 +470,6 @@ extern "C" int lmoe_down(const void* act, int H, int I, const void* w2_slots, in
   }
   if (path != LMOE_PATH_MFMA) return LMOE_ERR_UNSUPPORTED;
   if (tile_off == nullptr) return LMOE_ERR_ARG;
-  if (block_m != kBM) return LMOE_ERR_UNSUPPORTED;
   GemmArgs g{};
   g.topk = 1;
   g.offsets = offsets;
@@ -455,9 +483,8 @@ extern "C" int lmoe_down(const void* act, int H, int I, const void* w2_slots, in
   g.N = H;
   g.K = I;
   g.out = yb;
-  const int ub_tiles = n_pairs / kBM + max_active + 1;
-  hipLaunchKernelGGL(grouped_gemm_kernel<kDown>, dim3(ub_tiles, (H + 127) / 128), dim3(256), 0,
-                     stream, g);
+  st = launch_grouped_mfma<kDown>(g, n_pairs, max_active, block_m, stream);
+  if (st != LMOE_OK) return st;
   LMOE_RETURN_LAUNCH();
 }
 

@@ -26,7 +26,7 @@ LMOE_PATH_GEMV = 1
 LMOE_PATH_MFMA = 2
 META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
 META_COUNT = 4
-MFMA_BLOCK_M = 128
+MFMA_BLOCK_M = 256  # row-tile height of the prefill MFMA GEMM (tile table of lmoe_permute)
 FUSED_DECODE_MAX_PAIRS = 1024
 
 EXPORTED_SYMBOLS = (
@@ -235,6 +235,7 @@ class Permutation:
     tile_off: torch.Tensor      # [P+1] i32 MFMA tile prefix
     meta: torch.Tensor          # [4] i32
     workspace: torch.Tensor     # int8 scratch for the multi-block path
+    block_m: int = MFMA_BLOCK_M  # tile height tile_off was last built with
 
     @classmethod
     def allocate(cls, n_pairs: int, n_slots: int, device) -> "Permutation":
@@ -288,6 +289,7 @@ def permute(
         ),
         "lmoe_permute",
     )
+    perm.block_m = int(block_m)
     return perm
 
 
@@ -352,7 +354,7 @@ def grouped_mlp(
         lib.lmoe_grouped_mlp(
             _ptr(x), T, H, I, int(top_k), _ptr(w13_slots), _ptr(w2_slots), P,
             _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.active), _ptr(perm.tile_off),
-            _ptr(perm.meta), perm.n_pairs, MFMA_BLOCK_M, int(path), _ptr(act), _ptr(y),
+            _ptr(perm.meta), perm.n_pairs, perm.block_m, int(path), _ptr(act), _ptr(y),
             _stream(stream),
         ),
         "lmoe_grouped_mlp",
@@ -375,7 +377,7 @@ def gateup_silu(x: torch.Tensor, top_k: int, w13_slots: torch.Tensor, perm: Perm
     _check(
         lib.lmoe_gateup_silu(
             _ptr(x), T, H, I, int(top_k), _ptr(w13_slots), P, _ptr(perm.offsets), _ptr(perm.sorted_pairs),
-            _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta), perm.n_pairs, MFMA_BLOCK_M, int(path),
+            _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta), perm.n_pairs, perm.block_m, int(path),
             _ptr(act), _stream(stream),
         ),
         "lmoe_gateup_silu",
@@ -396,7 +398,7 @@ def down(act: torch.Tensor, w2_slots: torch.Tensor, perm: Permutation, y: torch.
     _check(
         lib.lmoe_down(
             _ptr(act), H, I, _ptr(w2_slots), P, _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.active),
-            _ptr(perm.tile_off), _ptr(perm.meta), perm.n_pairs, MFMA_BLOCK_M, int(path), _ptr(y), _stream(stream),
+            _ptr(perm.tile_off), _ptr(perm.meta), perm.n_pairs, perm.block_m, int(path), _ptr(y), _stream(stream),
         ),
         "lmoe_down",
     )
