@@ -266,10 +266,10 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
         for (int q = 0; q < 4; ++q) {
           uint32_t lo, hi;
           if (MODE == kGateUp) {
-            lo = static_cast<uint32_t>(swiglu_bf16(acc[i][j][4 * q + 0], acc[i][j + JO][4 * q + 0])) |
-                 (static_cast<uint32_t>(swiglu_bf16(acc[i][j][4 * q + 1], acc[i][j + JO][4 * q + 1])) << 16);
-            hi = static_cast<uint32_t>(swiglu_bf16(acc[i][j][4 * q + 2], acc[i][j + JO][4 * q + 2])) |
-                 (static_cast<uint32_t>(swiglu_bf16(acc[i][j][4 * q + 3], acc[i][j + JO][4 * q + 3])) << 16);
+            lo = swiglu_bf16x2(acc[i][j][4 * q + 0], acc[i][j + JO][4 * q + 0],
+                               acc[i][j][4 * q + 1], acc[i][j + JO][4 * q + 1]);
+            hi = swiglu_bf16x2(acc[i][j][4 * q + 2], acc[i][j + JO][4 * q + 2],
+                               acc[i][j][4 * q + 3], acc[i][j + JO][4 * q + 3]);
           } else {
             lo = pack_bf16x2(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1]);
             hi = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);

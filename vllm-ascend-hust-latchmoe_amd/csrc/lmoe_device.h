@@ -39,8 +39,13 @@ __device__ __forceinline__ float round_bf16(float f) {
 // SwiGLU with the reference's op boundaries: gate and up leave GMM1 as bf16,
 // the activation is formed in f32 and leaves as bf16 (returned as bits).
 __device__ __forceinline__ uint16_t swiglu_bf16(float gate_acc, float up_acc);
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// Two f32 -> packed bf16 pair (lo in bits 0..15), round to nearest even: one
+// v_cvt_pk_bf16_f32 on gfx950 (same bits as f32_to_bf16_bits for every
+// non-NaN input; NaNs stay NaN).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // dot of 8 bf16 pairs held in two uint4, accumulated into acc in element order
@@ -163,15 +168,25 @@ __device__ __forceinline__ float sigmoid_det(float x) {
 }
 
 __device__ __forceinline__ float silu_f32(float g) {
-  // silu(g) = g / (1 + exp(-g)); plain device expf is fine here (FP path
-  // checked against tolerance, not bit-exactly).
-  return g / (1.0f + __expf(-g));
+  // silu(g) = g / (1 + exp(-g)) with the hardware exp and reciprocal (a
+  // floating-point path checked against tolerance, not bit-exactly)
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+
+// act = silu(gate) * up at the reference's op boundaries: gate and up leave
+// GMM1 as bf16, the product is formed in f32 and leaves as bf16.  Two
+// outputs per call (packed, lo first): the bf16 roundings are paired
+// v_cvt_pk_bf16_f32 instructions.
+__device__ __forceinline__ uint32_t swiglu_bf16x2(float g0, float u0, float g1, float u1) {
+  const uint32_t gp = pack_bf16x2(g0, g1);
+  const uint32_t up = pack_bf16x2(u0, u1);
+  const float gr0 = bf16lo(gp), gr1 = bf16hi(gp);
+  const float ur0 = bf16lo(up), ur1 = bf16hi(up);
+  return pack_bf16x2(silu_f32(gr0) * ur0, silu_f32(gr1) * ur1);
 }
 
 __device__ __forceinline__ uint16_t swiglu_bf16(float gate_acc, float up_acc) {
-  const float g = round_bf16(gate_acc);
-  const float u = round_bf16(up_acc);
-  return static_cast<uint16_t>(f32_to_bf16_bits(silu_f32(g) * u));
+  return static_cast<uint16_t>(swiglu_bf16x2(gate_acc, up_acc, 0.0f, 0.0f) & 0xffffu);
 }
 
 }  // namespace lmoe
