@@ -150,10 +150,12 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
     ws = fused_moe.get_workspace(B, K, P, H, I, dev, tag=f"bench{B}")
 
     def compute_layer(l):
-        _route(static_x, model, l, ws_w[l], ws_ids[l], logits[l])
+        # the slot table is final (staged from the eager routing of this
+        # step), so selection and permutation run as one launch
         bank = model.bank(l)
-        fused_moe.fused_experts(static_x, ws_w[l], ws_ids[l], bank.w13_slots, bank.w2_slots,
-                                rt.log2phy_buffer(l), out=outs[l], workspace=ws)
+        fused_moe.decode_layer(static_x, model.gates[l], model.specs[l], bank.w13_slots, bank.w2_slots,
+                               rt.log2phy_buffer(l), workspace=ws, out=outs[l], logits_out=logits[l],
+                               w_out=ws_w[l], ids_out=ws_ids[l])
 
     def compute_all():
         for l in range(L):

@@ -24,6 +24,8 @@
  *   lmoe_router_gate   gate(hidden) in ops/fused_moe/moe_router_op.py:228-231
  *   lmoe_router_topk   select_experts (moe_router_op.py:108-124) with the
  *                      renorm contract of patches/patch_fused_moe.py:597-632
+ *   lmoe_router_topk_permute  select_experts then remap + init routing in
+ *                      one launch (decode with a final slot table)
  *   lmoe_permute       log2phy remap moe_offload/slot_mapping.py:116-140 and
  *                      npu_moe_init_routing_v2, patch_fused_moe.py:668-701
  *                      (stable sort by slot, expanded_row_idx, count histogram)
@@ -99,6 +101,25 @@ int lmoe_router_topk(const void* logits, int logits_f32, int T, int E, int k,
                      int topk_group, int renorm, float routed_scale,
                      float* w_f32, uint16_t* w_bf16, int32_t* ids,
                      hipStream_t stream);
+
+/* lmoe_router_topk followed by lmoe_permute (same arguments, same outputs,
+ * bit for bit) in one launch, for a slot table that is final before the
+ * router runs: the decode replay after staging, where the reference calls
+ * select_experts (moe_router_op.py:108-124) and then remap + init routing
+ * (slot_mapping.py:116-140, patch_fused_moe.py:668-701) back to back.
+ * Returns LMOE_ERR_SHAPE when T > 16, E > 256 or n_slots > 8192 (then use
+ * the two calls). */
+int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
+                             int k, int scoring, const float* bias,
+                             int n_group, int topk_group, int renorm,
+                             float routed_scale, float* w_f32,
+                             uint16_t* w_bf16, int32_t* ids,
+                             const int32_t* log2phy, int n_log2phy,
+                             int n_slots, int skip_unmapped, int block_m,
+                             int32_t* counts, int32_t* offsets,
+                             int32_t* sorted_pairs, int32_t* row_idx,
+                             int32_t* active, int32_t* tile_off,
+                             int32_t* meta, hipStream_t stream);
 
 /* Bytes of device workspace lmoe_permute needs for n_pairs pairs, n_slots. */
 size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);

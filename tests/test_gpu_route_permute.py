@@ -1,0 +1,155 @@
+"""GPU parity of the one-launch selection + permutation (lmoe_router_topk_permute)
+and of the decode layer built on it.
+
+Everything here is integer or bit-exact: the ids, bf16 and f32 weights
+against oracle.router, the permutation against oracle.permute, and the
+decode layer against route() + fused_experts() on the same GPU.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import permute as operm
+from oracle import router as orc
+from oracle.bf16 import bf16_to_f32, f32_to_bf16, normal_bf16
+from tests._util import from_dev_bf16, to_dev_bf16, to_dev_i32
+
+pytestmark = pytest.mark.gpu
+
+
+def _native():
+    from vllm_moe_offload_amd import native
+
+    return native
+
+
+def _tied_logits(rng, T, E, step=0.25):
+    v = np.round(rng.standard_normal((T, E)) / step) * step
+    return f32_to_bf16(v.astype(np.float32))
+
+
+def _check_perm(native, perm, ref, n_pairs):
+    np.testing.assert_array_equal(perm.counts.cpu().numpy(), ref.counts)
+    np.testing.assert_array_equal(perm.offsets.cpu().numpy(), ref.offsets)
+    np.testing.assert_array_equal(perm.sorted_pairs.cpu().numpy()[: ref.placed], ref.sorted_pairs)
+    np.testing.assert_array_equal(perm.row_idx.cpu().numpy()[:n_pairs], ref.row_idx)
+    np.testing.assert_array_equal(perm.active.cpu().numpy()[: ref.active.size], ref.active)
+    np.testing.assert_array_equal(perm.tile_off.cpu().numpy(), ref.tile_off)
+    meta = perm.meta.cpu().numpy()
+    assert list(meta) == [ref.active.size, ref.placed, ref.errors, ref.tile_off[-1]]
+
+
+@pytest.mark.parametrize("T,E,k,P,skip", [
+    (1, 128, 8, 64, False),
+    (4, 128, 8, 64, False),
+    (16, 128, 8, 64, False),
+    (16, 128, 8, 32, True),    # a wave table: ids outside it are left to another pass
+    (17, 128, 8, 128, False),  # past the one-block limit: the two-launch path
+    (3, 60, 4, 16, False),
+])
+def test_softmax_select_and_permute_bit_exact(T, E, k, P, skip):
+    native = _native()
+    print(f"case topk-permute softmax T={T} E={E} k={k} P={P} skip={skip}", flush=True)
+    rng = np.random.default_rng(500 + T * 13 + P)
+    bits = _tied_logits(rng, T, E)
+    bias = (rng.standard_normal(E) * 0.7).astype(np.float32)
+    r_ids, r_w, r_wb = orc.softmax_topk(bf16_to_f32(bits), k, bias=bias)
+    # slot table: every selected expert mapped (skip: only a subset)
+    used = np.unique(r_ids)
+    l2p = np.full(E, -1, dtype=np.int32)
+    chosen = used[: P] if not skip else used[: min(P, max(1, used.size // 2))]
+    l2p[chosen] = rng.permutation(P)[: chosen.size]
+    perm = native.Permutation.allocate(T * k, P, "cuda")
+    w_f32 = torch.empty((T, k), dtype=torch.float32, device="cuda")
+    w, ids, _ = native.router_topk_permute(
+        to_dev_bf16(bits), k, perm, log2phy=to_dev_i32(l2p), skip_unmapped=skip,
+        bias=torch.from_numpy(bias).cuda(), w_f32=w_f32,
+    )
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
+    np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
+    np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
+    ref = operm.init_routing(r_ids, P, log2phy=l2p, skip_unmapped=skip, block_m=native.MFMA_BLOCK_M)
+    _check_perm(native, perm, ref, T * k)
+    assert perm.block_m == native.MFMA_BLOCK_M
+
+
+@pytest.mark.parametrize("T", [1, 8, 16])
+def test_grouped_sigmoid_select_and_permute_bit_exact(T):
+    native = _native()
+    E, G, TG, k, P, scale = 256, 8, 4, 8, 128, 2.5  # P covers the <= 128 selected experts
+    print(f"case topk-permute sigmoid T={T}", flush=True)
+    rng = np.random.default_rng(900 + T)
+    bits = _tied_logits(rng, T, E, step=0.125)
+    bias = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    r_ids, r_w, r_wb = orc.grouped_sigmoid_topk(bf16_to_f32(bits), k, bias=bias, n_group=G, topk_group=TG,
+                                                scale=scale)
+    used = np.unique(r_ids)
+    l2p = np.full(E, -1, dtype=np.int32)
+    l2p[used] = rng.permutation(P)[: used.size]
+    perm = native.Permutation.allocate(T * k, P, "cuda")
+    w, ids, _ = native.router_topk_permute(
+        to_dev_bf16(bits), k, perm, log2phy=to_dev_i32(l2p), scoring="sigmoid",
+        bias=torch.from_numpy(bias).cuda(), num_expert_group=G, topk_group=TG,
+        routed_scaling_factor=scale,
+    )
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
+    np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
+    _check_perm(native, perm, operm.init_routing(r_ids, P, log2phy=l2p, block_m=native.MFMA_BLOCK_M), T * k)
+
+
+def test_unmapped_selection_counts_as_error():
+    """An id the table does not map (outside wave mode) is an error pair."""
+    native = _native()
+    T, E, k, P = 2, 64, 4, 8
+    rng = np.random.default_rng(3)
+    bits = _tied_logits(rng, T, E)
+    r_ids, _, _ = orc.softmax_topk(bf16_to_f32(bits), k)
+    l2p = np.full(E, -1, dtype=np.int32)
+    l2p[np.unique(r_ids)[:-1]] = np.arange(np.unique(r_ids).size - 1) % P
+    perm = native.Permutation.allocate(T * k, P, "cuda")
+    native.router_topk_permute(to_dev_bf16(bits), k, perm, log2phy=to_dev_i32(l2p))
+    torch.cuda.synchronize()
+    ref = operm.init_routing(r_ids, P, log2phy=l2p, block_m=native.MFMA_BLOCK_M)
+    assert ref.errors > 0
+    _check_perm(native, perm, ref, T * k)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16])
+def test_decode_layer_equals_route_then_fused_experts(T):
+    from vllm_moe_offload_amd import fused_moe
+    from vllm_moe_offload_amd.fused_moe import RouterSpec
+
+    native = _native()
+    H, I, E, k = 2048, 768, 128, 8
+    P = 64 if T <= 4 else 128  # enough slots for every selected expert
+    print(f"case decode-layer T={T}", flush=True)
+    rng = np.random.default_rng(40 + T)
+    x = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
+    gate = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
+    bias = torch.from_numpy((rng.standard_normal(E) * 0.5).astype(np.float32)).cuda()
+    spec = RouterSpec(top_k=k, e_score_correction_bias=bias)
+    w13 = to_dev_bf16(normal_bf16(rng, (P, 2 * I, H), 0.02))
+    w2 = to_dev_bf16(normal_bf16(rng, (P, H, I), 0.02))
+    # the table: route once to learn the experts, map them to slots
+    w0, ids0, _ = fused_moe.route(x, gate, spec)
+    torch.cuda.synchronize()
+    used = np.unique(ids0.cpu().numpy())
+    l2p = np.full(E, -1, dtype=np.int32)
+    l2p[used] = rng.permutation(P)[: used.size]
+    d_l2p = to_dev_i32(l2p)
+    ws_a = fused_moe.get_workspace(T, k, P, H, I, "cuda", tag="t-sep")
+    ws_b = fused_moe.get_workspace(T, k, P, H, I, "cuda", tag="t-fused")
+    w1, ids1, _ = fused_moe.route(x, gate, spec)
+    out1 = fused_moe.fused_experts(x, w1, ids1, w13, w2, d_l2p, workspace=ws_a).clone()
+    out2, w2_, ids2 = fused_moe.decode_layer(x, gate, spec, w13, w2, d_l2p, workspace=ws_b)
+    torch.cuda.synchronize()
+    assert torch.equal(ids1, ids2)
+    assert torch.equal(w1.view(torch.int16), w2_.view(torch.int16))
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    for name in ("counts", "offsets", "sorted_pairs", "row_idx", "active", "tile_off", "meta"):
+        a, b = getattr(ws_a.perm, name), getattr(ws_b.perm, name)
+        n = T * k if name in ("sorted_pairs", "row_idx") else a.numel()
+        assert torch.equal(a[:n], b[:n]), name

@@ -1,0 +1,202 @@
+// Permutation building blocks shared by the permutation kernels and the
+// fused decode router: token->slot remap through log2phy, count histogram per
+// physical slot, stable counting sort of the flat (token, k) pairs by slot,
+// active-slot list and the MFMA tile table.
+//
+// Reference behaviour: ExpertSlotMapping.remap_topk_ids
+// (moe_offload/slot_mapping.py:116-140, phys = log2phy[ids], fail closed on
+// -1) feeding npu_moe_init_routing_v2 (patches/patch_fused_moe.py:668-701:
+// stable sort by expert, expanded_row_idx, count-type histogram).  The wave
+// filter (skip_unmapped) plays the role of the per-wave expert table of
+// phase_split.build_b2_device_wave_microbatch_plans (:1224-1384).
+//
+// Integer work only; every output is bit-exact and independent of launch
+// shape.  Pairs of one chunk (1024 pairs) are ranked with wave64 ballots.
+#pragma once
+
+#include "lmoe_device.h"
+
+namespace lmoe {
+
+constexpr int kChunk = 1024;       // pairs per block
+constexpr int kMaxSlots = 8192;    // LDS histogram bound
+
+// slot of pair p: >= 0 placed, -1 skipped silently, -2 error
+__device__ __forceinline__ int map_pair(const int32_t* ids, int p,
+                                        const int32_t* __restrict__ log2phy,
+                                        int n_log2phy, int P, int skip) {
+  const int id = ids[p];
+  int s;
+  if (log2phy != nullptr) {
+    // in wave mode an id the table does not cover belongs to another pass
+    if (id < 0 || id >= n_log2phy) return skip ? -1 : -2;
+    s = log2phy[id];
+  } else {
+    s = id;
+  }
+  if (s >= 0 && s < P) return s;
+  if (skip && s == -1) return -1;
+  return -2;
+}
+
+__device__ __forceinline__ uint64_t match_key(int key, int nbits) {
+  uint64_t m = __ballot(1);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (key >> b) & 1;
+    const uint64_t bb = __ballot(bit);
+    m &= bit ? bb : ~bb;
+  }
+  return m;
+}
+
+// Exclusive scan over a block of 1024 threads.  Returns the exclusive prefix
+// of v; *total receives the block sum.  Uses scan_lds[32].
+__device__ int block_exclusive_scan(int v, int* scan_lds, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) scan_lds[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < nw; ++w) {
+      const int c = scan_lds[w];
+      scan_lds[w] = run;
+      run += c;
+    }
+    scan_lds[nw] = run;
+  }
+  __syncthreads();
+  const int excl = scan_lds[wave] + inc - v;
+  *total = scan_lds[nw];
+  __syncthreads();
+  return excl;
+}
+
+// Scan counts[0..P) held in LDS (hist) into offsets/active/tile_off; writes
+// counts, offsets, active, tile_off and meta[ACTIVE, PAIRS, TILES], and
+// replaces hist[s] by offsets[s] in place (each s is owned by one thread).
+__device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
+                           int32_t* counts, int32_t* offsets, int32_t* active,
+                           int32_t* tile_off, int32_t* meta) {
+  const int per = (P + blockDim.x - 1) / blockDim.x;
+  const int s0 = threadIdx.x * per;
+  int csum = 0, asum = 0, tsum = 0;
+  for (int i = 0; i < per; ++i) {
+    const int s = s0 + i;
+    if (s < P) {
+      const int c = hist[s];
+      csum += c;
+      asum += c > 0;
+      tsum += (c + block_m - 1) / block_m;
+    }
+  }
+  int ctot, atot, ttot;
+  int cpre = block_exclusive_scan(csum, scan_lds, &ctot);
+  int apre = block_exclusive_scan(asum, scan_lds, &atot);
+  int tpre = block_exclusive_scan(tsum, scan_lds, &ttot);
+  for (int i = 0; i < per; ++i) {
+    const int s = s0 + i;
+    if (s < P) {
+      const int c = hist[s];
+      counts[s] = c;
+      offsets[s] = cpre;
+      tile_off[s] = tpre;
+      if (c > 0) active[apre++] = s;
+      hist[s] = cpre;
+      cpre += c;
+      tpre += (c + block_m - 1) / block_m;
+    }
+  }
+  if (threadIdx.x == 0) {
+    offsets[P] = ctot;
+    tile_off[P] = ttot;
+    meta[LMOE_META_ACTIVE] = atot;
+    meta[LMOE_META_PAIRS] = ctot;
+    meta[LMOE_META_TILES] = ttot;
+  }
+}
+
+// Stable ranks of one chunk.  slot[] is this thread's slot (>= 0 placed),
+// run_base[s] holds the next free position of slot s and is advanced.
+__device__ int chunk_positions(int s, int nbits, int* run_base) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const bool placed = s >= 0;
+  const int key = placed ? s : (1 << nbits) - 1;
+  const uint64_t m = match_key(key, nbits);
+  const int rank = __popcll(m & lanemask_lt(lane));
+  const int cnt = __popcll(m);
+  const bool last = lane == 63 - __clzll(m);
+  int pos = -1;
+  for (int w = 0; w < nw; ++w) {
+    if (wave == w && placed) {
+      const int b = run_base[s];
+      pos = b + rank;
+      if (last) run_base[s] = b + cnt;
+    }
+    __syncthreads();
+  }
+  return pos;
+}
+
+__device__ __forceinline__ int key_bits(int P) {
+  // keys 0..P (P = "not placed" sentinel fits when (1<<nbits)-1 >= P)
+  int nbits = 1;
+  while ((1 << nbits) - 1 < P) ++nbits;
+  return nbits;
+}
+
+// Whole permutation of N <= kChunk pairs by one block.  ids may live in
+// global memory or LDS; hist is LDS of P ints, scan_lds 33 ints, err_lds one.
+// Thread i owns pairs i + c * blockDim.x.
+__device__ __forceinline__ void permute_block(
+    const int32_t* ids, int N, const int32_t* __restrict__ log2phy,
+    int n_log2phy, int P, int skip, int block_m, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
+    int32_t* __restrict__ row_idx, int32_t* __restrict__ active,
+    int32_t* __restrict__ tile_off, int32_t* __restrict__ meta, int* hist,
+    int* scan_lds, int* err_lds) {
+  for (int s = threadIdx.x; s < P; s += blockDim.x) hist[s] = 0;
+  if (threadIdx.x == 0) *err_lds = 0;
+  __syncthreads();
+  constexpr int kSmallChunks = kChunk / 64;
+  int sl[kSmallChunks];
+#pragma unroll
+  for (int c = 0; c < kSmallChunks; ++c) {
+    const int p = threadIdx.x + c * blockDim.x;
+    sl[c] = -1;
+    if (p < N) {
+      const int s = map_pair(ids, p, log2phy, n_log2phy, P, skip);
+      sl[c] = s;
+      if (s >= 0) atomicAdd(&hist[s], 1);
+      if (s == -2) atomicAdd(err_lds, 1);
+    }
+  }
+  __syncthreads();
+  scan_slots(hist, P, block_m, scan_lds, counts, offsets, active, tile_off, meta);
+  if (threadIdx.x == 0) meta[LMOE_META_ERRORS] = *err_lds;
+  __syncthreads();  // hist now holds offsets: the running base of each slot
+  const int nb = key_bits(P);
+#pragma unroll
+  for (int c = 0; c < kSmallChunks; ++c) {
+    if (c * static_cast<int>(blockDim.x) < N) {  // uniform across the block
+      const int p = threadIdx.x + c * blockDim.x;
+      const int s = sl[c] >= 0 ? sl[c] : -1;
+      const int pos = chunk_positions(s, nb, hist);  // chunks in pair order: stable
+      if (p < N) {
+        row_idx[p] = pos;
+        if (pos >= 0) sorted_pairs[pos] = p;
+      }
+    }
+  }
+}
+
+}  // namespace lmoe

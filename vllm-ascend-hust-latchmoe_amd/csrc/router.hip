@@ -8,6 +8,7 @@
 // DeepSeek-V3-style layer (bias for selection only, sum of the two best scores
 // per group, keep topk_group groups, renormalise, then scale).
 #include "gemm_mfma.h"
+#include "permute.h"
 #include "select.h"
 
 namespace lmoe {
@@ -64,7 +65,7 @@ __global__ __launch_bounds__(256) void topk_kernel(
     const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16,
     int32_t* __restrict__ ids) {
-  __shared__ SelectLds lds[4];
+  __shared__ SelectLds<EPL> lds[4];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
@@ -79,6 +80,47 @@ __global__ __launch_bounds__(256) void topk_kernel(
     w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
     if (w_f32 != nullptr) w_f32[o] = w;
   }
+}
+
+// Expert selection and the permutation of the selected pairs in one block,
+// for a slot table that is final before the router runs (decode replay
+// after staging).  Wave t selects token t (T <= kFusedTopkTokens); the ids
+// go to LDS and feed the same permutation as permute_small_kernel, so every
+// output equals what lmoe_router_topk followed by lmoe_permute writes.
+constexpr int kFusedTopkTokens = 16;
+
+template <int EPL>
+__global__ __launch_bounds__(1024) void topk_permute_kernel(
+    const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
+    float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
+    const int32_t* __restrict__ log2phy, int n_log2phy, int P, int skip, int block_m,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
+    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
+  extern __shared__ int hist[];  // [P]
+  __shared__ SelectLds<EPL> sel_lds[kFusedTopkTokens];
+  __shared__ int32_t ids_lds[kFusedTopkTokens * kMaxK];
+  __shared__ int scan_lds[33];
+  __shared__ int err_lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (wave < T) {
+    float lg[EPL];
+    load_logits<EPL>(logits, logits_f32, wave, sp.E, lg);
+    int e;
+    float w;
+    select_token<EPL>(sp, lg, sel_lds[wave], e, w);
+    if (lane < sp.k) {
+      const int o = wave * sp.k + lane;
+      ids[o] = e;
+      ids_lds[o] = e;
+      w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
+      if (w_f32 != nullptr) w_f32[o] = w;
+    }
+  }
+  __syncthreads();
+  permute_block(ids_lds, T * sp.k, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
+                sorted_pairs, row_idx, active, tile_off, meta, hist, scan_lds, &err_lds);
 }
 
 }  // namespace lmoe
@@ -174,5 +216,43 @@ extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
   } else {
     hipLaunchKernelGGL(topk_kernel<8>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
   }
+  LMOE_RETURN_LAUNCH();
+}
+
+extern "C" int lmoe_router_topk_permute(
+    const void* logits, int logits_f32, int T, int E, int k, int scoring, const float* bias,
+    int n_group, int topk_group, int renorm, float routed_scale, float* w_f32, uint16_t* w_bf16,
+    int32_t* ids, const int32_t* log2phy, int n_log2phy, int n_slots, int skip_unmapped,
+    int block_m, int32_t* counts, int32_t* offsets, int32_t* sorted_pairs, int32_t* row_idx,
+    int32_t* active, int32_t* tile_off, int32_t* meta, hipStream_t stream) {
+  if (logits == nullptr || w_bf16 == nullptr || ids == nullptr || counts == nullptr ||
+      offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
+      active == nullptr || tile_off == nullptr || meta == nullptr)
+    return LMOE_ERR_ARG;
+  int st = check_select(T, E, k, scoring, n_group, topk_group);
+  if (st != LMOE_OK) return st;
+  if (n_slots <= 0 || block_m <= 0) return LMOE_ERR_ARG;
+  if (log2phy != nullptr && n_log2phy <= 0) return LMOE_ERR_ARG;
+  // one block: a token per wave, the whole permutation in LDS
+  if (T > kFusedTopkTokens || E > 256 || n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
+  if (T == 0) return LMOE_OK;
+  const SelectParams sp =
+      make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  const int n_pairs = T * k;
+  int threads = n_pairs > n_slots / 16 ? n_pairs : n_slots / 16;
+  threads = threads > T * 64 ? threads : T * 64;
+  threads = ((threads + 63) / 64) * 64;
+  threads = threads < 64 ? 64 : (threads > kChunk ? kChunk : threads);
+  const size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
+  const int skip = skip_unmapped ? 1 : 0;
+#define LMOE_TP(EPL)                                                                         \
+  hipLaunchKernelGGL(topk_permute_kernel<EPL>, dim3(1), dim3(threads), lds, stream, logits,  \
+                     logits_f32, T, sp, w_f32, w_bf16, ids, log2phy, n_log2phy, n_slots,    \
+                     skip, block_m, counts, offsets, sorted_pairs, row_idx, active, tile_off, \
+                     meta)
+  if (E <= 64) LMOE_TP(1);
+  else if (E <= 128) LMOE_TP(2);
+  else LMOE_TP(4);
+#undef LMOE_TP
   LMOE_RETURN_LAUNCH();
 }

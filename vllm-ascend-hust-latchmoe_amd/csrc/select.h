@@ -43,23 +43,30 @@ struct SelectParams {
   float routed_scale;
 };
 
-// Per-wave LDS scratch of one selection.  Score/id pairs are interleaved so
-// one 16-byte LDS read returns two entries; the ranking loops are unrolled
-// so all their reads are in flight together (a rolled loop waits for each
-// read in turn: ~120 cycles x 64).
+// Per-wave LDS scratch of one selection over up to EPL*64 experts.  Score/id
+// pairs are interleaved so one 16-byte LDS read returns two entries; the
+// ranking loops are unrolled so all their reads are in flight together (a
+// rolled loop waits for each read in turn: ~120 cycles x 64).
+template <int EPL>
 struct SelectLds {
-  float2 lm[kWave];   // (score, id as float bits) of every lane maximum
-  float2 cand[kMaxE]; // (score, id bits) of the candidates
-  float c_w[kMaxE];
-  float c_s[kMaxE];   // score table of the groups (grouped sigmoid)
+  float2 lm[kWave];         // (score, id as float bits) of every lane maximum
+  float2 cand[EPL * kWave]; // (score, id bits) of the candidates
+  float c_w[EPL * kWave];
+  float c_s[EPL * kWave];   // score table of the groups (grouped sigmoid)
   float gsc[kWave];
   float o_w[kMaxK];
   int o_e[kMaxK];
 };
 
-// (value desc, id asc) ordering used by every selection step.
+// (value desc, id asc) ordering used by every selection step.  Written
+// without short-circuit evaluation: as `a || (b && c)` the compiler emits a
+// divergent branch (and a separate LDS read and wait) per comparison, which
+// serialises the unrolled ranking loops.
 __device__ __forceinline__ bool better(float v, int e, float v2, int e2) {
-  return (v > v2) || (v == v2 && e < e2);
+  const bool gt = v > v2;
+  const bool eq = v == v2;
+  const bool lt = e < e2;
+  return gt | (eq & lt);
 }
 
 // Order LDS traffic of one wave: stores before the fence are seen by every
@@ -76,7 +83,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 template <int EPL>
 __device__ __forceinline__ void select_token(const SelectParams& sp,
                                              float (&lg)[EPL],
-                                             SelectLds& L, int& out_e,
+                                             SelectLds<EPL>& L, int& out_e,
                                              float& out_w) {
   const int lane = threadIdx.x & 63;
   const int E = sp.E;
@@ -225,7 +232,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     }
     C += __popcll(bm);
   }
-  // pad to a multiple of 8 with entries that beat nothing (C <= E <= kMaxE,
+  // pad to a multiple of 8 with entries that beat nothing (C <= E <= EPL*64,
   // a multiple of 8, so the padded range stays inside cand[])
   const int C8 = (C + 7) >> 3;
   if (lane < 8 && C + lane < C8 * 8) L.cand[C + lane] = make_float2(-INFINITY, __int_as_float(0x7fffffff));

@@ -149,6 +149,53 @@ def fused_experts(
     return dst
 
 
+def decode_layer(
+    hidden: torch.Tensor,
+    gate_weight: torch.Tensor,
+    spec: RouterSpec,
+    w13_slots: torch.Tensor,
+    w2_slots: torch.Tensor,
+    log2phy: torch.Tensor | None,
+    *,
+    workspace: MoEWorkspace,
+    add: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    logits_out: torch.Tensor | None = None,
+    w_out: torch.Tensor | None = None,
+    ids_out: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """route() followed by fused_experts(), for a slot table that is final
+    before the router runs (the decode replay after staging): gate, then the
+    expert selection and the permutation in one launch, then the decode MLP
+    body.  Returns (out, topk_weights, topk_ids), equal bit for bit to the
+    separate calls."""
+    T = hidden.shape[0]
+    k = int(spec.top_k)
+    P = int(w13_slots.shape[0])
+    ws = workspace
+    if ws.perm.n_slots != P or ws.perm.n_pairs != T * k:
+        raise ValueError("workspace permutation does not match the slot bank or the batch")
+    if logits_out is None:
+        logits_out = torch.empty((T, gate_weight.shape[0]), dtype=hidden.dtype, device=hidden.device)
+    logits = native.router_gate(hidden, gate_weight, logits_out)
+    grouped = bool(spec.use_grouped_topk)
+    w, ids, _ = native.router_topk_permute(
+        logits, k, ws.perm, log2phy=log2phy, scoring=spec.scoring_func,
+        bias=spec.e_score_correction_bias,
+        num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
+        topk_group=int(spec.topk_group or 1) if grouped else 1,
+        renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
+        w_bf16=w_out, ids=ids_out,
+    )
+    dst = out if out is not None else ws.out[:T]
+    if T * k <= native.FUSED_DECODE_MAX_PAIRS:
+        native.fused_moe_decode(hidden, w, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add)
+    else:
+        native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k])
+        native.combine(ws.y[: T * k], w, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
+    return dst, w, ids
+
+
 def check_placed(ws: MoEWorkspace) -> None:
     """Host validation (synchronising): fail if a pair mapped to no slot."""
     meta = ws.perm.meta.cpu().tolist()

@@ -24,6 +24,7 @@ LMOE_SCORING_SIGMOID = 1
 LMOE_PATH_AUTO = 0
 LMOE_PATH_GEMV = 1
 LMOE_PATH_MFMA = 2
+LMOE_ERR_SHAPE = 1001
 META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
 META_COUNT = 4
 MFMA_BLOCK_M = 256  # row-tile height of the prefill MFMA GEMM (tile table of lmoe_permute)
@@ -34,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "lmoe_abi_version",
     "lmoe_router_gate",
     "lmoe_router_topk",
+    "lmoe_router_topk_permute",
     "lmoe_permute_workspace_bytes",
     "lmoe_permute",
     "lmoe_gather_rows",
@@ -58,6 +60,11 @@ _SIGNATURES = {
     "lmoe_router_topk": (
         _i,
         [_vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp],
+    ),
+    "lmoe_router_topk_permute": (
+        _i,
+        [_vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
+         _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "lmoe_permute_workspace_bytes": (_sz, [_i, _i]),
     "lmoe_permute": (
@@ -212,6 +219,75 @@ def router_topk(
         ),
         "lmoe_router_topk",
     )
+    return w_bf16, ids, w_f32
+
+
+def router_topk_permute(
+    logits: torch.Tensor,
+    top_k: int,
+    perm: "Permutation",
+    *,
+    log2phy: torch.Tensor | None = None,
+    skip_unmapped: bool = False,
+    block_m: int | None = None,
+    scoring: str = "softmax",
+    bias: torch.Tensor | None = None,
+    num_expert_group: int = 1,
+    topk_group: int = 1,
+    renormalize: bool = True,
+    routed_scaling_factor: float = 1.0,
+    w_bf16: torch.Tensor | None = None,
+    ids: torch.Tensor | None = None,
+    w_f32: torch.Tensor | None = None,
+    stream=None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """router_topk then permute into perm, in one launch when the shape allows
+    it (T <= 16, E <= 256); otherwise the two launches.  For a slot table
+    (log2phy) that is final before the router runs."""
+    lib = load_library()
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("logits must be bf16 or f32")
+    _need(logits, "logits", logits.dtype)
+    T, E = logits.shape
+    mode = {"softmax": LMOE_SCORING_SOFTMAX, "sigmoid": LMOE_SCORING_SIGMOID}.get(scoring)
+    if mode is None:
+        raise ValueError(f"unsupported scoring function {scoring!r}")
+    if bias is not None:
+        _need(bias, "e_score_correction_bias", torch.float32, (E,))
+    dev = logits.device
+    if w_bf16 is None:
+        w_bf16 = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
+    if ids is None:
+        ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    _need(w_bf16, "topk_weights", torch.bfloat16, (T, top_k))
+    _need(ids, "topk_ids", torch.int32, (T, top_k))
+    if w_f32 is not None:
+        _need(w_f32, "w_f32", torch.float32, (T, top_k))
+    if T * top_k != perm.n_pairs:
+        raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {T * top_k}")
+    n_table = 0
+    if log2phy is not None:
+        _need(log2phy, "log2phy", torch.int32)
+        n_table = int(log2phy.numel())
+    bm = MFMA_BLOCK_M if block_m is None else int(block_m)
+    status = lib.lmoe_router_topk_permute(
+        _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), mode,
+        _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
+        int(bool(renormalize)), float(routed_scaling_factor),
+        _ptr(w_f32), _ptr(w_bf16), _ptr(ids),
+        _ptr(log2phy), n_table, perm.n_slots, int(bool(skip_unmapped)), bm,
+        _ptr(perm.counts), _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.row_idx),
+        _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta), _stream(stream),
+    )
+    if status == LMOE_ERR_SHAPE:
+        router_topk(logits, top_k, scoring=scoring, bias=bias, num_expert_group=num_expert_group,
+                    topk_group=topk_group, renormalize=renormalize,
+                    routed_scaling_factor=routed_scaling_factor, w_bf16=w_bf16, ids=ids, w_f32=w_f32,
+                    stream=stream)
+        permute(ids, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, block_m=bm, stream=stream)
+        return w_bf16, ids, w_f32
+    _check(status, "lmoe_router_topk_permute")
+    perm.block_m = bm
     return w_bf16, ids, w_f32
 
 
