@@ -133,7 +133,8 @@ size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);
  * Outputs: counts[s]; offsets[s] = exclusive prefix of counts (offsets[P] =
  * placed pairs); sorted_pairs[offsets[s] + r] = the r-th pair of slot s in
  * flat order; row_idx[p] = sorted position of pair p or -1; active[a] = a-th
- * slot with count > 0 (ascending); tile_off[s] = sum over s' < s of
+ * slot with count > 0 (ascending), -1 for a >= meta[LMOE_META_ACTIVE];
+ * tile_off[s] = sum over s' < s of
  * ceil(counts[s'] / block_m); meta[LMOE_META_COUNT].
  * Replaces slot_mapping.py:116-140 + npu_moe_init_routing_v2
  * (patch_fused_moe.py:668-701: expert_capacity=-1, drop_pad_mode=0,

@@ -25,6 +25,7 @@ def _check(perm, ref, n_pairs):
     np.testing.assert_array_equal(perm.row_idx.cpu().numpy()[:n_pairs], ref.row_idx)
     na = ref.active.size
     np.testing.assert_array_equal(perm.active.cpu().numpy()[:na], ref.active)
+    assert (perm.active.cpu().numpy()[na:] == -1).all()  # -1 past the active slots
     np.testing.assert_array_equal(perm.tile_off.cpu().numpy(), ref.tile_off)
     meta = perm.meta.cpu().numpy()
     assert meta[0] == na

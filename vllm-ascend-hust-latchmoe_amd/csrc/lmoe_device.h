@@ -127,6 +127,14 @@ __device__ __forceinline__ uint4 load_stream16(const uint16_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Order LDS traffic of one wave: stores before the fence are seen by every
+// lane's loads after it.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }

@@ -36,11 +36,11 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ active,
     const int32_t* __restrict__ meta, uint16_t* __restrict__ act) {
   __shared__ float s_up[2];
-  const int a = blockIdx.y;
-  if (a >= meta[LMOE_META_ACTIVE]) return;
+  const int a = blockIdx.y;  // < n_slots: active[] has an entry (-1 past the active slots)
+  const int s = active[a];
+  if (s < 0) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int s = active[a];
   const int p0 = offsets[s];
   const int n = offsets[s + 1] - p0;
   if (!SPLIT) {
@@ -126,7 +126,7 @@ template <int DNC, int R, bool PF>
 __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     const uint16_t* __restrict__ act, int I, int H, int T, int topk,
     const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ active, const int32_t* __restrict__ meta,
+    const int32_t* __restrict__ active, int P,
     const int32_t* __restrict__ row_idx, const uint16_t* __restrict__ wts,
     const uint16_t* __restrict__ add, uint16_t* __restrict__ out) {
   constexpr int LV = (R >= 4) ? 2 : 1;
@@ -136,7 +136,6 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
   const int l5 = lane & 31;
   const int half = lane >> 5;
   const int hw = (tid >> 6) * 2 + half;
-  const int na = meta[LMOE_META_ACTIVE];
   const int h0 = blockIdx.x * R;
 
   uint4 wcur[R][DNC], wnxt[PF ? R : 1][PF ? DNC : 1];
@@ -153,13 +152,14 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
       }
     }
   };
+  // active[] is -1 past the active slots, so one load per rank decides
   int rank = hw;
-  int s_cur = rank < na ? active[rank] : -1;
+  int s_cur = rank < P ? active[rank] : -1;
   if (s_cur >= 0) load_rows(s_cur, wcur);
   // both halves of a wave run the loop together (shuffles span the wave)
   while (__ballot(s_cur >= 0) != 0ull) {
     const int nrank = rank + 8;
-    const int s_nxt = (s_cur >= 0 && nrank < na) ? active[nrank] : -1;
+    const int s_nxt = (s_cur >= 0 && nrank < P) ? active[nrank] : -1;
     if constexpr (PF) {
       if (s_nxt >= 0) load_rows(s_nxt, wnxt);
     }
@@ -227,13 +227,13 @@ __global__ __launch_bounds__(256) void down_gemv_kernel(
     const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ active,
     const int32_t* __restrict__ meta, uint16_t* __restrict__ y) {
-  const int a = blockIdx.y;
-  if (a >= meta[LMOE_META_ACTIVE]) return;
+  const int a = blockIdx.y;  // < n_slots: active[] has an entry (-1 past the active slots)
+  const int s = active[a];
+  if (s < 0) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int h0 = blockIdx.x * 16 + wave * 4;
   if (h0 >= H) return;
-  const int s = active[a];
   const int p0 = offsets[s];
   const int n = offsets[s + 1] - p0;
   uint2 wv[4][NU];
@@ -522,7 +522,7 @@ extern "C" int lmoe_down_combine(const void* act, int T, int H, int I, int k,
 #define LMOE_DC(DNC, R, PF)                                                                  \
   hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, PF>), dim3((H + R - 1) / R), dim3(256), \
                      0, stream, static_cast<const uint16_t*>(act), I, H, T, k,               \
-                     static_cast<const uint16_t*>(w2_slots), offsets, active, meta, row_idx,  \
+                     static_cast<const uint16_t*>(w2_slots), offsets, active, n_slots, row_idx, \
                      w, static_cast<const uint16_t*>(add), static_cast<uint16_t*>(out))
   if (dnc <= 2) LMOE_DC(2, 4, true);
   else if (dnc <= 3) LMOE_DC(3, 4, true);

@@ -114,6 +114,9 @@ __device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
       tpre += (c + block_m - 1) / block_m;
     }
   }
+  // active[a] = -1 past the active slots: kernels that serve "the a-th
+  // active slot" read one value (no dependent load of meta first)
+  for (int a = atot + threadIdx.x; a < P; a += blockDim.x) active[a] = -1;
   if (threadIdx.x == 0) {
     offsets[P] = ctot;
     tile_off[P] = ttot;
@@ -197,6 +200,120 @@ __device__ __forceinline__ void permute_block(
       }
     }
   }
+}
+
+// One wave permutes N <= 64 pairs over P <= 64 * SPL slots (the decode
+// sizes) with ballots, shuffles and LDS, but no block barrier: pair p is lane
+// p, slot s is owned by lane s / SPL.  Same outputs as permute_block.
+// lds: at least 64 * SPL ints of the calling wave's own LDS.
+constexpr int kWavePermMaxSlotsPerLane = 16;
+
+__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+template <int SPL>
+__device__ __forceinline__ void permute_wave(
+    const int32_t* ids, int N, const int32_t* __restrict__ log2phy, int n_log2phy, int P,
+    int skip, int block_m, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
+    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
+    int* lds) {
+  const int lane = threadIdx.x & 63;
+  const bool have = lane < N;
+  const int s = have ? map_pair(ids, lane, log2phy, n_log2phy, P, skip) : -1;
+  const bool placed = s >= 0;
+  const int errs = __popcll(__ballot(have && s == -2));
+  // pairs of the same slot, and this pair's rank among them (flat order)
+  const int nbits = key_bits(P);
+  const uint64_t m = match_key(placed ? s : (1 << nbits) - 1, nbits);
+  const int rank = __popcll(m & lanemask_lt(lane));
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) lds[lane * SPL + i] = 0;
+  wave_lds_sync();
+  if (placed && rank == 0) lds[s] = __popcll(m);
+  wave_lds_sync();
+  // this lane's slots s0 .. s0+SPL-1: counts, then wave-wide prefixes
+  const int s0 = lane * SPL;
+  int c[SPL];
+  int csum = 0, asum = 0, tsum = 0;
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) {
+    c[i] = (s0 + i < P) ? lds[s0 + i] : 0;
+    csum += c[i];
+    asum += c[i] > 0;
+    tsum += (c[i] + block_m - 1) / block_m;
+  }
+  const int cinc = wave_inclusive_scan(csum, lane);
+  const int ainc = wave_inclusive_scan(asum, lane);
+  const int tinc = wave_inclusive_scan(tsum, lane);
+  int cpre = cinc - csum, apre = ainc - asum, tpre = tinc - tsum;
+  const int ctot = __shfl(cinc, 63, kWave);
+  const int atot = __shfl(ainc, 63, kWave);
+  const int ttot = __shfl(tinc, 63, kWave);
+  wave_lds_sync();  // every lane has read its counts before lds is reused
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) {
+    const int sl = s0 + i;
+    if (sl < P) {
+      counts[sl] = c[i];
+      offsets[sl] = cpre;
+      tile_off[sl] = tpre;
+      if (c[i] > 0) active[apre++] = sl;
+      lds[sl] = cpre;  // running base of the slot
+      cpre += c[i];
+      tpre += (c[i] + block_m - 1) / block_m;
+    }
+  }
+  // active[a] = -1 past the active slots (see scan_slots)
+  for (int a = atot + lane; a < P; a += kWave) active[a] = -1;
+  if (lane == 0) {
+    offsets[P] = ctot;
+    tile_off[P] = ttot;
+    meta[LMOE_META_ACTIVE] = atot;
+    meta[LMOE_META_PAIRS] = ctot;
+    meta[LMOE_META_ERRORS] = errs;
+    meta[LMOE_META_TILES] = ttot;
+  }
+  wave_lds_sync();
+  if (have) {
+    const int pos = placed ? lds[s] + rank : -1;
+    row_idx[lane] = pos;
+    if (pos >= 0) sorted_pairs[pos] = lane;
+  }
+}
+
+// Slots per lane of permute_wave for P slots (0 when P exceeds the wave path).
+__host__ __device__ inline int wave_perm_spl(int P) {
+  const int need = (P + 63) / 64;
+  int spl = 1;
+  while (spl < need) spl <<= 1;
+  return spl <= kWavePermMaxSlotsPerLane ? spl : 0;
+}
+
+// permute_wave for any P <= 64 * kWavePermMaxSlotsPerLane (lds: 64 *
+// wave_perm_spl(P) ints).
+__device__ __forceinline__ void permute_wave_any(
+    const int32_t* ids, int N, const int32_t* __restrict__ log2phy, int n_log2phy, int P,
+    int skip, int block_m, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
+    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
+    int* lds) {
+  const int spl = wave_perm_spl(P);
+#define LMOE_PW(S)                                                                              \
+  permute_wave<S>(ids, N, log2phy, n_log2phy, P, skip, block_m, counts, offsets, sorted_pairs, \
+                  row_idx, active, tile_off, meta, lds)
+  if (spl <= 1) LMOE_PW(1);
+  else if (spl == 2) LMOE_PW(2);
+  else if (spl == 4) LMOE_PW(4);
+  else if (spl == 8) LMOE_PW(8);
+  else LMOE_PW(16);
+#undef LMOE_PW
 }
 
 }  // namespace lmoe

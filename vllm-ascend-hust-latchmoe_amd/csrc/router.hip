@@ -119,8 +119,15 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
     }
   }
   __syncthreads();
-  permute_block(ids_lds, T * sp.k, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
-                sorted_pairs, row_idx, active, tile_off, meta, hist, scan_lds, &err_lds);
+  const int n_pairs = T * sp.k;
+  if (n_pairs <= kWave && wave_perm_spl(P) > 0) {
+    if (wave == 0)
+      permute_wave_any(ids_lds, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
+                       sorted_pairs, row_idx, active, tile_off, meta, hist);
+  } else {
+    permute_block(ids_lds, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
+                  sorted_pairs, row_idx, active, tile_off, meta, hist, scan_lds, &err_lds);
+  }
 }
 
 }  // namespace lmoe
@@ -243,7 +250,11 @@ extern "C" int lmoe_router_topk_permute(
   threads = threads > T * 64 ? threads : T * 64;
   threads = ((threads + 63) / 64) * 64;
   threads = threads < 64 ? 64 : (threads > kChunk ? kChunk : threads);
-  const size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
+  size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
+  if (n_pairs <= kWave && wave_perm_spl(n_slots) > 0) {
+    const size_t wlds = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(n_slots));
+    lds = wlds > lds ? wlds : lds;
+  }
   const int skip = skip_unmapped ? 1 : 0;
 #define LMOE_TP(EPL)                                                                         \
   hipLaunchKernelGGL(topk_permute_kernel<EPL>, dim3(1), dim3(threads), lds, stream, logits,  \

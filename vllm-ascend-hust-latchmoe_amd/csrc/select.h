@@ -2,18 +2,12 @@
 // correction bias + group-limited top-k, with renormalisation and scaling.
 //
 // Selection order is (score desc, expert id asc), the order torch.topk gives
-// with ties to the lower id.  Instead of k serial rounds of wave arg-max
-// (a chain of 12 cross-lane shuffles per round), the k best are found by
-// ranking:
-//   1. every lane takes the best of its own experts (e = j*64 + lane);
-//   2. the lane maxima are ranked against each other through LDS; the value
-//      of the lane maximum of rank k-1 is a lower bound on the k-th best
-//      score (k distinct experts reach it), so only experts at or above it
-//      can be selected;
-//   3. those candidates (usually k..2k) are compacted with ballots and each
-//      is ranked against the others; rank r < k lands in output slot r.
-// The rank of a candidate among candidates equals its rank among all
-// experts, because every expert that beats a candidate is a candidate too.
+// with ties to the lower id.  Instead of k serial rounds of wave arg-max,
+// each score becomes an order-preserving 32-bit key and a most-significant-
+// bit-first radix select (one ballot per expert slot and bit) finds the k-th
+// largest key and how many of the experts equal to it are taken; the taken
+// experts (the lowest ids among the equal ones) are compacted with ballots
+// and only those k are ranked against each other through LDS.
 //
 // Reference behaviour: moe_router_op.py:191-278 (gate then select_experts),
 // renorm contract patches/patch_fused_moe.py:597-632
@@ -49,8 +43,7 @@ struct SelectParams {
 // rolled loop waits for each read in turn: ~120 cycles x 64).
 template <int EPL>
 struct SelectLds {
-  float2 lm[kWave];         // (score, id as float bits) of every lane maximum
-  float2 cand[EPL * kWave]; // (score, id bits) of the candidates
+  float2 cand[EPL * kWave]; // (key bits, id bits) of the taken experts
   float c_w[EPL * kWave];
   float c_s[EPL * kWave];   // score table of the groups (grouped sigmoid)
   float gsc[kWave];
@@ -67,14 +60,6 @@ __device__ __forceinline__ bool better(float v, int e, float v2, int e2) {
   const bool eq = v == v2;
   const bool lt = e < e2;
   return gt | (eq & lt);
-}
-
-// Order LDS traffic of one wave: stores before the fence are seen by every
-// lane's loads after it.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Selects the k experts of one token from its logits lg[j] (expert j*64 +
@@ -186,78 +171,75 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     }
   }
 
-  // 1. lane maxima
-  float m = -INFINITY;
-  int me = 0x7fffffff;
+  // 1. order-preserving 32-bit keys: key(a) > key(b) <=> a > b for scores
+  //    (-0 is made +0 so equal scores tie and go to the lower id); key 0
+  //    marks an expert that is not eligible
+  uint32_t key[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    const int e = j * kWave + lane;
-    if (elig[j] && better(sel[j], e, m, me)) {
-      m = sel[j];
-      me = e;
-    }
+    const uint32_t u = __float_as_uint(sel[j] + 0.0f);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    key[j] = elig[j] ? o : 0u;
   }
-  L.lm[lane] = make_float2(m, __int_as_float(me));
+  // 2. radix select, most significant bit first: thr = the k-th largest key,
+  //    need = how many experts with key == thr are taken (the lowest ids)
+  uint32_t thr = 0u, tmask = 0u;
+  int need = k;
+#pragma unroll 4
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t bit = 1u << b;
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const bool c = (key[j] != 0u) & ((key[j] & tmask) == thr) & ((key[j] & bit) != 0u);
+      cnt += __popcll(__ballot(c));
+    }
+    if (cnt >= need) thr |= bit;
+    else need -= cnt;
+    tmask |= bit;
+  }
+  // 3. the taken experts (k, or every eligible one if fewer), compacted in
+  //    id order, then each ranked among the others by (key desc, id asc)
   if (lane < kMaxK) {
     L.o_e[lane] = -1;
     L.o_w[lane] = 0.0f;
   }
-  wave_lds_sync();
-  // 2. threshold: value of the lane maximum of rank k-1 (-inf if fewer than
-  //    k lanes hold an eligible expert)
-  int r = 0;
-  {
-    const float4* lm4 = reinterpret_cast<const float4*>(L.lm);
-#pragma unroll
-    for (int l = 0; l < kWave / 2; ++l) {
-      const float4 q = lm4[l];
-      r += better(q.x, __float_as_int(q.y), m, me) ? 1 : 0;
-      r += better(q.z, __float_as_int(q.w), m, me) ? 1 : 0;
-    }
-  }
-  const uint64_t at = __ballot(me != 0x7fffffff && r == k - 1);
-  const float thr = at ? __shfl(m, __ffsll(static_cast<long long>(at)) - 1, kWave)
-                       : -INFINITY;
-  // 3. compact the candidates, in ascending expert id order
-  int C = 0;
+  int C = 0, eq_before = 0;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = j * kWave + lane;
-    const bool c = elig[j] && sel[j] >= thr;
-    const uint64_t bm = __ballot(c);
-    if (c) {
-      const int idx = C + __popcll(bm & lanemask_lt(lane));
-      L.cand[idx] = make_float2(sel[j], __int_as_float(e));
+    const bool eq = (key[j] != 0u) & (key[j] == thr);
+    const uint64_t beq = __ballot(eq);
+    const bool take = (key[j] != 0u) &
+                      ((key[j] > thr) | (eq & (eq_before + __popcll(beq & lanemask_lt(lane)) < need)));
+    eq_before += __popcll(beq);
+    const uint64_t bt = __ballot(take);
+    if (take) {
+      const int idx = C + __popcll(bt & lanemask_lt(lane));
+      L.cand[idx] = make_float2(__uint_as_float(key[j]), __int_as_float(e));
       L.c_w[idx] = wgt[j];
     }
-    C += __popcll(bm);
+    C += __popcll(bt);
   }
-  // pad to a multiple of 8 with entries that beat nothing (C <= E <= EPL*64,
-  // a multiple of 8, so the padded range stays inside cand[])
-  const int C8 = (C + 7) >> 3;
-  if (lane < 8 && C + lane < C8 * 8) L.cand[C + lane] = make_float2(-INFINITY, __int_as_float(0x7fffffff));
+  // pad to kMaxK entries with key 0 (beats nothing)
+  if (lane >= C && lane < kMaxK) L.cand[lane] = make_float2(__uint_as_float(0u), __int_as_float(0x7fffffff));
   wave_lds_sync();
-  const float4* cand4 = reinterpret_cast<const float4*>(L.cand);
-  for (int i0 = 0; i0 < C; i0 += kWave) {
-    const int i = i0 + lane;
-    const float2 me2 = i < C ? L.cand[i] : make_float2(-INFINITY, __int_as_float(0x7fffffff));
-    const float cs = me2.x;
-    const int ce = __float_as_int(me2.y);
+  if (lane < C) {
+    const float2 me2 = L.cand[lane];
+    const uint32_t mk = __float_as_uint(me2.x);
+    const int mid = __float_as_int(me2.y);
+    const float4* cand4 = reinterpret_cast<const float4*>(L.cand);
     int rr = 0;
-    for (int b = 0; b < C8; ++b) {
-      float4 q[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) q[u] = cand4[b * 4 + u];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        rr += better(q[u].x, __float_as_int(q[u].y), cs, ce) ? 1 : 0;
-        rr += better(q[u].z, __float_as_int(q[u].w), cs, ce) ? 1 : 0;
-      }
+    for (int u = 0; u < kMaxK / 2; ++u) {
+      const float4 q = cand4[u];
+      const uint32_t k0 = __float_as_uint(q.x), k1 = __float_as_uint(q.z);
+      const int i0 = __float_as_int(q.y), i1 = __float_as_int(q.w);
+      rr += ((k0 > mk) | ((k0 == mk) & (i0 < mid))) ? 1 : 0;
+      rr += ((k1 > mk) | ((k1 == mk) & (i1 < mid))) ? 1 : 0;
     }
-    if (i < C && rr < k) {
-      L.o_e[rr] = ce;
-      L.o_w[rr] = L.c_w[i];
-    }
+    L.o_e[rr] = mid;
+    L.o_w[rr] = L.c_w[lane];
   }
   wave_lds_sync();
   // renormalise in selection order, scale
