@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define LMOE_ABI_VERSION 1
+#define LMOE_ABI_VERSION 2
 
 enum {
   LMOE_OK = 0,
@@ -204,20 +204,25 @@ int lmoe_down_combine(const void* act, int T, int H, int I, int k,
                       const int32_t* active, const int32_t* meta,
                       const void* add, void* out, hipStream_t stream);
 
-/* Decode MoE for small pair counts, two launches: gate_up GEMV + SiLU*mul
- * into act (sorted order), then down GEMV fused with the weighted combine
- * (each workgroup owns a few output columns of every token):
+/* Decode MoE for small pair counts:
  *   out[t] = (add ? add[t] : 0) + sum_j w[t][j] * W2_s(t,j) act[pos(t,j)].
- * Each slot's weights are read once however many tokens chose it.  Needs
- * T*k <= 1024, H % 8 == 0, I % 64 == 0, I <= 4096, H <= 8192; x, slot banks
- * and act 16-byte aligned.  Permutation arrays as produced by lmoe_permute. */
+ * gate_up GEMV + SiLU*mul into act (sorted order), then either the down GEMV
+ * fused with the weighted combine (each workgroup owns a few output columns
+ * of every token; two launches, used for T == 1 or y == NULL), or, for
+ * T > 1 with a y workspace ([T*k, H] bf16, flat pair order on return),
+ * the down GEMV per (row block, slot) into y and the combine (three
+ * launches: no workgroup walks the slots in turn).  Both give the same out
+ * bit for bit.  Each slot's weights are read once however many tokens chose
+ * it.  Needs T*k <= 1024, H % 8 == 0, I % 64 == 0, I <= 4096, H <= 8192;
+ * x, slot banks, act and y 16-byte aligned.  Permutation arrays as produced
+ * by lmoe_permute. */
 int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                           const void* w13_slots, const void* w2_slots,
                           int n_slots, const uint16_t* w,
                           const int32_t* offsets, const int32_t* sorted_pairs,
                           const int32_t* row_idx, const int32_t* active,
                           const int32_t* meta, const void* add, void* act,
-                          void* out, hipStream_t stream);
+                          void* y, void* out, hipStream_t stream);
 
 /* Batched host->device (or device->device) expert copies on a transfer
  * stream: optionally wait on wait_event, then for i < n copy bytes[i] from

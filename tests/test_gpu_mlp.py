@@ -171,7 +171,9 @@ def test_combine_masks_unplaced_pairs_and_adds_shared():
     assert rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref) <= 1e-2
 
 
-def _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None):
+def _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None, with_y=False):
+    """with_y: the three-launch body (down per row block and slot into y,
+    then the combine) that T > 1 takes when given the y workspace."""
     T, H = d_x.shape
     k = d_ids.shape[1]
     P, I = d_w13.shape[0], d_w13.shape[1] // 2
@@ -179,7 +181,8 @@ def _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None):
     native.permute(d_ids, perm, log2phy=d_l2p)
     act = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
-    native.fused_moe_decode(d_x, d_w, d_w13, d_w2, perm, act, out, add=add)
+    y = torch.empty((T * k, H), dtype=torch.bfloat16, device="cuda") if with_y else None
+    native.fused_moe_decode(d_x, d_w, d_w13, d_w2, perm, act, out, add=add, y=y)
     return out, perm.meta
 
 
@@ -198,10 +201,40 @@ def test_fused_decode_more_shapes(T, k, E, P, H, I):
     ids, l2p, x, w13, w2, wb = _case(T * 31 + H + k, T, k, E, P, H, I)
     d_ids, d_l2p, d_x, d_w13, d_w2, d_w = _dev(ids, l2p, x, w13, w2, wb)
     out, meta = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
-    out2, _ = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
+    out2, _ = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, with_y=True)
     torch.cuda.synchronize()
     assert meta[native.META_ACTIVE].item() == np.unique(ids).size
+    # the fused down+combine body and the y + combine body agree bit for bit
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    ref = omlp.moe_layer(x, ids, wb, l2p, w13, w2)
+    err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
+    print(f"  rel max err {err:.3e}", flush=True)
+    assert err <= OUT_TOL
+
+
+@pytest.mark.parametrize("T,k,E,H,I", [
+    (13, 6, 8, 2048, 768),   # ~10 tokens per slot: groups of 4 and a ragged tail
+    (7, 3, 4, 7168, 2048),   # split gate/up waves; down rows in groups of 2 pairs
+    (9, 2, 3, 768, 4096),    # widest I: one pair per down reduction
+])
+def test_batched_tokens_equal_one_token_at_a_time(T, k, E, H, I):
+    """Slots serving several tokens reduce them in groups; every token's
+    output must be bit-identical to running that token alone."""
+    native = _native()
+    print(f"case batched-vs-single T={T} k={k} E={E} H={H} I={I}", flush=True)
+    ids, l2p, x, w13, w2, wb = _case(T * 7 + H + I, T, k, E, E, H, I)
+    d_ids, d_l2p, d_x, d_w13, d_w2, d_w = _dev(ids, l2p, x, w13, w2, wb)
+    out, meta = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
+    out_y, _ = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, with_y=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out_y.view(torch.int16))
+    counts = np.bincount(l2p[ids].ravel(), minlength=E)
+    assert counts.max() > 4  # the grouped path is exercised
+    for t in range(T):
+        o1, _ = _fused(native, d_x[t:t + 1].contiguous(), d_w[t:t + 1].contiguous(),
+                       d_ids[t:t + 1].contiguous(), d_w13, d_w2, d_l2p)
+        torch.cuda.synchronize()
+        assert torch.equal(o1.view(torch.int16)[0], out.view(torch.int16)[t]), t
     ref = omlp.moe_layer(x, ids, wb, l2p, w13, w2)
     err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
     print(f"  rel max err {err:.3e}", flush=True)

@@ -114,7 +114,7 @@ def test_grouped_sigmoid_bit_exact(T, E, G, TG, k, scale):
     np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
 
 
-@pytest.mark.parametrize("T,H,E", [(1, 2048, 128), (16, 2048, 128), (64, 7168, 256), (300, 2048, 128), (1000, 7168, 256)])
+@pytest.mark.parametrize("T,H,E", [(1, 2048, 128), (7, 2048, 128), (16, 2048, 128), (64, 7168, 256), (300, 2048, 128), (1000, 7168, 256)])
 def test_gate_within_one_bf16_ulp(T, H, E):
     native = _native()
     print(f"case gate T={T} H={H} E={E}", flush=True)
@@ -133,6 +133,24 @@ def test_gate_within_one_bf16_ulp(T, H, E):
     assert np.all(np.abs(got - ref) <= bound)
     frac, _ = ulp_mismatch_stats(got, ref)
     assert frac < 1e-3
+
+
+@pytest.mark.parametrize("T,H", [(7, 2048), (13, 7168)])
+def test_gate_grouped_tokens_equal_one_at_a_time(T, H):
+    """The GEMV path reduces several tokens at once; each token's f32
+    logits must be bit-identical to a call with that token alone."""
+    native = _native()
+    E = 128
+    rng = np.random.default_rng(31 + T)
+    x = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
+    wg = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
+    all_t = torch.empty((T, E), dtype=torch.float32, device="cuda")
+    native.router_gate(x, wg, all_t)
+    for t in range(T):
+        one = torch.empty((1, E), dtype=torch.float32, device="cuda")
+        native.router_gate(x[t:t + 1].contiguous(), wg, one)
+        torch.cuda.synchronize()
+        assert torch.equal(one[0].view(torch.int32), all_t[t].view(torch.int32)), t
 
 
 def test_gate_f32_output():

@@ -27,7 +27,9 @@ namespace lmoe {
 // up row I+i, 2*NC 16-byte chunks per lane, loaded non-temporally, RPB = 4);
 // with SPLIT (long rows, NC > 8) waves 2w and 2w+1 own the gate and the up
 // row of one i (RPB = 2) and meet in LDS.  The slot's tokens stream past one
-// at a time (x rows from L2); act is written in sorted order.
+// at a time (x rows from L2); act is written in sorted order.  (Reducing
+// several tokens per step needs twice the registers, and the lost occupancy
+// costs more than the shorter chain saves: measured slower at B = 4 and 16.)
 // ---------------------------------------------------------------------------
 template <int NC, bool SPLIT>
 __global__ __launch_bounds__(256) void gateup_gemv_kernel(
@@ -218,67 +220,77 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// down GEMV per slot, writes y[pair][h] (bf16).  grid (ceil(H/16),
-// max_active); wave w owns rows h0 + 4w .. h0 + 4w + 3 of the a-th slot.
+// down GEMV per (row block, slot), y in bf16.  grid (ceil(H / (8 R)),
+// max_active); half wave hw of block (bx, a) owns rows h0 = (8 bx + hw) R ..
+// h0 + R - 1 of the a-th active slot: DNC 16-byte chunks per lane and row
+// (non-temporal), then the slot's act rows one pair at a time (sorted order,
+// from L2).  Every (slot, row block) is its own workgroup, so a slot's rows
+// are streamed by many CUs at once and no workgroup walks the slots in turn.
+// y row = flat pair (sorted_pairs[pos]).  Per value the reduction is the
+// lane-pair tree of down_combine_gemv_kernel, so y equals its LDS values bit
+// for bit.
 // ---------------------------------------------------------------------------
-template <int NU>
-__global__ __launch_bounds__(256) void down_gemv_kernel(
+template <int DNC, int R>
+__global__ __launch_bounds__(256) void down_rows_kernel(
     const uint16_t* __restrict__ act, int I, int H,
     const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ active,
-    const int32_t* __restrict__ meta, uint16_t* __restrict__ y) {
+    uint16_t* __restrict__ y) {
+  constexpr int LV = (R >= 4) ? 2 : 1;
   const int a = blockIdx.y;  // < n_slots: active[] has an entry (-1 past the active slots)
   const int s = active[a];
   if (s < 0) return;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int h0 = blockIdx.x * 16 + wave * 4;
-  if (h0 >= H) return;
+  const int l5 = lane & 31;
+  const int hw = (threadIdx.x >> 6) * 2 + (lane >> 5);
+  const int h0 = (blockIdx.x * 8 + hw) * R;
   const int p0 = offsets[s];
   const int n = offsets[s + 1] - p0;
-  uint2 wv[4][NU];
+  // both halves of a wave serve the same slot: loop bounds are wave-uniform
+  const uint16_t* base2 = w2 + static_cast<size_t>(s) * H * I;
+  uint4 w[R][DNC];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int h = h0 + rr;
-    const uint16_t* row = w2 + (static_cast<size_t>(s) * H + (h < H ? h : 0)) * I;
+  for (int r = 0; r < R; ++r) {
+    const int h = h0 + r;
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const int e = (u * 64 + lane) * 4;
-      wv[rr][u] = (h < H && e < I) ? *reinterpret_cast<const uint2*>(row + e)
-                                   : make_uint2(0u, 0u);
+    for (int c = 0; c < DNC; ++c) {
+      const int col = c * 256 + l5 * 8;
+      w[r][c] = (h < H && col < I) ? load_stream16(base2 + static_cast<size_t>(h) * I + col)
+                                   : make_uint4(0u, 0u, 0u, 0u);
     }
   }
-  for (int r = 0; r < n; ++r) {
-    const int pos = p0 + r;
-    const uint16_t* arow = act + static_cast<size_t>(pos) * I;
-    uint2 av[NU];
+  for (int q = 0; q < n; ++q) {
+    const int pos = p0 + q;
+    const uint16_t* ar = act + static_cast<size_t>(pos) * I;
+    const int dst = sorted_pairs[pos];
+    float v[R];
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const int e = (u * 64 + lane) * 4;
-      av[u] = (e < I) ? *reinterpret_cast<const uint2*>(arow + e) : make_uint2(0u, 0u);
+    for (int r = 0; r < R; ++r) v[r] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < DNC; ++c) {
+      const int col = c * 256 + l5 * 8;
+      if (col < I) {
+        const uint4 av = *reinterpret_cast<const uint4*>(ar + col);
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = dot8(av, w[r][c], v[r]);
+      }
     }
-    float acc[4];
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      acc[rr] = 0.0f;
-#pragma unroll
-      for (int u = 0; u < NU; ++u) acc[rr] = dot4(av[u], wv[rr][u], acc[rr]);
-      acc[rr] = wave_sum(acc[rr]);
-    }
-    if (lane == 0) {
-      const int pair = sorted_pairs[pos];
-      uint16_t* yr = y + static_cast<size_t>(pair) * H;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        if (h0 + rr < H) yr[h0 + rr] = static_cast<uint16_t>(f32_to_bf16_bits(acc[rr]));
-    }
+    // reduce over the 32 lanes of each half wave: lane holds row r
+    const float tot = reduce_scatter<R, 4, 0>(v, lane);
+    const int r = scatter_index<4, 0, LV>(lane);
+    if ((l5 & ((1 << (5 - LV)) - 1)) == 0 && h0 + r < H)
+      y[static_cast<size_t>(dst) * H + h0 + r] = static_cast<uint16_t>(f32_to_bf16_bits(tot));
   }
 }
 
 // ---------------------------------------------------------------------------
 // weighted combine, y indexed by flat pair.  grid (T, ceil(H/2048)); each
-// thread owns 8 consecutive columns.
+// thread owns 8 consecutive columns.  The k rows of its token are loaded
+// together (up to kCombineStep per step, independent of row_idx, which only
+// masks), then added in j order.
 // ---------------------------------------------------------------------------
+constexpr int kCombineStep = 16;
+
 __global__ __launch_bounds__(256) void combine_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ row_idx,
     const uint16_t* __restrict__ w, int T, int topk, int H,
@@ -289,30 +301,46 @@ __global__ __launch_bounds__(256) void combine_kernel(
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  for (int j = 0; j < topk; ++j) {
-    const int p = t * topk + j;
-    if (row_idx != nullptr && row_idx[p] < 0) continue;
-    const float wj = bf16_to_f32(w[p]);
-    const uint4 v = *reinterpret_cast<const uint4*>(y + static_cast<size_t>(p) * H + h);
-    acc[0] += wj * bf16lo(v.x);
-    acc[1] += wj * bf16hi(v.x);
-    acc[2] += wj * bf16lo(v.y);
-    acc[3] += wj * bf16hi(v.y);
-    acc[4] += wj * bf16lo(v.z);
-    acc[5] += wj * bf16hi(v.z);
-    acc[6] += wj * bf16lo(v.w);
-    acc[7] += wj * bf16hi(v.w);
+  uint4 av = make_uint4(0u, 0u, 0u, 0u);
+  if (add != nullptr) av = *reinterpret_cast<const uint4*>(add + static_cast<size_t>(t) * H + h);
+  for (int j0 = 0; j0 < topk; j0 += kCombineStep) {
+    uint4 v[kCombineStep];
+    float wj[kCombineStep];
+    bool use[kCombineStep];
+#pragma unroll
+    for (int jj = 0; jj < kCombineStep; ++jj) {
+      const int j = j0 + jj;
+      const int p = t * topk + j;
+      const bool in = j < topk;
+      use[jj] = in && (row_idx == nullptr || row_idx[p] >= 0);
+      wj[jj] = in ? bf16_to_f32(w[p]) : 0.0f;
+      v[jj] = in ? *reinterpret_cast<const uint4*>(y + static_cast<size_t>(p) * H + h)
+                 : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int jj = 0; jj < kCombineStep; ++jj) {
+      if (use[jj]) {
+        const float q = wj[jj];
+        acc[0] += q * bf16lo(v[jj].x);
+        acc[1] += q * bf16hi(v[jj].x);
+        acc[2] += q * bf16lo(v[jj].y);
+        acc[3] += q * bf16hi(v[jj].y);
+        acc[4] += q * bf16lo(v[jj].z);
+        acc[5] += q * bf16hi(v[jj].z);
+        acc[6] += q * bf16lo(v[jj].w);
+        acc[7] += q * bf16hi(v[jj].w);
+      }
+    }
   }
   if (add != nullptr) {
-    const uint4 v = *reinterpret_cast<const uint4*>(add + static_cast<size_t>(t) * H + h);
-    acc[0] += bf16lo(v.x);
-    acc[1] += bf16hi(v.x);
-    acc[2] += bf16lo(v.y);
-    acc[3] += bf16hi(v.y);
-    acc[4] += bf16lo(v.z);
-    acc[5] += bf16hi(v.z);
-    acc[6] += bf16lo(v.w);
-    acc[7] += bf16hi(v.w);
+    acc[0] += bf16lo(av.x);
+    acc[1] += bf16hi(av.x);
+    acc[2] += bf16lo(av.y);
+    acc[3] += bf16hi(av.y);
+    acc[4] += bf16lo(av.z);
+    acc[5] += bf16hi(av.z);
+    acc[6] += bf16lo(av.w);
+    acc[7] += bf16hi(av.w);
   }
   uint4 o;
   o.x = pack_bf16x2(acc[0], acc[1]);
@@ -346,7 +374,32 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
   return LMOE_OK;
 }
 
-static int nu_for(int I) { return (I + 255) / 256; }
+// down_rows_kernel launch: R = 2 rows per half wave, 16 rows per workgroup
+// (measured faster than 4 at B = 4 and 16: twice the workgroups, fewer
+// registers).
+static int launch_down_rows(const uint16_t* act, int H, int I, const uint16_t* w2,
+                            const int32_t* offsets, const int32_t* sorted_pairs,
+                            const int32_t* active, int max_active, uint16_t* y,
+                            hipStream_t stream) {
+  const int dnc = (I + 255) / 256;
+#define LMOE_DR(DNC, R)                                                                         \
+  hipLaunchKernelGGL((down_rows_kernel<DNC, R>), dim3((H + 8 * (R)-1) / (8 * (R)), max_active), \
+                     dim3(256), 0, stream, act, I, H, w2, offsets, sorted_pairs, active, y)
+  if (dnc <= 2) LMOE_DR(2, 2);
+  else if (dnc <= 3) LMOE_DR(3, 2);
+  else if (dnc <= 4) LMOE_DR(4, 2);
+  else if (dnc <= 8) LMOE_DR(8, 2);
+  else if (dnc <= 16) LMOE_DR(16, 2);
+  else return LMOE_ERR_SHAPE;
+#undef LMOE_DR
+  return LMOE_OK;
+}
+
+static void launch_combine(const uint16_t* y, const int32_t* row_idx, const uint16_t* w, int T,
+                           int k, int H, const uint16_t* add, uint16_t* out, hipStream_t stream) {
+  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + 2047) / 2048), dim3(256), 0, stream, y, row_idx,
+                     w, T, k, H, add, out);
+}
 
 // ---------------------------------------------------------------------------
 // grouped MFMA GEMM launch (prefill).  block_m is the tile height the
@@ -455,17 +508,10 @@ extern "C" int lmoe_down(const void* act, int H, int I, const void* w2_slots, in
   const uint16_t* w2 = static_cast<const uint16_t*>(w2_slots);
   uint16_t* yb = static_cast<uint16_t*>(y);
   if (path == LMOE_PATH_GEMV) {
-    dim3 grid((H + 15) / 16, max_active);
-    const int nu = nu_for(I);
-#define LMOE_DN(NU)                                                            \
-  hipLaunchKernelGGL(down_gemv_kernel<NU>, grid, dim3(256), 0, stream, actb, I, H, \
-                     w2, offsets, sorted_pairs, active, meta, yb)
-    if (nu <= 3) LMOE_DN(3);
-    else if (nu <= 4) LMOE_DN(4);
-    else if (nu <= 8) LMOE_DN(8);
-    else if (nu <= 16) LMOE_DN(16);
-    else return LMOE_ERR_SHAPE;
-#undef LMOE_DN
+    if ((reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(w2_slots)) & 15u)
+      return LMOE_ERR_SHAPE;
+    st = launch_down_rows(actb, H, I, w2, offsets, sorted_pairs, active, max_active, yb, stream);
+    if (st != LMOE_OK) return st;
     LMOE_RETURN_LAUNCH();
   }
   if (path != LMOE_PATH_MFMA) return LMOE_ERR_UNSUPPORTED;
@@ -541,7 +587,7 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                                      const int32_t* sorted_pairs,
                                      const int32_t* row_idx,
                                      const int32_t* active, const int32_t* meta,
-                                     const void* add, void* act, void* out,
+                                     const void* add, void* act, void* y, void* out,
                                      hipStream_t stream) {
   if (x == nullptr || w13_slots == nullptr || w2_slots == nullptr || w == nullptr ||
       offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
@@ -552,7 +598,8 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
   const int n_pairs = T * k;
   if (n_pairs > kFusedMaxPairs) return LMOE_ERR_SHAPE;
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w13_slots) |
-       reinterpret_cast<uintptr_t>(w2_slots) | reinterpret_cast<uintptr_t>(act)) & 15u)
+       reinterpret_cast<uintptr_t>(w2_slots) | reinterpret_cast<uintptr_t>(act) |
+       reinterpret_cast<uintptr_t>(y)) & 15u)
     return LMOE_ERR_SHAPE;
   if (T == 0) return LMOE_OK;
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
@@ -561,6 +608,17 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                               sorted_pairs, active, meta, max_active,
                               static_cast<uint16_t*>(act), stream);
   if (st != LMOE_OK) return st;
+  if (y != nullptr && T > 1) {
+    // slots serving several tokens: down per (row block, slot) into y (flat
+    // pair order), then the combine
+    st = launch_down_rows(static_cast<const uint16_t*>(act), H, I,
+                          static_cast<const uint16_t*>(w2_slots), offsets, sorted_pairs, active,
+                          max_active, static_cast<uint16_t*>(y), stream);
+    if (st != LMOE_OK) return st;
+    launch_combine(static_cast<const uint16_t*>(y), row_idx, w, T, k, H,
+                   static_cast<const uint16_t*>(add), static_cast<uint16_t*>(out), stream);
+    LMOE_RETURN_LAUNCH();
+  }
   return lmoe_down_combine(act, T, H, I, k, w2_slots, n_slots, w, offsets, row_idx, active, meta,
                            add, out, stream);
 }
@@ -572,9 +630,7 @@ extern "C" int lmoe_combine(const void* y, const int32_t* row_idx,
   if (T < 0 || k <= 0 || H <= 0) return LMOE_ERR_ARG;
   if (H % 8 != 0) return LMOE_ERR_SHAPE;
   if (T == 0) return LMOE_OK;
-  dim3 grid(T, (H + 2047) / 2048);
-  hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, stream,
-                     static_cast<const uint16_t*>(y), row_idx, w, T, k, H,
-                     static_cast<const uint16_t*>(add), static_cast<uint16_t*>(out));
+  launch_combine(static_cast<const uint16_t*>(y), row_idx, w, T, k, H,
+                 static_cast<const uint16_t*>(add), static_cast<uint16_t*>(out), stream);
   LMOE_RETURN_LAUNCH();
 }

@@ -14,6 +14,7 @@
 namespace lmoe {
 
 constexpr int kGateMaxChunks = 16;  // H <= 16 * 512 = 8192 in the GEMV path
+constexpr int kGateTok = 4;         // tokens per reduction in the gate GEMV
 
 // logits[t][e] for e = 4*blockIdx.x + wave, tokens [t0, t1).  The expert row
 // stays in registers (one 16-byte chunk per 512 columns per lane) while the
@@ -38,8 +39,11 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
     w[c] = (h < H) ? *reinterpret_cast<const uint4*>(wrow + h)
                    : make_uint4(0u, 0u, 0u, 0u);
   }
-  for (int t = t0; t < t1; ++t) {
-    const uint16_t* xr = x + static_cast<size_t>(t) * H;
+  // kGateTok tokens per reduction (x rows in flight together; the same
+  // lane-pair tree per token as a lone wave_sum, so the logits do not depend
+  // on how tokens are grouped)
+  if (t1 - t0 == 1) {
+    const uint16_t* xr = x + static_cast<size_t>(t0) * H;
     float acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -48,6 +52,37 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
     }
     acc = wave_sum(acc);
     if (lane == 0) {
+      const size_t o = static_cast<size_t>(t0) * E + e;
+      if (logits_f32) {
+        reinterpret_cast<float*>(logits)[o] = acc;
+      } else {
+        reinterpret_cast<uint16_t*>(logits)[o] =
+            static_cast<uint16_t>(f32_to_bf16_bits(acc));
+      }
+    }
+    return;
+  }
+  for (int tb = t0; tb < t1; tb += kGateTok) {
+    const uint16_t* xr[kGateTok];
+#pragma unroll
+    for (int g = 0; g < kGateTok; ++g)
+      xr[g] = x + static_cast<size_t>(tb + g < t1 ? tb + g : t1 - 1) * H;
+    float v[kGateTok];
+#pragma unroll
+    for (int g = 0; g < kGateTok; ++g) v[g] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int h = c * 512 + lane * 8;
+      if (h < H) {
+#pragma unroll
+        for (int g = 0; g < kGateTok; ++g)
+          v[g] = dot8(*reinterpret_cast<const uint4*>(xr[g] + h), w[c], v[g]);
+      }
+    }
+    // lane l ends with the total of token tb + l / 16
+    const float acc = reduce_scatter<kGateTok, 5, 0>(v, lane);
+    const int t = tb + (lane >> 4);
+    if ((lane & 15) == 0 && t < t1) {
       const size_t o = static_cast<size_t>(t) * E + e;
       if (logits_f32) {
         reinterpret_cast<float*>(logits)[o] = acc;
@@ -69,11 +104,12 @@ __global__ __launch_bounds__(256) void topk_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
-  float lg[EPL];
+  float bv[EPL], lg[EPL];
+  load_bias<EPL>(sp, bv);
   load_logits<EPL>(logits, logits_f32, t < T ? t : 0, sp.E, lg);
   int e;
   float w;
-  select_token<EPL>(sp, lg, lds[wave], e, w);
+  select_token<EPL>(sp, lg, bv, lds[wave], e, w);
   if (t < T && lane < sp.k) {
     const size_t o = static_cast<size_t>(t) * sp.k + lane;
     ids[o] = e;
@@ -105,11 +141,12 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   if (wave < T) {
-    float lg[EPL];
+    float bv[EPL], lg[EPL];
+    load_bias<EPL>(sp, bv);
     load_logits<EPL>(logits, logits_f32, wave, sp.E, lg);
     int e;
     float w;
-    select_token<EPL>(sp, lg, sel_lds[wave], e, w);
+    select_token<EPL>(sp, lg, bv, sel_lds[wave], e, w);
     if (lane < sp.k) {
       const int o = wave * sp.k + lane;
       ids[o] = e;
@@ -157,7 +194,9 @@ extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
                        0, stream, g);
     LMOE_RETURN_LAUNCH();
   }
-  const int tpb = 16;
+  // kGateTok tokens per block: blocks (bx, by) read the same weight rows
+  // (from L2 after the first, and on one XCD when E / 4 is a multiple of 8)
+  const int tpb = kGateTok;
   dim3 grid((E + 3) / 4, (T + tpb - 1) / tpb);
   const int nc = (H + 511) / 512;
 #define LMOE_GATE(NC)                                                              \

@@ -4,10 +4,11 @@
 // Selection order is (score desc, expert id asc), the order torch.topk gives
 // with ties to the lower id.  Instead of k serial rounds of wave arg-max,
 // each score becomes an order-preserving 32-bit key and a most-significant-
-// bit-first radix select (one ballot per expert slot and bit) finds the k-th
-// largest key and how many of the experts equal to it are taken; the taken
-// experts (the lowest ids among the equal ones) are compacted with ballots
-// and only those k are ranked against each other through LDS.
+// bit-first radix select (one ballot per expert slot and bit, stopping once
+// the prefix found is shared by exactly the experts still needed) finds the
+// k-th largest key's prefix; the taken experts (the lowest ids among equal
+// keys) are compacted with ballots and only those k are ranked against each
+// other through LDS.
 //
 // Reference behaviour: moe_router_op.py:191-278 (gate then select_experts),
 // renorm contract patches/patch_fused_moe.py:597-632
@@ -63,11 +64,13 @@ __device__ __forceinline__ bool better(float v, int e, float v2, int e2) {
 }
 
 // Selects the k experts of one token from its logits lg[j] (expert j*64 +
-// lane, -inf beyond E; EPL*64 >= E).  Lane l < k returns the l-th selected
-// expert id (-1 if fewer than k are eligible) and its final f32 weight.
+// lane, -inf beyond E; EPL*64 >= E) and the correction bias bv[j]
+// (load_bias; used only when sp.bias is set).  Lane l < k returns the l-th
+// selected expert id (-1 if fewer than k are eligible) and its final f32
+// weight.
 template <int EPL>
 __device__ __forceinline__ void select_token(const SelectParams& sp,
-                                             float (&lg)[EPL],
+                                             float (&lg)[EPL], const float (&bv)[EPL],
                                              SelectLds<EPL>& L, int& out_e,
                                              float& out_w) {
   const int lane = threadIdx.x & 63;
@@ -82,7 +85,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
 #pragma unroll
       for (int j = 0; j < EPL; ++j) {
         const int e = j * kWave + lane;
-        if (e < E) lg[j] = lg[j] + sp.bias[e];
+        if (e < E) lg[j] = lg[j] + bv[j];
       }
     }
     float m = -INFINITY;
@@ -111,7 +114,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     for (int j = 0; j < EPL; ++j) {
       const int e = j * kWave + lane;
       const float sg = sigmoid_det(lg[j]);
-      const float sb = (e < E && sp.bias != nullptr) ? sg + sp.bias[e] : sg;
+      const float sb = (e < E && sp.bias != nullptr) ? sg + bv[j] : sg;
       sel[j] = sb;
       wgt[j] = sg;
       elig[j] = e < E;
@@ -181,22 +184,29 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     key[j] = elig[j] ? o : 0u;
   }
-  // 2. radix select, most significant bit first: thr = the k-th largest key,
-  //    need = how many experts with key == thr are taken (the lowest ids)
+  // 2. radix select, most significant bit first.  Invariant: thr holds the
+  //    bits above b of the k-th largest key (tmask marks them), `match`
+  //    experts share that prefix and `need` of them are still to be taken.
+  //    Stops as soon as match == need (all of them are taken), or after bit
+  //    0 with ties on the full key (the lowest ids are taken).
+  int match = 0;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) match += __popcll(__builtin_amdgcn_ballot_w64(key[j] != 0u));
   uint32_t thr = 0u, tmask = 0u;
   int need = k;
-#pragma unroll 4
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t bit = 1u << b;
-    int cnt = 0;
+  for (int b = 31; b >= 0 && match > need; --b) {
+    const uint32_t tgt = (thr >> b) | 1u;  // prefix with bit b set
+    int c1 = 0;
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const bool c = (key[j] != 0u) & ((key[j] & tmask) == thr) & ((key[j] & bit) != 0u);
-      cnt += __popcll(__ballot(c));
+    for (int j = 0; j < EPL; ++j) c1 += __popcll(__builtin_amdgcn_ballot_w64((key[j] >> b) == tgt));
+    if (c1 >= need) {
+      thr |= 1u << b;
+      match = c1;
+    } else {
+      need -= c1;
+      match -= c1;
     }
-    if (cnt >= need) thr |= bit;
-    else need -= cnt;
-    tmask |= bit;
+    tmask |= 1u << b;
   }
   // 3. the taken experts (k, or every eligible one if fewer), compacted in
   //    id order, then each ranked among the others by (key desc, id asc)
@@ -208,12 +218,13 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = j * kWave + lane;
-    const bool eq = (key[j] != 0u) & (key[j] == thr);
-    const uint64_t beq = __ballot(eq);
-    const bool take = (key[j] != 0u) &
-                      ((key[j] > thr) | (eq & (eq_before + __popcll(beq & lanemask_lt(lane)) < need)));
+    const uint32_t pre = key[j] & tmask;
+    const bool live = key[j] != 0u;
+    const bool eq = live & (pre == thr);
+    const uint64_t beq = __builtin_amdgcn_ballot_w64(eq);
+    const bool take = live & ((pre > thr) | (eq & (eq_before + __popcll(beq & lanemask_lt(lane)) < need)));
     eq_before += __popcll(beq);
-    const uint64_t bt = __ballot(take);
+    const uint64_t bt = __builtin_amdgcn_ballot_w64(take);
     if (take) {
       const int idx = C + __popcll(bt & lanemask_lt(lane));
       L.cand[idx] = make_float2(__uint_as_float(key[j]), __int_as_float(e));
@@ -268,6 +279,18 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     out_w = w * sp.routed_scale;
   }
   wave_lds_sync();  // the scratch may be reused by the next token
+}
+
+// Correction bias in the lane layout (0 where absent).  Issued before the
+// logits so that both loads are in flight together.
+template <int EPL>
+__device__ __forceinline__ void load_bias(const SelectParams& sp, float (&bv)[EPL]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = j * kWave + lane;
+    bv[j] = (sp.bias != nullptr && e < sp.E) ? sp.bias[e] : 0.0f;
+  }
 }
 
 // Logits of token t in the lane layout (expert j*64 + lane), -inf beyond E.

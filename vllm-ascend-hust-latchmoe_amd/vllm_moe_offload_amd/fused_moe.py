@@ -5,7 +5,8 @@ slot bank in place of the expert weights: lmoe_permute remaps the top-k ids
 through log2phy and sorts the pairs by slot, then either
 
   * lmoe_fused_moe_decode (<= 1024 pairs): gate_up GEMV + SiLU*mul, then the
-    down GEMV fused with the weighted combine — 3 kernels per layer; or
+    down GEMV fused with the weighted combine (one token), or the down GEMV
+    per (row block, slot) into y and the combine (several tokens); or
   * lmoe_grouped_mlp (GEMV or bf16 MFMA) into a flat-pair buffer y, then
     lmoe_combine.
 
@@ -142,7 +143,8 @@ def fused_experts(
     dst = out if out is not None else ws.out[:T]
     native.permute(topk_ids, ws.perm, log2phy=log2phy)
     if T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA:
-        native.fused_moe_decode(hidden, topk_weights, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add)
+        native.fused_moe_decode(hidden, topk_weights, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add,
+                                y=ws.y[: T * k])
     else:
         native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
         native.combine(ws.y[: T * k], topk_weights, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
@@ -189,7 +191,8 @@ def decode_layer(
     )
     dst = out if out is not None else ws.out[:T]
     if T * k <= native.FUSED_DECODE_MAX_PAIRS:
-        native.fused_moe_decode(hidden, w, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add)
+        native.fused_moe_decode(hidden, w, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add,
+                                y=ws.y[: T * k])
     else:
         native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k])
         native.combine(ws.y[: T * k], w, dst, row_mask=ws.perm.row_idx[: T * k], add=add)

@@ -84,7 +84,8 @@ _SIGNATURES = {
     "lmoe_combine": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "lmoe_fused_moe_decode": (
         _i,
-        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+         _vp],
     ),
     "lmoe_down_combine": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "lmoe_stage_copy": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
@@ -521,9 +522,12 @@ def fused_moe_decode(
     out: torch.Tensor,
     *,
     add: torch.Tensor | None = None,
+    y: torch.Tensor | None = None,
     stream=None,
 ) -> torch.Tensor:
-    """Decode layer body: gate_up GEMV, then down GEMV fused with the combine."""
+    """Decode layer body: gate_up GEMV, then down GEMV fused with the combine
+    (T == 1 or no y), or for T > 1 with a [T*k, H] bf16 workspace y the down
+    GEMV per (row block, slot) into y and the combine; same out either way."""
     lib = load_library()
     _need(x, "x", torch.bfloat16)
     T, H = x.shape
@@ -538,11 +542,13 @@ def fused_moe_decode(
     _need(out, "out", torch.bfloat16, (T, H))
     if add is not None:
         _need(add, "add", torch.bfloat16, (T, H))
+    if y is not None:
+        _need(y, "y", torch.bfloat16, (perm.n_pairs, H))
     _check(
         lib.lmoe_fused_moe_decode(
             _ptr(x), T, H, I, k, _ptr(w13_slots), _ptr(w2_slots), P, _ptr(topk_weights),
             _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.row_idx), _ptr(perm.active),
-            _ptr(perm.meta), _ptr(add), _ptr(act), _ptr(out), _stream(stream),
+            _ptr(perm.meta), _ptr(add), _ptr(act), _ptr(y), _ptr(out), _stream(stream),
         ),
         "lmoe_fused_moe_decode",
     )
