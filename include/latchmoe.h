@@ -26,6 +26,8 @@
  *                      renorm contract of patches/patch_fused_moe.py:597-632
  *   lmoe_router_topk_permute  select_experts then remap + init routing in
  *                      one launch (decode with a final slot table)
+ *   lmoe_router_gate_topk_permute  gate, select_experts, remap + init
+ *                      routing in one launch (same decode case)
  *   lmoe_permute       log2phy remap moe_offload/slot_mapping.py:116-140 and
  *                      npu_moe_init_routing_v2, patch_fused_moe.py:668-701
  *                      (stable sort by slot, expanded_row_idx, count histogram)
@@ -120,6 +122,31 @@ int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
                              int32_t* sorted_pairs, int32_t* row_idx,
                              int32_t* active, int32_t* tile_off,
                              int32_t* meta, hipStream_t stream);
+
+/* lmoe_router_gate, lmoe_router_topk and lmoe_permute (same arguments, same
+ * outputs, bit for bit; logits is still written) in one launch, for the same
+ * final-table decode case as lmoe_router_topk_permute: gate(hidden)
+ * (moe_router_op.py:228-231), select_experts (:108-124) and remap + init
+ * routing (slot_mapping.py:116-140, patch_fused_moe.py:668-701).  The gate
+ * workgroups store their logits and count themselves in on *sync; the last
+ * one to arrive runs the selection and the permutation and resets *sync to 0.
+ * sync is one int32, zero before the first call (it is left at zero after
+ * every call); calls that may run concurrently need separate sync words.
+ * Returns LMOE_ERR_SHAPE when T > 16, E > 256, n_slots > 8192, H % 8 != 0,
+ * H > 8192 or x / wg are not 16-byte aligned (then use the separate calls). */
+int lmoe_router_gate_topk_permute(const void* x, const void* wg, int T, int H,
+                                  int E, void* logits, int logits_f32, int k,
+                                  int scoring, const float* bias, int n_group,
+                                  int topk_group, int renorm,
+                                  float routed_scale, float* w_f32,
+                                  uint16_t* w_bf16, int32_t* ids,
+                                  const int32_t* log2phy, int n_log2phy,
+                                  int n_slots, int skip_unmapped, int block_m,
+                                  int32_t* counts, int32_t* offsets,
+                                  int32_t* sorted_pairs, int32_t* row_idx,
+                                  int32_t* active, int32_t* tile_off,
+                                  int32_t* meta, int32_t* sync,
+                                  hipStream_t stream);
 
 /* Bytes of device workspace lmoe_permute needs for n_pairs pairs, n_slots. */
 size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);

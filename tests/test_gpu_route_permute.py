@@ -153,3 +153,53 @@ def test_decode_layer_equals_route_then_fused_experts(T):
         a, b = getattr(ws_a.perm, name), getattr(ws_b.perm, name)
         n = T * k if name in ("sorted_pairs", "row_idx") else a.numel()
         assert torch.equal(a[:n], b[:n]), name
+
+
+@pytest.mark.parametrize("T,E,k,P,H,scoring,f32", [
+    (1, 128, 8, 64, 2048, "softmax", False),
+    (4, 128, 8, 64, 2048, "softmax", True),
+    (16, 128, 8, 128, 2048, "softmax", False),   # 1024-thread blocks, block permutation
+    (3, 60, 4, 16, 512, "softmax", False),       # E not a multiple of the waves per block
+    (8, 256, 8, 128, 7168, "sigmoid", False),    # grouped sigmoid, long rows
+])
+def test_gate_select_permute_one_launch_equals_separate_calls(T, E, k, P, H, scoring, f32):
+    """lmoe_router_gate_topk_permute == lmoe_router_gate then
+    lmoe_router_topk_permute, bit for bit, over three calls in a row (the
+    arrival counter must be back at zero after each)."""
+    native = _native()
+    print(f"case gate-topk-permute T={T} E={E} k={k} P={P} H={H} {scoring} f32={f32}", flush=True)
+    rng = np.random.default_rng(70 + T + E)
+    grouped = scoring == "sigmoid"
+    kw = dict(scoring=scoring, num_expert_group=8 if grouped else 1, topk_group=4 if grouped else 1,
+              routed_scaling_factor=2.5 if grouped else 1.0)
+    bias = torch.from_numpy((rng.standard_normal(E) * (0.01 if grouped else 0.5)).astype(np.float32)).cuda()
+    dt = torch.float32 if f32 else torch.bfloat16
+    wg = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
+    perm_a = native.Permutation.allocate(T * k, P, "cuda")
+    perm_b = native.Permutation.allocate(T * k, P, "cuda")
+    for it in range(3):
+        x = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
+        # slot table covering whatever this step selects
+        lg0 = torch.empty((T, E), dtype=dt, device="cuda")
+        native.router_gate(x, wg, lg0)
+        _, ids0, _ = native.router_topk(lg0, k, bias=bias, **kw)
+        used = np.unique(ids0.cpu().numpy())
+        l2p = np.full(E, -1, dtype=np.int32)
+        l2p[used] = rng.permutation(P)[: used.size]
+        d_l2p = to_dev_i32(l2p)
+        lg_a = torch.empty((T, E), dtype=dt, device="cuda")
+        native.router_gate(x, wg, lg_a)
+        wa, ida, wfa = native.router_topk_permute(lg_a, k, perm_a, log2phy=d_l2p, bias=bias,
+                                                  w_f32=torch.empty((T, k), device="cuda"), **kw)
+        lg_b = torch.empty((T, E), dtype=dt, device="cuda")
+        wb, idb, wfb = native.router_gate_topk_permute(x, wg, lg_b, k, perm_b, log2phy=d_l2p, bias=bias,
+                                                       w_f32=torch.empty((T, k), device="cuda"), **kw)
+        torch.cuda.synchronize()
+        view = torch.int32 if f32 else torch.int16
+        assert torch.equal(lg_a.view(view), lg_b.view(view)), it
+        assert torch.equal(ida, idb), it
+        assert torch.equal(wa.view(torch.int16), wb.view(torch.int16)), it
+        assert torch.equal(wfa.view(torch.int32), wfb.view(torch.int32)), it
+        for name in ("counts", "offsets", "sorted_pairs", "row_idx", "active", "tile_off", "meta"):
+            assert torch.equal(getattr(perm_a, name), getattr(perm_b, name)), (it, name)
+        assert perm_b.sync.item() == 0

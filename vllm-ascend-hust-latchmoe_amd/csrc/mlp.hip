@@ -31,7 +31,7 @@ namespace lmoe {
 // several tokens per step needs twice the registers, and the lost occupancy
 // costs more than the shorter chain saves: measured slower at B = 4 and 16.)
 // ---------------------------------------------------------------------------
-template <int NC, bool SPLIT>
+template <int NC, bool SPLIT, bool ONE>
 __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, int H, int I, int topk,
     const uint16_t* __restrict__ w13, const int32_t* __restrict__ offsets,
@@ -39,12 +39,41 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     const int32_t* __restrict__ meta, uint16_t* __restrict__ act) {
   __shared__ float s_up[2];
   const int a = blockIdx.y;  // < n_slots: active[] has an entry (-1 past the active slots)
-  const int s = active[a];
-  if (s < 0) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int p0 = offsets[s];
-  const int n = offsets[s + 1] - p0;
+  if (ONE && !SPLIT) {
+    // one token: its x row needs no index, so it is loaded before active[a]
+    // returns, and the weight rows wait on that one load only
+    uint4 xv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int h = c * 512 + lane * 8;
+      xv[c] = (h < H) ? *reinterpret_cast<const uint4*>(x + h) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    const int s = active[a];
+    const int i = blockIdx.x * 4 + wave;
+    if (s < 0 || i >= I) return;
+    const uint16_t* grow = w13 + (static_cast<size_t>(s) * 2 * I + i) * H;
+    const uint16_t* urow = grow + static_cast<size_t>(I) * H;
+    float v[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int h = c * 512 + lane * 8;
+      if (h < H) {
+        v[0] = dot8(xv[c], load_stream16(grow + h), v[0]);
+        v[1] = dot8(xv[c], load_stream16(urow + h), v[1]);
+      }
+    }
+    const float tot = reduce_scatter<2, 5, 0>(v, lane);
+    const float up = __shfl_xor(tot, 32, kWave);
+    if (lane == 0) act[static_cast<size_t>(a) * I + i] = swiglu_bf16(tot, up);
+    return;
+  }
+  const int s = active[a];
+  if (s < 0) return;
+  // one token: active rank a is sorted position a and serves one pair
+  const int p0 = ONE ? a : offsets[s];
+  const int n = ONE ? 1 : offsets[s + 1] - p0;
   if (!SPLIT) {
     const int i = blockIdx.x * 4 + wave;
     if (i >= I) return;
@@ -92,7 +121,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
       wr[c] = (ok && h < H) ? load_stream16(row + h) : make_uint4(0u, 0u, 0u, 0u);
     }
     for (int r = 0; r < n; ++r) {
-      const int t = sorted_pairs[p0 + r] / topk;
+      const int t = ONE ? 0 : sorted_pairs[p0 + r] / topk;
       const uint16_t* xr = x + static_cast<size_t>(t) * H;
       float acc = 0.0f;
 #pragma unroll
@@ -124,7 +153,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 constexpr int kFusedMaxPairs = 1024;
 constexpr int kDnMaxRows = 4;
 
-template <int DNC, int R, bool PF>
+template <int DNC, int R, bool PF, bool ONE>
 __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     const uint16_t* __restrict__ act, int I, int H, int T, int topk,
     const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
@@ -133,6 +162,8 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     const uint16_t* __restrict__ add, uint16_t* __restrict__ out) {
   constexpr int LV = (R >= 4) ? 2 : 1;
   __shared__ float s_y[kFusedMaxPairs * kDnMaxRows];
+  __shared__ int s_pos[kFusedMaxPairs];
+  __shared__ float s_w[kFusedMaxPairs];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int l5 = lane & 31;
@@ -158,6 +189,21 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
   int rank = hw;
   int s_cur = rank < P ? active[rank] : -1;
   if (s_cur >= 0) load_rows(s_cur, wcur);
+  // the combine's per-pair inputs, loaded behind the first W2 rows so they
+  // arrive with them instead of one dependent round trip per pair at the end
+  const int NP = T * topk;
+  int pre_pos[kFusedMaxPairs / 256];
+  float pre_w[kFusedMaxPairs / 256];
+#pragma unroll
+  for (int u = 0; u < kFusedMaxPairs / 256; ++u) {
+    const int p = tid + u * 256;
+    pre_pos[u] = p < NP ? row_idx[p] : -1;
+    pre_w[u] = p < NP ? bf16_to_f32(wts[p]) : 0.0f;
+  }
+  // add term of this thread's first output (T * R <= 256 covers decode)
+  const float pre_add = (add != nullptr && tid < T * R && h0 + tid % R < H)
+                            ? bf16_to_f32(add[static_cast<size_t>(tid / R) * H + h0 + tid % R])
+                            : 0.0f;
   // both halves of a wave run the loop together (shuffles span the wave)
   while (__ballot(s_cur >= 0) != 0ull) {
     const int nrank = rank + 8;
@@ -165,8 +211,9 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     if constexpr (PF) {
       if (s_nxt >= 0) load_rows(s_nxt, wnxt);
     }
-    const int p0 = s_cur >= 0 ? offsets[s_cur] : 0;
-    const int n = s_cur >= 0 ? offsets[s_cur + 1] - p0 : 0;
+    // one token: active rank r is sorted position r and serves one pair
+    const int p0 = s_cur >= 0 ? (ONE ? rank : offsets[s_cur]) : 0;
+    const int n = s_cur >= 0 ? (ONE ? 1 : offsets[s_cur + 1] - p0) : 0;
     const int n_other = __shfl_xor(n, 32, kWave);
     const int n_max = n > n_other ? n : n_other;
     for (int q = 0; q < n_max; ++q) {
@@ -202,8 +249,16 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
       if (s_cur >= 0) load_rows(s_cur, wcur);
     }
   }
+#pragma unroll
+  for (int u = 0; u < kFusedMaxPairs / 256; ++u) {
+    s_pos[tid + u * 256] = pre_pos[u];
+    s_w[tid + u * 256] = pre_w[u];
+  }
   __syncthreads();
-  for (int qq = tid; qq < T * R; qq += 256) {
+#pragma unroll
+  for (int u = 0; u < kFusedMaxPairs * kDnMaxRows / 256; ++u) {
+    const int qq = tid + u * 256;
+    if (qq >= T * R) break;
     const int t = qq / R;
     const int r = qq % R;
     const int h = h0 + r;
@@ -211,10 +266,11 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     float acc = 0.0f;
     for (int j = 0; j < topk; ++j) {
       const int p = t * topk + j;
-      const int pos = row_idx[p];
-      if (pos >= 0) acc += bf16_to_f32(wts[p]) * s_y[pos * kDnMaxRows + r];
+      const int pos = s_pos[p];
+      if (pos >= 0) acc += s_w[p] * s_y[pos * kDnMaxRows + r];
     }
-    if (add != nullptr) acc += bf16_to_f32(add[static_cast<size_t>(t) * H + h]);
+    if (add != nullptr)
+      acc += u == 0 ? pre_add : bf16_to_f32(add[static_cast<size_t>(t) * H + h]);
     out[static_cast<size_t>(t) * H + h] = static_cast<uint16_t>(f32_to_bf16_bits(acc));
   }
 }
@@ -353,17 +409,25 @@ __global__ __launch_bounds__(256) void combine_kernel(
 // ---------------------------------------------------------------------------
 // launch helpers
 // ---------------------------------------------------------------------------
+// one: T == 1 (every slot serves at most one pair; log2phy maps distinct
+// experts to distinct slots).
 static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
                               const uint16_t* w13, const int32_t* offsets,
                               const int32_t* sorted_pairs, const int32_t* active,
-                              const int32_t* meta, int max_active, uint16_t* act,
+                              const int32_t* meta, int max_active, bool one, uint16_t* act,
                               hipStream_t stream) {
   const int nc = (H + 511) / 512;
   const dim3 g4((I + 3) / 4, max_active);
   const dim3 g2((I + 1) / 2, max_active);
-#define LMOE_GU(NC, SPLIT, G)                                                        \
-  hipLaunchKernelGGL((gateup_gemv_kernel<NC, SPLIT>), G, dim3(256), 0, stream, x, H, \
-                     I, topk, w13, offsets, sorted_pairs, active, meta, act)
+#define LMOE_GU(NC, SPLIT, G)                                                                 \
+  do {                                                                                        \
+    if (one)                                                                                  \
+      hipLaunchKernelGGL((gateup_gemv_kernel<NC, SPLIT, true>), G, dim3(256), 0, stream, x, H, \
+                         I, topk, w13, offsets, sorted_pairs, active, meta, act);             \
+    else                                                                                      \
+      hipLaunchKernelGGL((gateup_gemv_kernel<NC, SPLIT, false>), G, dim3(256), 0, stream, x,   \
+                         H, I, topk, w13, offsets, sorted_pairs, active, meta, act);          \
+  } while (0)
   if (nc <= 2) LMOE_GU(2, false, g4);
   else if (nc <= 4) LMOE_GU(4, false, g4);
   else if (nc <= 8) LMOE_GU(8, false, g4);
@@ -466,7 +530,8 @@ extern "C" int lmoe_gateup_silu(const void* x, int T, int H, int I, int k,
   if (path == LMOE_PATH_GEMV) {
     st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
                             static_cast<const uint16_t*>(w13_slots), offsets, sorted_pairs,
-                            active, meta, max_active, static_cast<uint16_t*>(act), stream);
+                            active, meta, max_active, T == 1, static_cast<uint16_t*>(act),
+                            stream);
     if (st != LMOE_OK) return st;
     LMOE_RETURN_LAUNCH();
   }
@@ -565,11 +630,22 @@ extern "C" int lmoe_down_combine(const void* act, int T, int H, int I, int k,
     return LMOE_ERR_SHAPE;
   if (T == 0) return LMOE_OK;
   const int dnc = (I + 255) / 256;
-#define LMOE_DC(DNC, R, PF)                                                                  \
-  hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, PF>), dim3((H + R - 1) / R), dim3(256), \
-                     0, stream, static_cast<const uint16_t*>(act), I, H, T, k,               \
-                     static_cast<const uint16_t*>(w2_slots), offsets, active, n_slots, row_idx, \
-                     w, static_cast<const uint16_t*>(add), static_cast<uint16_t*>(out))
+#define LMOE_DC(DNC, R, PF)                                                                    \
+  do {                                                                                         \
+    const dim3 grid((H + R - 1) / R);                                                          \
+    const uint16_t* a_ = static_cast<const uint16_t*>(act);                                    \
+    const uint16_t* w2_ = static_cast<const uint16_t*>(w2_slots);                              \
+    const uint16_t* add_ = static_cast<const uint16_t*>(add);                                  \
+    uint16_t* out_ = static_cast<uint16_t*>(out);                                              \
+    if (T == 1)                                                                                \
+      hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, PF, true>), grid, dim3(256), 0,      \
+                         stream, a_, I, H, T, k, w2_, offsets, active, n_slots, row_idx, w,     \
+                         add_, out_);                                                          \
+    else                                                                                       \
+      hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, PF, false>), grid, dim3(256), 0,     \
+                         stream, a_, I, H, T, k, w2_, offsets, active, n_slots, row_idx, w,     \
+                         add_, out_);                                                          \
+  } while (0)
   if (dnc <= 2) LMOE_DC(2, 4, true);
   else if (dnc <= 3) LMOE_DC(3, 4, true);
   else if (dnc <= 4) LMOE_DC(4, 4, true);
@@ -605,7 +681,7 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
   int st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
                               static_cast<const uint16_t*>(w13_slots), offsets,
-                              sorted_pairs, active, meta, max_active,
+                              sorted_pairs, active, meta, max_active, T == 1,
                               static_cast<uint16_t*>(act), stream);
   if (st != LMOE_OK) return st;
   if (y != nullptr && T > 1) {

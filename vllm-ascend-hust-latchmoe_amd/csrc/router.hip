@@ -16,20 +16,15 @@ namespace lmoe {
 constexpr int kGateMaxChunks = 16;  // H <= 16 * 512 = 8192 in the GEMV path
 constexpr int kGateTok = 4;         // tokens per reduction in the gate GEMV
 
-// logits[t][e] for e = 4*blockIdx.x + wave, tokens [t0, t1).  The expert row
-// stays in registers (one 16-byte chunk per 512 columns per lane) while the
-// token rows stream through L1.
+// logits[t][e] of one expert e for tokens [t0, t1), by the calling wave.
+// The expert row stays in registers (one 16-byte chunk per 512 columns per
+// lane) while the token rows stream through L1.
 template <int NC>
-__global__ __launch_bounds__(256) void gate_gemv_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T,
-    int H, int E, int tokens_per_block, void* __restrict__ logits,
-    int logits_f32) {
+__device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
+                                         const uint16_t* __restrict__ wg, int t0, int t1,
+                                         int H, int E, int e, void* __restrict__ logits,
+                                         int logits_f32) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int e = blockIdx.x * 4 + wave;
-  if (e >= E) return;
-  const int t0 = blockIdx.y * tokens_per_block;
-  const int t1 = min(T, t0 + tokens_per_block);
   const uint16_t* wrow = wg + static_cast<size_t>(e) * H;
 
   uint4 w[NC];
@@ -94,6 +89,18 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
   }
 }
 
+// logits[t][e] for e = 4*blockIdx.x + wave, tokens of block row blockIdx.y.
+template <int NC>
+__global__ __launch_bounds__(256) void gate_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T,
+    int H, int E, int tokens_per_block, void* __restrict__ logits,
+    int logits_f32) {
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= E) return;
+  const int t0 = blockIdx.y * tokens_per_block;
+  gate_row<NC>(x, wg, t0, min(T, t0 + tokens_per_block), H, E, e, logits, logits_f32);
+}
+
 // One wave per token; EPL experts per lane (EPL*64 >= E).
 template <int EPL>
 __global__ __launch_bounds__(256) void topk_kernel(
@@ -125,19 +132,25 @@ __global__ __launch_bounds__(256) void topk_kernel(
 // output equals what lmoe_router_topk followed by lmoe_permute writes.
 constexpr int kFusedTopkTokens = 16;
 
+// Selection of T <= kFusedTopkTokens tokens (wave t selects token t) and the
+// permutation of their pairs, by one block of at least T waves.
 template <int EPL>
-__global__ __launch_bounds__(1024) void topk_permute_kernel(
-    const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
+struct TopkPermuteLds {
+  SelectLds<EPL> sel[kFusedTopkTokens];
+  int32_t ids[kFusedTopkTokens * kMaxK];
+  int scan[33];
+  int err;
+};
+
+template <int EPL>
+__device__ __forceinline__ void select_and_permute(
+    const void* __restrict__ logits, int logits_f32, int T, const SelectParams& sp,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
     const int32_t* __restrict__ log2phy, int n_log2phy, int P, int skip, int block_m,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
-    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
-  extern __shared__ int hist[];  // [P]
-  __shared__ SelectLds<EPL> sel_lds[kFusedTopkTokens];
-  __shared__ int32_t ids_lds[kFusedTopkTokens * kMaxK];
-  __shared__ int scan_lds[33];
-  __shared__ int err_lds;
+    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
+    int* hist, TopkPermuteLds<EPL>& L) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   if (wave < T) {
@@ -146,11 +159,11 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
     load_logits<EPL>(logits, logits_f32, wave, sp.E, lg);
     int e;
     float w;
-    select_token<EPL>(sp, lg, bv, sel_lds[wave], e, w);
+    select_token<EPL>(sp, lg, bv, L.sel[wave], e, w);
     if (lane < sp.k) {
       const int o = wave * sp.k + lane;
       ids[o] = e;
-      ids_lds[o] = e;
+      L.ids[o] = e;
       w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
       if (w_f32 != nullptr) w_f32[o] = w;
     }
@@ -159,12 +172,68 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
   const int n_pairs = T * sp.k;
   if (n_pairs <= kWave && wave_perm_spl(P) > 0) {
     if (wave == 0)
-      permute_wave_any(ids_lds, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
+      permute_wave_any(L.ids, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
                        sorted_pairs, row_idx, active, tile_off, meta, hist);
   } else {
-    permute_block(ids_lds, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
-                  sorted_pairs, row_idx, active, tile_off, meta, hist, scan_lds, &err_lds);
+    permute_block(L.ids, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
+                  sorted_pairs, row_idx, active, tile_off, meta, hist, L.scan, &L.err);
   }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(1024) void topk_permute_kernel(
+    const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
+    float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
+    const int32_t* __restrict__ log2phy, int n_log2phy, int P, int skip, int block_m,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
+    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
+  extern __shared__ int hist[];  // [max(P, 64 * wave_perm_spl(P))]
+  __shared__ TopkPermuteLds<EPL> L;
+  select_and_permute<EPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids, log2phy, n_log2phy, P,
+                          skip, block_m, counts, offsets, sorted_pairs, row_idx, active,
+                          tile_off, meta, hist, L);
+}
+
+// Gate, selection and permutation in one launch.  Block b's waves compute
+// the logits of experts b * nw + wave for all T tokens and store them; the
+// block then counts itself in with a release fence and an atomic add on
+// *sync.  The last block to arrive (the add returns gridDim.x - 1) takes an
+// acquire fence, resets *sync to 0 for the next launch, and runs the
+// selection and the permutation over everything the others stored.  No block
+// ever waits for another: the last one only starts once all have finished
+// their stores.  Calls that may run concurrently need separate sync words.
+template <int NC, int EPL>
+__global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T, int H,
+    void* __restrict__ logits, int logits_f32, SelectParams sp, float* __restrict__ w_f32,
+    uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
+    const int32_t* __restrict__ log2phy, int n_log2phy, int P, int skip, int block_m,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
+    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
+    int32_t* __restrict__ sync) {
+  extern __shared__ int hist[];  // [max(P, 64 * wave_perm_spl(P))]
+  __shared__ TopkPermuteLds<EPL> L;
+  __shared__ int last;
+  const int nw = blockDim.x >> 6;
+  const int e = blockIdx.x * nw + (threadIdx.x >> 6);
+  if (e < sp.E) gate_row<NC>(x, wg, 0, T, H, sp.E, e, logits, logits_f32);
+  __syncthreads();  // every wave's logits are stored before thread 0 counts the block in
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int prev = __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == static_cast<int>(gridDim.x) - 1;
+    if (last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (!last) return;
+  select_and_permute<EPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids, log2phy, n_log2phy, P,
+                          skip, block_m, counts, offsets, sorted_pairs, row_idx, active,
+                          tile_off, meta, hist, L);
 }
 
 }  // namespace lmoe
@@ -304,5 +373,64 @@ extern "C" int lmoe_router_topk_permute(
   else if (E <= 128) LMOE_TP(2);
   else LMOE_TP(4);
 #undef LMOE_TP
+  LMOE_RETURN_LAUNCH();
+}
+
+extern "C" int lmoe_router_gate_topk_permute(
+    const void* x, const void* wg, int T, int H, int E, void* logits, int logits_f32, int k,
+    int scoring, const float* bias, int n_group, int topk_group, int renorm, float routed_scale,
+    float* w_f32, uint16_t* w_bf16, int32_t* ids, const int32_t* log2phy, int n_log2phy,
+    int n_slots, int skip_unmapped, int block_m, int32_t* counts, int32_t* offsets,
+    int32_t* sorted_pairs, int32_t* row_idx, int32_t* active, int32_t* tile_off, int32_t* meta,
+    int32_t* sync, hipStream_t stream) {
+  if (x == nullptr || wg == nullptr || logits == nullptr || w_bf16 == nullptr || ids == nullptr ||
+      counts == nullptr || offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
+      active == nullptr || tile_off == nullptr || meta == nullptr || sync == nullptr)
+    return LMOE_ERR_ARG;
+  if (T < 0 || H <= 0) return LMOE_ERR_ARG;
+  int st = check_select(T, E, k, scoring, n_group, topk_group);
+  if (st != LMOE_OK) return st;
+  if (n_slots <= 0 || block_m <= 0) return LMOE_ERR_ARG;
+  if (log2phy != nullptr && n_log2phy <= 0) return LMOE_ERR_ARG;
+  if (H % 8 != 0 || H > kGateMaxChunks * 512) return LMOE_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(wg)) & 15u)
+    return LMOE_ERR_SHAPE;
+  // the last block holds the whole selection and permutation
+  if (T > kFusedTopkTokens || E > 256 || n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
+  if (T == 0) return LMOE_OK;
+  const SelectParams sp =
+      make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  const int n_pairs = T * k;
+  int threads = n_pairs > n_slots / 16 ? n_pairs : n_slots / 16;
+  threads = threads > T * 64 ? threads : T * 64;
+  threads = threads > 256 ? threads : 256;  // four gate rows per block at least
+  threads = ((threads + 63) / 64) * 64;
+  threads = threads > kChunk ? kChunk : threads;
+  const int nw = threads / 64;
+  const int blocks = (E + nw - 1) / nw;
+  size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
+  if (n_pairs <= kWave && wave_perm_spl(n_slots) > 0) {
+    const size_t wlds = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(n_slots));
+    lds = wlds > lds ? wlds : lds;
+  }
+  const int skip = skip_unmapped ? 1 : 0;
+  const int nc = (H + 511) / 512;
+#define LMOE_GTP(NC, EPL)                                                                       \
+  hipLaunchKernelGGL((gate_topk_permute_kernel<NC, EPL>), dim3(blocks), dim3(threads), lds,     \
+                     stream, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(wg), \
+                     T, H, logits, logits_f32, sp, w_f32, w_bf16, ids, log2phy, n_log2phy,      \
+                     n_slots, skip, block_m, counts, offsets, sorted_pairs, row_idx, active,    \
+                     tile_off, meta, sync)
+#define LMOE_GTP_E(NC)            \
+  do {                            \
+    if (E <= 64) LMOE_GTP(NC, 1); \
+    else if (E <= 128) LMOE_GTP(NC, 2); \
+    else LMOE_GTP(NC, 4);         \
+  } while (0)
+  if (nc <= 4) LMOE_GTP_E(4);
+  else if (nc <= 8) LMOE_GTP_E(8);
+  else LMOE_GTP_E(16);
+#undef LMOE_GTP_E
+#undef LMOE_GTP
   LMOE_RETURN_LAUNCH();
 }

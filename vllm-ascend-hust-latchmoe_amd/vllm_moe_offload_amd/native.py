@@ -36,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "lmoe_router_gate",
     "lmoe_router_topk",
     "lmoe_router_topk_permute",
+    "lmoe_router_gate_topk_permute",
     "lmoe_permute_workspace_bytes",
     "lmoe_permute",
     "lmoe_gather_rows",
@@ -65,6 +66,11 @@ _SIGNATURES = {
         _i,
         [_vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
          _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
+    "lmoe_router_gate_topk_permute": (
+        _i,
+        [_vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
+         _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "lmoe_permute_workspace_bytes": (_sz, [_i, _i]),
     "lmoe_permute": (
@@ -292,6 +298,83 @@ def router_topk_permute(
     return w_bf16, ids, w_f32
 
 
+def router_gate_topk_permute(
+    x: torch.Tensor,
+    wg: torch.Tensor,
+    logits: torch.Tensor,
+    top_k: int,
+    perm: "Permutation",
+    *,
+    log2phy: torch.Tensor | None = None,
+    skip_unmapped: bool = False,
+    block_m: int | None = None,
+    scoring: str = "softmax",
+    bias: torch.Tensor | None = None,
+    num_expert_group: int = 1,
+    topk_group: int = 1,
+    renormalize: bool = True,
+    routed_scaling_factor: float = 1.0,
+    w_bf16: torch.Tensor | None = None,
+    ids: torch.Tensor | None = None,
+    w_f32: torch.Tensor | None = None,
+    stream=None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """router_gate, router_topk and permute into perm in one launch when the
+    shape allows it (T <= 16, E <= 256, H <= 8192); otherwise router_gate and
+    router_topk_permute.  Same outputs bit for bit; logits is written too.
+    Uses perm.sync as the arrival counter: calls that may run concurrently
+    need separate Permutation buffers."""
+    lib = load_library()
+    T, H = x.shape
+    E = wg.shape[0]
+    _need(x, "x", torch.bfloat16)
+    _need(wg, "wg", torch.bfloat16, (E, H))
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("logits must be bf16 or f32")
+    _need(logits, "logits", logits.dtype, (T, E))
+    mode = {"softmax": LMOE_SCORING_SOFTMAX, "sigmoid": LMOE_SCORING_SIGMOID}.get(scoring)
+    if mode is None:
+        raise ValueError(f"unsupported scoring function {scoring!r}")
+    if bias is not None:
+        _need(bias, "e_score_correction_bias", torch.float32, (E,))
+    dev = x.device
+    if w_bf16 is None:
+        w_bf16 = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
+    if ids is None:
+        ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    _need(w_bf16, "topk_weights", torch.bfloat16, (T, top_k))
+    _need(ids, "topk_ids", torch.int32, (T, top_k))
+    if w_f32 is not None:
+        _need(w_f32, "w_f32", torch.float32, (T, top_k))
+    if T * top_k != perm.n_pairs:
+        raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {T * top_k}")
+    n_table = 0
+    if log2phy is not None:
+        _need(log2phy, "log2phy", torch.int32)
+        n_table = int(log2phy.numel())
+    bm = MFMA_BLOCK_M if block_m is None else int(block_m)
+    status = lib.lmoe_router_gate_topk_permute(
+        _ptr(x), _ptr(wg), T, H, E, _ptr(logits), int(logits.dtype == torch.float32), int(top_k),
+        mode, _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
+        int(bool(renormalize)), float(routed_scaling_factor),
+        _ptr(w_f32), _ptr(w_bf16), _ptr(ids),
+        _ptr(log2phy), n_table, perm.n_slots, int(bool(skip_unmapped)), bm,
+        _ptr(perm.counts), _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.row_idx),
+        _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta), _ptr(perm.sync), _stream(stream),
+    )
+    if status == LMOE_ERR_SHAPE:
+        router_gate(x, wg, logits, stream=stream)
+        return router_topk_permute(
+            logits, top_k, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, block_m=bm,
+            scoring=scoring, bias=bias, num_expert_group=num_expert_group, topk_group=topk_group,
+            renormalize=renormalize, routed_scaling_factor=routed_scaling_factor, w_bf16=w_bf16,
+            ids=ids, w_f32=w_f32, stream=stream,
+        )
+    _check(status, "lmoe_router_gate_topk_permute")
+    perm.block_m = bm
+    return w_bf16, ids, w_f32
+
+
 # ---------------------------------------------------------------------------
 # permutation
 # ---------------------------------------------------------------------------
@@ -312,6 +395,7 @@ class Permutation:
     tile_off: torch.Tensor      # [P+1] i32 MFMA tile prefix
     meta: torch.Tensor          # [4] i32
     workspace: torch.Tensor     # int8 scratch for the multi-block path
+    sync: torch.Tensor          # [1] i32 arrival counter of the one-launch router, kept at 0
     block_m: int = MFMA_BLOCK_M  # tile height tile_off was last built with
 
     @classmethod
@@ -330,6 +414,7 @@ class Permutation:
             tile_off=torch.zeros(n_slots + 1, **i32),
             meta=torch.zeros(META_COUNT, **i32),
             workspace=torch.empty(max(ws, 1), dtype=torch.int8, device=device),
+            sync=torch.zeros(1, **i32),
         )
 
 
