@@ -215,9 +215,15 @@ __global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
     int32_t* __restrict__ sync) {
   extern __shared__ int hist[];  // [max(P, 64 * wave_perm_spl(P))]
   __shared__ TopkPermuteLds<EPL> L;
+  __shared__ int32_t l2p_lds[kMaxE];
   __shared__ int last;
   const int nw = blockDim.x >> 6;
   const int e = blockIdx.x * nw + (threadIdx.x >> 6);
+  // every block copies the slot table while its gate rows load, so that the
+  // last one remaps the selected ids from LDS
+  const bool l2p_in_lds = log2phy != nullptr && n_log2phy <= kMaxE;
+  if (l2p_in_lds)
+    for (int i = threadIdx.x; i < n_log2phy; i += blockDim.x) l2p_lds[i] = log2phy[i];
   if (e < sp.E) gate_row<NC>(x, wg, 0, T, H, sp.E, e, logits, logits_f32);
   __syncthreads();  // every wave's logits are stored before thread 0 counts the block in
   if (threadIdx.x == 0) {
@@ -231,9 +237,9 @@ __global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
   }
   __syncthreads();
   if (!last) return;
-  select_and_permute<EPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids, log2phy, n_log2phy, P,
-                          skip, block_m, counts, offsets, sorted_pairs, row_idx, active,
-                          tile_off, meta, hist, L);
+  select_and_permute<EPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids,
+                          l2p_in_lds ? l2p_lds : log2phy, n_log2phy, P, skip, block_m, counts,
+                          offsets, sorted_pairs, row_idx, active, tile_off, meta, hist, L);
 }
 
 }  // namespace lmoe
