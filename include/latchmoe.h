@@ -260,6 +260,17 @@ int lmoe_stage_copy(void* const* dst, const void* const* src,
                     const size_t* bytes, int n, hipStream_t transfer_stream,
                     hipEvent_t wait_event, hipEvent_t done_event);
 
+/* table[idx[i]] = val[i] for i < n, on stream; the idx must be distinct
+ * (LMOE_ERR_ARG otherwise).  idx and val are HOST arrays read during the
+ * call; the pairs travel as kernel arguments (no staging buffer, no copy),
+ * so the update is capturable and can follow a stage copy batch on the
+ * transfer stream, inside the same ready event.  Every idx must lie in
+ * [0, n_table).  Replaces the persistent-log2phy write of
+ * _update_log2phy_entries (moe_offload/runtime.py:3068-3101: one scalar
+ * write, or an index_copy_ of the changed entries). */
+int lmoe_table_update(int32_t* table, int n_table, const int32_t* idx,
+                      const int32_t* val, int n, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,9 +53,21 @@ def _nbytes(t: torch.Tensor) -> int:
     return int(t.numel()) * int(t.element_size())
 
 
+_CUDA_AVAILABLE: bool | None = None
+
+
+def _cuda_available() -> bool:
+    """torch.cuda.is_available(), asked once (it costs microseconds per call
+    on the per-layer staging path)."""
+    global _CUDA_AVAILABLE
+    if _CUDA_AVAILABLE is None:
+        _CUDA_AVAILABLE = bool(torch.cuda.is_available())
+    return _CUDA_AVAILABLE
+
+
 def _is_current_graph_capturing() -> bool:
     try:
-        return bool(torch.cuda.is_available() and torch.cuda.is_current_stream_capturing())
+        return bool(_cuda_available() and torch.cuda.is_current_stream_capturing())
     except Exception:
         return False
 
@@ -127,6 +139,7 @@ class PendingFixedSlotStage:
     log2phy: torch.Tensor
     step_id: int
     started: float
+    table_updates: int = -1  # entries already written with the copies (-1: publish writes them)
 
 
 @dataclass(frozen=True)
@@ -576,12 +589,28 @@ class MoeOffloadRuntime:
             self._layer_release_events[int(layer_id)] = ev
 
     # ------------------------------------------------------ decode staging
+    def _compute_device_index(self) -> int | None:
+        """Device index of the first device slot bank (None: host-only banks).
+        Passing it to current_stream() skips torch's device lookup."""
+        for b in self._slot_banks.values():
+            if b.w13_slots.device.type == "cuda":
+                idx = b.w13_slots.device.index
+                return int(idx) if idx is not None else int(torch.cuda.current_device())
+        return None
+
+    def _consumer_stream(self):
+        """The current stream of the slot banks' device (a no-op stream for
+        host-only banks)."""
+        idx = self._compute_device_index()
+        return _NullStream() if idx is None else torch.cuda.current_stream(idx)
+
     def _record_current_stream_event_or_none(self):
         """Completion event of the compute stream (None for host-only banks)."""
-        if not any(b.w13_slots.device.type == "cuda" for b in self._slot_banks.values()):
+        idx = self._compute_device_index()
+        if idx is None:
             return None
         ev = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream())
+        ev.record(torch.cuda.current_stream(idx))
         return ev
 
     def prepare_fixed_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int,
@@ -650,7 +679,8 @@ class MoeOffloadRuntime:
         bank = self._slot_banks.get(layer_id)
         if bank is None:
             raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
-        if any(s.state in (SlotState.LOADING, SlotState.COMPUTING) for s in bank.slots):
+        states = [s.state for s in bank.slots]
+        if SlotState.LOADING in states or SlotState.COMPUTING in states:
             self._drain_slot_bank_inflight_work(bank)
         step_id = self._step(step_id)
         t0 = perf_counter()
@@ -690,17 +720,27 @@ class MoeOffloadRuntime:
                 self._release_allocated_loads(bank, sync_loads)
                 raise
         ready = None
+        table_updates = -1
         if async_loads:
+            # device bank and table: the changed log2phy entries ride with the
+            # copies on the transfer stream, inside their ready event
+            with_table = log2phy.device.type == "cuda" and bank.w13_slots.device.type == "cuda"
+            upd = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=slot_ids) \
+                if with_table else ((), ())
+            extra = {"table_update": (log2phy, upd[0], upd[1])} if upd[0] else {}
             try:
                 ready = self._transfer_engine.load_many_async(
                     async_loads, wait_event=self._layer_release_events.get(layer_id), record_event=True,
-                    validate_layout=False,
+                    validate_layout=False, **extra,
                 )
             except Exception:
                 self._release_allocated_loads(bank, async_loads)
                 raise
+            if with_table:
+                self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd[0], slot_ids=upd[1])
+                table_updates = len(upd[0])
         return PendingFixedSlotStage(layer_id, active, tuple(slot_ids), owners, ready, tuple(hits), tuple(misses),
-                                     log2phy, step_id, t0)
+                                     log2phy, step_id, t0, table_updates)
 
     def _publish(self, pending: PendingFixedSlotStage, *, record_stage_profile: bool) -> PreparedSlotWeights:
         layer_id = pending.layer_id
@@ -709,10 +749,14 @@ class MoeOffloadRuntime:
         if pending.ready is not None:
             self._wait_transfer_event(pending.ready)
         active, slot_ids, owners = pending.active, pending.slot_ids, pending.owners
-        upd_e, upd_s = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=slot_ids)
-        if upd_e:
-            _update_log2phy_entries(pending.log2phy, expert_ids=upd_e, slot_ids=upd_s)
-            self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd_e, slot_ids=upd_s)
+        if pending.table_updates >= 0:
+            n_updates = pending.table_updates  # written on the transfer stream with the copies
+        else:
+            upd_e, upd_s = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=slot_ids)
+            if upd_e:
+                _update_log2phy_entries(pending.log2phy, expert_ids=upd_e, slot_ids=upd_s)
+                self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd_e, slot_ids=upd_s)
+            n_updates = len(upd_e)
         for e, sid in zip(active, slot_ids):
             owners[sid] = e
         mapping = ExpertSlotMapping(layer_id, active, pending.log2phy, tuple(owners), tuple(slot_ids))
@@ -733,7 +777,7 @@ class MoeOffloadRuntime:
                     "step_id": pending.step_id,
                     "num_slots": int(self.config.num_slots),
                     "mapping_mode": "persistent_log2phy",
-                    "log2phy_update_count": len(upd_e),
+                    "log2phy_update_count": n_updates,
                     "stage_mode": "main_slot_hit" if not pending.misses else (
                         "async_decode_load_many" if pending.ready is not None else "sync_decode_load"),
                     "consumer_dependency_installed": True,
@@ -855,12 +899,12 @@ class MoeOffloadRuntime:
         if ready_event is None:
             return
         install = getattr(ready_event, "install_consumer_dependency", None)
-        if callable(install):
-            install(_current_stream_for(ready_event))
-            return
         ev = getattr(ready_event, "event", ready_event)
+        if callable(install):
+            install(self._consumer_stream() if isinstance(ev, torch.cuda.Event) else _NullStream())
+            return
         if isinstance(ev, torch.cuda.Event):
-            torch.cuda.current_stream().wait_event(ev)
+            self._consumer_stream().wait_event(ev)
         mark = getattr(ready_event, "mark_ready", None)
         if callable(mark):
             mark()
@@ -1180,13 +1224,6 @@ def _synchronize_event(ev: object) -> None:
         wait()
 
 
-def _current_stream_for(ready_event):
-    ev = getattr(ready_event, "event", None)
-    if isinstance(ev, torch.cuda.Event) and torch.cuda.is_available():
-        return torch.cuda.current_stream()
-    return _NullStream()
-
-
 class _NullStream:
     def wait_event(self, _event) -> None:  # host-only slot banks need no ordering
         return None
@@ -1202,24 +1239,21 @@ def _validate_active_expert_ids(*, layer_id: int, active_experts, num_logical_ex
 
 
 def _update_log2phy_entries(log2phy: torch.Tensor, *, expert_ids, slot_ids) -> None:
-    """Write the changed entries of a persistent log2phy in one tensor op."""
+    """Write the changed entries of a persistent log2phy in one operation
+    (reference: runtime.py:3068-3101, one scalar write or an index_copy_)."""
     if len(expert_ids) != len(slot_ids):
         raise ValueError(f"expert_ids and slot_ids length mismatch: {len(expert_ids)} != {len(slot_ids)}")
     if not expert_ids:
         return
-    if len(expert_ids) == 1:
-        log2phy[int(expert_ids[0])] = int(slot_ids[0])
-        return
-    n = len(expert_ids)
     if log2phy.device.type != "cuda":
         idx = torch.tensor([int(e) for e in expert_ids], dtype=torch.long)
         log2phy.index_copy_(0, idx, torch.tensor([int(v) for v in slot_ids], dtype=log2phy.dtype))
         return
-    # one page-locked staging tensor and an asynchronous copy: no host sync
-    # (the caching host allocator keeps it alive until the copy has run)
-    host = torch.tensor([int(e) for e in expert_ids] + [int(v) for v in slot_ids], dtype=torch.int32).pin_memory()
-    dev = host.to(log2phy.device, non_blocking=True)
-    log2phy.index_copy_(0, dev[:n].long(), dev[n:].to(log2phy.dtype))
+    # one kernel on the current stream whose arguments carry the pairs: no
+    # staging tensor, no copy, no host sync
+    from vllm_moe_offload_amd import native
+
+    native.table_update_entries(log2phy, expert_ids, slot_ids)
 
 
 _runtime: MoeOffloadRuntime | None = None

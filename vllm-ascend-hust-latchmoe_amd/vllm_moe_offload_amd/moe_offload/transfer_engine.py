@@ -98,9 +98,11 @@ class TransferEngine:
         return self.load_many_async([(bundle, slot)], wait_event=wait_event, record_event=record_event)
 
     def load_many_async(self, loads: list[Load], *, wait_event=None, record_event: bool = True,
-                        validate_layout: bool = True):
+                        validate_layout: bool = True, table_update=None):
         """Queue the loads on the transfer stream; returns a TransferReadyEvent
-        (or None when the copy completed synchronously)."""
+        (or None when the copy completed synchronously).  table_update =
+        (device int32 table, indices, values) is written on the transfer
+        stream after the copies, before the ready event (device slots only)."""
         if not loads:
             return None
         if validate_layout:
@@ -118,7 +120,8 @@ class TransferEngine:
         for _, slot in loads:
             slot.state = SlotState.LOADING
         done = torch.cuda.Event() if record_event else None
-        self._copy(tuple(loads), stream=stream, wait_event=_torch_event(wait_event), done_event=done)
+        self._copy(tuple(loads), stream=stream, wait_event=_torch_event(wait_event), done_event=done,
+                   table_update=table_update)
         slots = tuple(slot for _, slot in loads)
         if done is None:
             stream.synchronize()
@@ -147,7 +150,8 @@ class TransferEngine:
         return self._h2d_stream
 
     # -- copies -----------------------------------------------------------
-    def _copy(self, loads: tuple[Load, ...], *, stream, wait_event=None, done_event=None) -> None:
+    def _copy(self, loads: tuple[Load, ...], *, stream, wait_event=None, done_event=None,
+              table_update=None) -> None:
         runs = contiguous_load_runs(loads)
         if stream is None:
             for run in runs:
@@ -165,7 +169,8 @@ class TransferEngine:
                 src, dst = getattr(b0, name), getattr(s0, name)
                 nbytes = int(src.numel()) * int(src.element_size()) * n
                 copies.append((int(dst.data_ptr()), int(src.data_ptr()), nbytes))
-        native.stage_copy(copies, stream, wait_event=wait_event, done_event=done_event)
+        native.stage_copy(copies, stream, wait_event=wait_event, done_event=done_event,
+                          table_update=table_update)
         self.copies_issued += len(copies)
         self.bytes_issued += sum(c[2] for c in copies)
 

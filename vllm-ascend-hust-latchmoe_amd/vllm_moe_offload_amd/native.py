@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "lmoe_fused_moe_decode",
     "lmoe_down_combine",
     "lmoe_stage_copy",
+    "lmoe_table_update",
 )
 
 _vp = ctypes.c_void_p
@@ -95,6 +96,7 @@ _SIGNATURES = {
     ),
     "lmoe_down_combine": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "lmoe_stage_copy": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
+    "lmoe_table_update": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -681,12 +683,15 @@ def stage_copy(
     *,
     wait_event: torch.cuda.Event | None = None,
     done_event: torch.cuda.Event | None = None,
+    table_update: tuple[torch.Tensor, tuple, tuple] | None = None,
 ) -> None:
     """Queue (dst_ptr, src_ptr, nbytes) copies on transfer_stream.
 
     The stream first waits for wait_event (slot release) and done_event is
     recorded after the batch; both are torch events, ordered through torch so
-    their lazily created handles stay valid.
+    their lazily created handles stay valid.  table_update = (table,
+    indices, values) writes those int32 entries after the copies, inside the
+    same done_event (the slot table that publishes the staged experts).
     """
     lib = load_library()
     if wait_event is not None:
@@ -699,5 +704,24 @@ def stage_copy(
         lib.lmoe_stage_copy(dst, src, nbytes, n, int(transfer_stream.cuda_stream), None, None),
         "lmoe_stage_copy",
     )
+    if table_update is not None:
+        table, idx, val = table_update
+        table_update_entries(table, idx, val, stream=transfer_stream)
     if done_event is not None:
         done_event.record(transfer_stream)
+
+
+def table_update_entries(table: torch.Tensor, idx, val, *, stream=None) -> None:
+    """table[idx[i]] = val[i] (distinct int indices) with one small kernel
+    whose arguments carry the pairs: no staging tensor, no copy."""
+    lib = load_library()
+    _need(table, "table", torch.int32)
+    n = len(idx)
+    if n != len(val):
+        raise ValueError(f"indices and values differ in length: {n} != {len(val)}")
+    if n == 0:
+        return
+    ia = (ctypes.c_int32 * n)(*[int(i) for i in idx])
+    va = (ctypes.c_int32 * n)(*[int(v) for v in val])
+    _check(lib.lmoe_table_update(_ptr(table), int(table.numel()), ia, va, n, _stream(stream)),
+           "lmoe_table_update")
