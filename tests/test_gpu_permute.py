@@ -114,3 +114,21 @@ def test_permute_is_stable_across_repeated_launches():
         native.permute(d, perm)
     torch.cuda.synchronize()
     assert torch.equal(first, perm.sorted_pairs)
+
+
+@pytest.mark.parametrize("n_table,n", [(128, 1), (128, 9), (300, 150)])  # 150: three launches of 64
+def test_table_update_writes_exactly_the_pairs(n_table, n):
+    """lmoe_table_update (the staging path's log2phy write) against numpy."""
+    from vllm_moe_offload_amd import native
+
+    print(f"case table-update n_table={n_table} n={n}", flush=True)
+    rng = np.random.default_rng(n_table + n)
+    init = rng.integers(-1, 64, n_table).astype(np.int32)
+    table = torch.from_numpy(init.copy()).cuda()
+    idx = rng.permutation(n_table)[:n].astype(np.int32)
+    val = rng.integers(-1, 64, n).astype(np.int32)
+    native.table_update_entries(table, idx.tolist(), val.tolist())
+    torch.cuda.synchronize()
+    ref = init.copy()
+    ref[idx] = val
+    np.testing.assert_array_equal(table.cpu().numpy(), ref)

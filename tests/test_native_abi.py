@@ -46,6 +46,14 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert lib.lmoe_permute_workspace_bytes(1024, 64) == 0
     assert lib.lmoe_permute_workspace_bytes(32768, 48) > 0
     assert lib.lmoe_stage_copy(None, None, None, 0, None, None, None) == 0
+    # slot-table update: indices must be distinct and inside the table
+    i3 = (ctypes.c_int32 * 3)
+    tbl = ctypes.c_void_p(16)
+    assert lib.lmoe_table_update(tbl, 8, i3(1, 5, 1), i3(0, 1, 2), 3, None) == 1000
+    assert lib.lmoe_table_update(tbl, 8, i3(1, 8, 2), i3(0, 1, 2), 3, None) == 1000
+    assert lib.lmoe_table_update(tbl, 8, i3(-1, 3, 2), i3(0, 1, 2), 3, None) == 1000
+    assert lib.lmoe_table_update(None, 8, i3(1, 3, 2), i3(0, 1, 2), 3, None) == 1000
+    assert lib.lmoe_table_update(None, 8, None, None, 0, None) == 0
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
