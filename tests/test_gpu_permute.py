@@ -38,7 +38,10 @@ def _check(perm, ref, n_pairs):
 @pytest.mark.parametrize("T,k,E,P,use_map", [
     (1, 8, 128, 64, True),
     (8, 8, 128, 32, False),
-    (16, 8, 128, 64, True),
+    (16, 8, 128, 64, True),     # one wave, two pairs per lane
+    (24, 8, 128, 64, True),     # one wave, four pairs per lane (partly filled)
+    (32, 8, 1024, 1024, False), # one wave: 256 pairs, 16 slots per lane
+    (40, 6, 8, 8, False),       # one wave, ~30 pairs per slot across the pair groups
     (64, 8, 128, 64, True),
     (128, 8, 128, 128, False),
     (129, 8, 128, 64, True),
@@ -62,7 +65,7 @@ def test_permute_matches_oracle(T, k, E, P, use_map, block_m):
     _check(perm, orc.init_routing(ids, P, log2phy=log2phy, block_m=block_m), T * k)
 
 
-@pytest.mark.parametrize("N,P", [(64, 16), (5000, 40)])
+@pytest.mark.parametrize("N,P", [(64, 16), (200, 16), (5000, 40)])
 def test_permute_skip_unmapped_wave_filter(N, P):
     native = _native()
     rng = np.random.default_rng(N)

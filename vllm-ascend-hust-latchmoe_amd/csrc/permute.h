@@ -202,11 +202,14 @@ __device__ __forceinline__ void permute_block(
   }
 }
 
-// One wave permutes N <= 64 pairs over P <= 64 * SPL slots (the decode
-// sizes) with ballots, shuffles and LDS, but no block barrier: pair p is lane
-// p, slot s is owned by lane s / SPL.  Same outputs as permute_block.
-// lds: at least 64 * SPL ints of the calling wave's own LDS.
+// One wave permutes N <= 64 * PPL pairs over P <= 64 * SPL slots (the
+// decode sizes) with ballots, shuffles and LDS, but no block barrier: pair
+// p = 64 g + lane belongs to group g of lane `lane`, slot s is owned by lane
+// s / SPL.  Groups are ranked in order, so pairs of one slot keep their flat
+// order.  Same outputs as permute_block.  lds: at least 64 * SPL ints of the
+// calling wave's own LDS.
 constexpr int kWavePermMaxSlotsPerLane = 16;
+constexpr int kWavePermMaxPairsPerLane = 4;
 
 __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 #pragma unroll
@@ -217,7 +220,7 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
   return v;
 }
 
-template <int SPL>
+template <int SPL, int PPL>
 __device__ __forceinline__ void permute_wave(
     const int32_t* ids, int N, const int32_t* __restrict__ log2phy, int n_log2phy, int P,
     int skip, int block_m, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
@@ -225,18 +228,33 @@ __device__ __forceinline__ void permute_wave(
     int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
     int* lds) {
   const int lane = threadIdx.x & 63;
-  const bool have = lane < N;
-  const int s = have ? map_pair(ids, lane, log2phy, n_log2phy, P, skip) : -1;
-  const bool placed = s >= 0;
-  const int errs = __popcll(__ballot(have && s == -2));
-  // pairs of the same slot, and this pair's rank among them (flat order)
   const int nbits = key_bits(P);
-  const uint64_t m = match_key(placed ? s : (1 << nbits) - 1, nbits);
-  const int rank = __popcll(m & lanemask_lt(lane));
+  int s[PPL], rank[PPL], cnt[PPL];
+  int errs = 0;
+#pragma unroll
+  for (int g = 0; g < PPL; ++g) {
+    const int p = g * kWave + lane;
+    const bool have = p < N;
+    s[g] = have ? map_pair(ids, p, log2phy, n_log2phy, P, skip) : -1;
+    errs += __popcll(__ballot(have && s[g] == -2));
+  }
 #pragma unroll
   for (int i = 0; i < SPL; ++i) lds[lane * SPL + i] = 0;
   wave_lds_sync();
-  if (placed && rank == 0) lds[s] = __popcll(m);
+  // pairs of the same slot within each group, this pair's rank among them,
+  // and the slot counts (the group's first pair of a slot adds the group's
+  // count; one LDS add per slot and group)
+#pragma unroll
+  for (int g = 0; g < PPL; ++g) {
+    const bool placed = s[g] >= 0;
+    const uint64_t m = match_key(placed ? s[g] : (1 << nbits) - 1, nbits);
+    rank[g] = __popcll(m & lanemask_lt(lane));
+    cnt[g] = __popcll(m);
+    if (placed && rank[g] == 0) {
+      if constexpr (PPL == 1) lds[s[g]] = cnt[g];  // one group: one writer per slot
+      else atomicAdd(&lds[s[g]], cnt[g]);
+    }
+  }
   wave_lds_sync();
   // this lane's slots s0 .. s0+SPL-1: counts, then wave-wide prefixes
   const int s0 = lane * SPL;
@@ -280,11 +298,22 @@ __device__ __forceinline__ void permute_wave(
     meta[LMOE_META_ERRORS] = errs;
     meta[LMOE_META_TILES] = ttot;
   }
-  wave_lds_sync();
-  if (have) {
-    const int pos = placed ? lds[s] + rank : -1;
-    row_idx[lane] = pos;
-    if (pos >= 0) sorted_pairs[pos] = lane;
+  // groups in flat order: read the slot's running base, then its first
+  // pair of the group advances it past the group's pairs
+#pragma unroll
+  for (int g = 0; g < PPL; ++g) {
+    wave_lds_sync();
+    const int p = g * kWave + lane;
+    const bool placed = s[g] >= 0;
+    const int pos = placed ? lds[s[g]] + rank[g] : -1;
+    if constexpr (PPL > 1) {
+      wave_lds_sync();
+      if (placed && rank[g] == 0) lds[s[g]] = pos + cnt[g];
+    }
+    if (p < N) {
+      row_idx[p] = pos;
+      if (pos >= 0) sorted_pairs[pos] = p;
+    }
   }
 }
 
@@ -296,8 +325,21 @@ __host__ __device__ inline int wave_perm_spl(int P) {
   return spl <= kWavePermMaxSlotsPerLane ? spl : 0;
 }
 
-// permute_wave for any P <= 64 * kWavePermMaxSlotsPerLane (lds: 64 *
-// wave_perm_spl(P) ints).
+// Pairs per lane of permute_wave for N pairs (0 when N exceeds the wave path).
+__host__ __device__ inline int wave_perm_ppl(int N) {
+  return N <= kWave ? 1 : N <= 2 * kWave ? 2 : N <= 4 * kWave ? 4 : 0;
+}
+
+// Whether one wave permutes N pairs over P slots.
+__host__ __device__ inline bool wave_perm_fits(int N, int P) {
+  return wave_perm_ppl(N) > 0 && wave_perm_spl(P) > 0;
+}
+
+// permute_wave with PPL pairs per lane for any P <= 64 *
+// kWavePermMaxSlotsPerLane (lds: 64 * wave_perm_spl(P) ints).  PPL is a
+// template parameter of the callers' kernels: one pair layout per kernel
+// keeps the latency-bound routers' code (and registers) small.
+template <int PPL>
 __device__ __forceinline__ void permute_wave_any(
     const int32_t* ids, int N, const int32_t* __restrict__ log2phy, int n_log2phy, int P,
     int skip, int block_m, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
@@ -305,9 +347,9 @@ __device__ __forceinline__ void permute_wave_any(
     int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
     int* lds) {
   const int spl = wave_perm_spl(P);
-#define LMOE_PW(S)                                                                              \
-  permute_wave<S>(ids, N, log2phy, n_log2phy, P, skip, block_m, counts, offsets, sorted_pairs, \
-                  row_idx, active, tile_off, meta, lds)
+#define LMOE_PW(S)                                                                                  \
+  permute_wave<S, PPL>(ids, N, log2phy, n_log2phy, P, skip, block_m, counts, offsets, sorted_pairs, \
+                       row_idx, active, tile_off, meta, lds)
   if (spl <= 1) LMOE_PW(1);
   else if (spl == 2) LMOE_PW(2);
   else if (spl == 4) LMOE_PW(4);

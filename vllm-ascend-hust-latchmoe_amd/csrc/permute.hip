@@ -17,7 +17,8 @@ __global__ __launch_bounds__(1024) void permute_small_kernel(
                 row_idx, active, tile_off, meta, hist, scan_lds, &err_lds);
 }
 
-// Whole permutation by one wave (n_pairs <= 64, n_slots <= 1024).
+// Whole permutation by one wave (n_pairs <= 64 * PPL, n_slots <= 1024).
+template <int PPL>
 __global__ __launch_bounds__(64) void permute_wave_kernel(
     const int32_t* __restrict__ ids, int N, const int32_t* __restrict__ log2phy,
     int n_log2phy, int P, int skip, int block_m, int32_t* __restrict__ counts,
@@ -25,8 +26,8 @@ __global__ __launch_bounds__(64) void permute_wave_kernel(
     int32_t* __restrict__ row_idx, int32_t* __restrict__ active,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
   extern __shared__ int lds[];  // [64 * wave_perm_spl(P)]
-  permute_wave_any(ids, N, log2phy, n_log2phy, P, skip, block_m, counts, offsets, sorted_pairs,
-                   row_idx, active, tile_off, meta, lds);
+  permute_wave_any<PPL>(ids, N, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
+                        sorted_pairs, row_idx, active, tile_off, meta, lds);
 }
 
 // Multi-block path, step 1: per-chunk histograms.
@@ -145,12 +146,18 @@ extern "C" int lmoe_permute(const int32_t* ids, int n_pairs,
   if (n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
   const int skip = skip_unmapped ? 1 : 0;
   const size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
-  if (n_pairs <= kWave && wave_perm_spl(n_slots) > 0) {
+  if (wave_perm_fits(n_pairs, n_slots)) {
     // decode sizes: one wave, no block barriers
     const size_t wlds = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(n_slots));
-    hipLaunchKernelGGL(permute_wave_kernel, dim3(1), dim3(kWave), wlds, stream, ids, n_pairs,
-                       log2phy, n_log2phy, n_slots, skip, block_m, counts, offsets, sorted_pairs,
-                       row_idx, active, tile_off, meta);
+#define LMOE_PWK(Q)                                                                           \
+  hipLaunchKernelGGL(permute_wave_kernel<Q>, dim3(1), dim3(kWave), wlds, stream, ids, n_pairs, \
+                     log2phy, n_log2phy, n_slots, skip, block_m, counts, offsets, sorted_pairs,  \
+                     row_idx, active, tile_off, meta)
+    const int ppl = wave_perm_ppl(n_pairs);
+    if (ppl == 1) LMOE_PWK(1);
+    else if (ppl == 2) LMOE_PWK(2);
+    else LMOE_PWK(4);
+#undef LMOE_PWK
     LMOE_RETURN_LAUNCH();
   }
   if (n_pairs <= kChunk) {

@@ -142,7 +142,9 @@ struct TopkPermuteLds {
   int err;
 };
 
-template <int EPL>
+// PPL > 0: one wave permutes with PPL pairs per lane; PPL == 0: the block
+// permutation (more pairs or slots than one wave takes).
+template <int EPL, int PPL>
 __device__ __forceinline__ void select_and_permute(
     const void* __restrict__ logits, int logits_f32, int T, const SelectParams& sp,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
@@ -170,17 +172,23 @@ __device__ __forceinline__ void select_and_permute(
   }
   __syncthreads();
   const int n_pairs = T * sp.k;
-  if (n_pairs <= kWave && wave_perm_spl(P) > 0) {
+  if constexpr (PPL > 0) {
     if (wave == 0)
-      permute_wave_any(L.ids, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
-                       sorted_pairs, row_idx, active, tile_off, meta, hist);
+      permute_wave_any<PPL>(L.ids, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts,
+                            offsets, sorted_pairs, row_idx, active, tile_off, meta, hist);
   } else {
     permute_block(L.ids, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
                   sorted_pairs, row_idx, active, tile_off, meta, hist, L.scan, &L.err);
   }
 }
 
-template <int EPL>
+// Pair layout of the routers' permutation: pairs per lane of the one-wave
+// path, 0 for the block path.
+__host__ inline int router_perm_ppl(int n_pairs, int n_slots) {
+  return wave_perm_fits(n_pairs, n_slots) ? wave_perm_ppl(n_pairs) : 0;
+}
+
+template <int EPL, int PPL>
 __global__ __launch_bounds__(1024) void topk_permute_kernel(
     const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
@@ -190,9 +198,9 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
     int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
   extern __shared__ int hist[];  // [max(P, 64 * wave_perm_spl(P))]
   __shared__ TopkPermuteLds<EPL> L;
-  select_and_permute<EPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids, log2phy, n_log2phy, P,
-                          skip, block_m, counts, offsets, sorted_pairs, row_idx, active,
-                          tile_off, meta, hist, L);
+  select_and_permute<EPL, PPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids, log2phy,
+                               n_log2phy, P, skip, block_m, counts, offsets, sorted_pairs,
+                               row_idx, active, tile_off, meta, hist, L);
 }
 
 // Gate, selection and permutation in one launch.  Block b's waves compute
@@ -203,7 +211,7 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
 // selection and the permutation over everything the others stored.  No block
 // ever waits for another: the last one only starts once all have finished
 // their stores.  Calls that may run concurrently need separate sync words.
-template <int NC, int EPL>
+template <int NC, int EPL, int PPL>
 __global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T, int H,
     void* __restrict__ logits, int logits_f32, SelectParams sp, float* __restrict__ w_f32,
@@ -237,9 +245,10 @@ __global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
   }
   __syncthreads();
   if (!last) return;
-  select_and_permute<EPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids,
-                          l2p_in_lds ? l2p_lds : log2phy, n_log2phy, P, skip, block_m, counts,
-                          offsets, sorted_pairs, row_idx, active, tile_off, meta, hist, L);
+  select_and_permute<EPL, PPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids,
+                               l2p_in_lds ? l2p_lds : log2phy, n_log2phy, P, skip, block_m,
+                               counts, offsets, sorted_pairs, row_idx, active, tile_off, meta,
+                               hist, L);
 }
 
 }  // namespace lmoe
@@ -365,19 +374,27 @@ extern "C" int lmoe_router_topk_permute(
   threads = ((threads + 63) / 64) * 64;
   threads = threads < 64 ? 64 : (threads > kChunk ? kChunk : threads);
   size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
-  if (n_pairs <= kWave && wave_perm_spl(n_slots) > 0) {
+  if (wave_perm_fits(n_pairs, n_slots)) {
     const size_t wlds = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(n_slots));
     lds = wlds > lds ? wlds : lds;
   }
   const int skip = skip_unmapped ? 1 : 0;
-#define LMOE_TP(EPL)                                                                         \
-  hipLaunchKernelGGL(topk_permute_kernel<EPL>, dim3(1), dim3(threads), lds, stream, logits,  \
-                     logits_f32, T, sp, w_f32, w_bf16, ids, log2phy, n_log2phy, n_slots,    \
-                     skip, block_m, counts, offsets, sorted_pairs, row_idx, active, tile_off, \
-                     meta)
-  if (E <= 64) LMOE_TP(1);
-  else if (E <= 128) LMOE_TP(2);
-  else LMOE_TP(4);
+#define LMOE_TP(EPL, Q)                                                                        \
+  hipLaunchKernelGGL((topk_permute_kernel<EPL, Q>), dim3(1), dim3(threads), lds, stream, logits, \
+                     logits_f32, T, sp, w_f32, w_bf16, ids, log2phy, n_log2phy, n_slots, skip,  \
+                     block_m, counts, offsets, sorted_pairs, row_idx, active, tile_off, meta)
+#define LMOE_TP_Q(EPL)                  \
+  do {                                  \
+    if (ppl == 1) LMOE_TP(EPL, 1);      \
+    else if (ppl == 2) LMOE_TP(EPL, 2); \
+    else if (ppl == 4) LMOE_TP(EPL, 4); \
+    else LMOE_TP(EPL, 0);               \
+  } while (0)
+  const int ppl = router_perm_ppl(n_pairs, n_slots);
+  if (E <= 64) LMOE_TP_Q(1);
+  else if (E <= 128) LMOE_TP_Q(2);
+  else LMOE_TP_Q(4);
+#undef LMOE_TP_Q
 #undef LMOE_TP
   LMOE_RETURN_LAUNCH();
 }
@@ -415,28 +432,37 @@ extern "C" int lmoe_router_gate_topk_permute(
   const int nw = threads / 64;
   const int blocks = (E + nw - 1) / nw;
   size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
-  if (n_pairs <= kWave && wave_perm_spl(n_slots) > 0) {
+  if (wave_perm_fits(n_pairs, n_slots)) {
     const size_t wlds = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(n_slots));
     lds = wlds > lds ? wlds : lds;
   }
   const int skip = skip_unmapped ? 1 : 0;
   const int nc = (H + 511) / 512;
-#define LMOE_GTP(NC, EPL)                                                                       \
-  hipLaunchKernelGGL((gate_topk_permute_kernel<NC, EPL>), dim3(blocks), dim3(threads), lds,     \
-                     stream, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(wg), \
-                     T, H, logits, logits_f32, sp, w_f32, w_bf16, ids, log2phy, n_log2phy,      \
-                     n_slots, skip, block_m, counts, offsets, sorted_pairs, row_idx, active,    \
+#define LMOE_GTP(NC, EPL, Q)                                                                   \
+  hipLaunchKernelGGL((gate_topk_permute_kernel<NC, EPL, Q>), dim3(blocks), dim3(threads), lds,   \
+                     stream, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(wg),  \
+                     T, H, logits, logits_f32, sp, w_f32, w_bf16, ids, log2phy, n_log2phy,       \
+                     n_slots, skip, block_m, counts, offsets, sorted_pairs, row_idx, active,     \
                      tile_off, meta, sync)
-#define LMOE_GTP_E(NC)            \
-  do {                            \
-    if (E <= 64) LMOE_GTP(NC, 1); \
-    else if (E <= 128) LMOE_GTP(NC, 2); \
-    else LMOE_GTP(NC, 4);         \
+#define LMOE_GTP_Q(NC, EPL)                 \
+  do {                                      \
+    if (ppl == 1) LMOE_GTP(NC, EPL, 1);     \
+    else if (ppl == 2) LMOE_GTP(NC, EPL, 2); \
+    else if (ppl == 4) LMOE_GTP(NC, EPL, 4); \
+    else LMOE_GTP(NC, EPL, 0);              \
   } while (0)
+#define LMOE_GTP_E(NC)                  \
+  do {                                  \
+    if (E <= 64) LMOE_GTP_Q(NC, 1);     \
+    else if (E <= 128) LMOE_GTP_Q(NC, 2); \
+    else LMOE_GTP_Q(NC, 4);             \
+  } while (0)
+  const int ppl = router_perm_ppl(n_pairs, n_slots);
   if (nc <= 4) LMOE_GTP_E(4);
   else if (nc <= 8) LMOE_GTP_E(8);
   else LMOE_GTP_E(16);
 #undef LMOE_GTP_E
+#undef LMOE_GTP_Q
 #undef LMOE_GTP
   LMOE_RETURN_LAUNCH();
 }
