@@ -1,93 +1,13 @@
-// Router kernels: gate linear (bf16 GEMV, f32 accumulation) and expert
-// selection (softmax top-k, or sigmoid + correction bias + group-limited
-// top-k), one wave64 per token.
+// Router entry points: gate linear (bf16 GEMV, f32 accumulation; dense MFMA
+// GEMM for many tokens), expert selection, and the one-launch decode routers
+// whose kernels are instantiated per scoring mode in
+// router_fused_softmax.hip / router_fused_sigmoid.hip.
 //
 // Reference behaviour: moe_router_op.py:191-278 (gate then select_experts),
-// renorm contract patches/patch_fused_moe.py:597-632
-// (w / w.sum().clamp_min(eps)), grouped sigmoid as configured for the
-// DeepSeek-V3-style layer (bias for selection only, sum of the two best scores
-// per group, keep topk_group groups, renormalise, then scale).
-#include "gemm_mfma.h"
-#include "permute.h"
-#include "select.h"
+// renorm contract patches/patch_fused_moe.py:597-632.
+#include "router.h"
 
 namespace lmoe {
-
-constexpr int kGateMaxChunks = 16;  // H <= 16 * 512 = 8192 in the GEMV path
-constexpr int kGateTok = 4;         // tokens per reduction in the gate GEMV
-
-// logits[t][e] of one expert e for tokens [t0, t1), by the calling wave.
-// The expert row stays in registers (one 16-byte chunk per 512 columns per
-// lane) while the token rows stream through L1.
-template <int NC>
-__device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
-                                         const uint16_t* __restrict__ wg, int t0, int t1,
-                                         int H, int E, int e, void* __restrict__ logits,
-                                         int logits_f32) {
-  const int lane = threadIdx.x & 63;
-  const uint16_t* wrow = wg + static_cast<size_t>(e) * H;
-
-  uint4 w[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int h = c * 512 + lane * 8;
-    w[c] = (h < H) ? *reinterpret_cast<const uint4*>(wrow + h)
-                   : make_uint4(0u, 0u, 0u, 0u);
-  }
-  // kGateTok tokens per reduction (x rows in flight together; the same
-  // lane-pair tree per token as a lone wave_sum, so the logits do not depend
-  // on how tokens are grouped)
-  if (t1 - t0 == 1) {
-    const uint16_t* xr = x + static_cast<size_t>(t0) * H;
-    float acc = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int h = c * 512 + lane * 8;
-      if (h < H) acc = dot8(*reinterpret_cast<const uint4*>(xr + h), w[c], acc);
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) {
-      const size_t o = static_cast<size_t>(t0) * E + e;
-      if (logits_f32) {
-        reinterpret_cast<float*>(logits)[o] = acc;
-      } else {
-        reinterpret_cast<uint16_t*>(logits)[o] =
-            static_cast<uint16_t>(f32_to_bf16_bits(acc));
-      }
-    }
-    return;
-  }
-  for (int tb = t0; tb < t1; tb += kGateTok) {
-    const uint16_t* xr[kGateTok];
-#pragma unroll
-    for (int g = 0; g < kGateTok; ++g)
-      xr[g] = x + static_cast<size_t>(tb + g < t1 ? tb + g : t1 - 1) * H;
-    float v[kGateTok];
-#pragma unroll
-    for (int g = 0; g < kGateTok; ++g) v[g] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int h = c * 512 + lane * 8;
-      if (h < H) {
-#pragma unroll
-        for (int g = 0; g < kGateTok; ++g)
-          v[g] = dot8(*reinterpret_cast<const uint4*>(xr[g] + h), w[c], v[g]);
-      }
-    }
-    // lane l ends with the total of token tb + l / 16
-    const float acc = reduce_scatter<kGateTok, 5, 0>(v, lane);
-    const int t = tb + (lane >> 4);
-    if ((lane & 15) == 0 && t < t1) {
-      const size_t o = static_cast<size_t>(t) * E + e;
-      if (logits_f32) {
-        reinterpret_cast<float*>(logits)[o] = acc;
-      } else {
-        reinterpret_cast<uint16_t*>(logits)[o] =
-            static_cast<uint16_t>(f32_to_bf16_bits(acc));
-      }
-    }
-  }
-}
 
 // logits[t][e] for e = 4*blockIdx.x + wave, tokens of block row blockIdx.y.
 template <int NC>
@@ -98,11 +18,13 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
   const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (e >= E) return;
   const int t0 = blockIdx.y * tokens_per_block;
-  gate_row<NC>(x, wg, t0, min(T, t0 + tokens_per_block), H, E, e, logits, logits_f32);
+  const int t1 = min(T, t0 + tokens_per_block);
+  if (t1 - t0 == 1) gate_row<NC, true>(x, wg, t0, t1, H, E, e, logits, logits_f32);
+  else gate_row<NC, false>(x, wg, t0, t1, H, E, e, logits, logits_f32);
 }
 
 // One wave per token; EPL experts per lane (EPL*64 >= E).
-template <int EPL>
+template <int EPL, int SCORE>
 __global__ __launch_bounds__(256) void topk_kernel(
     const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
     float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16,
@@ -116,139 +38,13 @@ __global__ __launch_bounds__(256) void topk_kernel(
   load_logits<EPL>(logits, logits_f32, t < T ? t : 0, sp.E, lg);
   int e;
   float w;
-  select_token<EPL>(sp, lg, bv, lds[wave], e, w);
+  select_token<EPL, SCORE>(sp, lg, bv, lds[wave], e, w);
   if (t < T && lane < sp.k) {
     const size_t o = static_cast<size_t>(t) * sp.k + lane;
     ids[o] = e;
     w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
     if (w_f32 != nullptr) w_f32[o] = w;
   }
-}
-
-// Expert selection and the permutation of the selected pairs in one block,
-// for a slot table that is final before the router runs (decode replay
-// after staging).  Wave t selects token t (T <= kFusedTopkTokens); the ids
-// go to LDS and feed the same permutation as permute_small_kernel, so every
-// output equals what lmoe_router_topk followed by lmoe_permute writes.
-constexpr int kFusedTopkTokens = 16;
-
-// Selection of T <= kFusedTopkTokens tokens (wave t selects token t) and the
-// permutation of their pairs, by one block of at least T waves.
-template <int EPL>
-struct TopkPermuteLds {
-  SelectLds<EPL> sel[kFusedTopkTokens];
-  int32_t ids[kFusedTopkTokens * kMaxK];
-  int scan[33];
-  int err;
-};
-
-// PPL > 0: one wave permutes with PPL pairs per lane; PPL == 0: the block
-// permutation (more pairs or slots than one wave takes).
-template <int EPL, int PPL>
-__device__ __forceinline__ void select_and_permute(
-    const void* __restrict__ logits, int logits_f32, int T, const SelectParams& sp,
-    float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
-    const int32_t* __restrict__ log2phy, int n_log2phy, int P, int skip, int block_m,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
-    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
-    int* hist, TopkPermuteLds<EPL>& L) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  if (wave < T) {
-    float bv[EPL], lg[EPL];
-    load_bias<EPL>(sp, bv);
-    load_logits<EPL>(logits, logits_f32, wave, sp.E, lg);
-    int e;
-    float w;
-    select_token<EPL>(sp, lg, bv, L.sel[wave], e, w);
-    if (lane < sp.k) {
-      const int o = wave * sp.k + lane;
-      ids[o] = e;
-      L.ids[o] = e;
-      w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
-      if (w_f32 != nullptr) w_f32[o] = w;
-    }
-  }
-  __syncthreads();
-  const int n_pairs = T * sp.k;
-  if constexpr (PPL > 0) {
-    if (wave == 0)
-      permute_wave_any<PPL>(L.ids, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts,
-                            offsets, sorted_pairs, row_idx, active, tile_off, meta, hist);
-  } else {
-    permute_block(L.ids, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
-                  sorted_pairs, row_idx, active, tile_off, meta, hist, L.scan, &L.err);
-  }
-}
-
-// Pair layout of the routers' permutation: pairs per lane of the one-wave
-// path, 0 for the block path.
-__host__ inline int router_perm_ppl(int n_pairs, int n_slots) {
-  return wave_perm_fits(n_pairs, n_slots) ? wave_perm_ppl(n_pairs) : 0;
-}
-
-template <int EPL, int PPL>
-__global__ __launch_bounds__(1024) void topk_permute_kernel(
-    const void* __restrict__ logits, int logits_f32, int T, SelectParams sp,
-    float* __restrict__ w_f32, uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
-    const int32_t* __restrict__ log2phy, int n_log2phy, int P, int skip, int block_m,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
-    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
-  extern __shared__ int hist[];  // [max(P, 64 * wave_perm_spl(P))]
-  __shared__ TopkPermuteLds<EPL> L;
-  select_and_permute<EPL, PPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids, log2phy,
-                               n_log2phy, P, skip, block_m, counts, offsets, sorted_pairs,
-                               row_idx, active, tile_off, meta, hist, L);
-}
-
-// Gate, selection and permutation in one launch.  Block b's waves compute
-// the logits of experts b * nw + wave for all T tokens and store them; the
-// block then counts itself in with a release fence and an atomic add on
-// *sync.  The last block to arrive (the add returns gridDim.x - 1) takes an
-// acquire fence, resets *sync to 0 for the next launch, and runs the
-// selection and the permutation over everything the others stored.  No block
-// ever waits for another: the last one only starts once all have finished
-// their stores.  Calls that may run concurrently need separate sync words.
-template <int NC, int EPL, int PPL>
-__global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T, int H,
-    void* __restrict__ logits, int logits_f32, SelectParams sp, float* __restrict__ w_f32,
-    uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
-    const int32_t* __restrict__ log2phy, int n_log2phy, int P, int skip, int block_m,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
-    int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
-    int32_t* __restrict__ sync) {
-  extern __shared__ int hist[];  // [max(P, 64 * wave_perm_spl(P))]
-  __shared__ TopkPermuteLds<EPL> L;
-  __shared__ int32_t l2p_lds[kMaxE];
-  __shared__ int last;
-  const int nw = blockDim.x >> 6;
-  const int e = blockIdx.x * nw + (threadIdx.x >> 6);
-  // every block copies the slot table while its gate rows load, so that the
-  // last one remaps the selected ids from LDS
-  const bool l2p_in_lds = log2phy != nullptr && n_log2phy <= kMaxE;
-  if (l2p_in_lds)
-    for (int i = threadIdx.x; i < n_log2phy; i += blockDim.x) l2p_lds[i] = log2phy[i];
-  if (e < sp.E) gate_row<NC>(x, wg, 0, T, H, sp.E, e, logits, logits_f32);
-  __syncthreads();  // every wave's logits are stored before thread 0 counts the block in
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const int prev = __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = prev == static_cast<int>(gridDim.x) - 1;
-    if (last) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  __syncthreads();
-  if (!last) return;
-  select_and_permute<EPL, PPL>(logits, logits_f32, T, sp, w_f32, w_bf16, ids,
-                               l2p_in_lds ? l2p_lds : log2phy, n_log2phy, P, skip, block_m,
-                               counts, offsets, sorted_pairs, row_idx, active, tile_off, meta,
-                               hist, L);
 }
 
 }  // namespace lmoe
@@ -294,35 +90,6 @@ extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
   LMOE_RETURN_LAUNCH();
 }
 
-static int check_select(int T, int E, int k, int scoring, int n_group,
-                        int topk_group) {
-  if (T < 0 || E <= 0 || k <= 0) return LMOE_ERR_ARG;
-  if (E > kMaxE || k > kMaxK || k > E) return LMOE_ERR_SHAPE;
-  if (scoring != LMOE_SCORING_SOFTMAX && scoring != LMOE_SCORING_SIGMOID)
-    return LMOE_ERR_UNSUPPORTED;
-  if (scoring == LMOE_SCORING_SIGMOID && n_group > 1) {
-    if (n_group > 64 || E % n_group != 0 || E / n_group < 2) return LMOE_ERR_SHAPE;
-    if (topk_group <= 0 || topk_group > n_group) return LMOE_ERR_SHAPE;
-    if (k > topk_group * (E / n_group)) return LMOE_ERR_SHAPE;
-  }
-  return LMOE_OK;
-}
-
-static SelectParams make_select(int E, int k, int scoring, const float* bias,
-                                int n_group, int topk_group, int renorm,
-                                float routed_scale) {
-  SelectParams sp;
-  sp.E = E;
-  sp.k = k;
-  sp.scoring = scoring;
-  sp.bias = bias;
-  sp.n_group = scoring == LMOE_SCORING_SIGMOID ? (n_group > 1 ? n_group : 1) : 1;
-  sp.topk_group = topk_group;
-  sp.renorm = renorm;
-  sp.routed_scale = routed_scale;
-  return sp;
-}
-
 extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
                                 int E, int k, int scoring, const float* bias,
                                 int n_group, int topk_group, int renorm,
@@ -337,15 +104,19 @@ extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
   const SelectParams sp =
       make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
   const dim3 grid((T + 3) / 4);
-  if (E <= 64) {
-    hipLaunchKernelGGL(topk_kernel<1>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
-  } else if (E <= 128) {
-    hipLaunchKernelGGL(topk_kernel<2>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
-  } else if (E <= 256) {
-    hipLaunchKernelGGL(topk_kernel<4>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
-  } else {
-    hipLaunchKernelGGL(topk_kernel<8>, grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids);
-  }
+#define LMOE_TK(EPL, S) \
+  hipLaunchKernelGGL((topk_kernel<EPL, S>), grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids)
+#define LMOE_TK_E(S)                 \
+  do {                               \
+    if (E <= 64) LMOE_TK(1, S);      \
+    else if (E <= 128) LMOE_TK(2, S); \
+    else if (E <= 256) LMOE_TK(4, S); \
+    else LMOE_TK(8, S);              \
+  } while (0)
+  if (scoring == LMOE_SCORING_SOFTMAX) LMOE_TK_E(LMOE_SCORING_SOFTMAX);
+  else LMOE_TK_E(LMOE_SCORING_SIGMOID);
+#undef LMOE_TK_E
+#undef LMOE_TK
   LMOE_RETURN_LAUNCH();
 }
 
@@ -366,37 +137,28 @@ extern "C" int lmoe_router_topk_permute(
   // one block: a token per wave, the whole permutation in LDS
   if (T > kFusedTopkTokens || E > 256 || n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
   if (T == 0) return LMOE_OK;
-  const SelectParams sp =
-      make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
-  const int n_pairs = T * k;
-  int threads = n_pairs > n_slots / 16 ? n_pairs : n_slots / 16;
-  threads = threads > T * 64 ? threads : T * 64;
-  threads = ((threads + 63) / 64) * 64;
-  threads = threads < 64 ? 64 : (threads > kChunk ? kChunk : threads);
-  size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
-  if (wave_perm_fits(n_pairs, n_slots)) {
-    const size_t wlds = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(n_slots));
-    lds = wlds > lds ? wlds : lds;
-  }
-  const int skip = skip_unmapped ? 1 : 0;
-#define LMOE_TP(EPL, Q)                                                                        \
-  hipLaunchKernelGGL((topk_permute_kernel<EPL, Q>), dim3(1), dim3(threads), lds, stream, logits, \
-                     logits_f32, T, sp, w_f32, w_bf16, ids, log2phy, n_log2phy, n_slots, skip,  \
-                     block_m, counts, offsets, sorted_pairs, row_idx, active, tile_off, meta)
-#define LMOE_TP_Q(EPL)                  \
-  do {                                  \
-    if (ppl == 1) LMOE_TP(EPL, 1);      \
-    else if (ppl == 2) LMOE_TP(EPL, 2); \
-    else if (ppl == 4) LMOE_TP(EPL, 4); \
-    else LMOE_TP(EPL, 0);               \
-  } while (0)
-  const int ppl = router_perm_ppl(n_pairs, n_slots);
-  if (E <= 64) LMOE_TP_Q(1);
-  else if (E <= 128) LMOE_TP_Q(2);
-  else LMOE_TP_Q(4);
-#undef LMOE_TP_Q
-#undef LMOE_TP
-  LMOE_RETURN_LAUNCH();
+  RouterPermuteArgs ra{};
+  ra.T = T;
+  ra.logits = const_cast<void*>(logits);
+  ra.logits_f32 = logits_f32;
+  ra.sp = make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  ra.w_f32 = w_f32;
+  ra.w_bf16 = w_bf16;
+  ra.ids = ids;
+  ra.log2phy = log2phy;
+  ra.n_log2phy = n_log2phy;
+  ra.n_slots = n_slots;
+  ra.skip = skip_unmapped ? 1 : 0;
+  ra.block_m = block_m;
+  ra.counts = counts;
+  ra.offsets = offsets;
+  ra.sorted_pairs = sorted_pairs;
+  ra.row_idx = row_idx;
+  ra.active = active;
+  ra.tile_off = tile_off;
+  ra.meta = meta;
+  return scoring == LMOE_SCORING_SOFTMAX ? launch_topk_permute<LMOE_SCORING_SOFTMAX>(ra, stream)
+                                         : launch_topk_permute<LMOE_SCORING_SIGMOID>(ra, stream);
 }
 
 extern "C" int lmoe_router_gate_topk_permute(
@@ -421,48 +183,31 @@ extern "C" int lmoe_router_gate_topk_permute(
   // the last block holds the whole selection and permutation
   if (T > kFusedTopkTokens || E > 256 || n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
   if (T == 0) return LMOE_OK;
-  const SelectParams sp =
-      make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
-  const int n_pairs = T * k;
-  int threads = n_pairs > n_slots / 16 ? n_pairs : n_slots / 16;
-  threads = threads > T * 64 ? threads : T * 64;
-  threads = threads > 256 ? threads : 256;  // four gate rows per block at least
-  threads = ((threads + 63) / 64) * 64;
-  threads = threads > kChunk ? kChunk : threads;
-  const int nw = threads / 64;
-  const int blocks = (E + nw - 1) / nw;
-  size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
-  if (wave_perm_fits(n_pairs, n_slots)) {
-    const size_t wlds = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(n_slots));
-    lds = wlds > lds ? wlds : lds;
-  }
-  const int skip = skip_unmapped ? 1 : 0;
-  const int nc = (H + 511) / 512;
-#define LMOE_GTP(NC, EPL, Q)                                                                   \
-  hipLaunchKernelGGL((gate_topk_permute_kernel<NC, EPL, Q>), dim3(blocks), dim3(threads), lds,   \
-                     stream, static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(wg),  \
-                     T, H, logits, logits_f32, sp, w_f32, w_bf16, ids, log2phy, n_log2phy,       \
-                     n_slots, skip, block_m, counts, offsets, sorted_pairs, row_idx, active,     \
-                     tile_off, meta, sync)
-#define LMOE_GTP_Q(NC, EPL)                 \
-  do {                                      \
-    if (ppl == 1) LMOE_GTP(NC, EPL, 1);     \
-    else if (ppl == 2) LMOE_GTP(NC, EPL, 2); \
-    else if (ppl == 4) LMOE_GTP(NC, EPL, 4); \
-    else LMOE_GTP(NC, EPL, 0);              \
-  } while (0)
-#define LMOE_GTP_E(NC)                  \
-  do {                                  \
-    if (E <= 64) LMOE_GTP_Q(NC, 1);     \
-    else if (E <= 128) LMOE_GTP_Q(NC, 2); \
-    else LMOE_GTP_Q(NC, 4);             \
-  } while (0)
-  const int ppl = router_perm_ppl(n_pairs, n_slots);
-  if (nc <= 4) LMOE_GTP_E(4);
-  else if (nc <= 8) LMOE_GTP_E(8);
-  else LMOE_GTP_E(16);
-#undef LMOE_GTP_E
-#undef LMOE_GTP_Q
-#undef LMOE_GTP
-  LMOE_RETURN_LAUNCH();
+  RouterPermuteArgs ra{};
+  ra.x = x;
+  ra.wg = wg;
+  ra.H = H;
+  ra.sync = sync;
+  ra.T = T;
+  ra.logits = logits;
+  ra.logits_f32 = logits_f32;
+  ra.sp = make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  ra.w_f32 = w_f32;
+  ra.w_bf16 = w_bf16;
+  ra.ids = ids;
+  ra.log2phy = log2phy;
+  ra.n_log2phy = n_log2phy;
+  ra.n_slots = n_slots;
+  ra.skip = skip_unmapped ? 1 : 0;
+  ra.block_m = block_m;
+  ra.counts = counts;
+  ra.offsets = offsets;
+  ra.sorted_pairs = sorted_pairs;
+  ra.row_idx = row_idx;
+  ra.active = active;
+  ra.tile_off = tile_off;
+  ra.meta = meta;
+  return scoring == LMOE_SCORING_SOFTMAX
+             ? launch_gate_topk_permute<LMOE_SCORING_SOFTMAX>(ra, stream)
+             : launch_gate_topk_permute<LMOE_SCORING_SIGMOID>(ra, stream);
 }

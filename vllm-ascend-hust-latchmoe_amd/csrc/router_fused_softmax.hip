@@ -1,0 +1,12 @@
+// One-launch decode routers for softmax scoring: the kernels of
+// launch_topk_permute / launch_gate_topk_permute (router.h), instantiated in
+// a translation unit of their own so the build compiles the scoring modes in
+// parallel.
+#include "router.h"
+
+namespace lmoe {
+
+template int launch_topk_permute<LMOE_SCORING_SOFTMAX>(const RouterPermuteArgs&, hipStream_t);
+template int launch_gate_topk_permute<LMOE_SCORING_SOFTMAX>(const RouterPermuteArgs&, hipStream_t);
+
+}  // namespace lmoe

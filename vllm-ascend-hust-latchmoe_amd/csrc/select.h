@@ -65,10 +65,11 @@ __device__ __forceinline__ bool better(float v, int e, float v2, int e2) {
 
 // Selects the k experts of one token from its logits lg[j] (expert j*64 +
 // lane, -inf beyond E; EPL*64 >= E) and the correction bias bv[j]
-// (load_bias; used only when sp.bias is set).  Lane l < k returns the l-th
-// selected expert id (-1 if fewer than k are eligible) and its final f32
-// weight.
-template <int EPL>
+// (load_bias; used only when sp.bias is set).  SCORE (LMOE_SCORING_*) is a
+// template parameter so that a kernel holds only the code of its scoring.
+// Lane l < k returns the l-th selected expert id (-1 if fewer than k are
+// eligible) and its final f32 weight.
+template <int EPL, int SCORE>
 __device__ __forceinline__ void select_token(const SelectParams& sp,
                                              float (&lg)[EPL], const float (&bv)[EPL],
                                              SelectLds<EPL>& L, int& out_e,
@@ -79,7 +80,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
   float sel[EPL];  // selection score
   float wgt[EPL];  // weight carried by a selected expert
   bool elig[EPL];
-  if (sp.scoring == LMOE_SCORING_SOFTMAX) {
+  if constexpr (SCORE == LMOE_SCORING_SOFTMAX) {
     if (sp.bias != nullptr) {
       // additive per-expert logit bias (rounded once, before the softmax)
 #pragma unroll
