@@ -47,6 +47,7 @@ def _check(perm, ref, n_pairs):
     (129, 8, 128, 64, True),
     (4096, 8, 128, 48, True),
     (2048, 8, 256, 256, False),
+    (5000, 8, 1024, 1024, False),  # 40 chunks x 1024 slots: scan over the table in global memory
     (3, 1, 5, 3, True),
 ])
 def test_permute_matches_oracle(T, k, E, P, use_map, block_m):

@@ -53,7 +53,14 @@ __global__ __launch_bounds__(1024) void permute_hist_kernel(
   if (threadIdx.x == 0) chunk_err[blockIdx.x] = err_lds;
 }
 
-// Step 2 (one block): column sums -> offsets, per-chunk bases.
+// Step 2 (one block): column sums -> offsets, per-chunk bases.  With
+// IN_LDS the nchunks x P count table is read into LDS with coalesced loads,
+// each slot's column is scanned there, and the bases go back in parallel
+// (the global walk costs one dependent round trip per chunk and slot).
+// LDS: P ints (hist), plus nchunks * P with IN_LDS.
+constexpr int kScanLdsInts = 16384;  // count table held in LDS up to 64 KiB
+
+template <bool IN_LDS>
 __global__ __launch_bounds__(1024) void permute_scan_kernel(
     int P, int nchunks, int block_m, int32_t* __restrict__ chunk_cnt,
     const int32_t* __restrict__ chunk_err, int32_t* __restrict__ counts,
@@ -61,10 +68,16 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(
     int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
   extern __shared__ int hist[];
   __shared__ int scan_lds[33];
+  int* cc = hist + P;  // [nchunks][P] with IN_LDS
+  const int n = nchunks * P;
+  if (IN_LDS) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) cc[i] = chunk_cnt[i];
+    __syncthreads();
+  }
   for (int s = threadIdx.x; s < P; s += blockDim.x) {
     int run = 0;
     for (int c = 0; c < nchunks; ++c) {
-      int32_t* q = chunk_cnt + static_cast<size_t>(c) * P + s;
+      int* q = IN_LDS ? cc + c * P + s : chunk_cnt + static_cast<size_t>(c) * P + s;
       const int v = *q;
       *q = run;
       run += v;
@@ -79,9 +92,13 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(
     meta[LMOE_META_ERRORS] = e;
   }
   __syncthreads();  // hist now holds offsets
-  for (int s = threadIdx.x; s < P; s += blockDim.x) {
-    const int base = hist[s];
-    for (int c = 0; c < nchunks; ++c) chunk_cnt[static_cast<size_t>(c) * P + s] += base;
+  if (IN_LDS) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) chunk_cnt[i] = cc[i] + hist[i % P];
+  } else {
+    for (int s = threadIdx.x; s < P; s += blockDim.x) {
+      const int base = hist[s];
+      for (int c = 0; c < nchunks; ++c) chunk_cnt[static_cast<size_t>(c) * P + s] += base;
+    }
   }
 }
 
@@ -185,9 +202,17 @@ extern "C" int lmoe_permute(const int32_t* ids, int n_pairs,
   hipLaunchKernelGGL(permute_hist_kernel, dim3(nchunks), dim3(kChunk), lds,
                      stream, ids, n_pairs, log2phy, n_log2phy, n_slots, skip,
                      slot_of, chunk_cnt, chunk_err);
-  hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(kChunk), lds, stream,
-                     n_slots, nchunks, block_m, chunk_cnt, chunk_err, counts,
-                     offsets, active, tile_off, meta);
+  if (static_cast<long long>(nchunks) * n_slots <= kScanLdsInts) {
+    const size_t scan_lds = sizeof(int) * (static_cast<size_t>(n_slots) +
+                                           static_cast<size_t>(nchunks) * n_slots);
+    hipLaunchKernelGGL(permute_scan_kernel<true>, dim3(1), dim3(kChunk), scan_lds, stream,
+                       n_slots, nchunks, block_m, chunk_cnt, chunk_err, counts, offsets, active,
+                       tile_off, meta);
+  } else {
+    hipLaunchKernelGGL(permute_scan_kernel<false>, dim3(1), dim3(kChunk), lds, stream,
+                       n_slots, nchunks, block_m, chunk_cnt, chunk_err, counts, offsets, active,
+                       tile_off, meta);
+  }
   hipLaunchKernelGGL(permute_scatter_kernel, dim3(nchunks), dim3(kChunk), lds,
                      stream, n_pairs, n_slots, slot_of, chunk_cnt, sorted_pairs,
                      row_idx);
