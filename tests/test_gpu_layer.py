@@ -201,3 +201,72 @@ def test_c1_config_eight_tokens_thirty_two_slots():
     err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
     print(f"C1: rel max err {err:.3e}", flush=True)
     assert err <= OUT_TOL
+
+
+@pytest.mark.parametrize("B", [1, 4, 16])
+def test_decode_layer_graph_replays_equal_eager(B):
+    """decode_layer captured once (one-launch router up to 4 tokens, the
+    several-token y body above 1) and replayed over steps whose staging
+    changes the slot table: every replay equals an eager decode_layer on the
+    same inputs bit for bit, the router's arrival counter is back at zero,
+    and the output matches the oracle."""
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    from vllm_moe_offload_amd.fused_moe import RouterSpec
+
+    rng = np.random.default_rng(700 + B)
+    E, H, I, k = 64, 1024, 256, 8
+    slots = 48 if B <= 4 else E  # 16 random tokens touch ~57 of 64 experts
+    w13, w2, wg = _weights(rng, E, H, I)
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True, graph_compatible_offload=True))
+    layer = SlotMoELayer(layer_id=5, runtime=rt, gate_weight=to_dev_bf16(wg), w13_weight=torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16),
+                         w2_weight=torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16), top_k=k)
+    layer.register()
+    spec = RouterSpec(top_k=k)
+    prepared = rt.capture_safe_slot_weights(layer_id=5)
+    P = prepared.physical_expert_count
+    ws_g = fused_moe.get_workspace(B, k, P, H, I, "cuda", tag=f"graph-dl-{B}")
+    ws_e = fused_moe.get_workspace(B, k, P, H, I, "cuda", tag=f"eager-dl-{B}")
+    static_x = torch.zeros((B, H), dtype=torch.bfloat16, device="cuda")
+    g_out = torch.zeros((B, H), dtype=torch.bfloat16, device="cuda")
+    g_logits = torch.zeros((B, E), dtype=torch.bfloat16, device="cuda")
+    g_w = torch.zeros((B, k), dtype=torch.bfloat16, device="cuda")
+    g_ids = torch.zeros((B, k), dtype=torch.int32, device="cuda")
+
+    def stage(dx):
+        _, ids, _ = fused_moe.route(dx, layer.gate_weight, spec)
+        rt.stage_fixed_slot_plan(layer_id=5, active_experts=tuple(sorted(set(ids.cpu().flatten().tolist()))),
+                                 num_logical_experts=E)
+
+    def piece():
+        fused_moe.decode_layer(static_x, layer.gate_weight, spec, prepared.w1, prepared.w2, prepared.log2phy,
+                               workspace=ws_g, out=g_out, logits_out=g_logits, w_out=g_w, ids_out=g_ids)
+
+    x0 = to_dev_bf16(normal_bf16(rng, (B, H), 1.0))
+    stage(x0)
+    static_x.copy_(x0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        piece()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        piece()
+    for step in range(5):
+        x = normal_bf16(rng, (B, H), 1.0)
+        dx = to_dev_bf16(x)
+        stage(dx)
+        static_x.copy_(dx)
+        g.replay()
+        torch.cuda.synchronize()
+        e_out, e_w, e_ids = fused_moe.decode_layer(dx, layer.gate_weight, spec, prepared.w1, prepared.w2,
+                                                   prepared.log2phy, workspace=ws_e)
+        torch.cuda.synchronize()
+        print(f"B={B} replay {step}", flush=True)
+        assert torch.equal(g_ids, e_ids), step
+        assert torch.equal(g_w.view(torch.int16), e_w.view(torch.int16)), step
+        assert torch.equal(g_out.view(torch.int16), e_out.view(torch.int16)), step
+        assert ws_g.perm.sync.item() == 0 and ws_e.perm.sync.item() == 0
+        ref = _oracle_layer(x, g_ids.cpu().numpy(), from_dev_bf16(g_w), w13, w2)
+        assert rel_max_err(bf16_to_f32(from_dev_bf16(g_out)), ref) <= OUT_TOL
