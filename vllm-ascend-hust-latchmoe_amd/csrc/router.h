@@ -96,12 +96,13 @@ __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
 // Expert selection and the permutation of the selected pairs in one block,
 // for a slot table that is final before the router runs (decode replay
 // after staging).  Wave t selects token t (T <= kFusedTopkTokens); the ids
-// go to LDS and feed the same permutation as permute_small_kernel, so every
-// output equals what lmoe_router_topk followed by lmoe_permute writes.
+// go to LDS and feed the same permutation code as lmoe_permute (one wave, or
+// the whole block), so every output equals what lmoe_router_topk followed by
+// lmoe_permute writes.
 constexpr int kFusedTopkTokens = 16;
 
-// Selection of T <= kFusedTopkTokens tokens (wave t selects token t) and the
-// permutation of their pairs, by one block of at least T waves.
+// LDS of the selection of T <= kFusedTopkTokens tokens and the permutation
+// of their pairs.
 template <int EPL>
 struct TopkPermuteLds {
   SelectLds<EPL> sel[kFusedTopkTokens];

@@ -223,7 +223,8 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     const bool live = key[j] != 0u;
     const bool eq = live & (pre == thr);
     const uint64_t beq = __builtin_amdgcn_ballot_w64(eq);
-    const bool take = live & ((pre > thr) | (eq & (eq_before + __popcll(beq & lanemask_lt(lane)) < need)));
+    const int eq_rank = eq_before + static_cast<int>(__popcll(beq & lanemask_lt(lane)));
+    const bool take = live & ((pre > thr) | (eq & (eq_rank < need)));
     eq_before += __popcll(beq);
     const uint64_t bt = __builtin_amdgcn_ballot_w64(take);
     if (take) {
