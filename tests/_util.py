@@ -38,14 +38,15 @@ def bf16_ulp(v: np.ndarray) -> np.ndarray:
     return np.abs(np.spacing(np.asarray(v, dtype=np.float32))) * np.float32(65536.0)
 
 
-def ulp_mismatch_stats(got: np.ndarray, ref: np.ndarray, abs_floor: float = 0.0) -> tuple[float, float]:
-    """(fraction of elements off by more than one bf16 ulp, max error in units
-    of (one ulp + abs_floor)).  abs_floor absorbs cancellation: an element that
-    is a small difference of large terms carries the absolute rounding noise of
-    its terms, not of its own magnitude."""
+def ulp_mismatch_stats(got: np.ndarray, ref: np.ndarray, abs_floor: float = 0.0,
+                       count_floor: float = 0.0) -> tuple[float, float]:
+    """(fraction of elements off by more than one bf16 ulp + count_floor, max
+    error in units of (one ulp + abs_floor)).  The floors absorb cancellation:
+    an element that is a small difference of large terms carries the absolute
+    rounding noise of its terms, not of its own magnitude."""
     got = np.asarray(got, dtype=np.float32)
     ref = np.asarray(ref, dtype=np.float32)
     ulp = np.maximum(bf16_ulp(ref), bf16_ulp(got))
     ulp = np.maximum(ulp, np.float32(2.0 ** -126))
     d = np.abs(got - ref)
-    return float(np.mean(d > ulp)), float((d / (ulp + np.float32(abs_floor))).max())
+    return float(np.mean(d > ulp + np.float32(count_floor))), float((d / (ulp + np.float32(abs_floor))).max())

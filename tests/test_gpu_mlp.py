@@ -99,10 +99,14 @@ def test_grouped_mlp_and_combine_match_oracle(path, T, k, E, P, H, I):
     slot = operm.remap(ids, l2p, P)
     y_ref = omlp.grouped_mlp(x, slot, k, w13, w2)
     # y (GMM2 output, bf16 on both sides): accumulation-order noise flips the
-    # bf16 rounding of a few elements by one ulp; near-zero elements (sums
-    # that cancel) carry absolute noise, bounded by 2^-8 RMS(y)
+    # bf16 rounding of a few gate/up/act elements by one ulp, and each flip
+    # moves y by ~2^-8 of one of its terms (~1e-4 RMS(y) in all).  Elements
+    # near zero (sums that cancel) carry that absolute noise: the count of
+    # >1-ulp elements allows RMS(y)/4096 on top of the ulp, the maximum
+    # 2^-8 RMS(y)
     rms_y = float(np.sqrt(np.mean(y_ref.astype(np.float64) ** 2)))
-    frac, max_ulps = ulp_mismatch_stats(bf16_to_f32(from_dev_bf16(y)), y_ref, abs_floor=rms_y / 256)
+    frac, max_ulps = ulp_mismatch_stats(bf16_to_f32(from_dev_bf16(y)), y_ref, abs_floor=rms_y / 256,
+                                        count_floor=rms_y / 4096)
     out_ref = omlp.combine(y_ref, wb, round_output=False)
     err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), out_ref)
     print(f"  y: frac>1ulp {frac:.2e} max {max_ulps:.2f} ulp; out rel max err {err:.3e}", flush=True)
@@ -307,7 +311,7 @@ def test_mfma_tile_heights_agree_bitwise(T, k, E, P, H, I, skip):
     got = bf16_to_f32(from_dev_bf16(outs[256][1]))[placed]
     ref = y_ref[placed]
     rms_y = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
-    frac, max_ulps = ulp_mismatch_stats(got, ref, abs_floor=rms_y / 256)
+    frac, max_ulps = ulp_mismatch_stats(got, ref, abs_floor=rms_y / 256, count_floor=rms_y / 4096)
     print(f"  y vs oracle: frac>1ulp {frac:.2e} max {max_ulps:.2f} ulp", flush=True)
     # f32 summation-order noise grows with K (7168 for the DeepSeek shape vs
     # <= 2048 elsewhere): more near-cancelling elements cross one ulp, while

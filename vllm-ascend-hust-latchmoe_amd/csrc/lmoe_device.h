@@ -48,23 +48,24 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// dot of 8 bf16 pairs held in two uint4, accumulated into acc in element order
+// One packed bf16 pair dot: acc + a.lo*b.lo + a.hi*b.hi in one
+// v_dot2c_f32_bf16 (f32 accumulation; no unpacking to f32 first).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+// dot of 8 bf16 pairs held in two uint4, accumulated into acc pair by pair
+// in element order (four dot2 steps).
 __device__ __forceinline__ float dot8(const uint4 a, const uint4 b, float acc) {
-  acc += bf16lo(a.x) * bf16lo(b.x);
-  acc += bf16hi(a.x) * bf16hi(b.x);
-  acc += bf16lo(a.y) * bf16lo(b.y);
-  acc += bf16hi(a.y) * bf16hi(b.y);
-  acc += bf16lo(a.z) * bf16lo(b.z);
-  acc += bf16hi(a.z) * bf16hi(b.z);
-  acc += bf16lo(a.w) * bf16lo(b.w);
-  acc += bf16hi(a.w) * bf16hi(b.w);
+  acc = dot2(a.x, b.x, acc);
+  acc = dot2(a.y, b.y, acc);
+  acc = dot2(a.z, b.z, acc);
+  acc = dot2(a.w, b.w, acc);
   return acc;
 }
 __device__ __forceinline__ float dot4(const uint2 a, const uint2 b, float acc) {
-  acc += bf16lo(a.x) * bf16lo(b.x);
-  acc += bf16hi(a.x) * bf16hi(b.x);
-  acc += bf16lo(a.y) * bf16lo(b.y);
-  acc += bf16hi(a.y) * bf16hi(b.y);
+  acc = dot2(a.x, b.x, acc);
+  acc = dot2(a.y, b.y, acc);
   return acc;
 }
 
