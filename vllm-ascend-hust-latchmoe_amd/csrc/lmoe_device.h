@@ -70,22 +70,142 @@ __device__ __forceinline__ float dot4(const uint2 a, const uint2 b, float acc) {
 }
 
 // ---------------------------------------------------------------------------
-// wave64 reductions (butterfly: every lane ends with the same value)
+// wave64 lane exchanges and reductions, without the LDS crossbar
 // ---------------------------------------------------------------------------
+// lane_xor<M>(v) is v of lane (lane ^ M).  Distances 32 and 16 use the gfx950
+// permlane swaps (v_permlane32_swap: upper half of the first operand with
+// the lower half of the second; v_permlane16_swap: odd rows of the first
+// with even rows of the second), 8 a row rotate, 4 a half-row mirror (^7)
+// then a quad reversal (^3), 2 and 1 quad permutes.  Every step pairs lane i
+// with lane i ^ M, so a butterfly built from them adds in the same tree as a
+// shuffle butterfly and gives the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppQuadXor1 = 0xb1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4e;     // quad_perm [2,3,0,1]
+constexpr int kDppQuadXor3 = 0x1b;     // quad_perm [3,2,1,0]
+constexpr int kDppHalfRowMirror = 0x141;
+constexpr int kDppRowRor8 = 0x128;
+
+// Swap through the permlane instructions: on return a holds, in lanes with
+// bit M clear, their own a and in the others the partner's b; b holds the
+// partner's a resp. their own b.  With a == b: {a, b} = {own, partner} in
+// some order, so a commutative op of the two is the butterfly step.
+template <int M>
+__device__ __forceinline__ void permlane_swap(float& a, float& b) {
+  static_assert(M == 32 || M == 16, "permlane swaps exist for 32 and 16");
+  const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+  if constexpr (M == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+  }
+}
+
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (M == 32 || M == 16) {
+    float a = v, b = v;
+    permlane_swap<M>(a, b);
+    return (__lane_id() & M) ? a : b;
+  } else if constexpr (M == 8) {
+    return dpp_f32<kDppRowRor8>(v);
+  } else if constexpr (M == 4) {
+    return dpp_f32<kDppQuadXor3>(dpp_f32<kDppHalfRowMirror>(v));
+  } else if constexpr (M == 2) {
+    return dpp_f32<kDppQuadXor2>(v);
+  } else {
+    static_assert(M == 1, "lane distance must be a power of two <= 32");
+    return dpp_f32<kDppQuadXor1>(v);
+  }
+}
+
+// v of lane l (wave-uniform l), broadcast through a scalar register
+__device__ __forceinline__ float read_lane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// v (op) v of lane ^ M, for a commutative op
+template <int M, typename Op>
+__device__ __forceinline__ float xor_step(float v, Op op) {
+  if constexpr (M == 32 || M == 16) {
+    float a = v, b = v;
+    permlane_swap<M>(a, b);
+    return op(a, b);
+  } else {
+    return op(v, lane_xor<M>(v));
+  }
+}
+
+struct AddOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct MaxOp {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+
+// Butterfly over all 64 lanes: every lane ends with the same value.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  v = xor_step<32>(v, AddOp{});
+  v = xor_step<16>(v, AddOp{});
+  v = xor_step<8>(v, AddOp{});
+  v = xor_step<4>(v, AddOp{});
+  v = xor_step<2>(v, AddOp{});
+  return xor_step<1>(v, AddOp{});
 }
 __device__ __forceinline__ float wave_max(float v) {
+  v = xor_step<32>(v, MaxOp{});
+  v = xor_step<16>(v, MaxOp{});
+  v = xor_step<8>(v, MaxOp{});
+  v = xor_step<4>(v, MaxOp{});
+  v = xor_step<2>(v, MaxOp{});
+  return xor_step<1>(v, MaxOp{});
+}
+
+// One reduce-scatter step over lane bit M: lanes with the bit clear end with
+// lo + partner's lo, the others with hi + partner's hi.
+template <int M>
+__device__ __forceinline__ float exchange_add(float lo, float hi, int lane) {
+  if constexpr (M == 32 || M == 16) {
+    permlane_swap<M>(lo, hi);
+    return lo + hi;
+  } else {
+    const bool upper = (lane & M) != 0;
+    const float send = upper ? lo : hi;
+    const float keep = upper ? hi : lo;
+    return keep + lane_xor<M>(send);
+  }
+}
+
+template <int BIT, int LO>
+__device__ __forceinline__ float butterfly_sum(float r) {
+  if constexpr (BIT >= LO) {
+    r = xor_step<(1 << BIT)>(r, AddOp{});
+    return butterfly_sum<BIT - 1, LO>(r);
+  } else {
+    return r;
+  }
+}
+
+template <int V, int B, int HI>
+__device__ __forceinline__ void scatter_steps(float (&v)[V], int lane) {
+  if constexpr ((V >> (B + 1)) >= 1) {
+    constexpr int half = V >> (B + 1);
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+    for (int i = 0; i < half; ++i) v[i] = exchange_add<(1 << (HI - B))>(v[i], v[half + i], lane);
+    scatter_steps<V, B + 1, HI>(v, lane);
+  }
 }
 
 // Sum V values per lane over the lanes that differ in bits LO..HI of the lane
 // id, leaving ONE total per lane: the first log2(V) steps exchange halves of
-// the value set (a reduce-scatter: V-1 shuffles instead of V*(HI-LO+1)), the
+// the value set (a reduce-scatter: V-1 exchanges instead of V*(HI-LO+1)), the
 // rest are plain butterfly adds.  On return, the lane holds value index
 // scatter_index<HI, LO, log2 V>(lane).
 template <int V, int HI, int LO>
@@ -93,22 +213,9 @@ __device__ __forceinline__ float reduce_scatter(float (&v)[V], int lane) {
   constexpr int L = (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
   static_assert((1 << L) == V, "V must be a power of two <= 16");
   static_assert(HI - LO + 1 >= L, "not enough lane bits");
-#pragma unroll
-  for (int b = 0; b < L; ++b) {
-    const int bit = HI - b;
-    const int half = V >> (b + 1);
-    const bool upper = (lane >> bit) & 1;
-#pragma unroll
-    for (int i = 0; i < half; ++i) {
-      const float send = upper ? v[i] : v[half + i];
-      const float keep = upper ? v[half + i] : v[i];
-      v[i] = keep + __shfl_xor(send, 1 << bit, kWave);
-    }
-  }
-  float r = v[0];
-#pragma unroll
-  for (int bit = HI - L; bit >= LO; --bit) r += __shfl_xor(r, 1 << bit, kWave);
-  return r;
+  static_assert(HI <= 5 && LO >= 0, "lane bits of a wave64");
+  scatter_steps<V, 0, HI>(v, lane);
+  return butterfly_sum<HI - L, LO>(v[0]);
 }
 
 template <int HI, int LO, int L>

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
       }
     }
     const float tot = reduce_scatter<2, 5, 0>(v, lane);
-    const float up = __shfl_xor(tot, 32, kWave);
+    const float up = read_lane(tot, 32);  // lane 32 holds the up total
     if (lane == 0) act[static_cast<size_t>(a) * I + i] = swiglu_bf16(tot, up);
     return;
   }
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
       }
       // lanes 0..31 end with the gate total, 32..63 with the up total
       const float tot = reduce_scatter<2, 5, 0>(v, lane);
-      const float up = __shfl_xor(tot, 32, kWave);
+      const float up = read_lane(tot, 32);  // lane 32 holds the up total
       if (lane == 0) act[static_cast<size_t>(p0 + r) * I + i] = swiglu_bf16(tot, up);
     }
   } else {
