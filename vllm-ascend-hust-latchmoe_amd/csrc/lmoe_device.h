@@ -168,6 +168,65 @@ __device__ __forceinline__ float wave_max(float v) {
   return xor_step<1>(v, MaxOp{});
 }
 
+// Unsigned max over the wave: row rotates by 8, 4, 2, 1 (each lane then
+// holds its row's max), then the two permlane swaps across rows.  Every
+// lane ends with the wave's max.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = umax32(v, dpp_u32<0x128>(v));  // row_ror:8
+  v = umax32(v, dpp_u32<0x124>(v));  // row_ror:4
+  v = umax32(v, dpp_u32<0x122>(v));  // row_ror:2
+  v = umax32(v, dpp_u32<0x121>(v));  // row_ror:1
+  float a = __uint_as_float(v), b = a;
+  permlane_swap<16>(a, b);
+  v = umax32(__float_as_uint(a), __float_as_uint(b));
+  a = __uint_as_float(v);
+  b = a;
+  permlane_swap<32>(a, b);
+  return umax32(__float_as_uint(a), __float_as_uint(b));
+}
+
+// The same max as a wave-uniform (scalar) value: row maxima by DPP, then
+// the four rows' lanes 0, 16, 32, 48 read into scalar registers.
+__device__ __forceinline__ uint32_t wave_max_u32_uniform(uint32_t v) {
+  v = umax32(v, dpp_u32<0x128>(v));  // row_ror:8
+  v = umax32(v, dpp_u32<0x124>(v));  // row_ror:4
+  v = umax32(v, dpp_u32<0x122>(v));  // row_ror:2
+  v = umax32(v, dpp_u32<0x121>(v));  // row_ror:1
+  const uint32_t r0 = __builtin_amdgcn_readlane(static_cast<int>(v), 0);
+  const uint32_t r1 = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(static_cast<int>(v), 32);
+  const uint32_t r3 = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
+  return umax32(umax32(r0, r1), umax32(r2, r3));
+}
+
+// Inclusive prefix sum over the wave's 64 lanes (lane l: v of lanes 0..l),
+// all in DPP: row shifts by 1, 2, 4, 8 (zero fill at the row start) give
+// the prefix within each row of 16; row_bcast:15 adds row 0's total to row
+// 1 and row 2's to row 3; row_bcast:31 adds lane 31's prefix (rows 0-1) to
+// rows 2 and 3.  Integer adds: exact in any order.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_i32_zero(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, true);
+}
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  v += dpp_i32_zero<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_i32_zero<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_i32_zero<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_i32_zero<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_i32_zero<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_i32_zero<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+__device__ __forceinline__ int read_lane_i32(int v, int l) {
+  return __builtin_amdgcn_readlane(v, l);
+}
+
 // One reduce-scatter step over lane bit M: lanes with the bit clear end with
 // lo + partner's lo, the others with hi + partner's hi.
 template <int M>

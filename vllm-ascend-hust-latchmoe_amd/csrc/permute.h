@@ -55,12 +55,7 @@ __device__ int block_exclusive_scan(int v, int* scan_lds, int* total) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  int inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(inc, o, kWave);
-    if (lane >= o) inc += t;
-  }
+  const int inc = wave_inclusive_sum(v);
   if (lane == 63) scan_lds[wave] = inc;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -211,15 +206,6 @@ __device__ __forceinline__ void permute_block(
 constexpr int kWavePermMaxSlotsPerLane = 16;
 constexpr int kWavePermMaxPairsPerLane = 4;
 
-__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o, kWave);
-    if (lane >= o) v += t;
-  }
-  return v;
-}
-
 template <int SPL, int PPL>
 __device__ __forceinline__ void permute_wave(
     const int32_t* ids, int N, const int32_t* __restrict__ log2phy, int n_log2phy, int P,
@@ -267,13 +253,29 @@ __device__ __forceinline__ void permute_wave(
     asum += c[i] > 0;
     tsum += (c[i] + block_m - 1) / block_m;
   }
-  const int cinc = wave_inclusive_scan(csum, lane);
-  const int ainc = wave_inclusive_scan(asum, lane);
-  const int tinc = wave_inclusive_scan(tsum, lane);
-  int cpre = cinc - csum, apre = ainc - asum, tpre = tinc - tsum;
-  const int ctot = __shfl(cinc, 63, kWave);
-  const int atot = __shfl(ainc, 63, kWave);
-  const int ttot = __shfl(tinc, 63, kWave);
+  const int cinc = wave_inclusive_sum(csum);
+  int cpre = cinc - csum;
+  const int ctot = read_lane_i32(cinc, 63);
+  int apre, atot, tpre, ttot;
+  if constexpr (SPL == 1) {
+    // one slot per lane: the active prefix is a ballot count
+    const uint64_t am = __builtin_amdgcn_ballot_w64(asum > 0);
+    apre = static_cast<int>(__popcll(am & lanemask_lt(lane)));
+    atot = static_cast<int>(__popcll(am));
+  } else {
+    const int ainc = wave_inclusive_sum(asum);
+    apre = ainc - asum;
+    atot = read_lane_i32(ainc, 63);
+  }
+  if (SPL == 1 && N <= block_m) {
+    // no slot holds more than block_m pairs: one tile per active slot
+    tpre = apre;
+    ttot = atot;
+  } else {
+    const int tinc = wave_inclusive_sum(tsum);
+    tpre = tinc - tsum;
+    ttot = read_lane_i32(tinc, 63);
+  }
   wave_lds_sync();  // every lane has read its counts before lds is reused
 #pragma unroll
   for (int i = 0; i < SPL; ++i) {

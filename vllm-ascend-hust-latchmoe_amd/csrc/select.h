@@ -2,13 +2,11 @@
 // correction bias + group-limited top-k, with renormalisation and scaling.
 //
 // Selection order is (score desc, expert id asc), the order torch.topk gives
-// with ties to the lower id.  Instead of k serial rounds of wave arg-max,
-// each score becomes an order-preserving 32-bit key and a most-significant-
-// bit-first radix select (one ballot per expert slot and bit, stopping once
-// the prefix found is shared by exactly the experts still needed) finds the
-// k-th largest key's prefix; the taken experts (the lowest ids among equal
-// keys) are compacted with ballots and only those k are ranked against each
-// other through LDS.
+// with ties to the lower id.  Each score becomes an order-preserving 32-bit
+// key; k rounds of wave arg-max (an unsigned max over the wave through DPP
+// row rotates and the permlane swaps, then a ballot on equality that picks
+// the lowest id among equal keys) produce the experts already in selection
+// order, with no sort, compaction or LDS ranking.
 //
 // Reference behaviour: moe_router_op.py:191-278 (gate then select_experts),
 // renorm contract patches/patch_fused_moe.py:597-632
@@ -38,18 +36,12 @@ struct SelectParams {
   float routed_scale;
 };
 
-// Per-wave LDS scratch of one selection over up to EPL*64 experts.  Score/id
-// pairs are interleaved so one 16-byte LDS read returns two entries; the
-// ranking loops are unrolled so all their reads are in flight together (a
-// rolled loop waits for each read in turn: ~120 cycles x 64).
+// Per-wave LDS scratch of one selection: the score table and group scores
+// of the grouped sigmoid (the other scorings use none).
 template <int EPL>
 struct SelectLds {
-  float2 cand[EPL * kWave]; // (key bits, id bits) of the taken experts
-  float c_w[EPL * kWave];
   float c_s[EPL * kWave];   // score table of the groups (grouped sigmoid)
   float gsc[kWave];
-  float o_w[kMaxK];
-  int o_e[kMaxK];
 };
 
 // (value desc, id asc) ordering used by every selection step.  Written
@@ -171,7 +163,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
         const int e = j * kWave + lane;
         elig[j] = (e < E) && ((kept >> (e / gs)) & 1ull);
       }
-      wave_lds_sync();  // c_s is reused below
+      wave_lds_sync();  // the scratch may be reused by the next token
     }
   }
 
@@ -185,102 +177,56 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     key[j] = elig[j] ? o : 0u;
   }
-  // 2. radix select, most significant bit first.  Invariant: thr holds the
-  //    bits above b of the k-th largest key (tmask marks them), `match`
-  //    experts share that prefix and `need` of them are still to be taken.
-  //    Stops as soon as match == need (all of them are taken), or after bit
-  //    0 with ties on the full key (the lowest ids are taken).
-  int match = 0;
+  // 2. k rounds of wave arg-max, without branches.  Round r takes the
+  //    largest key left (the lowest id among equal keys), writes its id and
+  //    weight into lane r and clears it; the weights are summed in
+  //    selection order as they come.  Once the largest key left is 0 (fewer
+  //    than k experts are eligible) the remaining rounds write -1 and 0.
+  int my_e = -1;
+  float my_w = 0.0f;
+  float sum = 0.0f;
+  for (int r = 0; r < k; ++r) {
+    uint32_t lm = key[0];
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) match += __popcll(__builtin_amdgcn_ballot_w64(key[j] != 0u));
-  uint32_t thr = 0u, tmask = 0u;
-  int need = k;
-  for (int b = 31; b >= 0 && match > need; --b) {
-    const uint32_t tgt = (thr >> b) | 1u;  // prefix with bit b set
-    int c1 = 0;
+    for (int j = 1; j < EPL; ++j) lm = lm > key[j] ? lm : key[j];
+    const uint32_t best = wave_max_u32_uniform(lm);
+    uint64_t bm[EPL];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) c1 += __popcll(__builtin_amdgcn_ballot_w64((key[j] >> b) == tgt));
-    if (c1 >= need) {
-      thr |= 1u << b;
-      match = c1;
-    } else {
-      need -= c1;
-      match -= c1;
+    for (int j = 0; j < EPL; ++j) bm[j] = __builtin_amdgcn_ballot_w64(key[j] == best);
+    uint64_t bsel = bm[EPL - 1];
+    int wj = EPL - 1;
+#pragma unroll
+    for (int j = EPL - 2; j >= 0; --j) {
+      if (bm[j] != 0ull) {
+        bsel = bm[j];
+        wj = j;
+      }
     }
-    tmask |= 1u << b;
-  }
-  // 3. the taken experts (k, or every eligible one if fewer), compacted in
-  //    id order, then each ranked among the others by (key desc, id asc)
-  if (lane < kMaxK) {
-    L.o_e[lane] = -1;
-    L.o_w[lane] = 0.0f;
-  }
-  int C = 0, eq_before = 0;
+    const bool ok = best != 0u;
+    const int wl = static_cast<int>(__builtin_ctzll(bsel | (1ull << 63)));  // in [0, 63]
+    float w = read_lane(wgt[0], wl);
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = j * kWave + lane;
-    const uint32_t pre = key[j] & tmask;
-    const bool live = key[j] != 0u;
-    const bool eq = live & (pre == thr);
-    const uint64_t beq = __builtin_amdgcn_ballot_w64(eq);
-    const int eq_rank = eq_before + static_cast<int>(__popcll(beq & lanemask_lt(lane)));
-    const bool take = live & ((pre > thr) | (eq & (eq_rank < need)));
-    eq_before += __popcll(beq);
-    const uint64_t bt = __builtin_amdgcn_ballot_w64(take);
-    if (take) {
-      const int idx = C + __popcll(bt & lanemask_lt(lane));
-      L.cand[idx] = make_float2(__uint_as_float(key[j]), __int_as_float(e));
-      L.c_w[idx] = wgt[j];
+    for (int j = 1; j < EPL; ++j) {
+      const float wjv = read_lane(wgt[j], wl);
+      w = (j == wj) ? wjv : w;
     }
-    C += __popcll(bt);
-  }
-  // pad to kMaxK entries with key 0 (beats nothing)
-  if (lane >= C && lane < kMaxK) L.cand[lane] = make_float2(__uint_as_float(0u), __int_as_float(0x7fffffff));
-  wave_lds_sync();
-  if (lane < C) {
-    const float2 me2 = L.cand[lane];
-    const uint32_t mk = __float_as_uint(me2.x);
-    const int mid = __float_as_int(me2.y);
-    const float4* cand4 = reinterpret_cast<const float4*>(L.cand);
-    int rr = 0;
+    w = ok ? w : 0.0f;
+    sum = (r == 0) ? w : sum + w;
+    const bool mine = lane == r;
+    my_e = mine ? (ok ? wj * kWave + wl : -1) : my_e;
+    my_w = mine ? w : my_w;
 #pragma unroll
-    for (int u = 0; u < kMaxK / 2; ++u) {
-      const float4 q = cand4[u];
-      const uint32_t k0 = __float_as_uint(q.x), k1 = __float_as_uint(q.z);
-      const int i0 = __float_as_int(q.y), i1 = __float_as_int(q.w);
-      rr += ((k0 > mk) | ((k0 == mk) & (i0 < mid))) ? 1 : 0;
-      rr += ((k1 > mk) | ((k1 == mk) & (i1 < mid))) ? 1 : 0;
-    }
-    L.o_e[rr] = mid;
-    L.o_w[rr] = L.c_w[lane];
+    for (int j = 0; j < EPL; ++j) key[j] = (j == wj && lane == wl) ? 0u : key[j];
   }
-  wave_lds_sync();
-  // renormalise in selection order, scale
-  float ow[kMaxK];
-  {
-    const float4* o4 = reinterpret_cast<const float4*>(L.o_w);
-#pragma unroll
-    for (int u = 0; u < kMaxK / 4; ++u) {
-      const float4 q = o4[u];
-      ow[4 * u] = q.x;
-      ow[4 * u + 1] = q.y;
-      ow[4 * u + 2] = q.z;
-      ow[4 * u + 3] = q.w;
-    }
-  }
-  float sum = ow[0];
-#pragma unroll
-  for (int it = 1; it < kMaxK; ++it)
-    if (it < k) sum = sum + ow[it];
+  // 3. renormalise (sum in selection order), scale
   const float denom = fmaxf(sum, FLT_EPSILON);
   out_e = -1;
   out_w = 0.0f;
   if (lane < k) {
-    out_e = L.o_e[lane];
-    const float w = sp.renorm ? L.o_w[lane] / denom : L.o_w[lane];
+    out_e = my_e;
+    const float w = sp.renorm ? my_w / denom : my_w;
     out_w = w * sp.routed_scale;
   }
-  wave_lds_sync();  // the scratch may be reused by the next token
 }
 
 // Correction bias in the lane layout (0 where absent).  Issued before the
