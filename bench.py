@@ -392,9 +392,11 @@ def bench_prefill(host_w13, host_w2, T: int = 4096, slots: int = 48, reps: int =
     y = torch.empty((pairs, H), dtype=torch.bfloat16, device=dev)
     out = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
 
+    wave_bm = [native.prefill_block_m(len(wv), H, I, dev) for wv in rep.waves]
+
     def waves_compute():
-        for (w13, w2, l2p), pw in zip(wave_banks, perms_w):
-            native.permute(ids, pw, log2phy=l2p, skip_unmapped=True)
+        for (w13, w2, l2p), pw, bm in zip(wave_banks, perms_w, wave_bm):
+            native.permute(ids, pw, log2phy=l2p, skip_unmapped=True, block_m=bm)
             native.grouped_mlp(x, K, w13, w2, pw, act, y, path=native.LMOE_PATH_MFMA)
         native.combine(y, w, out)
 
@@ -419,6 +421,17 @@ def bench_prefill(host_w13, host_w2, T: int = 4096, slots: int = 48, reps: int =
         res[f"{name}_ms"] = round(ms, 3)
         res[f"{name}_tflops"] = round(tf, 1)
         res[f"{name}_mfma_frac"] = round(tf / BF16_PEAK_TFLOPS, 4)
+    # per-wave grouped GEMM time and the row-tile height each wave ran with
+    per_wave = []
+    for (w13, w2, l2p), pw, bm in zip(wave_banks, perms_w, wave_bm):
+        native.permute(ids, pw, log2phy=l2p, skip_unmapped=True, block_m=bm)
+        with Timer() as t:
+            for _ in range(reps):
+                native.grouped_mlp(x, K, w13, w2, pw, act, y, path=native.LMOE_PATH_MFMA)
+        per_wave.append(round(t.ms() / reps, 3))
+    res["wave_block_m"] = wave_bm
+    res["wave_gemm_ms"] = per_wave
+    res["wave_max_pairs_per_slot"] = [int(pw.counts.max().item()) for pw in perms_w]
     torch.cuda.synchronize()
     same = torch.equal(out.view(torch.int16), ws_full.out[:T].view(torch.int16))
     res["waves_equal_full_layer_bitwise"] = bool(same)

@@ -187,7 +187,11 @@ int lmoe_gather_rows(const void* x, int H, int k, const int32_t* sorted_pairs,
  * indexed by flat pair (rows of unplaced pairs are left untouched).
  * path = LMOE_PATH_GEMV (weight-streaming, small slot groups),
  * LMOE_PATH_MFMA (bf16 MFMA tiles, block_m must equal the block_m given to
- * lmoe_permute) or LMOE_PATH_AUTO.  H % 8 == 0, I % 64 == 0. */
+ * lmoe_permute: 320 = one workgroup per CU with equal shares of 32-column
+ * blocks of 320-row tiles, 256 = a grid of 256 x 256 tiles, 128 = 128 x 128
+ * tiles; 320 needs H % 64 == 0) or
+ * LMOE_PATH_AUTO.  H % 8 == 0, I % 64 == 0.  Every block_m gives the same
+ * bits. */
 int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
                      const void* w13_slots, const void* w2_slots, int n_slots,
                      const int32_t* offsets, const int32_t* sorted_pairs,

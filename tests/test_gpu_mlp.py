@@ -278,8 +278,9 @@ def test_fused_decode_unmapped_pairs_and_add_term():
     (160, 8, 32, 16, 7168, 2048, True),    # DeepSeek-V3 expert shape
 ])
 def test_mfma_tile_heights_agree_bitwise(T, k, E, P, H, I, skip):
-    """The 256-row direct-to-LDS kernel against the 128-row kernel: both sum
-    every output's K/16 MFMA steps in the same order, so act and y must agree
+    """The 320-row block-range kernel and the 256-row direct-to-LDS kernel
+    against the 128-row kernel: all sum every output's K/16 MFMA steps in the
+    same order, so act and y must agree
     bit for bit; y is also held to the oracle's tolerance."""
     native = _native()
     print(f"case tile-heights T={T} k={k} E={E} P={P} H={H} I={I} skip={skip}", flush=True)
@@ -294,7 +295,8 @@ def test_mfma_tile_heights_agree_bitwise(T, k, E, P, H, I, skip):
     w2 = normal_bf16(rng, (P, H, I), 0.02)
     d_ids, d_l2p, d_x, d_w13, d_w2 = to_dev_i32(ids), to_dev_i32(l2p), to_dev_bf16(x), to_dev_bf16(w13), to_dev_bf16(w2)
     outs = {}
-    for bm in (128, 256):
+    bms = (128, 256, 320) if H % 64 == 0 else (128, 256)  # 320 needs K = H a multiple of 64
+    for bm in bms:
         perm = native.Permutation.allocate(T * k, P, "cuda")
         native.permute(d_ids, perm, log2phy=d_l2p, skip_unmapped=skip, block_m=bm)
         act = torch.zeros((T * k, I), dtype=torch.bfloat16, device="cuda")
@@ -303,8 +305,9 @@ def test_mfma_tile_heights_agree_bitwise(T, k, E, P, H, I, skip):
         torch.cuda.synchronize()
         n_placed = int(perm.meta[native.META_PAIRS].item())
         outs[bm] = (act[:n_placed].clone(), y.clone())
-    assert torch.equal(outs[128][0].view(torch.int16), outs[256][0].view(torch.int16))
-    assert torch.equal(outs[128][1].view(torch.int16), outs[256][1].view(torch.int16))
+    for bm in bms[1:]:
+        assert torch.equal(outs[128][0].view(torch.int16), outs[bm][0].view(torch.int16)), bm
+        assert torch.equal(outs[128][1].view(torch.int16), outs[bm][1].view(torch.int16)), bm
     slot = operm.remap(ids, l2p, P, skip_unmapped=skip)
     y_ref = omlp.grouped_mlp(x, slot, k, w13, w2)
     placed = (slot.reshape(-1) >= 0)
@@ -317,3 +320,41 @@ def test_mfma_tile_heights_agree_bitwise(T, k, E, P, H, I, skip):
     # <= 2048 elsewhere): more near-cancelling elements cross one ulp, while
     # every element stays within 2 x (ulp + cancellation floor)
     assert frac <= 1e-3 * max(1.0, H / 2048) and max_ulps <= 2.0
+
+
+@pytest.mark.parametrize("T,E,P", [
+    (2048, 64, 64),    # 384 gate-up units on 256 CUs: one or two per workgroup
+    (4096, 128, 128),  # the full Qwen3-shaped layer: three units per workgroup
+    (1400, 128, 42),   # a 42-slot wave: one unit per workgroup, some idle
+])
+def test_block_range_kernel_equals_tile_grid_at_prefill_sizes(T, E, P):
+    """The 320-row block-range GEMM over several rounds of units against the
+    256-row tile grid, bit for bit (the 256-row kernel is held to the oracle
+    above; an oracle pass at these sizes would take minutes)."""
+    native = _native()
+    k, H, I = 8, 2048, 768
+    print(f"case block-range T={T} E={E} P={P}", flush=True)
+    rng = np.random.default_rng(T + P)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    l2p = np.full(E, -1, dtype=np.int32)
+    l2p[rng.permutation(E)[:P]] = np.arange(P, dtype=np.int32)
+    g = torch.Generator(device="cuda").manual_seed(T)
+    d_x = (torch.randn((T, H), generator=g, device="cuda")).to(torch.bfloat16)
+    d_w13 = (0.02 * torch.randn((P, 2 * I, H), generator=g, device="cuda")).to(torch.bfloat16)
+    d_w2 = (0.02 * torch.randn((P, H, I), generator=g, device="cuda")).to(torch.bfloat16)
+    d_ids, d_l2p = to_dev_i32(ids), to_dev_i32(l2p)
+    outs = {}
+    for bm in (256, 320):
+        perm = native.Permutation.allocate(T * k, P, "cuda")
+        native.permute(d_ids, perm, log2phy=d_l2p, skip_unmapped=True, block_m=bm)
+        act = torch.zeros((T * k, I), dtype=torch.bfloat16, device="cuda")
+        y = torch.zeros((T * k, H), dtype=torch.bfloat16, device="cuda")
+        native.grouped_mlp(d_x, k, d_w13, d_w2, perm, act, y, path=native.LMOE_PATH_MFMA)
+        torch.cuda.synchronize()
+        n_placed = int(perm.meta[native.META_PAIRS].item())
+        assert n_placed > 0
+        outs[bm] = (act[:n_placed].clone(), y.clone())
+    assert torch.equal(outs[256][0].view(torch.int16), outs[320][0].view(torch.int16))
+    assert torch.equal(outs[256][1].view(torch.int16), outs[320][1].view(torch.int16))
+    assert torch.isfinite(outs[320][1].float()).all()
+

@@ -34,7 +34,7 @@ def _check(perm, ref, n_pairs):
     assert meta[3] == ref.tile_off[-1]
 
 
-@pytest.mark.parametrize("block_m", [128, 256])
+@pytest.mark.parametrize("block_m", [128, 256, 320])
 @pytest.mark.parametrize("T,k,E,P,use_map", [
     (1, 8, 128, 64, True),
     (8, 8, 128, 32, False),

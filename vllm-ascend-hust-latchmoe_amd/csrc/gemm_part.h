@@ -1,0 +1,315 @@
+// Prefill grouped GEMM with the work split evenly over the CUs.
+//
+// The unit of work is a block of 32 output columns of one row tile (a slot's
+// rows, up to BM = 320 of them: one tile covers a slot of up to 320 pairs,
+// the typical ~256 of a prefill wave plus its spread).  Blocks are grouped
+// into units of up to BN/2 (gate-up) or BN (down) columns, aligned within
+// the row tile.  The grid holds one workgroup per CU; with U units and G
+// workgroups, workgroup r runs the units [U*r/G, U*(r+1)/G), whole (a unit's
+// time is set by its K loop, ~2.5 us per 64 K-columns whatever its width,
+// so narrower pieces of a unit would not finish sooner).  A slot of up to 320
+// pairs is one row tile, so the usual prefill slot (~256 pairs plus spread)
+// streams each weight block once; the 256-row tiles of grouped_gemm_lds_kernel
+// cut such slots into a full tile and a remainder tile that streams the same
+// weights again.  The full Qwen3-shaped layer (128 slots, 6 gate-up units
+// per row tile) is exactly 3 units per CU.
+//
+// Ranges are numbered XCD-major (workgroup b runs on XCD b % 8), so that the
+// sub-tiles of one row tile, which read the same activation rows, share an L2.
+//
+// A sub-tile is the 256-row kernel's tile (grouped_gemm_lds_kernel) grown to
+// 320 rows: 8 waves as 2 x 4, each owning 160 x 64 (5 x 2 blocks of
+// v_mfma_f32_32x32x16_bf16 with the weight fragment first), operands staged
+// 64 K-columns at a time by direct-to-LDS loads into a two-stage ring, LDS
+// rows swizzled as there.  Weight rows of columns outside the sub-tile are not
+// loaded, and waves without live columns skip their MFMAs.  Every output
+// element accumulates its K/16 MFMA steps in increasing k, the order of the
+// other grouped kernels, so all of them give identical bits.
+//
+// Epilogue through LDS as in grouped_gemm_lds_kernel; the down tile (320 x 256
+// bf16 = 169 KB with padding) does not fit beside nothing else in 160 KB, so
+// it leaves in two halves of 160 rows, one per wave row.
+#pragma once
+
+#include <type_traits>
+
+#include "gemm_lds.h"
+
+namespace lmoe {
+
+struct PartTile {
+  static constexpr int BM = 320, BN = 256, BK = 64, WM = 2, WN = 4;
+  static constexpr int NW = WM * WN;
+  static constexpr int THREADS = NW * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;  // 160 x 64
+  static constexpr int NI = WTM / 32, NJ = WTN / 32;  // 5 x 2
+  static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int QA = A_BYTES / 1024 / NW;  // 5 loads per wave per stage
+  static constexpr int QB = B_BYTES / 1024 / NW;  // 4
+  static constexpr int RING_BYTES = 2 * STAGE_BYTES;                 // 144 KiB
+  static constexpr int GU_OUT_BYTES = BM * ((BN / 2) * 2 + 16);      // 85 KiB
+  static constexpr int DN_OUT_BYTES = (BM / 2) * (BN * 2 + 16);      // 82.5 KiB per half
+  static constexpr int MAIN_BYTES = RING_BYTES;
+  static constexpr int LDS_BYTES = MAIN_BYTES + BM * 4;  // + destination row ids (down)
+  static_assert(GU_OUT_BYTES <= MAIN_BYTES && DN_OUT_BYTES <= MAIN_BYTES, "epilogue staging");
+  static_assert(QA * NW * 1024 == A_BYTES && QB * NW * 1024 == B_BYTES, "1 KiB loads per wave");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS footprint too large");
+  static_assert(WTM * 2 == BM, "the down epilogue stages one wave row at a time");
+};
+
+// Columns (32-column blocks) of one sub-tile: gate-up BN/2 act columns
+// (BN weight rows, gate then up), down BN output columns.
+template <int MODE, class C>
+constexpr int part_max_blocks() {
+  return (MODE == kGateUp ? C::BN / 2 : C::BN) / 32;
+}
+
+template <int MODE, class C>
+__global__ __launch_bounds__(C::THREADS) void grouped_gemm_part_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+  int* s_rowid = reinterpret_cast<int*>(smem + C::MAIN_BYTES);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / C::WN;
+  const int wn = wave % C::WN;
+  constexpr int MAXB = part_max_blocks<MODE, C>();
+
+  // ---- this workgroup's share (XCD-major numbering) ----
+  // units: MAXB-block column groups of a row tile, aligned within it (the
+  // last one of a row tile may be narrower).  Workgroup r runs the whole
+  // units [U * r / G, U * (r + 1) / G) in row-major (tile, unit) order.
+  const int NB = (g.N + 31) >> 5;
+  const int UPT = (NB + MAXB - 1) / MAXB;  // units per row tile
+  const long long U = static_cast<long long>(g.meta[LMOE_META_TILES]) * UPT;
+  const int G = gridDim.x;  // a multiple of 8
+  const int r = (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3);
+  // blocks of units [0, u)
+  auto blocks_before = [&](long long u) {
+    const long long t = u / UPT;
+    return t * NB + (u - t * UPT) * MAXB;
+  };
+  long long b = blocks_before(U * r / G);
+  const long long b_end = blocks_before(U * (r + 1) / G);
+
+  const int lrow = lane >> 3;
+  const int frow = lane & 31;
+  const int fhi = lane >> 5;
+  const int fsw = (lane & 7) ^ ((lane >> 3) & 1);
+  const int KT = g.K / C::BK;
+
+  while (b < b_end) {
+    // ---- sub-tile: row tile `tile`, output columns [n0, n0 + 32 * w) ----
+    const int tile = static_cast<int>(b / NB);
+    const int cb = static_cast<int>(b - static_cast<long long>(tile) * NB);
+    // one unit: up to MAXB blocks, ending at the row tile's end
+    const int w = min(MAXB, NB - cb);
+    b += w;
+    const int n0 = cb * 32;
+    const int slot = find_tile_slot(g.tile_off, g.P, tile);
+    const int p0 = g.offsets[slot];
+    const int row0 = p0 + (tile - g.tile_off[slot]) * C::BM;
+    const int rows = min(C::BM, g.offsets[slot + 1] - row0);
+    const uint16_t* wbase = g.w + static_cast<long long>(slot) * g.w_slot_stride;
+    if (MODE == kDown) {
+      for (int t = tid; t < C::BM; t += C::THREADS)
+        s_rowid[t] = g.sorted_pairs[row0 + (t < rows ? t : 0)];
+    }
+
+    // per-lane source rows of this wave's load instructions (see gemm_lds.h),
+    // as 32-bit element offsets from the operand bases (the host checks that
+    // every operand spans fewer than 2^31 elements)
+    int a_src[C::QA];
+    int b_src[C::QB];
+#pragma unroll
+    for (int q = 0; q < C::QA; ++q) {
+      const int gq = wave * C::QA + q;
+      const int rr = gq * 8 + lrow;
+      const int pos = row0 + (rr < rows ? rr : 0);
+      const int arow = (MODE == kGateUp) ? g.sorted_pairs[pos] / g.topk : pos;
+      const int lchunk = ((lane & 7) ^ lrow ^ (gq & 1)) * 8;
+      a_src[q] = arow * g.K + lchunk;
+    }
+    // an instruction's 8 weight rows lie in one 32-row block, so whether
+    // they belong to a live column block is wave-uniform
+    auto b_live = [&](int q) {
+      const int gq = wave * C::QB + q;
+      return (MODE == kGateUp) ? ((gq * 8) % (C::BN / 2)) < 32 * w : gq * 8 < 32 * w;
+    };
+#pragma unroll
+    for (int q = 0; q < C::QB; ++q) {
+      const int gq = wave * C::QB + q;
+      const int rr = gq * 8 + lrow;
+      const int lchunk = ((lane & 7) ^ lrow ^ (gq & 1)) * 8;
+      int wrow;
+      if (MODE == kGateUp) {
+        const int half = rr / (C::BN / 2);
+        int i = n0 + rr - half * (C::BN / 2);
+        if (i >= g.N || !b_live(q)) i = n0;
+        wrow = half * g.I + i;
+      } else {
+        wrow = (n0 + rr < g.N && b_live(q)) ? n0 + rr : n0;
+      }
+      b_src[q] = wrow * g.K + lchunk;
+    }
+
+    auto issue = [&](int kt, int buf) {
+      char* st = smem + buf * C::STAGE_BYTES;
+      const int koff = kt * C::BK;
+#pragma unroll
+      for (int q = 0; q < C::QA; ++q)
+        load_lds16(g.a + (a_src[q] + koff), st + (wave * C::QA + q) * 1024);
+#pragma unroll
+      for (int q = 0; q < C::QB; ++q)
+        if (b_live(q)) load_lds16(wbase + (b_src[q] + koff), st + C::A_BYTES + (wave * C::QB + q) * 1024);
+    };
+
+    f32x16_t acc[C::NI][C::NJ];
+#pragma unroll
+    for (int i = 0; i < C::NI; ++i)
+#pragma unroll
+      for (int j = 0; j < C::NJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    int a_off[C::NI], b_off[C::NJ];
+#pragma unroll
+    for (int i = 0; i < C::NI; ++i) a_off[i] = (wm * C::WTM + i * 32 + frow) * 128;
+#pragma unroll
+    for (int j = 0; j < C::NJ; ++j) {
+      int br;
+      if (MODE == kGateUp) {
+        constexpr int HJ = C::NJ / 2;
+        br = (j < HJ) ? wn * (C::WTN / 2) + j * 32
+                      : C::BN / 2 + wn * (C::WTN / 2) + (j - HJ) * 32;
+      } else {
+        br = wn * C::WTN + j * 32;
+      }
+      b_off[j] = C::A_BYTES + (br + frow) * 128;
+    }
+    // this wave's live 32-row blocks and whether any of its columns is live
+    const int wave_rows = rows - wm * C::WTM;
+    const bool cols_live = (MODE == kGateUp) ? (wn * (C::WTN / 2) < 32 * w) : (wn * C::WTN < 32 * w);
+    const int ni_live = (wave_rows <= 0 || !cols_live) ? 0 : min(C::NI, (wave_rows + 31) >> 5);
+
+    issue(0, 0);
+    auto main_loop = [&](auto nl_tag) {
+      constexpr int NL = decltype(nl_tag)::value;
+      int buf = 0;
+      for (int kt = 0; kt < KT; ++kt) {
+        // stage kt landed and every wave is done with the other buffer
+        vm_wait_barrier<0>();
+        if (kt + 1 < KT) issue(kt + 1, buf ^ 1);
+        if constexpr (NL > 0) {
+          const char* st = smem + buf * C::STAGE_BYTES;
+          bf16x8_t bfr[2][C::NJ], af[2][NL];
+          auto read_frags = [&](int ks, int sl) {
+            const int cpos = ((2 * ks + fhi) ^ fsw) * 16;
+#pragma unroll
+            for (int j = 0; j < C::NJ; ++j) bfr[sl][j] = lds_read16(st + b_off[j] + cpos);
+#pragma unroll
+            for (int i = 0; i < NL; ++i) af[sl][i] = lds_read16(st + a_off[i] + cpos);
+          };
+          read_frags(0, 0);
+#pragma unroll
+          for (int ks = 0; ks < C::BK / 16; ++ks) {
+            if (ks + 1 < C::BK / 16) read_frags(ks + 1, (ks + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < NL; ++i)
+#pragma unroll
+              for (int j = 0; j < C::NJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][j], af[ks & 1][i],
+                                                                     acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        buf ^= 1;
+      }
+    };
+    // NL: 32-row blocks computed (a partial tile rounds up to 1, 2 or NI)
+    if (ni_live > 2) main_loop(std::integral_constant<int, C::NI>{});
+    else if (ni_live == 2) main_loop(std::integral_constant<int, 2>{});
+    else if (ni_live == 1) main_loop(std::integral_constant<int, 1>{});
+    else main_loop(std::integral_constant<int, 0>{});
+
+    // ---- epilogue: bf16 tile -> LDS -> 16-byte row stores ----
+    vm_wait_barrier<0>();  // every wave is done reading the operand ring
+    const int cb_base = (MODE == kGateUp ? wn * (C::WTN / 2) : wn * C::WTN) + 4 * fhi;
+    const int n_end = min(g.N, n0 + 32 * w);
+    if constexpr (MODE == kGateUp) {
+      constexpr int PITCH = (C::BN / 2) * 2 + 16;
+      constexpr int HJ = C::NJ / 2;
+      const int m = wm * C::WTM + frow;
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i) {
+        if (i >= ni_live) continue;
+        char* rowp = smem + (m + 32 * i) * PITCH;
+#pragma unroll
+        for (int j = 0; j < HJ; ++j) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = swiglu_bf16x2(acc[i][j][4 * q + 0], acc[i][j + HJ][4 * q + 0],
+                                              acc[i][j][4 * q + 1], acc[i][j + HJ][4 * q + 1]);
+            const uint32_t hi = swiglu_bf16x2(acc[i][j][4 * q + 2], acc[i][j + HJ][4 * q + 2],
+                                              acc[i][j][4 * q + 3], acc[i][j + HJ][4 * q + 3]);
+            *reinterpret_cast<uint2*>(rowp + (cb_base + j * 32 + 8 * q) * 2) = make_uint2(lo, hi);
+          }
+        }
+      }
+      vm_wait_barrier<0>();
+      constexpr int CPR = (C::BN / 2) / 8;  // 16-byte chunks per staged row
+      for (int e = tid; e < C::BM * CPR; e += C::THREADS) {
+        const int mm = e / CPR;
+        if (mm >= rows) break;
+        const int c = e - mm * CPR;
+        const int n = n0 + c * 8;
+        if (n >= n_end) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(smem + mm * PITCH + c * 16);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(g.out) +
+                                  static_cast<long long>(row0 + mm) * g.I + n) = v;
+      }
+      vm_wait_barrier<0>();  // the staged rows are read before the next sub-tile loads
+    } else {
+      constexpr int PITCH = C::BN * 2 + 16;
+      constexpr int CPR = C::BN / 8;
+#pragma unroll
+      for (int h = 0; h < C::WM; ++h) {
+        if (wm == h) {
+#pragma unroll
+          for (int i = 0; i < C::NI; ++i) {
+            if (i >= ni_live) continue;
+            char* rowp = smem + (frow + 32 * i) * PITCH;
+#pragma unroll
+            for (int j = 0; j < C::NJ; ++j) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const uint32_t lo = pack_bf16x2(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1]);
+                const uint32_t hi = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                *reinterpret_cast<uint2*>(rowp + (cb_base + j * 32 + 8 * q) * 2) =
+                    make_uint2(lo, hi);
+              }
+            }
+          }
+        }
+        vm_wait_barrier<0>();
+        const int hrows = min(C::WTM, rows - h * C::WTM);
+        for (int e = tid; e < C::WTM * CPR; e += C::THREADS) {
+          const int mm = e / CPR;
+          if (mm >= hrows) break;
+          const int c = e - mm * CPR;
+          const int n = n0 + c * 8;
+          if (n >= n_end) continue;
+          const uint4 v = *reinterpret_cast<const uint4*>(smem + mm * PITCH + c * 16);
+          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(g.out) +
+                                    static_cast<long long>(s_rowid[h * C::WTM + mm]) * g.N + n) = v;
+        }
+        vm_wait_barrier<0>();  // staged rows read before the next half / sub-tile
+      }
+    }
+  }
+}
+
+}  // namespace lmoe

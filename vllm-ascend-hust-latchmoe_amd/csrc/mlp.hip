@@ -17,6 +17,7 @@
 // npu_moe_token_unpermute (:3363-3366; out[t] = sum_j w[t,j] y[row(t,j)],
 // phase_split.py:1649-1656).
 #include "gemm_lds.h"
+#include "gemm_part.h"
 
 namespace lmoe {
 
@@ -467,21 +468,45 @@ static void launch_combine(const uint16_t* y, const int32_t* row_idx, const uint
 
 // ---------------------------------------------------------------------------
 // grouped MFMA GEMM launch (prefill).  block_m is the tile height the
-// permutation's tile table was built with: 256 runs the direct-to-LDS
-// 256 x 256 kernel (K a multiple of 64, 16-byte aligned operands), else the
-// 128 x 128 register-staged kernel over kBM-row parts of each tile.
+// permutation's tile table was built with: 320 runs the block-range kernel
+// (gemm_part.h: one workgroup per CU, equal column-block shares), 256 the
+// direct-to-LDS 256 x 256 tile grid (both: K a multiple of 64, 16-byte
+// aligned operands), 128 the register-staged 128 x 128 kernel.
 // ---------------------------------------------------------------------------
 using PrefillTile = LdsTile<256, 256, 2, 4, 2>;
+
+// Workgroups of the block-range kernel: one per CU, a multiple of 8 (one
+// share per XCD), queried once per device.
+static int part_grid() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  const int grid = ((cus + 7) / 8) * 8;
+  if (dev < 64) cached[dev] = grid;
+  return grid;
+}
 
 template <int MODE>
 static int launch_grouped_mfma(GemmArgs g, int n_pairs, int max_active, int block_m,
                                hipStream_t stream) {
-  if (block_m != PrefillTile::BM && block_m != kBM) return LMOE_ERR_UNSUPPORTED;
+  if (block_m != PartTile::BM && block_m != PrefillTile::BM && block_m != kBM)
+    return LMOE_ERR_UNSUPPORTED;
   const int ub_tiles = n_pairs / block_m + max_active + 1;
   g.block_m = block_m;
   const bool aligned = ((reinterpret_cast<uintptr_t>(g.a) | reinterpret_cast<uintptr_t>(g.w) |
                          reinterpret_cast<uintptr_t>(g.out)) & 15u) == 0;
   if (!aligned) return LMOE_ERR_SHAPE;
+  if (block_m == PartTile::BM) {
+    if (g.K % PartTile::BK != 0 || g.N % 8 != 0) return LMOE_ERR_SHAPE;
+    hipLaunchKernelGGL((grouped_gemm_part_kernel<MODE, PartTile>), dim3(part_grid()),
+                       dim3(PartTile::THREADS), 0, stream, g);
+    return LMOE_OK;
+  }
   if (block_m == PrefillTile::BM && g.K % PrefillTile::BK == 0 && g.N % 8 == 0) {
     const int col_tile = (MODE == kGateUp) ? PrefillTile::BN / 2 : PrefillTile::BN;
     const int grid = lds_gemm_grid(ub_tiles, (g.N + col_tile - 1) / col_tile);

@@ -141,8 +141,10 @@ def fused_experts(
     I = int(w13_slots.shape[1]) // 2
     ws = workspace or get_workspace(T, k, P, H, I, hidden.device)
     dst = out if out is not None else ws.out[:T]
-    native.permute(topk_ids, ws.perm, log2phy=log2phy)
-    if T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA:
+    decode = T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA
+    bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P, H, I, hidden.device)
+    native.permute(topk_ids, ws.perm, log2phy=log2phy, block_m=bm)
+    if decode:
         native.fused_moe_decode(hidden, topk_weights, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add,
                                 y=ws.y[: T * k])
     else:
@@ -384,7 +386,8 @@ def run_wave_prefill(
             handle = runtime.begin_slot_compute(prepared)
             try:
                 native.permute(topk_ids, ws.perm, log2phy=prepared.log2phy, skip_unmapped=True,
-                               table_len=total_logical if first else routed)
+                               table_len=total_logical if first else routed,
+                               block_m=native.prefill_block_m(len(plan.waves[w]), H, I, hidden.device))
                 first = False
                 native.grouped_mlp(hidden, k, prepared.w1, prepared.w2, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
             finally:
