@@ -163,8 +163,8 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     const uint16_t* __restrict__ add, uint16_t* __restrict__ out) {
   constexpr int LV = (R >= 4) ? 2 : 1;
   __shared__ float s_y[kFusedMaxPairs * kDnMaxRows];
-  __shared__ int s_pos[kFusedMaxPairs];
-  __shared__ float s_w[kFusedMaxPairs];
+  __shared__ __attribute__((aligned(16))) int s_pos[kFusedMaxPairs];
+  __shared__ __attribute__((aligned(16))) float s_w[kFusedMaxPairs];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int l5 = lane & 31;
@@ -265,7 +265,25 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     const int h = h0 + r;
     if (h >= H) continue;
     float acc = 0.0f;
-    for (int j = 0; j < topk; ++j) {
+    int j = 0;
+    if (topk % 4 == 0) {
+      // four pairs per step: one 16-byte read each of positions and weights,
+      // then the four y reads in flight together (summed in pair order)
+      for (; j < topk; j += 4) {
+        const int p = t * topk + j;
+        const int4 pos4 = *reinterpret_cast<const int4*>(&s_pos[p]);
+        const float4 w4 = *reinterpret_cast<const float4*>(&s_w[p]);
+        const float y0 = pos4.x >= 0 ? s_y[pos4.x * kDnMaxRows + r] : 0.0f;
+        const float y1 = pos4.y >= 0 ? s_y[pos4.y * kDnMaxRows + r] : 0.0f;
+        const float y2 = pos4.z >= 0 ? s_y[pos4.z * kDnMaxRows + r] : 0.0f;
+        const float y3 = pos4.w >= 0 ? s_y[pos4.w * kDnMaxRows + r] : 0.0f;
+        if (pos4.x >= 0) acc += w4.x * y0;
+        if (pos4.y >= 0) acc += w4.y * y1;
+        if (pos4.z >= 0) acc += w4.z * y2;
+        if (pos4.w >= 0) acc += w4.w * y3;
+      }
+    }
+    for (; j < topk; ++j) {
       const int p = t * topk + j;
       const int pos = s_pos[p];
       if (pos >= 0) acc += s_w[p] * s_y[pos * kDnMaxRows + r];
