@@ -280,14 +280,16 @@ struct RouterPermuteArgs {
 };
 
 // Block size and dynamic LDS of the one-launch routers: enough waves for
-// the tokens (and, gate form, at least four gate rows per block), the
+// the tokens (and, gate form, at least eight gate rows per block: 16
+// workgroups count in for 128 experts; measured 0.24 us faster than 32
+// workgroups of four rows, and 8 of sixteen rows slower again), the
 // permutation's pairs and its slot scan.
 inline void router_launch_shape(const RouterPermuteArgs& a, bool gate, int* threads,
                                 size_t* lds) {
   const int n_pairs = a.T * a.sp.k;
   int t = n_pairs > a.n_slots / 16 ? n_pairs : a.n_slots / 16;
   t = t > a.T * 64 ? t : a.T * 64;
-  if (gate) t = t > 256 ? t : 256;
+  if (gate) t = t > 512 ? t : 512;
   t = ((t + 63) / 64) * 64;
   t = t < 64 ? 64 : (t > kChunk ? kChunk : t);
   *threads = t;
