@@ -63,3 +63,22 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("LATCHMOE_HIP_LIB", str(tmp_path / "absent.so"))
     with pytest.raises(native.NativeLibraryMissing, match="no CPU or PyTorch fallback"):
         native.load_library()
+
+
+def test_prefill_block_m_policy():
+    """Row-tile height per prefill pass (no GPU: the CU count is given).
+    One round of 320-row units (6 per slot at I = 768) or many rounds -> 320;
+    just past one round on 256 CUs (258..320 units) -> the 256-row grid."""
+    from vllm_moe_offload_amd import native
+
+    H, I = 2048, 768
+    pick = lambda n, cus=256, h=H, i=I: native.prefill_block_m(n, h, i, cu_count=cus)
+    assert pick(42) == 320    # 252 units: one round
+    assert pick(43) == 256    # 258 units: two would run alone
+    assert pick(53) == 256    # 318 units
+    assert pick(54) == 320    # 324 units: balanced rounds
+    assert pick(128) == 320   # the full layer: 3 units per CU
+    assert pick(1) == 320
+    assert pick(43, cus=304) == 320          # fits one round on a larger part
+    assert pick(42, h=1000) == 256           # K = H not a multiple of 64
+    assert pick(64, i=2048) == 320           # 16 units per slot: 1024 units, 4 rounds

@@ -392,7 +392,8 @@ def _cu_count(device) -> int:
     return _CU_COUNT[idx]
 
 
-def prefill_block_m(n_experts: int, hidden: int, intermediate: int, device="cuda") -> int:
+def prefill_block_m(n_experts: int, hidden: int, intermediate: int, device="cuda",
+                    cu_count: int | None = None) -> int:
     """Row-tile height for the prefill GEMMs of one pass over n_experts slots
     (the block_m to build the permutation with).
 
@@ -403,10 +404,11 @@ def prefill_block_m(n_experts: int, hidden: int, intermediate: int, device="cuda
     are many.  Just past one round (a 43-slot wave on 256 CUs: 258 units) the
     last units would run alone, and the 256-row tile grid finishes first
     (measured 136 + 64 us against 166 + 74 us for gate_up + down); there 256
-    is returned.  Needs hidden % 64 == 0 (else 256)."""
+    is returned.  Needs hidden % 64 == 0 (else 256).  cu_count defaults to
+    the device's."""
     if hidden % 64 != 0:
         return MFMA_BLOCK_M
-    cus = _cu_count(device)
+    cus = int(cu_count) if cu_count is not None else _cu_count(device)
     units = int(n_experts) * ((int(intermediate) + 127) // 128)
     if cus < units <= cus + cus // 4:
         return MFMA_BLOCK_M
