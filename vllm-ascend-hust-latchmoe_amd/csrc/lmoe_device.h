@@ -294,6 +294,21 @@ __device__ __forceinline__ uint4 load_stream16(const uint16_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16-byte loads issued by every lane whatever the guard: where !ok the
+// address is clamped to p itself (a valid element) and the value replaced
+// by zeros.  A load inside a lane-dependent branch is waited for before the
+// branch ends, so per-chunk guarded loads complete one after another (a
+// decode GEMV measured 1.05 us slower out of 10); these stay in flight
+// together.
+__device__ __forceinline__ uint4 load_stream16_if(const uint16_t* p, int off, bool ok) {
+  const uint4 v = load_stream16(p + (ok ? off : 0));
+  return ok ? v : make_uint4(0u, 0u, 0u, 0u);
+}
+__device__ __forceinline__ uint4 load16_if(const uint16_t* p, int off, bool ok) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p + (ok ? off : 0));
+  return ok ? v : make_uint4(0u, 0u, 0u, 0u);
+}
+
 // Order LDS traffic of one wave: stores before the fence are seen by every
 // lane's loads after it.
 __device__ __forceinline__ void wave_lds_sync() {

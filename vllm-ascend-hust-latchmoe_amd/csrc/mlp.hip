@@ -49,7 +49,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      xv[c] = (h < H) ? *reinterpret_cast<const uint4*>(x + h) : make_uint4(0u, 0u, 0u, 0u);
+      xv[c] = load16_if(x, h, h < H);
     }
     const int s = active[a];
     const int i = blockIdx.x * 4 + wave;
@@ -60,10 +60,8 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      if (h < H) {
-        v[0] = dot8(xv[c], load_stream16(grow + h), v[0]);
-        v[1] = dot8(xv[c], load_stream16(urow + h), v[1]);
-      }
+      v[0] = dot8(xv[c], load_stream16_if(grow, h, h < H), v[0]);
+      v[1] = dot8(xv[c], load_stream16_if(urow, h, h < H), v[1]);
     }
     const float tot = reduce_scatter<2, 5, 0>(v, lane);
     const float up = read_lane(tot, 32);  // lane 32 holds the up total
@@ -84,13 +82,8 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      if (h < H) {
-        wg[c] = load_stream16(grow + h);
-        wu[c] = load_stream16(urow + h);
-      } else {
-        wg[c] = make_uint4(0u, 0u, 0u, 0u);
-        wu[c] = make_uint4(0u, 0u, 0u, 0u);
-      }
+      wg[c] = load_stream16_if(grow, h, h < H);
+      wu[c] = load_stream16_if(urow, h, h < H);
     }
     for (int r = 0; r < n; ++r) {
       const int t = sorted_pairs[p0 + r] / topk;
@@ -99,11 +92,9 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int h = c * 512 + lane * 8;
-        if (h < H) {
-          const uint4 xv = *reinterpret_cast<const uint4*>(xr + h);
-          v[0] = dot8(xv, wg[c], v[0]);
-          v[1] = dot8(xv, wu[c], v[1]);
-        }
+        const uint4 xv = load16_if(xr, h, h < H);
+        v[0] = dot8(xv, wg[c], v[0]);
+        v[1] = dot8(xv, wu[c], v[1]);
       }
       // lanes 0..31 end with the gate total, 32..63 with the up total
       const float tot = reduce_scatter<2, 5, 0>(v, lane);
@@ -119,7 +110,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      wr[c] = (ok && h < H) ? load_stream16(row + h) : make_uint4(0u, 0u, 0u, 0u);
+      wr[c] = load_stream16_if(row, h, ok && h < H);
     }
     for (int r = 0; r < n; ++r) {
       const int t = ONE ? 0 : sorted_pairs[p0 + r] / topk;
@@ -128,7 +119,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int h = c * 512 + lane * 8;
-        if (h < H) acc = dot8(*reinterpret_cast<const uint4*>(xr + h), wr[c], acc);
+        acc = dot8(load16_if(xr, h, h < H), wr[c], acc);
       }
       acc = wave_sum(acc);
       if (which == 1 && lane == 0) s_up[wave >> 1] = acc;
@@ -181,8 +172,7 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
 #pragma unroll
       for (int c = 0; c < DNC; ++c) {
         const int col = c * 256 + l5 * 8;
-        w[r][c] = (h < H && col < I) ? load_stream16(base2 + static_cast<size_t>(h) * I + col)
-                                     : make_uint4(0u, 0u, 0u, 0u);
+        w[r][c] = load_stream16_if(base2, h * I + col, h < H && col < I);
       }
     }
   };
@@ -221,16 +211,16 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
       float v[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) v[r] = 0.0f;
-      if (q < n) {
-        const uint16_t* ar = act + static_cast<size_t>(p0 + q) * I;
+      {
+        // the two half waves may have different token counts: loads past a
+        // half wave's count are clamped to act[0] and zeroed
+        const uint16_t* ar = act + static_cast<size_t>(q < n ? p0 + q : 0) * I;
 #pragma unroll
         for (int c = 0; c < DNC; ++c) {
           const int col = c * 256 + l5 * 8;
-          if (col < I) {
-            const uint4 av = *reinterpret_cast<const uint4*>(ar + col);
+          const uint4 av = load16_if(ar, col, q < n && col < I);
 #pragma unroll
-            for (int r = 0; r < R; ++r) v[r] = dot8(av, wcur[r][c], v[r]);
-          }
+          for (int r = 0; r < R; ++r) v[r] = dot8(av, wcur[r][c], v[r]);
         }
       }
       // reduce over the 32 lanes of each half wave: lane holds row r
@@ -330,8 +320,7 @@ __global__ __launch_bounds__(256) void down_rows_kernel(
 #pragma unroll
     for (int c = 0; c < DNC; ++c) {
       const int col = c * 256 + l5 * 8;
-      w[r][c] = (h < H && col < I) ? load_stream16(base2 + static_cast<size_t>(h) * I + col)
-                                   : make_uint4(0u, 0u, 0u, 0u);
+      w[r][c] = load_stream16_if(base2, h * I + col, h < H && col < I);
     }
   }
   for (int q = 0; q < n; ++q) {
@@ -344,11 +333,9 @@ __global__ __launch_bounds__(256) void down_rows_kernel(
 #pragma unroll
     for (int c = 0; c < DNC; ++c) {
       const int col = c * 256 + l5 * 8;
-      if (col < I) {
-        const uint4 av = *reinterpret_cast<const uint4*>(ar + col);
+      const uint4 av = load16_if(ar, col, col < I);
 #pragma unroll
-        for (int r = 0; r < R; ++r) v[r] = dot8(av, w[r][c], v[r]);
-      }
+      for (int r = 0; r < R; ++r) v[r] = dot8(av, w[r][c], v[r]);
     }
     // reduce over the 32 lanes of each half wave: lane holds row r
     const float tot = reduce_scatter<R, 4, 0>(v, lane);

@@ -35,8 +35,7 @@ __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int h = c * 512 + lane * 8;
-    w[c] = (h < H) ? *reinterpret_cast<const uint4*>(wrow + h)
-                   : make_uint4(0u, 0u, 0u, 0u);
+    w[c] = load16_if(wrow, h, h < H);
   }
   // kGateTok tokens per reduction (x rows in flight together; the same
   // lane-pair tree per token as a lone wave_sum, so the logits do not depend
@@ -47,7 +46,7 @@ __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      if (h < H) acc = dot8(*reinterpret_cast<const uint4*>(xr + h), w[c], acc);
+      acc = dot8(load16_if(xr, h, h < H), w[c], acc);
     }
     acc = wave_sum(acc);
     if (lane == 0) {
@@ -71,11 +70,8 @@ __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int h = c * 512 + lane * 8;
-        if (h < H) {
 #pragma unroll
-          for (int g = 0; g < kGateTok; ++g)
-            v[g] = dot8(*reinterpret_cast<const uint4*>(xr[g] + h), w[c], v[g]);
-        }
+        for (int g = 0; g < kGateTok; ++g) v[g] = dot8(load16_if(xr[g], h, h < H), w[c], v[g]);
       }
       // lane l ends with the total of token tb + l / 16
       const float acc = reduce_scatter<kGateTok, 5, 0>(v, lane);
