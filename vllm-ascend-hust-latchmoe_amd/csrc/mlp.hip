@@ -667,7 +667,12 @@ extern "C" int lmoe_down_combine(const void* act, int T, int H, int I, int k,
     const uint16_t* w2_ = static_cast<const uint16_t*>(w2_slots);                              \
     const uint16_t* add_ = static_cast<const uint16_t*>(add);                                  \
     uint16_t* out_ = static_cast<uint16_t*>(out);                                              \
-    if (T == 1)                                                                                \
+    if (T == 1 && k <= 8)                                                                      \
+      /* one slot per half wave (ranks < k <= 8): no next-slot prefetch */                     \
+      hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, false, true>), grid, dim3(256), 0,   \
+                         stream, a_, I, H, T, k, w2_, offsets, active, n_slots, row_idx, w,     \
+                         add_, out_);                                                          \
+    else if (T == 1)                                                                           \
       hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, PF, true>), grid, dim3(256), 0,      \
                          stream, a_, I, H, T, k, w2_, offsets, active, n_slots, row_idx, w,     \
                          add_, out_);                                                          \
