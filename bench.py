@@ -595,24 +595,28 @@ def bench_deepseek(batches=(1, 8, 32), prefill_tokens: int = 2048, reps: int = 2
                      torch.tensor([P], dtype=torch.int32, device=dev)])
     res: dict = {}
     per_expert = 3 * Hd * Id * 2
+    # the router appends the shared expert (id Ed -> slot P, weight 1)
+    spec = fused_moe.RouterSpec(top_k=Kd, scoring_func="sigmoid", use_grouped_topk=True, num_expert_group=8,
+                                topk_group=4, routed_scaling_factor=2.5, e_score_correction_bias=bias, n_shared=1)
 
     def make_step(B, path):
         x = torch.randn((B, Hd), generator=g, device=dev).to(torch.bfloat16)
         logits = torch.empty((B, Ed), dtype=torch.bfloat16, device=dev)
-        wk = torch.empty((B, Kd), dtype=torch.bfloat16, device=dev)
-        idk = torch.empty((B, Kd), dtype=torch.int32, device=dev)
-        wv = torch.ones((B, Kd + 1), dtype=torch.bfloat16, device=dev)
-        idv = torch.full((B, Kd + 1), Ed, dtype=torch.int32, device=dev)
+        wv = torch.empty((B, Kd + 1), dtype=torch.bfloat16, device=dev)
+        idv = torch.empty((B, Kd + 1), dtype=torch.int32, device=dev)
         ws = fused_moe.get_workspace(B, Kd + 1, P + 1, Hd, Id, dev, tag=f"ds{B}")
         out = torch.empty((B, Hd), dtype=torch.bfloat16, device=dev)
 
-        def step():
-            native.router_gate(x, gate, logits)
-            native.router_topk(logits, Kd, scoring="sigmoid", bias=bias, num_expert_group=8, topk_group=4,
-                               routed_scaling_factor=2.5, w_bf16=wk, ids=idk)
-            wv[:, :Kd].copy_(wk)
-            idv[:, :Kd].copy_(idk)
-            fused_moe.fused_experts(x, wv, idv, w13, w2, l2p, out=out, workspace=ws, path=path)
+        if path == native.LMOE_PATH_AUTO:
+            # decode: gate, selection and permutation (one launch up to 4
+            # tokens), then the GEMV body
+            def step():
+                fused_moe.decode_layer(x, gate, spec, w13, w2, l2p, workspace=ws, out=out, logits_out=logits,
+                                       w_out=wv, ids_out=idv)
+        else:
+            def step():
+                w, ids, _ = fused_moe.route(x, gate, spec, logits_out=logits, w_out=wv, ids_out=idv)
+                fused_moe.fused_experts(x, w, ids, w13, w2, l2p, out=out, workspace=ws, path=path)
 
         return step, ws
 

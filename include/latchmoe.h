@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define LMOE_ABI_VERSION 2
+#define LMOE_ABI_VERSION 3
 
 enum {
   LMOE_OK = 0,
@@ -96,10 +96,14 @@ int lmoe_router_gate(const void* x, const void* wg, int T, int H, int E,
  * Ties break toward the lower expert (or group) id.  Output order is the
  * selection order (descending score).  If renorm, w /= max(sum(w), FLT_EPSILON)
  * (sum in selection order); then w *= routed_scale.  w_f32 may be NULL.
- * E <= 512, k <= 16, n_group <= 64.  Replaces select_experts
+ * Rows of w / ids are k + n_shared wide: columns k .. k + n_shared - 1 hold
+ * the pinned shared-expert suffix, ids E, E + 1, ... with weight 1 (outside
+ * the renormalisation), the mix-placement suffix that select_experts appends
+ * (patch_fused_moe.py:4697-4727; checked as ids [E, E + S) at :2338-2370).
+ * E <= 512, k + n_shared <= 16, n_group <= 64.  Replaces select_experts
  * (moe_router_op.py:108-124, patch_fused_moe.py:597-632). */
 int lmoe_router_topk(const void* logits, int logits_f32, int T, int E, int k,
-                     int scoring, const float* bias, int n_group,
+                     int n_shared, int scoring, const float* bias, int n_group,
                      int topk_group, int renorm, float routed_scale,
                      float* w_f32, uint16_t* w_bf16, int32_t* ids,
                      hipStream_t stream);
@@ -112,7 +116,7 @@ int lmoe_router_topk(const void* logits, int logits_f32, int T, int E, int k,
  * Returns LMOE_ERR_SHAPE when T > 16, E > 256 or n_slots > 8192 (then use
  * the two calls). */
 int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
-                             int k, int scoring, const float* bias,
+                             int k, int n_shared, int scoring, const float* bias,
                              int n_group, int topk_group, int renorm,
                              float routed_scale, float* w_f32,
                              uint16_t* w_bf16, int32_t* ids,
@@ -136,7 +140,7 @@ int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
  * H > 8192 or x / wg are not 16-byte aligned (then use the separate calls). */
 int lmoe_router_gate_topk_permute(const void* x, const void* wg, int T, int H,
                                   int E, void* logits, int logits_f32, int k,
-                                  int scoring, const float* bias, int n_group,
+                                  int n_shared, int scoring, const float* bias, int n_group,
                                   int topk_group, int renorm,
                                   float routed_scale, float* w_f32,
                                   uint16_t* w_bf16, int32_t* ids,

@@ -203,3 +203,68 @@ def test_gate_select_permute_one_launch_equals_separate_calls(T, E, k, P, H, sco
         for name in ("counts", "offsets", "sorted_pairs", "row_idx", "active", "tile_off", "meta"):
             assert torch.equal(getattr(perm_a, name), getattr(perm_b, name)), (it, name)
         assert perm_b.sync.item() == 0
+
+
+@pytest.mark.parametrize("T,E,k,S,scoring,H", [
+    (1, 128, 8, 1, "softmax", 2048),
+    (16, 128, 8, 2, "softmax", 2048),
+    (1, 256, 8, 1, "sigmoid", 7168),   # the DeepSeek-style decode layer with its shared expert
+    (3, 256, 8, 1, "sigmoid", 7168),
+])
+def test_shared_suffix_in_all_three_routers(T, E, k, S, scoring, H):
+    """n_shared = S appends ids E..E+S-1 with weight 1 after the k routed
+    columns (the mix-placement suffix), in the plain selection, the
+    selection + permutation, and the gate + selection + permutation
+    launches; the permutation covers the suffix pairs through the slot
+    table like any other."""
+    native = _native()
+    print(f"case shared-suffix T={T} E={E} k={k} S={S} {scoring}", flush=True)
+    rng = np.random.default_rng(4100 + T * 7 + S)
+    grouped = scoring == "sigmoid"
+    G, TG, scale = (8, 4, 2.5) if grouped else (1, 1, 1.0)
+    kw = dict(scoring=scoring, num_expert_group=G, topk_group=TG, routed_scaling_factor=scale, n_shared=S)
+    bias_np = (rng.standard_normal(E) * (0.01 if grouped else 0.5)).astype(np.float32)
+    bias = torch.from_numpy(bias_np).cuda()
+    x = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
+    wg = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device="cuda")
+    native.router_gate(x, wg, logits)
+    lg = bf16_to_f32(from_dev_bf16(logits))
+    if grouped:
+        r_ids, r_w, r_wb = orc.grouped_sigmoid_topk(lg, k, bias=bias_np, n_group=G, topk_group=TG, scale=scale)
+    else:
+        r_ids, r_w, r_wb = orc.softmax_topk(lg, k, bias=bias_np)
+    # expected rows: the routed columns, then the suffix with weight 1
+    suffix = np.broadcast_to(np.arange(E, E + S, dtype=np.int32), (T, S))
+    e_ids = np.concatenate([r_ids, suffix], axis=1)
+    e_w = np.concatenate([r_w, np.ones((T, S), np.float32)], axis=1)
+    e_wb = np.concatenate([r_wb, np.full((T, S), 0x3F80, np.uint16)], axis=1)
+    # slot table over E + S ids: the suffix pinned at the last S slots
+    used = np.unique(r_ids)
+    P = max(64, used.size + S)
+    l2p = np.full(E + S, -1, dtype=np.int32)
+    l2p[used] = rng.permutation(P - S)[: used.size]
+    l2p[E:] = np.arange(P - S, P, dtype=np.int32)
+    d_l2p = to_dev_i32(l2p)
+    ref = operm.init_routing(e_ids, P, log2phy=l2p, block_m=native.MFMA_BLOCK_M)
+
+    def check(w, ids, w_f32):
+        np.testing.assert_array_equal(ids.cpu().numpy(), e_ids)
+        np.testing.assert_array_equal(from_dev_bf16(w), e_wb)
+        np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), e_w.view(np.uint32))
+
+    wf = torch.empty((T, k + S), dtype=torch.float32, device="cuda")
+    w, ids, _ = native.router_topk(logits, k, bias=bias, w_f32=wf, **kw)
+    torch.cuda.synchronize()
+    check(w, ids, wf)
+    for fused_gate in (False, True):
+        perm = native.Permutation.allocate(T * (k + S), P, "cuda")
+        wf = torch.empty((T, k + S), dtype=torch.float32, device="cuda")
+        if fused_gate:
+            lg2 = torch.empty((T, E), dtype=torch.bfloat16, device="cuda")
+            w, ids, _ = native.router_gate_topk_permute(x, wg, lg2, k, perm, log2phy=d_l2p, bias=bias, w_f32=wf, **kw)
+        else:
+            w, ids, _ = native.router_topk_permute(logits, k, perm, log2phy=d_l2p, bias=bias, w_f32=wf, **kw)
+        torch.cuda.synchronize()
+        check(w, ids, wf)
+        _check_perm(native, perm, ref, T * (k + S))

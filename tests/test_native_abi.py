@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = native.load_library()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.lmoe_abi_version() == 2
+    assert lib.lmoe_abi_version() == 3
     assert lib.lmoe_status_string(1001) == b"unsupported shape"
 
 
@@ -37,9 +37,13 @@ def test_argument_errors_are_reported_without_a_gpu():
 
     lib = native.load_library()
     # null outputs / bad sizes are rejected on the host
-    assert lib.lmoe_router_topk(None, 0, 1, 128, 8, 0, None, 1, 1, 1, 1.0, None, None, None, None) == 1000
-    assert lib.lmoe_router_topk(ctypes.c_void_p(16), 0, 1, 1024, 8, 0, None, 1, 1, 1, 1.0, None,
+    assert lib.lmoe_router_topk(None, 0, 1, 128, 8, 0, 0, None, 1, 1, 1, 1.0, None, None, None, None) == 1000
+    assert lib.lmoe_router_topk(ctypes.c_void_p(16), 0, 1, 1024, 8, 0, 0, None, 1, 1, 1, 1.0, None,
                                 ctypes.c_void_p(16), ctypes.c_void_p(16), None) == 1001
+    # shared suffix: a negative count is an argument error, k + n_shared > 16 a shape error
+    p16 = ctypes.c_void_p(16)
+    assert lib.lmoe_router_topk(p16, 0, 1, 128, 8, -1, 0, None, 1, 1, 1, 1.0, None, p16, p16, None) == 1000
+    assert lib.lmoe_router_topk(p16, 0, 1, 128, 8, 9, 0, None, 1, 1, 1, 1.0, None, p16, p16, None) == 1001
     assert lib.lmoe_permute(None, 4, None, 0, 0, 0, 128, *([None] * 7), None, 0, None) == 1000
     assert lib.lmoe_grouped_mlp(*([ctypes.c_void_p(16)] * 1), 1, 2048, 100, 8, *([ctypes.c_void_p(16)] * 2), 4,
                                 *([ctypes.c_void_p(16)] * 5), 8, 128, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == 1001

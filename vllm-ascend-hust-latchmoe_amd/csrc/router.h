@@ -128,8 +128,14 @@ __device__ __forceinline__ void select_and_permute(
     int e;
     float w;
     select_token<EPL, SCORE>(sp, lg, bv, L.sel[wave], e, w);
-    if (lane < sp.k) {
-      const int o = wave * sp.k + lane;
+    const int kw = sp.k + sp.n_shared;
+    if (lane >= sp.k) {
+      // the pinned shared-expert suffix: ids E, E + 1, ..., weight 1
+      e = sp.E + lane - sp.k;
+      w = 1.0f;
+    }
+    if (lane < kw) {
+      const int o = wave * kw + lane;
       ids[o] = e;
       L.ids[o] = e;
       w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
@@ -137,7 +143,7 @@ __device__ __forceinline__ void select_and_permute(
     }
   }
   __syncthreads();
-  const int n_pairs = T * sp.k;
+  const int n_pairs = T * (sp.k + sp.n_shared);
   if constexpr (PPL > 0) {
     if (wave == 0)
       permute_wave_any<PPL>(L.ids, n_pairs, log2phy, n_log2phy, P, skip, block_m, counts,
@@ -218,10 +224,10 @@ __global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
                                       tile_off, meta, hist, L);
 }
 
-inline int check_select(int T, int E, int k, int scoring, int n_group,
+inline int check_select(int T, int E, int k, int n_shared, int scoring, int n_group,
                         int topk_group) {
-  if (T < 0 || E <= 0 || k <= 0) return LMOE_ERR_ARG;
-  if (E > kMaxE || k > kMaxK || k > E) return LMOE_ERR_SHAPE;
+  if (T < 0 || E <= 0 || k <= 0 || n_shared < 0) return LMOE_ERR_ARG;
+  if (E > kMaxE || k + n_shared > kMaxK || k > E) return LMOE_ERR_SHAPE;
   if (scoring != LMOE_SCORING_SOFTMAX && scoring != LMOE_SCORING_SIGMOID)
     return LMOE_ERR_UNSUPPORTED;
   if (scoring == LMOE_SCORING_SIGMOID && n_group > 1) {
@@ -232,12 +238,13 @@ inline int check_select(int T, int E, int k, int scoring, int n_group,
   return LMOE_OK;
 }
 
-inline SelectParams make_select(int E, int k, int scoring, const float* bias,
+inline SelectParams make_select(int E, int k, int n_shared, int scoring, const float* bias,
                                 int n_group, int topk_group, int renorm,
                                 float routed_scale) {
   SelectParams sp;
   sp.E = E;
   sp.k = k;
+  sp.n_shared = n_shared;
   sp.scoring = scoring;
   sp.bias = bias;
   sp.n_group = scoring == LMOE_SCORING_SIGMOID ? (n_group > 1 ? n_group : 1) : 1;
@@ -282,7 +289,7 @@ struct RouterPermuteArgs {
 // permutation's pairs and its slot scan.
 inline void router_launch_shape(const RouterPermuteArgs& a, bool gate, int* threads,
                                 size_t* lds) {
-  const int n_pairs = a.T * a.sp.k;
+  const int n_pairs = a.T * (a.sp.k + a.sp.n_shared);
   int t = n_pairs > a.n_slots / 16 ? n_pairs : a.n_slots / 16;
   t = t > a.T * 64 ? t : a.T * 64;
   if (gate) t = t > 512 ? t : 512;
@@ -305,7 +312,7 @@ int launch_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
   int threads;
   size_t lds;
   router_launch_shape(a, false, &threads, &lds);
-  const int ppl = router_perm_ppl(a.T * a.sp.k, a.n_slots);
+  const int ppl = router_perm_ppl(a.T * (a.sp.k + a.sp.n_shared), a.n_slots);
 #define LMOE_TP(EPL, Q)                                                                            \
   hipLaunchKernelGGL((topk_permute_kernel<EPL, Q, SCORE>), dim3(1), dim3(threads), lds, stream,    \
                      a.logits, a.logits_f32, a.T, a.sp, a.w_f32, a.w_bf16, a.ids, a.log2phy,      \
@@ -334,7 +341,7 @@ int launch_gate_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
   router_launch_shape(a, true, &threads, &lds);
   const int nw = threads / 64;
   const int blocks = (a.sp.E + nw - 1) / nw;
-  const int ppl = router_perm_ppl(a.T * a.sp.k, a.n_slots);
+  const int ppl = router_perm_ppl(a.T * (a.sp.k + a.sp.n_shared), a.n_slots);
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const uint16_t* wg = static_cast<const uint16_t*>(a.wg);
 #define LMOE_GTP(NC, EPL, Q, ONE)                                                                 \

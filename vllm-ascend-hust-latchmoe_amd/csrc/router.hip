@@ -39,8 +39,14 @@ __global__ __launch_bounds__(256) void topk_kernel(
   int e;
   float w;
   select_token<EPL, SCORE>(sp, lg, bv, lds[wave], e, w);
-  if (t < T && lane < sp.k) {
-    const size_t o = static_cast<size_t>(t) * sp.k + lane;
+  const int kw = sp.k + sp.n_shared;
+  if (lane >= sp.k) {
+    // the pinned shared-expert suffix: ids E, E + 1, ..., weight 1
+    e = sp.E + lane - sp.k;
+    w = 1.0f;
+  }
+  if (t < T && lane < kw) {
+    const size_t o = static_cast<size_t>(t) * kw + lane;
     ids[o] = e;
     w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
     if (w_f32 != nullptr) w_f32[o] = w;
@@ -91,18 +97,18 @@ extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
 }
 
 extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
-                                int E, int k, int scoring, const float* bias,
+                                int E, int k, int n_shared, int scoring, const float* bias,
                                 int n_group, int topk_group, int renorm,
                                 float routed_scale, float* w_f32,
                                 uint16_t* w_bf16, int32_t* ids,
                                 hipStream_t stream) {
   if (logits == nullptr || w_bf16 == nullptr || ids == nullptr)
     return LMOE_ERR_ARG;
-  const int st = check_select(T, E, k, scoring, n_group, topk_group);
+  const int st = check_select(T, E, k, n_shared, scoring, n_group, topk_group);
   if (st != LMOE_OK) return st;
   if (T == 0) return LMOE_OK;
   const SelectParams sp =
-      make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+      make_select(E, k, n_shared, scoring, bias, n_group, topk_group, renorm, routed_scale);
   const dim3 grid((T + 3) / 4);
 #define LMOE_TK(EPL, S) \
   hipLaunchKernelGGL((topk_kernel<EPL, S>), grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids)
@@ -121,8 +127,8 @@ extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
 }
 
 extern "C" int lmoe_router_topk_permute(
-    const void* logits, int logits_f32, int T, int E, int k, int scoring, const float* bias,
-    int n_group, int topk_group, int renorm, float routed_scale, float* w_f32, uint16_t* w_bf16,
+    const void* logits, int logits_f32, int T, int E, int k, int n_shared, int scoring,
+    const float* bias, int n_group, int topk_group, int renorm, float routed_scale, float* w_f32, uint16_t* w_bf16,
     int32_t* ids, const int32_t* log2phy, int n_log2phy, int n_slots, int skip_unmapped,
     int block_m, int32_t* counts, int32_t* offsets, int32_t* sorted_pairs, int32_t* row_idx,
     int32_t* active, int32_t* tile_off, int32_t* meta, hipStream_t stream) {
@@ -130,7 +136,7 @@ extern "C" int lmoe_router_topk_permute(
       offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
       active == nullptr || tile_off == nullptr || meta == nullptr)
     return LMOE_ERR_ARG;
-  int st = check_select(T, E, k, scoring, n_group, topk_group);
+  int st = check_select(T, E, k, n_shared, scoring, n_group, topk_group);
   if (st != LMOE_OK) return st;
   if (n_slots <= 0 || block_m <= 0) return LMOE_ERR_ARG;
   if (log2phy != nullptr && n_log2phy <= 0) return LMOE_ERR_ARG;
@@ -141,7 +147,7 @@ extern "C" int lmoe_router_topk_permute(
   ra.T = T;
   ra.logits = const_cast<void*>(logits);
   ra.logits_f32 = logits_f32;
-  ra.sp = make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  ra.sp = make_select(E, k, n_shared, scoring, bias, n_group, topk_group, renorm, routed_scale);
   ra.w_f32 = w_f32;
   ra.w_bf16 = w_bf16;
   ra.ids = ids;
@@ -163,7 +169,7 @@ extern "C" int lmoe_router_topk_permute(
 
 extern "C" int lmoe_router_gate_topk_permute(
     const void* x, const void* wg, int T, int H, int E, void* logits, int logits_f32, int k,
-    int scoring, const float* bias, int n_group, int topk_group, int renorm, float routed_scale,
+    int n_shared, int scoring, const float* bias, int n_group, int topk_group, int renorm, float routed_scale,
     float* w_f32, uint16_t* w_bf16, int32_t* ids, const int32_t* log2phy, int n_log2phy,
     int n_slots, int skip_unmapped, int block_m, int32_t* counts, int32_t* offsets,
     int32_t* sorted_pairs, int32_t* row_idx, int32_t* active, int32_t* tile_off, int32_t* meta,
@@ -173,7 +179,7 @@ extern "C" int lmoe_router_gate_topk_permute(
       active == nullptr || tile_off == nullptr || meta == nullptr || sync == nullptr)
     return LMOE_ERR_ARG;
   if (T < 0 || H <= 0) return LMOE_ERR_ARG;
-  int st = check_select(T, E, k, scoring, n_group, topk_group);
+  int st = check_select(T, E, k, n_shared, scoring, n_group, topk_group);
   if (st != LMOE_OK) return st;
   if (n_slots <= 0 || block_m <= 0) return LMOE_ERR_ARG;
   if (log2phy != nullptr && n_log2phy <= 0) return LMOE_ERR_ARG;
@@ -191,7 +197,7 @@ extern "C" int lmoe_router_gate_topk_permute(
   ra.T = T;
   ra.logits = logits;
   ra.logits_f32 = logits_f32;
-  ra.sp = make_select(E, k, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  ra.sp = make_select(E, k, n_shared, scoring, bias, n_group, topk_group, renorm, routed_scale);
   ra.w_f32 = w_f32;
   ra.w_bf16 = w_bf16;
   ra.ids = ids;

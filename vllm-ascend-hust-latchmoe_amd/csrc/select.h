@@ -28,6 +28,7 @@ constexpr int kMaxE = kMaxEPL * kWave;
 struct SelectParams {
   int E;
   int k;
+  int n_shared;  // shared-expert suffix appended to every token (ids E.., weight 1)
   int scoring;
   const float* bias;
   int n_group;

@@ -87,13 +87,18 @@ class RouterSpec:
     topk_group: int = 1
     routed_scaling_factor: float = 1.0
     e_score_correction_bias: torch.Tensor | None = None
+    # pinned shared experts appended to every token by the router (ids
+    # E, E+1, ..., weight 1): select_experts' mix-placement suffix
+    # (patch_fused_moe.py:4697-4727)
+    n_shared: int = 0
 
 
 def route(hidden: torch.Tensor, gate_weight: torch.Tensor | None, spec: RouterSpec, *,
           router_logits: torch.Tensor | None = None, logits_out: torch.Tensor | None = None,
           w_out: torch.Tensor | None = None, ids_out: torch.Tensor | None = None):
     """Gate (if gate_weight is given) then expert selection on the GPU.
-    Returns (topk_weights bf16 [T,k], topk_ids int32 [T,k], logits)."""
+    Returns (topk_weights bf16 [T,k+S], topk_ids int32 [T,k+S], logits), S =
+    spec.n_shared suffix columns."""
     if gate_weight is not None:
         T = hidden.shape[0]
         E = gate_weight.shape[0]
@@ -109,7 +114,7 @@ def route(hidden: torch.Tensor, gate_weight: torch.Tensor | None, spec: RouterSp
         num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
         topk_group=int(spec.topk_group or 1) if grouped else 1,
         renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
-        w_bf16=w_out, ids=ids_out,
+        n_shared=int(spec.n_shared), w_bf16=w_out, ids=ids_out,
     )
     return w, ids, router_logits
 
@@ -182,9 +187,10 @@ def decode_layer(
     separate calls."""
     T = hidden.shape[0]
     k = int(spec.top_k)
+    kw = k + int(spec.n_shared)  # pairs per token, shared suffix included
     P = int(w13_slots.shape[0])
     ws = workspace
-    if ws.perm.n_slots != P or ws.perm.n_pairs != T * k:
+    if ws.perm.n_slots != P or ws.perm.n_pairs != T * kw:
         raise ValueError("workspace permutation does not match the slot bank or the batch")
     if logits_out is None:
         logits_out = torch.empty((T, gate_weight.shape[0]), dtype=hidden.dtype, device=hidden.device)
@@ -194,7 +200,7 @@ def decode_layer(
         num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
         topk_group=int(spec.topk_group or 1) if grouped else 1,
         renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
-        w_bf16=w_out, ids=ids_out,
+        n_shared=int(spec.n_shared), w_bf16=w_out, ids=ids_out,
     )
     if T <= ONE_LAUNCH_ROUTER_MAX_TOKENS:
         w, ids, _ = native.router_gate_topk_permute(hidden, gate_weight, logits_out, k, ws.perm, **sel)
@@ -202,12 +208,12 @@ def decode_layer(
         logits = native.router_gate(hidden, gate_weight, logits_out)
         w, ids, _ = native.router_topk_permute(logits, k, ws.perm, **sel)
     dst = out if out is not None else ws.out[:T]
-    if T * k <= native.FUSED_DECODE_MAX_PAIRS:
-        native.fused_moe_decode(hidden, w, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add,
-                                y=ws.y[: T * k])
+    if T * kw <= native.FUSED_DECODE_MAX_PAIRS:
+        native.fused_moe_decode(hidden, w, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], dst, add=add,
+                                y=ws.y[: T * kw])
     else:
-        native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k])
-        native.combine(ws.y[: T * k], w, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
+        native.grouped_mlp(hidden, kw, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], ws.y[: T * kw])
+        native.combine(ws.y[: T * kw], w, dst, row_mask=ws.perm.row_idx[: T * kw], add=add)
     return dst, w, ids
 
 

@@ -114,17 +114,13 @@ class SlotMoELayer(torch.nn.Module):
             use_grouped_topk=self.use_grouped_topk, num_expert_group=self.num_expert_group,
             topk_group=self.topk_group, routed_scaling_factor=self.routed_scaling_factor,
             e_score_correction_bias=self.e_score_correction_bias,
+            n_shared=self.n_shared_experts if self.mix_placement else 0,
         )
 
     # ------------------------------------------------------------ pieces
     def router(self, hidden: torch.Tensor):
         """Captured piece 1: (topk_weights, topk_ids) incl. the shared suffix."""
         w, ids, _ = route(hidden, self.gate_weight, self.router_spec)
-        if self.mix_placement:
-            T = ids.shape[0]
-            sid = torch.full((T, 1), self.num_routed_experts, dtype=torch.int32, device=ids.device)
-            ids = torch.cat([ids, sid], dim=1).contiguous()
-            w = torch.cat([w, torch.ones((T, 1), dtype=w.dtype, device=w.device)], dim=1).contiguous()
         return w, ids
 
     def stage(self, topk_ids: torch.Tensor, phase: int = PHASE_DECODE) -> None:

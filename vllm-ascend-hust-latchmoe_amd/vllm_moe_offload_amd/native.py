@@ -62,16 +62,16 @@ _SIGNATURES = {
     "lmoe_router_gate": (_i, [_vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "lmoe_router_topk": (
         _i,
-        [_vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp],
+        [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp],
     ),
     "lmoe_router_topk_permute": (
         _i,
-        [_vp, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
+        [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
          _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "lmoe_router_gate_topk_permute": (
         _i,
-        [_vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
+        [_vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
          _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "lmoe_permute_workspace_bytes": (_sz, [_i, _i]),
@@ -192,12 +192,15 @@ def router_topk(
     topk_group: int = 1,
     renormalize: bool = True,
     routed_scaling_factor: float = 1.0,
+    n_shared: int = 0,
     w_bf16: torch.Tensor | None = None,
     ids: torch.Tensor | None = None,
     w_f32: torch.Tensor | None = None,
     stream=None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
-    """Select top_k experts per token; returns (w_bf16 [T,k], ids int32 [T,k], w_f32)."""
+    """Select top_k experts per token; returns (w_bf16 [T,k+S], ids int32
+    [T,k+S], w_f32) with S = n_shared columns of the pinned shared-expert
+    suffix (ids E, E+1, ..., weight 1) after the routed ones."""
     lib = load_library()
     if logits.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("logits must be bf16 or f32")
@@ -212,17 +215,18 @@ def router_topk(
     if bias is not None:
         _need(bias, "e_score_correction_bias", torch.float32, (E,))
     dev = logits.device
+    kw = int(top_k) + int(n_shared)
     if w_bf16 is None:
-        w_bf16 = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
+        w_bf16 = torch.empty((T, kw), dtype=torch.bfloat16, device=dev)
     if ids is None:
-        ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
-    _need(w_bf16, "topk_weights", torch.bfloat16, (T, top_k))
-    _need(ids, "topk_ids", torch.int32, (T, top_k))
+        ids = torch.empty((T, kw), dtype=torch.int32, device=dev)
+    _need(w_bf16, "topk_weights", torch.bfloat16, (T, kw))
+    _need(ids, "topk_ids", torch.int32, (T, kw))
     if w_f32 is not None:
-        _need(w_f32, "w_f32", torch.float32, (T, top_k))
+        _need(w_f32, "w_f32", torch.float32, (T, kw))
     _check(
         lib.lmoe_router_topk(
-            _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), mode,
+            _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), int(n_shared), mode,
             _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
             int(bool(renormalize)), float(routed_scaling_factor),
             _ptr(w_f32), _ptr(w_bf16), _ptr(ids), _stream(stream),
@@ -246,6 +250,7 @@ def router_topk_permute(
     topk_group: int = 1,
     renormalize: bool = True,
     routed_scaling_factor: float = 1.0,
+    n_shared: int = 0,
     w_bf16: torch.Tensor | None = None,
     ids: torch.Tensor | None = None,
     w_f32: torch.Tensor | None = None,
@@ -265,23 +270,24 @@ def router_topk_permute(
     if bias is not None:
         _need(bias, "e_score_correction_bias", torch.float32, (E,))
     dev = logits.device
+    kw = int(top_k) + int(n_shared)
     if w_bf16 is None:
-        w_bf16 = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
+        w_bf16 = torch.empty((T, kw), dtype=torch.bfloat16, device=dev)
     if ids is None:
-        ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
-    _need(w_bf16, "topk_weights", torch.bfloat16, (T, top_k))
-    _need(ids, "topk_ids", torch.int32, (T, top_k))
+        ids = torch.empty((T, kw), dtype=torch.int32, device=dev)
+    _need(w_bf16, "topk_weights", torch.bfloat16, (T, kw))
+    _need(ids, "topk_ids", torch.int32, (T, kw))
     if w_f32 is not None:
-        _need(w_f32, "w_f32", torch.float32, (T, top_k))
-    if T * top_k != perm.n_pairs:
-        raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {T * top_k}")
+        _need(w_f32, "w_f32", torch.float32, (T, kw))
+    if T * kw != perm.n_pairs:
+        raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {T * kw}")
     n_table = 0
     if log2phy is not None:
         _need(log2phy, "log2phy", torch.int32)
         n_table = int(log2phy.numel())
     bm = MFMA_BLOCK_M if block_m is None else int(block_m)
     status = lib.lmoe_router_topk_permute(
-        _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), mode,
+        _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), int(n_shared), mode,
         _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
         int(bool(renormalize)), float(routed_scaling_factor),
         _ptr(w_f32), _ptr(w_bf16), _ptr(ids),
@@ -292,8 +298,8 @@ def router_topk_permute(
     if status == LMOE_ERR_SHAPE:
         router_topk(logits, top_k, scoring=scoring, bias=bias, num_expert_group=num_expert_group,
                     topk_group=topk_group, renormalize=renormalize,
-                    routed_scaling_factor=routed_scaling_factor, w_bf16=w_bf16, ids=ids, w_f32=w_f32,
-                    stream=stream)
+                    routed_scaling_factor=routed_scaling_factor, n_shared=n_shared, w_bf16=w_bf16, ids=ids,
+                    w_f32=w_f32, stream=stream)
         permute(ids, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, block_m=bm, stream=stream)
         return w_bf16, ids, w_f32
     _check(status, "lmoe_router_topk_permute")
@@ -317,6 +323,7 @@ def router_gate_topk_permute(
     topk_group: int = 1,
     renormalize: bool = True,
     routed_scaling_factor: float = 1.0,
+    n_shared: int = 0,
     w_bf16: torch.Tensor | None = None,
     ids: torch.Tensor | None = None,
     w_f32: torch.Tensor | None = None,
@@ -341,16 +348,17 @@ def router_gate_topk_permute(
     if bias is not None:
         _need(bias, "e_score_correction_bias", torch.float32, (E,))
     dev = x.device
+    kw = int(top_k) + int(n_shared)
     if w_bf16 is None:
-        w_bf16 = torch.empty((T, top_k), dtype=torch.bfloat16, device=dev)
+        w_bf16 = torch.empty((T, kw), dtype=torch.bfloat16, device=dev)
     if ids is None:
-        ids = torch.empty((T, top_k), dtype=torch.int32, device=dev)
-    _need(w_bf16, "topk_weights", torch.bfloat16, (T, top_k))
-    _need(ids, "topk_ids", torch.int32, (T, top_k))
+        ids = torch.empty((T, kw), dtype=torch.int32, device=dev)
+    _need(w_bf16, "topk_weights", torch.bfloat16, (T, kw))
+    _need(ids, "topk_ids", torch.int32, (T, kw))
     if w_f32 is not None:
-        _need(w_f32, "w_f32", torch.float32, (T, top_k))
-    if T * top_k != perm.n_pairs:
-        raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {T * top_k}")
+        _need(w_f32, "w_f32", torch.float32, (T, kw))
+    if T * kw != perm.n_pairs:
+        raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {T * kw}")
     n_table = 0
     if log2phy is not None:
         _need(log2phy, "log2phy", torch.int32)
@@ -358,7 +366,7 @@ def router_gate_topk_permute(
     bm = MFMA_BLOCK_M if block_m is None else int(block_m)
     status = lib.lmoe_router_gate_topk_permute(
         _ptr(x), _ptr(wg), T, H, E, _ptr(logits), int(logits.dtype == torch.float32), int(top_k),
-        mode, _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
+        int(n_shared), mode, _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
         int(bool(renormalize)), float(routed_scaling_factor),
         _ptr(w_f32), _ptr(w_bf16), _ptr(ids),
         _ptr(log2phy), n_table, perm.n_slots, int(bool(skip_unmapped)), bm,
@@ -370,8 +378,8 @@ def router_gate_topk_permute(
         return router_topk_permute(
             logits, top_k, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, block_m=bm,
             scoring=scoring, bias=bias, num_expert_group=num_expert_group, topk_group=topk_group,
-            renormalize=renormalize, routed_scaling_factor=routed_scaling_factor, w_bf16=w_bf16,
-            ids=ids, w_f32=w_f32, stream=stream,
+            renormalize=renormalize, routed_scaling_factor=routed_scaling_factor, n_shared=n_shared,
+            w_bf16=w_bf16, ids=ids, w_f32=w_f32, stream=stream,
         )
     _check(status, "lmoe_router_gate_topk_permute")
     perm.block_m = bm

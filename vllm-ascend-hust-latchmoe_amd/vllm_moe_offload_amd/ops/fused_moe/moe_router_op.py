@@ -48,16 +48,13 @@ def _moe_router_impl(
         use_grouped_topk=bool(use_grouped_topk), num_expert_group=int(num_expert_group or 1),
         topk_group=int(topk_group or 1), routed_scaling_factor=float(routed_scaling_factor),
         e_score_correction_bias=bias,
+        # the selection kernel appends the shared suffix (ids num_experts..,
+        # weight 1) itself
+        n_shared=int(num_shared_experts) if mix_placement else 0,
     )
     w, ids, _ = route(hidden_states, None, spec, router_logits=logits)
     if w.dtype != hidden_states.dtype:
         w = w.to(hidden_states.dtype)
-    if mix_placement and int(num_shared_experts) > 0:
-        T = int(ids.shape[0])
-        S = int(num_shared_experts)
-        shared_ids = torch.arange(int(num_experts), int(num_experts) + S, dtype=torch.int32, device=ids.device)
-        ids = torch.cat([ids, shared_ids.expand(T, S)], dim=1).contiguous()
-        w = torch.cat([w, torch.ones((T, S), dtype=w.dtype, device=w.device)], dim=1).contiguous()
     return w, ids
 
 
