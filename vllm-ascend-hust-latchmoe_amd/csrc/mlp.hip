@@ -22,27 +22,25 @@
 namespace lmoe {
 
 // ---------------------------------------------------------------------------
-// gate_up GEMV + SiLU*mul.  grid (ceil(I/RPB), max_active), 4 waves.
-// Block (bx, a) serves the a-th active slot (active[] / offsets[] of the
-// permutation).  Without SPLIT each wave owns one row pair i (gate row i and
-// up row I+i, 2*NC 16-byte chunks per lane, loaded non-temporally, RPB = 4);
-// with SPLIT (long rows, NC > 8) waves 2w and 2w+1 own the gate and the up
-// row of one i (RPB = 2) and meet in LDS.  The slot's tokens stream past one
-// at a time (x rows from L2); act is written in sorted order.  (Reducing
+// gate_up GEMV + SiLU*mul, rows up to 4096 columns.  grid (ceil(I/4),
+// max_active), 4 waves.  Block (bx, a) serves the a-th active slot (active[] /
+// offsets[] of the permutation); each wave owns one row pair i (gate row i
+// and up row I+i, 2*NC 16-byte chunks per lane, loaded non-temporally).  The
+// slot's tokens stream past one at a time (x rows from L2); act is written in
+// sorted order.  Longer rows: gateup_gemv_cols_kernel.  (Reducing
 // several tokens per step needs twice the registers, and the lost occupancy
 // costs more than the shorter chain saves: measured slower at B = 4 and 16.)
 // ---------------------------------------------------------------------------
-template <int NC, bool SPLIT, bool ONE>
+template <int NC, bool ONE>
 __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, int H, int I, int topk,
     const uint16_t* __restrict__ w13, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ active,
     const int32_t* __restrict__ meta, uint16_t* __restrict__ act) {
-  __shared__ float s_up[2];
   const int a = blockIdx.y;  // < n_slots: active[] has an entry (-1 past the active slots)
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  if (ONE && !SPLIT) {
+  if (ONE) {
     // one token: its x row needs no index, so it is loaded before active[a]
     // returns, and the weight rows wait on that one load only
     uint4 xv[NC];
@@ -70,63 +68,110 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
   }
   const int s = active[a];
   if (s < 0) return;
-  // one token: active rank a is sorted position a and serves one pair
-  const int p0 = ONE ? a : offsets[s];
-  const int n = ONE ? 1 : offsets[s + 1] - p0;
-  if (!SPLIT) {
-    const int i = blockIdx.x * 4 + wave;
-    if (i >= I) return;
-    const uint16_t* grow = w13 + (static_cast<size_t>(s) * 2 * I + i) * H;
-    const uint16_t* urow = grow + static_cast<size_t>(I) * H;
-    uint4 wg[NC], wu[NC];
+  const int p0 = offsets[s];
+  const int n = offsets[s + 1] - p0;
+  const int i = blockIdx.x * 4 + wave;
+  if (i >= I) return;
+  const uint16_t* grow = w13 + (static_cast<size_t>(s) * 2 * I + i) * H;
+  const uint16_t* urow = grow + static_cast<size_t>(I) * H;
+  uint4 wg[NC], wu[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int h = c * 512 + lane * 8;
+    wg[c] = load_stream16_if(grow, h, h < H);
+    wu[c] = load_stream16_if(urow, h, h < H);
+  }
+  for (int r = 0; r < n; ++r) {
+    const int t = sorted_pairs[p0 + r] / topk;
+    const uint16_t* xr = x + static_cast<size_t>(t) * H;
+    float v[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      wg[c] = load_stream16_if(grow, h, h < H);
-      wu[c] = load_stream16_if(urow, h, h < H);
+      const uint4 xv = load16_if(xr, h, h < H);
+      v[0] = dot8(xv, wg[c], v[0]);
+      v[1] = dot8(xv, wu[c], v[1]);
     }
-    for (int r = 0; r < n; ++r) {
-      const int t = sorted_pairs[p0 + r] / topk;
-      const uint16_t* xr = x + static_cast<size_t>(t) * H;
-      float v[2] = {0.0f, 0.0f};
+    // lanes 0..31 end with the gate total, 32..63 with the up total
+    const float tot = reduce_scatter<2, 5, 0>(v, lane);
+    const float up = read_lane(tot, 32);  // lane 32 holds the up total
+    if (lane == 0) act[static_cast<size_t>(p0 + r) * I + i] = swiglu_bf16(tot, up);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gate_up GEMV + SiLU*mul with the columns split over the waves.  grid
+// (ceil(I/RP), max_active), 4 waves.  Block (bx, a) owns the RP row pairs
+// i0 = RP bx .. i0 + RP - 1 of the a-th active slot; wave w holds chunks w,
+// w + 4, w + 8, ... (512 columns each, 16 bytes per lane, non-temporal) of
+// all 2 RP rows (gate i, up i for each i), so each token's x row is read
+// once per block, a quarter by each wave, instead of once per wave and row
+// pair.  The four waves' partial sums meet in LDS (double-buffered by token
+// parity, one barrier per token) and wave 0 adds them in wave order.  Every
+// token's act is computed the same way whatever the batch, so one token
+// alone gives the bits it gets in a batch.
+// ---------------------------------------------------------------------------
+template <int NC, int RP>
+__global__ __launch_bounds__(256) void gateup_gemv_cols_kernel(
+    const uint16_t* __restrict__ x, int H, int I, int topk,
+    const uint16_t* __restrict__ w13, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ active,
+    uint16_t* __restrict__ act) {
+  constexpr int CPW = (NC + 3) / 4;  // chunks per wave
+  constexpr int NR = 2 * RP;         // rows: gate i0, up i0, gate i0 + 1, ...
+  constexpr int LB = (NR >= 8) ? 3 : (NR >= 4) ? 2 : 1;
+  static_assert((1 << LB) == NR, "2 RP must be a power of two");
+  __shared__ float s_part[2][4][NR];  // [token parity][wave][row]
+  const int a = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int s = active[a];
+  if (s < 0) return;  // uniform over the block
+  const int i0 = blockIdx.x * RP;
+  uint4 wr[NR][CPW];
+  {
+    const uint16_t* g0 = w13 + (static_cast<size_t>(s) * 2 * I) * H;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int h = c * 512 + lane * 8;
-        const uint4 xv = load16_if(xr, h, h < H);
-        v[0] = dot8(xv, wg[c], v[0]);
-        v[1] = dot8(xv, wu[c], v[1]);
+    for (int j = 0; j < NR; ++j) {
+      // rows past I (the last block of a ragged I) load row 0 and are not stored
+      const int i = i0 + (j >> 1);
+      const uint16_t* row = g0 + (static_cast<size_t>((j & 1) * I) + (i < I ? i : 0)) * H;
+#pragma unroll
+      for (int q = 0; q < CPW; ++q) {
+        const int h = (wave + 4 * q) * 512 + lane * 8;
+        wr[j][q] = load_stream16_if(row, h, h < H);
       }
-      // lanes 0..31 end with the gate total, 32..63 with the up total
-      const float tot = reduce_scatter<2, 5, 0>(v, lane);
-      const float up = read_lane(tot, 32);  // lane 32 holds the up total
-      if (lane == 0) act[static_cast<size_t>(p0 + r) * I + i] = swiglu_bf16(tot, up);
     }
-  } else {
-    const int i = blockIdx.x * 2 + (wave >> 1);
-    const int which = wave & 1;  // 0 gate row, 1 up row
-    const bool ok = i < I;
-    const uint16_t* row = w13 + (static_cast<size_t>(s) * 2 * I + which * I + (ok ? i : 0)) * H;
-    uint4 wr[NC];
+  }
+  const int p0 = offsets[s];
+  const int n = offsets[s + 1] - p0;
+  int t_next = n > 0 ? sorted_pairs[p0] / topk : 0;
+  for (int r = 0; r < n; ++r) {
+    const int t = t_next;
+    if (r + 1 < n) t_next = sorted_pairs[p0 + r + 1] / topk;
+    const uint16_t* xr = x + static_cast<size_t>(t) * H;
+    float v[NR];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int h = c * 512 + lane * 8;
-      wr[c] = load_stream16_if(row, h, ok && h < H);
+    for (int j = 0; j < NR; ++j) v[j] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < CPW; ++q) {
+      const int h = (wave + 4 * q) * 512 + lane * 8;
+      const uint4 xv = load16_if(xr, h, h < H);
+#pragma unroll
+      for (int j = 0; j < NR; ++j) v[j] = dot8(xv, wr[j][q], v[j]);
     }
-    for (int r = 0; r < n; ++r) {
-      const int t = ONE ? 0 : sorted_pairs[p0 + r] / topk;
-      const uint16_t* xr = x + static_cast<size_t>(t) * H;
-      float acc = 0.0f;
+    // lane groups of 64 / NR end with one row's partial sum each
+    const float tot = reduce_scatter<NR, 5, 0>(v, lane);
+    if ((lane & ((64 >> LB) - 1)) == 0) s_part[r & 1][wave][lane >> (6 - LB)] = tot;
+    __syncthreads();
+    if (wave == 0 && lane < RP && i0 + lane < I) {
+      float g = 0.0f, u = 0.0f;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int h = c * 512 + lane * 8;
-        acc = dot8(load16_if(xr, h, h < H), wr[c], acc);
+      for (int w = 0; w < 4; ++w) {
+        g += s_part[r & 1][w][2 * lane];
+        u += s_part[r & 1][w][2 * lane + 1];
       }
-      acc = wave_sum(acc);
-      if (which == 1 && lane == 0) s_up[wave >> 1] = acc;
-      __syncthreads();
-      if (ok && which == 0 && lane == 0)
-        act[static_cast<size_t>(p0 + r) * I + i] = swiglu_bf16(acc, s_up[wave >> 1]);
-      __syncthreads();
+      act[static_cast<size_t>(p0 + r) * I + i0 + lane] = swiglu_bf16(g, u);
     }
   }
 }
@@ -424,22 +469,33 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
                               hipStream_t stream) {
   const int nc = (H + 511) / 512;
   const dim3 g4((I + 3) / 4, max_active);
-  const dim3 g2((I + 1) / 2, max_active);
-#define LMOE_GU(NC, SPLIT, G)                                                                 \
+  // long rows: the column-split kernel.  (For H <= 4096 it measured 3%
+  // faster at 16 tokens but 0.7 us slower at one token, and one layout must
+  // serve every batch size, so the row-per-wave kernels stay there.)
+  const bool cols = nc > 8;
+#define LMOE_GU(NC)                                                                           \
   do {                                                                                        \
     if (one)                                                                                  \
-      hipLaunchKernelGGL((gateup_gemv_kernel<NC, SPLIT, true>), G, dim3(256), 0, stream, x, H, \
-                         I, topk, w13, offsets, sorted_pairs, active, meta, act);             \
+      hipLaunchKernelGGL((gateup_gemv_kernel<NC, true>), g4, dim3(256), 0, stream, x, H, I,    \
+                         topk, w13, offsets, sorted_pairs, active, meta, act);                \
     else                                                                                      \
-      hipLaunchKernelGGL((gateup_gemv_kernel<NC, SPLIT, false>), G, dim3(256), 0, stream, x,   \
-                         H, I, topk, w13, offsets, sorted_pairs, active, meta, act);          \
+      hipLaunchKernelGGL((gateup_gemv_kernel<NC, false>), g4, dim3(256), 0, stream, x, H, I,   \
+                         topk, w13, offsets, sorted_pairs, active, meta, act);                \
   } while (0)
-  if (nc <= 2) LMOE_GU(2, false, g4);
-  else if (nc <= 4) LMOE_GU(4, false, g4);
-  else if (nc <= 8) LMOE_GU(8, false, g4);
-  else if (nc <= 14) LMOE_GU(14, true, g2);
-  else if (nc <= 16) LMOE_GU(16, true, g2);
-  else return LMOE_ERR_SHAPE;
+#define LMOE_GC(NC, RP)                                                                      \
+  hipLaunchKernelGGL((gateup_gemv_cols_kernel<NC, RP>), dim3((I + (RP)-1) / (RP), max_active),  \
+                     dim3(256), 0, stream, x, H, I, topk, w13, offsets, sorted_pairs, active, act)
+  if (cols) {
+    // the four waves split each row's columns and share every x row (for
+    // one token too, so that a token's act does not depend on its batch)
+    if (nc <= 16) LMOE_GC(16, 2);
+    else return LMOE_ERR_SHAPE;
+    return LMOE_OK;
+  }
+#undef LMOE_GC
+  if (nc <= 2) LMOE_GU(2);
+  else if (nc <= 4) LMOE_GU(4);
+  else LMOE_GU(8);
 #undef LMOE_GU
   return LMOE_OK;
 }
