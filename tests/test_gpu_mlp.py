@@ -194,7 +194,7 @@ def _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None, with_y=Fals
     (16, 8, 64, 64, 2048, 768),
     (64, 8, 128, 128, 2048, 768),   # 512 pairs
     (128, 8, 128, 128, 2048, 768),  # 1024 pairs, the entry point's maximum
-    (2, 9, 12, 12, 7168, 2048),     # DeepSeek-V3-style rows (split gate/up waves)
+    (2, 9, 12, 12, 7168, 2048),     # DeepSeek-V3-style rows (column-split gate_up waves)
     (5, 4, 40, 24, 1024, 192),      # I not a multiple of the 256-column chunk
     (2, 6, 70, 70, 4096, 1536),
     (3, 4, 16, 16, 768, 4096),      # widest I (R = 2 rows per down block)
@@ -218,7 +218,7 @@ def test_fused_decode_more_shapes(T, k, E, P, H, I):
 
 @pytest.mark.parametrize("T,k,E,H,I", [
     (13, 6, 8, 2048, 768),   # ~10 tokens per slot: groups of 4 and a ragged tail
-    (7, 3, 4, 7168, 2048),   # split gate/up waves; down rows in groups of 2 pairs
+    (7, 3, 4, 7168, 2048),   # column-split gate_up waves; down rows in groups of 2 pairs
     (9, 2, 3, 768, 4096),    # widest I: one pair per down reduction
 ])
 def test_batched_tokens_equal_one_token_at_a_time(T, k, E, H, I):
