@@ -243,8 +243,8 @@ int lmoe_down_combine(const void* act, int T, int H, int I, int k,
  *   out[t] = (add ? add[t] : 0) + sum_j w[t][j] * W2_s(t,j) act[pos(t,j)].
  * gate_up GEMV + SiLU*mul into act (sorted order), then either the down GEMV
  * fused with the weighted combine (each workgroup owns a few output columns
- * of every token; two launches, used for T == 1 or y == NULL), or, for
- * T > 1 with a y workspace ([T*k, H] bf16, flat pair order on return),
+ * of every token; two launches, used for T*k <= 16 or y == NULL), or, for
+ * more pairs with a y workspace ([T*k, H] bf16, flat pair order on return),
  * the down GEMV per (row block, slot) into y and the combine (three
  * launches: no workgroup walks the slots in turn).  Both give the same out
  * bit for bit.  Each slot's weights are read once however many tokens chose

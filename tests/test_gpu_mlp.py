@@ -177,7 +177,8 @@ def test_combine_masks_unplaced_pairs_and_adds_shared():
 
 def _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None, with_y=False):
     """with_y: the three-launch body (down per row block and slot into y,
-    then the combine) that T > 1 takes when given the y workspace."""
+    then the combine) that more than 16 pairs take when given the y
+    workspace (up to 16 pairs run the fused body either way)."""
     T, H = d_x.shape
     k = d_ids.shape[1]
     P, I = d_w13.shape[0], d_w13.shape[1] // 2

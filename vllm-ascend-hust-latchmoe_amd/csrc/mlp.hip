@@ -778,9 +778,12 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                               sorted_pairs, active, meta, max_active, T == 1,
                               static_cast<uint16_t*>(act), stream);
   if (st != LMOE_OK) return st;
-  if (y != nullptr && T > 1) {
+  if (y != nullptr && T > 1 && n_pairs > 16) {
     // slots serving several tokens: down per (row block, slot) into y (flat
-    // pair order), then the combine
+    // pair order), then the combine.  Up to 16 pairs (two slots per half
+    // wave of the fused kernel) the fused down + combine is faster: 27.7
+    // against 28.9 us per layer at 2 tokens, equal at 4, slower from 8 on;
+    // both give the same bits.
     st = launch_down_rows(static_cast<const uint16_t*>(act), H, I,
                           static_cast<const uint16_t*>(w2_slots), offsets, sorted_pairs, active,
                           max_active, static_cast<uint16_t*>(y), stream);

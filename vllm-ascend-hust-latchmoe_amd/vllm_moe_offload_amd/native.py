@@ -656,8 +656,9 @@ def fused_moe_decode(
     stream=None,
 ) -> torch.Tensor:
     """Decode layer body: gate_up GEMV, then down GEMV fused with the combine
-    (T == 1 or no y), or for T > 1 with a [T*k, H] bf16 workspace y the down
-    GEMV per (row block, slot) into y and the combine; same out either way."""
+    (up to 16 pairs, or no y), or with a [T*k, H] bf16 workspace y and more
+    pairs the down GEMV per (row block, slot) into y and the combine; same out
+    either way."""
     lib = load_library()
     _need(x, "x", torch.bfloat16)
     T, H = x.shape
