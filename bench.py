@@ -608,8 +608,8 @@ def bench_deepseek(batches=(1, 8, 32), prefill_tokens: int = 2048, reps: int = 2
         out = torch.empty((B, Hd), dtype=torch.bfloat16, device=dev)
 
         if path == native.LMOE_PATH_AUTO:
-            # decode: gate, selection and permutation (one launch up to 4
-            # tokens), then the GEMV body
+            # decode: gate, selection and permutation (one launch for one
+            # token), then the GEMV body
             def step():
                 fused_moe.decode_layer(x, gate, spec, w13, w2, l2p, workspace=ws, out=out, logits_out=logits,
                                        w_out=wv, ids_out=idv)

@@ -205,7 +205,7 @@ def test_c1_config_eight_tokens_thirty_two_slots():
 
 @pytest.mark.parametrize("B", [1, 4, 16])
 def test_decode_layer_graph_replays_equal_eager(B):
-    """decode_layer captured once (one-launch router up to 4 tokens, the
+    """decode_layer captured once (one-launch router for one token, the
     several-token y body above 1) and replayed over steps whose staging
     changes the slot table: every replay equals an eager decode_layer on the
     same inputs bit for bit, the router's arrival counter is back at zero,

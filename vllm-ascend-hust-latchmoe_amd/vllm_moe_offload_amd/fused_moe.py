@@ -159,10 +159,12 @@ def fused_experts(
 
 
 # Up to this many tokens the decode router runs as one launch (gate,
-# selection, permutation); with more, the gate's few large workgroups of the
-# one-launch form cost more than the separate gate launch saves (measured at
-# 16 tokens: 24.5 us against 4.9 + 12.0 us).
-ONE_LAUNCH_ROUTER_MAX_TOKENS = 4
+# selection, permutation); with more, the separate gate launch and the
+# selection + permutation launch are faster.  Measured in the 48-layer decode
+# graph: one token 23.6 against 23.8 us per layer, four tokens 43.8 against
+# 43.6 us; router-only loops give the two launches 0.1 us at 2 and 3 tokens
+# and 7.4 us at 16.
+ONE_LAUNCH_ROUTER_MAX_TOKENS = 1
 
 
 def decode_layer(
