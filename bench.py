@@ -107,8 +107,9 @@ class DecodeModel:
         for l in range(n_layers):
             g.manual_seed(seed * 1000 + l)
             self.gates.append((torch.randn((E, H), generator=g, device=dev) * 0.02).to(torch.bfloat16))
+            # the Zipf skew is a gate bias (added to the logits before the softmax)
             bias = torch.tensor(zipf_bias(seed * 7919 + l), dtype=torch.float32, device=dev)
-            self.specs.append(RouterSpec(top_k=K, scoring_func="softmax", renormalize=True, e_score_correction_bias=bias))
+            self.specs.append(RouterSpec(top_k=K, scoring_func="softmax", renormalize=True, logit_bias=bias))
             self.rt.register_host_buffers(layer_id=l, w13_host=host_w13, w2_host=host_w2, slot_device=dev)
 
     def bank(self, l):
@@ -120,7 +121,7 @@ def _route(x, model, l, w_out, ids_out, logits_out):
     from vllm_moe_offload_amd import native
 
     native.router_gate(x, model.gates[l], logits_out)
-    native.router_topk(logits_out, K, bias=model.specs[l].e_score_correction_bias, w_bf16=w_out, ids=ids_out)
+    native.router_topk(logits_out, K, logit_bias=model.specs[l].logit_bias, w_bf16=w_out, ids=ids_out)
 
 
 def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int, budget_s: float) -> dict:

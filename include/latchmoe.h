@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define LMOE_ABI_VERSION 3
+#define LMOE_ABI_VERSION 4
 
 enum {
   LMOE_OK = 0,
@@ -87,12 +87,15 @@ int lmoe_abi_version(void);
 int lmoe_router_gate(const void* x, const void* wg, int T, int H, int E,
                      void* logits, int logits_f32, hipStream_t stream);
 
-/* Expert selection.  scoring = LMOE_SCORING_SOFTMAX: f32 softmax over E of
- * l + bias (bias may be NULL: an additive per-expert logit bias), the k
- * largest probabilities.  scoring = LMOE_SCORING_SIGMOID: s = sigmoid(l),
- * selection score s + bias (bias may be NULL), n_group contiguous groups
- * ranked by the sum of their two largest selection scores, the topk_group best
- * groups kept, k largest selection scores inside the kept groups, weights = s.
+/* Expert selection.  l = logits + logit_bias (logit_bias may be NULL: the
+ * router gate's linear bias, one f32 add before scoring).
+ * scoring = LMOE_SCORING_SOFTMAX: p = f32 softmax over E of l.
+ * scoring = LMOE_SCORING_SIGMOID: p = sigmoid(l).  The selection score is
+ * p + bias (bias = e_score_correction_bias, may be NULL: used for selection
+ * only, as vLLM's grouped_topk and CANN's gating top-k use it); with
+ * sigmoid and n_group > 1, n_group contiguous groups ranked by the sum of
+ * their two largest selection scores, the topk_group best groups kept; the
+ * k largest selection scores (inside the kept groups); weights = p.
  * Ties break toward the lower expert (or group) id.  Output order is the
  * selection order (descending score).  If renorm, w /= max(sum(w), FLT_EPSILON)
  * (sum in selection order); then w *= routed_scale.  w_f32 may be NULL.
@@ -103,7 +106,8 @@ int lmoe_router_gate(const void* x, const void* wg, int T, int H, int E,
  * E <= 512, k + n_shared <= 16, n_group <= 64.  Replaces select_experts
  * (moe_router_op.py:108-124, patch_fused_moe.py:597-632). */
 int lmoe_router_topk(const void* logits, int logits_f32, int T, int E, int k,
-                     int n_shared, int scoring, const float* bias, int n_group,
+                     int n_shared, int scoring, const float* bias,
+                     const float* logit_bias, int n_group,
                      int topk_group, int renorm, float routed_scale,
                      float* w_f32, uint16_t* w_bf16, int32_t* ids,
                      hipStream_t stream);
@@ -117,6 +121,7 @@ int lmoe_router_topk(const void* logits, int logits_f32, int T, int E, int k,
  * the two calls). */
 int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
                              int k, int n_shared, int scoring, const float* bias,
+                             const float* logit_bias,
                              int n_group, int topk_group, int renorm,
                              float routed_scale, float* w_f32,
                              uint16_t* w_bf16, int32_t* ids,
@@ -128,7 +133,8 @@ int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
                              int32_t* meta, hipStream_t stream);
 
 /* lmoe_router_gate, lmoe_router_topk and lmoe_permute (same arguments, same
- * outputs, bit for bit; logits is still written) in one launch, for the same
+ * outputs, bit for bit; logits is still written, without the logit bias,
+ * as lmoe_router_gate writes it) in one launch, for the same
  * final-table decode case as lmoe_router_topk_permute: gate(hidden)
  * (moe_router_op.py:228-231), select_experts (:108-124) and remap + init
  * routing (slot_mapping.py:116-140, patch_fused_moe.py:668-701).  The gate
@@ -140,7 +146,8 @@ int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
  * H > 8192 or x / wg are not 16-byte aligned (then use the separate calls). */
 int lmoe_router_gate_topk_permute(const void* x, const void* wg, int T, int H,
                                   int E, void* logits, int logits_f32, int k,
-                                  int n_shared, int scoring, const float* bias, int n_group,
+                                  int n_shared, int scoring, const float* bias,
+                                  const float* logit_bias, int n_group,
                                   int topk_group, int renorm,
                                   float routed_scale, float* w_f32,
                                   uint16_t* w_bf16, int32_t* ids,
@@ -248,16 +255,22 @@ int lmoe_down_combine(const void* act, int T, int H, int I, int k,
  * the down GEMV per (row block, slot) into y and the combine (three
  * launches: no workgroup walks the slots in turn).  Both give the same out
  * bit for bit.  Each slot's weights are read once however many tokens chose
- * it.  Needs T*k <= 1024, H % 8 == 0, I % 64 == 0, I <= 4096, H <= 8192;
- * x, slot banks, act and y 16-byte aligned.  Permutation arrays as produced
- * by lmoe_permute. */
+ * it.  distinct_slots != 0 promises that no slot serves two pairs of one
+ * token (true for ids from the routers, which pick distinct experts, through
+ * a slot table, which maps distinct experts to distinct slots); with one
+ * token it selects kernels that take active rank a as sorted position a.
+ * Ids from elsewhere pass 0 (the general kernels; same bits when the
+ * promise holds).  Needs T*k <= 1024, H % 8 == 0, I % 64 == 0, I <= 4096,
+ * H <= 8192; x, slot banks, act and y 16-byte aligned.  Permutation arrays
+ * as produced by lmoe_permute. */
 int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                           const void* w13_slots, const void* w2_slots,
                           int n_slots, const uint16_t* w,
                           const int32_t* offsets, const int32_t* sorted_pairs,
                           const int32_t* row_idx, const int32_t* active,
                           const int32_t* meta, const void* add, void* act,
-                          void* y, void* out, hipStream_t stream);
+                          void* y, void* out, int distinct_slots,
+                          hipStream_t stream);
 
 /* Batched host->device (or device->device) expert copies on a transfer
  * stream: optionally wait on wait_event, then for i < n copy bytes[i] from

@@ -3,7 +3,9 @@
 Restates expert selection as the hot path defines it:
   * gate: logits = x . Wg^T, exact (float64) accumulation rounded to f32
     then bf16 — the gate matmul of ops/fused_moe/moe_router_op.py:228-231;
-  * softmax top-k: f32 softmax over E, k best probabilities, ties to the
+  * logit bias (the gate's linear bias): added to the logits before scoring;
+  * softmax top-k: f32 softmax over E, k best probabilities (plus the
+    correction bias, for the selection only), ties to the
     lower expert id, renorm w / max(sum w, eps) (patch_fused_moe.py:597-632),
     times routed_scaling_factor, cast to bf16 (moe_router_op.py:128-162
     fixes the bf16 weight / int32 id ABI);
@@ -124,20 +126,35 @@ def _finish(sel_w: np.ndarray, renorm: bool, scale: float) -> tuple[np.ndarray, 
     return w, f32_to_bf16(w)
 
 
-def softmax_topk(
-    logits: np.ndarray, k: int, *, renorm: bool = True, scale: float = 1.0, bias: np.ndarray | None = None
-) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
-    """Returns (ids int32 [T,k], w_f32 [T,k], w_bf16 bits [T,k]).  bias is an
-    additive per-expert logit bias applied (one f32 rounding) before softmax."""
+def _with_logit_bias(logits: np.ndarray, logit_bias: np.ndarray | None) -> np.ndarray:
+    """logits + logit_bias in f32 (the router gate's linear bias, one rounding)."""
     lg = np.asarray(logits, dtype=np.float32)
-    if bias is not None:
-        lg = (lg + np.asarray(bias, dtype=np.float32)[None, :]).astype(np.float32)
-    p = softmax_probs(lg)
+    if logit_bias is None:
+        return lg
+    return (lg + np.asarray(logit_bias, dtype=np.float32)[None, :]).astype(np.float32)
+
+
+def softmax_topk(
+    logits: np.ndarray,
+    k: int,
+    *,
+    renorm: bool = True,
+    scale: float = 1.0,
+    bias: np.ndarray | None = None,
+    logit_bias: np.ndarray | None = None,
+) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Returns (ids int32 [T,k], w_f32 [T,k], w_bf16 bits [T,k]).
+
+    logit_bias is added to the logits (one f32 rounding) before the softmax;
+    bias (e_score_correction_bias) is added to the probabilities for the
+    selection only, the weights stay the unbiased probabilities."""
+    p = softmax_probs(_with_logit_bias(logits, logit_bias))
     T, E = p.shape
+    ps = (p + np.asarray(bias, dtype=np.float32)[None, :]).astype(np.float32) if bias is not None else p
     ids = np.empty((T, k), dtype=np.int32)
     sel = np.empty((T, k), dtype=np.float32)
     for t in range(T):
-        o = _order(p[t], np.ones(E, dtype=bool))[:k]
+        o = _order(ps[t], np.ones(E, dtype=bool))[:k]
         ids[t] = o
         sel[t] = p[t, o]
     w, wb = _finish(sel, renorm, scale)
@@ -153,9 +170,10 @@ def grouped_sigmoid_topk(
     topk_group: int,
     renorm: bool = True,
     scale: float = 1.0,
+    logit_bias: np.ndarray | None = None,
 ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """DeepSeek-V3-style selection.  Returns (ids, w_f32, w_bf16 bits)."""
-    lg = np.asarray(logits, dtype=np.float32)
+    lg = _with_logit_bias(logits, logit_bias)
     T, E = lg.shape
     sg = sigmoid(lg)
     sb = (sg + np.asarray(bias, dtype=np.float32)[None, :]).astype(np.float32) if bias is not None else sg

@@ -270,3 +270,50 @@ def test_decode_layer_graph_replays_equal_eager(B):
         assert ws_g.perm.sync.item() == 0 and ws_e.perm.sync.item() == 0
         ref = _oracle_layer(x, g_ids.cpu().numpy(), from_dev_bf16(g_w), w13, w2)
         assert rel_max_err(bf16_to_f32(from_dev_bf16(g_out)), ref) <= OUT_TOL
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_mlp_shared_tuple_with_wide_separate_shared_expert(T):
+    """A Qwen1.5-MoE-shaped layer (H 2048, 60 experts, top-4, routed I 1408)
+    with a separate shared expert of I 5632 (> the decode GEMVs' 4096, so it
+    runs on the MFMA path).  vllm::moe_mlp_shared returns (shared_out,
+    routed_out) apart, the runner adds them (ref moe_mlp_op.py:152-201):
+    routed_out alone matches the routed-only oracle, shared_out the shared
+    expert, and vllm::moe_mlp refuses a layer with a separate shared expert."""
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    from vllm_moe_offload_amd import plugin
+
+    plugin.register()
+    rng = np.random.default_rng(90 + T)
+    E, H, I, Is, k, slots = 60, 2048, 1408, 5632, 4, 16
+    w13, w2, wg = _weights(rng, E, H, I)
+    s13 = normal_bf16(rng, (2 * Is, H), 0.02)
+    s2 = normal_bf16(rng, (H, Is), 0.02)
+    tb = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True))
+    name = f"model.layers.{40 + T}.mlp.experts"
+    layer = SlotMoELayer(layer_id=40 + T, runtime=rt, gate_weight=to_dev_bf16(wg), w13_weight=tb(w13),
+                         w2_weight=tb(w2), top_k=k, shared_w13=tb(s13).cuda(), shared_w2=tb(s2).cuda(),
+                         layer_name=name)
+    layer.register()
+    assert layer.has_separate_shared_expert and not layer.mix_placement
+    print(f"case moe_mlp_shared T={T} shared I={Is}", flush=True)
+    x = normal_bf16(rng, (T, H), 1.0)
+    dx = to_dev_bf16(x)
+    logits = torch.empty((T, E), dtype=torch.bfloat16, device="cuda")
+    w, ids, _ = fused_moe.route(dx, layer.gate_weight, layer.router_spec, logits_out=logits)
+    layer.stage(ids)
+    shared_out, routed_out = torch.ops.vllm.moe_mlp_shared(dx, logits, w, ids, None, None, name)
+    torch.cuda.synchronize()
+    ids_np, wb = ids.cpu().numpy(), from_dev_bf16(w)
+    routed_ref = _oracle_layer(x, ids_np, wb, w13, w2)
+    err_r = rel_max_err(bf16_to_f32(from_dev_bf16(routed_out)), routed_ref)
+    shared_ref = omlp.moe_layer(x, np.zeros((T, 1), np.int32), np.full((T, 1), 0x3F80, np.uint16), None,
+                                s13[None], s2[None])
+    err_s = rel_max_err(bf16_to_f32(from_dev_bf16(shared_out)), shared_ref)
+    total = bf16_to_f32(from_dev_bf16(routed_out)) + bf16_to_f32(from_dev_bf16(shared_out))
+    err_t = rel_max_err(total, _oracle_layer(x, ids_np, wb, w13, w2, shared=(s13, s2)))
+    print(f"  routed {err_r:.3e} shared {err_s:.3e} sum {err_t:.3e}", flush=True)
+    assert err_r <= OUT_TOL and err_s <= OUT_TOL and err_t <= OUT_TOL
+    with pytest.raises(RuntimeError, match="moe_mlp_shared"):
+        torch.ops.vllm.moe_mlp(dx, logits, w, ids, None, None, name)

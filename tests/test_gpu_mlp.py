@@ -175,10 +175,12 @@ def test_combine_masks_unplaced_pairs_and_adds_shared():
     assert rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref) <= 1e-2
 
 
-def _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None, with_y=False):
+def _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None, with_y=False, distinct=False):
     """with_y: the three-launch body (down per row block and slot into y,
     then the combine) that more than 16 pairs take when given the y
-    workspace (up to 16 pairs run the fused body either way)."""
+    workspace (up to 16 pairs run the fused body either way).  distinct:
+    the caller's promise of one pair per slot per token (the one-token
+    kernels)."""
     T, H = d_x.shape
     k = d_ids.shape[1]
     P, I = d_w13.shape[0], d_w13.shape[1] // 2
@@ -187,8 +189,25 @@ def _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, *, add=None, with_y=Fals
     act = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
     out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
     y = torch.empty((T * k, H), dtype=torch.bfloat16, device="cuda") if with_y else None
-    native.fused_moe_decode(d_x, d_w, d_w13, d_w2, perm, act, out, add=add, y=y)
+    native.fused_moe_decode(d_x, d_w, d_w13, d_w2, perm, act, out, add=add, y=y, distinct_slots=distinct)
     return out, perm.meta
+
+
+def _gemv_halves(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p):
+    """The decode layer as its separate GEMV halves: gate_up + SiLU*mul, the
+    down GEMV per (row block, slot) into y, then the combine."""
+    T, H = d_x.shape
+    k = d_ids.shape[1]
+    P, I = d_w13.shape[0], d_w13.shape[1] // 2
+    perm = native.Permutation.allocate(T * k, P, "cuda")
+    native.permute(d_ids, perm, log2phy=d_l2p)
+    act = torch.empty((T * k, I), dtype=torch.bfloat16, device="cuda")
+    y = torch.zeros((T * k, H), dtype=torch.bfloat16, device="cuda")
+    native.gateup_silu(d_x, k, d_w13, perm, act, path=native.LMOE_PATH_GEMV)
+    native.down(act, d_w2, perm, y, path=native.LMOE_PATH_GEMV)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    native.combine(y, d_w, out, row_mask=perm.row_idx)
+    return out
 
 
 @pytest.mark.parametrize("T,k,E,P,H,I", [
@@ -207,10 +226,14 @@ def test_fused_decode_more_shapes(T, k, E, P, H, I):
     d_ids, d_l2p, d_x, d_w13, d_w2, d_w = _dev(ids, l2p, x, w13, w2, wb)
     out, meta = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
     out2, _ = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, with_y=True)
+    out3 = _gemv_halves(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
     torch.cuda.synchronize()
     assert meta[native.META_ACTIVE].item() == np.unique(ids).size
     # the fused down+combine body and the y + combine body agree bit for bit
+    # (up to 16 pairs both calls take the fused body, so the separate GEMV
+    # halves pin the y body at every shape)
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(out.view(torch.int16), out3.view(torch.int16))
     ref = omlp.moe_layer(x, ids, wb, l2p, w13, w2)
     err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
     print(f"  rel max err {err:.3e}", flush=True)
@@ -240,6 +263,51 @@ def test_batched_tokens_equal_one_token_at_a_time(T, k, E, H, I):
                        d_ids[t:t + 1].contiguous(), d_w13, d_w2, d_l2p)
         torch.cuda.synchronize()
         assert torch.equal(o1.view(torch.int16)[0], out.view(torch.int16)[t]), t
+    ref = omlp.moe_layer(x, ids, wb, l2p, w13, w2)
+    err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
+    print(f"  rel max err {err:.3e}", flush=True)
+    assert err <= OUT_TOL
+
+
+@pytest.mark.parametrize("k,E,P,H,I", [
+    (8, 128, 64, 2048, 768),     # the Qwen3-shaped decode layer
+    (9, 257, 16, 7168, 2048),    # DeepSeek-V3 expert shape, nine pairs
+    (4, 40, 24, 1024, 192),
+])
+def test_one_token_distinct_slot_kernels_equal_general_kernels(k, E, P, H, I):
+    """The one-token kernels (active rank = sorted position) give the same
+    bits as the general kernels when each slot serves one pair."""
+    native = _native()
+    print(f"case one-token distinct k={k} E={E} P={P} H={H} I={I}", flush=True)
+    ids, l2p, x, w13, w2, wb = _case(5000 + H + k, 1, k, E, P, H, I)
+    d_ids, d_l2p, d_x, d_w13, d_w2, d_w = _dev(ids, l2p, x, w13, w2, wb)
+    a, _ = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, distinct=True)
+    b, _ = _fused(native, d_x, d_w, d_ids, d_w13, d_w2, d_l2p, distinct=False)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    err = rel_max_err(bf16_to_f32(from_dev_bf16(a)), omlp.moe_layer(x, ids, wb, l2p, w13, w2))
+    assert err <= OUT_TOL
+
+
+@pytest.mark.parametrize("dup_kind", ["same_id", "same_slot"])
+def test_one_token_duplicate_pairs_match_oracle(dup_kind):
+    """A caller's ids may name one expert twice (or map two ids to one
+    slot): fused_experts takes the general kernels and matches the oracle."""
+    from vllm_moe_offload_amd import fused_moe
+
+    native = _native()
+    print(f"case one-token duplicate {dup_kind}", flush=True)
+    T, k, E, P, H, I = 1, 8, 64, 32, 2048, 768
+    ids, l2p, x, w13, w2, wb = _case(777, T, k, E, P, H, I)
+    ids = ids.copy()
+    l2p = l2p.copy()
+    if dup_kind == "same_id":
+        ids[0, 5] = ids[0, 1]
+    else:
+        l2p[ids[0, 6]] = l2p[ids[0, 2]]
+    d_ids, d_l2p, d_x, d_w13, d_w2, d_w = _dev(ids, l2p, x, w13, w2, wb)
+    out = fused_moe.fused_experts(d_x, d_w, d_ids, d_w13, d_w2, d_l2p)
+    torch.cuda.synchronize()
     ref = omlp.moe_layer(x, ids, wb, l2p, w13, w2)
     err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
     print(f"  rel max err {err:.3e}", flush=True)

@@ -53,8 +53,9 @@ def test_softmax_select_and_permute_bit_exact(T, E, k, P, skip):
     print(f"case topk-permute softmax T={T} E={E} k={k} P={P} skip={skip}", flush=True)
     rng = np.random.default_rng(500 + T * 13 + P)
     bits = _tied_logits(rng, T, E)
-    bias = (rng.standard_normal(E) * 0.7).astype(np.float32)
-    r_ids, r_w, r_wb = orc.softmax_topk(bf16_to_f32(bits), k, bias=bias)
+    lbias = (rng.standard_normal(E) * 0.7).astype(np.float32)
+    cbias = (rng.standard_normal(E) * 0.004).astype(np.float32)
+    r_ids, r_w, r_wb = orc.softmax_topk(bf16_to_f32(bits), k, bias=cbias, logit_bias=lbias)
     # slot table: every selected expert mapped (skip: only a subset)
     used = np.unique(r_ids)
     l2p = np.full(E, -1, dtype=np.int32)
@@ -64,7 +65,7 @@ def test_softmax_select_and_permute_bit_exact(T, E, k, P, skip):
     w_f32 = torch.empty((T, k), dtype=torch.float32, device="cuda")
     w, ids, _ = native.router_topk_permute(
         to_dev_bf16(bits), k, perm, log2phy=to_dev_i32(l2p), skip_unmapped=skip,
-        bias=torch.from_numpy(bias).cuda(), w_f32=w_f32,
+        bias=torch.from_numpy(cbias).cuda(), logit_bias=torch.from_numpy(lbias).cuda(), w_f32=w_f32,
     )
     torch.cuda.synchronize()
     np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
@@ -129,8 +130,9 @@ def test_decode_layer_equals_route_then_fused_experts(T):
     rng = np.random.default_rng(40 + T)
     x = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
     gate = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
-    bias = torch.from_numpy((rng.standard_normal(E) * 0.5).astype(np.float32)).cuda()
-    spec = RouterSpec(top_k=k, e_score_correction_bias=bias)
+    lbias = torch.from_numpy((rng.standard_normal(E) * 0.5).astype(np.float32)).cuda()
+    cbias = torch.from_numpy((rng.standard_normal(E) * 0.004).astype(np.float32)).cuda()
+    spec = RouterSpec(top_k=k, e_score_correction_bias=cbias, logit_bias=lbias)
     w13 = to_dev_bf16(normal_bf16(rng, (P, 2 * I, H), 0.02))
     w2 = to_dev_bf16(normal_bf16(rng, (P, H, I), 0.02))
     # the table: route once to learn the experts, map them to slots
@@ -172,7 +174,9 @@ def test_gate_select_permute_one_launch_equals_separate_calls(T, E, k, P, H, sco
     grouped = scoring == "sigmoid"
     kw = dict(scoring=scoring, num_expert_group=8 if grouped else 1, topk_group=4 if grouped else 1,
               routed_scaling_factor=2.5 if grouped else 1.0)
-    bias = torch.from_numpy((rng.standard_normal(E) * (0.01 if grouped else 0.5)).astype(np.float32)).cuda()
+    bias = torch.from_numpy((rng.standard_normal(E) * 0.01).astype(np.float32)).cuda()
+    if not grouped:  # softmax: a gate bias as well as the correction bias
+        kw["logit_bias"] = torch.from_numpy((rng.standard_normal(E) * 0.5).astype(np.float32)).cuda()
     dt = torch.float32 if f32 else torch.bfloat16
     wg = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
     perm_a = native.Permutation.allocate(T * k, P, "cuda")
@@ -223,7 +227,7 @@ def test_shared_suffix_in_all_three_routers(T, E, k, S, scoring, H):
     grouped = scoring == "sigmoid"
     G, TG, scale = (8, 4, 2.5) if grouped else (1, 1, 1.0)
     kw = dict(scoring=scoring, num_expert_group=G, topk_group=TG, routed_scaling_factor=scale, n_shared=S)
-    bias_np = (rng.standard_normal(E) * (0.01 if grouped else 0.5)).astype(np.float32)
+    bias_np = (rng.standard_normal(E) * 0.01).astype(np.float32)
     bias = torch.from_numpy(bias_np).cuda()
     x = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
     wg = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))

@@ -64,12 +64,38 @@ def test_softmax_with_logit_bias_bit_exact():
     bits = _tied_logits(rng, T, E)
     bias = (rng.standard_normal(E) * 0.7).astype(np.float32)
     w_f32 = torch.empty((T, k), dtype=torch.float32, device="cuda")
-    w, ids, _ = native.router_topk(to_dev_bf16(bits), k, bias=torch.from_numpy(bias).cuda(), w_f32=w_f32)
+    w, ids, _ = native.router_topk(to_dev_bf16(bits), k, logit_bias=torch.from_numpy(bias).cuda(), w_f32=w_f32)
     torch.cuda.synchronize()
-    r_ids, r_w, r_wb = orc.softmax_topk(bf16_to_f32(bits), k, bias=bias)
+    r_ids, r_w, r_wb = orc.softmax_topk(bf16_to_f32(bits), k, logit_bias=bias)
     np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
     np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
     np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
+
+
+@pytest.mark.parametrize("E", [64, 128, 256])
+def test_softmax_with_correction_bias_selects_only(E):
+    """e_score_correction_bias with softmax scoring: selection by p + bias,
+    weights the unbiased probabilities (renormalised), bit for bit."""
+    native = _native()
+    print(f"case softmax correction bias E={E}", flush=True)
+    rng = np.random.default_rng(22 + E)
+    T, k = 48, 8
+    bits = _tied_logits(rng, T, E)
+    cb = (rng.standard_normal(E) * 0.01).astype(np.float32)
+    lb = (rng.standard_normal(E) * 0.5).astype(np.float32)
+    for logit_bias in (None, lb):
+        w_f32 = torch.empty((T, k), dtype=torch.float32, device="cuda")
+        w, ids, _ = native.router_topk(
+            to_dev_bf16(bits), k, bias=torch.from_numpy(cb).cuda(),
+            logit_bias=None if logit_bias is None else torch.from_numpy(logit_bias).cuda(), w_f32=w_f32)
+        torch.cuda.synchronize()
+        r_ids, r_w, r_wb = orc.softmax_topk(bf16_to_f32(bits), k, bias=cb, logit_bias=logit_bias)
+        np.testing.assert_array_equal(ids.cpu().numpy(), r_ids)
+        np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
+        np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
+    # the bias changed the choice somewhere (else the test pins nothing)
+    plain, _, _ = orc.softmax_topk(bf16_to_f32(bits), k)
+    assert not np.array_equal(plain, orc.softmax_topk(bf16_to_f32(bits), k, bias=cb)[0])
 
 
 def test_softmax_ties_break_to_lower_id():

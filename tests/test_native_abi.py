@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = native.load_library()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.lmoe_abi_version() == 3
+    assert lib.lmoe_abi_version() == 4
     assert lib.lmoe_status_string(1001) == b"unsupported shape"
 
 
@@ -37,13 +37,13 @@ def test_argument_errors_are_reported_without_a_gpu():
 
     lib = native.load_library()
     # null outputs / bad sizes are rejected on the host
-    assert lib.lmoe_router_topk(None, 0, 1, 128, 8, 0, 0, None, 1, 1, 1, 1.0, None, None, None, None) == 1000
-    assert lib.lmoe_router_topk(ctypes.c_void_p(16), 0, 1, 1024, 8, 0, 0, None, 1, 1, 1, 1.0, None,
+    assert lib.lmoe_router_topk(None, 0, 1, 128, 8, 0, 0, None, None, 1, 1, 1, 1.0, None, None, None, None) == 1000
+    assert lib.lmoe_router_topk(ctypes.c_void_p(16), 0, 1, 1024, 8, 0, 0, None, None, 1, 1, 1, 1.0, None,
                                 ctypes.c_void_p(16), ctypes.c_void_p(16), None) == 1001
     # shared suffix: a negative count is an argument error, k + n_shared > 16 a shape error
     p16 = ctypes.c_void_p(16)
-    assert lib.lmoe_router_topk(p16, 0, 1, 128, 8, -1, 0, None, 1, 1, 1, 1.0, None, p16, p16, None) == 1000
-    assert lib.lmoe_router_topk(p16, 0, 1, 128, 8, 9, 0, None, 1, 1, 1, 1.0, None, p16, p16, None) == 1001
+    assert lib.lmoe_router_topk(p16, 0, 1, 128, 8, -1, 0, None, None, 1, 1, 1, 1.0, None, p16, p16, None) == 1000
+    assert lib.lmoe_router_topk(p16, 0, 1, 128, 8, 9, 0, None, None, 1, 1, 1, 1.0, None, p16, p16, None) == 1001
     assert lib.lmoe_permute(None, 4, None, 0, 0, 0, 128, *([None] * 7), None, 0, None) == 1000
     assert lib.lmoe_grouped_mlp(*([ctypes.c_void_p(16)] * 1), 1, 2048, 100, 8, *([ctypes.c_void_p(16)] * 2), 4,
                                 *([ctypes.c_void_p(16)] * 5), 8, 128, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None) == 1001
@@ -58,6 +58,31 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert lib.lmoe_table_update(tbl, 8, i3(-1, 3, 2), i3(0, 1, 2), 3, None) == 1000
     assert lib.lmoe_table_update(None, 8, i3(1, 3, 2), i3(0, 1, 2), 3, None) == 1000
     assert lib.lmoe_table_update(None, 8, None, None, 0, None) == 0
+
+
+def test_block_range_gemm_refuses_operands_past_32_bit_offsets():
+    """The 320-row block-range prefill kernel forms activation offsets in 32
+    bits; an activation operand of 2^31 elements or more is refused on the
+    host (LMOE_ERR_SHAPE) before any launch, and prefill_block_m then picks
+    the 256-row kernel, whose offsets are 64-bit."""
+    import torch
+
+    from vllm_moe_offload_amd import native
+
+    if torch.cuda.is_available():
+        pytest.skip("host-only check: the pointers below are placeholders")
+    lib = native.load_library()
+    p = ctypes.c_void_p(4096)
+    H, I, k = 2048, 768, 8
+    # down: n_pairs * I = 2.3e9 elements of act
+    n = 3_000_000
+    assert lib.lmoe_down(p, H, I, p, 64, p, p, p, p, p, n, 320, native.LMOE_PATH_MFMA, p, None) == 1001
+    # gate-up: T * H = 2.25e9 elements of x
+    T = 1_100_000
+    assert lib.lmoe_gateup_silu(p, T, H, I, k, p, 64, p, p, p, p, p, T * k, 320, native.LMOE_PATH_MFMA,
+                                p, None) == 1001
+    assert native.prefill_block_m(128, H, I, cu_count=256, n_pairs=n) == native.MFMA_BLOCK_M
+    assert native.prefill_block_m(128, H, I, cu_count=256, n_pairs=32768) == native.PART_BLOCK_M
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

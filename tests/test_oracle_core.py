@@ -88,6 +88,33 @@ def test_softmax_topk_selection_brute_force_with_ties():
         np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
 
 
+def test_softmax_correction_bias_selects_only_and_logit_bias_shifts_logits():
+    """The correction bias moves the choice, never the weights; the logit bias
+    is the same as adding it to the logits first."""
+    rng = np.random.default_rng(31)
+    for _ in range(200):
+        E = int(rng.integers(4, 20))
+        k = int(rng.integers(1, E + 1))
+        lg = (rng.integers(-3, 4, size=(1, E)) * 0.5).astype(np.float32)
+        bias = (rng.integers(-2, 3, size=E) * 0.125).astype(np.float32)
+        ids, w, _ = orouter.softmax_topk(lg, k, bias=bias, renorm=False)
+        p = orouter.softmax_probs(lg)[0]
+        sel = (p + bias).astype(np.float32)
+        want = _brute_topk(sel.tolist(), k)
+        assert ids[0].tolist() == want
+        np.testing.assert_array_equal(w[0], p[want])  # unbiased probabilities
+        ids2, w2, _ = orouter.softmax_topk(lg, k, logit_bias=bias)
+        ids3, w3, _ = orouter.softmax_topk((lg + bias).astype(np.float32), k)
+        np.testing.assert_array_equal(ids2, ids3)
+        np.testing.assert_array_equal(w2, w3)
+    # a large bias on one expert selects it although its probability is low
+    lg = np.array([[2.0, 1.0, 0.0, -1.0]], np.float32)
+    ids, w, _ = orouter.softmax_topk(lg, 2, bias=np.array([0, 0, 0, 5.0], np.float32), renorm=False)
+    p = orouter.softmax_probs(lg)[0]
+    assert ids[0].tolist() == [3, 0]
+    assert w[0].tolist() == [p[3], p[0]]
+
+
 def test_renorm_golden_vector_of_reference():
     """weights [1, 3] -> [0.25, 0.75] (reference tests/test_patch_fused_moe.py:560)."""
     w, wb = orouter._finish(np.array([[1.0, 3.0]], np.float32), True, 1.0)

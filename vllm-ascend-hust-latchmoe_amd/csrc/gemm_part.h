@@ -119,8 +119,9 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_part_kernel(GemmArgs 
     }
 
     // per-lane source rows of this wave's load instructions (see gemm_lds.h),
-    // as 32-bit element offsets from the operand bases (the host checks that
-    // every operand spans fewer than 2^31 elements)
+    // as 32-bit element offsets from the operand bases: the launch refuses
+    // (LMOE_ERR_SHAPE) an activation operand whose rows reach 2^31 elements
+    // (part_offsets_fit), and a weight offset stays inside one slot
     int a_src[C::QA];
     int b_src[C::QB];
 #pragma unroll

@@ -552,6 +552,19 @@ static int part_grid() {
   return grid;
 }
 
+// The block-range kernel forms operand offsets in 32 bits: activation row r
+// starts at r * K, the rows read are token rows (gate-up: sorted pair / topk
+// < ceil(n_pairs / topk)) or sorted positions (down: < n_pairs), and a
+// weight row lies inside one slot of w_slot_stride elements.  All of them
+// must end below 2^31.
+template <int MODE>
+static bool part_offsets_fit(const GemmArgs& g, int n_pairs) {
+  const long long a_rows =
+      MODE == kGateUp ? (static_cast<long long>(n_pairs) + g.topk - 1) / g.topk : n_pairs;
+  const long long lim = 0x7fffffffLL;
+  return a_rows * g.K <= lim && g.w_slot_stride <= lim;
+}
+
 template <int MODE>
 static int launch_grouped_mfma(GemmArgs g, int n_pairs, int max_active, int block_m,
                                hipStream_t stream) {
@@ -564,6 +577,7 @@ static int launch_grouped_mfma(GemmArgs g, int n_pairs, int max_active, int bloc
   if (!aligned) return LMOE_ERR_SHAPE;
   if (block_m == PartTile::BM) {
     if (g.K % PartTile::BK != 0 || g.N % 8 != 0) return LMOE_ERR_SHAPE;
+    if (!part_offsets_fit<MODE>(g, n_pairs)) return LMOE_ERR_SHAPE;  // take block_m 256
     hipLaunchKernelGGL((grouped_gemm_part_kernel<MODE, PartTile>), dim3(part_grid()),
                        dim3(PartTile::THREADS), 0, stream, g);
     return LMOE_OK;
@@ -614,9 +628,11 @@ extern "C" int lmoe_gateup_silu(const void* x, int T, int H, int I, int k,
   path = resolve_path(path, n_pairs);
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
   if (path == LMOE_PATH_GEMV) {
+    // general form: a caller's permutation may give one slot several pairs
+    // of the one token
     st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
                             static_cast<const uint16_t*>(w13_slots), offsets, sorted_pairs,
-                            active, meta, max_active, T == 1, static_cast<uint16_t*>(act),
+                            active, meta, max_active, false, static_cast<uint16_t*>(act),
                             stream);
     if (st != LMOE_OK) return st;
     LMOE_RETURN_LAUNCH();
@@ -701,11 +717,13 @@ extern "C" int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
                    n_pairs, block_m, path, y, stream);
 }
 
-extern "C" int lmoe_down_combine(const void* act, int T, int H, int I, int k,
-                                 const void* w2_slots, int n_slots, const uint16_t* w,
-                                 const int32_t* offsets, const int32_t* row_idx,
-                                 const int32_t* active, const int32_t* meta,
-                                 const void* add, void* out, hipStream_t stream) {
+// one: a single token whose pairs sit in distinct slots (active rank a is
+// sorted position a), the precondition of the ONE kernels.
+static int down_combine_impl(const void* act, int T, int H, int I, int k,
+                             const void* w2_slots, int n_slots, const uint16_t* w,
+                             const int32_t* offsets, const int32_t* row_idx,
+                             const int32_t* active, const int32_t* meta,
+                             const void* add, void* out, bool one, hipStream_t stream) {
   if (act == nullptr || w2_slots == nullptr || w == nullptr || offsets == nullptr ||
       row_idx == nullptr || active == nullptr || meta == nullptr || out == nullptr)
     return LMOE_ERR_ARG;
@@ -723,12 +741,12 @@ extern "C" int lmoe_down_combine(const void* act, int T, int H, int I, int k,
     const uint16_t* w2_ = static_cast<const uint16_t*>(w2_slots);                              \
     const uint16_t* add_ = static_cast<const uint16_t*>(add);                                  \
     uint16_t* out_ = static_cast<uint16_t*>(out);                                              \
-    if (T == 1 && k <= 8)                                                                      \
+    if (one && k <= 8)                                                                         \
       /* one slot per half wave (ranks < k <= 8): no next-slot prefetch */                     \
       hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, false, true>), grid, dim3(256), 0,   \
                          stream, a_, I, H, T, k, w2_, offsets, active, n_slots, row_idx, w,     \
                          add_, out_);                                                          \
-    else if (T == 1)                                                                           \
+    else if (one)                                                                              \
       hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, PF, true>), grid, dim3(256), 0,      \
                          stream, a_, I, H, T, k, w2_, offsets, active, n_slots, row_idx, w,     \
                          add_, out_);                                                          \
@@ -750,6 +768,15 @@ extern "C" int lmoe_down_combine(const void* act, int T, int H, int I, int k,
   LMOE_RETURN_LAUNCH();
 }
 
+extern "C" int lmoe_down_combine(const void* act, int T, int H, int I, int k,
+                                 const void* w2_slots, int n_slots, const uint16_t* w,
+                                 const int32_t* offsets, const int32_t* row_idx,
+                                 const int32_t* active, const int32_t* meta,
+                                 const void* add, void* out, hipStream_t stream) {
+  return down_combine_impl(act, T, H, I, k, w2_slots, n_slots, w, offsets, row_idx, active, meta,
+                           add, out, false, stream);
+}
+
 extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                                      const void* w13_slots, const void* w2_slots,
                                      int n_slots, const uint16_t* w,
@@ -758,7 +785,7 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                                      const int32_t* row_idx,
                                      const int32_t* active, const int32_t* meta,
                                      const void* add, void* act, void* y, void* out,
-                                     hipStream_t stream) {
+                                     int distinct_slots, hipStream_t stream) {
   if (x == nullptr || w13_slots == nullptr || w2_slots == nullptr || w == nullptr ||
       offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
       active == nullptr || meta == nullptr || act == nullptr || out == nullptr)
@@ -773,9 +800,10 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
     return LMOE_ERR_SHAPE;
   if (T == 0) return LMOE_OK;
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
+  const bool one = T == 1 && distinct_slots != 0;
   int st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
                               static_cast<const uint16_t*>(w13_slots), offsets,
-                              sorted_pairs, active, meta, max_active, T == 1,
+                              sorted_pairs, active, meta, max_active, one,
                               static_cast<uint16_t*>(act), stream);
   if (st != LMOE_OK) return st;
   if (y != nullptr && T > 1 && n_pairs > 16) {
@@ -792,8 +820,8 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                    static_cast<const uint16_t*>(add), static_cast<uint16_t*>(out), stream);
     LMOE_RETURN_LAUNCH();
   }
-  return lmoe_down_combine(act, T, H, I, k, w2_slots, n_slots, w, offsets, row_idx, active, meta,
-                           add, out, stream);
+  return down_combine_impl(act, T, H, I, k, w2_slots, n_slots, w, offsets, row_idx, active, meta,
+                           add, out, one, stream);
 }
 
 extern "C" int lmoe_combine(const void* y, const int32_t* row_idx,

@@ -122,12 +122,12 @@ __device__ __forceinline__ void select_and_permute(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   if (wave < T) {
-    float bv[EPL], lg[EPL];
-    load_bias<EPL>(sp, bv);
+    float bv[EPL], lb[EPL], lg[EPL];
+    load_bias<EPL>(sp, bv, lb);
     load_logits<EPL>(logits, logits_f32, wave, sp.E, lg);
     int e;
     float w;
-    select_token<EPL, SCORE>(sp, lg, bv, L.sel[wave], e, w);
+    select_token<EPL, SCORE>(sp, lg, bv, lb, L.sel[wave], e, w);
     const int kw = sp.k + sp.n_shared;
     if (lane >= sp.k) {
       // the pinned shared-expert suffix: ids E, E + 1, ..., weight 1
@@ -239,14 +239,15 @@ inline int check_select(int T, int E, int k, int n_shared, int scoring, int n_gr
 }
 
 inline SelectParams make_select(int E, int k, int n_shared, int scoring, const float* bias,
-                                int n_group, int topk_group, int renorm,
-                                float routed_scale) {
+                                const float* logit_bias, int n_group, int topk_group,
+                                int renorm, float routed_scale) {
   SelectParams sp;
   sp.E = E;
   sp.k = k;
   sp.n_shared = n_shared;
   sp.scoring = scoring;
   sp.bias = bias;
+  sp.logit_bias = logit_bias;
   sp.n_group = scoring == LMOE_SCORING_SIGMOID ? (n_group > 1 ? n_group : 1) : 1;
   sp.topk_group = topk_group;
   sp.renorm = renorm;

@@ -33,12 +33,12 @@ __global__ __launch_bounds__(256) void topk_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
-  float bv[EPL], lg[EPL];
-  load_bias<EPL>(sp, bv);
+  float bv[EPL], lb[EPL], lg[EPL];
+  load_bias<EPL>(sp, bv, lb);
   load_logits<EPL>(logits, logits_f32, t < T ? t : 0, sp.E, lg);
   int e;
   float w;
-  select_token<EPL, SCORE>(sp, lg, bv, lds[wave], e, w);
+  select_token<EPL, SCORE>(sp, lg, bv, lb, lds[wave], e, w);
   const int kw = sp.k + sp.n_shared;
   if (lane >= sp.k) {
     // the pinned shared-expert suffix: ids E, E + 1, ..., weight 1
@@ -98,7 +98,7 @@ extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
 
 extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
                                 int E, int k, int n_shared, int scoring, const float* bias,
-                                int n_group, int topk_group, int renorm,
+                                const float* logit_bias, int n_group, int topk_group, int renorm,
                                 float routed_scale, float* w_f32,
                                 uint16_t* w_bf16, int32_t* ids,
                                 hipStream_t stream) {
@@ -108,7 +108,8 @@ extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
   if (st != LMOE_OK) return st;
   if (T == 0) return LMOE_OK;
   const SelectParams sp =
-      make_select(E, k, n_shared, scoring, bias, n_group, topk_group, renorm, routed_scale);
+      make_select(E, k, n_shared, scoring, bias, logit_bias, n_group, topk_group, renorm,
+                  routed_scale);
   const dim3 grid((T + 3) / 4);
 #define LMOE_TK(EPL, S) \
   hipLaunchKernelGGL((topk_kernel<EPL, S>), grid, dim3(256), 0, stream, logits, logits_f32, T, sp, w_f32, w_bf16, ids)
@@ -128,7 +129,8 @@ extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
 
 extern "C" int lmoe_router_topk_permute(
     const void* logits, int logits_f32, int T, int E, int k, int n_shared, int scoring,
-    const float* bias, int n_group, int topk_group, int renorm, float routed_scale, float* w_f32, uint16_t* w_bf16,
+    const float* bias, const float* logit_bias, int n_group, int topk_group, int renorm,
+    float routed_scale, float* w_f32, uint16_t* w_bf16,
     int32_t* ids, const int32_t* log2phy, int n_log2phy, int n_slots, int skip_unmapped,
     int block_m, int32_t* counts, int32_t* offsets, int32_t* sorted_pairs, int32_t* row_idx,
     int32_t* active, int32_t* tile_off, int32_t* meta, hipStream_t stream) {
@@ -147,7 +149,8 @@ extern "C" int lmoe_router_topk_permute(
   ra.T = T;
   ra.logits = const_cast<void*>(logits);
   ra.logits_f32 = logits_f32;
-  ra.sp = make_select(E, k, n_shared, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  ra.sp = make_select(E, k, n_shared, scoring, bias, logit_bias, n_group, topk_group, renorm,
+                      routed_scale);
   ra.w_f32 = w_f32;
   ra.w_bf16 = w_bf16;
   ra.ids = ids;
@@ -169,7 +172,8 @@ extern "C" int lmoe_router_topk_permute(
 
 extern "C" int lmoe_router_gate_topk_permute(
     const void* x, const void* wg, int T, int H, int E, void* logits, int logits_f32, int k,
-    int n_shared, int scoring, const float* bias, int n_group, int topk_group, int renorm, float routed_scale,
+    int n_shared, int scoring, const float* bias, const float* logit_bias, int n_group,
+    int topk_group, int renorm, float routed_scale,
     float* w_f32, uint16_t* w_bf16, int32_t* ids, const int32_t* log2phy, int n_log2phy,
     int n_slots, int skip_unmapped, int block_m, int32_t* counts, int32_t* offsets,
     int32_t* sorted_pairs, int32_t* row_idx, int32_t* active, int32_t* tile_off, int32_t* meta,
@@ -197,7 +201,8 @@ extern "C" int lmoe_router_gate_topk_permute(
   ra.T = T;
   ra.logits = logits;
   ra.logits_f32 = logits_f32;
-  ra.sp = make_select(E, k, n_shared, scoring, bias, n_group, topk_group, renorm, routed_scale);
+  ra.sp = make_select(E, k, n_shared, scoring, bias, logit_bias, n_group, topk_group, renorm,
+                      routed_scale);
   ra.w_f32 = w_f32;
   ra.w_bf16 = w_bf16;
   ra.ids = ids;

@@ -1,5 +1,9 @@
 // Expert selection for one token per wave64: softmax top-k, or sigmoid +
-// correction bias + group-limited top-k, with renormalisation and scaling.
+// group-limited top-k, with renormalisation and scaling.  Two optional
+// per-expert f32 biases: a logit bias added to the logits before scoring
+// (the router gate's linear bias), and the correction bias
+// (e_score_correction_bias), added to the scores for selection only: the
+// weights are the unbiased scores, for softmax and sigmoid alike.
 //
 // Selection order is (score desc, expert id asc), the order torch.topk gives
 // with ties to the lower id.  Each score becomes an order-preserving 32-bit
@@ -30,7 +34,8 @@ struct SelectParams {
   int k;
   int n_shared;  // shared-expert suffix appended to every token (ids E.., weight 1)
   int scoring;
-  const float* bias;
+  const float* bias;        // correction bias: selection only
+  const float* logit_bias;  // added to the logits before scoring
   int n_group;
   int topk_group;
   int renorm;
@@ -57,31 +62,32 @@ __device__ __forceinline__ bool better(float v, int e, float v2, int e2) {
 }
 
 // Selects the k experts of one token from its logits lg[j] (expert j*64 +
-// lane, -inf beyond E; EPL*64 >= E) and the correction bias bv[j]
-// (load_bias; used only when sp.bias is set).  SCORE (LMOE_SCORING_*) is a
+// lane, -inf beyond E; EPL*64 >= E), the correction bias bv[j] and the
+// logit bias lb[j] (load_bias; used only when sp.bias / sp.logit_bias are
+// set).  SCORE (LMOE_SCORING_*) is a
 // template parameter so that a kernel holds only the code of its scoring.
 // Lane l < k returns the l-th selected expert id (-1 if fewer than k are
 // eligible) and its final f32 weight.
 template <int EPL, int SCORE>
 __device__ __forceinline__ void select_token(const SelectParams& sp,
                                              float (&lg)[EPL], const float (&bv)[EPL],
-                                             SelectLds<EPL>& L, int& out_e,
-                                             float& out_w) {
+                                             const float (&lb)[EPL], SelectLds<EPL>& L,
+                                             int& out_e, float& out_w) {
   const int lane = threadIdx.x & 63;
   const int E = sp.E;
   const int k = sp.k;
   float sel[EPL];  // selection score
   float wgt[EPL];  // weight carried by a selected expert
   bool elig[EPL];
-  if constexpr (SCORE == LMOE_SCORING_SOFTMAX) {
-    if (sp.bias != nullptr) {
-      // additive per-expert logit bias (rounded once, before the softmax)
+  if (sp.logit_bias != nullptr) {
+    // additive per-expert logit bias (one f32 rounding, before scoring)
 #pragma unroll
-      for (int j = 0; j < EPL; ++j) {
-        const int e = j * kWave + lane;
-        if (e < E) lg[j] = lg[j] + bv[j];
-      }
+    for (int j = 0; j < EPL; ++j) {
+      const int e = j * kWave + lane;
+      if (e < E) lg[j] = lg[j] + lb[j];
     }
+  }
+  if constexpr (SCORE == LMOE_SCORING_SOFTMAX) {
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) m = fmaxf(m, lg[j]);
@@ -99,7 +105,7 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     for (int j = 0; j < EPL; ++j) {
       const int e = j * kWave + lane;
       const float p = ex[j] / s;
-      sel[j] = p;
+      sel[j] = (e < E && sp.bias != nullptr) ? p + bv[j] : p;
       wgt[j] = p;
       elig[j] = e < E;
     }
@@ -230,15 +236,17 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
   }
 }
 
-// Correction bias in the lane layout (0 where absent).  Issued before the
-// logits so that both loads are in flight together.
+// Correction bias bv and logit bias lb in the lane layout (0 where absent).
+// Issued before the logits so that all loads are in flight together.
 template <int EPL>
-__device__ __forceinline__ void load_bias(const SelectParams& sp, float (&bv)[EPL]) {
+__device__ __forceinline__ void load_bias(const SelectParams& sp, float (&bv)[EPL],
+                                          float (&lb)[EPL]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = j * kWave + lane;
     bv[j] = (sp.bias != nullptr && e < sp.E) ? sp.bias[e] : 0.0f;
+    lb[j] = (sp.logit_bias != nullptr && e < sp.E) ? sp.logit_bias[e] : 0.0f;
   }
 }
 

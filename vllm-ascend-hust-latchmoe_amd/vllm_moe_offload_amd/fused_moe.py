@@ -86,7 +86,10 @@ class RouterSpec:
     num_expert_group: int = 1
     topk_group: int = 1
     routed_scaling_factor: float = 1.0
+    # selection-only bias of the scores (vLLM's e_score_correction_bias)
     e_score_correction_bias: torch.Tensor | None = None
+    # the router gate's linear bias, added to the logits before scoring
+    logit_bias: torch.Tensor | None = None
     # pinned shared experts appended to every token by the router (ids
     # E, E+1, ..., weight 1): select_experts' mix-placement suffix
     # (patch_fused_moe.py:4697-4727)
@@ -110,7 +113,7 @@ def route(hidden: torch.Tensor, gate_weight: torch.Tensor | None, spec: RouterSp
     grouped = bool(spec.use_grouped_topk)
     w, ids, _ = native.router_topk(
         router_logits, int(spec.top_k), scoring=spec.scoring_func,
-        bias=spec.e_score_correction_bias,
+        bias=spec.e_score_correction_bias, logit_bias=spec.logit_bias,
         num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
         topk_group=int(spec.topk_group or 1) if grouped else 1,
         renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
@@ -137,21 +140,26 @@ def fused_experts(
 ) -> torch.Tensor:
     """out[t] = add[t] + sum_j w[t,j] * MLP_{slot(ids[t,j])}(x_t).
 
-    Permute, then: up to 1024 pairs (unless path is MFMA) the decode body
-    (gate_up GEMV, down GEMV fused with the combine); more pairs the grouped
-    GEMM (MFMA unless path is GEMV) and the combine."""
+    Permute, then: up to 1024 pairs (unless path is MFMA) and I <= 4096 the
+    decode body (gate_up GEMV, down GEMV fused with the combine); otherwise
+    the grouped GEMM (MFMA unless path is GEMV; always MFMA past the GEMV's
+    I <= 4096) and the combine.  topk_ids come from the caller, so a token
+    may name one expert twice: the decode body takes its general form,
+    which holds no one-pair-per-slot assumption."""
     T, H = hidden.shape
     k = int(topk_ids.shape[1])
     P = int(w13_slots.shape[0])
     I = int(w13_slots.shape[1]) // 2
     ws = workspace or get_workspace(T, k, P, H, I, hidden.device)
     dst = out if out is not None else ws.out[:T]
+    if I > native.GEMV_MAX_I and path == native.LMOE_PATH_AUTO:
+        path = native.LMOE_PATH_MFMA
     decode = T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA
-    bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P, H, I, hidden.device)
+    bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P, H, I, hidden.device, n_pairs=T * k)
     native.permute(topk_ids, ws.perm, log2phy=log2phy, block_m=bm)
     if decode:
         native.fused_moe_decode(hidden, topk_weights, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add,
-                                y=ws.y[: T * k])
+                                y=ws.y[: T * k], distinct_slots=False)
     else:
         native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
         native.combine(ws.y[: T * k], topk_weights, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
@@ -199,6 +207,7 @@ def decode_layer(
     grouped = bool(spec.use_grouped_topk)
     sel = dict(
         log2phy=log2phy, scoring=spec.scoring_func, bias=spec.e_score_correction_bias,
+        logit_bias=spec.logit_bias,
         num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
         topk_group=int(spec.topk_group or 1) if grouped else 1,
         renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
@@ -210,11 +219,14 @@ def decode_layer(
         logits = native.router_gate(hidden, gate_weight, logits_out)
         w, ids, _ = native.router_topk_permute(logits, k, ws.perm, **sel)
     dst = out if out is not None else ws.out[:T]
-    if T * kw <= native.FUSED_DECODE_MAX_PAIRS:
+    I = int(w13_slots.shape[1]) // 2
+    if T * kw <= native.FUSED_DECODE_MAX_PAIRS and I <= native.GEMV_MAX_I:
+        # router-fed ids: distinct experts per token, in distinct slots
         native.fused_moe_decode(hidden, w, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], dst, add=add,
-                                y=ws.y[: T * kw])
+                                y=ws.y[: T * kw], distinct_slots=True)
     else:
-        native.grouped_mlp(hidden, kw, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], ws.y[: T * kw])
+        path = native.LMOE_PATH_MFMA if I > native.GEMV_MAX_I else native.LMOE_PATH_AUTO
+        native.grouped_mlp(hidden, kw, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], ws.y[: T * kw], path=path)
         native.combine(ws.y[: T * kw], w, dst, row_mask=ws.perm.row_idx[: T * kw], add=add)
     return dst, w, ids
 
@@ -395,7 +407,7 @@ def run_wave_prefill(
             try:
                 native.permute(topk_ids, ws.perm, log2phy=prepared.log2phy, skip_unmapped=True,
                                table_len=total_logical if first else routed,
-                               block_m=native.prefill_block_m(len(plan.waves[w]), H, I, hidden.device))
+                               block_m=native.prefill_block_m(len(plan.waves[w]), H, I, hidden.device, n_pairs=T * k))
                 first = False
                 native.grouped_mlp(hidden, k, prepared.w1, prepared.w2, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
             finally:

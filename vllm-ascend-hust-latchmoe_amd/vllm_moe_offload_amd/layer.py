@@ -53,6 +53,7 @@ class SlotMoELayer(torch.nn.Module):
         topk_group: int = 1,
         routed_scaling_factor: float = 1.0,
         e_score_correction_bias: torch.Tensor | None = None,
+        gate_bias: torch.Tensor | None = None,
         shared_w13: torch.Tensor | None = None,
         shared_w2: torch.Tensor | None = None,
         layer_name: str | None = None,
@@ -72,6 +73,8 @@ class SlotMoELayer(torch.nn.Module):
         self.routed_scaling_factor = float(routed_scaling_factor)
         self.e_score_correction_bias = e_score_correction_bias
         self.gate_weight = gate_weight
+        # the gate's linear bias (f32 [E]), added to the logits before scoring
+        self.gate_bias = gate_bias
         self.num_routed_experts = int(w13_weight.shape[0])
         self.hidden_size = int(w13_weight.shape[2])
         self.intermediate_size = int(w13_weight.shape[1]) // 2
@@ -114,6 +117,7 @@ class SlotMoELayer(torch.nn.Module):
             use_grouped_topk=self.use_grouped_topk, num_expert_group=self.num_expert_group,
             topk_group=self.topk_group, routed_scaling_factor=self.routed_scaling_factor,
             e_score_correction_bias=self.e_score_correction_bias,
+            logit_bias=self.gate_bias,
             n_shared=self.n_shared_experts if self.mix_placement else 0,
         )
 
@@ -138,14 +142,22 @@ class SlotMoELayer(torch.nn.Module):
         ws = get_workspace(T, 1, 1, H, int(self.shared_w13.shape[1]) // 2, x.device, tag=f"shared{self.layer_id}")
         return fused_experts(x, ones, zeros, self.shared_w13, self.shared_w2, None, workspace=ws)
 
-    def forward_experts(self, hidden: torch.Tensor, shared_experts_input: torch.Tensor | None = None) -> torch.Tensor:
-        """Captured piece 2, with the injected router output."""
+    @property
+    def has_separate_shared_expert(self) -> bool:
+        return self.shared_w13 is not None
+
+    def forward_experts(self, hidden: torch.Tensor, shared_experts_input: torch.Tensor | None = None, *,
+                        include_shared: bool = True) -> torch.Tensor:
+        """Captured piece 2, with the injected router output.  A separate
+        shared expert is added to the routed output unless include_shared is
+        False (the tuple ABI of moe_mlp_shared returns the two apart); a
+        pinned-suffix shared expert is one of the routed pairs."""
         injected = moe_seam_inject.peek_injected_topk(self.layer_id)
         if injected is None:
             raise RuntimeError(f"layer {self.layer_id}: forward_experts needs the injected top-k")
         w, ids = injected
         add = None
-        if self.shared_w13 is not None:
+        if include_shared and self.shared_w13 is not None:
             add = self.shared_expert_forward(shared_experts_input if shared_experts_input is not None else hidden)
         rt = self.runtime
         if not _is_current_graph_capturing():

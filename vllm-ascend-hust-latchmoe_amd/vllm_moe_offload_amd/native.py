@@ -30,6 +30,7 @@ META_COUNT = 4
 MFMA_BLOCK_M = 256  # row-tile height of the prefill MFMA GEMM (tile table of lmoe_permute)
 PART_BLOCK_M = 320  # row tiles of the one-workgroup-per-CU prefill GEMM (lmoe_grouped_mlp)
 FUSED_DECODE_MAX_PAIRS = 1024
+GEMV_MAX_I = 4096  # the decode GEMV kernels hold at most 16 chunks of 256 act columns
 
 EXPORTED_SYMBOLS = (
     "lmoe_status_string",
@@ -62,16 +63,16 @@ _SIGNATURES = {
     "lmoe_router_gate": (_i, [_vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "lmoe_router_topk": (
         _i,
-        [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp],
+        [_vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp],
     ),
     "lmoe_router_topk_permute": (
         _i,
-        [_vp, _i, _i, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
+        [_vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
          _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "lmoe_router_gate_topk_permute": (
         _i,
-        [_vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _i, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
+        [_vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
          _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "lmoe_permute_workspace_bytes": (_sz, [_i, _i]),
@@ -93,7 +94,7 @@ _SIGNATURES = {
     "lmoe_fused_moe_decode": (
         _i,
         [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
-         _vp],
+         _i, _vp],
     ),
     "lmoe_down_combine": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "lmoe_stage_copy": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
@@ -164,6 +165,13 @@ def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple | None = 
 # ---------------------------------------------------------------------------
 # router
 # ---------------------------------------------------------------------------
+def _check_biases(bias: torch.Tensor | None, logit_bias: torch.Tensor | None, E: int) -> None:
+    if bias is not None:
+        _need(bias, "e_score_correction_bias", torch.float32, (E,))
+    if logit_bias is not None:
+        _need(logit_bias, "logit_bias", torch.float32, (E,))
+
+
 def router_gate(x: torch.Tensor, wg: torch.Tensor, logits: torch.Tensor, *, stream=None) -> torch.Tensor:
     """logits = x . wg^T with f32 accumulation (bf16 or f32 output)."""
     lib = load_library()
@@ -188,6 +196,7 @@ def router_topk(
     *,
     scoring: str = "softmax",
     bias: torch.Tensor | None = None,
+    logit_bias: torch.Tensor | None = None,
     num_expert_group: int = 1,
     topk_group: int = 1,
     renormalize: bool = True,
@@ -198,9 +207,11 @@ def router_topk(
     w_f32: torch.Tensor | None = None,
     stream=None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
-    """Select top_k experts per token; returns (w_bf16 [T,k+S], ids int32
-    [T,k+S], w_f32) with S = n_shared columns of the pinned shared-expert
-    suffix (ids E, E+1, ..., weight 1) after the routed ones."""
+    """Select top_k experts per token (bias: e_score_correction_bias, for
+    selection only; logit_bias: added to the logits before scoring).
+    Returns (w_bf16 [T,k+S], ids int32 [T,k+S], w_f32) with S = n_shared
+    columns of the pinned shared-expert suffix (ids E, E+1, ..., weight 1)
+    after the routed ones."""
     lib = load_library()
     if logits.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("logits must be bf16 or f32")
@@ -212,8 +223,7 @@ def router_topk(
         mode = LMOE_SCORING_SIGMOID
     else:
         raise ValueError(f"unsupported scoring function {scoring!r}")
-    if bias is not None:
-        _need(bias, "e_score_correction_bias", torch.float32, (E,))
+    _check_biases(bias, logit_bias, E)
     dev = logits.device
     kw = int(top_k) + int(n_shared)
     if w_bf16 is None:
@@ -227,7 +237,7 @@ def router_topk(
     _check(
         lib.lmoe_router_topk(
             _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), int(n_shared), mode,
-            _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
+            _ptr(bias), _ptr(logit_bias), int(num_expert_group or 1), int(topk_group or 1),
             int(bool(renormalize)), float(routed_scaling_factor),
             _ptr(w_f32), _ptr(w_bf16), _ptr(ids), _stream(stream),
         ),
@@ -246,6 +256,7 @@ def router_topk_permute(
     block_m: int | None = None,
     scoring: str = "softmax",
     bias: torch.Tensor | None = None,
+    logit_bias: torch.Tensor | None = None,
     num_expert_group: int = 1,
     topk_group: int = 1,
     renormalize: bool = True,
@@ -267,8 +278,7 @@ def router_topk_permute(
     mode = {"softmax": LMOE_SCORING_SOFTMAX, "sigmoid": LMOE_SCORING_SIGMOID}.get(scoring)
     if mode is None:
         raise ValueError(f"unsupported scoring function {scoring!r}")
-    if bias is not None:
-        _need(bias, "e_score_correction_bias", torch.float32, (E,))
+    _check_biases(bias, logit_bias, E)
     dev = logits.device
     kw = int(top_k) + int(n_shared)
     if w_bf16 is None:
@@ -288,7 +298,7 @@ def router_topk_permute(
     bm = MFMA_BLOCK_M if block_m is None else int(block_m)
     status = lib.lmoe_router_topk_permute(
         _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), int(n_shared), mode,
-        _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
+        _ptr(bias), _ptr(logit_bias), int(num_expert_group or 1), int(topk_group or 1),
         int(bool(renormalize)), float(routed_scaling_factor),
         _ptr(w_f32), _ptr(w_bf16), _ptr(ids),
         _ptr(log2phy), n_table, perm.n_slots, int(bool(skip_unmapped)), bm,
@@ -296,7 +306,8 @@ def router_topk_permute(
         _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta), _stream(stream),
     )
     if status == LMOE_ERR_SHAPE:
-        router_topk(logits, top_k, scoring=scoring, bias=bias, num_expert_group=num_expert_group,
+        router_topk(logits, top_k, scoring=scoring, bias=bias, logit_bias=logit_bias,
+                    num_expert_group=num_expert_group,
                     topk_group=topk_group, renormalize=renormalize,
                     routed_scaling_factor=routed_scaling_factor, n_shared=n_shared, w_bf16=w_bf16, ids=ids,
                     w_f32=w_f32, stream=stream)
@@ -319,6 +330,7 @@ def router_gate_topk_permute(
     block_m: int | None = None,
     scoring: str = "softmax",
     bias: torch.Tensor | None = None,
+    logit_bias: torch.Tensor | None = None,
     num_expert_group: int = 1,
     topk_group: int = 1,
     renormalize: bool = True,
@@ -345,8 +357,7 @@ def router_gate_topk_permute(
     mode = {"softmax": LMOE_SCORING_SOFTMAX, "sigmoid": LMOE_SCORING_SIGMOID}.get(scoring)
     if mode is None:
         raise ValueError(f"unsupported scoring function {scoring!r}")
-    if bias is not None:
-        _need(bias, "e_score_correction_bias", torch.float32, (E,))
+    _check_biases(bias, logit_bias, E)
     dev = x.device
     kw = int(top_k) + int(n_shared)
     if w_bf16 is None:
@@ -366,7 +377,8 @@ def router_gate_topk_permute(
     bm = MFMA_BLOCK_M if block_m is None else int(block_m)
     status = lib.lmoe_router_gate_topk_permute(
         _ptr(x), _ptr(wg), T, H, E, _ptr(logits), int(logits.dtype == torch.float32), int(top_k),
-        int(n_shared), mode, _ptr(bias), int(num_expert_group or 1), int(topk_group or 1),
+        int(n_shared), mode, _ptr(bias), _ptr(logit_bias), int(num_expert_group or 1),
+        int(topk_group or 1),
         int(bool(renormalize)), float(routed_scaling_factor),
         _ptr(w_f32), _ptr(w_bf16), _ptr(ids),
         _ptr(log2phy), n_table, perm.n_slots, int(bool(skip_unmapped)), bm,
@@ -377,7 +389,8 @@ def router_gate_topk_permute(
         router_gate(x, wg, logits, stream=stream)
         return router_topk_permute(
             logits, top_k, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, block_m=bm,
-            scoring=scoring, bias=bias, num_expert_group=num_expert_group, topk_group=topk_group,
+            scoring=scoring, bias=bias, logit_bias=logit_bias, num_expert_group=num_expert_group,
+            topk_group=topk_group,
             renormalize=renormalize, routed_scaling_factor=routed_scaling_factor, n_shared=n_shared,
             w_bf16=w_bf16, ids=ids, w_f32=w_f32, stream=stream,
         )
@@ -400,8 +413,11 @@ def _cu_count(device) -> int:
     return _CU_COUNT[idx]
 
 
+_OFFSET32_LIMIT = 2**31 - 1
+
+
 def prefill_block_m(n_experts: int, hidden: int, intermediate: int, device="cuda",
-                    cu_count: int | None = None) -> int:
+                    cu_count: int | None = None, n_pairs: int | None = None) -> int:
     """Row-tile height for the prefill GEMMs of one pass over n_experts slots
     (the block_m to build the permutation with).
 
@@ -412,9 +428,13 @@ def prefill_block_m(n_experts: int, hidden: int, intermediate: int, device="cuda
     are many.  Just past one round (a 43-slot wave on 256 CUs: 258 units) the
     last units would run alone, and the 256-row tile grid finishes first
     (measured 136 + 64 us against 166 + 74 us for gate_up + down); there 256
-    is returned.  Needs hidden % 64 == 0 (else 256).  cu_count defaults to
-    the device's."""
+    is returned.  Needs hidden % 64 == 0 (else 256), and activation operands
+    below 2^31 elements (the 320-row kernel's offsets are 32-bit: n_pairs
+    rows of max(hidden, intermediate) bounds both GEMMs; else 256, whose
+    offsets are 64-bit).  cu_count defaults to the device's."""
     if hidden % 64 != 0:
+        return MFMA_BLOCK_M
+    if n_pairs is not None and int(n_pairs) * max(int(hidden), int(intermediate)) > _OFFSET32_LIMIT:
         return MFMA_BLOCK_M
     cus = int(cu_count) if cu_count is not None else _cu_count(device)
     units = int(n_experts) * ((int(intermediate) + 127) // 128)
@@ -653,12 +673,15 @@ def fused_moe_decode(
     *,
     add: torch.Tensor | None = None,
     y: torch.Tensor | None = None,
+    distinct_slots: bool = False,
     stream=None,
 ) -> torch.Tensor:
     """Decode layer body: gate_up GEMV, then down GEMV fused with the combine
     (up to 16 pairs, or no y), or with a [T*k, H] bf16 workspace y and more
     pairs the down GEMV per (row block, slot) into y and the combine; same out
-    either way."""
+    either way.  distinct_slots: the caller promises that no slot serves two
+    pairs of one token (router-fed ids through a slot table); with one token
+    it selects the faster one-pair-per-slot kernels."""
     lib = load_library()
     _need(x, "x", torch.bfloat16)
     T, H = x.shape
@@ -679,7 +702,8 @@ def fused_moe_decode(
         lib.lmoe_fused_moe_decode(
             _ptr(x), T, H, I, k, _ptr(w13_slots), _ptr(w2_slots), P, _ptr(topk_weights),
             _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.row_idx), _ptr(perm.active),
-            _ptr(perm.meta), _ptr(add), _ptr(act), _ptr(y), _ptr(out), _stream(stream),
+            _ptr(perm.meta), _ptr(add), _ptr(act), _ptr(y), _ptr(out), int(bool(distinct_slots)),
+            _stream(stream),
         ),
         "lmoe_fused_moe_decode",
     )

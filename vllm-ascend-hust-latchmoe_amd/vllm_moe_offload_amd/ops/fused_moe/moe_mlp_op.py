@@ -33,6 +33,11 @@ def _moe_mlp_impl(
 ) -> torch.Tensor:
     layer = get_layer_from_name(layer_name)
     layer_id = int(getattr(layer, "layer_id", -1))
+    if bool(getattr(layer, "has_separate_shared_expert", False)):
+        # the reference's single-tensor op covers only layers without a
+        # separate shared expert (moe_mlp_op.py:124-127); those take
+        # moe_mlp_shared and its (shared_out, routed_out) tuple
+        raise RuntimeError("moe_mlp seam supports only the _shared_experts is None path; use moe_mlp_shared")
     moe_seam_inject.set_injected_topk(layer_id, topk_weights, topk_ids)
     try:
         out = layer.forward_experts(hidden_states, shared_experts_input=shared_experts_input)
@@ -76,12 +81,15 @@ def _moe_mlp_shared_impl(
         raise RuntimeError(f"moe_mlp_shared requires a stable non-negative layer_id; layer={layer_name!r}")
     moe_seam_inject.set_injected_topk(layer_id, topk_weights, topk_ids)
     try:
-        routed = layer.forward_experts(hidden_states, shared_experts_input=None)
+        # routed_out excludes the shared expert: the runner adds the two
+        # (moe_mlp_op.py:152-201)
+        routed = layer.forward_experts(hidden_states, shared_experts_input=None, include_shared=False)
+        routed = routed.clone()  # the shared pass below may reuse the output workspace
         src = shared_experts_input if shared_experts_input is not None else hidden_states
-        shared = layer.shared_expert_forward(src)
+        shared = layer.shared_expert_forward(src).clone()
     finally:
         moe_seam_inject.clear_injected_topk(layer_id)
-    return shared.clone(), routed.clone()
+    return shared, routed
 
 
 def _moe_mlp_shared_fake(

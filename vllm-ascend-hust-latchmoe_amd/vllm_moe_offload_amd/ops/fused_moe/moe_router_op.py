@@ -93,6 +93,12 @@ def _moe_router_indirect_impl(
         router_logits = native.router_gate(
             hidden_states, gate, torch.empty((T, gate.shape[0]), dtype=hidden_states.dtype, device=hidden_states.device)
         )
+        if getattr(layer, "gate_bias", None) is not None:
+            # a gate with a linear bias: the selection adds it to the logits
+            from vllm_moe_offload_amd.fused_moe import route
+
+            w, ids, _ = route(hidden_states, None, layer.router_spec, router_logits=router_logits)
+            return w, ids
     return _moe_router_impl(
         hidden_states, router_logits, layer.top_k, layer.use_grouped_topk, layer.renormalize,
         layer.topk_group, layer.num_expert_group, layer.scoring_func,
