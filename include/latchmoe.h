@@ -272,6 +272,29 @@ int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                           void* y, void* out, int distinct_slots,
                           hipStream_t stream);
 
+/* Size of the per-device scratch array of lmoe_fused_moe_decode_noalloc. */
+#define LMOE_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* lmoe_fused_moe_decode (same arguments, same out bit for bit) without the
+ * act / y workspaces: they live in a library-owned __device__ array of
+ * LMOE_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.  No
+ * counterpart in the reference: for callers that cannot allocate (code under
+ * hipGraph capture, serving loops or harnesses that forbid hipMalloc).  The
+ * call allocates nothing.  Limit: align256(T*k*I*2) + align256(T*k*H*2)
+ * bytes must fit the array (else LMOE_ERR_WORKSPACE, before any device
+ * work); e.g. Qwen3 shape (H 2048, I 768, k 8) up to T = 409.  Every call on
+ * one GPU shares that GPU's array: calls that may overlap on one GPU race and
+ * must be ordered by the caller. */
+int lmoe_fused_moe_decode_noalloc(const void* x, int T, int H, int I, int k,
+                                  const void* w13_slots, const void* w2_slots,
+                                  int n_slots, const uint16_t* w,
+                                  const int32_t* offsets,
+                                  const int32_t* sorted_pairs,
+                                  const int32_t* row_idx, const int32_t* active,
+                                  const int32_t* meta, const void* add,
+                                  void* out, int distinct_slots,
+                                  hipStream_t stream);
+
 /* Batched host->device (or device->device) expert copies on a transfer
  * stream: optionally wait on wait_event, then for i < n copy bytes[i] from
  * src[i] to dst[i] with hipMemcpyAsync, then record done_event (may be NULL).

@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "lmoe_down",
     "lmoe_combine",
     "lmoe_fused_moe_decode",
+    "lmoe_fused_moe_decode_noalloc",
     "lmoe_down_combine",
     "lmoe_stage_copy",
     "lmoe_table_update",
@@ -95,6 +96,10 @@ _SIGNATURES = {
         _i,
         [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
          _i, _vp],
+    ),
+    "lmoe_fused_moe_decode_noalloc": (
+        _i,
+        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp],
     ),
     "lmoe_down_combine": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "lmoe_stage_copy": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
@@ -706,6 +711,45 @@ def fused_moe_decode(
             _stream(stream),
         ),
         "lmoe_fused_moe_decode",
+    )
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 8 << 20  # LMOE_NOALLOC_SCRATCH_BYTES
+
+
+def fused_moe_decode_noalloc(
+    x: torch.Tensor,
+    topk_weights: torch.Tensor,
+    w13_slots: torch.Tensor,
+    w2_slots: torch.Tensor,
+    perm: Permutation,
+    out: torch.Tensor,
+    *,
+    add: torch.Tensor | None = None,
+    distinct_slots: bool = False,
+    stream=None,
+) -> torch.Tensor:
+    """fused_moe_decode with act / y in the library's per-GPU scratch array
+    (nothing is allocated; calls that overlap on one GPU race)."""
+    lib = load_library()
+    _need(x, "x", torch.bfloat16)
+    T, H = x.shape
+    _need(topk_weights, "topk_weights", torch.bfloat16)
+    k = topk_weights.shape[1]
+    P, I = _check_bank(w13_slots, w2_slots, H)
+    if perm.n_pairs != T * k or perm.n_slots != P:
+        raise ValueError("permutation does not match the batch or the slot bank")
+    _need(out, "out", torch.bfloat16, (T, H))
+    if add is not None:
+        _need(add, "add", torch.bfloat16, (T, H))
+    _check(
+        lib.lmoe_fused_moe_decode_noalloc(
+            _ptr(x), T, H, I, k, _ptr(w13_slots), _ptr(w2_slots), P, _ptr(topk_weights),
+            _ptr(perm.offsets), _ptr(perm.sorted_pairs), _ptr(perm.row_idx), _ptr(perm.active),
+            _ptr(perm.meta), _ptr(add), _ptr(out), int(bool(distinct_slots)), _stream(stream),
+        ),
+        "lmoe_fused_moe_decode_noalloc",
     )
     return out
 
