@@ -304,6 +304,47 @@ int lmoe_stage_copy(void* const* dst, const void* const* src,
                     const size_t* bytes, int n, hipStream_t transfer_stream,
                     hipEvent_t wait_event, hipEvent_t done_event);
 
+/* Batched expert copies by a gather-copy kernel on the transfer stream:
+ * optionally wait on wait_event, then for i < n copy bytes[i] from src[i] to
+ * dst[i] (sources: page-locked host memory mapped for the device at the same
+ * address, or device memory; destinations: device memory), then
+ * table[idx[p]] = val[p] for p < n_tab (fill != 0: every other entry of the
+ * n_table-entry table becomes -1), then record done_event (may be NULL).
+ * One launch per 32 copies; the table rides with the last one (fill: at
+ * most 128 pairs).  Every range
+ * is checked before anything is queued: a range outside one runtime
+ * allocation, or a source the device cannot read at its host address
+ * (pageable memory), returns LMOE_ERR_ARG, and bytes or addresses not
+ * multiples of 16 LMOE_ERR_SHAPE (use lmoe_stage_copy then).  Replaces
+ * TransferEngine.load_many_async (transfer_engine.py:139-187) with the
+ * contiguous-run batching of :205-228 done by the caller, and the
+ * persistent-log2phy write (runtime.py:3068-3101) or the stage-bank table
+ * build (runtime.py:2035-2258) that publishes the batch. */
+int lmoe_stage_gather(void* const* dst, const void* const* src,
+                      const size_t* bytes, int n, int32_t* table, int n_table,
+                      const int32_t* idx, const int32_t* val, int n_tab,
+                      int fill, hipStream_t transfer_stream,
+                      hipEvent_t wait_event, hipEvent_t done_event);
+
+/* Host-side slot planning of one decode staging over a slot table held as
+ * arrays (no device work): state[s] (0 EMPTY, 1 LOADING, 2 READY,
+ * 3 COMPUTING), owner[s] (expert id, -1 none), version[s], last_used[s] for
+ * s < n_slots, and slot_of[e] (slot of resident expert e, -1 none) for
+ * e < n_experts.  For each active[j] in order: a resident READY expert is a
+ * hit (last_used = step); otherwise the lowest-id EMPTY slot, else the READY
+ * slot of smallest (last_used, id), is reserved: its previous owner loses
+ * residency, owner = expert, state LOADING, version + 1, last_used = step.
+ * slot_ids[j] is the slot, miss[j] 1 for a reservation.  Returns the number
+ * of misses, or -(j + 1) when expert j needs in-flight work drained first
+ * (resident but LOADING / COMPUTING, or every slot LOADING / COMPUTING;
+ * experts before j are planned), or LMOE_ERR_ARG.  Replaces the staging
+ * loop of prepare_fixed_slot_plan_into_log2phy (runtime.py:1636-1936) with
+ * ExpertSlotBank.allocate_for (slot_bank.py:211-336). */
+int lmoe_slot_plan(int8_t* state, int32_t* owner, int64_t* version,
+                   int64_t* last_used, int n_slots, int32_t* slot_of,
+                   int n_experts, const int32_t* active, int n_active,
+                   int64_t step, int32_t* slot_ids, int8_t* miss);
+
 /* table[idx[i]] = val[i] for i < n, on stream; the idx must be distinct
  * (LMOE_ERR_ARG otherwise).  idx and val are HOST arrays read during the
  * call; the pairs travel as kernel arguments (no staging buffer, no copy),

@@ -190,3 +190,77 @@ def test_c3_full_size_waves_equal_full_layer_bitwise(qwen_experts):
     frac, max_ulps = ulp_mismatch_stats(got, ref, abs_floor=rms / 256, count_floor=rms / 4096)
     print(f"  sampled y: frac>1ulp {frac:.2e} max {max_ulps:.2f} ulp", flush=True)
     assert frac <= 1e-3 and max_ulps <= 2.0
+
+
+def test_stage_gather_copies_and_publishes_the_table():
+    """lmoe_stage_gather: ranges from page-locked host memory and from device
+    memory into device memory, more ranges than one launch holds, and the
+    slot-table entries (pairs only, or the whole table with -1 elsewhere)
+    written by the same batch; the ready event orders it all before the
+    compute stream."""
+    from vllm_moe_offload_amd import native
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    n_rows, row = 80, 48 * 1024  # 96 KiB rows
+    src_dev = torch.randint(-30000, 30000, (n_rows, row), generator=g, device="cuda", dtype=torch.int16)
+    src_host = torch.empty((n_rows, row), dtype=torch.int16, pin_memory=True)
+    src_host.copy_(src_dev)
+    dst = torch.zeros((n_rows, row), dtype=torch.int16, device="cuda")
+    rng = np.random.default_rng(3)
+    order = rng.permutation(n_rows)
+    copies = []
+    for i, r in enumerate(order[:70]):  # 70 ranges: three launches
+        src = src_host if i % 3 else src_dev
+        copies.append((int(dst[i].data_ptr()), int(src[int(r)].data_ptr()), row * 2))
+    table = torch.full((300,), 7, dtype=torch.int32, device="cuda")
+    idx = tuple(int(v) for v in rng.permutation(300)[:150])  # 150 pairs: two table launches
+    val = tuple(range(150))
+    stream = torch.cuda.Stream()
+    done = torch.cuda.Event()
+    assert native.stage_gather(copies, stream, table_update=(table, idx, val))
+    done.record(stream)
+    torch.cuda.current_stream().wait_event(done)
+    want = torch.stack([src_dev[int(r)] for r in order[:70]])
+    assert torch.equal(dst[:70], want)
+    assert torch.equal(dst[70:], torch.zeros_like(dst[70:]))
+    t = table.cpu().numpy()
+    exp = np.full(300, 7, dtype=np.int32)
+    exp[list(idx)] = val
+    np.testing.assert_array_equal(t, exp)
+    # fill: every entry not among the pairs becomes -1
+    assert native.stage_gather(copies[:2], stream, table_update=(table, idx[:40], val[:40], True))
+    torch.cuda.current_stream().wait_stream(stream)
+    exp = np.full(300, -1, dtype=np.int32)
+    exp[list(idx[:40])] = val[:40]
+    np.testing.assert_array_equal(table.cpu().numpy(), exp)
+    # misaligned ranges are refused before anything is queued
+    assert not native.stage_gather([(int(dst[0].data_ptr()) + 8, int(src_dev[0].data_ptr()), 64)], stream)
+    # torch reports pageable memory as not page-locked (the same runtime
+    # query the library's range check makes), so the transfer engine sends
+    # such sources to the copy engines
+    assert not torch.empty(64, dtype=torch.int16).is_pinned() and src_host.is_pinned()
+
+
+def test_transfer_engine_takes_copy_engines_for_pageable_sources():
+    """Host rows that are not page-locked go through hipMemcpyAsync; the
+    batch still lands and publishes."""
+    from vllm_moe_offload_amd.moe_offload.expert_key import ExpertKey
+    from vllm_moe_offload_amd.moe_offload.host_store import ExpertWeightBundle
+    from vllm_moe_offload_amd.moe_offload.slot_bank import ExpertSlotBank, SlotState
+    from vllm_moe_offload_amd.moe_offload.transfer_engine import TransferEngine
+
+    bank = ExpertSlotBank(4, (64, 32), (32, 32), dtype=torch.bfloat16, device=torch.device("cuda"))
+    host13 = torch.randn((3, 64, 32)).to(torch.bfloat16)   # pageable
+    host2 = torch.randn((3, 32, 32)).to(torch.bfloat16)
+    eng = TransferEngine()
+    loads = []
+    for e in range(3):
+        slot = bank.allocate_for(ExpertKey(0, e), step_id=1)
+        loads.append((ExpertWeightBundle(0, e, host13[e], host2[e]), slot))
+    table = torch.full((3,), -1, dtype=torch.int32, device="cuda")
+    ready = eng.load_many_async(loads, table_update=(table, (0, 1, 2), (0, 1, 2)))
+    ready.install_consumer_dependency(torch.cuda.current_stream())
+    assert eng.batches_gathered == 0
+    assert all(s.state == SlotState.READY for _, s in loads)
+    assert torch.equal(bank.w13_slots[:3].cpu(), host13) and torch.equal(bank.w2_slots[:3].cpu(), host2)
+    assert table.tolist() == [0, 1, 2]

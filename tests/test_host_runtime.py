@@ -145,7 +145,7 @@ def test_stage_drains_prior_compute_before_reserving_sync_misses():  # test_fixe
     for sid in initial.mapping.active_slot_ids:
         s = bank.slots[sid]
         s.state = SlotState.COMPUTING
-        rt._slot_compute_done_events[(7, s.slot_id, s.version)] = done
+    rt._note_compute_fence(7, [(sid, bank.slots[sid].version) for sid in initial.mapping.active_slot_ids], done)
     prepared = rt.stage_fixed_slot_plan(layer_id=7, active_experts=(2, 3, 4), num_logical_experts=5)
     assert done.synchronize_calls == 1
     assert all(s.state == SlotState.READY for s in bank.slots)
@@ -164,13 +164,13 @@ def test_capture_handoff_releases_prior_compute_without_host_sync(monkeypatch): 
     for sid in prepared.mapping.active_slot_ids:
         s = bank.slots[sid]
         s.state = SlotState.COMPUTING
-        rt._slot_compute_done_events[(7, s.slot_id, s.version)] = done
+    rt._note_compute_fence(7, [(sid, bank.slots[sid].version) for sid in prepared.mapping.active_slot_ids], done)
     monkeypatch.setattr(runtime_mod, "_is_current_graph_capturing", lambda: True)
     cap = rt.capture_safe_slot_weights(layer_id=7)
     handle = rt.begin_slot_compute(cap)
     assert handle is not None and done.synchronize_calls == 0
     assert all(bank.slots[s].state == SlotState.COMPUTING for s in handle.slot_ids)
-    assert not rt._slot_compute_done_events
+    assert not rt._compute_fences.get(7)
 
 
 def test_stage_fixed_slot_plan_writes_persistent_log2phy():  # :1388-1419

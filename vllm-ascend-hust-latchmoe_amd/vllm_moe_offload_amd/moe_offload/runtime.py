@@ -34,6 +34,7 @@ from contextlib import contextmanager
 from dataclasses import dataclass
 from time import perf_counter
 
+import numpy as np
 import torch
 
 from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
@@ -195,7 +196,7 @@ class MoeOffloadRuntime:
         self._profile_events: list[dict[str, object]] = []
         self._prefill_route_stats_by_layer: dict[int, MoePrefillRouteStats] = {}
         self._active_slot_ids_by_layer: dict[int, tuple[int, ...]] = {}
-        self._slot_compute_done_events: dict[tuple[int, int, int], object] = {}
+        self._compute_fences: dict[int, list] = {}
         self._layer_release_events: dict[int, object] = {}
         self._placement_plan_provider: PlacementPlanProvider | None = None
         self._fixed_slot_execution_state = threading.local()
@@ -457,54 +458,82 @@ class MoeOffloadRuntime:
         return ledger
 
     # ----------------------------------------------------- slot lifecycle
+    # Compute fences: per layer, the events that end queued compute reading
+    # the main bank, each with the (slot, version) generations it covers.  A
+    # COMPUTING slot is released (READY) only once a fence covering its
+    # current generation has completed; a slot whose generation moved on
+    # while its compute was in flight is an error.
+    def _note_compute_fence(self, layer_id: int, generations, event) -> None:
+        self._compute_fences.setdefault(int(layer_id), []).append(
+            (event, tuple((int(s), int(v)) for s, v in generations)))
+
+    def _take_fences(self, layer_id: int, generations) -> list:
+        """Remove and return the fences covering these (slot, version)
+        generations; raise for a generation no fence covers."""
+        fences = self._compute_fences.get(int(layer_id), [])
+        wanted = set(generations)
+        covered: set = set()
+        taken, kept = [], []
+        for ev, gens in fences:
+            hit = wanted.intersection(gens)
+            if hit:
+                taken.append(ev)
+                covered |= hit
+                rest = tuple(g for g in gens if g not in wanted)
+                if rest:
+                    kept.append((ev, rest))
+            else:
+                kept.append((ev, gens))
+        missing = sorted(wanted - covered)
+        if missing:
+            s, v = missing[0]
+            raise RuntimeError(f"computing slot has no completion event: layer={int(layer_id)} slot={s} version={v}")
+        self._compute_fences[int(layer_id)] = kept
+        return list({id(e): e for e in taken}.values())
+
     def _allocate_slot_with_loading_fallback(self, bank: ExpertSlotBank, key: ExpertKey, *, step_id: int):
         try:
             return bank.allocate_for(key, step_id=step_id)
         except RuntimeError:
-            if not any(s.state in (SlotState.LOADING, SlotState.COMPUTING) for s in bank.slots):
+            if not bank.has_inflight():
                 raise
             self._drain_slot_bank_inflight_work(bank)
             return bank.allocate_for(key, step_id=step_id)
 
     def _drain_slot_bank_inflight_work(self, bank: ExpertSlotBank) -> None:
-        """Finish every in-flight copy and compute touching this bank."""
-        if any(s.state == SlotState.LOADING for s in bank.slots):
+        """Finish every in-flight copy into the bank and every queued compute
+        reading it, then release the computing slots."""
+        from vllm_moe_offload_amd.moe_offload.slot_bank import COMPUTING, LOADING
+
+        if (bank._state == LOADING).any():
             self._transfer_engine.synchronize()
-            still = [s.slot_id for s in bank.slots if s.state == SlotState.LOADING]
+            still = np.flatnonzero(bank._state == LOADING).tolist()
             if still:
                 raise RuntimeError(f"H2D synchronization completed without a matching ready event for slots {still}")
-        computing = [s for s in bank.slots if s.state == SlotState.COMPUTING]
-        leases = [s.lease() for s in computing]
-        events: list[object] = []
-        seen: set[int] = set()
-        for lease in leases:
-            ev = self._slot_compute_done_events.pop((int(lease.expert_key.layer_id), int(lease.slot_id), int(lease.version)), None)
-            if ev is None:
-                raise RuntimeError(
-                    f"computing slot has no completion event: layer={lease.expert_key.layer_id} "
-                    f"slot={lease.slot_id} version={lease.version}"
-                )
-            if id(ev) not in seen:
-                seen.add(id(ev))
-                events.append(ev)
+        comp = np.flatnonzero(bank._state == COMPUTING)
+        if comp.size == 0:
+            return
+        layer_id = int(bank._owner_layer[comp[0]])
+        gens = [(int(s), int(bank._version[s])) for s in comp]
+        owners = [int(bank._owner[s]) for s in comp]
+        events = self._take_fences(layer_id, gens)
         for ev in events:
             _synchronize_event(ev)
-        for slot, lease in zip(computing, leases):
-            if not slot.matches_lease(lease):
-                raise RuntimeError(f"slot {lease.slot_id} ownership changed while compute was in flight")
-            if slot.state == SlotState.COMPUTING:
-                slot.state = SlotState.READY
-        for layer_id in sorted({int(l.expert_key.layer_id) for l in leases} - self._slot_generation_protection_evidence):
-            mine = [l for l in leases if int(l.expert_key.layer_id) == layer_id]
+        for (sid, ver), e in zip(gens, owners):
+            if int(bank._version[sid]) != ver or int(bank._owner[sid]) != e:
+                raise RuntimeError(f"slot {sid} ownership changed while compute was in flight")
+            if int(bank._state[sid]) == COMPUTING:
+                bank.mark_ready(sid)
+        if layer_id not in self._slot_generation_protection_evidence:
             self._slot_generation_protection_evidence.add(layer_id)
             self._record_profile_event(
                 "slot_generation_protected_until_compute_complete",
                 layer_id=layer_id,
                 start=perf_counter(),
                 payload={
-                    "slot_ids": [int(l.slot_id) for l in mine],
-                    "generations": [int(l.version) for l in mine],
-                    "expert_ids": [int(l.expert_key.expert_id) for l in mine],
+                    "slot_ids": [g[0] for g in gens],
+                    "generations": [g[1] for g in gens],
+                    "expert_ids": owners,
                     "completion_events_synchronized": len(events),
                     "leases_still_match": True,
                 },
@@ -527,27 +556,29 @@ class MoeOffloadRuntime:
             slot_ids = tuple(int(s) for s in self._active_slot_ids_by_layer.get(layer_id, ()))
         if not slot_ids:
             return None
-        capturing = _is_current_graph_capturing()
-        leases: list[SlotLease] = []
-        for sid in slot_ids:
-            slot = bank.slots[sid]
-            if sid >= len(prepared.mapping.slot_to_expert):
-                raise RuntimeError(f"prepared slot mapping has no owner entry for slot {sid}")
-            owner = prepared.mapping.slot_to_expert[sid]
-            expected = ExpertKey(layer_id, int(owner)) if owner is not None else None
-            if slot.expert_key != expected:
-                raise RuntimeError(f"prepared mapping owner mismatch for slot {sid}: expected {expected}, found {slot.expert_key}")
-            if slot.state == SlotState.COMPUTING and capturing:
-                # capture follows the preceding eager compute on the same
-                # device stream order; hand its completion record over
-                # instead of synchronising the host inside capture
-                lease = slot.lease()
-                if self._slot_compute_done_events.pop((layer_id, sid, int(lease.version)), None) is None:
+        owners = prepared.mapping.slot_to_expert
+        if _is_current_graph_capturing():
+            # the capture follows the preceding eager compute in stream order:
+            # its fences are handed over, the host does not wait inside capture
+            busy = [sid for sid in slot_ids if bank.slots[sid].state == SlotState.COMPUTING]
+            if busy:
+                try:
+                    self._take_fences(layer_id, [(sid, bank.slots[sid].version) for sid in busy])
+                except RuntimeError as exc:
                     raise RuntimeError(
                         "capturing slot has no completion event from the preceding eager compute: "
-                        f"layer={layer_id} slot={sid} version={lease.version}"
-                    )
-                slot.state = SlotState.READY
+                        f"{str(exc).split(': ', 1)[-1]}"
+                    ) from exc
+                for sid in busy:
+                    bank.mark_ready(sid)
+        leases = []
+        for sid in slot_ids:
+            if sid >= len(owners):
+                raise RuntimeError(f"prepared slot mapping has no owner entry for slot {sid}")
+            slot = bank.slots[sid]
+            want = ExpertKey(layer_id, int(owners[sid])) if owners[sid] is not None else None
+            if slot.expert_key != want:
+                raise RuntimeError(f"prepared mapping owner mismatch for slot {sid}: expected {want}, found {slot.expert_key}")
             if slot.state != SlotState.READY:
                 raise RuntimeError(f"prepared slot {sid} is not ready for compute: {slot.state.value}")
             leases.append(slot.lease())
@@ -556,7 +587,8 @@ class MoeOffloadRuntime:
         return SlotComputeHandle(layer_id, slot_ids, tuple(leases))
 
     def end_slot_compute(self, handle: SlotComputeHandle | None) -> None:
-        """Record the compute stream's completion event for the leased slots."""
+        """Fence the leased slots with an event at the end of the queued
+        compute (host-only banks: released at once)."""
         if handle is None:
             return
         bank = self._slot_banks.get(int(handle.layer_id))
@@ -569,14 +601,12 @@ class MoeOffloadRuntime:
             if slot.state != SlotState.COMPUTING:
                 raise RuntimeError(f"slot {lease.slot_id} is not computing at compute completion: {slot.state.value}")
         ev = self._record_current_stream_event_or_none()
-        if ev is not None:
-            self._layer_release_events[int(handle.layer_id)] = ev
-        for lease in handle.leases:
-            slot = bank.slots[int(lease.slot_id)]
-            if ev is None:
-                slot.state = SlotState.READY
-            else:
-                self._slot_compute_done_events[(int(handle.layer_id), int(lease.slot_id), int(lease.version))] = ev
+        if ev is None:
+            for lease in handle.leases:
+                bank.mark_ready(int(lease.slot_id))
+            return
+        self._layer_release_events[int(handle.layer_id)] = ev
+        self._note_compute_fence(handle.layer_id, [(l.slot_id, l.version) for l in handle.leases], ev)
 
     def record_layer_compute(self, layer_id: int) -> None:
         """Record, on the current stream, the end of compute the caller has
@@ -679,68 +709,65 @@ class MoeOffloadRuntime:
         bank = self._slot_banks.get(layer_id)
         if bank is None:
             raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
-        states = [s.state for s in bank.slots]
-        if SlotState.LOADING in states or SlotState.COMPUTING in states:
+        if bank.has_inflight():
             self._drain_slot_bank_inflight_work(bank)
         step_id = self._step(step_id)
         t0 = perf_counter()
-        hits: list[int] = []
-        misses: list[int] = []
-        async_loads = []
-        sync_loads = []
-        slot_ids: list[int] = []
-        owners: list[int | None] = [None] * bank.physical_expert_count
-        for logical_id in bank.pinned_logical_ids:
-            owners[int(bank.pinned_slot_for_logical_id(logical_id))] = int(logical_id)
-        for e in active:
-            key = ExpertKey(layer_id, e)
-            slot = bank.lookup(key)
-            if slot is not None and slot.state != SlotState.READY:
-                self._drain_slot_bank_inflight_work(bank)
-                slot = bank.lookup(key)
-            if slot is not None and slot.state == SlotState.READY:
-                slot.last_used_step = step_id
-                hits.append(e)
-            else:
-                misses.append(e)
-                try:
-                    slot = self._allocate_slot_with_loading_fallback(bank, key, step_id=step_id)
-                except RuntimeError as exc:
-                    raise RuntimeError(
-                        f"failed to allocate expert slot for layer {layer_id} expert {e} with "
-                        f"num_slots={self.config.num_slots}; async_load={self.config.async_load}"
-                    ) from exc
-                bundle = self._host_store.get(layer_id, e)
-                (async_loads if self.config.async_load else sync_loads).append((bundle, slot))
-            slot_ids.append(int(slot.slot_id))
-        if sync_loads:
-            try:
-                self._transfer_engine.load_many_sync(sync_loads, validate_layout=False)
-            except Exception:
-                self._release_allocated_loads(bank, sync_loads)
-                raise
+        ids = np.fromiter(active, dtype=np.int32, count=len(active))
+        # one native call plans every expert (hit: touch; miss: reserve a
+        # slot, LOADING); it stops where in-flight work must finish first
+        st, slot_ids, miss = bank.plan(layer_id, ids, step_id=step_id)
+        base = 0
+        while st < 0:
+            j = base + (-st - 1)  # the expert the plan stopped at
+            if not bank.has_inflight():
+                self._raise_no_slot(layer_id, int(ids[j]), bank)
+            self._drain_slot_bank_inflight_work(bank)
+            st, rest_ids, rest_miss = bank.plan(layer_id, ids[j:], step_id=step_id)
+            slot_ids[j:], miss[j:] = rest_ids, rest_miss
+            if st == -1:  # stopped at the same expert with nothing left to wait for
+                self._raise_no_slot(layer_id, int(ids[j]), bank)
+            base = j
+        slot_list = [int(v) for v in slot_ids]
+        is_miss = miss.astype(bool)
+        hits = tuple(int(e) for e in ids[~is_miss])
+        misses = tuple(int(e) for e in ids[is_miss])
+        loads = [(self._host_store.get(layer_id, e), bank.slots[sid])
+                 for e, sid in zip(misses, (v for v, m in zip(slot_list, is_miss) if m))]
         ready = None
         table_updates = -1
-        if async_loads:
+        if loads and not self.config.async_load:
+            try:
+                self._transfer_engine.load_many_sync(loads, validate_layout=False)
+            except Exception:
+                self._release_allocated_loads(bank, loads)
+                raise
+        elif loads:
             # device bank and table: the changed log2phy entries ride with the
             # copies on the transfer stream, inside their ready event
             with_table = log2phy.device.type == "cuda" and bank.w13_slots.device.type == "cuda"
-            upd = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=slot_ids) \
+            upd = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=slot_list) \
                 if with_table else ((), ())
             extra = {"table_update": (log2phy, upd[0], upd[1])} if upd[0] else {}
             try:
                 ready = self._transfer_engine.load_many_async(
-                    async_loads, wait_event=self._layer_release_events.get(layer_id), record_event=True,
+                    loads, wait_event=self._layer_release_events.get(layer_id), record_event=True,
                     validate_layout=False, **extra,
                 )
             except Exception:
-                self._release_allocated_loads(bank, async_loads)
+                self._release_allocated_loads(bank, loads)
                 raise
             if with_table:
                 self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd[0], slot_ids=upd[1])
                 table_updates = len(upd[0])
-        return PendingFixedSlotStage(layer_id, active, tuple(slot_ids), owners, ready, tuple(hits), tuple(misses),
+        return PendingFixedSlotStage(layer_id, active, tuple(slot_list), bank.owners(), ready, hits, misses,
                                      log2phy, step_id, t0, table_updates)
+
+    def _raise_no_slot(self, layer_id: int, expert_id: int, bank: ExpertSlotBank) -> None:
+        raise RuntimeError(
+            f"failed to allocate expert slot for layer {layer_id} expert {expert_id} with "
+            f"num_slots={self.config.num_slots}; async_load={self.config.async_load}"
+        ) from RuntimeError(f"no evictable expert slots; states={bank.state_counts()}")
 
     def _publish(self, pending: PendingFixedSlotStage, *, record_stage_profile: bool) -> PreparedSlotWeights:
         layer_id = pending.layer_id
@@ -748,7 +775,7 @@ class MoeOffloadRuntime:
         # order the copies before the consumer, THEN publish the mapping
         if pending.ready is not None:
             self._wait_transfer_event(pending.ready)
-        active, slot_ids, owners = pending.active, pending.slot_ids, pending.owners
+        active, slot_ids = pending.active, pending.slot_ids
         if pending.table_updates >= 0:
             n_updates = pending.table_updates  # written on the transfer stream with the copies
         else:
@@ -757,9 +784,7 @@ class MoeOffloadRuntime:
                 _update_log2phy_entries(pending.log2phy, expert_ids=upd_e, slot_ids=upd_s)
                 self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd_e, slot_ids=upd_s)
             n_updates = len(upd_e)
-        for e, sid in zip(active, slot_ids):
-            owners[sid] = e
-        mapping = ExpertSlotMapping(layer_id, active, pending.log2phy, tuple(owners), tuple(slot_ids))
+        mapping = ExpertSlotMapping(layer_id, active, pending.log2phy, tuple(pending.owners), tuple(slot_ids))
         self._active_slot_ids_by_layer[layer_id] = tuple(slot_ids)
         self.last_stage_stats = (len(pending.hits), len(pending.misses))
         if record_stage_profile and (self.config.profile_path or os.environ.get("LATCHMOE_PROFILE")):
@@ -1052,15 +1077,9 @@ class MoeOffloadRuntime:
         hits: list[int] = []
         misses: list[int] = []
         loads = []
-        if build_log2phy:
-            values = [-1] * total
-            for logical_id in stage.pinned_logical_ids:
-                values[logical_id] = int(stage.pinned_slot_for_logical_id(logical_id))
         for i, e in enumerate(active):
             key = ExpertKey(layer_id, e)
             slot = (stage.assign_transient_slot if known_miss else stage.assign_slot)(i, key, step_id=step_id)
-            if build_log2phy:
-                values[e] = i
             hit = None if known_miss else src.lookup(key)
             if hit is not None and hit.state == SlotState.READY:
                 hits.append(e)
@@ -1068,13 +1087,22 @@ class MoeOffloadRuntime:
             else:
                 misses.append(e)
                 loads.append((self._host_store.get(layer_id, e), slot))
-        if build_log2phy:
-            table.copy_(torch.tensor(values, dtype=torch.int32), non_blocking=False)
+        # the wave's table: slot i <- i-th expert, the pinned suffix, -1 elsewhere
+        pairs = (tuple(active) + tuple(stage.pinned_logical_ids),
+                 tuple(range(len(active))) + tuple(stage.pinned_slot_ids))
+        fused_table = build_log2phy and async_load and bool(loads) and table.device.type == "cuda" \
+            and stage.w13_slots.device.type == "cuda"
+        if build_log2phy and not fused_table:
+            values = np.full(total, -1, dtype=np.int32)
+            values[list(pairs[0])] = pairs[1]
+            table.copy_(torch.from_numpy(values), non_blocking=False)
         ready = None
         if loads:
             if async_load:
+                extra = {"table_update": (table, pairs[0], pairs[1], True)} if fused_table else {}
                 try:
-                    ready = self._transfer_engine.load_many_async(loads, wait_event=wait_event, record_event=True, validate_layout=False)
+                    ready = self._transfer_engine.load_many_async(loads, wait_event=wait_event, record_event=True,
+                                                                  validate_layout=False, **extra)
                 except Exception:
                     self._release_allocated_loads(stage, loads)
                     raise
@@ -1090,12 +1118,8 @@ class MoeOffloadRuntime:
             stage.clear_slot(sid)
         if async_load and ready is None:
             ready = wait_event
-        owners: list[int | None] = [None] * stage.physical_expert_count
-        for logical_id in stage.pinned_logical_ids:
-            owners[int(stage.pinned_slot_for_logical_id(logical_id))] = int(logical_id)
-        for i, e in enumerate(active):
-            owners[i] = e
-        mapping = ExpertSlotMapping(layer_id, active, table, tuple(owners), tuple(range(len(active))), log2phy_valid=build_log2phy)
+        mapping = ExpertSlotMapping(layer_id, active, table, tuple(stage.owners()), tuple(range(len(active))),
+                                   log2phy_valid=build_log2phy)
         per = int(self._expert_weight_bytes_by_layer.get(layer_id, 0))
         payload = {
             "buffer_index": int(buffer_index),

@@ -1,24 +1,33 @@
-"""Address-stable expert slot bank in HBM.
+"""Address-stable expert slot bank in HBM with its slot table.
 
-Two device tensors hold every physical slot for the life of the process:
-w13_slots [P, 2I, H] and w2_slots [P, H, I] (bf16, checkpoint layout, K
-contiguous so the gfx950 GEMV/MFMA kernels stream rows with 16-byte loads).
-Rows [0, num_slots) are the dynamic routed cache; rows after it are pinned
-shared experts that LRU can never pick.  Slot ownership is versioned: every
-reassignment bumps the slot's version, and a lease (slot, owner, version)
-detects stale completions.
+Storage: two device tensors hold every physical slot for the life of the
+process, w13_slots [P, 2I, H] and w2_slots [P, H, I] (bf16, checkpoint
+layout, K contiguous for the gfx950 GEMV / MFMA kernels).  Rows [0,
+num_slots) are the dynamic cache; rows past it hold pinned shared experts
+that are never reassigned.
 
-Reference: moe_offload/slot_bank.py:27-335.  Allocation policy kept exactly:
-a resident expert is touched; otherwise the lowest-id EMPTY slot; otherwise
-the READY slot with the smallest (last_used_step, slot_id); LOADING and
-COMPUTING slots are never reassigned.
+Bookkeeping is a struct of arrays, one entry per dynamic slot: state code,
+owning expert id (and the layer of its key), version and last use, plus an
+expert-id -> slot residency array.  The decode staging plans a whole layer
+in one call of the native planner (lmoe_slot_plan, which mutates these
+arrays in place); the per-slot methods below work on the same arrays.
+`slots[i]` is a view of entry i, not a copy: reading or assigning
+`slots[i].state` reads or writes the table.
+
+Reference: moe_offload/slot_bank.py:27-336 (SlotState, SlotLease,
+ExpertSlot, ExpertSlotBank).  The allocation policy is the reference's,
+because its tests pin its exact choices: a resident expert is touched;
+otherwise the lowest-id EMPTY slot; otherwise the READY slot with the
+smallest (last use, slot id); LOADING and COMPUTING slots are never taken.
 """
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from enum import Enum
 
+import numpy as np
 import torch
 
 from vllm_moe_offload_amd.moe_offload.expert_key import ExpertKey
@@ -32,6 +41,12 @@ class SlotState(str, Enum):
     COMPUTING = "computing"
 
 
+# state codes of the slot table (shared with the native planner)
+_CODES = (SlotState.EMPTY, SlotState.LOADING, SlotState.READY, SlotState.COMPUTING)
+_CODE_OF = {st: np.int8(i) for i, st in enumerate(_CODES)}
+EMPTY, LOADING, READY, COMPUTING = (int(_CODE_OF[s]) for s in _CODES)
+
+
 @dataclass(frozen=True)
 class SlotLease:
     """One ownership interval of a slot: (slot, owner, version)."""
@@ -41,35 +56,84 @@ class SlotLease:
     version: int
 
 
-@dataclass
 class ExpertSlot:
-    slot_id: int
-    w13: torch.Tensor
-    w2: torch.Tensor
-    state: SlotState = SlotState.EMPTY
-    expert_key: ExpertKey | None = None
-    version: int = 0
-    last_used_step: int = -1
+    """View of one slot-table entry and its weight rows."""
+
+    __slots__ = ("_bank", "slot_id", "w13", "w2")
+
+    def __init__(self, bank: "ExpertSlotBank", slot_id: int) -> None:
+        self._bank = bank
+        self.slot_id = int(slot_id)
+        self.w13 = bank.w13_slots[slot_id]
+        self.w2 = bank.w2_slots[slot_id]
+
+    @property
+    def state(self) -> SlotState:
+        return _CODES[int(self._bank._state[self.slot_id])]
+
+    @state.setter
+    def state(self, value: SlotState) -> None:
+        self._bank._state[self.slot_id] = _CODE_OF[SlotState(value)]
+
+    @property
+    def expert_key(self) -> ExpertKey | None:
+        return self._bank._key_of(self.slot_id)
+
+    @property
+    def version(self) -> int:
+        return int(self._bank._version[self.slot_id])
+
+    @property
+    def last_used_step(self) -> int:
+        return int(self._bank._last_used[self.slot_id])
+
+    @last_used_step.setter
+    def last_used_step(self, step: int) -> None:
+        self._bank._last_used[self.slot_id] = int(step)
 
     def as_bundle(self) -> ExpertWeightBundle:
         key = self.expert_key or ExpertKey(-1, -1)
         return ExpertWeightBundle(key.layer_id, key.expert_id, self.w13, self.w2)
 
     def lease(self) -> SlotLease:
-        if self.expert_key is None:
+        key = self.expert_key
+        if key is None:
             raise RuntimeError(f"slot {self.slot_id} has no owner")
-        return SlotLease(int(self.slot_id), self.expert_key, int(self.version))
+        return SlotLease(self.slot_id, key, self.version)
 
     def matches_lease(self, lease: SlotLease) -> bool:
+        b = self._bank
+        s = self.slot_id
         return (
-            int(self.slot_id) == int(lease.slot_id)
-            and self.expert_key == lease.expert_key
-            and int(self.version) == int(lease.version)
+            s == int(lease.slot_id)
+            and int(b._owner[s]) == int(lease.expert_key.expert_id)
+            and int(b._owner_layer[s]) == int(lease.expert_key.layer_id)
+            and int(b._version[s]) == int(lease.version)
         )
+
+    def __repr__(self) -> str:
+        return f"ExpertSlot({self.slot_id}, {self.state.value}, {self.expert_key}, v{self.version})"
 
 
 def _nbytes(t: torch.Tensor) -> int:
     return int(t.numel()) * int(t.element_size())
+
+
+_PLAN_FN = None
+
+
+def _native_plan():
+    """ctypes handle of lmoe_slot_plan (host code of the kernel library)."""
+    global _PLAN_FN
+    if _PLAN_FN is None:
+        from vllm_moe_offload_amd import native
+
+        fn = native.load_library().lmoe_slot_plan
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                               ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+        _PLAN_FN = fn
+    return _PLAN_FN
 
 
 class ExpertSlotBank:
@@ -90,17 +154,20 @@ class ExpertSlotBank:
             raise ValueError("pinned logical expert ids must be unique")
         if any(e < 0 for e in pinned):
             raise ValueError("pinned logical expert ids must be non-negative")
-        self.num_dynamic_slots = int(num_slots)
+        n = int(num_slots)
+        self.num_dynamic_slots = n
         self.pinned_logical_ids = pinned
-        self._pinned_slot = {e: int(num_slots) + i for i, e in enumerate(pinned)}
-        rows = int(num_slots) + len(pinned)
+        rows = n + len(pinned)
         self.w13_slots = torch.empty((rows, *w13_shape), dtype=dtype, device=device)
         self.w2_slots = torch.empty((rows, *w2_shape), dtype=dtype, device=device)
-        self.slots = [
-            ExpertSlot(slot_id=i, w13=self.w13_slots[i], w2=self.w2_slots[i]) for i in range(num_slots)
-        ]
-        self._resident: dict[ExpertKey, int] = {}
-        self._resident_by_expert_id: dict[int, int] = {}
+        # the slot table
+        self._state = np.zeros(n, dtype=np.int8)
+        self._owner = np.full(n, -1, dtype=np.int32)
+        self._owner_layer = np.full(n, -1, dtype=np.int64)
+        self._version = np.zeros(n, dtype=np.int64)
+        self._last_used = np.full(n, -1, dtype=np.int64)
+        self._slot_of = np.full(max(1, max(pinned, default=0) + 1), -1, dtype=np.int32)
+        self.slots = [ExpertSlot(self, i) for i in range(n)]
 
     # -- geometry ---------------------------------------------------------
     @property
@@ -109,7 +176,7 @@ class ExpertSlotBank:
 
     @property
     def pinned_slot_ids(self) -> tuple[int, ...]:
-        return tuple(self._pinned_slot[e] for e in self.pinned_logical_ids)
+        return tuple(range(self.num_dynamic_slots, self.num_dynamic_slots + len(self.pinned_logical_ids)))
 
     @property
     def dynamic_bytes(self) -> int:
@@ -118,36 +185,32 @@ class ExpertSlotBank:
 
     @property
     def pinned_bytes(self) -> int:
-        n = self.num_dynamic_slots
-        return _nbytes(self.w13_slots[n:]) + _nbytes(self.w2_slots[n:])
+        return self.total_bytes - self.dynamic_bytes
 
     @property
     def total_bytes(self) -> int:
         return _nbytes(self.w13_slots) + _nbytes(self.w2_slots)
 
     def pinned_slot_for_logical_id(self, logical_id: int) -> int | None:
-        return self._pinned_slot.get(int(logical_id))
+        try:
+            return self.num_dynamic_slots + self.pinned_logical_ids.index(int(logical_id))
+        except ValueError:
+            return None
 
     # -- pinned shared suffix --------------------------------------------
     def install_pinned_weights(self, w13: torch.Tensor, w2: torch.Tensor) -> None:
         """Copy the always-resident shared rows into the suffix."""
-        count = len(self.pinned_logical_ids)
-        if count == 0:
+        n_pin = len(self.pinned_logical_ids)
+        if n_pin == 0:
             if w13.numel() or w2.numel():
                 raise ValueError("cannot install pinned weights into a routed-only bank")
             return
-        exp13 = tuple(int(d) for d in self.w13_slots.shape[1:])
-        exp2 = tuple(int(d) for d in self.w2_slots.shape[1:])
-        if (
-            int(w13.shape[0]) != count
-            or tuple(int(d) for d in w13.shape[1:]) != exp13
-            or int(w2.shape[0]) != count
-            or tuple(int(d) for d in w2.shape[1:]) != exp2
-        ):
+        want13 = (n_pin, *self.w13_slots.shape[1:])
+        want2 = (n_pin, *self.w2_slots.shape[1:])
+        if tuple(w13.shape) != tuple(want13) or tuple(w2.shape) != tuple(want2):
             raise ValueError(
                 "pinned shared weight layout does not match slot bank: "
-                f"w13={tuple(w13.shape)} expected=({count}, {exp13}); "
-                f"w2={tuple(w2.shape)} expected=({count}, {exp2})"
+                f"w13={tuple(w13.shape)} expected={tuple(want13)}; w2={tuple(w2.shape)} expected={tuple(want2)}"
             )
         with torch.no_grad():
             self.w13_slots[self.num_dynamic_slots:].copy_(w13)
@@ -156,113 +219,174 @@ class ExpertSlotBank:
     def copy_pinned_weights_from(self, source: "ExpertSlotBank") -> None:
         if self.pinned_logical_ids != source.pinned_logical_ids:
             raise ValueError("cannot copy pinned weights across different logical layouts")
-        if not self.pinned_logical_ids:
-            return
-        with torch.no_grad():
-            self.w13_slots[self.num_dynamic_slots:].copy_(source.w13_slots[source.num_dynamic_slots:])
-            self.w2_slots[self.num_dynamic_slots:].copy_(source.w2_slots[source.num_dynamic_slots:])
+        if self.pinned_logical_ids:
+            with torch.no_grad():
+                self.w13_slots[self.num_dynamic_slots:].copy_(source.w13_slots[source.num_dynamic_slots:])
+                self.w2_slots[self.num_dynamic_slots:].copy_(source.w2_slots[source.num_dynamic_slots:])
 
     def install_pinned_log2phy(self, log2phy: torch.Tensor) -> None:
-        for logical_id, slot_id in self._pinned_slot.items():
-            if logical_id >= int(log2phy.numel()):
-                raise ValueError(
-                    f"log2phy does not cover pinned logical expert {logical_id}; size={int(log2phy.numel())}"
-                )
-            log2phy[logical_id] = slot_id
+        """Write the pinned suffix's entries of a slot table (one indexed write)."""
+        if not self.pinned_logical_ids:
+            return
+        ids = list(self.pinned_logical_ids)
+        too_big = [e for e in ids if e >= int(log2phy.numel())]
+        if too_big:
+            raise ValueError(f"log2phy does not cover pinned logical expert {too_big[0]}; size={int(log2phy.numel())}")
+        idx = torch.tensor(ids, dtype=torch.long)
+        val = torch.tensor(self.pinned_slot_ids, dtype=log2phy.dtype)
+        log2phy.index_put_((idx.to(log2phy.device),), val.to(log2phy.device))
 
-    # -- ownership ----------------------------------------------------------
-    def _take(self, slot: ExpertSlot, key: ExpertKey, step_id: int, *, index: bool) -> ExpertSlot:
-        if slot.expert_key is not None:
-            self._resident.pop(slot.expert_key, None)
-            self._resident_by_expert_id.pop(int(slot.expert_key.expert_id), None)
-        slot.expert_key = key
-        slot.state = SlotState.LOADING
-        slot.version += 1
-        slot.last_used_step = int(step_id)
-        if index:
-            self._resident[key] = slot.slot_id
-            self._resident_by_expert_id[int(key.expert_id)] = slot.slot_id
-        return slot
+    # -- slot table ------------------------------------------------------------
+    def _key_of(self, s: int) -> ExpertKey | None:
+        e = int(self._owner[s])
+        return None if e < 0 else ExpertKey(int(self._owner_layer[s]), e)
+
+    def _ensure_expert(self, e: int) -> None:
+        if e >= self._slot_of.size:
+            grown = np.full(max(e + 1, 2 * self._slot_of.size), -1, dtype=np.int32)
+            grown[: self._slot_of.size] = self._slot_of
+            self._slot_of = grown
+
+    def _resident_slot(self, key: ExpertKey) -> int:
+        e = int(key.expert_id)
+        if e < 0 or e >= self._slot_of.size:
+            return -1
+        s = int(self._slot_of[e])
+        if s < 0 or int(self._owner[s]) != e or int(self._owner_layer[s]) != int(key.layer_id):
+            return -1
+        return s
+
+    def _unindex(self, s: int) -> None:
+        e = int(self._owner[s])
+        if 0 <= e < self._slot_of.size and int(self._slot_of[e]) == s:
+            self._slot_of[e] = -1
+
+    def _claim(self, s: int, key: ExpertKey, step_id: int, *, indexed: bool) -> ExpertSlot:
+        self._unindex(s)
+        e = int(key.expert_id)
+        self._owner[s] = e
+        self._owner_layer[s] = int(key.layer_id)
+        self._state[s] = LOADING
+        self._version[s] += 1
+        self._last_used[s] = int(step_id)
+        if indexed:
+            self._ensure_expert(e)
+            self._slot_of[e] = s
+        return self.slots[s]
+
+    def _victim(self) -> int:
+        """Lowest-id EMPTY slot, else the READY slot of smallest (last use,
+        id); -1 when every slot is LOADING or COMPUTING."""
+        empty = np.flatnonzero(self._state == EMPTY)
+        if empty.size:
+            return int(empty[0])
+        ready = self._state == READY
+        if not ready.any():
+            return -1
+        return int(np.argmin(np.where(ready, self._last_used, np.iinfo(np.int64).max)))
 
     def allocate_for(self, expert_key: ExpertKey, *, step_id: int) -> ExpertSlot:
         """Touch a resident expert or reserve a slot for it (state LOADING)."""
-        resident = self._resident.get(expert_key)
-        if resident is not None:
-            slot = self.slots[resident]
-            slot.last_used_step = int(step_id)
-            return slot
-        slot = self._first_empty_slot() or self._lru_evictable_slot()
-        if slot is None:
+        s = self._resident_slot(expert_key)
+        if s >= 0:
+            self._last_used[s] = int(step_id)
+            return self.slots[s]
+        s = self._victim()
+        if s < 0:
             raise RuntimeError(f"no evictable expert slots; states={self.state_counts()}")
-        return self._take(slot, expert_key, step_id, index=True)
+        return self._claim(s, expert_key, step_id, indexed=True)
+
+    def plan(self, layer_id: int, expert_ids, *, step_id: int) -> tuple[int, np.ndarray, np.ndarray]:
+        """Hit / miss and slot reservation for a list of experts of one layer,
+        in one native call (lmoe_slot_plan).  Returns (status, slot ids,
+        miss flags): status >= 0 is the number of misses; -(j + 1) means
+        expert j needs in-flight work drained first (experts before j are
+        done; call again with the rest after draining)."""
+        ids = np.ascontiguousarray(expert_ids, dtype=np.int32)
+        n = int(ids.size)
+        if n and int(ids.max()) >= self._slot_of.size:
+            self._ensure_expert(int(ids.max()))
+        # residency by expert id serves one layer: entries of other layers'
+        # keys (test-only mixtures) are dropped from the index first
+        other = (self._owner >= 0) & (self._owner_layer != int(layer_id))
+        for s in np.flatnonzero(other):
+            self._unindex(int(s))
+        slot_ids = np.empty(n, dtype=np.int32)
+        miss = np.empty(n, dtype=np.int8)
+        st = _native_plan()(
+            self._state.ctypes.data, self._owner.ctypes.data, self._version.ctypes.data,
+            self._last_used.ctypes.data, self.num_dynamic_slots, self._slot_of.ctypes.data,
+            int(self._slot_of.size), ids.ctypes.data, n, int(step_id), slot_ids.ctypes.data, miss.ctypes.data,
+        )
+        if st >= 1000:
+            raise ValueError(f"slot planning refused the expert ids (status {st})")
+        done = n if st >= 0 else -st - 1
+        claimed = slot_ids[:done][miss[:done] == 1]
+        self._owner_layer[claimed] = int(layer_id)
+        return int(st), slot_ids, miss
 
     def assign_slot(self, slot_id: int, expert_key: ExpertKey, *, step_id: int) -> ExpertSlot:
         """Place expert_key in a given slot (moving it if resident elsewhere)."""
-        slot = self.slots[int(slot_id)]
-        self._require_reassignable(slot)
-        other = self._resident.get(expert_key)
-        if other is not None and other != int(slot_id):
-            old = self.slots[other]
-            old.expert_key = None
-            old.state = SlotState.EMPTY
-            self._resident.pop(expert_key, None)
-            self._resident_by_expert_id.pop(int(expert_key.expert_id), None)
-        if slot.expert_key == expert_key:
-            slot.version += 1
-            slot.last_used_step = int(step_id)
-            slot.state = SlotState.LOADING
-            self._resident[expert_key] = slot.slot_id
-            self._resident_by_expert_id[int(expert_key.expert_id)] = slot.slot_id
-            return slot
-        return self._take(slot, expert_key, step_id, index=True)
+        s = int(slot_id)
+        self._require_reassignable(s)
+        other = self._resident_slot(expert_key)
+        if other >= 0 and other != s:
+            self._unindex(other)
+            self._owner[other] = -1
+            self._owner_layer[other] = -1
+            self._state[other] = EMPTY
+        return self._claim(s, expert_key, step_id, indexed=True)
 
     def assign_transient_slot(self, slot_id: int, expert_key: ExpertKey, *, step_id: int) -> ExpertSlot:
         """Place expert_key in a stage-bank slot without indexing it."""
-        slot = self.slots[int(slot_id)]
-        self._require_reassignable(slot)
-        return self._take(slot, expert_key, step_id, index=False)
+        s = int(slot_id)
+        self._require_reassignable(s)
+        return self._claim(s, expert_key, step_id, indexed=False)
 
     def mark_ready(self, slot_id: int) -> None:
-        self.slots[int(slot_id)].state = SlotState.READY
+        self._state[int(slot_id)] = READY
 
     def mark_computing(self, slot_id: int) -> None:
-        self.slots[int(slot_id)].state = SlotState.COMPUTING
+        self._state[int(slot_id)] = COMPUTING
 
     def mark_released(self, slot_id: int) -> None:
-        self.slots[int(slot_id)].state = SlotState.EMPTY
+        self._state[int(slot_id)] = EMPTY
 
     def lookup(self, expert_key: ExpertKey) -> ExpertSlot | None:
-        i = self._resident.get(expert_key)
-        return None if i is None else self.slots[i]
+        s = self._resident_slot(expert_key)
+        return None if s < 0 else self.slots[s]
 
     def lookup_expert_id(self, expert_id: int) -> ExpertSlot | None:
-        i = self._resident_by_expert_id.get(int(expert_id))
-        return None if i is None else self.slots[i]
+        e = int(expert_id)
+        if e < 0 or e >= self._slot_of.size:
+            return None
+        s = int(self._slot_of[e])
+        return None if s < 0 or int(self._owner[s]) != e else self.slots[s]
 
     def clear_slot(self, slot_id: int, *, force: bool = False) -> None:
-        slot = self.slots[int(slot_id)]
-        if not force and slot.state == SlotState.COMPUTING:
-            raise RuntimeError(f"slot {slot.slot_id} is computing and cannot be reassigned")
-        if slot.expert_key is not None:
-            self._resident.pop(slot.expert_key, None)
-            self._resident_by_expert_id.pop(int(slot.expert_key.expert_id), None)
-        slot.expert_key = None
-        slot.state = SlotState.EMPTY
+        s = int(slot_id)
+        if not force and int(self._state[s]) == COMPUTING:
+            raise RuntimeError(f"slot {s} is computing and cannot be reassigned")
+        self._unindex(s)
+        self._owner[s] = -1
+        self._owner_layer[s] = -1
+        self._state[s] = EMPTY
 
     def state_counts(self) -> dict[str, int]:
-        counts = {s.value: 0 for s in SlotState}
-        for slot in self.slots:
-            counts[slot.state.value] += 1
-        return counts
+        counts = np.bincount(self._state, minlength=len(_CODES))
+        return {st.value: int(counts[i]) for i, st in enumerate(_CODES)}
 
-    def _first_empty_slot(self) -> ExpertSlot | None:
-        return next((s for s in self.slots if s.state == SlotState.EMPTY), None)
+    def has_inflight(self) -> bool:
+        """Any slot LOADING or COMPUTING."""
+        return bool(((self._state == LOADING) | (self._state == COMPUTING)).any())
 
-    def _lru_evictable_slot(self) -> ExpertSlot | None:
-        ready = [s for s in self.slots if s.state == SlotState.READY]
-        return min(ready, key=lambda s: (s.last_used_step, s.slot_id)) if ready else None
+    def owners(self) -> list[int | None]:
+        """Owning expert id of every physical slot (pinned suffix included)."""
+        out: list[int | None] = [int(e) if e >= 0 else None for e in self._owner.tolist()]
+        out.extend(int(e) for e in self.pinned_logical_ids)
+        return out
 
-    @staticmethod
-    def _require_reassignable(slot: ExpertSlot) -> None:
-        if slot.state in (SlotState.LOADING, SlotState.COMPUTING):
-            raise RuntimeError(f"slot {slot.slot_id} is {slot.state.value} and cannot be reassigned")
+    def _require_reassignable(self, s: int) -> None:
+        code = int(self._state[s])
+        if code in (LOADING, COMPUTING):
+            raise RuntimeError(f"slot {s} is {_CODES[code].value} and cannot be reassigned")

@@ -1,16 +1,26 @@
-"""Host-store -> slot transfers on a dedicated HIP transfer stream.
+"""Expert copies into slots on a dedicated transfer stream.
 
-A batch of expert loads becomes one lmoe_stage_copy call: hipMemcpyAsync per
-contiguous run (expert e, e+1, ... into slot s, s+1, ... is one copy per
-weight tensor) on the transfer stream, then one hipEvent.  The consumer
-(compute) stream waits on that event before the slots are published READY,
-so no kernel can read a slot whose bytes are still in flight.  Leases make a
-late completion for a slot that changed owner fail instead of publishing.
+A batch of loads becomes a list of byte ranges: consecutive loads whose
+host rows and slot rows are both back to back merge into one range per
+weight tensor.  The batch then goes to the device in one call:
 
-Reference: moe_offload/transfer_engine.py:29-342 (TransferReadyEvent lease
-validation and consumer wait :29-69; load_many_async :139-187; contiguous-run
-batching :205-342).  Slots on the CPU (host-only tests) take a synchronous
-copy, as the reference's CPU branch does.
+  * lmoe_stage_gather (default): one gather-copy kernel launch on the
+    transfer stream reads page-locked host rows (or device rows) and writes
+    the slots at the host link's rate, with no per-copy command overhead,
+    and writes the slot-table entries that publish the batch in the same
+    launch;
+  * lmoe_stage_copy: one hipMemcpyAsync per range, for sources the device
+    cannot read directly (pageable host memory), or when the gather entry
+    refuses a range.
+
+One event recorded after the batch orders it before its consumer (the
+compute stream waits on it before the slots are published READY).  A ready
+event carries the (slot, owner, version) of every slot it fills, so a late
+completion for a slot that changed owner fails instead of publishing.
+
+Reference: moe_offload/transfer_engine.py:29-342 (TransferReadyEvent and
+its checks and messages, load_many_async's arguments, contiguous batching);
+the reference copies with torch copy_ on its transfer stream.
 """
 
 from __future__ import annotations
@@ -23,6 +33,8 @@ from vllm_moe_offload_amd.moe_offload.host_store import ExpertWeightBundle
 from vllm_moe_offload_amd.moe_offload.layout import LayoutValidator
 from vllm_moe_offload_amd.moe_offload.slot_bank import ExpertSlot, SlotLease, SlotState
 
+Load = tuple[ExpertWeightBundle, ExpertSlot]
+
 
 @dataclass
 class TransferReadyEvent:
@@ -33,25 +45,7 @@ class TransferReadyEvent:
     completed: bool = False
     consumer_wait_installed: bool = False
 
-    def install_consumer_dependency(self, consumer_stream) -> None:
-        """Order the copies before consumer_stream, then publish READY."""
-        if self.completed:
-            return
-        self._validate_loading_leases()
-        if self.event is not None:
-            consumer_stream.wait_event(self.event)
-        self.consumer_wait_installed = True
-        self.mark_ready()
-
-    def mark_ready(self) -> None:
-        if self.completed:
-            return
-        self._validate_loading_leases()
-        for slot, _ in self.leases:
-            slot.state = SlotState.READY
-        self.completed = True
-
-    def _validate_loading_leases(self) -> None:
+    def _check_owners(self) -> None:
         for slot, lease in self.leases:
             if not slot.matches_lease(lease):
                 raise RuntimeError(
@@ -63,22 +57,67 @@ class TransferReadyEvent:
                     f"H2D completion for slot {slot.slot_id} requires loading state, found {slot.state.value}"
                 )
 
+    def install_consumer_dependency(self, consumer_stream) -> None:
+        """The consumer stream waits for the batch, then its slots are READY."""
+        if self.completed:
+            return
+        self._check_owners()
+        if self.event is not None:
+            consumer_stream.wait_event(self.event)
+        self.consumer_wait_installed = True
+        self.mark_ready()
 
-Load = tuple[ExpertWeightBundle, ExpertSlot]
+    def mark_ready(self) -> None:
+        if self.completed:
+            return
+        self._check_owners()
+        for slot, _ in self.leases:
+            slot.state = SlotState.READY
+        self.completed = True
+
+
+def _span(t: torch.Tensor) -> tuple[int, int]:
+    return int(t.data_ptr()), int(t.numel()) * int(t.element_size())
+
+
+def contiguous_load_runs(loads) -> tuple[tuple[Load, ...], ...]:
+    """Group loads into runs whose host bytes and slot bytes are both back to
+    back, for w13 and for w2 (each run is then one range per tensor)."""
+    runs: list[list[Load]] = []
+    ends = None  # (host w13 end, host w2 end, slot w13 end, slot w2 end) of the open run
+    for bundle, slot in loads:
+        spans = (_span(bundle.w13), _span(bundle.w2), _span(slot.w13), _span(slot.w2))
+        dense = all(t.is_contiguous() for t in (bundle.w13, bundle.w2, slot.w13, slot.w2))
+        starts = tuple(p for p, _ in spans)
+        if runs and dense and ends == starts and bundle.w13.device == runs[-1][-1][0].w13.device:
+            runs[-1].append((bundle, slot))
+        else:
+            runs.append([(bundle, slot)])
+        ends = tuple(p + n for p, n in spans) if dense else None
+    return tuple(tuple(r) for r in runs)
+
+
+def copy_ranges(loads) -> list[tuple[int, int, int]]:
+    """(dst, src, bytes) per weight tensor per contiguous run."""
+    out = []
+    for run in contiguous_load_runs(loads):
+        b0, s0 = run[0]
+        for src, dst in ((b0.w13, s0.w13), (b0.w2, s0.w2)):
+            out.append((int(dst.data_ptr()), int(src.data_ptr()), _span(src)[1] * len(run)))
+    return out
 
 
 class TransferEngine:
     def __init__(self) -> None:
-        self._h2d_stream: torch.cuda.Stream | None = None
-        self._pending_ready_events: list[TransferReadyEvent] = []
+        self._stream: torch.cuda.Stream | None = None
+        self._in_flight: list[TransferReadyEvent] = []
         self.bytes_issued = 0
         self.copies_issued = 0
+        self.batches_gathered = 0  # batches the gather kernel carried
 
-    # -- synchronous --------------------------------------------------------
+    # -- synchronous -------------------------------------------------------
     def load_sync(self, bundle: ExpertWeightBundle, slot: ExpertSlot) -> None:
-        LayoutValidator.validate_copy_compatible(bundle, slot.as_bundle())
-        self._copy(((bundle, slot),), stream=None)
-        slot.state = SlotState.READY
+        self.load_many_sync([(bundle, slot)])
 
     def load_many_sync(self, loads: list[Load], *, validate_layout: bool = True) -> None:
         if not loads:
@@ -88,11 +127,16 @@ class TransferEngine:
                 LayoutValidator.validate_copy_compatible(bundle, slot.as_bundle())
         for _, slot in loads:
             slot.state = SlotState.LOADING
-        self._copy(tuple(loads), stream=None)
+        for run in contiguous_load_runs(loads):
+            for bundle, slot in run:
+                slot.w13.copy_(bundle.w13)
+                slot.w2.copy_(bundle.w2)
         for _, slot in loads:
             slot.state = SlotState.READY
+        self.copies_issued += 2 * len(loads)
+        self.bytes_issued += sum(b.nbytes for b, _ in loads)
 
-    # -- asynchronous -------------------------------------------------------
+    # -- asynchronous ------------------------------------------------------
     def load_async(self, bundle: ExpertWeightBundle, slot: ExpertSlot, *, wait_event=None,
                    record_event: bool = True):
         return self.load_many_async([(bundle, slot)], wait_event=wait_event, record_event=record_event)
@@ -100,28 +144,28 @@ class TransferEngine:
     def load_many_async(self, loads: list[Load], *, wait_event=None, record_event: bool = True,
                         validate_layout: bool = True, table_update=None):
         """Queue the loads on the transfer stream; returns a TransferReadyEvent
-        (or None when the copy completed synchronously).  table_update =
-        (device int32 table, indices, values) is written on the transfer
-        stream after the copies, before the ready event (device slots only)."""
+        (None when the copy completed synchronously).  table_update =
+        (device int32 table, indices, values[, fill]) is written by the same
+        batch, before its ready event (device slots only); fill=True writes
+        -1 into every other entry."""
         if not loads:
             return None
         if validate_layout:
             for bundle, slot in loads:
                 LayoutValidator.validate_copy_compatible(bundle, slot.as_bundle())
-        if all(slot.w13.device.type == "cpu" and slot.w2.device.type == "cpu" for _, slot in loads):
+        if all(slot.w13.device.type == "cpu" for _, slot in loads):
             _host_wait(wait_event)
-            for _, slot in loads:
-                slot.state = SlotState.LOADING
-            self._copy(tuple(loads), stream=None)
-            for _, slot in loads:
-                slot.state = SlotState.READY
+            self.load_many_sync(loads, validate_layout=False)
             return None
-        stream = self._get_h2d_stream(loads[0][1].w13.device)
+        stream = self._transfer_stream(loads[0][1].w13.device)
         for _, slot in loads:
             slot.state = SlotState.LOADING
         done = torch.cuda.Event() if record_event else None
-        self._copy(tuple(loads), stream=stream, wait_event=_torch_event(wait_event), done_event=done,
-                   table_update=table_update)
+        ranges = copy_ranges(loads)
+        self._issue(ranges, stream, _torch_event(wait_event), done, table_update,
+                    direct=all(b.host_pinned or b.w13.device.type == "cuda" for b, _ in loads))
+        self.copies_issued += len(ranges)
+        self.bytes_issued += sum(r[2] for r in ranges)
         slots = tuple(slot for _, slot in loads)
         if done is None:
             stream.synchronize()
@@ -129,55 +173,40 @@ class TransferEngine:
                 slot.state = SlotState.READY
             return None
         ready = TransferReadyEvent(done, tuple((s, s.lease()) for s in slots))
-        self._pending_ready_events.append(ready)
+        self._in_flight.append(ready)
         return ready
+
+    def _issue(self, ranges, stream, wait_event, done, table_update, *, direct: bool) -> None:
+        from vllm_moe_offload_amd import native
+
+        if wait_event is not None:
+            stream.wait_event(wait_event)
+        if direct and native.stage_gather(ranges, stream, table_update=table_update):
+            self.batches_gathered += 1
+        else:
+            native.stage_copy(ranges, stream, table_update=table_update)
+        if done is not None:
+            done.record(stream)
 
     def synchronize(self) -> None:
         """Wait for every queued copy and publish its slots READY."""
-        if self._h2d_stream is not None:
-            self._h2d_stream.synchronize()
-        pending, self._pending_ready_events = self._pending_ready_events, []
-        for ready in pending:
+        if self._stream is not None:
+            self._stream.synchronize()
+        in_flight, self._in_flight = self._in_flight, []
+        for ready in in_flight:
             ready.mark_ready()
 
     @property
     def stream(self) -> torch.cuda.Stream | None:
-        return self._h2d_stream
+        return self._stream
 
-    def _get_h2d_stream(self, device) -> torch.cuda.Stream:
-        if self._h2d_stream is None:
-            self._h2d_stream = torch.cuda.Stream(device=device)  # default priority
-        return self._h2d_stream
-
-    # -- copies -----------------------------------------------------------
-    def _copy(self, loads: tuple[Load, ...], *, stream, wait_event=None, done_event=None,
-              table_update=None) -> None:
-        runs = contiguous_load_runs(loads)
-        if stream is None:
-            for run in runs:
-                for bundle, slot in run:
-                    slot.w13.copy_(bundle.w13)
-                    slot.w2.copy_(bundle.w2)
-            return
-        from vllm_moe_offload_amd import native
-
-        copies: list[tuple[int, int, int]] = []
-        for run in runs:
-            b0, s0 = run[0]
-            n = len(run)
-            for name in ("w13", "w2"):
-                src, dst = getattr(b0, name), getattr(s0, name)
-                nbytes = int(src.numel()) * int(src.element_size()) * n
-                copies.append((int(dst.data_ptr()), int(src.data_ptr()), nbytes))
-        native.stage_copy(copies, stream, wait_event=wait_event, done_event=done_event,
-                          table_update=table_update)
-        self.copies_issued += len(copies)
-        self.bytes_issued += sum(c[2] for c in copies)
+    def _transfer_stream(self, device) -> torch.cuda.Stream:
+        if self._stream is None:
+            self._stream = torch.cuda.Stream(device=device)  # default priority
+        return self._stream
 
 
 def _host_wait(wait_event) -> None:
-    if wait_event is None:
-        return
     ev = getattr(wait_event, "event", wait_event)
     sync = getattr(ev, "synchronize", None)
     if callable(sync):
@@ -185,39 +214,5 @@ def _host_wait(wait_event) -> None:
 
 
 def _torch_event(wait_event):
-    if wait_event is None:
-        return None
     ev = getattr(wait_event, "event", wait_event)
     return ev if isinstance(ev, torch.cuda.Event) else None
-
-
-def _next_contiguous(prev: torch.Tensor, cur: torch.Tensor) -> bool:
-    if cur.device != prev.device or cur.dtype != prev.dtype:
-        return False
-    if tuple(cur.shape) != tuple(prev.shape) or tuple(cur.stride()) != tuple(prev.stride()):
-        return False
-    if not prev.is_contiguous():
-        return False
-    return int(cur.data_ptr()) - int(prev.data_ptr()) == int(prev.numel()) * int(prev.element_size())
-
-
-def contiguous_load_runs(loads: tuple[Load, ...]) -> tuple[tuple[Load, ...], ...]:
-    """Split loads into runs of consecutive experts landing in consecutive
-    slots whose host and device bytes are both back to back."""
-    runs: list[list[Load]] = []
-    for bundle, slot in loads:
-        if runs:
-            pb, ps = runs[-1][-1]
-            if (
-                int(bundle.layer_id) == int(pb.layer_id)
-                and int(bundle.expert_id) == int(pb.expert_id) + 1
-                and int(slot.slot_id) == int(ps.slot_id) + 1
-                and _next_contiguous(pb.w13, bundle.w13)
-                and _next_contiguous(pb.w2, bundle.w2)
-                and _next_contiguous(ps.w13, slot.w13)
-                and _next_contiguous(ps.w2, slot.w2)
-            ):
-                runs[-1].append((bundle, slot))
-                continue
-        runs.append([(bundle, slot)])
-    return tuple(tuple(r) for r in runs)

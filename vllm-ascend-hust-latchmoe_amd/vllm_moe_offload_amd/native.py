@@ -24,6 +24,7 @@ LMOE_SCORING_SIGMOID = 1
 LMOE_PATH_AUTO = 0
 LMOE_PATH_GEMV = 1
 LMOE_PATH_MFMA = 2
+LMOE_ERR_ARG = 1000
 LMOE_ERR_SHAPE = 1001
 META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
 META_COUNT = 4
@@ -50,7 +51,9 @@ EXPORTED_SYMBOLS = (
     "lmoe_fused_moe_decode_noalloc",
     "lmoe_down_combine",
     "lmoe_stage_copy",
+    "lmoe_stage_gather",
     "lmoe_table_update",
+    "lmoe_slot_plan",
 )
 
 _vp = ctypes.c_void_p
@@ -103,6 +106,8 @@ _SIGNATURES = {
     ),
     "lmoe_down_combine": (_i, [_vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "lmoe_stage_copy": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
+    "lmoe_stage_gather": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "lmoe_slot_plan": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, ctypes.c_int64, _vp, _vp]),
     "lmoe_table_update": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
 }
 
@@ -789,22 +794,29 @@ def down_combine(
 # ---------------------------------------------------------------------------
 # staging
 # ---------------------------------------------------------------------------
+def _table_pairs(table_update):
+    """(table, idx tuple, val tuple, fill) of a table_update argument."""
+    table, idx, val = table_update[:3]
+    fill = bool(table_update[3]) if len(table_update) > 3 else False
+    return table, tuple(int(i) for i in idx), tuple(int(v) for v in val), fill
+
+
 def stage_copy(
     copies: list[tuple[int, int, int]],
     transfer_stream: torch.cuda.Stream,
     *,
     wait_event: torch.cuda.Event | None = None,
     done_event: torch.cuda.Event | None = None,
-    table_update: tuple[torch.Tensor, tuple, tuple] | None = None,
+    table_update: tuple | None = None,
 ) -> None:
-    """Queue (dst_ptr, src_ptr, nbytes) copies on transfer_stream.
+    """Queue (dst_ptr, src_ptr, nbytes) copies on transfer_stream with one
+    hipMemcpyAsync each (any host memory, pageable included).
 
     The stream first waits for wait_event (slot release) and done_event is
     recorded after the batch; both are torch events, ordered through torch so
     their lazily created handles stay valid.  table_update = (table,
-    indices, values) writes those int32 entries after the copies, inside the
-    same done_event (the slot table that publishes the staged experts).
-    """
+    indices, values[, fill]) writes those int32 entries after the copies
+    (fill: every other entry becomes -1), inside the same done_event."""
     lib = load_library()
     if wait_event is not None:
         transfer_stream.wait_event(wait_event)
@@ -817,10 +829,48 @@ def stage_copy(
         "lmoe_stage_copy",
     )
     if table_update is not None:
-        table, idx, val = table_update
+        table, idx, val, fill = _table_pairs(table_update)
+        if fill:
+            full = dict.fromkeys(range(int(table.numel())), -1)
+            full.update(zip(idx, val))
+            idx, val = tuple(full), tuple(full.values())
         table_update_entries(table, idx, val, stream=transfer_stream)
     if done_event is not None:
         done_event.record(transfer_stream)
+
+
+def stage_gather(
+    copies: list[tuple[int, int, int]],
+    transfer_stream: torch.cuda.Stream,
+    *,
+    table_update: tuple | None = None,
+) -> bool:
+    """Queue (dst_ptr, src_ptr, nbytes) copies as gather-copy kernel launches
+    on transfer_stream, with the table_update = (table, indices, values[,
+    fill]) entries written by the same launch.  Sources must be page-locked
+    host memory or device memory; the library checks every range and refuses
+    (returns False, nothing queued) what the device cannot read or what is
+    not 16-byte aligned, so the caller can take stage_copy."""
+    lib = load_library()
+    n = len(copies)
+    dst = (ctypes.c_void_p * max(n, 1))(*[c[0] for c in copies])
+    src = (ctypes.c_void_p * max(n, 1))(*[c[1] for c in copies])
+    nbytes = (ctypes.c_size_t * max(n, 1))(*[c[2] for c in copies])
+    table = None
+    n_table = n_tab = fill = 0
+    ia = va = None
+    if table_update is not None:
+        table, idx, val, fill_b = _table_pairs(table_update)
+        _need(table, "table", torch.int32)
+        n_table, n_tab, fill = int(table.numel()), len(idx), int(fill_b)
+        ia = (ctypes.c_int32 * max(n_tab, 1))(*idx)
+        va = (ctypes.c_int32 * max(n_tab, 1))(*val)
+    status = lib.lmoe_stage_gather(dst, src, nbytes, n, _ptr(table), n_table, ia, va, n_tab, fill,
+                                   int(transfer_stream.cuda_stream), None, None)
+    if status in (LMOE_ERR_ARG, LMOE_ERR_SHAPE):
+        return False
+    _check(status, "lmoe_stage_gather")
+    return True
 
 
 def table_update_entries(table: torch.Tensor, idx, val, *, stream=None) -> None:
