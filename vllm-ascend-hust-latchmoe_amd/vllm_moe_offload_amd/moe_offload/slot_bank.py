@@ -168,6 +168,13 @@ class ExpertSlotBank:
         self._last_used = np.full(n, -1, dtype=np.int64)
         self._slot_of = np.full(max(1, max(pinned, default=0) + 1), -1, dtype=np.int32)
         self.slots = [ExpertSlot(self, i) for i in range(n)]
+        # planner scratch (one staging at a time) and the table's addresses
+        self._plan_ids = np.empty(n, dtype=np.int32)
+        self._plan_slots = np.empty(n, dtype=np.int32)
+        self._plan_miss = np.empty(n, dtype=np.int8)
+        self._mixed_layers = False  # keys of more than one layer held (tests)
+        self._layer_seen = -1
+        self._addr = None
 
     # -- geometry ---------------------------------------------------------
     @property
@@ -246,6 +253,14 @@ class ExpertSlotBank:
             grown = np.full(max(e + 1, 2 * self._slot_of.size), -1, dtype=np.int32)
             grown[: self._slot_of.size] = self._slot_of
             self._slot_of = grown
+            self._addr = None
+
+    def _addresses(self) -> tuple[int, ...]:
+        if self._addr is None:
+            arrs = (self._state, self._owner, self._version, self._last_used, self._slot_of,
+                    self._plan_ids, self._plan_slots, self._plan_miss)
+            self._addr = tuple(int(a.__array_interface__["data"][0]) for a in arrs)
+        return self._addr
 
     def _resident_slot(self, key: ExpertKey) -> int:
         e = int(key.expert_id)
@@ -264,6 +279,9 @@ class ExpertSlotBank:
     def _claim(self, s: int, key: ExpertKey, step_id: int, *, indexed: bool) -> ExpertSlot:
         self._unindex(s)
         e = int(key.expert_id)
+        if self._layer_seen not in (-1, int(key.layer_id)):
+            self._mixed_layers = True
+        self._layer_seen = int(key.layer_id)
         self._owner[s] = e
         self._owner_layer[s] = int(key.layer_id)
         self._state[s] = LOADING
@@ -302,27 +320,30 @@ class ExpertSlotBank:
         miss flags): status >= 0 is the number of misses; -(j + 1) means
         expert j needs in-flight work drained first (experts before j are
         done; call again with the rest after draining)."""
-        ids = np.ascontiguousarray(expert_ids, dtype=np.int32)
-        n = int(ids.size)
+        n = len(expert_ids)
+        if n > self.num_dynamic_slots:
+            raise ValueError(f"{n} experts to plan exceed num_slots={self.num_dynamic_slots}")
+        ids = self._plan_ids[:n]
+        ids[:] = expert_ids
         if n and int(ids.max()) >= self._slot_of.size:
             self._ensure_expert(int(ids.max()))
-        # residency by expert id serves one layer: entries of other layers'
-        # keys (test-only mixtures) are dropped from the index first
-        other = (self._owner >= 0) & (self._owner_layer != int(layer_id))
-        for s in np.flatnonzero(other):
-            self._unindex(int(s))
-        slot_ids = np.empty(n, dtype=np.int32)
-        miss = np.empty(n, dtype=np.int8)
-        st = _native_plan()(
-            self._state.ctypes.data, self._owner.ctypes.data, self._version.ctypes.data,
-            self._last_used.ctypes.data, self.num_dynamic_slots, self._slot_of.ctypes.data,
-            int(self._slot_of.size), ids.ctypes.data, n, int(step_id), slot_ids.ctypes.data, miss.ctypes.data,
-        )
+        layer_id = int(layer_id)
+        if self._mixed_layers or self._layer_seen not in (-1, layer_id):
+            # residency by expert id serves one layer: entries of other
+            # layers' keys (test-only mixtures) leave the index first
+            for s in np.flatnonzero((self._owner >= 0) & (self._owner_layer != layer_id)):
+                self._unindex(int(s))
+            self._mixed_layers = False
+        a = self._addresses()
+        st = _native_plan()(a[0], a[1], a[2], a[3], self.num_dynamic_slots, a[4], int(self._slot_of.size),
+                            a[5], n, int(step_id), a[6], a[7])
         if st >= 1000:
             raise ValueError(f"slot planning refused the expert ids (status {st})")
+        slot_ids = self._plan_slots[:n].copy()
+        miss = self._plan_miss[:n].copy()
         done = n if st >= 0 else -st - 1
-        claimed = slot_ids[:done][miss[:done] == 1]
-        self._owner_layer[claimed] = int(layer_id)
+        self._owner_layer[slot_ids[:done][miss[:done] == 1]] = layer_id
+        self._layer_seen = layer_id
         return int(st), slot_ids, miss
 
     def assign_slot(self, slot_id: int, expert_key: ExpertKey, *, step_id: int) -> ExpertSlot:
