@@ -317,3 +317,52 @@ def test_moe_mlp_shared_tuple_with_wide_separate_shared_expert(T):
     assert err_r <= OUT_TOL and err_s <= OUT_TOL and err_t <= OUT_TOL
     with pytest.raises(RuntimeError, match="moe_mlp_shared"):
         torch.ops.vllm.moe_mlp(dx, logits, w, ids, None, None, name)
+
+
+def test_installed_comm_hook_runs_the_slot_bank_kernels(monkeypatch):
+    """The fused-experts hook installed on a MoECommMethod class: an
+    offloaded layer's call swaps in the slot bank, runs the gfx950 kernels and
+    returns the result contract (routed_out within tolerance of the oracle,
+    per-slot token counts, the three events)."""
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    from types import SimpleNamespace
+
+    from vllm_moe_offload_amd.moe_offload import runtime as runtime_mod
+    from vllm_moe_offload_amd.patches import patch_fused_moe as pfm
+
+    rng = np.random.default_rng(61)
+    E, H, I, k, T, slots = 64, 1024, 256, 4, 5, 32
+    w13, w2, wg = _weights(rng, E, H, I)
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True,
+                     graph_compatible_offload=True))
+    monkeypatch.setattr(runtime_mod, "_runtime", rt)
+    tb = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+    layer = SlotMoELayer(layer_id=60, runtime=rt, gate_weight=to_dev_bf16(wg), w13_weight=tb(w13),
+                         w2_weight=tb(w2), top_k=k)
+    layer.register()
+    x = normal_bf16(rng, (T, H), 1.0)
+    dx = to_dev_bf16(x)
+    w, ids, _ = fused_moe.route(dx, layer.gate_weight, layer.router_spec)
+    layer.stage(ids)
+
+    class Comm:
+        def fused_experts(self, inp):
+            raise AssertionError("the offloaded layer must not reach the original method")
+
+        def _maybe_apply_moe_offload_plan(self, inp):
+            return inp
+
+    assert pfm._patch_moe_comm_method_runtime_hooks(SimpleNamespace(MoECommMethod=Comm))
+    inp = fused_moe.MoEFusedExpertsInput(
+        hidden_states=dx, topk_weights=w, topk_ids=ids,
+        offload=fused_moe.MoEOffloadParams(enabled=True, layer_id=60, num_logical_experts=E))
+    res = Comm().fused_experts(inp)
+    torch.cuda.synchronize()
+    ref = _oracle_layer(x, ids.cpu().numpy(), from_dev_bf16(w), w13, w2)
+    err = rel_max_err(bf16_to_f32(from_dev_bf16(res.routed_out)), ref)
+    print(f"hooked fused_experts err {err:.3e}", flush=True)
+    assert err <= OUT_TOL
+    assert int(res.expert_tokens.sum().item()) == T * k and res.group_list_type == 1
+    assert all(isinstance(e, torch.cuda.Event) for e in (res.before_dispatch_evt, res.before_gmm2_evt,
+                                                            res.before_combine_evt))
+    assert all(s.state.value == "ready" for s in rt.slot_bank(60).slots if s.expert_key is not None)

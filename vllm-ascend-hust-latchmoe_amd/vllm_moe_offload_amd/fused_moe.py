@@ -146,6 +146,14 @@ def fused_experts(
     I <= 4096) and the combine.  topk_ids come from the caller, so a token
     may name one expert twice: the decode body takes its general form,
     which holds no one-pair-per-slot assumption."""
+    return _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2phy, add=add, out=out,
+                             path=path, workspace=workspace)[0]
+
+
+def _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2phy, *, add=None, out=None,
+                      path=native.LMOE_PATH_AUTO, workspace=None, events=None):
+    """fused_experts returning (out, workspace); events = three torch events
+    recorded before the permutation, before GMM2 and before the combine."""
     T, H = hidden.shape
     k = int(topk_ids.shape[1])
     P = int(w13_slots.shape[0])
@@ -156,14 +164,24 @@ def fused_experts(
         path = native.LMOE_PATH_MFMA
     decode = T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA
     bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P, H, I, hidden.device, n_pairs=T * k)
+    if events:
+        events[0].record()
     native.permute(topk_ids, ws.perm, log2phy=log2phy, block_m=bm)
     if decode:
+        if events:  # the decode body fuses GMM2 with the combine
+            events[1].record()
+            events[2].record()
         native.fused_moe_decode(hidden, topk_weights, w13_slots, w2_slots, ws.perm, ws.act[: T * k], dst, add=add,
                                 y=ws.y[: T * k], distinct_slots=False)
     else:
-        native.grouped_mlp(hidden, k, w13_slots, w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
+        native.gateup_silu(hidden, k, w13_slots, ws.perm, ws.act[: T * k], path=path)
+        if events:
+            events[1].record()
+        native.down(ws.act[: T * k], w2_slots, ws.perm, ws.y[: T * k], path=path)
+        if events:
+            events[2].record()
         native.combine(ws.y[: T * k], topk_weights, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
-    return dst
+    return dst, ws
 
 
 # Up to this many tokens the decode router runs as one launch (gate,
@@ -241,24 +259,43 @@ def check_placed(ws: MoEWorkspace) -> None:
 # ---------------------------------------------------------------------------
 # the fused-experts extension hook
 # ---------------------------------------------------------------------------
+# The contract types of the hook, with every field the reference threads
+# through it (patch_fused_moe.py:2051-2099 input, :3462-3470 result).  When
+# vLLM provides its own classes the installer in patches/patch_fused_moe.py
+# uses those; these stand in for them otherwise.
 @dataclass
 class MoEWeights:
-    w1: torch.Tensor
-    w2: torch.Tensor
+    w1: torch.Tensor | None = None
+    w2: torch.Tensor | None = None
+    w1_bias: torch.Tensor | None = None
+    w2_bias: torch.Tensor | None = None
+    w1_scale: torch.Tensor | None = None
+    w2_scale: torch.Tensor | None = None
+    w1_scale_bias: torch.Tensor | None = None
+    w2_scale_bias: torch.Tensor | None = None
+    w1_offset: torch.Tensor | None = None
+    w2_offset: torch.Tensor | None = None
 
 
 @dataclass
 class MoERoutingParams:
+    expert_map: torch.Tensor | None = None
+    global_redundant_expert_num: int = 0
+    mc2_mask: torch.Tensor | None = None
+    apply_router_weight_on_input: bool = False
     log2phy: torch.Tensor | None = None
     physical_expert_count: int | None = None
+    pertoken_scale: torch.Tensor | None = None
 
 
 @dataclass
 class MoEOffloadParams:
     enabled: bool = False
+    profile_only: bool = False
     layer_id: int = -1
     num_logical_experts: int = 0
     expected_device_type: str = "cuda"
+    step_id: int = -1
 
 
 @dataclass
@@ -266,58 +303,152 @@ class MoEFusedExpertsInput:
     hidden_states: torch.Tensor
     topk_weights: torch.Tensor
     topk_ids: torch.Tensor
-    weights: MoEWeights
+    weights: MoEWeights = field(default_factory=MoEWeights)
     routing: MoERoutingParams = field(default_factory=MoERoutingParams)
+    quant: object | None = None
+    activation: str | None = "silu"
+    need_trans: bool = False
+    dynamic_eplb: bool = False
+    swiglu_limit: float | None = None
     offload: MoEOffloadParams = field(default_factory=MoEOffloadParams)
+    # resident shared-expert output added before the final rounding (this
+    # build's seam; vLLM's runner adds it itself)
     shared_output: torch.Tensor | None = None
 
 
 @dataclass
 class FusedExpertsResult:
     routed_out: torch.Tensor
+    before_dispatch_evt: object | None = None
+    before_gmm2_evt: object | None = None
+    before_combine_evt: object | None = None
     group_list_type: int = 1
     expert_tokens: torch.Tensor | None = None
+    swiglu_limit: float | None = None
+
+
+def check_supported_input(inp) -> None:
+    """Fail closed on the parts of the contract the gfx950 kernels do not
+    implement (bf16 SwiGLU experts on one GPU)."""
+    if getattr(inp, "quant", None) not in (None, False):
+        raise RuntimeError("slot-bank fused experts run bf16 weights only; quantized experts are not supported")
+    act = getattr(inp, "activation", None)
+    if act not in (None, "silu", "swiglu", "SiluAndMul"):
+        raise RuntimeError(f"slot-bank fused experts implement SwiGLU only, got activation={act!r}")
+    if getattr(inp, "swiglu_limit", None) is not None:
+        raise RuntimeError("slot-bank fused experts do not clamp SwiGLU (swiglu_limit must be None)")
+    if bool(getattr(inp, "need_trans", False)):
+        raise RuntimeError("slot banks hold checkpoint layout ([P, 2I, H] / [P, H, I]); need_trans must be False")
+    routing = getattr(inp, "routing", None)
+    if routing is not None:
+        if bool(getattr(routing, "apply_router_weight_on_input", False)):
+            raise RuntimeError("apply_router_weight_on_input is not supported by the slot-bank combine")
+        if getattr(routing, "expert_map", None) is not None:
+            raise RuntimeError("expert_map (expert parallelism) is not supported on one GPU")
+
+
+def run_fused_experts_contract(inp, *, result_cls=FusedExpertsResult, record_events: bool = False):
+    """The hook's body: experts over the input's weights (a slot bank with
+    its log2phy when prepared), returning the result contract with the
+    per-slot token counts (group_list_type 1) and, if asked for, the events
+    before dispatch (permutation), before GMM2 and before the combine."""
+    check_supported_input(inp)
+    hidden, w, ids = inp.hidden_states, inp.topk_weights, inp.topk_ids
+    routing = getattr(inp, "routing", None)
+    log2phy = getattr(routing, "log2phy", None) if routing is not None else None
+    w1, w2 = inp.weights.w1, inp.weights.w2
+    if w.dtype != torch.bfloat16:
+        w = w.to(torch.bfloat16)
+    if ids.dtype != torch.int32:
+        ids = ids.to(torch.int32)
+    evts = [torch.cuda.Event() for _ in range(3)] if record_events else None
+    out, ws = _fused_experts_ws(hidden, w, ids.contiguous(), w1, w2, log2phy,
+                                add=getattr(inp, "shared_output", None), events=evts)
+    P = int(w1.shape[0])
+    return result_cls(
+        routed_out=out,
+        before_dispatch_evt=evts[0] if evts else None,
+        before_gmm2_evt=evts[1] if evts else None,
+        before_combine_evt=evts[2] if evts else None,
+        group_list_type=1,
+        expert_tokens=ws.perm.counts[:P],
+        swiglu_limit=getattr(inp, "swiglu_limit", None),
+    )
 
 
 class MoECommMethod:
-    """World-size-1 fused-experts method over the slot bank."""
+    """World-size-1 fused-experts method over the slot bank (the contract the
+    vLLM seam calls: fused_experts, _maybe_apply_moe_offload_plan)."""
 
     def __init__(self, runtime: MoeOffloadRuntime) -> None:
         self.runtime = runtime
         self._slot_compute_handle = None
 
-    def _with_prepared_slot_weights(self, inp: MoEFusedExpertsInput, prepared: PreparedSlotWeights) -> MoEFusedExpertsInput:
+    def _with_prepared_slot_weights(self, inp, prepared: PreparedSlotWeights, *, offload_enabled=None,
+                                    use_log2phy: bool = True):
         self._slot_compute_handle = self.runtime.begin_slot_compute(prepared)
-        return MoEFusedExpertsInput(
-            hidden_states=inp.hidden_states,
-            topk_weights=inp.topk_weights,
-            topk_ids=inp.topk_ids,
-            weights=MoEWeights(prepared.w1, prepared.w2),
-            routing=MoERoutingParams(prepared.log2phy, prepared.physical_expert_count),
-            offload=inp.offload,
-            shared_output=inp.shared_output,
-        )
+        return with_slot_weights(inp, prepared, offload_enabled=offload_enabled, use_log2phy=use_log2phy)
 
-    def _maybe_apply_moe_offload_plan(self, inp: MoEFusedExpertsInput) -> MoEFusedExpertsInput:
-        if not inp.offload.enabled:
+    def _maybe_apply_moe_offload_plan(self, inp):
+        off = getattr(inp, "offload", None)
+        if off is None or not off.enabled:
             return inp
-        prepared = self.runtime.capture_safe_slot_weights(layer_id=int(inp.offload.layer_id))
+        prepared = self.runtime.capture_safe_slot_weights(layer_id=int(off.layer_id))
         if prepared is None:
-            raise RuntimeError(f"fixed-slot MoE layer {inp.offload.layer_id} is not registered")
-        prepared.validate_backend_ready(expected_device_type=inp.offload.expected_device_type)
+            raise RuntimeError(f"fixed-slot MoE layer {off.layer_id} is not registered")
+        prepared.validate_backend_ready(expected_device_type=off.expected_device_type)
         return self._with_prepared_slot_weights(inp, prepared)
 
-    def fused_experts(self, inp: MoEFusedExpertsInput) -> FusedExpertsResult:
+    def fused_experts(self, inp) -> FusedExpertsResult:
         inp = self._maybe_apply_moe_offload_plan(inp)
         try:
-            out = fused_experts(
-                inp.hidden_states, inp.topk_weights, inp.topk_ids, inp.weights.w1, inp.weights.w2,
-                inp.routing.log2phy, add=inp.shared_output,
-            )
+            return run_fused_experts_contract(inp)
         finally:
             self.runtime.end_slot_compute(self._slot_compute_handle)
             self._slot_compute_handle = None
-        return FusedExpertsResult(routed_out=out)
+
+
+def with_slot_weights(inp, prepared: PreparedSlotWeights, *, offload_enabled=None, use_log2phy: bool = True,
+                      contracts=None):
+    """A copy of a fused-experts input whose weights are the slot bank and
+    whose routing carries its log2phy and physical expert count; every other
+    field is carried over unchanged (patch_fused_moe.py:2039-2099).
+    contracts = (input, weights, routing, offload) classes to build with
+    (vLLM's own when the seam provides them)."""
+    in_cls, w_cls, r_cls, o_cls = contracts or (MoEFusedExpertsInput, MoEWeights, MoERoutingParams,
+                                                MoEOffloadParams)
+    src_w, src_r, src_o = inp.weights, getattr(inp, "routing", None), inp.offload
+    g = lambda obj, name, default=None: getattr(obj, name, default) if obj is not None else default
+    weights = w_cls(w1=prepared.w1, w2=prepared.w2, **{
+        k: g(src_w, k) for k in ("w1_bias", "w2_bias", "w1_scale", "w2_scale", "w1_scale_bias",
+                                 "w2_scale_bias", "w1_offset", "w2_offset")})
+    routing = r_cls(
+        expert_map=g(src_r, "expert_map"),
+        global_redundant_expert_num=g(src_r, "global_redundant_expert_num", 0),
+        mc2_mask=g(src_r, "mc2_mask"),
+        apply_router_weight_on_input=g(src_r, "apply_router_weight_on_input", False),
+        log2phy=prepared.log2phy if use_log2phy else None,
+        physical_expert_count=prepared.physical_expert_count,
+        pertoken_scale=g(src_r, "pertoken_scale"),
+    )
+    offload = o_cls(
+        enabled=g(src_o, "enabled", False) if offload_enabled is None else bool(offload_enabled),
+        profile_only=g(src_o, "profile_only", False),
+        layer_id=g(src_o, "layer_id", -1),
+        num_logical_experts=g(src_o, "num_logical_experts", 0),
+        expected_device_type=g(src_o, "expected_device_type", "cuda"),
+        step_id=g(src_o, "step_id", -1),
+    )
+    fields = dict(
+        hidden_states=inp.hidden_states, topk_weights=inp.topk_weights, topk_ids=inp.topk_ids,
+        weights=weights, routing=routing, quant=getattr(inp, "quant", None),
+        activation=getattr(inp, "activation", "silu"), need_trans=getattr(inp, "need_trans", False),
+        dynamic_eplb=getattr(inp, "dynamic_eplb", False), swiglu_limit=getattr(inp, "swiglu_limit", None),
+        offload=offload,
+    )
+    if hasattr(inp, "shared_output"):
+        fields["shared_output"] = inp.shared_output
+    return in_cls(**fields)
 
 
 # ---------------------------------------------------------------------------

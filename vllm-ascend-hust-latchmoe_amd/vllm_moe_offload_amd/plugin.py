@@ -1,9 +1,11 @@
-"""vLLM general-plugin wiring: custom ops of the seam and the splitting-op
-contract.
+"""vLLM general-plugin wiring: custom ops of the seam, the hooks and the
+splitting-op contract.
 
 register() is idempotent and safe to call in every vLLM process (API,
-EngineCore, Worker).  When vLLM is importable it also checks the compilation
-config contract: the seam needs PIECEWISE graph mode with
+EngineCore, Worker).  It registers the custom ops, then installs the
+fused-experts, router and EngineArgs hooks of patches/patch_fused_moe.py
+where the installed vLLM provides their targets; the EngineArgs hook checks
+the compilation config contract: the seam needs PIECEWISE graph mode with
 vllm::moe_offload_stage among the splitting ops, and fails closed otherwise.
 
 Reference: vllm_moe_offload_ascend/__init__.py:38-58 (register),
@@ -28,11 +30,19 @@ def register_plugin_ops() -> None:
     moe_mlp_op.register()
 
 
+INSTALLED_HOOKS: dict[str, bool] = {}
+
+
 def register() -> None:
     global _REGISTERED
     if _REGISTERED:
         return
     register_plugin_ops()
+    # the fused-experts, router and engine-config hooks, where the installed
+    # vLLM provides their targets (nothing is patched without vLLM)
+    from vllm_moe_offload_amd.patches.patch_fused_moe import apply_patches
+
+    INSTALLED_HOOKS.update(apply_patches())
     _REGISTERED = True
     if os.environ.get("LATCHMOE_VERBOSE"):
         print("LATCHMOE_PLUGIN registered ops=moe_router,moe_router_indirect,moe_offload_stage,moe_mlp,moe_mlp_shared",
