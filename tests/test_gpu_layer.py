@@ -365,4 +365,8 @@ def test_installed_comm_hook_runs_the_slot_bank_kernels(monkeypatch):
     assert int(res.expert_tokens.sum().item()) == T * k and res.group_list_type == 1
     assert all(isinstance(e, torch.cuda.Event) for e in (res.before_dispatch_evt, res.before_gmm2_evt,
                                                             res.before_combine_evt))
-    assert all(s.state.value == "ready" for s in rt.slot_bank(60).slots if s.expert_key is not None)
+    # the compute fenced the slots it read; the next staging drains the fence
+    busy = [s.slot_id for s in rt.slot_bank(60).slots if s.state.value == "computing"]
+    assert busy
+    layer.stage(ids)
+    assert all(rt.slot_bank(60).slots[s].state.value == "ready" for s in busy)
