@@ -370,3 +370,47 @@ def test_installed_comm_hook_runs_the_slot_bank_kernels(monkeypatch):
     assert busy
     layer.stage(ids)
     assert all(rt.slot_bank(60).slots[s].state.value == "ready" for s in busy)
+
+
+def test_cpu_first_layer_matches_the_copying_layer_bitwise(tmp_path):
+    """A layer loaded CPU-first from a safetensors checkpoint (host blocks
+    adopted, originals released, no full-layer device copy) computes the same
+    bits as one registered from in-memory weights."""
+    from safetensors.torch import save_file
+
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(29)
+    E, H, I, k, slots = 32, 512, 256, 4, 16
+    w13, w2, wg = _weights(rng, E, H, I)
+    t13 = torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16)
+    t2 = torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16)
+    save_file({f"model.layers.6.mlp.experts.{e}.{n}.weight": t.contiguous()
+               for e in range(E)
+               for n, t in (("gate_proj", t13[e, :I]), ("up_proj", t13[e, I:]), ("down_proj", t2[e]))},
+              str(tmp_path / "experts.safetensors"))
+    cfg = dict(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True)
+    rt_a = Runtime(Cfg(**cfg))
+    ref = SlotMoELayer(layer_id=6, runtime=rt_a, gate_weight=to_dev_bf16(wg), w13_weight=t13, w2_weight=t2, top_k=k)
+    ref.register()
+    torch.cuda.synchronize()
+    rt_b = Runtime(Cfg(cpu_first_load=True, release_original_expert_weights=True, **cfg))
+    before = torch.cuda.memory_allocated()
+    layer = SlotMoELayer.from_checkpoint(tmp_path / "experts.safetensors", prefix="model.layers.6.mlp", layer_id=6,
+                                         runtime=rt_b, num_experts=E, hidden_size=H, intermediate_size=I,
+                                         gate_weight=ref.gate_weight, top_k=k)
+    layer.register()
+    torch.cuda.synchronize()
+    grown = torch.cuda.memory_allocated() - before
+    buf = rt_b.host_store.get_layer_buffer(6)
+    assert buf.pinned and buf.w13.is_pinned() and buf.w2.is_pinned()
+    assert torch.equal(buf.w13, t13) and torch.equal(buf.w2, t2)
+    assert layer.w13_weight.numel() == 0 and not rt_b.original_expert_weights_available_for_layer(6)
+    full_layer = (t13.numel() + t2.numel()) * 2
+    assert grown < full_layer, (grown, full_layer)  # the slot bank (P=16 of 32) and its table only
+    for step, B in enumerate((1, 3, 4, 1)):
+        print(f"case cpu-first step {step} B={B}", flush=True)
+        dx = to_dev_bf16(normal_bf16(rng, (B, H), 1.0))
+        a = ref.forward(dx).clone()
+        b = layer.forward(dx).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)

@@ -165,6 +165,12 @@ def test_apply_patches_installs_into_stubbed_vllm_modules(monkeypatch):
         def apply(self, layer, *a, **k):
             return None
 
+        def create_weights(self, layer, *a, **k):
+            return None
+
+        def process_weights_after_loading(self, layer):
+            return None
+
     layer_mod.FusedMoE = FusedMoE
     layer_mod.UnquantizedFusedMoEMethod = UnquantizedFusedMoEMethod
     arg_mod = ModuleType("vllm.engine.arg_utils")
@@ -174,5 +180,47 @@ def test_apply_patches_installs_into_stubbed_vllm_modules(monkeypatch):
                       ("vllm.engine.arg_utils", arg_mod)):
         monkeypatch.setitem(sys.modules, name, mod)
     done = pfm.apply_patches()
-    assert done == {"comm_method": True, "select_experts": True, "quant_apply": True, "engine_args": True}
+    assert done == {"comm_method": True, "select_experts": True, "quant_apply": True, "quant_weights": True,
+                    "engine_args": True}
     assert comm_mod.MoECommMethod.fused_experts._latchmoe_patch_tag == pfm.PATCH_TAG
+
+
+def test_weight_hooks_create_host_experts_and_register_after_loading(monkeypatch):
+    """create_weights makes host blocks for an offloaded layer and defers to
+    vLLM for others; process_weights_after_loading registers both kinds
+    (patch_fused_moe.py:4537-4576, 4748-4790)."""
+    from vllm_moe_offload_amd.moe_offload import runtime as runtime_mod
+    from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+
+    rt = runtime_mod.MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=2, cpu_first_load=True,
+                                                        pin_host_memory=False,
+                                                        resident_layer_ids=frozenset({4})))
+    monkeypatch.setattr(runtime_mod, "get_moe_offload_runtime", lambda: rt)
+    calls = []
+
+    class Method:
+        moe = SimpleNamespace(is_act_and_mul=True, has_bias=False)
+
+        def create_weights(self, layer, num_experts, hidden_size, isz, params_dtype, **attrs):
+            calls.append(("create", layer.layer_id))
+            layer.w13_weight = torch.nn.Parameter(torch.ones(num_experts, 2 * isz, hidden_size), requires_grad=False)
+            layer.w2_weight = torch.nn.Parameter(torch.ones(num_experts, hidden_size, isz), requires_grad=False)
+
+        def process_weights_after_loading(self, layer):
+            calls.append(("process", layer.layer_id))
+
+    assert pfm._patch_quant_method_weights(Method) and pfm._patch_quant_method_weights(Method)  # idempotent
+    offloaded, resident = torch.nn.Module(), torch.nn.Module()
+    offloaded.layer_name, resident.layer_name = "model.layers.3.mlp.experts", "model.layers.4.mlp.experts"
+    m = Method()
+    for layer in (offloaded, resident):
+        m.create_weights(layer, 4, 3, 2, torch.float32, weight_loader=None)
+    assert calls == [("create", 4)]  # the offloaded layer never reached vLLM's allocation
+    assert offloaded.layer_id == 3 and offloaded.w13_weight.device.type == "cpu"
+    offloaded.w13_weight.data.fill_(2.0)
+    offloaded.w2_weight.data.fill_(3.0)
+    for layer in (offloaded, resident):
+        m.process_weights_after_loading(layer)
+    assert calls == [("create", 4), ("process", 4)]  # vLLM's processing ran for the resident layer only
+    assert rt.is_layer_registered(3) and not rt.is_layer_registered(4)
+    assert rt.host_store.get(3, 1).w13.data_ptr() == offloaded.w13_weight[1].data_ptr()

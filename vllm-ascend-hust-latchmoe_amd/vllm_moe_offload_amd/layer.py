@@ -31,6 +31,11 @@ from vllm_moe_offload_amd.fused_moe import (
     route,
     run_wave_prefill,
 )
+from vllm_moe_offload_amd.moe_offload.cpu_first_loader import (
+    CPU_FIRST_MARKER,
+    create_cpu_first_expert_weights,
+    load_expert_checkpoint,
+)
 from vllm_moe_offload_amd.moe_offload.runtime import MoeOffloadRuntime, _is_current_graph_capturing
 from vllm_moe_offload_amd.ops.fused_moe import moe_seam_inject
 from vllm_moe_offload_amd.ops.fused_moe.moe_offload_stage_op import PHASE_DECODE
@@ -91,9 +96,30 @@ class SlotMoELayer(torch.nn.Module):
             else:
                 self.shared_w13 = shared_w13.unsqueeze(0).contiguous()
                 self.shared_w2 = shared_w2.unsqueeze(0).contiguous()
-        # registration copies these to the host store; they are dropped after
+        # registration copies these to the host store (or adopts them, for a
+        # CPU-first layer); release_original_expert_weights drops them after
         self.w13_weight = w13_weight
         self.w2_weight = w2_weight
+
+    @classmethod
+    def from_checkpoint(cls, files, *, prefix: str, layer_id: int, runtime: MoeOffloadRuntime,
+                        num_experts: int, hidden_size: int, intermediate_size: int,
+                        dtype: torch.dtype = torch.bfloat16, names: tuple[str, str, str] | None = None,
+                        **kwargs) -> "SlotMoELayer":
+        """CPU-first construction: the routed experts under `prefix` stream
+        from safetensors `files` into host blocks (page-locked when the
+        runtime pins), which registration then adopts as the host store; the
+        device only ever holds the slot bank.  kwargs are the constructor's
+        (gate_weight, top_k, routing options, shared expert, device)."""
+        holder = torch.nn.Module()
+        create_cpu_first_expert_weights(
+            holder, num_experts=num_experts, hidden_size=hidden_size, intermediate_size=intermediate_size,
+            dtype=dtype, pin_memory=runtime.config.should_pin_host_memory)
+        load_expert_checkpoint(holder, files, prefix=prefix, names=names)
+        layer = cls(layer_id=layer_id, runtime=runtime, w13_weight=holder.w13_weight.data,
+                    w2_weight=holder.w2_weight.data, **kwargs)
+        setattr(layer, CPU_FIRST_MARKER, True)
+        return layer
 
     # -------------------------------------------------------------- setup
     @property
@@ -101,11 +127,13 @@ class SlotMoELayer(torch.nn.Module):
         return self.num_routed_experts + self.n_shared_experts
 
     def register(self) -> None:
-        self.runtime.register_layer_for_fixed_slots(self, slot_device=self.device)
-        self.runtime.stage_full_residency_slot_plan(layer_id=self.layer_id)
-        # the host store owns the routed rows now
-        self.w13_weight = None
-        self.w2_weight = None
+        rt = self.runtime
+        rt.register_layer_for_fixed_slots(self, slot_device=self.device)
+        rt.stage_full_residency_slot_plan(layer_id=self.layer_id)
+        # the host store owns the routed rows now; the originals go when the
+        # configuration asks for it (the ledger counts them until then)
+        if rt.config.release_original_expert_weights:
+            rt.release_original_expert_weights_if_ready(self)
         from vllm_moe_offload_amd.ops.fused_moe._register import register_moe_layer
 
         register_moe_layer(self.layer_name, self)

@@ -55,6 +55,11 @@ class MoeOffloadConfig:
     b2_avoid_mixed_wave_d2d: bool = True
     max_num_seqs_hint: int = 0
     profile_path: str = ""
+    # expert parameters of offloaded layers are created in host memory and
+    # the checkpoint loads straight into them (no full-layer device copy)
+    cpu_first_load: bool = False
+    # drop a layer's original expert tensors once its host store is complete
+    release_original_expert_weights: bool = False
 
     @classmethod
     def from_env(cls) -> "MoeOffloadConfig":
@@ -75,6 +80,8 @@ class MoeOffloadConfig:
             b2_avoid_mixed_wave_d2d=_bool("B2_AVOID_MIXED_D2D", True),
             max_num_seqs_hint=_int("MAX_NUM_SEQS_HINT", 0),
             profile_path=_env("PROFILE_PATH", ""),
+            cpu_first_load=_bool("CPU_FIRST_LOAD", False),
+            release_original_expert_weights=_bool("RELEASE_ORIGINAL_EXPERT_WEIGHTS", False),
         )
 
     @property

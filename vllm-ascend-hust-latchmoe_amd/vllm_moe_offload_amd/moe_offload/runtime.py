@@ -38,6 +38,8 @@ import numpy as np
 import torch
 
 from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+from vllm_moe_offload_amd.moe_offload.cpu_first_loader import CPU_FIRST_MARKER, is_cpu_first_layer
+from vllm_moe_offload_amd.moe_offload.expert_weight_release import release_layer_original_expert_weights
 from vllm_moe_offload_amd.moe_offload.expert_key import ExpertKey
 from vllm_moe_offload_amd.moe_offload.host_store import HostExpertStore
 from vllm_moe_offload_amd.moe_offload.placement_plan import PlacementPlanProvider, resolve_placement_plan
@@ -102,10 +104,24 @@ class MoeOffloadMemoryLedger:
     # name kept for callers of the reference ledger
     total_npu_slot_bytes = total_device_slot_bytes
 
+    @property
+    def original_expert_weights_retained(self) -> bool:
+        return self.original_expert_weight_bytes > 0
+
     def to_jsonable(self) -> dict[str, int]:
         d = {k: int(getattr(self, k)) for k in self.__dataclass_fields__}
         d["total_device_slot_bytes"] = int(self.total_device_slot_bytes)
+        d["original_expert_weights_retained"] = bool(self.original_expert_weights_retained)
         return d
+
+
+@dataclass(frozen=True)
+class MoeExpertReleasePlan:
+    """Whether original expert tensors may be dropped, and why not."""
+
+    ready: bool
+    layers_ready: tuple[int, ...]
+    blockers: tuple[str, ...]
 
 
 @dataclass(frozen=True)
@@ -186,6 +202,7 @@ class MoeOffloadRuntime:
         self._full_layer_prefill_pool: dict[tuple, ExpertSlotBank] = {}
         self._full_layer_prefill_log2phy: dict[tuple, torch.Tensor] = {}
         self._original_expert_weight_bytes_by_layer: dict[int, int] = {}
+        self._released_original_weight_layers: set[int] = set()
         self._expert_weight_bytes_by_layer: dict[int, int] = {}
         self._log2phy_buffers: dict[int, torch.Tensor] = {}
         self._log2phy_slot_by_expert: dict[int, dict[int, int]] = {}
@@ -339,10 +356,11 @@ class MoeOffloadRuntime:
         report = self._host_store.register_layer(
             layer,
             pin_memory=self.config.should_pin_host_memory,
-            clone_tensors=not bool(getattr(layer, "_cpu_first_expert_weights", False)),
+            clone_tensors=not is_cpu_first_layer(layer),
             routed_expert_count=routed,
         )
         self._original_expert_weight_bytes_by_layer[layer_id] = _nbytes(w13) + _nbytes(w2)
+        self._released_original_weight_layers.discard(layer_id)
         self._expert_weight_bytes_by_layer[layer_id] = _nbytes(w13[0]) + _nbytes(w2[0])
         device = slot_device if slot_device is not None else w13.device
         bank = ExpertSlotBank(
@@ -390,10 +408,11 @@ class MoeOffloadRuntime:
         holder.layer_id = layer_id
         holder.w13_weight = w13_host
         holder.w2_weight = w2_host
-        holder._cpu_first_expert_weights = True
+        setattr(holder, CPU_FIRST_MARKER, True)
         E = int(w13_host.shape[0])
         self._host_store.register_layer(holder, pin_memory=False, clone_tensors=False, routed_expert_count=E)
         self._original_expert_weight_bytes_by_layer[layer_id] = 0
+        self._released_original_weight_layers.discard(layer_id)
         self._expert_weight_bytes_by_layer[layer_id] = _nbytes(w13_host[0]) + _nbytes(w2_host[0])
         bank = ExpertSlotBank(self.config.num_slots, tuple(int(d) for d in w13_host.shape[1:]),
                               tuple(int(d) for d in w2_host.shape[1:]), dtype=w13_host.dtype, device=slot_device)
@@ -433,6 +452,64 @@ class MoeOffloadRuntime:
     def log2phy_buffer(self, layer_id: int) -> torch.Tensor | None:
         """The persistent, fixed-address log2phy table of a layer."""
         return self._log2phy_buffers.get(int(layer_id))
+
+    # ------------------------------------------- original weight release
+    def original_expert_weights_available_for_layer(self, layer_id: int) -> bool:
+        return int(layer_id) not in self._released_original_weight_layers
+
+    def plan_original_weight_release(self, *, expected_layer_ids, default_path_preserved: bool,
+                                     host_store_is_complete: bool | None = None,
+                                     allow_retained_original_weights: bool = False) -> MoeExpertReleasePlan:
+        """Blockers to dropping the original expert tensors of the given
+        layers: unregistered layers, an incomplete host store, a default path
+        that needs them, or (unless allowed) original tensors still counted."""
+        ids = tuple(int(i) for i in expected_layer_ids)
+        blockers: list[str] = []
+        if not ids:
+            blockers.append("no_expected_layers")
+        missing = [i for i in ids if i not in self._slot_banks]
+        if missing:
+            blockers.append(f"layers_not_registered:{missing}")
+        if not default_path_preserved:
+            blockers.append("default_path_not_preserved")
+        if host_store_is_complete is False:
+            blockers.append("host_store_not_marked_complete")
+        blockers.extend(self._host_store.validate_complete_layers(ids).blockers)
+        if self.memory_ledger().original_expert_weights_retained and not allow_retained_original_weights:
+            blockers.append("original_expert_weights_still_retained")
+        return MoeExpertReleasePlan(not blockers, () if blockers else ids, tuple(blockers))
+
+    def release_original_expert_weights_if_ready(self, layer: torch.nn.Module, *,
+                                                 default_path_preserved: bool = True) -> MoeExpertReleasePlan:
+        """Drop one offloaded layer's original w13/w2 once its host store is
+        complete (opt-in by release_original_expert_weights).  Idempotent."""
+        def blocked(reason: str) -> MoeExpertReleasePlan:
+            return MoeExpertReleasePlan(False, (), (reason,))
+
+        if not self.config.release_original_expert_weights:
+            return blocked("release_original_expert_weights_disabled")
+        if not self.should_use_fixed_slots:
+            return blocked("fixed_slots_disabled")
+        layer_id = int(getattr(layer, "layer_id", -1))
+        if layer_id < 0:
+            return blocked("invalid_layer_id")
+        if self.is_resident_layer(layer_id):
+            return blocked(f"resident_layer:{layer_id}")
+        if layer_id in self._released_original_weight_layers:
+            return MoeExpertReleasePlan(True, (layer_id,), ())
+        plan = self.plan_original_weight_release(expected_layer_ids=(layer_id,),
+                                                 default_path_preserved=default_path_preserved,
+                                                 allow_retained_original_weights=True)
+        if not plan.ready:
+            return plan
+        start = perf_counter()
+        freed = release_layer_original_expert_weights(layer)
+        self._released_original_weight_layers.add(layer_id)
+        self._original_expert_weight_bytes_by_layer[layer_id] = 0
+        self._memory_ledger_cache = None
+        self._record_profile_event("release_original_expert_weights", layer_id=layer_id, start=start,
+                                   payload={"released_bytes": int(freed)})
+        return MoeExpertReleasePlan(True, (layer_id,), ())
 
     # ------------------------------------------------------ memory ledger
     def memory_ledger(self) -> MoeOffloadMemoryLedger:

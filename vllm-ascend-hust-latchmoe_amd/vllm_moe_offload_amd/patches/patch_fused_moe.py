@@ -34,6 +34,7 @@ from contextlib import contextmanager
 PATCH_TAG = "vllm_moe_offload_amd.moe_comm_method_runtime"
 SELECT_TAG = "vllm_moe_offload_amd.select_experts"
 ENGINE_TAG = "vllm_moe_offload_amd.engine_args"
+WEIGHTS_TAG = "vllm_moe_offload_amd.cpu_first_weights"
 
 # the quant method's apply() publishes its layer here for select_experts
 _layer_ctx = threading.local()
@@ -232,6 +233,56 @@ def _patch_quant_method_apply(cls) -> bool:
     return True
 
 
+def _patch_quant_method_weights(cls) -> bool:
+    """CPU-first create_weights and the registration after loading:
+    create_weights makes host expert parameters for offloaded layers, and
+    process_weights_after_loading registers every offloaded layer's host
+    store and slot bank (then releases the originals when configured).
+    Reference: patches/patch_fused_moe.py:4537-4576 and :4748-4790."""
+    create = getattr(cls, "create_weights", None)
+    process = getattr(cls, "process_weights_after_loading", None)
+    if create is None or process is None:
+        return False
+    if _is_tagged(create, WEIGHTS_TAG) and _is_tagged(process, WEIGHTS_TAG):
+        return True
+    from vllm_moe_offload_amd.moe_offload.runtime import get_moe_offload_runtime
+    from vllm_moe_offload_amd.moe_offload.cpu_first_loader import (
+        ensure_moe_layer_id,
+        maybe_create_unquantized_cpu_first_weights,
+        maybe_process_unquantized_cpu_first_weights,
+        maybe_register_unquantized_fixed_slot_weights,
+    )
+
+    original_create, original_process = create, process
+
+    def create_weights(self, layer, num_experts, hidden_size, intermediate_size_per_partition,
+                       params_dtype, **extra_weight_attrs):
+        ensure_moe_layer_id(layer)
+        if maybe_create_unquantized_cpu_first_weights(
+            self, layer, runtime=get_moe_offload_runtime(), num_experts=num_experts,
+            hidden_size=hidden_size, intermediate_size_per_partition=intermediate_size_per_partition,
+            params_dtype=params_dtype, extra_weight_attrs=extra_weight_attrs,
+        ):
+            return None
+        return original_create(self, layer, num_experts, hidden_size, intermediate_size_per_partition,
+                               params_dtype, **extra_weight_attrs)
+
+    def process_weights_after_loading(self, layer):
+        ensure_moe_layer_id(layer)
+        rt = get_moe_offload_runtime()
+        if maybe_process_unquantized_cpu_first_weights(self, layer, runtime=rt):
+            return None
+        result = original_process(self, layer)
+        maybe_register_unquantized_fixed_slot_weights(layer, runtime=rt)
+        return result
+
+    if not _is_tagged(create, WEIGHTS_TAG):
+        cls.create_weights = _tagged(create_weights, WEIGHTS_TAG)
+    if not _is_tagged(process, WEIGHTS_TAG):
+        cls.process_weights_after_loading = _tagged(process_weights_after_loading, WEIGHTS_TAG)
+    return True
+
+
 def _patch_engine_args_autoconfig(arg_utils=None) -> bool:
     """Wrap EngineArgs.create_engine_config so the final config keeps the stage
     op as a PIECEWISE splitting op (fail closed on FULL graph modes)."""
@@ -272,7 +323,8 @@ def _stage_seam_enabled() -> bool:
 
 def apply_patches() -> dict[str, bool]:
     """Install every hook whose target the installed vLLM provides."""
-    done = {"comm_method": False, "select_experts": False, "quant_apply": False, "engine_args": False}
+    done = {"comm_method": False, "select_experts": False, "quant_apply": False, "quant_weights": False,
+            "engine_args": False}
     for mod in ("vllm.model_executor.layers.fused_moe.moe_comm_method",
                 "vllm_ascend.ops.fused_moe.moe_comm_method"):
         try:
@@ -291,5 +343,6 @@ def apply_patches() -> dict[str, bool]:
         method = getattr(layer_mod, "UnquantizedFusedMoEMethod", None)
         if method is not None:
             done["quant_apply"] = _patch_quant_method_apply(method)
+            done["quant_weights"] = _patch_quant_method_weights(method)
     done["engine_args"] = _patch_engine_args_autoconfig()
     return done
