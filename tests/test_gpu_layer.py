@@ -414,3 +414,46 @@ def test_cpu_first_layer_matches_the_copying_layer_bitwise(tmp_path):
         b = layer.forward(dx).clone()
         torch.cuda.synchronize()
         assert torch.equal(a, b)
+
+
+def test_wave_prefill_writes_work_conserving_evidence(tmp_path, monkeypatch):
+    """b2_work_conserving_prefill goes to the JSONL with the reference's keys
+    and passes the checks its evidence verifier makes
+    (verify_issue7_graph_unit.py:233-251 there)."""
+    import json
+
+    from vllm_moe_offload_amd.moe_offload.profile_io import close_profile_writes
+
+    monkeypatch.setenv("VLLM_ASCEND_MOE_B2_PROFILE_DETAILS", "1")
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(31)
+    E, H, I, k, T, slots = 64, 512, 256, 8, 256, 16
+    w13, w2, wg = _weights(rng, E, H, I)
+    path = tmp_path / "ev.jsonl"
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True, b2_wave_prefill=True,
+                     profile_path=str(path)))
+    layer = SlotMoELayer(layer_id=9, runtime=rt, gate_weight=to_dev_bf16(wg),
+                         w13_weight=torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16),
+                         w2_weight=torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16), top_k=k)
+    layer.register()
+    dx = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
+    w, ids, _ = fused_moe.route(dx, layer.gate_weight, layer.router_spec)
+    print("case wave evidence", flush=True)
+    _, report = fused_moe.run_wave_prefill(rt, layer_id=9, hidden=dx, topk_weights=w, topk_ids=ids,
+                                           num_logical_experts=E)
+    torch.cuda.synchronize()
+    close_profile_writes()
+    b2 = [r for r in map(json.loads, open(path, encoding="utf-8")) if r["name"] == "b2_work_conserving_prefill"]
+    assert len(b2) == 1 and b2[0]["layer_id"] == 9
+    p = b2[0]["payload"]
+    waves = (p.get("wave_plan") or {}).get("waves") or p.get("waves") or []
+    summary = p["wave_summary"]
+    assert p["num_slots"] == slots and p["n_active"] > 0 and p["n_tokens"] == T
+    assert waves and all(len(wv["experts"]) <= slots for wv in waves)
+    assert summary["wave_count"] == len(report.waves) >= 2
+    assert summary["prefetch_after_compute_issues"] == 0
+    assert summary["pairs"] == p["n_pairs"] == T * k
+    assert summary["h2d_bytes"] == report.h2d_bytes and summary["d2d_bytes"] == report.d2d_bytes
+    assert p["masked_full_prompt_pairs"] - p["work_conserving_saved_pairs"] == T * k
+    assert set(p["control_ms"]) >= {"token_count", "readiness", "wave_plan", "schedule", "loop", "scatter_total",
+                                    "end_to_end"}

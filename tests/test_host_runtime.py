@@ -173,8 +173,8 @@ def test_capture_handoff_releases_prior_compute_without_host_sync(monkeypatch): 
     assert not rt._compute_fences.get(7)
 
 
-def test_stage_fixed_slot_plan_writes_persistent_log2phy():  # :1388-1419
-    rt = _rt(num_slots=2, graph_compatible_offload=True, profile_path="x")
+def test_stage_fixed_slot_plan_writes_persistent_log2phy(tmp_path):  # :1388-1419
+    rt = _rt(num_slots=2, graph_compatible_offload=True, profile_path=str(tmp_path / "p.jsonl"))
     rt.register_layer_for_fixed_slots(TinyLayer(), slot_device=CPU)
     ptr = rt.log2phy_buffer(7).data_ptr()
     p = rt.stage_fixed_slot_plan(layer_id=7, active_experts=(3, 1), num_logical_experts=4)

@@ -181,7 +181,7 @@ def test_apply_patches_installs_into_stubbed_vllm_modules(monkeypatch):
         monkeypatch.setitem(sys.modules, name, mod)
     done = pfm.apply_patches()
     assert done == {"comm_method": True, "select_experts": True, "quant_apply": True, "quant_weights": True,
-                    "engine_args": True}
+                    "engine_args": True, "graph_replay_profile": False}
     assert comm_mod.MoECommMethod.fused_experts._latchmoe_patch_tag == pfm.PATCH_TAG
 
 

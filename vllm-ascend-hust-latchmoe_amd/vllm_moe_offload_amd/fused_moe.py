@@ -28,6 +28,7 @@ _run_b2_full_layer_reference :3472-3650; MoEFusedExpertsInput fields
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass, field
 from time import perf_counter
 
@@ -489,16 +490,21 @@ def run_wave_prefill(
         raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
     P = bank.physical_expert_count
     I = int(bank.w13_slots.shape[1]) // 2
+    cache_hit = token_counts_by_expert is not None
     if token_counts_by_expert is None:
         token_counts_by_expert = runtime.consume_prefill_route_stats(layer_id=layer_id, topk_ids=topk_ids)
+        cache_hit = token_counts_by_expert is not None
     if token_counts_by_expert is None:
         token_counts_by_expert = phase_split.count_routed_tokens_by_expert(topk_ids)  # D2H
+    t_count = perf_counter()
     routed = runtime.routed_expert_count_for_layer(layer_id=layer_id, fallback=num_logical_experts)
     counts = {e: c for e, c in token_counts_by_expert.items() if 0 <= e < routed}
+    readiness = runtime.slot_readiness_for_experts(layer_id=layer_id, expert_ids=tuple(counts))
+    t_ready = perf_counter()
     plan = phase_split.plan_balanced_b2_waves(counts, int(cfg.num_slots))
     if not plan.waves:
         raise phase_split.B2WaveFallback("no routed pairs to execute")
-    readiness = runtime.slot_readiness_for_experts(layer_id=layer_id, expert_ids=tuple(counts))
+    t_plan = perf_counter()
     per_expert = runtime.cached_layer_expert_weight_bytes(layer_id=layer_id)
     h2d = {i: per_expert * sum(1 for e in w if not readiness.get(e, False)) for i, w in enumerate(plan.waves)}
     cost = {i: float(plan.wave_tokens(w)) for i, w in enumerate(plan.waves)}
@@ -507,6 +513,9 @@ def run_wave_prefill(
         prefetch_depth=cfg.effective_prefill_prefetch_depth, buffer_count=cfg.effective_prefill_buffer_count,
         h2d_bytes_by_wave=h2d, compute_cost_by_wave=cost, transfer_aware=cfg.transfer_aware_wave_schedule,
     )
+    t_sched = perf_counter()
+    profiling = bool(runtime.profile_path)
+    wave_profiles: dict[int, dict] = {}
     ws = get_workspace(T, k, P, H, I, hidden.device, tag="waves")
     report = WaveRunReport(plan.waves, sched.compute_order)
     staged: dict[int, tuple] = {}
@@ -515,8 +524,11 @@ def run_wave_prefill(
     # computed wave only; later waves' tables stop at the routed ids
     shared_pairs = int((topk_ids >= routed).sum().item()) if total_logical > routed else 0
     first = True
+    t_loop = perf_counter()
+    computed: set[int] = set()
     for kind, w, buf in phase_split.iterate_b2_schedule(sched):
         report.issue_log.append((kind, w))
+        t_step = perf_counter()
         if kind == "issue_stage":
             prepared, ready, payload = runtime.prepare_prefill_stage_plan(
                 layer_id=layer_id, active_experts=plan.waves[w], num_logical_experts=total_logical,
@@ -525,15 +537,24 @@ def run_wave_prefill(
             report.h2d_bytes += int(payload["h2d_bytes"])
             report.d2d_bytes += int(payload["d2d_bytes"])
             staged[w] = (prepared, ready, buf)
+            if profiling:
+                wave_profiles[w] = _wave_profile(plan, w, "async_stage", len(payload["hit_experts"]),
+                                                 len(payload["miss_experts"]), payload["h2d_bytes"],
+                                                 payload["d2d_bytes"], computed, t_step, buf)
         elif kind == "issue_hit":
             prepared = runtime.prepare_ready_slot_plan(
                 layer_id=layer_id, active_experts=plan.waves[w], num_logical_experts=total_logical,
                 device=hidden.device,
             )
             staged[w] = (prepared, None, None)
+            if profiling:
+                wave_profiles[w] = _wave_profile(plan, w, "main_slot_hit", len(plan.waves[w]), 0, 0, 0,
+                                                 computed, t_step, None)
         else:
             prepared, ready, buf = staged.pop(w)
+            t_wait = perf_counter()
             runtime.wait_prefill_stage_plan(ready)
+            t_mlp = perf_counter()
             handle = runtime.begin_slot_compute(prepared)
             try:
                 native.permute(topk_ids, ws.perm, log2phy=prepared.log2phy, skip_unmapped=True,
@@ -547,15 +568,104 @@ def run_wave_prefill(
                 ev = torch.cuda.Event()
                 ev.record(torch.cuda.current_stream())
                 runtime.remember_prefill_stage_buffer_release(layer_id=layer_id, buffer_index=buf, event=ev)
+            computed.add(w)
+            if profiling and w in wave_profiles:
+                wp = wave_profiles[w]
+                wp["stage_wait_ms"] = round((t_mlp - t_wait) * 1000.0, 3)
+                wp["mlp_ms"] = round((perf_counter() - t_mlp) * 1000.0, 3)  # host issue time
+                wp["issue_end_to_compute_ms"] = round((t_wait - wp.pop("_issue_end")) * 1000.0, 3)
     if plan.total_pairs + shared_pairs != T * k:
         raise phase_split.B2WaveFallback(
             "B2 wave pair coverage does not match the original top-k routing: "
             f"covered={plan.total_pairs + shared_pairs} expected={T * k}"
         )
+    t_scatter = perf_counter()
     dst = out if out is not None else ws.out[:T]
     native.combine(ws.y[: T * k], topk_weights, dst, add=add)
-    report.seconds = perf_counter() - t0
+    t_end = perf_counter()
+    report.seconds = t_end - t0
+    if profiling:
+        _record_b2_prefill_event(
+            runtime, layer_id=layer_id, plan=plan, sched=sched, T=T, k=k, shared_pairs=shared_pairs,
+            waves=[wave_profiles[w] for w in sched.compute_order if w in wave_profiles],
+            cache_hit=cache_hit, start=t0,
+            control_ms={"token_count": t_count - t0, "readiness": t_ready - t_count, "wave_plan": t_plan - t_ready,
+                        "schedule": t_sched - t_plan, "loop": t_scatter - t_loop,
+                        "scatter_total": t_end - t_scatter, "end_to_end": t_end - t0},
+        )
     return dst, report
+
+
+def _wave_profile(plan, w: int, mode: str, hits: int, misses: int, h2d: int, d2d: int, computed: set,
+                  t_issue: float, buf) -> dict:
+    """Per-wave evidence at issue time; a stage issued after its own wave's
+    compute would count in prefetch_after_compute_count."""
+    experts = plan.waves[w]
+    tokens = plan.wave_tokens(experts)
+    return {"wave_index": int(w), "experts": [int(e) for e in experts], "tokens": tokens, "pairs": tokens,
+            "hits": int(hits), "misses": int(misses), "h2d_bytes": int(h2d), "d2d_bytes": int(d2d),
+            "stage_mode": mode, "buffer_index": buf, "issued_before_compute": w not in computed,
+            "prefetch_before_compute_count": int(w not in computed and mode != "main_slot_hit"),
+            "prefetch_after_compute_count": int(w in computed),
+            "stage_issue_ms": round((perf_counter() - t_issue) * 1000.0, 3), "_issue_end": perf_counter()}
+
+
+def _record_b2_prefill_event(runtime, *, layer_id, plan, sched, T, k, shared_pairs, waves, cache_hit, start,
+                             control_ms) -> None:
+    """The b2_work_conserving_prefill evidence line, with the reference's
+    payload keys (patches/patch_fused_moe.py:3386-3461, 1826-1930)."""
+    tokens = [int(wp["tokens"]) for wp in waves] or [0]
+    mean = sum(tokens) / len(tokens)
+    summary = {"wave_count": len(waves), "hit_only_waves": 0, "miss_only_waves": 0, "mixed_waves": 0,
+               "main_slot_hit_waves": 0, "staged_waves": 0, "sync_slot_cache_waves": 0,
+               "issued_before_compute_waves": 0, "prefetch_before_compute_issues": 0,
+               "prefetch_after_compute_issues": 0}
+    for key in ("tokens", "pairs", "hits", "misses", "h2d_bytes", "d2d_bytes"):
+        summary[key] = sum(int(wp[key]) for wp in waves)
+    for wp in waves:
+        h, m = int(wp["hits"]), int(wp["misses"])
+        kind = "hit_only_waves" if m == 0 and h > 0 else "miss_only_waves" if h == 0 and m > 0 else \
+            "mixed_waves" if h and m else None
+        if kind:
+            summary[kind] += 1
+        summary["main_slot_hit_waves" if wp["stage_mode"] == "main_slot_hit" else "staged_waves"] += 1
+        summary["issued_before_compute_waves"] += int(bool(wp["issued_before_compute"]))
+        summary["prefetch_before_compute_issues"] += int(wp["prefetch_before_compute_count"])
+        summary["prefetch_after_compute_issues"] += int(wp["prefetch_after_compute_count"])
+    for key in ("stage_issue_ms", "stage_wait_ms", "mlp_ms", "issue_end_to_compute_ms"):
+        summary[key] = round(sum(float(wp.get(key, 0.0)) for wp in waves), 3)
+    summary["max_issue_end_to_compute_ms"] = max((float(wp.get("issue_end_to_compute_ms", 0.0)) for wp in waves),
+                                                 default=0.0)
+    summary["max_stage_wait_ms"] = max((float(wp.get("stage_wait_ms", 0.0)) for wp in waves), default=0.0)
+    summary["layer_scatter_ms"] = round(control_ms["scatter_total"] * 1000.0, 3)
+    payload = {
+        "n_tokens": int(T),
+        "n_active": int(plan.active_expert_count),
+        "n_pairs": int(plan.total_pairs),
+        "logical_pairs": int(plan.total_pairs),
+        "shared_pairs": int(shared_pairs),
+        "num_slots": int(runtime.config.num_slots),
+        "n_waves": len(plan.waves),
+        "masked_full_prompt_pairs": int(T) * len(plan.waves) * int(k),
+        "work_conserving_saved_pairs": int(T) * len(plan.waves) * int(k) - int(plan.total_pairs),
+        "execution_mode": "pair_microbatch",
+        "wave_membership_uses_slot_readiness": False,
+        "wave_accumulation_dtype": "bfloat16_pairs_one_combine",
+        "wave_token_summary": {"min": min(tokens), "max": max(tokens), "mean": round(mean, 3),
+                               "imbalance": round(max(tokens) / mean, 3) if mean else 0.0},
+        "control_ms": {key: round(v * 1000.0, 3) for key, v in control_ms.items()},
+        "route_stats_cache_hit": bool(cache_hit),
+        "pair_index_cache_hit": False,
+        "pair_planner_mode": "device_permute",
+        "forward_phase": "prefill",
+        "wave_summary": summary,
+    }
+    if os.environ.get("VLLM_ASCEND_MOE_B2_PROFILE_DETAILS", "0").strip().lower() in {"1", "true", "yes", "on"}:
+        payload.update({"wave_plan": plan.to_jsonable(), "async_schedule": sched.to_jsonable(), "waves": waves})
+    else:
+        payload["profile_details"] = "omitted"
+    runtime._record_profile_event("b2_work_conserving_prefill", layer_id=int(layer_id), start=start,
+                                  payload=payload)
 
 
 def run_full_layer(

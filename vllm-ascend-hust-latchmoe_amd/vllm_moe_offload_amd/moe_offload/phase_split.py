@@ -54,11 +54,17 @@ class B2WavePlan:
         return int(sum(self.token_counts_by_expert.get(int(e), 0) for e in wave))
 
     def to_jsonable(self) -> dict[str, object]:
+        """Evidence form read by the reference's verifiers
+        (phase_split.py:151-167 there)."""
         return {
-            "waves": [list(w) for w in self.waves],
-            "wave_tokens": [self.wave_tokens(w) for w in self.waves],
-            "active_expert_count": self.active_expert_count,
-            "total_pairs": self.total_pairs,
+            "n_active": self.active_expert_count,
+            "n_pairs": self.total_pairs,
+            "n_waves": len(self.waves),
+            "waves": [
+                {"experts": [int(e) for e in w], "tokens": self.wave_tokens(w),
+                 "per_expert_tokens": {str(int(e)): int(self.token_counts_by_expert.get(int(e), 0)) for e in w}}
+                for w in self.waves
+            ],
         }
 
 

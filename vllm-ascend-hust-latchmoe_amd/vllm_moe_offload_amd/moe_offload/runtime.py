@@ -43,6 +43,7 @@ from vllm_moe_offload_amd.moe_offload.expert_weight_release import release_layer
 from vllm_moe_offload_amd.moe_offload.expert_key import ExpertKey
 from vllm_moe_offload_amd.moe_offload.host_store import HostExpertStore
 from vllm_moe_offload_amd.moe_offload.placement_plan import PlacementPlanProvider, resolve_placement_plan
+from vllm_moe_offload_amd.moe_offload.profile_io import append_jsonl, profile_path_from_env
 from vllm_moe_offload_amd.moe_offload.slot_bank import ExpertSlotBank, SlotLease, SlotState
 from vllm_moe_offload_amd.moe_offload.slot_mapping import (
     ExpertSlotMapping,
@@ -125,6 +126,24 @@ class MoeExpertReleasePlan:
 
 
 @dataclass(frozen=True)
+class MoeOffloadProfileEvent:
+    """One profile record (one JSONL line when a profile path is set)."""
+
+    name: str
+    layer_id: int | None
+    seconds: float
+    memory_ledger: MoeOffloadMemoryLedger
+    payload: dict[str, object] | None = None
+
+    def to_jsonable(self) -> dict[str, object]:
+        d: dict[str, object] = {"name": self.name, "layer_id": self.layer_id, "seconds": self.seconds,
+                                "memory_ledger": self.memory_ledger.to_jsonable()}
+        if self.payload is not None:
+            d["payload"] = self.payload
+        return d
+
+
+@dataclass(frozen=True)
 class MoePrefillRouteStats:
     layer_id: int
     topk_cache_key: tuple
@@ -157,6 +176,8 @@ class PendingFixedSlotStage:
     step_id: int
     started: float
     table_updates: int = -1  # entries already written with the copies (-1: publish writes them)
+    load_sync_ms: float = 0.0
+    load_enqueue_ms: float = 0.0
 
 
 @dataclass(frozen=True)
@@ -210,7 +231,9 @@ class MoeOffloadRuntime:
         self._graph_slot_address_evidence: set[int] = set()
         self._slot_generation_protection_evidence: set[int] = set()
         self._transfer_engine = TransferEngine()
-        self._profile_events: list[dict[str, object]] = []
+        self._profile_events: list[MoeOffloadProfileEvent] = []
+        # JSONL destination of the profile events ("" = kept in memory only)
+        self.profile_path = profile_path_from_env(self.config.profile_path)
         self._prefill_route_stats_by_layer: dict[int, MoePrefillRouteStats] = {}
         self._active_slot_ids_by_layer: dict[int, tuple[int, ...]] = {}
         self._compute_fences: dict[int, list] = {}
@@ -243,18 +266,26 @@ class MoeOffloadRuntime:
 
     def _record_profile_event(self, name: str, *, layer_id: int | None, start: float,
                               payload: dict[str, object] | None = None) -> None:
-        ev: dict[str, object] = {
-            "name": name,
-            "layer_id": layer_id,
-            "seconds": perf_counter() - start,
-            "memory_ledger": self.memory_ledger().to_jsonable(),
-        }
-        if payload is not None:
-            ev["payload"] = payload
+        ev = MoeOffloadProfileEvent(name, layer_id, perf_counter() - start, self.memory_ledger(), payload)
         self._profile_events.append(ev)
+        if self.profile_path:
+            append_jsonl(self.profile_path, ev.to_jsonable())
 
     def profiling_summary(self) -> dict[str, object]:
-        return {"events": list(self._profile_events), "memory_ledger": self.memory_ledger().to_jsonable()}
+        totals: dict[str, float] = {}
+        for ev in self._profile_events:
+            totals[ev.name] = totals.get(ev.name, 0.0) + ev.seconds
+        return {"events": [ev.to_jsonable() for ev in self._profile_events],
+                "total_seconds_by_event": totals,
+                "memory_ledger": self.memory_ledger().to_jsonable()}
+
+    def _collect_stage_profile(self, step_id: int) -> bool:
+        """Decode staging events go out when a profile path (or
+        LATCHMOE_PROFILE) is set, on every sample-rate-th step."""
+        if not (self.profile_path or os.environ.get("LATCHMOE_PROFILE")):
+            return False
+        rate = _decode_profile_sample_rate()
+        return rate <= 1 or int(step_id) % rate == 0
 
     # --------------------------------------------------------- predicates
     @property
@@ -813,12 +844,15 @@ class MoeOffloadRuntime:
                  for e, sid in zip(misses, (v for v, m in zip(slot_list, is_miss) if m))]
         ready = None
         table_updates = -1
+        t_load = perf_counter()
+        load_sync_ms = load_enqueue_ms = 0.0
         if loads and not self.config.async_load:
             try:
                 self._transfer_engine.load_many_sync(loads, validate_layout=False)
             except Exception:
                 self._release_allocated_loads(bank, loads)
                 raise
+            load_sync_ms = (perf_counter() - t_load) * 1000.0
         elif loads:
             # device bank and table: the changed log2phy entries ride with the
             # copies on the transfer stream, inside their ready event
@@ -837,8 +871,9 @@ class MoeOffloadRuntime:
             if with_table:
                 self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd[0], slot_ids=upd[1])
                 table_updates = len(upd[0])
+            load_enqueue_ms = (perf_counter() - t_load) * 1000.0
         return PendingFixedSlotStage(layer_id, active, tuple(slot_list), bank.owners(), ready, hits, misses,
-                                     log2phy, step_id, t0, table_updates)
+                                     log2phy, step_id, t0, table_updates, load_sync_ms, load_enqueue_ms)
 
     def _raise_no_slot(self, layer_id: int, expert_id: int, bank: ExpertSlotBank) -> None:
         raise RuntimeError(
@@ -850,8 +885,10 @@ class MoeOffloadRuntime:
         layer_id = pending.layer_id
         bank = self._slot_banks[layer_id]
         # order the copies before the consumer, THEN publish the mapping
+        t_wait = perf_counter()
         if pending.ready is not None:
             self._wait_transfer_event(pending.ready)
+        t_map = perf_counter()
         active, slot_ids = pending.active, pending.slot_ids
         if pending.table_updates >= 0:
             n_updates = pending.table_updates  # written on the transfer stream with the copies
@@ -864,31 +901,36 @@ class MoeOffloadRuntime:
         mapping = ExpertSlotMapping(layer_id, active, pending.log2phy, tuple(pending.owners), tuple(slot_ids))
         self._active_slot_ids_by_layer[layer_id] = tuple(slot_ids)
         self.last_stage_stats = (len(pending.hits), len(pending.misses))
-        if record_stage_profile and (self.config.profile_path or os.environ.get("LATCHMOE_PROFILE")):
+        if record_stage_profile and self._collect_stage_profile(pending.step_id):
+            now = perf_counter()
             per = int(self._expert_weight_bytes_by_layer.get(layer_id, 0))
-            self._record_profile_event(
-                "decode_fixed_slot_stage",
-                layer_id=layer_id,
-                start=pending.started,
-                payload={
-                    "n_active": len(active),
-                    "n_hits": len(pending.hits),
-                    "n_misses": len(pending.misses),
-                    "hit_rate": round(len(pending.hits) / len(active), 6) if active else 0.0,
-                    "h2d_bytes": per * len(pending.misses),
-                    "step_id": pending.step_id,
-                    "num_slots": int(self.config.num_slots),
-                    "mapping_mode": "persistent_log2phy",
-                    "log2phy_update_count": n_updates,
-                    "stage_mode": "main_slot_hit" if not pending.misses else (
-                        "async_decode_load_many" if pending.ready is not None else "sync_decode_load"),
-                    "consumer_dependency_installed": True,
-                    "mapping_published_after_ready": True,
-                    "active_experts": list(active),
-                    "hit_experts": list(pending.hits),
-                    "miss_experts": list(pending.misses),
-                },
-            )
+            payload = {
+                "n_active": len(active),
+                "n_hits": len(pending.hits),
+                "n_misses": len(pending.misses),
+                "hit_rate": round(len(pending.hits) / len(active), 6) if active else 0.0,
+                "h2d_bytes": per * len(pending.misses),
+                "stage_ms": round((now - pending.started) * 1000.0, 3),
+                "load_sync_ms": round(pending.load_sync_ms, 3),
+                "load_enqueue_ms": round(pending.load_enqueue_ms, 3),
+                "ready_wait_ms": round((t_map - t_wait) * 1000.0, 3),
+                "mapping_ms": round((now - t_map) * 1000.0, 3),
+                "step_id": pending.step_id,
+                "num_slots": int(self.config.num_slots),
+                "mapping_mode": "persistent_log2phy",
+                "log2phy_update_count": n_updates,
+                "stage_mode": "main_slot_hit" if not pending.misses else (
+                    "async_decode_load_many" if pending.ready is not None else "sync_decode_load"),
+                "consumer_dependency_installed": True,
+                "mapping_published_after_ready": True,
+                "profile_sample_rate": _decode_profile_sample_rate(),
+            }
+            if _profile_expert_lists_enabled():
+                payload.update({"active_experts": list(active), "hit_experts": list(pending.hits),
+                                "miss_experts": list(pending.misses)})
+            else:
+                payload["expert_lists"] = "omitted"
+            self._record_profile_event("decode_fixed_slot_stage", layer_id=layer_id, start=t_map, payload=payload)
         return PreparedSlotWeights.from_slot_bank(slot_bank=bank, mapping=mapping)
 
     def _changed_log2phy_entries(self, *, layer_id: int, expert_ids, slot_ids) -> tuple[tuple[int, ...], tuple[int, ...]]:
@@ -1315,6 +1357,17 @@ class MoeOffloadRuntime:
 
 
 # ---------------------------------------------------------------------------
+def _decode_profile_sample_rate() -> int:
+    try:
+        return max(1, int(os.environ.get("VLLM_ASCEND_MOE_DECODE_PROFILE_SAMPLE_RATE", "1")))
+    except ValueError:
+        return 1
+
+
+def _profile_expert_lists_enabled() -> bool:
+    return os.environ.get("VLLM_ASCEND_MOE_PROFILE_EXPERT_LISTS", "1").strip().lower() not in {"0", "false", "no", "off"}
+
+
 def _synchronize_event(ev: object) -> None:
     sync = getattr(ev, "synchronize", None)
     if callable(sync):

@@ -35,6 +35,7 @@ PATCH_TAG = "vllm_moe_offload_amd.moe_comm_method_runtime"
 SELECT_TAG = "vllm_moe_offload_amd.select_experts"
 ENGINE_TAG = "vllm_moe_offload_amd.engine_args"
 WEIGHTS_TAG = "vllm_moe_offload_amd.cpu_first_weights"
+REPLAY_TAG = "vllm_moe_offload_amd.graph_replay_profile"
 
 # the quant method's apply() publishes its layer here for select_experts
 _layer_ctx = threading.local()
@@ -314,6 +315,57 @@ def _patch_engine_args_autoconfig(arg_utils=None) -> bool:
     return True
 
 
+def _patch_graph_replay_profile(graph_mod=None, context_mod=None) -> bool:
+    """Sample the host-side issue time of hipGraph replays (the first replay,
+    then every N-th, N = VLLM_ASCEND_MOE_GRAPH_REPLAY_PROFILE_SAMPLE_RATE,
+    default 1024) as graph_replay_issue events; nothing synchronizes the
+    device.  Only replays count: capture and eager calls pass through.
+    Reference: patches/patch_fused_moe.py:1603-1667."""
+    try:
+        graph_mod = graph_mod or importlib.import_module("vllm.compilation.cuda_graph")
+        context_mod = context_mod or importlib.import_module("vllm.forward_context")
+    except Exception:
+        return False
+    wrapper = getattr(graph_mod, "CUDAGraphWrapper", None)
+    current = getattr(wrapper, "__call__", None) if wrapper is not None else None
+    get_context = getattr(context_mod, "get_forward_context", None)
+    if current is None or get_context is None:
+        return False
+    if _is_tagged(current, REPLAY_TAG):
+        return True
+    original = current
+
+    def __call__(self, *args, **kwargs):
+        ctx = get_context()
+        mode = getattr(ctx, "cudagraph_runtime_mode", None)
+        entry = (getattr(self, "concrete_cudagraph_entries", None) or {}).get(getattr(ctx, "batch_descriptor", None))
+        if mode is None or mode != getattr(self, "runtime_mode", None) or getattr(entry, "cudagraph", None) is None:
+            return original(self, *args, **kwargs)
+        count = int(getattr(self, "_latchmoe_replay_calls", 0)) + 1
+        self._latchmoe_replay_calls = count
+        try:
+            rate = max(1, int(os.environ.get("VLLM_ASCEND_MOE_GRAPH_REPLAY_PROFILE_SAMPLE_RATE", "1024")))
+        except ValueError:
+            rate = 1024
+        if not (count == 1 or count % rate == 0):
+            return original(self, *args, **kwargs)
+        from time import perf_counter
+
+        from vllm_moe_offload_amd.moe_offload.runtime import get_moe_offload_runtime
+
+        start = perf_counter()
+        out = original(self, *args, **kwargs)
+        get_moe_offload_runtime()._record_profile_event(
+            "graph_replay_issue", layer_id=None, start=start,
+            payload={"profile_sample_rate": 1 if count == 1 else rate, "replay_call_index": count,
+                     "runtime_mode": str(mode), "synchronizes_npu": False, "synchronizes_device": False},
+        )
+        return out
+
+    wrapper.__call__ = _tagged(__call__, REPLAY_TAG)
+    return True
+
+
 def _stage_seam_enabled() -> bool:
     from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
 
@@ -324,7 +376,7 @@ def _stage_seam_enabled() -> bool:
 def apply_patches() -> dict[str, bool]:
     """Install every hook whose target the installed vLLM provides."""
     done = {"comm_method": False, "select_experts": False, "quant_apply": False, "quant_weights": False,
-            "engine_args": False}
+            "engine_args": False, "graph_replay_profile": False}
     for mod in ("vllm.model_executor.layers.fused_moe.moe_comm_method",
                 "vllm_ascend.ops.fused_moe.moe_comm_method"):
         try:
@@ -345,4 +397,5 @@ def apply_patches() -> dict[str, bool]:
             done["quant_apply"] = _patch_quant_method_apply(method)
             done["quant_weights"] = _patch_quant_method_weights(method)
     done["engine_args"] = _patch_engine_args_autoconfig()
+    done["graph_replay_profile"] = _patch_graph_replay_profile()
     return done
