@@ -457,3 +457,102 @@ def test_wave_prefill_writes_work_conserving_evidence(tmp_path, monkeypatch):
     assert p["masked_full_prompt_pairs"] - p["work_conserving_saved_pairs"] == T * k
     assert set(p["control_ms"]) >= {"token_count", "readiness", "wave_plan", "schedule", "loop", "scatter_total",
                                     "end_to_end"}
+
+
+def test_decode_overflow_two_pass_equals_one_bank_bitwise_eager_and_replayed():
+    """A decode step whose routed experts exceed the bank runs the bank pass
+    plus one overflow pass (stage buffer) and equals, bit for bit, the same
+    step on a bank that holds every expert; a graph captured once with both
+    passes replays any later split, a step without overflow included."""
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(41)
+    E, H, I, k, T = 64, 1024, 256, 8, 16
+    w13, w2, wg = _weights(rng, E, H, I)
+    t13 = torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16)
+    t2 = torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16)
+    gate = to_dev_bf16(wg)
+    common = dict(enabled=True, async_load=True, pin_host_memory=True, graph_compatible_offload=True)
+    rt_a = Runtime(Cfg(num_slots=32, decode_overflow=True, **common))
+    rt_b = Runtime(Cfg(num_slots=64, **common))
+    la = SlotMoELayer(layer_id=70, runtime=rt_a, gate_weight=gate, w13_weight=t13, w2_weight=t2, top_k=k)
+    lb = SlotMoELayer(layer_id=71, runtime=rt_b, gate_weight=gate, w13_weight=t13, w2_weight=t2, top_k=k)
+    la.register()
+    lb.register()
+    spec = la.router_spec
+    ws_a = fused_moe.get_workspace(T, k, 32, H, I, torch.device("cuda"), tag="ovf_a")
+    ws_b = fused_moe.get_workspace(T, k, 64, H, I, torch.device("cuda"), tag="ovf_b")
+    static_x = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    out_a = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+
+    def stage(rt, layer_id, x):
+        w, ids, _ = fused_moe.route(x, gate, spec)
+        flat = ids.cpu().flatten().tolist()
+        counts = {e: flat.count(e) for e in set(flat)}
+        return rt.stage_fixed_slot_plan(layer_id=layer_id, active_experts=tuple(sorted(counts)),
+                                        num_logical_experts=E, token_counts=counts), len(counts)
+
+    def run_a():
+        ovf = rt_a.decode_overflow_slot_weights(layer_id=70, n_pairs=T * k)
+        fused_moe.decode_layer(static_x, gate, spec, rt_a.slot_bank(70).w13_slots, rt_a.slot_bank(70).w2_slots,
+                               rt_a.log2phy_buffer(70), workspace=ws_a, out=out_a, overflow=ovf)
+
+    graph = None
+    inputs = [normal_bf16(rng, (T, H), 1.0) for _ in range(3)] + [np.zeros((T, H), np.uint16)] + \
+        [normal_bf16(rng, (T, H), 1.0) for _ in range(2)]
+    n_over = []
+    for step, x in enumerate(inputs):
+        dx = to_dev_bf16(x)
+        static_x.copy_(dx)
+        pa, n_active = stage(rt_a, 70, dx)
+        n_over.append(0 if pa.overflow is None else len(pa.overflow.mapping.active_experts))
+        print(f"case overflow step {step} n_active={n_active} overflow={n_over[-1]}", flush=True)
+        if graph is None:
+            run_a()  # eager first (allocates the overflow permutation)
+        else:
+            graph.replay()
+        rt_a.record_layer_compute(70)
+        stage(rt_b, 71, dx)
+        out_b, _, _ = fused_moe.decode_layer(dx, gate, spec, rt_b.slot_bank(71).w13_slots,
+                                             rt_b.slot_bank(71).w2_slots, rt_b.log2phy_buffer(71), workspace=ws_b)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)), step
+        if step == 0:
+            ref = _oracle_layer(x, *(lambda w, i: (i.cpu().numpy(), from_dev_bf16(w)))(
+                *fused_moe.route(dx, gate, spec)[:2]), w13, w2)
+            assert rel_max_err(bf16_to_f32(from_dev_bf16(out_a)), ref) <= OUT_TOL
+            torch.cuda.synchronize()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                run_a()
+            torch.cuda.current_stream().wait_stream(s)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                run_a()
+            rt_a.record_layer_compute(70)
+    assert max(n_over) > 0 and n_over[3] == 0, n_over  # overflow steps and one without
+
+
+def test_decode_overflow_through_the_layer_seam_equals_one_bank():
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(43)
+    E, H, I, k, T = 64, 512, 256, 6, 10
+    w13, w2, wg = _weights(rng, E, H, I)
+    t13 = torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16)
+    t2 = torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16)
+    gate = to_dev_bf16(wg)
+    common = dict(enabled=True, async_load=True, pin_host_memory=True)
+    la = SlotMoELayer(layer_id=72, runtime=Runtime(Cfg(num_slots=24, decode_overflow=True, **common)),
+                      gate_weight=gate, w13_weight=t13, w2_weight=t2, top_k=k)
+    lb = SlotMoELayer(layer_id=73, runtime=Runtime(Cfg(num_slots=64, **common)), gate_weight=gate,
+                      w13_weight=t13, w2_weight=t2, top_k=k)
+    la.register()
+    lb.register()
+    for step in range(4):
+        print(f"case seam overflow step {step}", flush=True)
+        dx = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
+        a = la.forward(dx).clone()
+        b = lb.forward(dx).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), step
+    assert la.runtime.transfer_engine.bytes_issued > lb.runtime.transfer_engine.bytes_issued

@@ -2,6 +2,7 @@
 plan on CPU slot banks (no GPU).  Expected values are the golden vectors of
 the reference's own tests (file:line cited per test)."""
 
+import numpy as np
 import pytest
 import torch
 
@@ -545,3 +546,79 @@ def test_register_host_buffers_uses_buffers_in_place():
     rt.capture_safe_slot_weights(layer_id=5)
     with pytest.raises(RuntimeError, match="already captured"):
         rt.register_host_buffers(layer_id=5, w13_host=w13, w2_host=w2, slot_device=CPU)
+
+
+# ------------------------------------------------------------ decode overflow
+def _expert_rows(layer, e):
+    return layer.w13_weight[e].detach(), layer.w2_weight[e].detach()
+
+
+def test_decode_overflow_keeps_residents_in_the_bank_and_stages_the_rest():
+    rt = _rt(num_slots=3, graph_compatible_offload=True, decode_overflow=True)
+    layer = TinyLayer(experts=8)
+    rt.register_layer_for_fixed_slots(layer, slot_device=CPU)
+    first = rt.stage_fixed_slot_plan(layer_id=7, active_experts=(0, 1, 2), num_logical_experts=8)
+    assert first.overflow is None
+    p = rt.stage_fixed_slot_plan(layer_id=7, active_experts=(4, 0, 3, 1, 2), num_logical_experts=8,
+                                 token_counts={3: 5, 4: 1, 0: 1, 1: 1, 2: 1})
+    main = rt.log2phy_buffer(7).tolist()
+    assert sorted(p.mapping.active_experts) == [0, 1, 2]  # the residents stay: three hits
+    assert main[3] == -1 and main[4] == -1
+    ovf = p.overflow
+    assert ovf is not None and ovf.mapping.active_experts == (3, 4)  # more tokens first
+    assert ovf.log2phy.tolist() == [-1, -1, -1, 0, 1, -1, -1, -1]
+    for e, s in ((3, 0), (4, 1)):
+        w13, w2 = _expert_rows(layer, e)
+        assert torch.equal(ovf.w1[s], w13) and torch.equal(ovf.w2[s], w2)
+    assert rt.decode_overflow_slot_weights(layer_id=7).log2phy.data_ptr() == ovf.log2phy.data_ptr()
+    # a hot miss takes the least recently used non-active slot, a cold one overflows
+    p = rt.stage_fixed_slot_plan(layer_id=7, active_experts=(6, 5, 0, 1), num_logical_experts=8,
+                                 token_counts={5: 9, 6: 2, 0: 1, 1: 1})
+    main = rt.log2phy_buffer(7).tolist()
+    assert sorted(p.mapping.active_experts) == [0, 1, 5] and main[6] == -1
+    w13, _ = _expert_rows(layer, 5)
+    assert torch.equal(p.w1[main[5]], w13)
+    assert p.overflow.log2phy.tolist() == [-1] * 6 + [0, -1]
+    # a step without overflow clears the table the last one left
+    p = rt.stage_fixed_slot_plan(layer_id=7, active_experts=(0,), num_logical_experts=8)
+    assert p.overflow is None and rt.decode_overflow_slot_weights(layer_id=7).log2phy.tolist() == [-1] * 8
+
+
+def test_decode_overflow_bounds_and_switch():
+    rt = _rt(num_slots=2, decode_overflow=True)
+    rt.register_layer_for_fixed_slots(TinyLayer(experts=8), slot_device=CPU)
+    assert rt.can_stage_decode_overflow(layer_id=7, active_expert_count=4)
+    assert not rt.can_stage_decode_overflow(layer_id=7, active_expert_count=5)  # past one extra pass
+    assert not rt.can_stage_decode_overflow(layer_id=7, active_expert_count=2)  # fits the bank
+    with pytest.raises(RuntimeError, match="exceeds num_slots=2"):
+        rt.stage_fixed_slot_plan(layer_id=7, active_experts=(0, 1, 2, 3, 4), num_logical_experts=8)
+    assert rt.decode_overflow_slot_weights(layer_id=7, n_pairs=2) is None  # cannot overflow
+    off = _rt(num_slots=2)
+    off.register_layer_for_fixed_slots(TinyLayer(experts=8), slot_device=CPU)
+    with pytest.raises(RuntimeError, match="exceeds num_slots=2"):
+        off.stage_fixed_slot_plan(layer_id=7, active_experts=(0, 1, 2), num_logical_experts=8)
+    assert off.decode_overflow_slot_weights(layer_id=7) is None
+
+
+def test_decode_overflow_split_covers_every_expert_once():
+    from vllm_moe_offload_amd.moe_offload.runtime import _split_decode_overflow
+
+    rng = np.random.default_rng(5)
+    for trial in range(50):
+        P = int(rng.integers(1, 9))
+        rt = _rt(num_slots=P, decode_overflow=True)
+        rt.register_layer_for_fixed_slots(TinyLayer(experts=24), slot_device=CPU)
+        bank = rt.slot_bank(7)
+        warm = tuple(int(e) for e in rng.choice(24, size=P, replace=False))
+        rt.stage_fixed_slot_plan(layer_id=7, active_experts=warm, num_logical_experts=24)
+        n = int(rng.integers(P + 1, 2 * P + 1))
+        active = tuple(int(e) for e in rng.choice(24, size=n, replace=False))
+        counts = {e: int(rng.integers(1, 9)) for e in active}
+        main, over = _split_decode_overflow(bank, active, P, counts)
+        assert len(main) == P and sorted(main + over) == sorted(active)
+        assert set(warm) & set(active) <= set(main)  # residents are never pushed out
+        prepared = rt.stage_fixed_slot_plan(layer_id=7, active_experts=active, num_logical_experts=24,
+                                            token_counts=counts)
+        table, otab = rt.log2phy_buffer(7).tolist(), prepared.overflow.log2phy.tolist()
+        for e in active:  # every routed expert maps in exactly one of the two tables
+            assert (table[e] >= 0) != (otab[e] >= 0), (trial, e)

@@ -90,3 +90,64 @@ def test_stage_op_stages_or_defers_overflow_to_waves():
         assert rt.consume_prefill_route_stats(layer_id=3, topk_ids=big) == {0: 1, 1: 1, 2: 1, 3: 1}
     finally:
         rtm.reset_moe_offload_runtime()
+
+
+def test_stage_op_stages_a_decode_overflow_pass_instead_of_waves():
+    from vllm_moe_offload_amd.moe_offload import runtime as rtm
+    from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+    from vllm_moe_offload_amd.ops.fused_moe.moe_offload_stage_op import PHASE_DECODE, PHASE_PREFILL, _moe_offload_stage_impl
+
+    class L(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layer_id = 3
+            self.w13_weight = torch.nn.Parameter(torch.arange(12.0).reshape(6, 2, 1))
+            self.w2_weight = torch.nn.Parameter(torch.arange(6.0).reshape(6, 1, 1))
+
+    rtm._runtime = rtm.MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=2, b2_wave_prefill=True,
+                                                          decode_overflow=True))
+    try:
+        rt = rtm._runtime
+        rt.register_layer_for_fixed_slots(L(), slot_device=torch.device("cpu"))
+        ids = torch.tensor([[0, 1], [2, 1], [3, 1]], dtype=torch.int32)  # 4 experts, 2 slots
+        _moe_offload_stage_impl(ids, 3, 6, PHASE_DECODE)
+        main, ovf = rt.log2phy_buffer(3).tolist(), rt.decode_overflow_slot_weights(layer_id=3).log2phy.tolist()
+        assert rt.consume_prefill_route_stats(layer_id=3, topk_ids=ids) is None  # not deferred
+        assert [e for e in range(6) if main[e] >= 0] == [0, 1]  # expert 1 (3 tokens) first, then id order
+        assert [e for e in range(6) if ovf[e] >= 0] == [2, 3]
+        # a prefill-phase overflow still goes to the waves
+        _moe_offload_stage_impl(ids, 3, 6, PHASE_PREFILL)
+        assert rt.consume_prefill_route_stats(layer_id=3, topk_ids=ids) == {0: 1, 1: 3, 2: 1, 3: 1}
+    finally:
+        rtm.reset_moe_offload_runtime()
+
+
+def test_stage_op_stages_a_regime_a_layer_whose_full_residency_was_not_staged():
+    """Slots >= experts without graph mode: nothing staged the table at
+    registration, so the seam stages per step instead of leaving the pairs
+    unmapped."""
+    from vllm_moe_offload_amd.moe_offload import runtime as rtm
+    from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+    from vllm_moe_offload_amd.ops.fused_moe.moe_offload_stage_op import PHASE_DECODE, _moe_offload_stage_impl
+
+    class L(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layer_id = 3
+            self.w13_weight = torch.nn.Parameter(torch.zeros(4, 2, 1))
+            self.w2_weight = torch.nn.Parameter(torch.zeros(4, 1, 1))
+
+    for graph_mode in (False, True):
+        rtm._runtime = rtm.MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=4,
+                                                              graph_compatible_offload=graph_mode))
+        try:
+            rt = rtm._runtime
+            rt.register_layer_for_fixed_slots(L(), slot_device=torch.device("cpu"))
+            assert rt.stage_full_residency_slot_plan(layer_id=3) is graph_mode
+            _moe_offload_stage_impl(torch.tensor([[2, 1]], dtype=torch.int32), 3, 4, PHASE_DECODE)
+            table = rt.log2phy_buffer(3).tolist()
+            assert table[1] >= 0 and table[2] >= 0
+            if graph_mode:
+                assert table == [0, 1, 2, 3]  # the static table, untouched by the seam
+        finally:
+            rtm.reset_moe_offload_runtime()

@@ -49,6 +49,13 @@ class MoEWorkspace:
     act: torch.Tensor   # [N, I] bf16, sorted order
     y: torch.Tensor     # [N, H] bf16, flat pair order
     out: torch.Tensor   # [T, H] bf16
+    perm_overflow: native.Permutation | None = None  # the decode overflow pass's permutation
+
+    def overflow_perm(self, n_pairs: int, n_slots: int, device) -> native.Permutation:
+        p = self.perm_overflow
+        if p is None or p.n_pairs != int(n_pairs) or p.n_slots != int(n_slots):
+            p = self.perm_overflow = native.Permutation.allocate(int(n_pairs), int(n_slots), device)
+        return p
 
 
 _WORKSPACES: dict[tuple, MoEWorkspace] = {}
@@ -151,10 +158,26 @@ def fused_experts(
                              path=path, workspace=workspace)[0]
 
 
+def _overflow_pass(hidden, topk_ids, k: int, overflow: PreparedSlotWeights, ws: MoEWorkspace, *, decode: bool):
+    """Second pass of a decode step whose routed experts exceed the bank:
+    the pairs the overflow table maps (every other pair is skipped) run from
+    the stage buffer into their rows of y."""
+    T, H = hidden.shape
+    P2 = int(overflow.physical_expert_count)
+    I = int(overflow.w1.shape[1]) // 2
+    perm = ws.overflow_perm(T * k, P2, hidden.device)
+    bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P2, H, I, hidden.device, n_pairs=T * k)
+    native.permute(topk_ids, perm, log2phy=overflow.log2phy, skip_unmapped=True, block_m=bm)
+    native.grouped_mlp(hidden, k, overflow.w1, overflow.w2, perm, ws.act[: T * k], ws.y[: T * k],
+                       path=native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA)
+
+
 def _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2phy, *, add=None, out=None,
-                      path=native.LMOE_PATH_AUTO, workspace=None, events=None):
+                      path=native.LMOE_PATH_AUTO, workspace=None, events=None, overflow=None):
     """fused_experts returning (out, workspace); events = three torch events
-    recorded before the permutation, before GMM2 and before the combine."""
+    recorded before the permutation, before GMM2 and before the combine.
+    overflow: the decode overflow pass (the bank pass then skips the pairs
+    its table leaves unmapped, the combine sums both passes' rows)."""
     T, H = hidden.shape
     k = int(topk_ids.shape[1])
     P = int(w13_slots.shape[0])
@@ -167,7 +190,18 @@ def _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2p
     bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P, H, I, hidden.device, n_pairs=T * k)
     if events:
         events[0].record()
-    native.permute(topk_ids, ws.perm, log2phy=log2phy, block_m=bm)
+    native.permute(topk_ids, ws.perm, log2phy=log2phy, skip_unmapped=overflow is not None, block_m=bm)
+    if overflow is not None:
+        mlp_path = native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA
+        native.gateup_silu(hidden, k, w13_slots, ws.perm, ws.act[: T * k], path=mlp_path)
+        if events:
+            events[1].record()
+        native.down(ws.act[: T * k], w2_slots, ws.perm, ws.y[: T * k], path=mlp_path)
+        _overflow_pass(hidden, topk_ids, k, overflow, ws, decode=decode)
+        if events:
+            events[2].record()
+        native.combine(ws.y[: T * k], topk_weights, dst, add=add)
+        return dst, ws
     if decode:
         if events:  # the decode body fuses GMM2 with the combine
             events[1].record()
@@ -208,12 +242,16 @@ def decode_layer(
     logits_out: torch.Tensor | None = None,
     w_out: torch.Tensor | None = None,
     ids_out: torch.Tensor | None = None,
+    overflow: PreparedSlotWeights | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """route() followed by fused_experts(), for a slot table that is final
     before the router runs (the decode replay after staging): gate, expert
     selection and permutation (one launch for up to
-    ONE_LAUNCH_ROUTER_MAX_TOKENS tokens), then the decode MLP body.  Returns (out, topk_weights, topk_ids), equal bit for bit to the
-    separate calls."""
+    ONE_LAUNCH_ROUTER_MAX_TOKENS tokens), then the decode MLP body.  Returns
+    (out, topk_weights, topk_ids), equal bit for bit to the separate calls.
+    overflow: the layer's second pass (stage buffer + overflow table) for a
+    working set past the bank; both passes and the combine are fixed-shape
+    launches, so a graph captured with them replays any split."""
     T = hidden.shape[0]
     k = int(spec.top_k)
     kw = k + int(spec.n_shared)  # pairs per token, shared suffix included
@@ -230,7 +268,7 @@ def decode_layer(
         num_expert_group=int(spec.num_expert_group or 1) if grouped else 1,
         topk_group=int(spec.topk_group or 1) if grouped else 1,
         renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
-        n_shared=int(spec.n_shared), w_bf16=w_out, ids=ids_out,
+        n_shared=int(spec.n_shared), w_bf16=w_out, ids=ids_out, skip_unmapped=overflow is not None,
     )
     if T <= ONE_LAUNCH_ROUTER_MAX_TOKENS:
         w, ids, _ = native.router_gate_topk_permute(hidden, gate_weight, logits_out, k, ws.perm, **sel)
@@ -239,6 +277,13 @@ def decode_layer(
         w, ids, _ = native.router_topk_permute(logits, k, ws.perm, **sel)
     dst = out if out is not None else ws.out[:T]
     I = int(w13_slots.shape[1]) // 2
+    if overflow is not None:
+        decode = T * kw <= native.FUSED_DECODE_MAX_PAIRS and I <= native.GEMV_MAX_I
+        native.grouped_mlp(hidden, kw, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], ws.y[: T * kw],
+                           path=native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA)
+        _overflow_pass(hidden, ids, kw, overflow, ws, decode=decode)
+        native.combine(ws.y[: T * kw], w, dst, add=add)
+        return dst, w, ids
     if T * kw <= native.FUSED_DECODE_MAX_PAIRS and I <= native.GEMV_MAX_I:
         # router-fed ids: distinct experts per token, in distinct slots
         native.fused_moe_decode(hidden, w, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], dst, add=add,
@@ -348,7 +393,8 @@ def check_supported_input(inp) -> None:
             raise RuntimeError("expert_map (expert parallelism) is not supported on one GPU")
 
 
-def run_fused_experts_contract(inp, *, result_cls=FusedExpertsResult, record_events: bool = False):
+def run_fused_experts_contract(inp, *, result_cls=FusedExpertsResult, record_events: bool = False,
+                               overflow: PreparedSlotWeights | None = None):
     """The hook's body: experts over the input's weights (a slot bank with
     its log2phy when prepared), returning the result contract with the
     per-slot token counts (group_list_type 1) and, if asked for, the events
@@ -364,7 +410,7 @@ def run_fused_experts_contract(inp, *, result_cls=FusedExpertsResult, record_eve
         ids = ids.to(torch.int32)
     evts = [torch.cuda.Event() for _ in range(3)] if record_events else None
     out, ws = _fused_experts_ws(hidden, w, ids.contiguous(), w1, w2, log2phy,
-                                add=getattr(inp, "shared_output", None), events=evts)
+                                add=getattr(inp, "shared_output", None), events=evts, overflow=overflow)
     P = int(w1.shape[0])
     return result_cls(
         routed_out=out,
@@ -401,12 +447,19 @@ class MoECommMethod:
         return self._with_prepared_slot_weights(inp, prepared)
 
     def fused_experts(self, inp) -> FusedExpertsResult:
+        off = getattr(inp, "offload", None)
+        overflow = None
+        if off is not None and off.enabled:
+            overflow = self.runtime.decode_overflow_slot_weights(layer_id=int(off.layer_id),
+                                                                 n_pairs=int(inp.topk_ids.numel()))
         inp = self._maybe_apply_moe_offload_plan(inp)
         try:
-            return run_fused_experts_contract(inp)
+            return run_fused_experts_contract(inp, overflow=overflow)
         finally:
             self.runtime.end_slot_compute(self._slot_compute_handle)
             self._slot_compute_handle = None
+            if overflow is not None:
+                self.runtime.end_overflow_compute(int(off.layer_id))
 
 
 def with_slot_weights(inp, prepared: PreparedSlotWeights, *, offload_enabled=None, use_log2phy: bool = True,

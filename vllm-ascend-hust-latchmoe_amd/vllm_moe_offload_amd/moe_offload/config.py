@@ -60,6 +60,10 @@ class MoeOffloadConfig:
     cpu_first_load: bool = False
     # drop a layer's original expert tensors once its host store is complete
     release_original_expert_weights: bool = False
+    # decode whose routed experts exceed the slots: the first num_slots run
+    # from the bank, the rest (at most num_slots more) from a stage buffer in
+    # a second pass of the same captured graph, instead of eager waves
+    decode_overflow: bool = False
 
     @classmethod
     def from_env(cls) -> "MoeOffloadConfig":
@@ -82,6 +86,7 @@ class MoeOffloadConfig:
             profile_path=_env("PROFILE_PATH", ""),
             cpu_first_load=_bool("CPU_FIRST_LOAD", False),
             release_original_expert_weights=_bool("RELEASE_ORIGINAL_EXPERT_WEIGHTS", False),
+            decode_overflow=_bool("DECODE_OVERFLOW", False),
         )
 
     @property

@@ -178,6 +178,20 @@ class PendingFixedSlotStage:
     table_updates: int = -1  # entries already written with the copies (-1: publish writes them)
     load_sync_ms: float = 0.0
     load_enqueue_ms: float = 0.0
+    overflow: "DecodeOverflowStage | None" = None
+
+
+@dataclass
+class DecodeOverflowStage:
+    """Routed experts of a decode step past the bank's capacity, staged into
+    stage buffer `buffer_index` (slot i <- i-th expert) with the layer's own
+    overflow table (expert -> stage slot, -1 elsewhere)."""
+
+    buffer_index: int
+    bank: ExpertSlotBank
+    table: torch.Tensor
+    experts: tuple[int, ...]
+    ready: object | None
 
 
 @dataclass(frozen=True)
@@ -237,6 +251,13 @@ class MoeOffloadRuntime:
         self._prefill_route_stats_by_layer: dict[int, MoePrefillRouteStats] = {}
         self._active_slot_ids_by_layer: dict[int, tuple[int, ...]] = {}
         self._compute_fences: dict[int, list] = {}
+        # decode overflow: per-layer fixed-address tables, layers whose table
+        # holds entries, and stage buffers awaiting their compute's release
+        self._overflow_tables: dict[int, torch.Tensor] = {}
+        self._overflow_dirty: set[int] = set()
+        self._overflow_release_pending: dict[int, int] = {}
+        # layers whose table holds every routed expert (static residency)
+        self._full_residency_layers: set[int] = set()
         self._layer_release_events: dict[int, object] = {}
         self._placement_plan_provider: PlacementPlanProvider | None = None
         self._fixed_slot_execution_state = threading.local()
@@ -413,6 +434,7 @@ class MoeOffloadRuntime:
         bank.install_pinned_log2phy(table)
         self._log2phy_buffers[layer_id] = table
         self._log2phy_slot_by_expert[layer_id] = {}
+        self._full_residency_layers.discard(layer_id)
         self._memory_ledger_cache = None
         self._record_profile_event(
             "register_layer_for_fixed_slots",
@@ -451,6 +473,7 @@ class MoeOffloadRuntime:
         self._fused_shared_lane_layouts.pop(layer_id, None)
         self._log2phy_buffers[layer_id] = torch.full((E,), -1, dtype=torch.int32, device=slot_device)
         self._log2phy_slot_by_expert[layer_id] = {}
+        self._full_residency_layers.discard(layer_id)
         self._memory_ledger_cache = None
 
     # ----------------------------------------------------------- queries
@@ -725,6 +748,7 @@ class MoeOffloadRuntime:
         ev = self._record_current_stream_event_or_none()
         if ev is not None:
             self._layer_release_events[int(layer_id)] = ev
+        self.end_overflow_compute(int(layer_id))
 
     # ------------------------------------------------------ decode staging
     def _compute_device_index(self) -> int | None:
@@ -780,7 +804,8 @@ class MoeOffloadRuntime:
                                           num_logical_experts=num_logical_experts, log2phy=log2phy, step_id=step_id)
         return self._publish(pending, record_stage_profile=record_stage_profile)
 
-    def prefetch_fixed_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int) -> PendingFixedSlotStage:
+    def prefetch_fixed_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int,
+                                 token_counts: dict[int, int] | None = None) -> PendingFixedSlotStage:
         """Reserve slots and queue the miss copies on the transfer stream now;
         publish later with complete_fixed_slot_plan (after the previous layer's
         kernels are queued), so the copies overlap that compute."""
@@ -792,7 +817,8 @@ class MoeOffloadRuntime:
         )
         self._assert_locked_slot_addresses(int(layer_id))
         return self._reserve_and_issue(layer_id=layer_id, active_experts=active, num_logical_experts=num_logical_experts,
-                                       log2phy=self._log2phy_buffers[int(layer_id)], step_id=None)
+                                       log2phy=self._log2phy_buffers[int(layer_id)], step_id=None,
+                                       token_counts=token_counts)
 
     def complete_fixed_slot_plan(self, pending: PendingFixedSlotStage) -> PreparedSlotWeights:
         """Order the prefetched copies before the current stream, then publish."""
@@ -801,7 +827,7 @@ class MoeOffloadRuntime:
         return PreparedSlotWeights(prepared.w1, prepared.w2, buf, prepared.physical_expert_count, prepared.mapping)
 
     def _reserve_and_issue(self, *, layer_id: int, active_experts, num_logical_experts: int, log2phy: torch.Tensor,
-                           step_id: int | None) -> PendingFixedSlotStage:
+                           step_id: int | None, token_counts: dict[int, int] | None = None) -> PendingFixedSlotStage:
         if not self.should_use_fixed_slots:
             raise RuntimeError("fixed-slot plan requested while moe offload fixed slots are disabled")
         layer_id = int(layer_id)
@@ -810,7 +836,8 @@ class MoeOffloadRuntime:
         routed, total = self._resolve_fused_shared_counts(layer_id=layer_id, requested_logical_expert_count=num_logical_experts)
         active = dedupe_preserve_order(active_experts)
         _validate_active_expert_ids(layer_id=layer_id, active_experts=active, num_logical_experts=routed)
-        if len(active) > self.config.num_slots:
+        overflowing = len(active) > self.config.num_slots
+        if overflowing and not self.can_stage_decode_overflow(layer_id=layer_id, active_expert_count=len(active)):
             raise RuntimeError(f"active expert working set size {len(active)} exceeds num_slots={self.config.num_slots}")
         if int(log2phy.numel()) != total:
             raise RuntimeError(f"log2phy buffer for layer {layer_id} has size {int(log2phy.numel())}, expected {total}")
@@ -821,6 +848,9 @@ class MoeOffloadRuntime:
             self._drain_slot_bank_inflight_work(bank)
         step_id = self._step(step_id)
         t0 = perf_counter()
+        over: tuple[int, ...] = ()
+        if overflowing:
+            active, over = _split_decode_overflow(bank, active, int(self.config.num_slots), token_counts)
         ids = np.fromiter(active, dtype=np.int32, count=len(active))
         # one native call plans every expert (hit: touch; miss: reserve a
         # slot, LOADING); it stops where in-flight work must finish first
@@ -844,6 +874,9 @@ class MoeOffloadRuntime:
                  for e, sid in zip(misses, (v for v, m in zip(slot_list, is_miss) if m))]
         ready = None
         table_updates = -1
+        # the main table sends overflow experts to no slot (the second pass
+        # covers them); an evicted owner's stale entry must not catch them
+        tab_e, tab_s = tuple(active) + over, slot_list + [-1] * len(over)
         t_load = perf_counter()
         load_sync_ms = load_enqueue_ms = 0.0
         if loads and not self.config.async_load:
@@ -857,7 +890,7 @@ class MoeOffloadRuntime:
             # device bank and table: the changed log2phy entries ride with the
             # copies on the transfer stream, inside their ready event
             with_table = log2phy.device.type == "cuda" and bank.w13_slots.device.type == "cuda"
-            upd = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=slot_list) \
+            upd = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=tab_e, slot_ids=tab_s) \
                 if with_table else ((), ())
             extra = {"table_update": (log2phy, upd[0], upd[1])} if upd[0] else {}
             try:
@@ -872,8 +905,120 @@ class MoeOffloadRuntime:
                 self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd[0], slot_ids=upd[1])
                 table_updates = len(upd[0])
             load_enqueue_ms = (perf_counter() - t_load) * 1000.0
-        return PendingFixedSlotStage(layer_id, active, tuple(slot_list), bank.owners(), ready, hits, misses,
-                                     log2phy, step_id, t0, table_updates, load_sync_ms, load_enqueue_ms)
+        ovf = self._issue_decode_overflow(layer_id=layer_id, experts=over, total=total, step_id=step_id) \
+            if over else None
+        return PendingFixedSlotStage(layer_id, active, tuple(slot_list), bank.owners(), ready, hits, misses + over,
+                                     log2phy, step_id, t0, table_updates, load_sync_ms, load_enqueue_ms, ovf)
+
+    # ----------------------------------------------------- decode overflow
+    def can_stage_decode_overflow(self, *, layer_id: int, active_expert_count: int) -> bool:
+        """A decode working set past the bank fits one overflow pass: at most
+        num_slots more experts, from the layer's stage buffer."""
+        if not (self.config.decode_overflow and self.should_use_fixed_slot_plan_for_layer(int(layer_id))):
+            return False
+        n, P = int(active_expert_count), int(self.config.num_slots)
+        return P < n <= 2 * P
+
+    def decode_overflow_buffer_index(self, layer_id: int) -> int:
+        """Stage buffer of a layer's overflow pass: fixed per layer (a captured
+        graph records its address), alternating between neighbours so one
+        layer's copies overlap the previous layer's compute."""
+        return int(layer_id) % self.config.effective_prefill_buffer_count
+
+    def _overflow_table(self, layer_id: int, total: int, device) -> torch.Tensor:
+        t = self._overflow_tables.get(int(layer_id))
+        if t is None or int(t.numel()) != int(total):
+            t = torch.full((int(total),), -1, dtype=torch.int32, device=device)
+            self._overflow_tables[int(layer_id)] = t
+            self._memory_ledger_cache = None
+        return t
+
+    def decode_overflow_slot_weights(self, *, layer_id: int, n_pairs: int | None = None) -> PreparedSlotWeights | None:
+        """The second pass's weights of a layer: its stage buffer and its
+        overflow table, fixed addresses (what an eager call or a captured graph
+        reads).  None when overflow is off or when n_pairs routed pairs cannot
+        exceed the slots."""
+        layer_id = int(layer_id)
+        P = int(self.config.num_slots)
+        if not (self.config.decode_overflow and self.should_use_fixed_slot_plan_for_layer(layer_id)):
+            return None
+        if n_pairs is not None and int(n_pairs) <= P:
+            return None
+        src = self._slot_banks.get(layer_id)
+        if src is None:
+            return None
+        _, total = self._resolve_fused_shared_counts(
+            layer_id=layer_id, requested_logical_expert_count=int(self._log2phy_buffers[layer_id].numel()))
+        buf = self.decode_overflow_buffer_index(layer_id)
+        stage = self._get_prefill_stage_bank(layer_id=layer_id, buffer_index=buf, template_bank=src)
+        table = self._overflow_table(layer_id, total, src.w13_slots.device)
+        mapping = ExpertSlotMapping(layer_id, (), table, tuple(stage.owners()), ())
+        return PreparedSlotWeights(stage.w13_slots, stage.w2_slots, table, stage.physical_expert_count, mapping)
+
+    def _issue_decode_overflow(self, *, layer_id: int, experts: tuple[int, ...], total: int,
+                               step_id: int) -> DecodeOverflowStage:
+        """Queue the overflow experts' copies (host rows: by construction none
+        is resident) into the layer's stage buffer, with its table, after the
+        buffer's previous compute has released it."""
+        src = self._slot_banks[layer_id]
+        buf = self.decode_overflow_buffer_index(layer_id)
+        stage = self._get_prefill_stage_bank(layer_id=layer_id, buffer_index=buf, template_bank=src)
+        table = self._overflow_table(layer_id, total, src.w13_slots.device)
+        wait = self.prefill_stage_buffer_release_event(layer_id=layer_id, buffer_index=buf)
+        loads = [(self._host_store.get(layer_id, e), stage.assign_transient_slot(i, ExpertKey(layer_id, e), step_id=step_id))
+                 for i, e in enumerate(experts)]
+        for sid in range(len(experts), stage.num_dynamic_slots):
+            stage.clear_slot(sid, force=True)
+        device_path = table.device.type == "cuda" and stage.w13_slots.device.type == "cuda"
+        ready = None
+        try:
+            if self.config.async_load and device_path:
+                ready = self._transfer_engine.load_many_async(
+                    loads, wait_event=wait, record_event=True, validate_layout=False,
+                    table_update=(table, tuple(experts), tuple(range(len(experts))), True))
+            else:
+                if wait is not None:
+                    _synchronize_event(getattr(wait, "event", wait))
+                self._transfer_engine.load_many_sync(loads, validate_layout=False)
+                values = np.full(int(table.numel()), -1, dtype=np.int32)
+                values[list(experts)] = np.arange(len(experts), dtype=np.int32)
+                table.copy_(torch.from_numpy(values))
+        except Exception:
+            self._release_allocated_loads(stage, loads)
+            raise
+        self._overflow_dirty.add(int(layer_id))
+        return DecodeOverflowStage(buf, stage, table, tuple(experts), ready)
+
+    def _publish_decode_overflow(self, pending: PendingFixedSlotStage) -> PreparedSlotWeights | None:
+        """Order the overflow copies before the consumer and hand out the
+        second pass; with no overflow this step, a table still holding the
+        last one is cleared on the consumer stream (after the compute that
+        read it, before the one that will)."""
+        layer_id = pending.layer_id
+        ovf = pending.overflow
+        if ovf is None:
+            if layer_id in self._overflow_dirty:
+                self._overflow_tables[layer_id].fill_(-1)
+                self._overflow_dirty.discard(layer_id)
+            return None
+        if ovf.ready is not None:
+            self._wait_transfer_event(ovf.ready)
+        self._overflow_release_pending[layer_id] = ovf.buffer_index
+        mapping = ExpertSlotMapping(layer_id, ovf.experts, ovf.table, tuple(ovf.bank.owners()),
+                                   tuple(range(len(ovf.experts))))
+        return PreparedSlotWeights(ovf.bank.w13_slots, ovf.bank.w2_slots, ovf.table, ovf.bank.physical_expert_count,
+                                   mapping)
+
+    def end_overflow_compute(self, layer_id: int) -> None:
+        """After the compute that reads a layer's overflow pass is queued:
+        its stage buffer is released for the next copies once that compute
+        completes (no-op when the layer had no overflow)."""
+        buf = self._overflow_release_pending.pop(int(layer_id), None)
+        if buf is None:
+            return
+        ev = self._record_current_stream_event_or_none()
+        self.remember_prefill_stage_buffer_release(layer_id=int(layer_id), buffer_index=buf, event=ev)
+
 
     def _raise_no_slot(self, layer_id: int, expert_id: int, bank: ExpertSlotBank) -> None:
         raise RuntimeError(
@@ -890,14 +1035,17 @@ class MoeOffloadRuntime:
             self._wait_transfer_event(pending.ready)
         t_map = perf_counter()
         active, slot_ids = pending.active, pending.slot_ids
+        ovf_experts = pending.overflow.experts if pending.overflow is not None else ()
         if pending.table_updates >= 0:
             n_updates = pending.table_updates  # written on the transfer stream with the copies
         else:
-            upd_e, upd_s = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=active, slot_ids=slot_ids)
+            upd_e, upd_s = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=tuple(active) + ovf_experts,
+                                                         slot_ids=tuple(slot_ids) + (-1,) * len(ovf_experts))
             if upd_e:
                 _update_log2phy_entries(pending.log2phy, expert_ids=upd_e, slot_ids=upd_s)
                 self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd_e, slot_ids=upd_s)
             n_updates = len(upd_e)
+        overflow = self._publish_decode_overflow(pending)
         mapping = ExpertSlotMapping(layer_id, active, pending.log2phy, tuple(pending.owners), tuple(slot_ids))
         self._active_slot_ids_by_layer[layer_id] = tuple(slot_ids)
         self.last_stage_stats = (len(pending.hits), len(pending.misses))
@@ -924,6 +1072,7 @@ class MoeOffloadRuntime:
                 "consumer_dependency_installed": True,
                 "mapping_published_after_ready": True,
                 "profile_sample_rate": _decode_profile_sample_rate(),
+                "overflow_experts": len(ovf_experts),
             }
             if _profile_expert_lists_enabled():
                 payload.update({"active_experts": list(active), "hit_experts": list(pending.hits),
@@ -931,7 +1080,8 @@ class MoeOffloadRuntime:
             else:
                 payload["expert_lists"] = "omitted"
             self._record_profile_event("decode_fixed_slot_stage", layer_id=layer_id, start=t_map, payload=payload)
-        return PreparedSlotWeights.from_slot_bank(slot_bank=bank, mapping=mapping)
+        return PreparedSlotWeights(bank.w13_slots, bank.w2_slots, mapping.logical_to_physical,
+                                   bank.physical_expert_count, mapping, overflow)
 
     def _changed_log2phy_entries(self, *, layer_id: int, expert_ids, slot_ids) -> tuple[tuple[int, ...], tuple[int, ...]]:
         if len(expert_ids) != len(slot_ids):
@@ -945,7 +1095,8 @@ class MoeOffloadRuntime:
         for e, s in zip(expert_ids, slot_ids):
             cached[int(e)] = int(s)
 
-    def stage_fixed_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int) -> PreparedSlotWeights:
+    def stage_fixed_slot_plan(self, *, layer_id: int, active_experts, num_logical_experts: int,
+                              token_counts: dict[int, int] | None = None) -> PreparedSlotWeights:
         """Eager pre-replay staging into the persistent log2phy (never inside capture)."""
         if _is_current_graph_capturing():
             raise RuntimeError(
@@ -959,11 +1110,12 @@ class MoeOffloadRuntime:
         )
         self._assert_locked_slot_addresses(int(layer_id))
         buf = self._log2phy_buffers[int(layer_id)]
-        prepared = self.prepare_fixed_slot_plan_into_log2phy(
-            layer_id=int(layer_id), active_experts=active, num_logical_experts=int(num_logical_experts),
-            log2phy=buf, record_stage_profile=True,
-        )
-        return PreparedSlotWeights(prepared.w1, prepared.w2, buf, prepared.physical_expert_count, prepared.mapping)
+        pending = self._reserve_and_issue(layer_id=int(layer_id), active_experts=active,
+                                          num_logical_experts=int(num_logical_experts), log2phy=buf, step_id=None,
+                                          token_counts=token_counts)
+        prepared = self._publish(pending, record_stage_profile=True)
+        return PreparedSlotWeights(prepared.w1, prepared.w2, buf, prepared.physical_expert_count, prepared.mapping,
+                                   prepared.overflow)
 
     def stage_full_residency_slot_plan(self, *, layer_id: int) -> bool:
         """Regime A: stage every routed expert once, before capture."""
@@ -991,7 +1143,13 @@ class MoeOffloadRuntime:
             )
             return False
         self.stage_fixed_slot_plan(layer_id=layer_id, active_experts=tuple(range(routed)), num_logical_experts=total)
+        self._full_residency_layers.add(layer_id)
         return True
+
+    def is_full_residency_staged(self, layer_id: int) -> bool:
+        """Every routed expert of the layer is staged and its table static
+        (the per-step seam has nothing to do)."""
+        return int(layer_id) in self._full_residency_layers
 
     def capture_safe_slot_weights(self, *, layer_id: int) -> PreparedSlotWeights | None:
         """Fixed slot tensors + fixed log2phy, no host sync, no copy: what a
@@ -1357,6 +1515,23 @@ class MoeOffloadRuntime:
 
 
 # ---------------------------------------------------------------------------
+def _split_decode_overflow(bank: ExpertSlotBank, active: tuple[int, ...], capacity: int,
+                           token_counts: dict[int, int] | None) -> tuple[tuple[int, ...], tuple[int, ...]]:
+    """Split a decode working set larger than the bank: every READY resident
+    expert stays in the bank pass (a hit), the other experts fill the bank's
+    remaining slots by routed token count (more first, then id) and the rest
+    form the overflow pass.  Which pass serves a pair does not change its
+    result: each pair's row is computed alone and the combine sums in top-k
+    order."""
+    resident = bank.ready_resident_mask(active)
+    hits = [e for e, r in zip(active, resident) if r]
+    cold = [e for e, r in zip(active, resident) if not r]
+    counts = token_counts or {}
+    cold.sort(key=lambda e: (-int(counts.get(e, 0)), e))
+    room = capacity - len(hits)
+    return tuple(hits) + tuple(cold[:room]), tuple(cold[room:])
+
+
 def _decode_profile_sample_rate() -> int:
     try:
         return max(1, int(os.environ.get("VLLM_ASCEND_MOE_DECODE_PROFILE_SAMPLE_RATE", "1")))

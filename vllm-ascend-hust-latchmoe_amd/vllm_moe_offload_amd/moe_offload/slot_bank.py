@@ -377,6 +377,17 @@ class ExpertSlotBank:
         s = self._resident_slot(expert_key)
         return None if s < 0 else self.slots[s]
 
+    def ready_resident_mask(self, expert_ids) -> np.ndarray:
+        """Per expert id: resident in a dynamic slot and READY."""
+        ids = np.asarray(expert_ids, dtype=np.int64).reshape(-1)
+        ok = (ids >= 0) & (ids < self._slot_of.size)
+        s = np.full(ids.shape, -1, dtype=np.int64)
+        s[ok] = self._slot_of[ids[ok]]
+        ok &= (s >= 0) & (s < self.num_dynamic_slots)
+        idx = np.where(ok, s, 0)
+        ok &= (self._owner[idx] == ids) & (self._state[idx] == READY)
+        return ok
+
     def lookup_expert_id(self, expert_id: int) -> ExpertSlot | None:
         e = int(expert_id)
         if e < 0 or e >= self._slot_of.size:

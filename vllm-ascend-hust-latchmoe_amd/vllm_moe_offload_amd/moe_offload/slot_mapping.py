@@ -102,6 +102,9 @@ class PreparedSlotWeights:
     log2phy: torch.Tensor
     physical_expert_count: int
     mapping: ExpertSlotMapping
+    # decode overflow: the stage buffer (and its table) holding the routed
+    # experts past the bank's capacity, run as a second pass
+    overflow: "PreparedSlotWeights | None" = None
 
     def validate_backend_ready(self, *, expected_device_type: str) -> None:
         P = int(self.physical_expert_count)

@@ -4,8 +4,10 @@ router piece and the captured MLP piece.
 Reads the routed ids to the host (the one unavoidable D2H of the seam),
 counts the active experts, and either stages them into the fixed slots
 (runtime.stage_fixed_slot_plan: H2D on the transfer stream, consumer wait,
-in-place log2phy) or, when the union exceeds the slot capacity in a known
-phase, defers to the wave executor and caches the histogram for it.  It
+in-place log2phy), or, for a decode-sized batch whose union exceeds the slots
+by at most the slot count (with decode_overflow on), stages the bank plus one
+overflow pass, or, when the union exceeds the slot capacity otherwise in a
+known phase, defers to the wave executor and caches the histogram for it.  It
 returns nothing and declares topk_ids mutated so the MLP piece reads the
 router's tensor at its captured address.
 
@@ -97,7 +99,10 @@ def stage_topk_for_layer(runtime, topk_ids: torch.Tensor, layer_id: int, num_log
                 f"graph capture reached an unregistered fixed-slot MoE layer {layer_id}; refusing native-weight fallback"
             )
         return
-    if runtime.is_static_residency_regime_for_layer(layer_id=layer_id, fallback_routed_expert_count=routed):
+    if runtime.is_static_residency_regime_for_layer(layer_id=layer_id, fallback_routed_expert_count=routed) and (
+            runtime.is_full_residency_staged(layer_id) or not runtime.is_layer_registered(layer_id)):
+        # every expert is staged and the table static; a registered layer
+        # whose full residency was not staged (no graph mode) stages per step
         return
     if not runtime.should_use_fixed_slot_plan_for_layer(layer_id):
         return
@@ -112,6 +117,15 @@ def stage_topk_for_layer(runtime, topk_ids: torch.Tensor, layer_id: int, num_log
     known = phase in (PHASE_PREFILL, PHASE_DECODE, PHASE_MIXED)
     hint = int(runtime.config.max_num_seqs_hint or 0)
     tokens = int(topk_ids.shape[0]) if topk_ids.ndim > 0 else 0
+    decode_sized = phase == PHASE_DECODE or (phase == PHASE_UNKNOWN and 0 < tokens <= hint)
+    if over and decode_sized and not is_moe_offload_adaptive_wave_context() and \
+            runtime.can_stage_decode_overflow(layer_id=layer_id, active_expert_count=n_active):
+        # bank + one overflow pass, both inside the captured MLP piece
+        runtime.stage_fixed_slot_plan(layer_id=layer_id, active_experts=active, num_logical_experts=total,
+                                      token_counts=counts)
+        if os.environ.get("LATCHMOE_SEAM_PROBE"):
+            print(f"LATCHMOE_SEAM branch=decode_overflow layer={layer_id} n_active={n_active}", flush=True)
+        return
     defer = (known and runtime.should_use_b2_pair_waves(layer_id=layer_id, active_expert_count=n_active)) or (
         runtime.config.b2_wave_prefill and phase == PHASE_UNKNOWN and hint > 0 and tokens > hint and over
     ) or (is_moe_offload_adaptive_wave_context() and over)

@@ -145,13 +145,18 @@ def _patch_moe_comm_method_runtime_hooks(_comm) -> bool:
             return result_cls(routed_out=out, before_dispatch_evt=None, before_gmm2_evt=None,
                               before_combine_evt=None, group_list_type=1, expert_tokens=None,
                               swiglu_limit=getattr(fused_experts_input, "swiglu_limit", None))
+        overflow = runtime.decode_overflow_slot_weights(layer_id=layer_id,
+                                                        n_pairs=int(fused_experts_input.topk_ids.numel()))
         prepared_input = self._maybe_apply_moe_offload_plan(fused_experts_input)
         try:
-            return fused_moe.run_fused_experts_contract(prepared_input, result_cls=result_cls, record_events=True)
+            return fused_moe.run_fused_experts_contract(prepared_input, result_cls=result_cls, record_events=True,
+                                                        overflow=overflow)
         finally:
             handle = getattr(self, "_latchmoe_slot_compute_handle", None)
             self._latchmoe_slot_compute_handle = None
             runtime.end_slot_compute(handle)
+            if overflow is not None:
+                runtime.end_overflow_compute(layer_id)
 
     cls._with_prepared_slot_weights = _with_prepared_slot_weights
     cls._maybe_apply_moe_offload_plan = _tagged(_maybe_apply_moe_offload_plan, PATCH_TAG)
