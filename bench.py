@@ -100,7 +100,8 @@ class DecodeModel:
 
         self.L = n_layers
         self.rt = MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=num_slots, async_load=True,
-                                                     graph_compatible_offload=True, b2_wave_prefill=True))
+                                                     graph_compatible_offload=True, b2_wave_prefill=True,
+                                                     decode_overflow=True))
         dev = torch.device("cuda")
         g = torch.Generator(device=dev)
         self.gates, self.specs = [], []
@@ -151,10 +152,15 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
     Each replay is bracketed by HIP events recorded after the copy wait;
     that interval also holds any wait for the host to submit the replay, so
     it is reported as the pipelined layer interval, not as compute.  A layer
-    whose working set exceeds its slots runs eager capacity waves in its
-    turn (no graph).  The compute rate (the headline) is the 48-layer graph
-    replayed over the staged, HBM-resident step: one replay, timed with HIP
-    events."""
+    whose working set exceeds its slots (by at most the slot count) stages
+    the excess into its stage buffer and replays the graph captured with the
+    overflow pass; a larger excess would run eager capacity waves.  The
+    compute rate (the headline) is the 48-layer graph replayed over the
+    staged, HBM-resident step: one replay, timed with HIP events (on a step
+    with overflow layers, the variant with every layer's overflow pass; the
+    stage buffers then hold the last layers' overflow experts, the same
+    work)."""
+    import numpy as np
     import torch
 
     from vllm_moe_offload_amd import fused_moe
@@ -176,24 +182,32 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
     ws = fused_moe.get_workspace(B, K, P, H, I, dev, tag=f"bench{B}")
     cap = rt.config.num_slots
 
-    def compute_layer(l):
+    def compute_layer(l, two=False):
         # the slot table is final (staged from the eager routing of this
         # step), so selection and permutation run as one launch
         bank = model.bank(l)
+        ovf = rt.decode_overflow_slot_weights(layer_id=l, n_pairs=B * K) if two else None
         fused_moe.decode_layer(static_x, model.gates[l], model.specs[l], bank.w13_slots, bank.w2_slots,
                                rt.log2phy_buffer(l), workspace=ws, out=outs[l], logits_out=logits[l],
-                               w_out=ws_w[l], ids_out=ws_ids[l])
+                               w_out=ws_w[l], ids_out=ws_ids[l], overflow=ovf)
+
+    counts: list[dict[int, int]] = [{} for _ in range(L)]
 
     def route_all(i: int) -> list[tuple[int, ...]]:
         static_x.copy_(xs[i])
         for l in range(L):
             _route(static_x, model, l, ws_w[l], ws_ids[l], logits[l])
-        ids_host = torch.stack(ws_ids).cpu()  # one D2H for all layers' ids
-        return [tuple(sorted(set(ids_host[l].flatten().tolist()))) for l in range(L)]
+        ids_host = torch.stack(ws_ids).cpu().numpy()  # one D2H for all layers' ids
+        out = []
+        for l in range(L):
+            u, c = np.unique(ids_host[l], return_counts=True)
+            counts[l] = dict(zip(u.tolist(), c.tolist()))
+            out.append(tuple(u.tolist()))
+        return out
 
-    stats = {"hits": 0, "misses": 0}
-    graphs: list = [None] * L
-    big = None  # the 48-layer graph, captured once every layer fits
+    stats = {"hits": 0, "misses": 0, "overflow_layers": 0}
+    graphs: dict = {}  # (layer, overflow pass) -> graph
+    big: dict = {}  # overflow pass -> the 48-layer graph
     ev0 = [torch.cuda.Event(enable_timing=True) for _ in range(L)]
     ev1 = [torch.cuda.Event(enable_timing=True) for _ in range(L)]
     tx0 = [torch.cuda.Event(enable_timing=True) for _ in range(L)]
@@ -201,51 +215,58 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
     base = torch.cuda.Event(enable_timing=True)
 
     def prefetch(l, a):
-        if len(a[l]) > cap:
+        if len(a[l]) > cap and not rt.can_stage_decode_overflow(layer_id=l, active_expert_count=len(a[l])):
             return None
         s = engine._transfer_stream(dev)
         tx0[l].record(s)
-        p = rt.prefetch_fixed_slot_plan(layer_id=l, active_experts=a[l], num_logical_experts=E)
+        p = rt.prefetch_fixed_slot_plan(layer_id=l, active_experts=a[l], num_logical_experts=E, token_counts=counts[l])
         tx1[l].record(s)
         return p
 
-    def capture(l):
+    def capture(l, two):
         torch.cuda.synchronize()
         rt.capture_safe_slot_weights(layer_id=l)  # lock slot addresses
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            compute_layer(l)
+            compute_layer(l, two)
         torch.cuda.current_stream().wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            compute_layer(l)
+            compute_layer(l, two)
         return g
 
     def pipelined_step(a, timed: bool):
-        """Returns (compute ms, overflow ms, compute intervals, copy intervals)."""
+        """Returns (compute ms, overflow ms, compute intervals, copy intervals,
+        eager layers, overflow-pass layers)."""
         comp = torch.cuda.current_stream()
         base.record(comp)
         pend = prefetch(0, a)
         waves_ms = 0.0
         eager_layers = []
+        n_two = 0
         for l in range(L):
+            two = False
             if pend is not None:
-                rt.complete_fixed_slot_plan(pend)
+                prepared = rt.complete_fixed_slot_plan(pend)
+                two = prepared.overflow is not None
+                assert two == (pend.overflow is not None), "staged overflow lost before compute"
                 stats["hits"] += len(pend.hits)
                 stats["misses"] += len(pend.misses)
             nxt = prefetch(l + 1, a) if l + 1 < L else None
-            if len(a[l]) > cap:
+            if pend is None:
                 ev0[l].record(comp)
                 fused_moe.run_wave_prefill(rt, layer_id=l, hidden=static_x, topk_weights=ws_w[l],
                                            topk_ids=ws_ids[l], num_logical_experts=E, out=outs[l])
                 ev1[l].record(comp)
                 eager_layers.append(l)
             else:
-                if graphs[l] is None:
-                    graphs[l] = capture(l)
+                n_two += int(two)
+                g = graphs.get((l, two))
+                if g is None:
+                    g = graphs[(l, two)] = capture(l, two)
                 ev0[l].record(comp)
-                graphs[l].replay()
+                g.replay()
                 ev1[l].record(comp)
             rt.record_layer_compute(l)
             pend = nxt
@@ -261,34 +282,34 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
                 comp_iv.append((t0, t1))
         if timed:
             for l in range(L):
-                if len(a[l]) <= cap:
+                if l not in eager_layers:
                     copy_iv.append((base.elapsed_time(tx0[l]), base.elapsed_time(tx1[l])))
-        return c_ms, waves_ms, comp_iv, copy_iv, len(eager_layers)
+        return c_ms, waves_ms, comp_iv, copy_iv, len(eager_layers), n_two
 
-    def capture_big():
+    def capture_big(two):
         torch.cuda.synchronize()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for l in range(L):
-                compute_layer(l)
+                compute_layer(l, two)
         torch.cuda.current_stream().wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for l in range(L):
-                compute_layer(l)
+                compute_layer(l, two)
+        for l in range(L):
+            rt.record_layer_compute(l)
         return g
 
     t_begin = time.perf_counter()
     for i in range(warmup):
         pipelined_step(route_all(i), timed=False)
     torch.cuda.synchronize()
-    if all(g is not None for g in graphs):
-        big = capture_big()
     fp0 = [rt._slot_address_fingerprint(l) for l in range(L)]
     resident_ms = []
     stats["hits"] = stats["misses"] = 0
-    comp_ms, wave_ms, step_ms, U, ov_num, ov_den, n_eager = [], [], [], [], 0.0, 0.0, []
+    comp_ms, wave_ms, step_ms, U, ov_num, ov_den, n_eager, n_over = [], [], [], [], 0.0, 0.0, [], []
     done = 0
     for i in range(warmup, warmup + steps):
         if time.perf_counter() - t_begin > budget_s and done >= 8:
@@ -296,20 +317,23 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
         t0 = time.perf_counter()
         a = route_all(i)
         U.append(sum(len(x) for x in a) / L)
-        c, w, civ, tiv, ne = pipelined_step(a, timed=True)
+        c, w, civ, tiv, ne, n2 = pipelined_step(a, timed=True)
         step_ms.append((time.perf_counter() - t0) * 1000.0)
         ov_num += _interval_overlap(civ, tiv)
         ov_den += sum(t1 - t0_ for t0_, t1 in civ)
         n_eager.append(ne)
+        n_over.append(n2)
         if ne == 0:
             comp_ms.append(c)
-            if big is not None:
-                # the same step again with every layer resident: one replay
-                with Timer() as t:
-                    big.replay()
-                resident_ms.append(t.ms())
-                for l in range(L):
-                    rt.record_layer_compute(l)
+            two = n2 > 0
+            if two not in big:
+                big[two] = capture_big(two)
+            # the same step again with every layer resident: one replay
+            with Timer() as t:
+                big[two].replay()
+            resident_ms.append(t.ms())
+            for l in range(L):
+                rt.record_layer_compute(l)
         else:
             wave_ms.append(c + w)
         done += 1
@@ -317,7 +341,8 @@ def bench_decode(model: DecodeModel, B: int, steps: int, warmup: int, seed: int,
     assert fp0 == [rt._slot_address_fingerprint(l) for l in range(L)], "slot addresses moved"
     res: dict = {"B": B, "steps_run": done, "steps_all_graph": len(comp_ms),
                  "steps_with_wave_layers": len(wave_ms),
-                 "wave_layers_per_step": round(sum(n_eager) / max(1, len(n_eager)), 2)}
+                 "wave_layers_per_step": round(sum(n_eager) / max(1, len(n_eager)), 2),
+                 "overflow_pass_layers_per_step": round(sum(n_over) / max(1, len(n_over)), 2)}
     res["slot_miss_rate"] = round(stats["misses"] / max(1, stats["hits"] + stats["misses"]), 4)
     u = sum(U) / max(1, len(U))
     res["distinct_experts_per_layer"] = round(u, 2)

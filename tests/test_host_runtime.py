@@ -622,3 +622,16 @@ def test_decode_overflow_split_covers_every_expert_once():
         table, otab = rt.log2phy_buffer(7).tolist(), prepared.overflow.log2phy.tolist()
         for e in active:  # every routed expert maps in exactly one of the two tables
             assert (table[e] >= 0) != (otab[e] >= 0), (trial, e)
+
+
+def test_prefetch_then_complete_hands_out_the_overflow_pass():
+    rt = _rt(num_slots=2, decode_overflow=True)
+    rt.register_layer_for_fixed_slots(TinyLayer(experts=6), slot_device=CPU)
+    pend = rt.prefetch_fixed_slot_plan(layer_id=7, active_experts=(0, 1, 2), num_logical_experts=6,
+                                       token_counts={0: 1, 1: 3, 2: 2})
+    assert pend.overflow is not None and pend.overflow.experts == (0,)
+    prepared = rt.complete_fixed_slot_plan(pend)
+    assert prepared.overflow is not None and prepared.overflow.mapping.active_experts == (0,)
+    assert prepared.log2phy.data_ptr() == rt.log2phy_buffer(7).data_ptr()
+    table = rt.log2phy_buffer(7).tolist()
+    assert table[0] == -1 and table[1] >= 0 and table[2] >= 0

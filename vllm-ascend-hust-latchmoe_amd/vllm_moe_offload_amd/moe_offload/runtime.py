@@ -822,9 +822,7 @@ class MoeOffloadRuntime:
 
     def complete_fixed_slot_plan(self, pending: PendingFixedSlotStage) -> PreparedSlotWeights:
         """Order the prefetched copies before the current stream, then publish."""
-        prepared = self._publish(pending, record_stage_profile=True)
-        buf = self._log2phy_buffers[int(pending.layer_id)]
-        return PreparedSlotWeights(prepared.w1, prepared.w2, buf, prepared.physical_expert_count, prepared.mapping)
+        return self._publish(pending, record_stage_profile=True)
 
     def _reserve_and_issue(self, *, layer_id: int, active_experts, num_logical_experts: int, log2phy: torch.Tensor,
                            step_id: int | None, token_counts: dict[int, int] | None = None) -> PendingFixedSlotStage:
