@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define LMOE_ABI_VERSION 4
+#define LMOE_ABI_VERSION 5
 
 enum {
   LMOE_OK = 0,
@@ -355,6 +355,49 @@ int lmoe_slot_plan(int8_t* state, int32_t* owner, int64_t* version,
  * write, or an index_copy_ of the changed entries). */
 int lmoe_table_update(int32_t* table, int n_table, const int32_t* idx,
                       const int32_t* val, int n, hipStream_t stream);
+
+/* Bytes of the int32 plan buffer of lmoe_wave_plan / lmoe_wave_stage for
+ * n_routed <= 1024 experts, n_slots <= 1024 stage slots and max_waves <= 256
+ * waves; -1 outside those bounds. */
+long long lmoe_wave_plan_bytes(int n_routed, int n_slots, int max_waves);
+
+/* Capacity waves of a prefill layer planned on the device, one workgroup on
+ * stream: histogram of ids[0..n_pairs) over the routed experts
+ * [0, n_routed) (ids in [n_routed, n_total) are a pinned shared suffix, any
+ * other id is counted as invalid), experts taken in (-count, id) order, each
+ * into the wave of (least routed pairs, lowest index) among the
+ * ceil(n_active / n_slots) waves with room, members ascending per wave.
+ * plan: [0] waves (-1 when more than max_waves), [1] active experts, [2]
+ * invalid ids, [3] 0, counts[n_routed], wave_of[n_routed],
+ * slot_of[n_routed] (position in its wave, -1 inactive), size[max_waves],
+ * members[max_waves][n_slots] (-1 padded).  Replaces the host planning of
+ * phase_split.plan_balanced_b2_waves (moe_offload/phase_split.py:495-554)
+ * after count_routed_tokens_by_expert's D2H (:479-492), and the expert ->
+ * wave / slot maps of build_b2_device_wave_microbatch_plans (:1224-1384). */
+int lmoe_wave_plan(const int32_t* ids, int n_pairs, int n_routed, int n_total,
+                   int n_slots, int max_waves, int32_t* plan, hipStream_t stream);
+
+/* Stage wave `wave` of a device plan, on stream (the transfer stream): for
+ * member i (expert e) copy w13_expert_bytes and w2_expert_bytes into stage
+ * slot i of stage_w13 / stage_w2, from main-bank slot s = main_table[e] when
+ * s is in [0, main_slots) and main_owner[s] == e (the table keeps stale
+ * entries of evicted experts; main_owner[s] is the slot's current expert),
+ * else from host row e of host_w13 / host_w2
+ * (page-locked host blocks of n_routed experts, read by the device at their
+ * host address); then write stage_table[0..n_table): members -> i, ids
+ * n_routed .. n_routed + n_pinned - 1 -> pinned_slot0 + j for wave 0 only,
+ * -1 elsewhere.  A wave past the plan's count copies nothing and writes an
+ * all -1 table.  Sizes and addresses must be multiples of 16.  Replaces the
+ * stage-bank fill of prepare_prefill_stage_plan (runtime.py:2035-2258:
+ * D2D for main-bank hits, H2D for misses, the per-wave table). */
+int lmoe_wave_stage(const int32_t* plan, int n_routed, int n_slots, int max_waves,
+                    int wave, const int32_t* main_table, const int32_t* main_owner,
+                    const void* main_w13, const void* main_w2, int main_slots,
+                    const void* host_w13,
+                    const void* host_w2, void* stage_w13, void* stage_w2,
+                    long long w13_expert_bytes, long long w2_expert_bytes,
+                    int32_t* stage_table, int n_table, int n_pinned,
+                    int pinned_slot0, hipStream_t stream);
 
 #ifdef __cplusplus
 }

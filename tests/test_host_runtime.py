@@ -635,3 +635,23 @@ def test_prefetch_then_complete_hands_out_the_overflow_pass():
     assert prepared.log2phy.data_ptr() == rt.log2phy_buffer(7).data_ptr()
     table = rt.log2phy_buffer(7).tolist()
     assert table[0] == -1 and table[1] >= 0 and table[2] >= 0
+
+
+def test_slot_owner_tail_follows_every_reassignment():
+    """Behind the persistent table: the owner of each dynamic slot, written
+    with the same update that changes it (the device-side residency check of
+    the device wave planner), while the table keeps the reference's stale
+    entries for evicted experts."""
+    rt = _rt(num_slots=3)
+    rt.register_layer_for_fixed_slots(TinyLayer(experts=6), slot_device=CPU)
+    assert rt.slot_owner_buffer(7).tolist() == [-1, -1, -1]
+    rt.stage_fixed_slot_plan(layer_id=7, active_experts=(0, 1, 2), num_logical_experts=6)
+    assert rt.slot_owner_buffer(7).tolist() == [0, 1, 2]
+    rt.stage_fixed_slot_plan(layer_id=7, active_experts=(1, 3), num_logical_experts=6)  # 3 evicts 0
+    table, owner = rt.log2phy_buffer(7).tolist(), rt.slot_owner_buffer(7).tolist()
+    assert table[:4] == [0, 1, 2, 0] and owner == [3, 1, 2]  # stale table[0], exact owners
+    bank = rt.slot_bank(7)
+    assert owner == [int(o) for o in bank._owner[:3]]
+    resident = [e for e in range(6) if 0 <= table[e] < 3 and owner[table[e]] == e]
+    assert resident == [1, 2, 3]
+    assert rt.log2phy_buffer(7).numel() == 6  # the table keeps its size

@@ -36,7 +36,7 @@ import torch
 
 from vllm_moe_offload_amd import native
 from vllm_moe_offload_amd.moe_offload import phase_split
-from vllm_moe_offload_amd.moe_offload.runtime import MoeOffloadRuntime
+from vllm_moe_offload_amd.moe_offload.runtime import MoeOffloadRuntime, _is_current_graph_capturing
 from vllm_moe_offload_amd.moe_offload.slot_mapping import PreparedSlotWeights
 
 
@@ -719,6 +719,100 @@ def _record_b2_prefill_event(runtime, *, layer_id, plan, sched, T, k, shared_pai
         payload["profile_details"] = "omitted"
     runtime._record_profile_event("b2_work_conserving_prefill", layer_id=int(layer_id), start=start,
                                   payload=payload)
+
+
+def run_device_waves(
+    runtime: MoeOffloadRuntime,
+    *,
+    layer_id: int,
+    hidden: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    num_logical_experts: int,
+    add: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    path: int = native.LMOE_PATH_AUTO,
+) -> torch.Tensor:
+    """Overflow prefill with no host step: the waves are planned on the device
+    from the routed ids (lmoe_wave_plan), each wave's experts are copied into
+    a stage buffer on the transfer stream (main-bank slot or host row,
+    lmoe_wave_stage) while the previous wave computes, and every wave's pairs
+    land in one flat-pair y; then ONE combine.  The number of launched waves
+    is fixed by the shapes (ceil(min(routed, T k) / slots)); waves the plan
+    does not need copy and compute nothing, so the whole call can be
+    captured.  Same bits as the host-planned waves and the full layer: each
+    pair's row is computed alone."""
+    T, H = hidden.shape
+    k = int(topk_ids.shape[1])
+    bank = runtime.slot_bank(layer_id)
+    if bank is None:
+        raise RuntimeError(f"layer {layer_id} is not registered for fixed-slot execution")
+    if not runtime.can_run_device_waves(layer_id):
+        raise RuntimeError(f"device wave planning is not available for layer {layer_id}")
+    dev = hidden.device
+    P = int(bank.num_dynamic_slots)
+    I = int(bank.w13_slots.shape[1]) // 2
+    routed = runtime.routed_expert_count_for_layer(layer_id=layer_id, fallback=num_logical_experts)
+    total = runtime.total_logical_expert_count_for_layer(layer_id=layer_id, fallback=num_logical_experts)
+    n_pinned = total - routed
+    n_waves = max(1, -(-min(routed, T * k) // P))
+    plan = runtime.device_wave_plan_buffer(n_routed=routed, n_slots=P, max_waves=n_waves, device=dev)
+    host = runtime.host_store.get_layer_buffer(layer_id)
+    main_table = runtime.log2phy_buffer(layer_id)
+    main_owner = runtime.slot_owner_buffer(layer_id)
+    n_buf = runtime.config.effective_prefill_buffer_count
+    stages = [runtime._get_prefill_stage_bank(layer_id=layer_id, buffer_index=b, template_bank=bank)
+              for b in range(min(n_buf, n_waves))]
+    tables = [runtime._get_prefill_stage_log2phy_buffer(template_bank=bank, buffer_index=b, num_logical_experts=total,
+                                                        device=dev) for b in range(len(stages))]
+    ws = get_workspace(T, k, int(stages[0].physical_expert_count), H, I, dev, tag="device_waves")
+    capturing = _is_current_graph_capturing()
+    compute = torch.cuda.current_stream(dev)
+    tx = runtime.transfer_engine._transfer_stream(dev)
+    native.wave_plan(topk_ids, plan, n_total=total)
+    planned = torch.cuda.Event()
+    planned.record(compute)
+    tx.wait_event(planned)
+    if not capturing:
+        # earlier users of the stage buffers (host-planned waves, decode
+        # overflow passes) release them with events of their own
+        for b in range(len(stages)):
+            ev = runtime.prefill_stage_buffer_release_event(layer_id=layer_id, buffer_index=b)
+            ev = getattr(ev, "event", ev)
+            if isinstance(ev, torch.cuda.Event):
+                tx.wait_event(ev)
+    released: list = [None] * len(stages)
+    bm = native.prefill_block_m(P, H, I, dev, n_pairs=-(-(T * k) // n_waves))
+    for w in range(n_waves):
+        b = w % len(stages)
+        stage, table = stages[b], tables[b]
+        if released[b] is not None:
+            tx.wait_event(released[b])
+        native.wave_stage(plan, w, main_table=main_table, main_owner=main_owner, main_w13=bank.w13_slots,
+                          main_w2=bank.w2_slots, main_slots=P, host_w13=host.w13, host_w2=host.w2,
+                          stage_w13=stage.w13_slots, stage_w2=stage.w2_slots, stage_table=table,
+                          n_pinned=n_pinned, stream=tx)
+        ready = torch.cuda.Event()
+        ready.record(tx)
+        compute.wait_event(ready)
+        native.permute(topk_ids, ws.perm, log2phy=table, skip_unmapped=True, block_m=bm)
+        native.grouped_mlp(hidden, k, stage.w13_slots, stage.w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k],
+                           path=path)
+        done = torch.cuda.Event()
+        done.record(compute)
+        released[b] = done
+    if not capturing:
+        for b, ev in enumerate(released):
+            if ev is not None:
+                runtime.remember_prefill_stage_buffer_release(layer_id=layer_id, buffer_index=b, event=ev)
+                # the host copy of the stage buffer's contents is void now
+                for sid in range(stages[b].num_dynamic_slots):
+                    stages[b].clear_slot(sid, force=True)
+    else:
+        compute.wait_stream(tx)  # the forked transfer stream rejoins the capture
+    dst = out if out is not None else ws.out[:T]
+    native.combine(ws.y[: T * k], topk_weights, dst, add=add)
+    return dst
 
 
 def run_full_layer(

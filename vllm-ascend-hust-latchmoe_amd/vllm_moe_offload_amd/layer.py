@@ -29,6 +29,7 @@ from vllm_moe_offload_amd.fused_moe import (
     fused_experts,
     get_workspace,
     route,
+    run_device_waves,
     run_wave_prefill,
 )
 from vllm_moe_offload_amd.moe_offload.cpu_first_loader import (
@@ -188,6 +189,9 @@ class SlotMoELayer(torch.nn.Module):
         if include_shared and self.shared_w13 is not None:
             add = self.shared_expert_forward(shared_experts_input if shared_experts_input is not None else hidden)
         rt = self.runtime
+        if rt.consume_device_waves(layer_id=self.layer_id, topk_ids=ids):
+            return run_device_waves(rt, layer_id=self.layer_id, hidden=hidden, topk_weights=w, topk_ids=ids,
+                                    num_logical_experts=self.num_logical_experts, add=add)
         if not _is_current_graph_capturing():
             stats = rt.consume_prefill_route_stats_record(layer_id=self.layer_id, topk_ids=ids)
             if stats is not None:

@@ -64,6 +64,9 @@ class MoeOffloadConfig:
     # from the bank, the rest (at most num_slots more) from a stage buffer in
     # a second pass of the same captured graph, instead of eager waves
     decode_overflow: bool = False
+    # overflowing prefill: waves planned and staged on the device (no D2H of
+    # the routed ids, no host step between the router and the expert MLP)
+    device_wave_prefill: bool = False
 
     @classmethod
     def from_env(cls) -> "MoeOffloadConfig":
@@ -87,6 +90,7 @@ class MoeOffloadConfig:
             cpu_first_load=_bool("CPU_FIRST_LOAD", False),
             release_original_expert_weights=_bool("RELEASE_ORIGINAL_EXPERT_WEIGHTS", False),
             decode_overflow=_bool("DECODE_OVERFLOW", False),
+            device_wave_prefill=_bool("DEVICE_WAVE_PREFILL", False),
         )
 
     @property

@@ -179,6 +179,7 @@ class PendingFixedSlotStage:
     load_sync_ms: float = 0.0
     load_enqueue_ms: float = 0.0
     overflow: "DecodeOverflowStage | None" = None
+    owner_updates: tuple[tuple[int, int], ...] = ()  # (slot, expert) still to write behind the table
 
 
 @dataclass
@@ -240,6 +241,11 @@ class MoeOffloadRuntime:
         self._released_original_weight_layers: set[int] = set()
         self._expert_weight_bytes_by_layer: dict[int, int] = {}
         self._log2phy_buffers: dict[int, torch.Tensor] = {}
+        # per layer: [E_total + P] int32; the first E_total entries are the
+        # persistent log2phy, the last P the owner of each dynamic slot (the
+        # device-side residency check: expert e is resident iff
+        # owner[log2phy[e]] == e)
+        self._log2phy_backing: dict[int, torch.Tensor] = {}
         self._log2phy_slot_by_expert: dict[int, dict[int, int]] = {}
         self._graph_slot_address_fingerprints: dict[int, SlotAddressFingerprint] = {}
         self._graph_slot_address_evidence: set[int] = set()
@@ -258,6 +264,10 @@ class MoeOffloadRuntime:
         self._overflow_release_pending: dict[int, int] = {}
         # layers whose table holds every routed expert (static residency)
         self._full_residency_layers: set[int] = set()
+        # device-planned prefill waves: plan buffers per shape, and the
+        # routed-id tensors the seam handed to them (no D2H taken)
+        self._device_wave_plans: dict[tuple, object] = {}
+        self._device_wave_marks: dict[int, tuple] = {}
         self._layer_release_events: dict[int, object] = {}
         self._placement_plan_provider: PlacementPlanProvider | None = None
         self._fixed_slot_execution_state = threading.local()
@@ -430,9 +440,8 @@ class MoeOffloadRuntime:
         else:
             self._fused_shared_lane_layouts.pop(layer_id, None)
         self._prefill_stage_banks.pop(layer_id, None)
-        table = torch.full((total,), -1, dtype=torch.int32, device=device)
+        table = self._new_log2phy(layer_id, total, bank.num_dynamic_slots, device)
         bank.install_pinned_log2phy(table)
-        self._log2phy_buffers[layer_id] = table
         self._log2phy_slot_by_expert[layer_id] = {}
         self._full_residency_layers.discard(layer_id)
         self._memory_ledger_cache = None
@@ -471,7 +480,7 @@ class MoeOffloadRuntime:
                               tuple(int(d) for d in w2_host.shape[1:]), dtype=w13_host.dtype, device=slot_device)
         self._slot_banks[layer_id] = bank
         self._fused_shared_lane_layouts.pop(layer_id, None)
-        self._log2phy_buffers[layer_id] = torch.full((E,), -1, dtype=torch.int32, device=slot_device)
+        self._new_log2phy(layer_id, E, bank.num_dynamic_slots, slot_device)
         self._log2phy_slot_by_expert[layer_id] = {}
         self._full_residency_layers.discard(layer_id)
         self._memory_ledger_cache = None
@@ -506,6 +515,25 @@ class MoeOffloadRuntime:
     def log2phy_buffer(self, layer_id: int) -> torch.Tensor | None:
         """The persistent, fixed-address log2phy table of a layer."""
         return self._log2phy_buffers.get(int(layer_id))
+
+    def slot_owner_buffer(self, layer_id: int) -> torch.Tensor | None:
+        """Device copy of the owner of each dynamic slot of a layer (-1 none),
+        written with the copies that change it."""
+        b = self._log2phy_backing.get(int(layer_id))
+        t = self._log2phy_buffers.get(int(layer_id))
+        return None if b is None or t is None else b[int(t.numel()):]
+
+    def _new_log2phy(self, layer_id: int, total: int, n_slots: int, device) -> torch.Tensor:
+        backing = torch.full((int(total) + int(n_slots),), -1, dtype=torch.int32, device=device)
+        self._log2phy_backing[int(layer_id)] = backing
+        table = backing[: int(total)]
+        self._log2phy_buffers[int(layer_id)] = table
+        return table
+
+    def _owner_entries(self, layer_id: int, owner_updates) -> tuple[tuple[int, ...], tuple[int, ...]]:
+        """(index into the backing tensor, expert) of slot-owner changes."""
+        base = int(self._log2phy_buffers[int(layer_id)].numel())
+        return tuple(base + s for s, _ in owner_updates), tuple(e for _, e in owner_updates)
 
     # ------------------------------------------- original weight release
     def original_expert_weights_available_for_layer(self, layer_id: int) -> bool:
@@ -872,9 +900,11 @@ class MoeOffloadRuntime:
                  for e, sid in zip(misses, (v for v, m in zip(slot_list, is_miss) if m))]
         ready = None
         table_updates = -1
-        # the main table sends overflow experts to no slot (the second pass
-        # covers them); an evicted owner's stale entry must not catch them
+        # overflow experts map to no slot (the second pass covers them), so a
+        # stale entry of theirs cannot catch their pairs in the bank pass;
+        # the slot owners behind the table (device residency) follow the misses
         tab_e, tab_s = tuple(active) + over, slot_list + [-1] * len(over)
+        owner_upd = tuple((int(s_), int(e)) for e, s_, m in zip(ids, slot_list, is_miss) if m)
         t_load = perf_counter()
         load_sync_ms = load_enqueue_ms = 0.0
         if loads and not self.config.async_load:
@@ -890,7 +920,13 @@ class MoeOffloadRuntime:
             with_table = log2phy.device.type == "cuda" and bank.w13_slots.device.type == "cuda"
             upd = self._changed_log2phy_entries(layer_id=layer_id, expert_ids=tab_e, slot_ids=tab_s) \
                 if with_table else ((), ())
-            extra = {"table_update": (log2phy, upd[0], upd[1])} if upd[0] else {}
+            persistent = log2phy.data_ptr() == self._log2phy_backing[layer_id].data_ptr()
+            own = self._owner_entries(layer_id, owner_upd) if with_table and persistent else ((), ())
+            extra = {}
+            if own[0]:
+                extra = {"table_update": (self._log2phy_backing[layer_id], upd[0] + own[0], upd[1] + own[1])}
+            elif upd[0]:
+                extra = {"table_update": (log2phy, upd[0], upd[1])}
             try:
                 ready = self._transfer_engine.load_many_async(
                     loads, wait_event=self._layer_release_events.get(layer_id), record_event=True,
@@ -902,11 +938,15 @@ class MoeOffloadRuntime:
             if with_table:
                 self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd[0], slot_ids=upd[1])
                 table_updates = len(upd[0])
+                if not persistent:  # a fresh table: the owners follow on the transfer stream
+                    self._write_owner_entries(layer_id, owner_upd, stream=self._transfer_engine.stream)
+                owner_upd = ()
             load_enqueue_ms = (perf_counter() - t_load) * 1000.0
         ovf = self._issue_decode_overflow(layer_id=layer_id, experts=over, total=total, step_id=step_id) \
             if over else None
         return PendingFixedSlotStage(layer_id, active, tuple(slot_list), bank.owners(), ready, hits, misses + over,
-                                     log2phy, step_id, t0, table_updates, load_sync_ms, load_enqueue_ms, ovf)
+                                     log2phy, step_id, t0, table_updates, load_sync_ms, load_enqueue_ms, ovf,
+                                     owner_upd)
 
     # ----------------------------------------------------- decode overflow
     def can_stage_decode_overflow(self, *, layer_id: int, active_expert_count: int) -> bool:
@@ -1007,6 +1047,18 @@ class MoeOffloadRuntime:
         return PreparedSlotWeights(ovf.bank.w13_slots, ovf.bank.w2_slots, ovf.table, ovf.bank.physical_expert_count,
                                    mapping)
 
+    def _write_owner_entries(self, layer_id: int, owner_updates, stream=None) -> None:
+        idx, val = self._owner_entries(layer_id, owner_updates)
+        if not idx:
+            return
+        backing = self._log2phy_backing[int(layer_id)]
+        if backing.device.type != "cuda":
+            backing[list(idx)] = torch.tensor(val, dtype=backing.dtype)
+            return
+        from vllm_moe_offload_amd import native
+
+        native.table_update_entries(backing, idx, val, stream=stream)
+
     def end_overflow_compute(self, layer_id: int) -> None:
         """After the compute that reads a layer's overflow pass is queued:
         its stage buffer is released for the next copies once that compute
@@ -1043,6 +1095,8 @@ class MoeOffloadRuntime:
                 _update_log2phy_entries(pending.log2phy, expert_ids=upd_e, slot_ids=upd_s)
                 self._remember_log2phy_entries(layer_id=layer_id, expert_ids=upd_e, slot_ids=upd_s)
             n_updates = len(upd_e)
+        if pending.owner_updates:
+            self._write_owner_entries(layer_id, pending.owner_updates)
         overflow = self._publish_decode_overflow(pending)
         mapping = ExpertSlotMapping(layer_id, active, pending.log2phy, tuple(pending.owners), tuple(slot_ids))
         self._active_slot_ids_by_layer[layer_id] = tuple(slot_ids)
@@ -1510,6 +1564,44 @@ class MoeOffloadRuntime:
     def consume_prefill_route_stats(self, *, layer_id: int, topk_ids: torch.Tensor) -> dict[int, int] | None:
         stats = self.consume_prefill_route_stats_record(layer_id=layer_id, topk_ids=topk_ids)
         return None if stats is None else dict(stats.token_counts_by_expert)
+
+    # ------------------------------------------------- device-planned waves
+    def can_run_device_waves(self, layer_id: int) -> bool:
+        """Device wave planning applies: enabled, an offloaded registered layer
+        on a device bank, a page-locked host store, shapes within the planner."""
+        from vllm_moe_offload_amd import native
+
+        layer_id = int(layer_id)
+        if not (self.config.device_wave_prefill and self.should_use_fixed_slot_plan_for_layer(layer_id)):
+            return False
+        bank = self._slot_banks.get(layer_id)
+        if bank is None or bank.w13_slots.device.type != "cuda":
+            return False
+        try:
+            buf = self._host_store.get_layer_buffer(layer_id)
+        except KeyError:
+            return False
+        routed = self.routed_expert_count_for_layer(layer_id=layer_id, fallback=buf.num_experts)
+        return bool(buf.pinned) and routed <= native.WAVE_PLAN_MAX_EXPERTS and \
+            bank.num_dynamic_slots <= native.WAVE_PLAN_MAX_SLOTS and buf.num_experts >= routed
+
+    def device_wave_plan_buffer(self, *, n_routed: int, n_slots: int, max_waves: int, device):
+        from vllm_moe_offload_amd import native
+
+        key = (int(n_routed), int(n_slots), int(max_waves), str(device))
+        plan = self._device_wave_plans.get(key)
+        if plan is None:
+            plan = native.WavePlan(n_routed, n_slots, max_waves, device)
+            self._device_wave_plans[key] = plan
+        return plan
+
+    def mark_device_waves(self, *, layer_id: int, topk_ids: torch.Tensor) -> None:
+        """The seam handed this layer's routed ids to the device planner."""
+        self._device_wave_marks[int(layer_id)] = self._route_stats_key(layer_id=layer_id, topk_ids=topk_ids)
+
+    def consume_device_waves(self, *, layer_id: int, topk_ids: torch.Tensor) -> bool:
+        key = self._device_wave_marks.pop(int(layer_id), None)
+        return key is not None and key == self._route_stats_key(layer_id=layer_id, topk_ids=topk_ids)
 
 
 # ---------------------------------------------------------------------------

@@ -54,6 +54,9 @@ EXPORTED_SYMBOLS = (
     "lmoe_stage_gather",
     "lmoe_table_update",
     "lmoe_slot_plan",
+    "lmoe_wave_plan_bytes",
+    "lmoe_wave_plan",
+    "lmoe_wave_stage",
 )
 
 _vp = ctypes.c_void_p
@@ -109,6 +112,13 @@ _SIGNATURES = {
     "lmoe_stage_gather": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp]),
     "lmoe_slot_plan": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, ctypes.c_int64, _vp, _vp]),
     "lmoe_table_update": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
+    "lmoe_wave_plan_bytes": (ctypes.c_longlong, [_i, _i, _i]),
+    "lmoe_wave_plan": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp]),
+    "lmoe_wave_stage": (
+        _i,
+        [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, ctypes.c_longlong, ctypes.c_longlong,
+         _vp, _i, _i, _i, _vp],
+    ),
 }
 
 _LIB: ctypes.CDLL | None = None
@@ -887,3 +897,84 @@ def table_update_entries(table: torch.Tensor, idx, val, *, stream=None) -> None:
     va = (ctypes.c_int32 * n)(*[int(v) for v in val])
     _check(lib.lmoe_table_update(_ptr(table), int(table.numel()), ia, va, n, _stream(stream)),
            "lmoe_table_update")
+
+
+# ---------------------------------------------------------------------------
+# device-side capacity waves (lmoe_wave_plan / lmoe_wave_stage)
+# ---------------------------------------------------------------------------
+WAVE_PLAN_MAX_EXPERTS = 1024
+WAVE_PLAN_MAX_SLOTS = 1024
+WAVE_PLAN_MAX_WAVES = 256
+
+
+class WavePlan:
+    """Device buffer of one layer shape's wave plan (fixed address, graph safe)."""
+
+    HEADER = 4
+
+    def __init__(self, n_routed: int, n_slots: int, max_waves: int, device) -> None:
+        n = int(load_library().lmoe_wave_plan_bytes(int(n_routed), int(n_slots), int(max_waves)))
+        if n < 0:
+            raise ValueError(f"device wave plan supports <= {WAVE_PLAN_MAX_EXPERTS} experts, "
+                             f"<= {WAVE_PLAN_MAX_SLOTS} slots and <= {WAVE_PLAN_MAX_WAVES} waves; got "
+                             f"{n_routed}, {n_slots}, {max_waves}")
+        self.n_routed, self.n_slots, self.max_waves = int(n_routed), int(n_slots), int(max_waves)
+        self.buf = torch.zeros(n // 4, dtype=torch.int32, device=device)
+
+    # host views (tests and evidence; each reads the device buffer)
+    def to_host(self) -> dict:
+        b = self.buf.cpu().tolist()
+        E, W, P, h = self.n_routed, self.max_waves, self.n_slots, self.HEADER
+        counts = b[h:h + E]
+        wave_of = b[h + E:h + 2 * E]
+        slot_of = b[h + 2 * E:h + 3 * E]
+        size = b[h + 3 * E:h + 3 * E + W]
+        members = b[h + 3 * E + W:]
+        n_waves = b[0]
+        waves = tuple(tuple(members[w * P:w * P + size[w]]) for w in range(max(n_waves, 0)))
+        return {"n_waves": n_waves, "n_active": b[1], "invalid": b[2], "counts": counts, "wave_of": wave_of,
+                "slot_of": slot_of, "size": size, "waves": waves}
+
+
+def wave_plan(ids: torch.Tensor, plan: WavePlan, *, n_total: int | None = None, stream=None) -> WavePlan:
+    lib = load_library()
+    _need(ids, "topk_ids", torch.int32)
+    n_total = plan.n_routed if n_total is None else int(n_total)
+    _check(lib.lmoe_wave_plan(_ptr(ids), int(ids.numel()), plan.n_routed, n_total, plan.n_slots, plan.max_waves,
+                              _ptr(plan.buf), _stream(stream)), "lmoe_wave_plan")
+    return plan
+
+
+def wave_stage(plan: WavePlan, wave: int, *, main_table: torch.Tensor, main_owner: torch.Tensor,
+               main_w13: torch.Tensor,
+               main_w2: torch.Tensor, main_slots: int, host_w13: torch.Tensor, host_w2: torch.Tensor,
+               stage_w13: torch.Tensor, stage_w2: torch.Tensor, stage_table: torch.Tensor,
+               n_pinned: int = 0, stream=None) -> None:
+    """Copy wave `wave`'s experts into the stage buffer and write its table.
+    host_w13 / host_w2 must be page-locked [n_routed, ...] blocks."""
+    lib = load_library()
+    for name, t in (("main_w13", main_w13), ("main_w2", main_w2), ("stage_w13", stage_w13),
+                    ("stage_w2", stage_w2), ("host_w13", host_w13), ("host_w2", host_w2)):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bf16 tensor")
+    if not (host_w13.is_pinned() and host_w2.is_pinned()):
+        raise ValueError("device wave staging reads the host store directly: it must be page-locked")
+    if int(host_w13.shape[0]) < plan.n_routed or int(main_table.numel()) < plan.n_routed:
+        raise ValueError("host store or main table does not cover the routed experts")
+    if int(stage_w13.shape[0]) < plan.n_slots + int(n_pinned) or int(main_w13.shape[0]) < int(main_slots):
+        raise ValueError("stage buffer or main bank is smaller than its slot count")
+    _need(main_table, "main_table", torch.int32)
+    _need(main_owner, "main_owner", torch.int32)
+    if int(main_owner.numel()) < int(main_slots):
+        raise ValueError("main_owner must hold one entry per main slot")
+    _need(stage_table, "stage_table", torch.int32)
+    b13 = int(host_w13[0].numel()) * 2
+    b2 = int(host_w2[0].numel()) * 2
+    if int(stage_w13[0].numel()) * 2 != b13 or int(stage_w2[0].numel()) * 2 != b2 or \
+            int(main_w13[0].numel()) * 2 != b13 or int(main_w2[0].numel()) * 2 != b2:
+        raise ValueError("expert row sizes differ between host store, main bank and stage buffer")
+    _check(lib.lmoe_wave_stage(
+        _ptr(plan.buf), plan.n_routed, plan.n_slots, plan.max_waves, int(wave), _ptr(main_table),
+        _ptr(main_owner), _ptr(main_w13), _ptr(main_w2), int(main_slots), _ptr(host_w13), _ptr(host_w2), _ptr(stage_w13),
+        _ptr(stage_w2), b13, b2, _ptr(stage_table), int(stage_table.numel()), int(n_pinned), plan.n_slots,
+        _stream(stream)), "lmoe_wave_stage")

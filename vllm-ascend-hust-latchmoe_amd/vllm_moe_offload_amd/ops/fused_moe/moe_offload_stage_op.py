@@ -108,15 +108,22 @@ def stage_topk_for_layer(runtime, topk_ids: torch.Tensor, layer_id: int, num_log
         return
     if not runtime.is_layer_registered(layer_id):
         raise RuntimeError(f"fixed-slot MoE layer {layer_id} is not registered; refusing native-weight fallback")
+    phase = int(phase)
+    hint = int(runtime.config.max_num_seqs_hint or 0)
+    tokens = int(topk_ids.shape[0]) if topk_ids.ndim > 0 else 0
+    prefill_sized = phase == PHASE_PREFILL or (phase == PHASE_UNKNOWN and hint > 0 and tokens > hint)
+    if prefill_sized and runtime.can_run_device_waves(layer_id):
+        # the waves are planned and staged on the device: no D2H here
+        runtime.mark_device_waves(layer_id=layer_id, topk_ids=topk_ids)
+        if os.environ.get("LATCHMOE_SEAM_PROBE"):
+            print(f"LATCHMOE_SEAM branch=device_waves layer={layer_id}", flush=True)
+        return
     flat = topk_ids.detach().reshape(-1).to("cpu", non_blocking=False)  # the seam's D2H
     counts, _ = count_active_experts_from_cpu_topk(flat, num_logical_experts=routed)
     active = tuple(sorted(counts))
-    phase = int(phase)
     n_active = len(active)
     over = n_active > int(runtime.config.num_slots)
     known = phase in (PHASE_PREFILL, PHASE_DECODE, PHASE_MIXED)
-    hint = int(runtime.config.max_num_seqs_hint or 0)
-    tokens = int(topk_ids.shape[0]) if topk_ids.ndim > 0 else 0
     decode_sized = phase == PHASE_DECODE or (phase == PHASE_UNKNOWN and 0 < tokens <= hint)
     if over and decode_sized and not is_moe_offload_adaptive_wave_context() and \
             runtime.can_stage_decode_overflow(layer_id=layer_id, active_expert_count=n_active):

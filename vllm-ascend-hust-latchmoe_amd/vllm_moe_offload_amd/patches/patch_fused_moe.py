@@ -31,6 +31,8 @@ import os
 import threading
 from contextlib import contextmanager
 
+import torch
+
 PATCH_TAG = "vllm_moe_offload_amd.moe_comm_method_runtime"
 SELECT_TAG = "vllm_moe_offload_amd.select_experts"
 ENGINE_TAG = "vllm_moe_offload_amd.engine_args"
@@ -131,6 +133,20 @@ def _patch_moe_comm_method_runtime_hooks(_comm) -> bool:
             return original_fused(self, fused_experts_input)
         runtime = get_moe_offload_runtime()
         layer_id = int(off.layer_id)
+        if runtime.consume_device_waves(layer_id=layer_id, topk_ids=fused_experts_input.topk_ids):
+            # the seam left this overflow to the device planner: no host step
+            fused_moe.check_supported_input(fused_experts_input)
+            w = fused_experts_input.topk_weights
+            out = fused_moe.run_device_waves(
+                runtime, layer_id=layer_id, hidden=fused_experts_input.hidden_states,
+                topk_weights=w if w.dtype == torch.bfloat16 else w.to(torch.bfloat16),
+                topk_ids=fused_experts_input.topk_ids.to(torch.int32).contiguous(),
+                num_logical_experts=int(off.num_logical_experts),
+                add=getattr(fused_experts_input, "shared_output", None),
+            )
+            return result_cls(routed_out=out, before_dispatch_evt=None, before_gmm2_evt=None,
+                              before_combine_evt=None, group_list_type=1, expert_tokens=None,
+                              swiglu_limit=getattr(fused_experts_input, "swiglu_limit", None))
         stats = runtime.consume_prefill_route_stats_record(layer_id=layer_id, topk_ids=fused_experts_input.topk_ids)
         if stats is not None:
             # the stage op deferred an overflow: capacity waves, one combine
