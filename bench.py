@@ -482,6 +482,42 @@ def bench_prefill(host_w13, host_w2, T: int = 4096, slots: int = 48, reps: int =
                staged_h2d_gb=round(rep.h2d_bytes / 1e9, 3),
                staged_effective_h2d_gbs=round(rep.h2d_bytes / (staged_ms * 1e-3) / 1e9, 1))
 
+    # the same layer with the waves planned and staged on the device (no D2H
+    # of the ids, no host step per wave), eager and as one captured graph
+    rt_d = MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=slots, async_load=True, b2_wave_prefill=True,
+                                              device_wave_prefill=True))
+    rt_d.register_host_buffers(layer_id=0, w13_host=host_w13, w2_host=host_w2, slot_device=dev)
+    out_d = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+
+    def device_waves():
+        fused_moe.run_device_waves(rt_d, layer_id=0, hidden=x, topk_weights=w, topk_ids=ids, num_logical_experts=E,
+                                   out=out_d)
+
+    device_waves()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(nrep):
+        device_waves()
+    torch.cuda.synchronize()
+    dev_ms = (time.perf_counter() - t0) * 1000.0 / nrep
+    s_cap = torch.cuda.Stream()
+    s_cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_cap):
+        device_waves()
+    torch.cuda.current_stream().wait_stream(s_cap)
+    g_d = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_d):
+        device_waves()
+    with Timer() as t:
+        for _ in range(nrep):
+            g_d.replay()
+    graph_ms = t.ms() / nrep
+    torch.cuda.synchronize()
+    res.update(device_planned_staged_wave_ms=round(dev_ms, 2), device_planned_graph_ms=round(graph_ms, 2),
+               device_planned_equal_host_planned_bitwise=bool(torch.equal(out_d.view(torch.int16),
+                                                                          out_w.view(torch.int16))))
+    del g_d
+
     # compute-only: all waves' experts resident in per-wave banks
     full, _ = rt.prepare_full_layer_prefill_plan(layer_id=0, num_logical_experts=E, device=dev)
     torch.cuda.synchronize()
