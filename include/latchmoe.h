@@ -75,7 +75,11 @@ enum {
   LMOE_META_PAIRS = 1,   /* number of pairs placed in the sorted order      */
   LMOE_META_ERRORS = 2,  /* pairs dropped because their id did not map      */
   LMOE_META_TILES = 3,   /* sum over slots of ceil(count / block_m)         */
-  LMOE_META_COUNT = 4
+  LMOE_META_GEN = 4,     /* builds of this permutation so far (+1 per build) */
+  LMOE_META_DECODE_TIMEOUT = 5,  /* lmoe_decode_one: 1 if a wait gave up     */
+  LMOE_META_DECODE_HINT = 6,     /* lmoe_decode_one: 136 hand-off counters,
+                                    zeroed by every build                    */
+  LMOE_META_COUNT = 144
 };
 
 const char* lmoe_status_string(int status);
@@ -173,7 +177,8 @@ size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);
  * flat order; row_idx[p] = sorted position of pair p or -1; active[a] = a-th
  * slot with count > 0 (ascending), -1 for a >= meta[LMOE_META_ACTIVE];
  * tile_off[s] = sum over s' < s of
- * ceil(counts[s'] / block_m); meta[LMOE_META_COUNT].
+ * ceil(counts[s'] / block_m); meta[LMOE_META_COUNT] (ACTIVE, PAIRS, ERRORS,
+ * TILES; GEN advanced and the lmoe_decode_one counters zeroed).
  * Replaces slot_mapping.py:116-140 + npu_moe_init_routing_v2
  * (patch_fused_moe.py:668-701: expert_capacity=-1, drop_pad_mode=0,
  * expert_tokens_num_type=1). */
@@ -355,6 +360,28 @@ int lmoe_slot_plan(int8_t* state, int32_t* owner, int64_t* version,
  * write, or an index_copy_ of the changed entries). */
 int lmoe_table_update(int32_t* table, int n_table, const int32_t* idx,
                       const int32_t* val, int n, hipStream_t stream);
+
+/* One-token decode body in ONE launch (T = 1, k <= 8 pairs in distinct
+ * slots, as lmoe_fused_moe_decode with distinct_slots): gate_up + SiLU*mul
+ * producers and down + combine consumers in one grid, the consumers' W2
+ * rows in flight while the producers run.  act values pass between
+ * workgroups as tagged 32-bit words (bf16 | (meta[LMOE_META_GEN] & 0xffff)
+ * << 16, words [k, I] u32, zero before the first call) through agent-scope
+ * atomic accesses, and the producers' progress through the counters in
+ * meta[LMOE_META_DECODE_HINT..]; the permutation build (lmoe_permute,
+ * lmoe_router_*_permute) that precedes the call advances the generation
+ * and zeroes the counters, so AT MOST ONE lmoe_decode_one may run per
+ * build (a second one on the same build may read the first one's act), and
+ * one words buffer serves one permutation.  Every wait is bounded:
+ * meta[LMOE_META_DECODE_TIMEOUT] becomes 1 if one gave up (the result is
+ * then undefined).  out equals lmoe_fused_moe_decode's bit for bit.
+ * Shapes: H <= 4096, I <= 1024 (others return LMOE_ERR_UNSUPPORTED: use
+ * lmoe_fused_moe_decode).  Replaces the decode fused_experts call of
+ * patches/patch_fused_moe.py:3946-4009 for one token. */
+int lmoe_decode_one(const void* x, int H, int I, int k, const void* w13_slots,
+                    const void* w2_slots, int n_slots, const uint16_t* w,
+                    const int32_t* row_idx, const int32_t* active, const void* add,
+                    void* words, void* out, int32_t* meta, hipStream_t stream);
 
 /* Bytes of the int32 plan buffer of lmoe_wave_plan / lmoe_wave_stage for
  * n_routed <= 1024 experts, n_slots <= 1024 stage slots and max_waves <= 256

@@ -37,7 +37,8 @@ def _check_perm(native, perm, ref, n_pairs):
     np.testing.assert_array_equal(perm.active.cpu().numpy()[: ref.active.size], ref.active)
     np.testing.assert_array_equal(perm.tile_off.cpu().numpy(), ref.tile_off)
     meta = perm.meta.cpu().numpy()
-    assert list(meta) == [ref.active.size, ref.placed, ref.errors, ref.tile_off[-1]]
+    assert list(meta[:4]) == [ref.active.size, ref.placed, ref.errors, ref.tile_off[-1]]
+    assert meta[native.META_GEN] == perm.builds  # one per build
 
 
 @pytest.mark.parametrize("T,E,k,P,skip", [
@@ -153,7 +154,8 @@ def test_decode_layer_equals_route_then_fused_experts(T):
     assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
     for name in ("counts", "offsets", "sorted_pairs", "row_idx", "active", "tile_off", "meta"):
         a, b = getattr(ws_a.perm, name), getattr(ws_b.perm, name)
-        n = T * k if name in ("sorted_pairs", "row_idx") else a.numel()
+        # meta: the four counts (past them, build count and decode hand-off state)
+        n = T * k if name in ("sorted_pairs", "row_idx") else 4 if name == "meta" else a.numel()
         assert torch.equal(a[:n], b[:n]), name
 
 

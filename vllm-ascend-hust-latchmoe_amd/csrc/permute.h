@@ -39,6 +39,15 @@ __device__ __forceinline__ int map_pair(const int32_t* ids, int p,
   return -2;
 }
 
+// Per-build state past the four counts: the build counter advances and the
+// one-token decode body's hand-off counters start from zero.  Called by the
+// one thread that publishes meta.
+constexpr int kDecodeHintWords = LMOE_META_COUNT - LMOE_META_DECODE_TIMEOUT;
+__device__ __forceinline__ void publish_build(int32_t* meta) {
+  meta[LMOE_META_GEN] = meta[LMOE_META_GEN] + 1;
+  for (int i = LMOE_META_DECODE_TIMEOUT; i < LMOE_META_COUNT; ++i) meta[i] = 0;
+}
+
 __device__ __forceinline__ uint64_t match_key(int key, int nbits) {
   uint64_t m = __ballot(1);
   for (int b = 0; b < nbits; ++b) {
@@ -118,6 +127,7 @@ __device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
     meta[LMOE_META_ACTIVE] = atot;
     meta[LMOE_META_PAIRS] = ctot;
     meta[LMOE_META_TILES] = ttot;
+    publish_build(meta);
   }
 }
 
@@ -299,6 +309,7 @@ __device__ __forceinline__ void permute_wave(
     meta[LMOE_META_PAIRS] = ctot;
     meta[LMOE_META_ERRORS] = errs;
     meta[LMOE_META_TILES] = ttot;
+    publish_build(meta);
   }
   // groups in flat order: read the slot's running base, then its first
   // pair of the group advances it past the group's pairs

@@ -27,7 +27,8 @@ LMOE_PATH_MFMA = 2
 LMOE_ERR_ARG = 1000
 LMOE_ERR_SHAPE = 1001
 META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
-META_COUNT = 4
+META_GEN, META_DECODE_TIMEOUT = 4, 5
+META_COUNT = 144
 MFMA_BLOCK_M = 256  # row-tile height of the prefill MFMA GEMM (tile table of lmoe_permute)
 PART_BLOCK_M = 320  # row tiles of the one-workgroup-per-CU prefill GEMM (lmoe_grouped_mlp)
 FUSED_DECODE_MAX_PAIRS = 1024
@@ -54,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "lmoe_stage_gather",
     "lmoe_table_update",
     "lmoe_slot_plan",
+    "lmoe_decode_one",
     "lmoe_wave_plan_bytes",
     "lmoe_wave_plan",
     "lmoe_wave_stage",
@@ -112,6 +114,7 @@ _SIGNATURES = {
     "lmoe_stage_gather": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp]),
     "lmoe_slot_plan": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, ctypes.c_int64, _vp, _vp]),
     "lmoe_table_update": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
+    "lmoe_decode_one": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "lmoe_wave_plan_bytes": (ctypes.c_longlong, [_i, _i, _i]),
     "lmoe_wave_plan": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "lmoe_wave_stage": (
@@ -334,6 +337,7 @@ def router_topk_permute(
         permute(ids, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, block_m=bm, stream=stream)
         return w_bf16, ids, w_f32
     _check(status, "lmoe_router_topk_permute")
+    perm.builds += 1
     perm.block_m = bm
     return w_bf16, ids, w_f32
 
@@ -415,6 +419,7 @@ def router_gate_topk_permute(
             w_bf16=w_bf16, ids=ids, w_f32=w_f32, stream=stream,
         )
     _check(status, "lmoe_router_gate_topk_permute")
+    perm.builds += 1
     perm.block_m = bm
     return w_bf16, ids, w_f32
 
@@ -482,6 +487,17 @@ class Permutation:
     workspace: torch.Tensor     # int8 scratch for the multi-block path
     sync: torch.Tensor          # [1] i32 arrival counter of the one-launch router, kept at 0
     block_m: int = MFMA_BLOCK_M  # tile height tile_off was last built with
+    # the one-launch one-token decode body: its tagged act words ([8, I]
+    # u32 for the I it last ran with; the counters live in meta), and which
+    # build it last ran on (one launch per build)
+    decode_words: torch.Tensor | None = None
+    builds: int = 0
+    decoded_build: int = -1
+
+    def decode_words_for(self, I: int, device) -> torch.Tensor:
+        if self.decode_words is None or int(self.decode_words.shape[1]) != int(I):
+            self.decode_words = torch.zeros((8, int(I)), dtype=torch.int32, device=device)
+        return self.decode_words
 
     @classmethod
     def allocate(cls, n_pairs: int, n_slots: int, device) -> "Permutation":
@@ -537,6 +553,7 @@ def permute(
         "lmoe_permute",
     )
     perm.block_m = int(block_m)
+    perm.builds += 1
     return perm
 
 
@@ -718,6 +735,18 @@ def fused_moe_decode(
         _need(add, "add", torch.bfloat16, (T, H))
     if y is not None:
         _need(y, "y", torch.bfloat16, (perm.n_pairs, H))
+    if distinct_slots and T == 1 and decode_one_supported(H, I, k) and perm.decoded_build != perm.builds:
+        # one launch: the down weights stream in while gate_up runs (at most
+        # once per permutation build: the build starts its hand-off state)
+        words = perm.decode_words_for(I, x.device)
+        _check(
+            lib.lmoe_decode_one(_ptr(x), H, I, k, _ptr(w13_slots), _ptr(w2_slots), P, _ptr(topk_weights),
+                                _ptr(perm.row_idx), _ptr(perm.active), _ptr(add), _ptr(words), _ptr(out),
+                                _ptr(perm.meta), _stream(stream)),
+            "lmoe_decode_one",
+        )
+        perm.decoded_build = perm.builds
+        return out
     _check(
         lib.lmoe_fused_moe_decode(
             _ptr(x), T, H, I, k, _ptr(w13_slots), _ptr(w2_slots), P, _ptr(topk_weights),
@@ -728,6 +757,17 @@ def fused_moe_decode(
         "lmoe_fused_moe_decode",
     )
     return out
+
+
+def decode_one_supported(H: int, I: int, k: int) -> bool:
+    """lmoe_decode_one is switched on (LATCHMOE_DECODE_ONE=1; off by
+    default: on the Qwen3-shaped layer it measured 39.7 us per layer in the
+    48-layer decode graph against 23.4 us for the two-kernel body, its
+    consumers holding W2 in registers halve the producers' occupancy) and
+    takes the shape (the others run the two-kernel body)."""
+    if os.environ.get("LATCHMOE_DECODE_ONE", "0") != "1":
+        return False
+    return k <= 8 and H % 8 == 0 and I % 64 == 0 and (H + 511) // 512 <= 8 and (I + 255) // 256 <= 4
 
 
 NOALLOC_SCRATCH_BYTES = 8 << 20  # LMOE_NOALLOC_SCRATCH_BYTES
