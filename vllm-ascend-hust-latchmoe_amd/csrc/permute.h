@@ -39,13 +39,14 @@ __device__ __forceinline__ int map_pair(const int32_t* ids, int p,
   return -2;
 }
 
-// Per-build state past the four counts: the build counter advances and the
-// one-token decode body's hand-off counters start from zero.  Called by the
-// one thread that publishes meta.
-constexpr int kDecodeHintWords = LMOE_META_COUNT - LMOE_META_DECODE_TIMEOUT;
+// Per-build state past the four counts: the build counter advances (the
+// one thread that publishes meta) and the one-token decode body's hand-off
+// counters start from zero (every thread t of n takes words t, t + n, ...).
 __device__ __forceinline__ void publish_build(int32_t* meta) {
   meta[LMOE_META_GEN] = meta[LMOE_META_GEN] + 1;
-  for (int i = LMOE_META_DECODE_TIMEOUT; i < LMOE_META_COUNT; ++i) meta[i] = 0;
+}
+__device__ __forceinline__ void clear_decode_handoff(int32_t* meta, int t, int n) {
+  for (int i = LMOE_META_DECODE_TIMEOUT + t; i < LMOE_META_COUNT; i += n) meta[i] = 0;
 }
 
 __device__ __forceinline__ uint64_t match_key(int key, int nbits) {
@@ -121,6 +122,7 @@ __device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
   // active[a] = -1 past the active slots: kernels that serve "the a-th
   // active slot" read one value (no dependent load of meta first)
   for (int a = atot + threadIdx.x; a < P; a += blockDim.x) active[a] = -1;
+  clear_decode_handoff(meta, threadIdx.x, blockDim.x);
   if (threadIdx.x == 0) {
     offsets[P] = ctot;
     tile_off[P] = ttot;
@@ -302,6 +304,7 @@ __device__ __forceinline__ void permute_wave(
   }
   // active[a] = -1 past the active slots (see scan_slots)
   for (int a = atot + lane; a < P; a += kWave) active[a] = -1;
+  clear_decode_handoff(meta, lane, kWave);
   if (lane == 0) {
     offsets[P] = ctot;
     tile_off[P] = ttot;
