@@ -43,7 +43,8 @@ __device__ __forceinline__ int map_pair(const int32_t* ids, int p,
 // one thread that publishes meta) and the one-token decode body's hand-off
 // counters start from zero (every thread t of n takes words t, t + n, ...).
 __device__ __forceinline__ void publish_build(int32_t* meta) {
-  meta[LMOE_META_GEN] = meta[LMOE_META_GEN] + 1;
+  // no-return atomic: the publishing thread does not wait for the old value
+  __hip_atomic_fetch_add(meta + LMOE_META_GEN, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void clear_decode_handoff(int32_t* meta, int t, int n) {
   for (int i = LMOE_META_DECODE_TIMEOUT + t; i < LMOE_META_COUNT; i += n) meta[i] = 0;
