@@ -983,6 +983,17 @@ def main() -> int:
     if args.out:
         Path(args.out).write_text(text + "\n")
     log(f"decode phase {t_decode:.1f}s total")
+    # free page-locked and device memory while the runtime is still up (a
+    # profiler that shuts the runtime down first must not see it freed later)
+    import gc
+
+    from vllm_moe_offload_amd import fused_moe
+
+    del host_w13, host_w2
+    fused_moe.clear_workspaces()
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     return 0
 
 

@@ -2,14 +2,19 @@
 // C[m][n] = sum_k A[m][k] * W[n][k], f32 accumulation, A rows gathered per
 // slot group, W read from the slot bank ([P, N, K] row-major, K contiguous).
 //
-// Block tile BM x BN, K staged 64 columns at a time through a STAGES-deep
-// ring of LDS buffers.  Operands go HBM/L2 -> LDS with global_load_lds_dwordx4
-// (16 bytes per lane, no register staging): one instruction fills 8 LDS rows
-// of 128 bytes, lane l landing at row l/8, 16-byte chunk l%8.  LDS holds
-// logical chunk c of row r at position c ^ sw(r), sw(r) = (r%8) ^ ((r/8)%2),
-// so the lane loads the chunk that belongs at its landing position.  A
-// fragment read (32 rows, one chunk each) then hits distinct banks both per
-// 8 lanes over 128 bytes and per 16 lanes over 256 bytes.
+// Block tile BM x BN, K staged BK (64 or 32) columns at a time through a
+// STAGES-deep ring of LDS buffers.  Operands go HBM/L2 -> LDS with
+// global_load_lds_dwordx4 (16 bytes per lane, no register staging): one
+// instruction fills 1 KiB of LDS rows (BK 64: 8 rows of 128 bytes, lane l
+// landing at row l/8, 16-byte chunk l%8; BK 32: 16 rows of 64 bytes, row l/4,
+// chunk l%4).  LDS holds logical chunk c of row r at position c ^ sw(r), so
+// the lane loads the chunk that belongs at its landing position:
+//   BK 64: sw(r) = (r%8) ^ ((r/8)%2)
+//   BK 32: sw(r) = ((r/2) ^ (r/8)) % 4
+// A fragment read (32 rows, one chunk each) then hits distinct banks both per
+// 8 lanes over 128 bytes and per 16 lanes over 256 bytes.  The 32-column
+// stage halves the ring's footprint, so the same LDS holds twice the stages
+// and twice the loads in flight ahead of the MFMAs.
 //
 // Waves form a WM x WN grid; a wave owns a (BM/WM) x (BN/WN) sub-tile as
 // 32x32 blocks of v_mfma_f32_32x32x16_bf16 with the weight fragment as the
@@ -39,13 +44,24 @@
 
 namespace lmoe {
 
-template <int BM_, int BN_, int WM_, int WN_, int STAGES_>
+// Swizzle of staged row r (see the header): the chunk position that logical
+// chunk c of row r occupies is c ^ lds_swz<BK>(r).
+template <int BK>
+__device__ __forceinline__ int lds_swz(int r) {
+  static_assert(BK == 64 || BK == 32, "staged rows are 128 or 64 bytes");
+  return BK == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : (((r >> 1) ^ (r >> 3)) & 3);
+}
+
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_, int BK_ = 64>
 struct LdsTile {
-  static constexpr int BM = BM_, BN = BN_, BK = 64, WM = WM_, WN = WN_, STAGES = STAGES_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, STAGES = STAGES_;
   static constexpr int NW = WM * WN;
   static constexpr int THREADS = NW * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
   static constexpr int NI = WTM / 32, NJ = WTN / 32;
+  static constexpr int ROWB = BK * 2;        // bytes of one staged row
+  static constexpr int CPR = BK / 8;         // 16-byte chunks per staged row
+  static constexpr int RPL = 1024 / ROWB;    // rows one load instruction fills
   static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int QA = A_BYTES / 1024 / NW;  // load instructions per wave per stage
@@ -117,25 +133,27 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
   }
 
   // ---- per-lane source rows for this wave's load instructions ----
-  // instruction q fills rows 8*gq .. 8*gq+7; the lane lands at row 8*gq + l/8,
-  // position l%8, and loads the logical chunk stored there: (l%8) ^ sw(row)
-  const int lrow = lane >> 3;
+  // instruction q fills rows RPL*gq .. RPL*gq+RPL-1; the lane lands at row
+  // RPL*gq + l/CPR, position l%CPR, and loads the logical chunk stored
+  // there: (l%CPR) ^ sw(row)
+  const int lrow = lane / C::CPR;
+  const int lpos = lane % C::CPR;
   const uint16_t* a_src[C::QA];
   const uint16_t* b_src[C::QB];
 #pragma unroll
   for (int q = 0; q < C::QA; ++q) {
     const int gq = wave * C::QA + q;
-    const int r = gq * 8 + lrow;
+    const int r = gq * C::RPL + lrow;
     const int pos = row0 + (r < rows ? r : 0);
     const int arow = (MODE == kGateUp) ? g.sorted_pairs[pos] / g.topk : pos;
-    const int lchunk = ((lane & 7) ^ lrow ^ (gq & 1)) * 8;
+    const int lchunk = (lpos ^ lds_swz<C::BK>(r)) * 8;
     a_src[q] = g.a + static_cast<long long>(arow) * g.K + lchunk;
   }
 #pragma unroll
   for (int q = 0; q < C::QB; ++q) {
     const int gq = wave * C::QB + q;
-    const int r = gq * 8 + lrow;
-    const int lchunk = ((lane & 7) ^ lrow ^ (gq & 1)) * 8;
+    const int r = gq * C::RPL + lrow;
+    const int lchunk = (lpos ^ lds_swz<C::BK>(r)) * 8;
     int wrow;
     if (MODE == kGateUp) {
       const int half = r / (C::BN / 2);
@@ -167,13 +185,13 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   // fragment reads: row base + l%32 (bases are multiples of 32, so
-  // sw(row) = (l%8) ^ ((l/8)%2)), logical chunk 2*ks + l/32
+  // sw(row) = sw(l%32)), logical chunk 2*ks + l/32
   const int frow = lane & 31;
   const int fhi = lane >> 5;
-  const int fsw = (lane & 7) ^ ((lane >> 3) & 1);
+  const int fsw = lds_swz<C::BK>(frow);
   int a_off[C::NI], b_off[C::NJ];
 #pragma unroll
-  for (int i = 0; i < C::NI; ++i) a_off[i] = (wm * C::WTM + i * 32 + frow) * 128;
+  for (int i = 0; i < C::NI; ++i) a_off[i] = (wm * C::WTM + i * 32 + frow) * C::ROWB;
 #pragma unroll
   for (int j = 0; j < C::NJ; ++j) {
     int br;
@@ -184,7 +202,7 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
     } else {
       br = wn * C::WTN + j * 32;
     }
-    b_off[j] = C::A_BYTES + (br + frow) * 128;
+    b_off[j] = C::A_BYTES + (br + frow) * C::ROWB;
   }
   // 32-row blocks of this wave that hold at least one valid row
   const int wave_rows = rows - wm * C::WTM;

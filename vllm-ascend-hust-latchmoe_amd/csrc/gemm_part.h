@@ -20,9 +20,15 @@
 // A sub-tile is the 256-row kernel's tile (grouped_gemm_lds_kernel) grown to
 // 320 rows: 8 waves as 2 x 4, each owning 160 x 64 (5 x 2 blocks of
 // v_mfma_f32_32x32x16_bf16 with the weight fragment first), operands staged
-// 64 K-columns at a time by direct-to-LDS loads into a two-stage ring, LDS
-// rows swizzled as there.  Weight rows of columns outside the sub-tile are not
-// loaded, and waves without live columns skip their MFMAs.  Every output
+// 64 K-columns at a time by direct-to-LDS loads into a two-stage ring (LDS
+// rows of 128 bytes, swizzled as there).  A stage is 72 load instructions of
+// 1 KiB (40 for the 320 activation rows, 32 for the 256 weight rows), dealt
+// round-robin over the waves; a tile with BK 32 and up to four stages
+// deals 36 per stage (waves 0-3 issue 5, waves 4-7 issue 4) and each wave
+// waits for its own count.  Rows past the tile's valid rows and weight rows
+// of columns outside the sub-tile load a valid row whose result is dropped,
+// so the count per stage is fixed; waves without live columns skip their
+// MFMAs.  Every output
 // element accumulates its K/16 MFMA steps in increasing k, the order of the
 // other grouped kernels, so all of them give identical bits.
 //
@@ -38,22 +44,28 @@
 namespace lmoe {
 
 struct PartTile {
-  static constexpr int BM = 320, BN = 256, BK = 64, WM = 2, WN = 4;
+  static constexpr int BM = 320, BN = 256, BK = 64, STAGES = 2, WM = 2, WN = 4;
   static constexpr int NW = WM * WN;
   static constexpr int THREADS = NW * 64;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // 160 x 64
   static constexpr int NI = WTM / 32, NJ = WTN / 32;  // 5 x 2
-  static constexpr int A_BYTES = BM * BK * 2, B_BYTES = BN * BK * 2;
-  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  static constexpr int QA = A_BYTES / 1024 / NW;  // 5 loads per wave per stage
-  static constexpr int QB = B_BYTES / 1024 / NW;  // 4
-  static constexpr int RING_BYTES = 2 * STAGE_BYTES;                 // 144 KiB
+  static constexpr int ROWB = BK * 2;                 // 128-byte staged rows
+  static constexpr int CPR = BK / 8;                  // 8 chunks per row
+  static constexpr int RPL = 1024 / ROWB;             // 8 rows per load
+  static constexpr int A_LOADS = BM / RPL, B_LOADS = BN / RPL;  // 40, 32
+  static constexpr int LOADS = A_LOADS + B_LOADS;     // 72 per stage
+  static constexpr int Q_HI = (LOADS + NW - 1) / NW;  // waves below LOADS % NW
+  static constexpr int Q_LO = LOADS / NW;             // the others (9 = 9 here)
+  static constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;              // 72 KiB
+  static constexpr int RING_BYTES = STAGES * STAGE_BYTES;            // 144 KiB
   static constexpr int GU_OUT_BYTES = BM * ((BN / 2) * 2 + 16);      // 85 KiB
   static constexpr int DN_OUT_BYTES = (BM / 2) * (BN * 2 + 16);      // 82.5 KiB per half
   static constexpr int MAIN_BYTES = RING_BYTES;
   static constexpr int LDS_BYTES = MAIN_BYTES + BM * 4;  // + destination row ids (down)
   static_assert(GU_OUT_BYTES <= MAIN_BYTES && DN_OUT_BYTES <= MAIN_BYTES, "epilogue staging");
-  static_assert(QA * NW * 1024 == A_BYTES && QB * NW * 1024 == B_BYTES, "1 KiB loads per wave");
+  static_assert(A_LOADS * RPL == BM && B_LOADS * RPL == BN, "whole 1 KiB loads");
+  static_assert(STAGES >= 2 && STAGES <= 4, "the stage waits allow up to two later stages");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS footprint too large");
   static_assert(WTM * 2 == BM, "the down epilogue stages one wave row at a time");
 };
@@ -94,10 +106,9 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_part_kernel(GemmArgs 
   long long b = blocks_before(U * r / G);
   const long long b_end = blocks_before(U * (r + 1) / G);
 
-  const int lrow = lane >> 3;
   const int frow = lane & 31;
   const int fhi = lane >> 5;
-  const int fsw = (lane & 7) ^ ((lane >> 3) & 1);
+  const int fsw = lds_swz<C::BK>(frow);
   const int KT = g.K / C::BK;
 
   while (b < b_end) {
@@ -118,53 +129,62 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_part_kernel(GemmArgs 
         s_rowid[t] = g.sorted_pairs[row0 + (t < rows ? t : 0)];
     }
 
-    // per-lane source rows of this wave's load instructions (see gemm_lds.h),
-    // as 32-bit element offsets from the operand bases: the launch refuses
-    // (LMOE_ERR_SHAPE) an activation operand whose rows reach 2^31 elements
-    // (part_offsets_fit), and a weight offset stays inside one slot
-    int a_src[C::QA];
-    int b_src[C::QB];
+    // per-lane sources of this wave's load instructions: load t = wave + NW*q
+    // of a stage fills LDS bytes [1024 t, 1024 t + 1024) of it, activation
+    // rows for t < A_LOADS, weight rows after; the lane lands at row
+    // RPL*t' + l/CPR, position l%CPR, and loads the logical chunk stored there.
+    // Offsets are 32-bit element offsets from the operand bases: the launch
+    // refuses (LMOE_ERR_SHAPE) an activation operand whose rows reach 2^31
+    // elements (part_offsets_fit), and a weight offset stays inside one slot
+    const int lrow = lane / C::CPR;
+    const int lpos = lane % C::CPR;
+    const int nq = wave < C::LOADS % C::NW ? C::Q_HI : C::Q_LO;
+    int src[C::Q_HI];
 #pragma unroll
-    for (int q = 0; q < C::QA; ++q) {
-      const int gq = wave * C::QA + q;
-      const int rr = gq * 8 + lrow;
-      const int pos = row0 + (rr < rows ? rr : 0);
-      const int arow = (MODE == kGateUp) ? g.sorted_pairs[pos] / g.topk : pos;
-      const int lchunk = ((lane & 7) ^ lrow ^ (gq & 1)) * 8;
-      a_src[q] = arow * g.K + lchunk;
-    }
-    // an instruction's 8 weight rows lie in one 32-row block, so whether
-    // they belong to a live column block is wave-uniform
-    auto b_live = [&](int q) {
-      const int gq = wave * C::QB + q;
-      return (MODE == kGateUp) ? ((gq * 8) % (C::BN / 2)) < 32 * w : gq * 8 < 32 * w;
-    };
-#pragma unroll
-    for (int q = 0; q < C::QB; ++q) {
-      const int gq = wave * C::QB + q;
-      const int rr = gq * 8 + lrow;
-      const int lchunk = ((lane & 7) ^ lrow ^ (gq & 1)) * 8;
-      int wrow;
-      if (MODE == kGateUp) {
-        const int half = rr / (C::BN / 2);
-        int i = n0 + rr - half * (C::BN / 2);
-        if (i >= g.N || !b_live(q)) i = n0;
-        wrow = half * g.I + i;
+    for (int q = 0; q < C::Q_HI; ++q) {
+      const int t = wave + C::NW * q;
+      if (t < C::A_LOADS) {
+        const int rr = t * C::RPL + lrow;
+        const int pos = row0 + (rr < rows ? rr : 0);
+        const int arow = (MODE == kGateUp) ? g.sorted_pairs[pos] / g.topk : pos;
+        src[q] = arow * g.K + (lpos ^ lds_swz<C::BK>(rr)) * 8;
       } else {
-        wrow = (n0 + rr < g.N && b_live(q)) ? n0 + rr : n0;
+        const int rr = (t - C::A_LOADS) * C::RPL + lrow;
+        int wrow;
+        if (MODE == kGateUp) {
+          // gate rows n0.., then the matching up rows I + n0..
+          const int half = rr / (C::BN / 2);
+          const int c = rr - half * (C::BN / 2);
+          const int i = (c < 32 * w && n0 + c < g.N) ? n0 + c : n0;
+          wrow = half * g.I + i;
+        } else {
+          wrow = (rr < 32 * w && n0 + rr < g.N) ? n0 + rr : n0;
+        }
+        src[q] = wrow * g.K + (lpos ^ lds_swz<C::BK>(rr)) * 8;
       }
-      b_src[q] = wrow * g.K + lchunk;
     }
 
     auto issue = [&](int kt, int buf) {
       char* st = smem + buf * C::STAGE_BYTES;
       const int koff = kt * C::BK;
 #pragma unroll
-      for (int q = 0; q < C::QA; ++q)
-        load_lds16(g.a + (a_src[q] + koff), st + (wave * C::QA + q) * 1024);
-#pragma unroll
-      for (int q = 0; q < C::QB; ++q)
-        if (b_live(q)) load_lds16(wbase + (b_src[q] + koff), st + C::A_BYTES + (wave * C::QB + q) * 1024);
+      for (int q = 0; q < C::Q_HI; ++q) {
+        const int t = wave + C::NW * q;
+        if (q < nq) load_lds16((t < C::A_LOADS ? g.a : wbase) + (src[q] + koff), st + t * 1024);
+      }
+    };
+    // stage kt landed: at most `ahead` later stages of this wave's loads
+    // (nq each) still in flight; then meet the other waves
+    auto wait_stage = [&](int ahead) {
+      if (nq == C::Q_HI) {
+        if (ahead >= 2) vm_wait_barrier<2 * C::Q_HI>();
+        else if (ahead == 1) vm_wait_barrier<C::Q_HI>();
+        else vm_wait_barrier<0>();
+      } else {
+        if (ahead >= 2) vm_wait_barrier<2 * C::Q_LO>();
+        else if (ahead == 1) vm_wait_barrier<C::Q_LO>();
+        else vm_wait_barrier<0>();
+      }
     };
 
     f32x16_t acc[C::NI][C::NJ];
@@ -177,7 +197,7 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_part_kernel(GemmArgs 
 
     int a_off[C::NI], b_off[C::NJ];
 #pragma unroll
-    for (int i = 0; i < C::NI; ++i) a_off[i] = (wm * C::WTM + i * 32 + frow) * 128;
+    for (int i = 0; i < C::NI; ++i) a_off[i] = (wm * C::WTM + i * 32 + frow) * C::ROWB;
 #pragma unroll
     for (int j = 0; j < C::NJ; ++j) {
       int br;
@@ -188,21 +208,28 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_part_kernel(GemmArgs 
       } else {
         br = wn * C::WTN + j * 32;
       }
-      b_off[j] = C::A_BYTES + (br + frow) * 128;
+      b_off[j] = C::A_BYTES + (br + frow) * C::ROWB;
     }
     // this wave's live 32-row blocks and whether any of its columns is live
     const int wave_rows = rows - wm * C::WTM;
     const bool cols_live = (MODE == kGateUp) ? (wn * (C::WTN / 2) < 32 * w) : (wn * C::WTN < 32 * w);
     const int ni_live = (wave_rows <= 0 || !cols_live) ? 0 : min(C::NI, (wave_rows + 31) >> 5);
 
-    issue(0, 0);
+#pragma unroll
+    for (int s = 0; s < C::STAGES - 1; ++s)
+      if (s < KT) issue(s, s);
     auto main_loop = [&](auto nl_tag) {
       constexpr int NL = decltype(nl_tag)::value;
       int buf = 0;
       for (int kt = 0; kt < KT; ++kt) {
-        // stage kt landed and every wave is done with the other buffer
-        vm_wait_barrier<0>();
-        if (kt + 1 < KT) issue(kt + 1, buf ^ 1);
+        // stage kt landed and every wave is done with the buffer the next
+        // issue overwrites (the one stage kt-1 was multiplied from)
+        wait_stage(min(C::STAGES - 2, KT - 1 - kt));
+        if (kt + C::STAGES - 1 < KT) {
+          int nb = buf + C::STAGES - 1;
+          if (nb >= C::STAGES) nb -= C::STAGES;
+          issue(kt + C::STAGES - 1, nb);
+        }
         if constexpr (NL > 0) {
           const char* st = smem + buf * C::STAGE_BYTES;
           bf16x8_t bfr[2][C::NJ], af[2][NL];
@@ -227,7 +254,7 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_part_kernel(GemmArgs 
             __builtin_amdgcn_sched_barrier(0);
           }
         }
-        buf ^= 1;
+        buf = (buf + 1 == C::STAGES) ? 0 : buf + 1;
       }
     };
     // NL: 32-row blocks computed (a partial tile rounds up to 1, 2 or NI)

@@ -35,13 +35,16 @@ __global__ __launch_bounds__(64) void table_update_kernel(int32_t* __restrict__ 
 // stores, and writes the slot-table entries that publish them.  The batch is
 // cut into 256 KiB work items, dealt round-robin to kGatherGrid workgroups;
 // each lane keeps eight 16-byte loads in flight.  Measured on the MI355X
-// host link: ~57 GB/s from 64 workgroups on (a single large hipMemcpyAsync
-// reaches the same), with no per-copy command overhead.  Everything rides in
-// the kernel arguments: no descriptor buffer, no copy precedes the launch.
+// host link: 52-56 GB/s (a single large hipMemcpyAsync reaches the same),
+// with no per-copy command overhead, from 16 workgroups as from 128; the
+// smaller grid leaves the CUs to the compute kernels the copies overlap (the
+// B=1 decode step with prefetched misses: 7.5 ms against 8.0 ms).
+// Everything rides in the kernel arguments: no descriptor buffer, no copy
+// precedes the launch.
 // ---------------------------------------------------------------------------
 constexpr int kGatherMax = 32;        // copies per launch
 constexpr int kGatherTab = 128;       // slot-table pairs per launch
-constexpr int kGatherGrid = 128;      // workgroups (a multiple of 8: every XCD gets 16)
+constexpr int kGatherGrid = 16;       // workgroups (a multiple of 8: every XCD gets 2)
 constexpr long long kGatherItem16 = 16384;  // 16-byte words per work item (256 KiB)
 constexpr int kGatherThreads = 256;
 constexpr int kGatherUnroll = 8;

@@ -25,6 +25,7 @@ the reference copies with torch copy_ on its transfer stream.
 
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass
 
 import torch
@@ -114,6 +115,10 @@ class TransferEngine:
         self.bytes_issued = 0
         self.copies_issued = 0
         self.batches_gathered = 0  # batches the gather kernel carried
+        # "gather": page-locked sources go through the gather-copy kernel;
+        # "sdma": every batch goes to the copy engines (hipMemcpyAsync),
+        # which leave the compute units to the kernels they overlap
+        self.copy_engine = os.environ.get("LATCHMOE_COPY_ENGINE", "gather")
 
     # -- synchronous -------------------------------------------------------
     def load_sync(self, bundle: ExpertWeightBundle, slot: ExpertSlot) -> None:
@@ -181,7 +186,7 @@ class TransferEngine:
 
         if wait_event is not None:
             stream.wait_event(wait_event)
-        if direct and native.stage_gather(ranges, stream, table_update=table_update):
+        if direct and self.copy_engine == "gather" and native.stage_gather(ranges, stream, table_update=table_update):
             self.batches_gathered += 1
         else:
             native.stage_copy(ranges, stream, table_update=table_update)
