@@ -832,10 +832,29 @@ def bench_deepseek(batches=(1, 8, 32), prefill_tokens: int = 2048, reps: int = 2
 # ---------------------------------------------------------------------------
 # CPU baseline: the oracle of one layer on the host cores
 # ---------------------------------------------------------------------------
-def bench_cpu_baseline(budget_s: float = 15.0) -> dict:
-    """The numpy oracle of one Qwen3-shaped layer at decode B=1: gate,
-    softmax top-8, the 8 experts' SwiGLU MLP with f32 accumulation, combine.
-    Expert weights are generated lazily outside the timed region."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def bench_cpu_baseline(budget_s: float = 8.0) -> dict:
+    """The numpy oracle on the host cores, on bounded samples of the bench's
+    workloads (about 25 s in all):
+
+    * decode (C2): one Qwen3-shaped layer per step at B = 1, 4, 16, 64 --
+      gate, softmax top-8, the routed experts' SwiGLU MLP with f32
+      accumulation, combine; B = 1 is the headline `value`;
+    * prefill (C3): the 4096-token routing restricted to 16 of the 128
+      experts (~4096 pairs, ~256 rows per expert as in C3), GFLOP/s;
+    * staging (C4): expert copies (gate_up + down, 9.4 MB each) from one
+      host buffer to another, the CPU form of the host-store -> slot copy.
+
+    Expert weights are generated and stacked outside the timed regions."""
     import numpy as np
 
     from oracle import mlp as omlp
@@ -844,29 +863,75 @@ def bench_cpu_baseline(budget_s: float = 15.0) -> dict:
 
     rng = np.random.default_rng(5)
     wg = normal_bf16(rng, (E, H), 0.02)
-    experts: dict[int, tuple] = {}
-    t_total, tokens = 0.0, 0
+    # 16 distinct weight sets stand in for the 128 experts (expert e uses set
+    # e % 16): the oracle converts and multiplies each routed expert's weights
+    # whatever their values, and generating 128 sets would take longer than
+    # the legs themselves
+    pool = [(normal_bf16(rng, (2 * I, H), 0.02), normal_bf16(rng, (H, I), 0.02)) for _ in range(16)]
+
+    def expert(e: int):
+        return pool[e % len(pool)]
+
+    def decode_leg(B: int, budget: float) -> tuple[float, int]:
+        t_total, steps = 0.0, 0
+        t_start = time.perf_counter()
+        while time.perf_counter() - t_start < budget or steps < 2:
+            x = normal_bf16(rng, (B, H), 1.0)
+            t0 = time.perf_counter()
+            ids, _, wb = orouter.softmax_topk(orouter.gate_logits(x, wg), K)
+            t_route = time.perf_counter() - t0
+            used = np.unique(ids)
+            l2p = np.full(E, -1, dtype=np.int32)
+            l2p[used] = np.arange(used.size, dtype=np.int32)
+            w13 = np.stack([expert(int(e))[0] for e in used])
+            w2 = np.stack([expert(int(e))[1] for e in used])
+            t1 = time.perf_counter()
+            omlp.moe_layer(x, ids, wb, l2p, w13, w2)
+            t_total += t_route + (time.perf_counter() - t1)
+            steps += 1
+        return t_total / (steps * B) * 1e6, steps
+
+    decode = {}
+    for B, budget in ((1, budget_s), (4, 4.0), (16, 4.0), (64, 5.0)):
+        us, steps = decode_leg(B, budget)
+        decode[f"B{B}"] = {"us_per_token_per_layer": round(us, 1), "steps": steps}
+
+    # C3 sample: 4096 tokens routed uniformly, the pairs of 16 experts
+    T3, n3 = 4096, 16
+    ids3 = np.stack([rng.permutation(E)[:K] for _ in range(T3)]).astype(np.int32)
+    x3 = normal_bf16(rng, (T3, H), 1.0)
+    slot3 = np.where(ids3 < n3, ids3, -1).astype(np.int32)
+    w13_3 = np.stack([expert(e)[0] for e in range(n3)])
+    w2_3 = np.stack([expert(e)[1] for e in range(n3)])
+    pairs3 = int((slot3 >= 0).sum())
+    t0 = time.perf_counter()
+    omlp.grouped_mlp(x3, slot3, K, w13_3, w2_3)
+    t3 = time.perf_counter() - t0
+    prefill_gflops = 2.0 * pairs3 * 3 * H * I / t3 / 1e9
+
+    # C4 sample: expert copies host -> host (one thread)
+    src = [np.concatenate([expert(e)[0].reshape(-1), expert(e)[1].reshape(-1)]) for e in range(n3)]
+    dst = [np.empty_like(a) for a in src]
+    copied, t_copy = 0, 0.0
     t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s or tokens < 3:
-        x = normal_bf16(rng, (1, H), 1.0)
+    while time.perf_counter() - t_start < 2.0 or copied == 0:
         t0 = time.perf_counter()
-        ids, _, wb = orouter.softmax_topk(orouter.gate_logits(x, wg), K)
-        t_route = time.perf_counter() - t0
-        for e in ids[0]:
-            if int(e) not in experts:
-                experts[int(e)] = (normal_bf16(rng, (2 * I, H), 0.02), normal_bf16(rng, (H, I), 0.02))
-        w13 = np.stack([experts[int(e)][0] for e in ids[0]])
-        w2 = np.stack([experts[int(e)][1] for e in ids[0]])
-        t1 = time.perf_counter()
-        omlp.moe_layer(x, np.arange(K, dtype=np.int32)[None, :], wb, None, w13, w2)
-        t_total += t_route + (time.perf_counter() - t1)
-        tokens += 1
+        for a, b in zip(src, dst):
+            np.copyto(b, a)
+        t_copy += time.perf_counter() - t0
+        copied += sum(a.nbytes for a in src)
+
     cores = int(os.environ.get("OMP_NUM_THREADS") or (os.cpu_count() or 1))
-    return {"value": round(t_total / tokens * 1e6, 1), "unit": "us/token/layer (decode B=1)",
-            "cores": cores, "kind": "port",
-            "sample": f"{tokens} single-token decode passes of one Qwen3-shaped MoE layer through the numpy "
-                      f"oracle (gate, softmax top-8, 8 f32-accumulated SwiGLU experts, combine), "
-                      f"{budget_s:.0f} s budget; BLAS threads up to {cores}"}
+    return {"value": decode["B1"]["us_per_token_per_layer"], "unit": "us/token/layer (decode B=1)",
+            "cores": cores, "kind": "port", "cpu_model": _cpu_model(),
+            "sample": f"numpy oracle: decode B=1/4/16/64 of one Qwen3-shaped MoE layer (gate, softmax top-8, "
+                      f"routed f32-accumulated SwiGLU experts, combine; B=1 for {budget_s:.0f} s); prefill: "
+                      f"{pairs3} pairs of a 4096-token routing on {n3} of the 128 experts; staging: "
+                      f"{n3} expert copies host->host, one thread; BLAS threads up to {cores}",
+            "decode": decode,
+            "prefill_gflops": round(prefill_gflops, 1), "prefill_sample_pairs": pairs3,
+            "prefill_sample_s": round(t3, 2),
+            "host_copy_gbs": round(copied / t_copy / 1e9, 2), "host_copy_threads": 1}
 
 
 # ---------------------------------------------------------------------------
