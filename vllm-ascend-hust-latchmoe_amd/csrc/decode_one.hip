@@ -17,8 +17,9 @@
 // that precedes this launch), so a word of an earlier launch is never
 // taken.  Producer progress goes up a two-level counter tree in meta (16
 // first-level counters per rank, then one per rank; the build zeroed them),
-// which only tells a consumer when to start reading: a word whose tag does
-// not match yet is read again.  No counter has more than a few dozen
+// which only tells a consumer when to start reading (one lane per rank
+// polls, so every rank's counter is read in one round trip): a word whose
+// tag does not match yet is read again.  No counter has more than a few dozen
 // increments (contended agent-scope atomics are slow), and nothing is left
 // to reset.  Every wait is bounded: past kSpinLimit polls
 // meta[LMOE_META_DECODE_TIMEOUT] becomes 1 and the wave goes on, so no wave
@@ -149,18 +150,20 @@ __global__ __launch_bounds__(256) void decode_one_kernel(DecodeOneArgs a) {
     s_w[tid] = tid < a.k ? bf16_to_f32(a.wts[tid]) : 0.0f;
   }
   const float addv = (a.add != nullptr && tid < R && h0 + tid < a.H) ? bf16_to_f32(a.add[h0 + tid]) : 0.0f;
-  // start reading once the producers of every rank are done (a hint only)
-  if (tid == 0) {
+  // start reading once the producers of every rank are done (a hint only):
+  // lane r of wave 0 polls rank r's counter, all ranks in one round trip
+  if (wave == 0) {
     const int fans = a.gu_per_slot < kFan ? a.gu_per_slot : kFan;
+    bool done = lane >= a.ranks;
     long long n = 0;
-    for (int r = 0; r < a.ranks; ++r) {
-      while (ld_agent(a.meta + kLevel2 + r) < fans) {
-        if (++n >= kSpinLimit) {
-          give_up(a.meta);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(2);
+    while (true) {
+      if (!done) done = ld_agent(a.meta + kLevel2 + lane) >= fans;
+      if (__ballot(!done) == 0ull) break;
+      if (++n >= kSpinLimit) {
+        if (lane == 0) give_up(a.meta);
+        break;
       }
+      __builtin_amdgcn_s_sleep(2);
     }
   }
   __syncthreads();
@@ -168,8 +171,14 @@ __global__ __launch_bounds__(256) void decode_one_kernel(DecodeOneArgs a) {
     float v[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) v[r] = 0.0f;
-    // every word of the lane's act columns in flight at once, then the tags
-    // checked; words not yet of this launch are read again
+    // every word of the lane's act columns in flight at once, as ordinary
+    // 16-byte loads through this XCD's L2 (the launch began with the L2
+    // invalidated, so a line holds either a word of this launch or, if it
+    // was filled before the producer's write-through landed, an older one),
+    // then the tags checked; words not yet of this launch are read again
+    // past the L2 (agent-scope loads).  Through the L2, the 512 consumers'
+    // reads of the same 8 x I words reach memory once per XCD instead of
+    // once per consumer.
     const uint32_t* row = a.words + static_cast<size_t>(s >= 0 ? hw : 0) * a.I;
     uint32_t wv[DNC][8];
     bool ok[DNC];
@@ -177,9 +186,10 @@ __global__ __launch_bounds__(256) void decode_one_kernel(DecodeOneArgs a) {
     for (int c = 0; c < DNC; ++c) {
       const int col = c * 256 + l5 * 8;
       ok[c] = s >= 0 && col < a.I;
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        wv[c][j] = __hip_atomic_load(row + (ok[c] ? col + j : 0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint4* q = reinterpret_cast<const uint4*>(row + (ok[c] ? col : 0));
+      const uint4 lo = q[0], hi = q[1];
+      wv[c][0] = lo.x; wv[c][1] = lo.y; wv[c][2] = lo.z; wv[c][3] = lo.w;
+      wv[c][4] = hi.x; wv[c][5] = hi.y; wv[c][6] = hi.z; wv[c][7] = hi.w;
     }
     long long n = 0;
     while (true) {

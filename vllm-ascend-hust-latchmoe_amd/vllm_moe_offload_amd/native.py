@@ -761,10 +761,12 @@ def fused_moe_decode(
 
 def decode_one_supported(H: int, I: int, k: int) -> bool:
     """lmoe_decode_one is switched on (LATCHMOE_DECODE_ONE=1; off by
-    default: on the Qwen3-shaped layer it measured 39.7 us per layer in the
-    48-layer decode graph against 23.4 us for the two-kernel body, its
-    consumers holding W2 in registers halve the producers' occupancy) and
-    takes the shape (the others run the two-kernel body)."""
+    default: on the Qwen3-shaped layer it measured 30.8 us per layer in the
+    48-layer decode graph against 23.8 us for the two-kernel body: its
+    108 registers per lane halve gate_up's occupancy, and the consumers,
+    dispatched after every producer, start their W2 stream only as the
+    producers retire) and takes the shape (the others run the two-kernel
+    body)."""
     if os.environ.get("LATCHMOE_DECODE_ONE", "0") != "1":
         return False
     return k <= 8 and H % 8 == 0 and I % 64 == 0 and (H + 511) // 512 <= 8 and (I + 255) // 256 <= 4
