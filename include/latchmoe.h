@@ -77,9 +77,13 @@ enum {
   LMOE_META_TILES = 3,   /* sum over slots of ceil(count / block_m)         */
   LMOE_META_GEN = 4,     /* builds of this permutation so far (+1 per build) */
   LMOE_META_DECODE_TIMEOUT = 5,  /* lmoe_decode_one: 1 if a wait gave up     */
-  LMOE_META_DECODE_HINT = 6,     /* lmoe_decode_one: 136 hand-off counters,
-                                    zeroed by every build                    */
-  LMOE_META_COUNT = 144
+  LMOE_META_DECODE_HINT = 64,    /* lmoe_decode_one: hand-off counter c at
+                                    HINT + c * STRIDE (256 bytes apart, so
+                                    their atomics spread over the memory
+                                    channels), zeroed by every build          */
+  LMOE_META_DECODE_STRIDE = 64,
+  LMOE_META_DECODE_COUNTERS = 137,
+  LMOE_META_COUNT = 64 + 137 * 64 /* 8832 int32 words */
 };
 
 const char* lmoe_status_string(int status);
@@ -178,7 +182,8 @@ size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);
  * slot with count > 0 (ascending), -1 for a >= meta[LMOE_META_ACTIVE];
  * tile_off[s] = sum over s' < s of
  * ceil(counts[s'] / block_m); meta[LMOE_META_COUNT] (ACTIVE, PAIRS, ERRORS,
- * TILES; GEN advanced and the lmoe_decode_one counters zeroed).
+ * TILES; GEN advanced, the lmoe_decode_one timeout flag and counters
+ * zeroed; the other words are not written).
  * Replaces slot_mapping.py:116-140 + npu_moe_init_routing_v2
  * (patch_fused_moe.py:668-701: expert_capacity=-1, drop_pad_mode=0,
  * expert_tokens_num_type=1). */
@@ -367,8 +372,9 @@ int lmoe_table_update(int32_t* table, int n_table, const int32_t* idx,
  * rows in flight while the producers run.  act values pass between
  * workgroups as tagged 32-bit words (bf16 | (meta[LMOE_META_GEN] & 0xffff)
  * << 16, words [k, I] u32, zero before the first call) through agent-scope
- * atomic accesses, and the producers' progress through the counters in
- * meta[LMOE_META_DECODE_HINT..]; the permutation build (lmoe_permute,
+ * atomic accesses, and the producers' progress through the counters at
+ * meta[LMOE_META_DECODE_HINT + c * LMOE_META_DECODE_STRIDE]; the
+ * permutation build (lmoe_permute,
  * lmoe_router_*_permute) that precedes the call advances the generation
  * and zeroes the counters, so AT MOST ONE lmoe_decode_one may run per
  * build (a second one on the same build may read the first one's act), and

@@ -15,11 +15,11 @@
 // accesses, so a reader sees a whole word or an older one; the tag is the
 // permutation's build count (meta[LMOE_META_GEN], advanced by the build
 // that precedes this launch), so a word of an earlier launch is never
-// taken.  Producer progress goes up a two-level counter tree in meta (16
-// first-level counters per rank, then one per rank; the build zeroed them),
-// which only tells a consumer when to start reading (one lane per rank
-// polls, so every rank's counter is read in one round trip): a word whose
-// tag does not match yet is read again.  No counter has more than a few dozen
+// taken.  Producer progress goes up a counter tree in meta (16 first-level
+// counters per rank, one per rank, then the number of ranks done; the
+// build zeroed them; 256 bytes apart), which only tells a consumer when to
+// start reading (one thread polls the ranks-done count): a word whose tag
+// does not match yet is read again.  No counter has more than a few dozen
 // increments (contended agent-scope atomics are slow), and nothing is left
 // to reset.  Every wait is bounded: past kSpinLimit polls
 // meta[LMOE_META_DECODE_TIMEOUT] becomes 1 and the wave goes on, so no wave
@@ -44,10 +44,17 @@ constexpr int kOneRows = 4;   // output rows per consumer workgroup
 constexpr int kFan = 16;      // first-level counters per rank
 constexpr long long kSpinLimit = 1LL << 22;
 
-// hand-off counters in meta (zeroed by the permutation build)
-constexpr int kLevel1 = LMOE_META_DECODE_HINT;        // [kOneMaxK][kFan]
-constexpr int kLevel2 = kLevel1 + kOneMaxK * kFan;    // [kOneMaxK]
-static_assert(kLevel2 + kOneMaxK <= LMOE_META_COUNT, "meta holds the hand-off counters");
+// hand-off counters in meta (zeroed by the permutation build), 256 bytes
+// apart: kept together in a few cache lines, the producers' atomics all
+// queued at one memory channel and the last of them finished ~13 us late
+constexpr int kLevel1 = 0;                        // [kOneMaxK][kFan]
+constexpr int kLevel2 = kLevel1 + kOneMaxK * kFan;  // [kOneMaxK]
+constexpr int kLevel3 = kLevel2 + kOneMaxK;         // ranks done
+static_assert(kLevel3 + 1 <= LMOE_META_DECODE_COUNTERS, "meta holds the hand-off counters");
+
+__device__ __forceinline__ int32_t* counter(int32_t* meta, int c) {
+  return meta + LMOE_META_DECODE_HINT + c * LMOE_META_DECODE_STRIDE;
+}
 
 struct DecodeOneArgs {
   const uint16_t* x;
@@ -116,10 +123,17 @@ __global__ __launch_bounds__(256) void decode_one_kernel(DecodeOneArgs a) {
       const int bx = blockIdx.x % a.gu_per_slot;
       const int f = bx % kFan;
       const int members = (a.gu_per_slot - f + kFan - 1) / kFan;
-      const int done = __hip_atomic_fetch_add(a.meta + kLevel1 + ar * kFan + f, 1, __ATOMIC_RELAXED,
+      const int done = __hip_atomic_fetch_add(counter(a.meta, kLevel1 + ar * kFan + f), 1,
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (done == members - 1) {
+        // ... and the one that completes the rank moves the ranks-done count
+        const int fans = a.gu_per_slot < kFan ? a.gu_per_slot : kFan;
+        const int d2 = __hip_atomic_fetch_add(counter(a.meta, kLevel2 + ar), 1, __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
-      if (done == members - 1)
-        __hip_atomic_fetch_add(a.meta + kLevel2 + ar, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d2 == fans - 1)
+          __hip_atomic_fetch_add(counter(a.meta, kLevel3), 1, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     return;
   }
@@ -150,17 +164,12 @@ __global__ __launch_bounds__(256) void decode_one_kernel(DecodeOneArgs a) {
     s_w[tid] = tid < a.k ? bf16_to_f32(a.wts[tid]) : 0.0f;
   }
   const float addv = (a.add != nullptr && tid < R && h0 + tid < a.H) ? bf16_to_f32(a.add[h0 + tid]) : 0.0f;
-  // start reading once the producers of every rank are done (a hint only):
-  // lane r of wave 0 polls rank r's counter, all ranks in one round trip
-  if (wave == 0) {
-    const int fans = a.gu_per_slot < kFan ? a.gu_per_slot : kFan;
-    bool done = lane >= a.ranks;
+  // start reading once the producers of every rank are done (a hint only)
+  if (tid == 0) {
     long long n = 0;
-    while (true) {
-      if (!done) done = ld_agent(a.meta + kLevel2 + lane) >= fans;
-      if (__ballot(!done) == 0ull) break;
+    while (ld_agent(counter(a.meta, kLevel3)) < a.ranks) {
       if (++n >= kSpinLimit) {
-        if (lane == 0) give_up(a.meta);
+        give_up(a.meta);
         break;
       }
       __builtin_amdgcn_s_sleep(2);

@@ -46,8 +46,11 @@ __device__ __forceinline__ void publish_build(int32_t* meta) {
   // no-return atomic: the publishing thread does not wait for the old value
   __hip_atomic_fetch_add(meta + LMOE_META_GEN, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// the one-launch decode body's timeout flag and hand-off counters
 __device__ __forceinline__ void clear_decode_handoff(int32_t* meta, int t, int n) {
-  for (int i = LMOE_META_DECODE_TIMEOUT + t; i < LMOE_META_COUNT; i += n) meta[i] = 0;
+  for (int c = t; c <= LMOE_META_DECODE_COUNTERS; c += n)
+    meta[c == 0 ? LMOE_META_DECODE_TIMEOUT
+                : LMOE_META_DECODE_HINT + (c - 1) * LMOE_META_DECODE_STRIDE] = 0;
 }
 
 __device__ __forceinline__ uint64_t match_key(int key, int nbits) {
