@@ -873,9 +873,12 @@ def bench_cpu_baseline(budget_s: float = 8.0) -> dict:
         return pool[e % len(pool)]
 
     def decode_leg(B: int, budget: float) -> tuple[float, int]:
-        t_total, steps = 0.0, 0
+        """3 untimed steps, then the median step of at least 10 (more while
+        the budget lasts), per token."""
+        times = []
         t_start = time.perf_counter()
-        while time.perf_counter() - t_start < budget or steps < 2:
+        step = 0
+        while len(times) < 10 or time.perf_counter() - t_start < budget:
             x = normal_bf16(rng, (B, H), 1.0)
             t0 = time.perf_counter()
             ids, _, wb = orouter.softmax_topk(orouter.gate_logits(x, wg), K)
@@ -887,14 +890,15 @@ def bench_cpu_baseline(budget_s: float = 8.0) -> dict:
             w2 = np.stack([expert(int(e))[1] for e in used])
             t1 = time.perf_counter()
             omlp.moe_layer(x, ids, wb, l2p, w13, w2)
-            t_total += t_route + (time.perf_counter() - t1)
-            steps += 1
-        return t_total / (steps * B) * 1e6, steps
+            if step >= 3:
+                times.append(t_route + (time.perf_counter() - t1))
+            step += 1
+        return float(np.median(times)) / B * 1e6, len(times)
 
     decode = {}
-    for B, budget in ((1, budget_s), (4, 4.0), (16, 4.0), (64, 5.0)):
+    for B, budget in ((1, budget_s), (4, 3.0), (16, 3.0), (64, 3.0)):
         us, steps = decode_leg(B, budget)
-        decode[f"B{B}"] = {"us_per_token_per_layer": round(us, 1), "steps": steps}
+        decode[f"B{B}"] = {"us_per_token_per_layer": round(us, 1), "timed_steps": steps}
 
     # C3 sample: 4096 tokens routed uniformly, the pairs of 16 experts
     T3, n3 = 4096, 16
@@ -925,7 +929,8 @@ def bench_cpu_baseline(budget_s: float = 8.0) -> dict:
     return {"value": decode["B1"]["us_per_token_per_layer"], "unit": "us/token/layer (decode B=1)",
             "cores": cores, "kind": "port", "cpu_model": _cpu_model(),
             "sample": f"numpy oracle: decode B=1/4/16/64 of one Qwen3-shaped MoE layer (gate, softmax top-8, "
-                      f"routed f32-accumulated SwiGLU experts, combine; B=1 for {budget_s:.0f} s); prefill: "
+                      f"routed f32-accumulated SwiGLU experts, combine; median step after 3 untimed, at least 10 "
+                      f"timed, B=1 for {budget_s:.0f} s); prefill: "
                       f"{pairs3} pairs of a 4096-token routing on {n3} of the 128 experts; staging: "
                       f"{n3} expert copies host->host, one thread; BLAS threads up to {cores}",
             "decode": decode,
