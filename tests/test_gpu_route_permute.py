@@ -274,3 +274,64 @@ def test_shared_suffix_in_all_three_routers(T, E, k, S, scoring, H):
         torch.cuda.synchronize()
         check(w, ids, wf)
         _check_perm(native, perm, ref, T * (k + S))
+
+
+@pytest.mark.parametrize("E,k,P,H,tie_rows", [
+    (128, 8, 64, 2048, 6),   # the Qwen3-shaped decode router, six experts tied with a seventh
+    (256, 8, 128, 1024, 9),  # four experts per lane
+    (60, 4, 16, 512, 5),     # E not a multiple of 64: lanes past E hold no expert
+    (16, 2, 8, 512, 0),
+])
+def test_one_token_one_launch_router_with_ties_equals_separate_calls_and_oracle(E, k, P, H, tie_rows):
+    """The one-token one-launch router (gate, selection and permutation in
+    one kernel, the decode replay's router) against the separate calls and
+    the oracle, bit for bit, ties included: tie_rows gate rows are copies of
+    one row, so their logits are equal and the lower ids must be taken
+    first; every other step steers the token onto the tied rows."""
+    native = _native()
+    print(f"case one-token-router-ties E={E} k={k} P={P} H={H} ties={tie_rows}", flush=True)
+    rng = np.random.default_rng(900 + E + tie_rows)
+    wg_h = normal_bf16(rng, (E, H), 0.02)
+    if tie_rows:
+        src = int(rng.integers(E))
+        for r in rng.permutation(E)[:tie_rows]:
+            wg_h[r] = wg_h[src]
+    wg = to_dev_bf16(wg_h)
+    perm_a = native.Permutation.allocate(k, P, "cuda")
+    perm_b = native.Permutation.allocate(k, P, "cuda")
+    for it in range(4):
+        x_h = normal_bf16(rng, (1, H), 1.0)
+        x = to_dev_bf16(x_h)
+        if tie_rows and it % 2 == 1:
+            # steer the tied experts to the top: x along their shared row
+            x_h = f32_to_bf16(bf16_to_f32(wg_h[src])[None, :] * np.float32(40.0))
+            x = to_dev_bf16(x_h)
+        lg0 = torch.empty((1, E), dtype=torch.bfloat16, device="cuda")
+        native.router_gate(x, wg, lg0)
+        _, ids0, _ = native.router_topk(lg0, k)
+        used = np.unique(ids0.cpu().numpy())
+        l2p = np.full(E, -1, dtype=np.int32)
+        l2p[used] = rng.permutation(P)[: used.size]
+        d_l2p = to_dev_i32(l2p)
+        lg_a = torch.empty((1, E), dtype=torch.bfloat16, device="cuda")
+        native.router_gate(x, wg, lg_a)
+        wa, ida, wfa = native.router_topk_permute(lg_a, k, perm_a, log2phy=d_l2p,
+                                                  w_f32=torch.empty((1, k), device="cuda"))
+        lg_b = torch.empty((1, E), dtype=torch.bfloat16, device="cuda")
+        wb, idb, wfb = native.router_gate_topk_permute(x, wg, lg_b, k, perm_b, log2phy=d_l2p,
+                                                       w_f32=torch.empty((1, k), device="cuda"))
+        torch.cuda.synchronize()
+        assert torch.equal(lg_a.view(torch.int16), lg_b.view(torch.int16)), it
+        assert torch.equal(ida, idb), it
+        assert torch.equal(wa.view(torch.int16), wb.view(torch.int16)), it
+        assert torch.equal(wfa.view(torch.int32), wfb.view(torch.int32)), it
+        for name in ("counts", "offsets", "sorted_pairs", "row_idx", "active", "tile_off"):
+            assert torch.equal(getattr(perm_a, name), getattr(perm_b, name)), (it, name)
+        lg = bf16_to_f32(from_dev_bf16(lg_b))
+        r_ids, _, r_wb = orc.softmax_topk(lg, k)
+        assert np.array_equal(idb.cpu().numpy(), r_ids), it
+        assert np.array_equal(wb.view(torch.int16).cpu().numpy().view(np.uint16), r_wb), it
+        if tie_rows and it % 2 == 1:
+            # the steered step really selects tied experts
+            vals = lg[0, r_ids[0]]
+            assert np.unique(vals).size < k, "no tie among the selected experts"
