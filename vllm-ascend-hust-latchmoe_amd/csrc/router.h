@@ -175,10 +175,11 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
                                       sorted_pairs, row_idx, active, tile_off, meta, hist, L);
 }
 
-// Gate, selection and permutation in one launch.  Block b's waves compute
-// the logits of experts b * nw + wave for all T tokens and store them; the
-// block then counts itself in with a release fence and an atomic add on
-// *sync.  The last block to arrive (the add returns gridDim.x - 1) takes an
+// Gate, selection and permutation in one launch.  Block (b, g)'s waves
+// compute the logits of experts b * nw + wave for the tokens of group g
+// (kGateTok tokens per group, gridDim.y groups) and store them; the block
+// then counts itself in with a release fence and an atomic add on *sync.
+// The last block to arrive (the add returns the grid size - 1) takes an
 // acquire fence, resets *sync to 0 for the next launch, and runs the
 // selection and the permutation over everything the others stored.  No block
 // ever waits for another: the last one only starts once all have finished
@@ -205,12 +206,14 @@ __global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
   const bool l2p_in_lds = log2phy != nullptr && n_log2phy <= kMaxE;
   if (l2p_in_lds)
     for (int i = threadIdx.x; i < n_log2phy; i += blockDim.x) l2p_lds[i] = log2phy[i];
-  if (e < sp.E) gate_row<NC, ONE>(x, wg, 0, T, H, sp.E, e, logits, logits_f32);
+  const int t0 = ONE ? 0 : static_cast<int>(blockIdx.y) * kGateTok;
+  const int t1 = ONE ? T : min(T, t0 + kGateTok);
+  if (e < sp.E && t0 < t1) gate_row<NC, ONE>(x, wg, t0, t1, H, sp.E, e, logits, logits_f32);
   __syncthreads();  // every wave's logits are stored before thread 0 counts the block in
   if (threadIdx.x == 0) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     const int prev = __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = prev == static_cast<int>(gridDim.x) - 1;
+    last = prev == static_cast<int>(gridDim.x * gridDim.y) - 1;
     if (last) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -342,11 +345,14 @@ int launch_gate_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
   router_launch_shape(a, true, &threads, &lds);
   const int nw = threads / 64;
   const int blocks = (a.sp.E + nw - 1) / nw;
+  // several tokens: one block row per kGateTok tokens, so no wave walks
+  // the token groups in turn
+  const int tgroups = a.T == 1 ? 1 : (a.T + kGateTok - 1) / kGateTok;
   const int ppl = router_perm_ppl(a.T * (a.sp.k + a.sp.n_shared), a.n_slots);
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const uint16_t* wg = static_cast<const uint16_t*>(a.wg);
 #define LMOE_GTP(NC, EPL, Q, ONE)                                                                 \
-  hipLaunchKernelGGL((gate_topk_permute_kernel<NC, EPL, Q, SCORE, ONE>), dim3(blocks),          \
+  hipLaunchKernelGGL((gate_topk_permute_kernel<NC, EPL, Q, SCORE, ONE>), dim3(blocks, tgroups), \
                      dim3(threads), lds, stream, x, wg, a.T, a.H, a.logits, a.logits_f32, a.sp, \
                      a.w_f32, a.w_bf16, a.ids, a.log2phy, a.n_log2phy, a.n_slots, a.skip,       \
                      a.block_m, a.counts, a.offsets, a.sorted_pairs, a.row_idx, a.active,       \

@@ -222,9 +222,9 @@ def _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2p
 # Up to this many tokens the decode router runs as one launch (gate,
 # selection, permutation); with more, the separate gate launch and the
 # selection + permutation launch are faster.  Measured in the 48-layer decode
-# graph: one token 23.6 against 23.8 us per layer, four tokens 43.8 against
-# 43.6 us; router-only loops give the two launches 0.1 us at 2 and 3 tokens
-# and 7.4 us at 16.
+# graph: one token 23.6 against 23.8 us per layer; with the one launch's gate
+# split over token groups, four tokens 43.5 against 43.3 us and sixteen 81.7
+# against 80.5 us per layer.
 ONE_LAUNCH_ROUTER_MAX_TOKENS = 1
 
 
