@@ -39,7 +39,10 @@ Load = tuple[ExpertWeightBundle, ExpertSlot]
 
 @dataclass
 class TransferReadyEvent:
-    """Transfer-stream event plus the slots it makes consumable."""
+    """One copy batch in flight: the event recorded after its copies on the
+    transfer stream, and the (slot, lease) pairs it fills.  Completing it
+    (a consumer stream's wait, or the host's) checks that every slot still
+    holds the lease it was issued for and moves the slots to READY."""
 
     event: object | None
     leases: tuple[tuple[ExpertSlot, SlotLease], ...]
