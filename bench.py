@@ -15,7 +15,8 @@ after the step's eager staging has made every routed expert resident.  Also repo
               rotating through the 48 layers
   prefill     4096 tokens, 48 slots, uniform router: capacity waves with one
               combine (compute TFLOP/s and MFMA fraction; staged wall time;
-              H2D GB/s), against the blocking full layer
+              H2D GB/s), against the blocking full layer; torch.bmm
+              (hipBLASLt) on the same per-slot shapes as a reference point
   staging     forced k misses per layer per step (k in 1, 4, 8): H2D GB/s on
               the transfer stream and the fraction of compute overlapped,
               with per-layer graph replays and stable slot addresses
@@ -85,6 +86,18 @@ class Timer:
     def ms(self) -> float:
         self.b.synchronize()
         return float(self.a.elapsed_time(self.b))
+
+
+def time_queued(fn, reps: int) -> float:
+    """Mean ms per call of fn over reps calls (HIP events on the current
+    stream).  One untimed call is queued first, so the device is busy while
+    the host issues the timed calls: the first timed call does not wait for
+    the host."""
+    fn()
+    with Timer() as t:
+        for _ in range(reps):
+            fn()
+    return t.ms() / reps
 
 
 # ---------------------------------------------------------------------------
@@ -556,10 +569,7 @@ def bench_prefill(host_w13, host_w2, T: int = 4096, slots: int = 48, reps: int =
         fn()
     torch.cuda.synchronize()
     for name, fn in (("waves_compute", waves_compute), ("full_layer_compute", full_compute), ("grouped_gemm_only", gemm_only)):
-        with Timer() as t:
-            for _ in range(reps):
-                fn()
-        ms = t.ms() / reps
+        ms = time_queued(fn, reps)
         tf = flops / (ms * 1e-3) / 1e12
         res[f"{name}_ms"] = round(ms, 3)
         res[f"{name}_tflops"] = round(tf, 1)
@@ -568,17 +578,58 @@ def bench_prefill(host_w13, host_w2, T: int = 4096, slots: int = 48, reps: int =
     per_wave = []
     for (w13, w2, l2p), pw, bm in zip(wave_banks, perms_w, wave_bm):
         native.permute(ids, pw, log2phy=l2p, skip_unmapped=True, block_m=bm)
-        with Timer() as t:
-            for _ in range(reps):
-                native.grouped_mlp(x, K, w13, w2, pw, act, y, path=native.LMOE_PATH_MFMA)
-        per_wave.append(round(t.ms() / reps, 3))
+        ms = time_queued(lambda: native.grouped_mlp(x, K, w13, w2, pw, act, y, path=native.LMOE_PATH_MFMA), reps)
+        per_wave.append(round(ms, 3))
     res["wave_block_m"] = wave_bm
     res["wave_gemm_ms"] = per_wave
     res["wave_max_pairs_per_slot"] = [int(pw.counts.max().item()) for pw in perms_w]
     torch.cuda.synchronize()
     same = torch.equal(out.view(torch.int16), ws_full.out[:T].view(torch.int16))
     res["waves_equal_full_layer_bitwise"] = bool(same)
+
+    # the full layer's two grouped GEMMs alone (all 128 slots resident)
+    bm_full = native.prefill_block_m(E, H, I, dev, n_pairs=pairs)
+    perm_full = native.Permutation.allocate(pairs, E, dev)
+    native.permute(ids, perm_full, log2phy=full.log2phy, block_m=bm_full)
+    ms = time_queued(lambda: native.grouped_mlp(x, K, full.w1, full.w2, perm_full, act, y,
+                                                path=native.LMOE_PATH_MFMA), reps)
+    res["full_gemm_only_ms"] = round(ms, 3)
+    res["full_gemm_only_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+    del perm_full
+    res["library_bmm"] = bench_library_bmm((E, len(rep.waves[0])), M=pairs // E, reps=reps)
     return res
+
+
+def bench_library_bmm(slot_counts, M: int, reps: int = 5) -> dict:
+    """The vendor library on the same per-slot shapes, as a reference point
+    for the grouped GEMMs: torch.bmm (hipBLASLt) over S slots of a uniform
+    M rows each, gate-up [S, M, H] x [S, H, 2I] and down [S, M, I] x [S, I, H],
+    contiguous operands.  It does less than the grouped kernels (no row
+    gather, no SiLU*mul, no ragged slots, no padding), so its time is a floor
+    for what a library GEMM call per pass would take, not a parity check."""
+    import torch
+
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    out = {}
+    for S in slot_counts:
+        r = {}
+        total_us = 0.0
+        for name, k_dim, n_dim in (("gate_up", H, 2 * I), ("down", I, H)):
+            a = torch.randn((S, M, k_dim), generator=g, device=dev).to(torch.bfloat16)
+            b = (torch.randn((S, k_dim, n_dim), generator=g, device=dev) * 0.02).to(torch.bfloat16).contiguous()
+            c = torch.bmm(a, b)
+            us = time_queued(lambda: torch.bmm(a, b, out=c), reps) * 1000.0
+            total_us += us
+            r[f"{name}_us"] = round(us, 1)
+            r[f"{name}_tflops"] = round(2.0 * S * M * k_dim * n_dim / (us * 1e-6) / 1e12, 1)
+            del a, b, c
+        r["both_us"] = round(total_us, 1)
+        r["both_tflops"] = round(2.0 * S * M * 3 * H * I / (total_us * 1e-6) / 1e12, 1)
+        out[f"S{S}_M{M}"] = r
+    torch.cuda.empty_cache()
+    return out
 
 
 # ---------------------------------------------------------------------------

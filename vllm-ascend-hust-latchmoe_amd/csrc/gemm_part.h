@@ -28,7 +28,7 @@
 // waits for its own count.  Rows past the tile's valid rows and weight rows
 // of columns outside the sub-tile load a valid row whose result is dropped,
 // so the count per stage is fixed; waves without live columns skip their
-// MFMAs.  Every output
+// MFMAs, and a wave computes only its live 32-row blocks.  Every output
 // element accumulates its K/16 MFMA steps in increasing k, the order of the
 // other grouped kernels, so all of them give identical bits.
 //
@@ -257,8 +257,13 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_part_kernel(GemmArgs 
         buf = (buf + 1 == C::STAGES) ? 0 : buf + 1;
       }
     };
-    // NL: 32-row blocks computed (a partial tile rounds up to 1, 2 or NI)
-    if (ni_live > 2) main_loop(std::integral_constant<int, C::NI>{});
+    // NL: 32-row blocks computed, exactly the live ones: a slot of ~256
+    // pairs leaves the second wave row 3 of its 5 blocks, and MFMAs on
+    // padding rows cost time (6% of the full-layer gate-up, same box)
+    static_assert(C::NI >= 4 && C::NI <= 5, "live-block variants 1-4 and NI");
+    if (ni_live > 4) main_loop(std::integral_constant<int, C::NI>{});
+    else if (ni_live == 4) main_loop(std::integral_constant<int, 4>{});
+    else if (ni_live == 3) main_loop(std::integral_constant<int, 3>{});
     else if (ni_live == 2) main_loop(std::integral_constant<int, 2>{});
     else if (ni_live == 1) main_loop(std::integral_constant<int, 1>{});
     else main_loop(std::integral_constant<int, 0>{});
