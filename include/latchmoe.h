@@ -12,6 +12,12 @@
  * given stream and are legal inside hipStreamBeginCapture/EndCapture (no
  * allocation, no host synchronisation, no memset node).
  *
+ * An empty batch (T == 0 tokens, or n_pairs == 0) is legal everywhere: the
+ * call checks its sizes, then returns 0 without reading its token-sized
+ * operands, which may be null (an empty device tensor has no address).  The
+ * entry points that build a permutation still write it, empty (zero counts,
+ * no active slot), so a caller never reads the previous batch's.
+ *
  * Tensor conventions (row-major, element types in brackets):
  *   x         [T, H]        bf16   hidden states (T tokens)
  *   logits    [T, E]        bf16 or f32

@@ -60,6 +60,36 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert lib.lmoe_table_update(None, 8, None, None, 0, None) == 0
 
 
+def test_empty_batch_is_legal_with_null_operands():
+    """T == 0 (or n_pairs == 0): the sizes are still checked, then the call
+    returns 0 without touching its token-sized operands, which are null for
+    an empty device tensor.  These entries queue nothing for an empty batch,
+    so no GPU is needed; the permutation-building ones are covered on the GPU."""
+    from vllm_moe_offload_amd import native
+
+    lib = native.load_library()
+    N = None
+    H, E, I, k, P = 2048, 128, 768, 8, 64
+    assert lib.lmoe_router_gate(N, N, 0, H, E, N, 0, N) == 0
+    assert lib.lmoe_router_gate(N, N, -1, H, E, N, 0, N) == 1000
+    assert lib.lmoe_router_gate(N, N, 0, H + 4, E, N, 0, N) == 1001
+    assert lib.lmoe_router_topk(N, 0, 0, E, k, 0, 0, N, N, 1, 1, 1, 1.0, N, N, N, N) == 0
+    assert lib.lmoe_router_topk(N, 0, 0, E, E + 1, 0, 0, N, N, 1, 1, 1, 1.0, N, N, N, N) == 1001
+    assert lib.lmoe_gateup_silu(N, 0, H, I, k, N, P, N, N, N, N, N, 0, 320, 0, N, N) == 0
+    assert lib.lmoe_down(N, H, I, N, P, N, N, N, N, N, 0, 320, 0, N, N) == 0
+    assert lib.lmoe_grouped_mlp(N, 0, H, I, k, N, N, P, N, N, N, N, N, 0, 320, 0, N, N, N) == 0
+    assert lib.lmoe_grouped_mlp(N, 0, H, 100, k, N, N, P, N, N, N, N, N, 0, 320, 0, N, N, N) == 1001
+    assert lib.lmoe_fused_moe_decode(N, 0, H, I, k, N, N, P, *([N] * 10), 0, N) == 0
+    assert lib.lmoe_fused_moe_decode_noalloc(N, 0, H, I, k, N, N, P, *([N] * 8), 0, N) == 0
+    assert lib.lmoe_down_combine(N, 0, H, I, k, N, P, *([N] * 8)) == 0
+    assert lib.lmoe_combine(N, N, N, 0, k, H, N, N, N) == 0
+    assert lib.lmoe_combine(N, N, N, 0, k, H - 4, N, N, N) == 1001
+    assert lib.lmoe_gather_rows(N, H, k, N, N, 0, N, N) == 0
+    # a non-empty batch still needs its operands
+    assert lib.lmoe_combine(N, N, N, 1, k, H, N, N, N) == 1000
+    assert lib.lmoe_router_gate(N, N, 1, H, E, N, 0, N) == 1000
+
+
 def test_block_range_gemm_refuses_operands_past_32_bit_offsets():
     """The 320-row block-range prefill kernel forms activation offsets in 32
     bits; an activation operand of 2^31 elements or more is refused on the

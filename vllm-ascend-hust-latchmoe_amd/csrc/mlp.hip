@@ -619,12 +619,12 @@ extern "C" int lmoe_gateup_silu(const void* x, int T, int H, int I, int k,
                                 const int32_t* active, const int32_t* tile_off,
                                 const int32_t* meta, int n_pairs, int block_m,
                                 int path, void* act, hipStream_t stream) {
+  int st = check_mlp_args(T, H, I, k, n_slots, n_pairs);
+  if (st != LMOE_OK) return st;
+  if (n_pairs == 0) return LMOE_OK;  // an empty batch: nothing read or written
   if (x == nullptr || w13_slots == nullptr || offsets == nullptr || sorted_pairs == nullptr ||
       active == nullptr || meta == nullptr || act == nullptr)
     return LMOE_ERR_ARG;
-  int st = check_mlp_args(T, H, I, k, n_slots, n_pairs);
-  if (st != LMOE_OK) return st;
-  if (n_pairs == 0) return LMOE_OK;
   path = resolve_path(path, n_pairs);
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
   if (path == LMOE_PATH_GEMV) {
@@ -663,12 +663,12 @@ extern "C" int lmoe_down(const void* act, int H, int I, const void* w2_slots, in
                          const int32_t* active, const int32_t* tile_off,
                          const int32_t* meta, int n_pairs, int block_m, int path,
                          void* y, hipStream_t stream) {
+  int st = check_mlp_args(1, H, I, 1, n_slots, n_pairs);
+  if (st != LMOE_OK) return st;
+  if (n_pairs == 0) return LMOE_OK;  // an empty batch: nothing read or written
   if (act == nullptr || w2_slots == nullptr || offsets == nullptr || sorted_pairs == nullptr ||
       active == nullptr || meta == nullptr || y == nullptr)
     return LMOE_ERR_ARG;
-  int st = check_mlp_args(1, H, I, 1, n_slots, n_pairs);
-  if (st != LMOE_OK) return st;
-  if (n_pairs == 0) return LMOE_OK;
   path = resolve_path(path, n_pairs);
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
   const uint16_t* actb = static_cast<const uint16_t*>(act);
@@ -709,8 +709,11 @@ extern "C" int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
                                 const int32_t* meta, int n_pairs, int block_m,
                                 int path, void* act, void* y,
                                 hipStream_t stream) {
+  int st = check_mlp_args(T, H, I, k, n_slots, n_pairs);
+  if (st != LMOE_OK) return st;
+  if (n_pairs == 0) return LMOE_OK;
   if (w2_slots == nullptr || y == nullptr) return LMOE_ERR_ARG;
-  int st = lmoe_gateup_silu(x, T, H, I, k, w13_slots, n_slots, offsets, sorted_pairs, active,
+  st = lmoe_gateup_silu(x, T, H, I, k, w13_slots, n_slots, offsets, sorted_pairs, active,
                             tile_off, meta, n_pairs, block_m, path, act, stream);
   if (st != LMOE_OK) return st;
   return lmoe_down(act, H, I, w2_slots, n_slots, offsets, sorted_pairs, active, tile_off, meta,
@@ -724,15 +727,15 @@ static int down_combine_impl(const void* act, int T, int H, int I, int k,
                              const int32_t* offsets, const int32_t* row_idx,
                              const int32_t* active, const int32_t* meta,
                              const void* add, void* out, bool one, hipStream_t stream) {
-  if (act == nullptr || w2_slots == nullptr || w == nullptr || offsets == nullptr ||
-      row_idx == nullptr || active == nullptr || meta == nullptr || out == nullptr)
-    return LMOE_ERR_ARG;
   if (T < 0 || H <= 0 || I <= 0 || k <= 0 || n_slots <= 0) return LMOE_ERR_ARG;
   if (H % 8 != 0 || I % 64 != 0 || I > 4096 || H > 8192) return LMOE_ERR_SHAPE;
   if (T * k > kFusedMaxPairs) return LMOE_ERR_SHAPE;
+  if (T == 0) return LMOE_OK;  // an empty batch: nothing read or written
+  if (act == nullptr || w2_slots == nullptr || w == nullptr || offsets == nullptr ||
+      row_idx == nullptr || active == nullptr || meta == nullptr || out == nullptr)
+    return LMOE_ERR_ARG;
   if ((reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(w2_slots)) & 15u)
     return LMOE_ERR_SHAPE;
-  if (T == 0) return LMOE_OK;
   const int dnc = (I + 255) / 256;
 #define LMOE_DC(DNC, R, PF)                                                                    \
   do {                                                                                         \
@@ -786,19 +789,19 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                                      const int32_t* active, const int32_t* meta,
                                      const void* add, void* act, void* y, void* out,
                                      int distinct_slots, hipStream_t stream) {
-  if (x == nullptr || w13_slots == nullptr || w2_slots == nullptr || w == nullptr ||
-      offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
-      active == nullptr || meta == nullptr || act == nullptr || out == nullptr)
-    return LMOE_ERR_ARG;
   if (T < 0 || H <= 0 || I <= 0 || k <= 0 || n_slots <= 0) return LMOE_ERR_ARG;
   if (H % 8 != 0 || I % 64 != 0 || I > 4096 || H > 8192) return LMOE_ERR_SHAPE;
   const int n_pairs = T * k;
   if (n_pairs > kFusedMaxPairs) return LMOE_ERR_SHAPE;
+  if (T == 0) return LMOE_OK;  // an empty batch: nothing read or written
+  if (x == nullptr || w13_slots == nullptr || w2_slots == nullptr || w == nullptr ||
+      offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
+      active == nullptr || meta == nullptr || act == nullptr || out == nullptr)
+    return LMOE_ERR_ARG;
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w13_slots) |
        reinterpret_cast<uintptr_t>(w2_slots) | reinterpret_cast<uintptr_t>(act) |
        reinterpret_cast<uintptr_t>(y)) & 15u)
     return LMOE_ERR_SHAPE;
-  if (T == 0) return LMOE_OK;
   const int max_active = n_pairs < n_slots ? n_pairs : n_slots;
   const bool one = T == 1 && distinct_slots != 0;
   int st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
@@ -827,10 +830,10 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
 extern "C" int lmoe_combine(const void* y, const int32_t* row_idx,
                             const uint16_t* w, int T, int k, int H,
                             const void* add, void* out, hipStream_t stream) {
-  if (y == nullptr || w == nullptr || out == nullptr) return LMOE_ERR_ARG;
   if (T < 0 || k <= 0 || H <= 0) return LMOE_ERR_ARG;
   if (H % 8 != 0) return LMOE_ERR_SHAPE;
-  if (T == 0) return LMOE_OK;
+  if (T == 0) return LMOE_OK;  // an empty batch: nothing read or written
+  if (y == nullptr || w == nullptr || out == nullptr) return LMOE_ERR_ARG;
   launch_combine(static_cast<const uint16_t*>(y), row_idx, w, T, k, H,
                  static_cast<const uint16_t*>(add), static_cast<uint16_t*>(out), stream);
   LMOE_RETURN_LAUNCH();

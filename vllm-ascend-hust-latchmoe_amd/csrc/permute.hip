@@ -222,11 +222,11 @@ extern "C" int lmoe_permute(const int32_t* ids, int n_pairs,
 extern "C" int lmoe_gather_rows(const void* x, int H, int k,
                                 const int32_t* sorted_pairs, const int32_t* meta,
                                 int n_pairs, void* x_sorted, hipStream_t stream) {
-  if (x == nullptr || sorted_pairs == nullptr || meta == nullptr ||
-      x_sorted == nullptr || H <= 0 || k <= 0 || n_pairs < 0)
-    return LMOE_ERR_ARG;
+  if (H <= 0 || k <= 0 || n_pairs < 0) return LMOE_ERR_ARG;
   if (H % 8 != 0) return LMOE_ERR_SHAPE;
-  if (n_pairs == 0) return LMOE_OK;
+  if (n_pairs == 0) return LMOE_OK;  // an empty batch: nothing read or written
+  if (x == nullptr || sorted_pairs == nullptr || meta == nullptr || x_sorted == nullptr)
+    return LMOE_ERR_ARG;
   hipLaunchKernelGGL(gather_rows_kernel, dim3(n_pairs), dim3(256), 0, stream,
                      static_cast<const uint16_t*>(x), H, k, sorted_pairs, meta,
                      static_cast<uint16_t*>(x_sorted));

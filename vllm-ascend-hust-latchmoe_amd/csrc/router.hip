@@ -60,10 +60,10 @@ using namespace lmoe;
 extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
                                 int E, void* logits, int logits_f32,
                                 hipStream_t stream) {
-  if (x == nullptr || wg == nullptr || logits == nullptr) return LMOE_ERR_ARG;
   if (T < 0 || H <= 0 || E <= 0) return LMOE_ERR_ARG;
   if (H % 8 != 0 || H > kGateMaxChunks * 512) return LMOE_ERR_SHAPE;
-  if (T == 0) return LMOE_OK;
+  if (T == 0) return LMOE_OK;  // an empty batch: nothing read or written
+  if (x == nullptr || wg == nullptr || logits == nullptr) return LMOE_ERR_ARG;
   if (T > 64) {
     // large token counts: one dense bf16 MFMA GEMM, logits = x . wg^T
     GemmArgs g{};
@@ -102,11 +102,11 @@ extern "C" int lmoe_router_topk(const void* logits, int logits_f32, int T,
                                 float routed_scale, float* w_f32,
                                 uint16_t* w_bf16, int32_t* ids,
                                 hipStream_t stream) {
-  if (logits == nullptr || w_bf16 == nullptr || ids == nullptr)
-    return LMOE_ERR_ARG;
   const int st = check_select(T, E, k, n_shared, scoring, n_group, topk_group);
   if (st != LMOE_OK) return st;
-  if (T == 0) return LMOE_OK;
+  if (T == 0) return LMOE_OK;  // an empty batch: nothing read or written
+  if (logits == nullptr || w_bf16 == nullptr || ids == nullptr)
+    return LMOE_ERR_ARG;
   const SelectParams sp =
       make_select(E, k, n_shared, scoring, bias, logit_bias, n_group, topk_group, renorm,
                   routed_scale);
@@ -134,17 +134,21 @@ extern "C" int lmoe_router_topk_permute(
     int32_t* ids, const int32_t* log2phy, int n_log2phy, int n_slots, int skip_unmapped,
     int block_m, int32_t* counts, int32_t* offsets, int32_t* sorted_pairs, int32_t* row_idx,
     int32_t* active, int32_t* tile_off, int32_t* meta, hipStream_t stream) {
-  if (logits == nullptr || w_bf16 == nullptr || ids == nullptr || counts == nullptr ||
-      offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
-      active == nullptr || tile_off == nullptr || meta == nullptr)
-    return LMOE_ERR_ARG;
   int st = check_select(T, E, k, n_shared, scoring, n_group, topk_group);
   if (st != LMOE_OK) return st;
   if (n_slots <= 0 || block_m <= 0) return LMOE_ERR_ARG;
   if (log2phy != nullptr && n_log2phy <= 0) return LMOE_ERR_ARG;
   // one block: a token per wave, the whole permutation in LDS
   if (T > kFusedTopkTokens || E > 256 || n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
-  if (T == 0) return LMOE_OK;
+  // an empty batch still builds its (empty) permutation
+  if (T == 0)
+    return lmoe_permute(nullptr, 0, log2phy, n_log2phy, n_slots, skip_unmapped, block_m, counts,
+                        offsets, sorted_pairs, row_idx, active, tile_off, meta, nullptr, 0,
+                        stream);
+  if (logits == nullptr || w_bf16 == nullptr || ids == nullptr || counts == nullptr ||
+      offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
+      active == nullptr || tile_off == nullptr || meta == nullptr)
+    return LMOE_ERR_ARG;
   RouterPermuteArgs ra{};
   ra.T = T;
   ra.logits = const_cast<void*>(logits);
@@ -178,10 +182,6 @@ extern "C" int lmoe_router_gate_topk_permute(
     int n_slots, int skip_unmapped, int block_m, int32_t* counts, int32_t* offsets,
     int32_t* sorted_pairs, int32_t* row_idx, int32_t* active, int32_t* tile_off, int32_t* meta,
     int32_t* sync, hipStream_t stream) {
-  if (x == nullptr || wg == nullptr || logits == nullptr || w_bf16 == nullptr || ids == nullptr ||
-      counts == nullptr || offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
-      active == nullptr || tile_off == nullptr || meta == nullptr || sync == nullptr)
-    return LMOE_ERR_ARG;
   if (T < 0 || H <= 0) return LMOE_ERR_ARG;
   int st = check_select(T, E, k, n_shared, scoring, n_group, topk_group);
   if (st != LMOE_OK) return st;
@@ -192,7 +192,15 @@ extern "C" int lmoe_router_gate_topk_permute(
     return LMOE_ERR_SHAPE;
   // the last block holds the whole selection and permutation
   if (T > kFusedTopkTokens || E > 256 || n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
-  if (T == 0) return LMOE_OK;
+  // an empty batch still builds its (empty) permutation
+  if (T == 0)
+    return lmoe_permute(nullptr, 0, log2phy, n_log2phy, n_slots, skip_unmapped, block_m, counts,
+                        offsets, sorted_pairs, row_idx, active, tile_off, meta, nullptr, 0,
+                        stream);
+  if (x == nullptr || wg == nullptr || logits == nullptr || w_bf16 == nullptr || ids == nullptr ||
+      counts == nullptr || offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
+      active == nullptr || tile_off == nullptr || meta == nullptr || sync == nullptr)
+    return LMOE_ERR_ARG;
   RouterPermuteArgs ra{};
   ra.x = x;
   ra.wg = wg;

@@ -259,7 +259,8 @@ extern "C" long long lmoe_wave_plan_bytes(int n_routed, int n_slots, int max_wav
 
 extern "C" int lmoe_wave_plan(const int32_t* ids, int n_pairs, int n_routed, int n_total, int n_slots,
                               int max_waves, int32_t* plan, hipStream_t stream) {
-  if (ids == nullptr || plan == nullptr || n_pairs < 0) return LMOE_ERR_ARG;
+  // an empty batch (n_pairs 0, ids may be null) plans zero waves
+  if ((n_pairs > 0 && ids == nullptr) || plan == nullptr || n_pairs < 0) return LMOE_ERR_ARG;
   if (lmoe_wave_plan_bytes(n_routed, n_slots, max_waves) < 0 || n_total < n_routed)
     return LMOE_ERR_SHAPE;
   hipLaunchKernelGGL(wave_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, ids, n_pairs,
