@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define LMOE_ABI_VERSION 5
+#define LMOE_ABI_VERSION 6
 
 enum {
   LMOE_OK = 0,
@@ -83,6 +83,9 @@ enum {
   LMOE_META_TILES = 3,   /* sum over slots of ceil(count / block_m)         */
   LMOE_META_GEN = 4,     /* builds of this permutation so far (+1 per build) */
   LMOE_META_DECODE_TIMEOUT = 5,  /* lmoe_decode_one: 1 if a wait gave up     */
+  LMOE_META_ROUTER_TIMEOUT = 6,  /* lmoe_router_gate_topk_permute: 1 if the
+                                    selection gave up waiting for a logit
+                                    (sticky: the library never clears it)    */
   LMOE_META_DECODE_HINT = 64,    /* lmoe_decode_one: hand-off counter c at
                                     HINT + c * STRIDE (256 bytes apart, so
                                     their atomics spread over the memory
@@ -91,6 +94,10 @@ enum {
   LMOE_META_DECODE_COUNTERS = 137,
   LMOE_META_COUNT = 64 + 137 * 64 /* 8832 int32 words */
 };
+
+/* int32 words of the sync buffer of lmoe_router_gate_topk_permute: [0] the
+ * arrival count, from [64] the tagged logit words (u64, T x E <= 16 x 256). */
+enum { LMOE_ROUTER_SYNC_WORDS = 64 + 2 * 16 * 256 };
 
 const char* lmoe_status_string(int status);
 int lmoe_abi_version(void);
@@ -152,10 +159,16 @@ int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
  * final-table decode case as lmoe_router_topk_permute: gate(hidden)
  * (moe_router_op.py:228-231), select_experts (:108-124) and remap + init
  * routing (slot_mapping.py:116-140, patch_fused_moe.py:668-701).  The gate
- * workgroups store their logits and count themselves in on *sync; the last
- * one to arrive runs the selection and the permutation and resets *sync to 0.
- * sync is one int32, zero before the first call (it is left at zero after
- * every call); calls that may run concurrently need separate sync words.
+ * workgroups store their logits, also as tagged words in sync (the logit |
+ * the build number this launch makes, meta[LMOE_META_GEN] + 1, << 32, by
+ * agent-scope atomic stores: no cache write-back or invalidate), and count
+ * themselves in on sync[0]; the last one to arrive resets sync[0] to 0,
+ * reads the words back (again where a tag is not yet this launch's; a wait
+ * that gives up sets meta[LMOE_META_ROUTER_TIMEOUT], the result is then
+ * undefined) and runs the selection and the permutation.  sync is
+ * LMOE_ROUTER_SYNC_WORDS int32, zero before the first call; it serves one
+ * permutation (one meta), and calls that may run concurrently need separate
+ * sync buffers.
  * Returns LMOE_ERR_SHAPE when T > 16, E > 256, n_slots > 8192, H % 8 != 0,
  * H > 8192 or x / wg are not 16-byte aligned (then use the separate calls). */
 int lmoe_router_gate_topk_permute(const void* x, const void* wg, int T, int H,

@@ -267,7 +267,7 @@ def test_decode_layer_graph_replays_equal_eager(B):
         assert torch.equal(g_ids, e_ids), step
         assert torch.equal(g_w.view(torch.int16), e_w.view(torch.int16)), step
         assert torch.equal(g_out.view(torch.int16), e_out.view(torch.int16)), step
-        assert ws_g.perm.sync.item() == 0 and ws_e.perm.sync.item() == 0
+        assert ws_g.perm.sync[0].item() == 0 and ws_e.perm.sync[0].item() == 0
         ref = _oracle_layer(x, g_ids.cpu().numpy(), from_dev_bf16(g_w), w13, w2)
         assert rel_max_err(bf16_to_f32(from_dev_bf16(g_out)), ref) <= OUT_TOL
 

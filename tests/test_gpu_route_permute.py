@@ -208,7 +208,8 @@ def test_gate_select_permute_one_launch_equals_separate_calls(T, E, k, P, H, sco
         assert torch.equal(wfa.view(torch.int32), wfb.view(torch.int32)), it
         for name in ("counts", "offsets", "sorted_pairs", "row_idx", "active", "tile_off", "meta"):
             assert torch.equal(getattr(perm_a, name), getattr(perm_b, name)), (it, name)
-        assert perm_b.sync.item() == 0
+        assert perm_b.sync[0].item() == 0
+        assert perm_b.meta[native.META_ROUTER_TIMEOUT].item() == 0
 
 
 @pytest.mark.parametrize("T,E,k,S,scoring,H", [

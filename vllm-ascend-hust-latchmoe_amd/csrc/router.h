@@ -18,16 +18,44 @@ namespace lmoe {
 
 constexpr int kGateMaxChunks = 16;  // H <= 16 * 512 = 8192 in the GEMV path
 constexpr int kGateTok = 4;         // tokens per reduction in the gate GEMV
+// one-launch router: tagged logit words from int32 offset 64 of sync (256
+// bytes past the arrival counter), and the re-reads of a stale word
+constexpr int kRouterWordsOffset = 64;
+constexpr int kRouterSpinLimit = 1 << 16;
+static_assert(kRouterWordsOffset + 2 * 16 * 256 == LMOE_ROUTER_SYNC_WORDS, "sync layout");
+
+// A logit as the selection reads it (bf16 logits are rounded first).
+__device__ __forceinline__ float selected_logit(float acc, int logits_f32) {
+  return logits_f32 ? acc : bf16_to_f32(static_cast<uint16_t>(f32_to_bf16_bits(acc)));
+}
+
+// Store logit o: the logits output, and with words (the one-launch router)
+// the same value as a tagged word, (tag << 32) | f32 bits, by an
+// agent-scope atomic store that the selecting workgroup reads back.
+__device__ __forceinline__ void store_logit(void* __restrict__ logits, int logits_f32, size_t o,
+                                            float acc, uint64_t* __restrict__ words, uint32_t tag) {
+  if (logits_f32) {
+    reinterpret_cast<float*>(logits)[o] = acc;
+  } else {
+    reinterpret_cast<uint16_t*>(logits)[o] = static_cast<uint16_t>(f32_to_bf16_bits(acc));
+  }
+  if (words != nullptr) {
+    const uint64_t word = (static_cast<uint64_t>(tag) << 32) |
+                          __float_as_uint(selected_logit(acc, logits_f32));
+    __hip_atomic_store(words + o, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
 
 // logits[t][e] of one expert e for tokens [t0, t1), by the calling wave.
 // The expert row stays in registers (one 16-byte chunk per 512 columns per
 // lane) while the token rows stream through L1.  ONE: t1 == t0 + 1 (the
-// kernel holds only the single-token code).
+// kernel holds only the single-token code).  words: see store_logit.
 template <int NC, bool ONE>
 __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
                                          const uint16_t* __restrict__ wg, int t0, int t1,
                                          int H, int E, int e, void* __restrict__ logits,
-                                         int logits_f32) {
+                                         int logits_f32, uint64_t* __restrict__ words = nullptr,
+                                         uint32_t tag = 0) {
   const int lane = threadIdx.x & 63;
   const uint16_t* wrow = wg + static_cast<size_t>(e) * H;
 
@@ -49,16 +77,8 @@ __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
       acc = dot8(load16_if(xr, h, h < H), w[c], acc);
     }
     acc = wave_sum(acc);
-    if (lane == 0) {
-      const size_t o = static_cast<size_t>(t0) * E + e;
-      if (logits_f32) {
-        reinterpret_cast<float*>(logits)[o] = acc;
-      } else {
-          reinterpret_cast<uint16_t*>(logits)[o] =
-              static_cast<uint16_t>(f32_to_bf16_bits(acc));
-        }
-      }
-    } else {
+    if (lane == 0) store_logit(logits, logits_f32, static_cast<size_t>(t0) * E + e, acc, words, tag);
+  } else {
     for (int tb = t0; tb < t1; tb += kGateTok) {
       const uint16_t* xr[kGateTok];
 #pragma unroll
@@ -76,15 +96,8 @@ __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
       // lane l ends with the total of token tb + l / 16
       const float acc = reduce_scatter<kGateTok, 5, 0>(v, lane);
       const int t = tb + (lane >> 4);
-      if ((lane & 15) == 0 && t < t1) {
-        const size_t o = static_cast<size_t>(t) * E + e;
-        if (logits_f32) {
-          reinterpret_cast<float*>(logits)[o] = acc;
-        } else {
-          reinterpret_cast<uint16_t*>(logits)[o] =
-              static_cast<uint16_t>(f32_to_bf16_bits(acc));
-        }
-      }
+      if ((lane & 15) == 0 && t < t1)
+        store_logit(logits, logits_f32, static_cast<size_t>(t) * E + e, acc, words, tag);
     }
   }
 }
@@ -107,9 +120,53 @@ struct TopkPermuteLds {
   int err;
 };
 
+// Logits of token t from the one-launch router's tagged words (expert
+// j*64 + lane, -inf beyond E).  A word whose tag is not this launch's holds
+// an earlier launch's logit, or this launch's store is not visible here
+// yet: it is read again (agent scope) until its tag matches, at most
+// kRouterSpinLimit rounds; past them meta[LMOE_META_ROUTER_TIMEOUT] becomes 1
+// and the value read is used.
+template <int EPL>
+__device__ __forceinline__ void load_logits_tagged(const uint64_t* words, uint32_t tag, int t,
+                                                   int E, float (&lg)[EPL], int32_t* meta) {
+  const int lane = threadIdx.x & 63;
+  uint64_t wv[EPL];
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = j * kWave + lane;
+    wv[j] = e < E ? __hip_atomic_load(words + static_cast<size_t>(t) * E + e, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT)
+                  : static_cast<uint64_t>(tag) << 32;
+    ok = ok && static_cast<uint32_t>(wv[j] >> 32) == tag;
+  }
+  for (int spin = 0; __builtin_amdgcn_ballot_w64(!ok) != 0; ++spin) {
+    if (spin == kRouterSpinLimit) {
+      if (lane == 0)
+        __hip_atomic_store(meta + LMOE_META_ROUTER_TIMEOUT, 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    ok = true;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = j * kWave + lane;
+      if (static_cast<uint32_t>(wv[j] >> 32) != tag)
+        wv[j] = __hip_atomic_load(words + static_cast<size_t>(t) * E + e, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+      ok = ok && static_cast<uint32_t>(wv[j] >> 32) == tag;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < EPL; ++j)
+    lg[j] = j * kWave + lane < E ? __uint_as_float(static_cast<uint32_t>(wv[j])) : -INFINITY;
+}
+
 // PPL > 0: one wave permutes with PPL pairs per lane; PPL == 0: the block
 // permutation (more pairs or slots than one wave takes).  SCORE: the
-// scoring (LMOE_SCORING_*), sp.scoring must agree.
+// scoring (LMOE_SCORING_*), sp.scoring must agree.  words (the one-launch
+// router): the logits come from its tagged words, see load_logits_tagged.
 template <int EPL, int PPL, int SCORE>
 __device__ __forceinline__ void select_and_permute(
     const void* __restrict__ logits, int logits_f32, int T, const SelectParams& sp,
@@ -118,13 +175,14 @@ __device__ __forceinline__ void select_and_permute(
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
     int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
-    int* hist, TopkPermuteLds<EPL>& L) {
+    int* hist, TopkPermuteLds<EPL>& L, const uint64_t* words = nullptr, uint32_t tag = 0) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   if (wave < T) {
     float bv[EPL], lb[EPL], lg[EPL];
     load_bias<EPL>(sp, bv, lb);
-    load_logits<EPL>(logits, logits_f32, wave, sp.E, lg);
+    if (words != nullptr) load_logits_tagged<EPL>(words, tag, wave, sp.E, lg, meta);
+    else load_logits<EPL>(logits, logits_f32, wave, sp.E, lg);
     int e;
     float w;
     select_token<EPL, SCORE>(sp, lg, bv, lb, L.sel[wave], e, w);
@@ -177,14 +235,16 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
 
 // Gate, selection and permutation in one launch.  Block (b, g)'s waves
 // compute the logits of experts b * nw + wave for the tokens of group g
-// (kGateTok tokens per group, gridDim.y groups) and store them; the block
-// then counts itself in with a release fence and an atomic add on *sync.
-// The last block to arrive (the add returns the grid size - 1) takes an
-// acquire fence, resets *sync to 0 for the next launch, and runs the
-// selection and the permutation over everything the others stored.  No block
-// ever waits for another: the last one only starts once all have finished
-// their stores.  Calls that may run concurrently need separate sync words.
-// ONE: T == 1.
+// (kGateTok tokens per group, gridDim.y groups) and store them, to the
+// logits output and as tagged words in sync (value | this launch's build
+// number << 32, agent-scope atomic stores); the block then counts itself in
+// with an atomic add on sync[0].  The last block to arrive (the add returns
+// the grid size - 1) resets sync[0] to 0 for the next launch and runs the
+// selection and the permutation, reading the words back and reading again
+// any whose tag is not yet this launch's.  Only that last block ever waits,
+// for stores that every other block has already issued.  Calls that may run
+// concurrently need separate sync buffers, and a sync buffer serves one
+// permutation (one meta).  ONE: T == 1.
 template <int NC, int EPL, int PPL, int SCORE, bool ONE>
 __global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T, int H,
@@ -206,25 +266,33 @@ __global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
   const bool l2p_in_lds = log2phy != nullptr && n_log2phy <= kMaxE;
   if (l2p_in_lds)
     for (int i = threadIdx.x; i < n_log2phy; i += blockDim.x) l2p_lds[i] = log2phy[i];
+  // this launch's tag: the build it makes (every block reads the count
+  // before it counts in, and the count advances only after the last one has)
+  const uint32_t tag = static_cast<uint32_t>(__hip_atomic_load(
+                           meta + LMOE_META_GEN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
+  uint64_t* words = reinterpret_cast<uint64_t*>(sync + kRouterWordsOffset);
   const int t0 = ONE ? 0 : static_cast<int>(blockIdx.y) * kGateTok;
   const int t1 = ONE ? T : min(T, t0 + kGateTok);
-  if (e < sp.E && t0 < t1) gate_row<NC, ONE>(x, wg, t0, t1, H, sp.E, e, logits, logits_f32);
-  __syncthreads();  // every wave's logits are stored before thread 0 counts the block in
+  if (e < sp.E && t0 < t1)
+    gate_row<NC, ONE>(x, wg, t0, t1, H, sp.E, e, logits, logits_f32, words, tag);
+  // every wave's logits are issued before thread 0 counts the block in (not
+  // waited for: waiting for the stores to complete cost 0.35 us per layer,
+  // more than the last block's occasional second read)
+  __syncthreads();
   if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    // no release / acquire fences (with them the decode layer took 0.2 us
+    // longer): the count only elects the last block, and the tags tell it
+    // which words it still has to read again
     const int prev = __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = prev == static_cast<int>(gridDim.x * gridDim.y) - 1;
-    if (last) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (last) __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!last) return;
   select_and_permute<EPL, PPL, SCORE>(logits, logits_f32, T, sp, w_f32, w_bf16, ids,
                                       l2p_in_lds ? l2p_lds : log2phy, n_log2phy, P, skip,
                                       block_m, counts, offsets, sorted_pairs, row_idx, active,
-                                      tile_off, meta, hist, L);
+                                      tile_off, meta, hist, L, words, tag);
 }
 
 inline int check_select(int T, int E, int k, int n_shared, int scoring, int n_group,

@@ -27,7 +27,8 @@ LMOE_PATH_MFMA = 2
 LMOE_ERR_ARG = 1000
 LMOE_ERR_SHAPE = 1001
 META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
-META_GEN, META_DECODE_TIMEOUT = 4, 5
+META_GEN, META_DECODE_TIMEOUT, META_ROUTER_TIMEOUT = 4, 5, 6
+ROUTER_SYNC_WORDS = 64 + 2 * 16 * 256  # LMOE_ROUTER_SYNC_WORDS: arrival count, then the tagged logit words
 META_COUNT = 64 + 137 * 64  # LMOE_META_COUNT: the decode hand-off counters sit 256 bytes apart
 MFMA_BLOCK_M = 256  # row-tile height of the prefill MFMA GEMM (tile table of lmoe_permute)
 PART_BLOCK_M = 320  # row tiles of the one-workgroup-per-CU prefill GEMM (lmoe_grouped_mlp)
@@ -368,7 +369,7 @@ def router_gate_topk_permute(
     """router_gate, router_topk and permute into perm in one launch when the
     shape allows it (T <= 16, E <= 256, H <= 8192); otherwise router_gate and
     router_topk_permute.  Same outputs bit for bit; logits is written too.
-    Uses perm.sync as the arrival counter: calls that may run concurrently
+    Uses perm.sync (arrival count and tagged logit words): calls that may run concurrently
     need separate Permutation buffers."""
     lib = load_library()
     T, H = x.shape
@@ -485,7 +486,7 @@ class Permutation:
     tile_off: torch.Tensor      # [P+1] i32 MFMA tile prefix
     meta: torch.Tensor          # [4] i32
     workspace: torch.Tensor     # int8 scratch for the multi-block path
-    sync: torch.Tensor          # [1] i32 arrival counter of the one-launch router, kept at 0
+    sync: torch.Tensor          # [ROUTER_SYNC_WORDS] i32: the one-launch router's arrival count (kept at 0) and tagged logit words
     block_m: int = MFMA_BLOCK_M  # tile height tile_off was last built with
     # the one-launch one-token decode body: its tagged act words ([8, I]
     # u32 for the I it last ran with; the counters live in meta), and which
@@ -515,7 +516,7 @@ class Permutation:
             tile_off=torch.zeros(n_slots + 1, **i32),
             meta=torch.zeros(META_COUNT, **i32),
             workspace=torch.empty(max(ws, 1), dtype=torch.int8, device=device),
-            sync=torch.zeros(1, **i32),
+            sync=torch.zeros(ROUTER_SYNC_WORDS, **i32),
         )
 
 
