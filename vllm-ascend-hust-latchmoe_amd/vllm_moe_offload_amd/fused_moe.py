@@ -223,8 +223,8 @@ def _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2p
 # selection, permutation); with more, the separate gate launch and the
 # selection + permutation launch are faster.  Measured in the 48-layer decode
 # graph: one token 23.6 against 23.8 us per layer; with the one launch's gate
-# split over token groups, four tokens 43.5 against 43.3 us and sixteen 81.7
-# against 80.5 us per layer.
+# split over token groups and its fence-free logit hand-off, four tokens
+# 43.6 against 43.4 us and sixteen 81.5 against 80.4 us per layer (same box).
 ONE_LAUNCH_ROUTER_MAX_TOKENS = 1
 
 
