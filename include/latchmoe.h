@@ -166,11 +166,12 @@ int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
  * reads the words back (again where a tag is not yet this launch's; a wait
  * that gives up sets meta[LMOE_META_ROUTER_TIMEOUT], the result is then
  * undefined) and runs the selection and the permutation.  sync is
- * LMOE_ROUTER_SYNC_WORDS int32, zero before the first call; it serves one
- * permutation (one meta), and calls that may run concurrently need separate
- * sync buffers.
+ * LMOE_ROUTER_SYNC_WORDS int32, 8-byte aligned, zero before the first call;
+ * it serves one permutation (one meta), and calls that may run concurrently
+ * need separate sync buffers.
  * Returns LMOE_ERR_SHAPE when T > 16, E > 256, n_slots > 8192, H % 8 != 0,
- * H > 8192 or x / wg are not 16-byte aligned (then use the separate calls). */
+ * H > 8192, x / wg are not 16-byte aligned or sync is not 8-byte aligned
+ * (then use the separate calls). */
 int lmoe_router_gate_topk_permute(const void* x, const void* wg, int T, int H,
                                   int E, void* logits, int logits_f32, int k,
                                   int n_shared, int scoring, const float* bias,

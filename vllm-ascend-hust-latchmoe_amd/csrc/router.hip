@@ -201,6 +201,7 @@ extern "C" int lmoe_router_gate_topk_permute(
       counts == nullptr || offsets == nullptr || sorted_pairs == nullptr || row_idx == nullptr ||
       active == nullptr || tile_off == nullptr || meta == nullptr || sync == nullptr)
     return LMOE_ERR_ARG;
+  if (reinterpret_cast<uintptr_t>(sync) & 7u) return LMOE_ERR_SHAPE;  // u64 tagged words
   RouterPermuteArgs ra{};
   ra.x = x;
   ra.wg = wg;
