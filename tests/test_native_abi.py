@@ -58,6 +58,11 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert lib.lmoe_table_update(tbl, 8, i3(-1, 3, 2), i3(0, 1, 2), 3, None) == 1000
     assert lib.lmoe_table_update(None, 8, i3(1, 3, 2), i3(0, 1, 2), 3, None) == 1000
     assert lib.lmoe_table_update(None, 8, None, None, 0, None) == 0
+    # the one-launch router's sync buffer holds 64-bit words: 8-byte alignment
+    p = ctypes.c_void_p(4096)
+    args = [p, p, 1, 2048, 128, p, 0, 8, 0, 0, None, None, 1, 1, 1, 1.0, None, p, p, p, 128, 64, 0, 128,
+            p, p, p, p, p, p, p]
+    assert lib.lmoe_router_gate_topk_permute(*args, ctypes.c_void_p(4100), None) == 1001
 
 
 def test_empty_batch_is_legal_with_null_operands():
