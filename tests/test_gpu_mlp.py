@@ -271,7 +271,9 @@ def test_batched_tokens_equal_one_token_at_a_time(T, k, E, H, I):
 
 @pytest.mark.parametrize("k,E,P,H,I", [
     (8, 128, 64, 2048, 768),     # the Qwen3-shaped decode layer
-    (9, 257, 16, 7168, 2048),    # DeepSeek-V3 expert shape, nine pairs
+    (9, 257, 16, 7168, 2048),    # DeepSeek-V3 expert shape, nine pairs: a half wave takes a second slot
+    (10, 64, 16, 2048, 768),     # ten pairs at three chunks per row (next-slot prefetch)
+    (9, 32, 12, 1024, 512),      # two chunks per row
     (4, 40, 24, 1024, 192),
 ])
 def test_one_token_distinct_slot_kernels_equal_general_kernels(k, E, P, H, I):
