@@ -394,9 +394,11 @@ __global__ __launch_bounds__(256) void down_rows_kernel(
 // weighted combine, y indexed by flat pair.  grid (T, ceil(H/2048)); each
 // thread owns 8 consecutive columns.  The k rows of its token are loaded
 // together (up to kCombineStep per step, independent of row_idx, which only
-// masks), then added in j order.
+// masks; every load is issued, from a clamped address where j >= topk),
+// then added in j order.  Eight per step: the 4096-token, top-8 combine
+// took 23.7 us against 26.2 us with sixteen (same bits).
 // ---------------------------------------------------------------------------
-constexpr int kCombineStep = 16;
+constexpr int kCombineStep = 8;
 
 __global__ __launch_bounds__(256) void combine_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ row_idx,
@@ -421,8 +423,9 @@ __global__ __launch_bounds__(256) void combine_kernel(
       const bool in = j < topk;
       use[jj] = in && (row_idx == nullptr || row_idx[p] >= 0);
       wj[jj] = in ? bf16_to_f32(w[p]) : 0.0f;
-      v[jj] = in ? *reinterpret_cast<const uint4*>(y + static_cast<size_t>(p) * H + h)
-                 : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 yv =
+          *reinterpret_cast<const uint4*>(y + (in ? static_cast<size_t>(p) * H + h : 0));
+      v[jj] = in ? yv : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
     for (int jj = 0; jj < kCombineStep; ++jj) {
