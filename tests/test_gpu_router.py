@@ -161,6 +161,31 @@ def test_gate_within_one_bf16_ulp(T, H, E):
     assert frac < 1e-3
 
 
+@pytest.mark.parametrize("T,H,E", [(77, 2048, 200), (333, 1024, 64), (130, 2048, 60), (2048, 7168, 256)])
+def test_large_t_gate_f32_bound_and_bf16_is_its_rounding(T, H, E):
+    """Past 64 tokens the gate is one dense MFMA GEMM (64 x 128 tiles over a
+    4-stage ring when H % 64 == 0 and E % 8 == 0, else 128 x 128 tiles).
+    Ragged row and expert tiles included: the f32 logits stay within the
+    f32 accumulation bound of the exact product, and the bf16 logits are
+    exactly those f32 values rounded to nearest even."""
+    native = _native()
+    print(f"case large-T gate T={T} H={H} E={E}", flush=True)
+    rng = np.random.default_rng(11 + T + E)
+    x = normal_bf16(rng, (T, H), 1.0)
+    wg = normal_bf16(rng, (E, H), 0.02)
+    d_x, d_wg = to_dev_bf16(x), to_dev_bf16(wg)
+    lf = torch.empty((T, E), dtype=torch.float32, device="cuda")
+    lb = torch.empty((T, E), dtype=torch.bfloat16, device="cuda")
+    native.router_gate(d_x, d_wg, lf)
+    native.router_gate(d_x, d_wg, lb)
+    torch.cuda.synchronize()
+    got = lf.cpu().numpy()
+    exact = bf16_to_f32(x).astype(np.float64) @ bf16_to_f32(wg).astype(np.float64).T
+    absdot = np.abs(bf16_to_f32(x)).astype(np.float64) @ np.abs(bf16_to_f32(wg)).astype(np.float64).T
+    assert np.all(np.abs(got - exact) <= 4.0 * np.sqrt(H) * 2.0 ** -24 * absdot + 1e-30)
+    np.testing.assert_array_equal(from_dev_bf16(lb), f32_to_bf16(got))
+
+
 @pytest.mark.parametrize("T,H", [(7, 2048), (13, 7168)])
 def test_gate_grouped_tokens_equal_one_at_a_time(T, H):
     """The GEMV path reduces several tokens at once; each token's f32

@@ -112,9 +112,11 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
   const int wn = wave % C::WN;
 
   // ---- work item: XCD-contiguous chunks of (row tile, column tile) ----
+  // (kDense: one group of g.M_dense rows, no tile table)
   const int col_tile = (MODE == kGateUp) ? C::BN / 2 : C::BN;
   const int NT = (g.N + col_tile - 1) / col_tile;
-  const int total = g.meta[LMOE_META_TILES] * NT;
+  const int n_tiles = (MODE == kDense) ? (g.M_dense + C::BM - 1) / C::BM : g.meta[LMOE_META_TILES];
+  const int total = n_tiles * NT;
   const int chunk = (total + 7) >> 3;
   const int jj = blockIdx.x >> 3;
   if (jj >= chunk) return;
@@ -122,10 +124,10 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
   if (w >= total) return;
   const int tile = w / NT;
   const int n0 = (w - tile * NT) * col_tile;
-  const int slot = find_tile_slot(g.tile_off, g.P, tile);
-  const int p0 = g.offsets[slot];
-  const int row0 = p0 + (tile - g.tile_off[slot]) * C::BM;
-  const int rows = min(C::BM, g.offsets[slot + 1] - row0);
+  const int slot = (MODE == kDense) ? 0 : find_tile_slot(g.tile_off, g.P, tile);
+  const int p0 = (MODE == kDense) ? 0 : g.offsets[slot];
+  const int row0 = p0 + (tile - (MODE == kDense ? 0 : g.tile_off[slot])) * C::BM;
+  const int rows = min(C::BM, (MODE == kDense ? g.M_dense : g.offsets[slot + 1]) - row0);
   const uint16_t* wbase = g.w + static_cast<long long>(slot) * g.w_slot_stride;
   if (MODE == kDown) {
     for (int t = tid; t < C::BM; t += C::THREADS)
@@ -266,6 +268,31 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
   else if (ni_live == 1) main_loop(std::integral_constant<int, 1>{});
   else main_loop(std::integral_constant<int, 0>{});
 
+  // ---- kDense with f32 output: straight from the accumulators (lane l%32
+  // holds row 32 i + l%32, its 16 values are 4 runs of 4 columns) ----
+  if constexpr (MODE == kDense) {
+    if (g.out_f32) {
+      const int m0 = wm * C::WTM + frow;
+      const int cb = wn * C::WTN + 4 * fhi;
+#pragma unroll
+      for (int i = 0; i < C::NI; ++i) {
+        const int m = m0 + 32 * i;
+        if (i >= ni_live || m >= rows) continue;
+        float* orow = reinterpret_cast<float*>(g.out) + static_cast<long long>(row0 + m) * g.N;
+#pragma unroll
+        for (int j = 0; j < C::NJ; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = n0 + cb + j * 32 + 8 * q;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < g.N) orow[n + e] = acc[i][j][4 * q + e];
+          }
+      }
+      return;
+    }
+  }
+
   // ---- epilogue: bf16 tile -> LDS -> 16-byte row stores ----
   constexpr int BNO = C::out_cols(MODE);
   constexpr int PITCH = C::out_pitch(MODE);
@@ -309,6 +336,8 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
     uint16_t* dst;
     if (MODE == kGateUp) {
       dst = reinterpret_cast<uint16_t*>(g.out) + static_cast<long long>(row0 + m) * g.I + n;
+    } else if (MODE == kDense) {
+      dst = reinterpret_cast<uint16_t*>(g.out) + static_cast<long long>(row0 + m) * g.N + n;
     } else {
       dst = reinterpret_cast<uint16_t*>(g.out) + static_cast<long long>(s_rowid[m]) * g.N + n;
     }

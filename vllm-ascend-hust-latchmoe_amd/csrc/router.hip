@@ -64,8 +64,30 @@ extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
   if (H % 8 != 0 || H > kGateMaxChunks * 512) return LMOE_ERR_SHAPE;
   if (T == 0) return LMOE_OK;  // an empty batch: nothing read or written
   if (x == nullptr || wg == nullptr || logits == nullptr) return LMOE_ERR_ARG;
+  if (T > 64 && H % DenseGateTile::BK == 0 && E % 8 == 0 &&
+      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(wg) |
+        reinterpret_cast<uintptr_t>(logits)) & 15u) == 0) {
+    // large token counts: one dense bf16 MFMA GEMM, logits = x . wg^T, with
+    // 64 x 128 tiles and four stages of operands in flight per workgroup
+    // (a few dozen tiles, each a long K chain: the chain's stages, not the
+    // tile count, set the time)
+    GemmArgs g{};
+    g.a = static_cast<const uint16_t*>(x);
+    g.w = static_cast<const uint16_t*>(wg);
+    g.w_slot_stride = 0;
+    g.N = E;
+    g.K = H;
+    g.M_dense = T;
+    g.out = logits;
+    g.out_f32 = logits_f32;
+    const int grid = lds_gemm_grid((T + DenseGateTile::BM - 1) / DenseGateTile::BM,
+                                   (E + DenseGateTile::BN - 1) / DenseGateTile::BN);
+    hipLaunchKernelGGL((grouped_gemm_lds_kernel<kDense, DenseGateTile>), dim3(grid),
+                       dim3(DenseGateTile::THREADS), 0, stream, g);
+    LMOE_RETURN_LAUNCH();
+  }
   if (T > 64) {
-    // large token counts: one dense bf16 MFMA GEMM, logits = x . wg^T
+    // large token counts, other shapes: the 128 x 128 register-staged GEMM
     GemmArgs g{};
     g.a = static_cast<const uint16_t*>(x);
     g.w = static_cast<const uint16_t*>(wg);
