@@ -186,6 +186,24 @@ def test_large_t_gate_f32_bound_and_bf16_is_its_rounding(T, H, E):
     np.testing.assert_array_equal(from_dev_bf16(lb), f32_to_bf16(got))
 
 
+def test_large_t_gate_ring_tiles_equal_register_tiles_bitwise():
+    """The two dense kernels of the large-T gate sum every logit's K/16 MFMA
+    steps in the same order: 60 experts (E % 8 != 0: 128 x 128
+    register-staged tiles) give the same f32 bits as the first 60 of 64
+    experts with the same rows (the 64 x 128 ring tiles)."""
+    native = _native()
+    T, H = 200, 2048
+    rng = np.random.default_rng(77)
+    x = to_dev_bf16(normal_bf16(rng, (T, H), 1.0))
+    wg64 = normal_bf16(rng, (64, H), 0.02)
+    a = torch.empty((T, 60), dtype=torch.float32, device="cuda")
+    b = torch.empty((T, 64), dtype=torch.float32, device="cuda")
+    native.router_gate(x, to_dev_bf16(np.ascontiguousarray(wg64[:60])), a)
+    native.router_gate(x, to_dev_bf16(wg64), b)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b[:, :60].contiguous().view(torch.int32))
+
+
 @pytest.mark.parametrize("T,H", [(7, 2048), (13, 7168)])
 def test_gate_grouped_tokens_equal_one_at_a_time(T, H):
     """The GEMV path reduces several tokens at once; each token's f32
