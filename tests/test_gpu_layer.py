@@ -168,6 +168,52 @@ def test_deepseek_style_grouped_router_with_pinned_shared_expert():
     assert err <= OUT_TOL
 
 
+def test_deepseek_style_full_expert_shape_with_pinned_shared_expert():
+    """The DeepSeek-style layer at the DeepSeek-V3 expert shape (H 7168, I
+    2048; grouped sigmoid top-8 of 8 groups keeping 4, x2.5, correction bias,
+    a pinned shared expert of the routed shape) over 32 routed experts and
+    16 slots, two tokens.  Routing from the oracle on the kernel's logits,
+    output within 2e-2 x RMS of the oracle layer.  The weights are drawn on
+    the GPU (numpy takes minutes at this size) and the oracle reads only the
+    routed experts."""
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    E, H, I, k, B, slots, G, TG = 32, 7168, 2048, 8, 2, 16, 8, 4
+    print(f"case deepseek-style full expert shape E={E} H={H} I={I} B={B}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(7168)
+
+    def mk(*shape):
+        return (torch.randn(shape, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+
+    w13, w2, wg, s13, s2 = mk(E, 2 * I, H), mk(E, H, I), mk(E, H), mk(2 * I, H), mk(H, I)
+    bias = torch.randn((E,), generator=g, device="cuda") * 0.01
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+    rt = Runtime(Cfg(enabled=True, num_slots=slots, async_load=True, pin_host_memory=True))
+    layer = SlotMoELayer(layer_id=4, runtime=rt, gate_weight=wg, w13_weight=w13.cpu(), w2_weight=w2.cpu(), top_k=k,
+                         scoring_func="sigmoid", use_grouped_topk=True, num_expert_group=G, topk_group=TG,
+                         routed_scaling_factor=2.5, e_score_correction_bias=bias,
+                         shared_w13=s13.cpu(), shared_w2=s2.cpu())
+    layer.register()
+    assert layer.mix_placement
+    rng = np.random.default_rng(15)
+    x = normal_bf16(rng, (B, H), 1.0)
+    dx = to_dev_bf16(x)
+    logits = torch.empty((B, E), dtype=torch.bfloat16, device="cuda")
+    fused_moe.route(dx, layer.gate_weight, layer.router_spec, logits_out=logits)
+    out = layer.forward(dx).clone()
+    torch.cuda.synchronize()
+    r_ids, _, r_wb = orouter.grouped_sigmoid_topk(bf16_to_f32(from_dev_bf16(logits)), k,
+                                                  bias=bias.cpu().numpy(), n_group=G, topk_group=TG, scale=2.5)
+    used = np.unique(r_ids)
+    l2p = np.full(E, -1, dtype=np.int32)
+    l2p[used] = np.arange(used.size, dtype=np.int32)
+    idx = torch.from_numpy(used.astype(np.int64)).cuda()
+    ref = omlp.moe_layer(x, r_ids, r_wb, l2p, bits(w13.index_select(0, idx)), bits(w2.index_select(0, idx)),
+                         shared=(bits(s13), bits(s2)))
+    err = rel_max_err(bf16_to_f32(from_dev_bf16(out)), ref)
+    print(f"deepseek-style full-shape err {err:.3e}", flush=True)
+    assert err <= OUT_TOL
+
+
 def test_c1_config_eight_tokens_thirty_two_slots():
     """Qwen3-30B-A3B-shaped layer (H 2048, E 128, top-8
     softmax renormalised, I 768), 32 slots, 8 decode tokens N(0,1), weights
