@@ -345,6 +345,11 @@ __global__ __launch_bounds__(C::THREADS) void grouped_gemm_lds_kernel(GemmArgs g
   }
 }
 
+// 64-row x 128-column tiles with four stages of operands in flight: for a
+// few dozen tiles whose time is the K chain (the router gate over many
+// tokens)
+using SmallTile = LdsTile<64, 128, 1, 2, 4>;
+
 // Upper bound on launched workgroups for up to ub_tiles row tiles: the grid
 // is a multiple of 8 with ceil(items / 8) workgroups per XCD.
 __host__ inline int lds_gemm_grid(int ub_tiles, int n_col_tiles) {

@@ -19,7 +19,7 @@ namespace lmoe {
 
 constexpr int kGateMaxChunks = 16;  // H <= 16 * 512 = 8192 in the GEMV path
 // router gate at large T: 64-row x 128-expert tiles, 2 waves, 4-stage ring
-using DenseGateTile = LdsTile<64, 128, 1, 2, 4>;
+using DenseGateTile = SmallTile;
 constexpr int kGateTok = 4;         // tokens per reduction in the gate GEMV
 // one-launch router: tagged logit words from int32 offset 64 of sync (256
 // bytes past the arrival counter), and the re-reads of a stale word
