@@ -59,7 +59,18 @@
 extern "C" {
 #endif
 
-#define LMOE_ABI_VERSION 6
+#define LMOE_ABI_VERSION 7
+
+enum { LMOE_SKIP_KEEP_ROWS = 2 }; /* lmoe_permute skip_unmapped mode */
+
+/* Device status words (lmoe_device_flags). */
+enum {
+  LMOE_FLAG_UNPLACED = 0,        /* pairs a masked combine dropped: no pass
+                                    placed them (an id outside every table) */
+  LMOE_FLAG_ROUTER_TIMEOUT = 1,  /* one-launch router waits that gave up: the
+                                    routing of that step is invalid */
+  LMOE_FLAG_COUNT = 4
+};
 
 enum {
   LMOE_OK = 0,
@@ -82,17 +93,11 @@ enum {
   LMOE_META_ERRORS = 2,  /* pairs dropped because their id did not map      */
   LMOE_META_TILES = 3,   /* sum over slots of ceil(count / block_m)         */
   LMOE_META_GEN = 4,     /* builds of this permutation so far (+1 per build) */
-  LMOE_META_DECODE_TIMEOUT = 5,  /* lmoe_decode_one: 1 if a wait gave up     */
   LMOE_META_ROUTER_TIMEOUT = 6,  /* lmoe_router_gate_topk_permute: 1 if the
                                     selection gave up waiting for a logit
-                                    (sticky: the library never clears it)    */
-  LMOE_META_DECODE_HINT = 64,    /* lmoe_decode_one: hand-off counter c at
-                                    HINT + c * STRIDE (256 bytes apart, so
-                                    their atomics spread over the memory
-                                    channels), zeroed by every build          */
-  LMOE_META_DECODE_STRIDE = 64,
-  LMOE_META_DECODE_COUNTERS = 137,
-  LMOE_META_COUNT = 64 + 137 * 64 /* 8832 int32 words */
+                                    (sticky: the library never clears it; the
+                                    same event adds to LMOE_FLAG_ROUTER_TIMEOUT) */
+  LMOE_META_COUNT = 64           /* int32 words; the others are reserved */
 };
 
 /* int32 words of the sync buffer of lmoe_router_gate_topk_permute: [0] the
@@ -101,6 +106,16 @@ enum { LMOE_ROUTER_SYNC_WORDS = 64 + 2 * 16 * 256 };
 
 const char* lmoe_status_string(int status);
 int lmoe_abi_version(void);
+
+/* Device status of the current device, summed over the library's kernels:
+ * flags[LMOE_FLAG_COUNT] receives the words (LMOE_FLAG_UNPLACED,
+ * LMOE_FLAG_ROUTER_TIMEOUT); with clear, nonzero words are reset to 0.
+ * Synchronizes stream (a host check point: call it where the host already
+ * waits, e.g. beside the staging op's read of the routed ids).  A nonzero
+ * word means an output since the last clear is invalid.  No counterpart in
+ * the reference, whose host code sees every routed id before the experts
+ * run; this library's captured and device-planned paths do not. */
+int lmoe_device_flags(int32_t* flags, int clear, hipStream_t stream);
 
 /* Gate linear: logits[t][e] = sum_h x[t][h] * wg[e][h], f32 accumulation,
  * stored as bf16 (round to nearest even) or f32.  Replaces the gate matmul of
@@ -195,15 +210,18 @@ size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);
  * [0, n_log2phy) or whose slot is outside [0, n_slots) is left out of the
  * sorted order; it is counted in meta[LMOE_META_ERRORS] unless skip_unmapped
  * is set and the slot is -1 or the id lies outside the table (a pair of
- * another wave).
+ * another wave).  skip_unmapped = 2 (LMOE_SKIP_KEEP_ROWS) skips as 1 does and
+ * leaves row_idx[p] untouched for every pair it does not place: a layer run
+ * in several passes over one row_idx (the first pass with 0 or 1, the later
+ * ones with 2) ends with row_idx[p] >= 0 exactly for the pairs some pass
+ * placed, the row mask of its single combine.  Other values: LMOE_ERR_ARG.
  * Outputs: counts[s]; offsets[s] = exclusive prefix of counts (offsets[P] =
  * placed pairs); sorted_pairs[offsets[s] + r] = the r-th pair of slot s in
  * flat order; row_idx[p] = sorted position of pair p or -1; active[a] = a-th
  * slot with count > 0 (ascending), -1 for a >= meta[LMOE_META_ACTIVE];
  * tile_off[s] = sum over s' < s of
  * ceil(counts[s'] / block_m); meta[LMOE_META_COUNT] (ACTIVE, PAIRS, ERRORS,
- * TILES; GEN advanced, the lmoe_decode_one timeout flag and counters
- * zeroed; the other words are not written).
+ * TILES; GEN advanced; the other words are not written).
  * Replaces slot_mapping.py:116-140 + npu_moe_init_routing_v2
  * (patch_fused_moe.py:668-701: expert_capacity=-1, drop_pad_mode=0,
  * expert_tokens_num_type=1). */
@@ -310,9 +328,13 @@ int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
  * LMOE_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.  No
  * counterpart in the reference: for callers that cannot allocate (code under
  * hipGraph capture, serving loops or harnesses that forbid hipMalloc).  The
- * call allocates nothing.  Limit: align256(T*k*I*2) + align256(T*k*H*2)
- * bytes must fit the array (else LMOE_ERR_WORKSPACE, before any device
- * work); e.g. Qwen3 shape (H 2048, I 768, k 8) up to T = 409.  Every call on
+ * call allocates nothing.  Limits, both checked before any device work:
+ * T*k <= 1024 (the decode body's, else LMOE_ERR_SHAPE) and
+ * align256(T*k*I*2) + align256(T*k*H*2) <= LMOE_NOALLOC_SCRATCH_BYTES (else
+ * LMOE_ERR_WORKSPACE), i.e. T <= min(1024 / k, what the array holds):
+ * Qwen3 shape (H 2048, I 768, k 8) T <= 128 (the array alone would hold
+ * 186), DeepSeek-V3 expert shape with the shared pair (H 7168, I 2048,
+ * k 9) T <= 50.  Every call on
  * one GPU shares that GPU's array: calls that may overlap on one GPU race and
  * must be ordered by the caller. */
 int lmoe_fused_moe_decode_noalloc(const void* x, int T, int H, int I, int k,
@@ -385,29 +407,6 @@ int lmoe_slot_plan(int8_t* state, int32_t* owner, int64_t* version,
  * write, or an index_copy_ of the changed entries). */
 int lmoe_table_update(int32_t* table, int n_table, const int32_t* idx,
                       const int32_t* val, int n, hipStream_t stream);
-
-/* One-token decode body in ONE launch (T = 1, k <= 8 pairs in distinct
- * slots, as lmoe_fused_moe_decode with distinct_slots): gate_up + SiLU*mul
- * producers and down + combine consumers in one grid, the consumers' W2
- * rows in flight while the producers run.  act values pass between
- * workgroups as tagged 32-bit words (bf16 | (meta[LMOE_META_GEN] & 0xffff)
- * << 16, words [k, I] u32, zero before the first call) through agent-scope
- * atomic accesses, and the producers' progress through the counters at
- * meta[LMOE_META_DECODE_HINT + c * LMOE_META_DECODE_STRIDE]; the
- * permutation build (lmoe_permute,
- * lmoe_router_*_permute) that precedes the call advances the generation
- * and zeroes the counters, so AT MOST ONE lmoe_decode_one may run per
- * build (a second one on the same build may read the first one's act), and
- * one words buffer serves one permutation.  Every wait is bounded:
- * meta[LMOE_META_DECODE_TIMEOUT] becomes 1 if one gave up (the result is
- * then undefined).  out equals lmoe_fused_moe_decode's bit for bit.
- * Shapes: H <= 4096, I <= 1024 (others return LMOE_ERR_UNSUPPORTED: use
- * lmoe_fused_moe_decode).  Replaces the decode fused_experts call of
- * patches/patch_fused_moe.py:3946-4009 for one token. */
-int lmoe_decode_one(const void* x, int H, int I, int k, const void* w13_slots,
-                    const void* w2_slots, int n_slots, const uint16_t* w,
-                    const int32_t* row_idx, const int32_t* active, const void* add,
-                    void* words, void* out, int32_t* meta, hipStream_t stream);
 
 /* Bytes of the int32 plan buffer of lmoe_wave_plan / lmoe_wave_stage for
  * n_routed <= 1024 experts, n_slots <= 1024 stage slots and max_waves <= 256

@@ -602,3 +602,76 @@ def test_decode_overflow_through_the_layer_seam_equals_one_bank():
         torch.cuda.synchronize()
         assert torch.equal(a.view(torch.int16), b.view(torch.int16)), step
     assert la.runtime.transfer_engine.bytes_issued > lb.runtime.transfer_engine.bytes_issued
+
+
+def test_decode_overflow_buffers_shared_by_layers_under_seam_replays():
+    """Three layers over two overflow stage buffers (layers 0 and 2 share
+    one), every layer overflowing, the MLP piece replayed from a captured
+    graph after the eager stage op, and no record_layer_compute or
+    end_overflow_compute call: a layer's overflow copies must still wait for
+    the earlier reader of its buffer.  Every layer's output equals a
+    one-bank layer's bit for bit at every step."""
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    from vllm_moe_offload_amd.ops.fused_moe.moe_offload_stage_op import PHASE_DECODE, stage_topk_for_layer
+
+    rng = np.random.default_rng(47)
+    E, H, I, k, T, L = 64, 1024, 256, 8, 16, 3
+    common = dict(enabled=True, async_load=True, pin_host_memory=True, graph_compatible_offload=True)
+    rt_a = Runtime(Cfg(num_slots=32, decode_overflow=True, **common))
+    rt_b = Runtime(Cfg(num_slots=64, **common))
+    assert rt_a.config.effective_prefill_buffer_count == 2
+    layers = []
+    for l in range(L):
+        w13, w2, wg = _weights(rng, E, H, I)
+        t13 = torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16)
+        t2 = torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16)
+        gate = to_dev_bf16(wg)
+        la = SlotMoELayer(layer_id=100 + l, runtime=rt_a, gate_weight=gate, w13_weight=t13, w2_weight=t2, top_k=k)
+        lb = SlotMoELayer(layer_id=200 + l, runtime=rt_b, gate_weight=gate, w13_weight=t13, w2_weight=t2, top_k=k)
+        la.register()
+        lb.register()
+        layers.append((la, lb))
+    dev = torch.device("cuda")
+    static_x = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    static_w = [torch.empty((T, k), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    static_ids = [torch.empty((T, k), dtype=torch.int32, device=dev) for _ in range(L)]
+    out_a = [torch.empty((T, H), dtype=torch.bfloat16, device=dev) for _ in range(L)]
+    ws = [fused_moe.get_workspace(T, k, 32, H, I, dev, tag=f"shared_buf{l}") for l in range(L)]
+    graphs = [None] * L
+
+    def piece(l):
+        lid = 100 + l
+        bank = rt_a.slot_bank(lid)
+        ovf = rt_a.decode_overflow_slot_weights(layer_id=lid, n_pairs=T * k)
+        fused_moe._fused_experts_ws(static_x, static_w[l], static_ids[l], bank.w13_slots, bank.w2_slots,
+                                    rt_a.log2phy_buffer(lid), out=out_a[l], workspace=ws[l], overflow=ovf)
+
+    for step in range(4):
+        static_x.copy_(to_dev_bf16(normal_bf16(rng, (T, H), 1.0)))
+        for l, (la, _) in enumerate(layers):
+            w, ids, _ = fused_moe.route(static_x, la.gate_weight, la.router_spec)
+            static_w[l].copy_(w)
+            static_ids[l].copy_(ids)
+            stage_topk_for_layer(rt_a, static_ids[l], 100 + l, E, PHASE_DECODE)
+            if graphs[l] is None:
+                piece(l)
+                s = torch.cuda.Stream()
+                s.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(s):
+                    piece(l)
+                torch.cuda.current_stream().wait_stream(s)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    piece(l)
+                graphs[l] = g
+            graphs[l].replay()
+        torch.cuda.synchronize()
+        for l, (_, lb) in enumerate(layers):
+            print(f"case shared overflow buffers step {step} layer {l}", flush=True)
+            assert rt_a.decode_overflow_slot_weights(layer_id=100 + l, n_pairs=T * k) is not None
+            stage_topk_for_layer(rt_b, static_ids[l], 200 + l, E, PHASE_DECODE)
+            bank = rt_b.slot_bank(200 + l)
+            ref = fused_moe.fused_experts(static_x, static_w[l], static_ids[l], bank.w13_slots, bank.w2_slots,
+                                          rt_b.log2phy_buffer(200 + l))
+            torch.cuda.synchronize()
+            assert torch.equal(out_a[l].view(torch.int16), ref.view(torch.int16)), (step, l)

@@ -428,95 +428,3 @@ def test_block_range_kernel_equals_tile_grid_at_prefill_sizes(T, E, P):
     assert torch.equal(outs[256][0].view(torch.int16), outs[320][0].view(torch.int16))
     assert torch.equal(outs[256][1].view(torch.int16), outs[320][1].view(torch.int16))
     assert torch.isfinite(outs[320][1].float()).all()
-
-
-
-@pytest.mark.parametrize("k,E,P,H,I,with_add", [
-    (8, 128, 64, 2048, 768, False),   # the Qwen3-shaped decode layer
-    (8, 128, 64, 2048, 768, True),
-    (6, 64, 8, 4096, 1024, False),
-    (2, 16, 4, 512, 128, True),
-])
-def test_one_launch_one_token_body_equals_two_kernels(k, E, P, H, I, with_add, monkeypatch):
-    """lmoe_decode_one (gate_up producers and down consumers in one grid,
-    tagged-word hand-off) gives the two-kernel body's bits, build after
-    build and replayed from a captured graph, with no wait given up; a
-    second call on the same build takes the two-kernel body."""
-    native = _native()
-    print(f"case decode-one k={k} E={E} P={P} H={H} I={I} add={with_add}", flush=True)
-    rng = np.random.default_rng(7000 + H + k)
-    add = to_dev_bf16(normal_bf16(rng, (1, H), 1.0)) if with_add else None
-    perm = native.Permutation.allocate(k, P, "cuda")
-    act = torch.empty((k, I), dtype=torch.bfloat16, device="cuda")
-    out = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
-    ref = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
-    cases = []
-    for c in range(4):
-        ids, l2p, x, w13, w2, wb = _case(7100 + c * 13 + H, 1, k, E, P, H, I)
-        cases.append(_dev(ids, l2p, x, w13, w2, wb) + ((ids, l2p, x, w13, w2, wb),))
-    static = [torch.empty_like(t) for t in cases[0][:6]]
-
-    def load(c):
-        for dst, src in zip(static, cases[c][:6]):
-            dst.copy_(src)
-        native.permute(static[0], perm, log2phy=static[1])
-
-    def body():
-        monkeypatch.setenv("LATCHMOE_DECODE_ONE", "1")
-        native.fused_moe_decode(static[2], static[5], static[3], static[4], perm, act, out, add=add,
-                                distinct_slots=True)
-        monkeypatch.delenv("LATCHMOE_DECODE_ONE")
-
-    def timeout():
-        return int(perm.meta[native.META_DECODE_TIMEOUT].item())
-
-    def two_kernels():
-        monkeypatch.setenv("LATCHMOE_DECODE_ONE", "0")
-        native.fused_moe_decode(static[2], static[5], static[3], static[4], perm, act, ref, add=add,
-                                distinct_slots=True)
-        monkeypatch.delenv("LATCHMOE_DECODE_ONE")
-
-    monkeypatch.setenv("LATCHMOE_DECODE_ONE", "1")
-    assert native.decode_one_supported(H, I, k)
-    monkeypatch.delenv("LATCHMOE_DECODE_ONE")
-    for c in range(4):
-        load(c)
-        body()
-        assert perm.decoded_build == perm.builds
-        torch.cuda.synchronize()
-        assert timeout() == 0
-        two_kernels()
-        torch.cuda.synchronize()
-        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), c
-        body()  # same build again: the two-kernel body
-        torch.cuda.synchronize()
-        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), c
-    ids, l2p, x, w13, w2, wb = cases[0][6]
-    want = omlp.moe_layer(x, ids, wb, l2p, w13, w2)
-    if add is not None:
-        want = want + bf16_to_f32(from_dev_bf16(add))
-    load(0)
-    body()
-    torch.cuda.synchronize()
-    assert rel_max_err(bf16_to_f32(from_dev_bf16(out)), want) <= OUT_TOL
-    # captured once (on a fresh build, so the one-launch body is what the
-    # graph holds), replayed over every case
-    load(0)
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        body()
-    torch.cuda.current_stream().wait_stream(s)
-    load(0)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        body()
-    assert perm.decoded_build == perm.builds
-    for c in range(4):
-        load(c)  # a new build before every replay
-        g.replay()
-        torch.cuda.synchronize()
-        assert timeout() == 0
-        two_kernels()
-        torch.cuda.synchronize()
-        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), ("replay", c)

@@ -19,6 +19,7 @@ from vllm_moe_offload_amd.moe_offload.phase_split import (
     build_b2_routed_pair_index,
     build_b2_wave_microbatch_plans,
     count_routed_tokens_by_expert,
+    count_shared_suffix_pairs,
     direct_scatter_add_b2_permuted_output,
     direct_scatter_add_b2_permuted_outputs,
     materialize_b2_pair_microbatches_from_plans,
@@ -230,3 +231,15 @@ def test_long_lru_trajectories_match_oracle():
         assert prepared.mapping.active_slot_ids == want_slots
         assert rt.log2phy_buffer(3).tolist() == table.log2phy
     assert 0 < misses < 400 * slots
+
+
+def test_shared_suffix_pair_count_ignores_ids_past_the_layer():
+    """Only ids in [routed, total) are shared-suffix pairs: an id at or past
+    total is in no wave and no suffix, so the coverage check (waves + shared
+    == T * k) fails closed on it (phase_split.py:1808-1812)."""
+    ids = torch.tensor([[0, 4], [1, 5], [2, 6], [3, 9], [-1, 4]], dtype=torch.int32)  # routed 4, total 6
+    assert count_shared_suffix_pairs(ids, 4, 6) == 3        # the 4, 5, 4 entries
+    assert count_shared_suffix_pairs(ids, 4, 4) == 0        # no suffix
+    counts = {e: c for e, c in count_routed_tokens_by_expert(ids).items() if e < 4}
+    covered = sum(counts.values()) + count_shared_suffix_pairs(ids, 4, 6)
+    assert covered == 7 < ids.numel()                                   # 6, 9 and -1 are uncovered

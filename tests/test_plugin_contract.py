@@ -151,3 +151,32 @@ def test_stage_op_stages_a_regime_a_layer_whose_full_residency_was_not_staged():
                 assert table == [0, 1, 2, 3]  # the static table, untouched by the seam
         finally:
             rtm.reset_moe_offload_runtime()
+
+
+def test_stage_op_fails_closed_on_ids_outside_the_layer():
+    """An id outside [0, total) has no slot, stage buffer or wave: the seam
+    raises on the host copy of the ids instead of letting a pass skip it."""
+    from vllm_moe_offload_amd.moe_offload import runtime as rtm
+    from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+    from vllm_moe_offload_amd.ops.fused_moe.moe_offload_stage_op import PHASE_DECODE, PHASE_PREFILL, _moe_offload_stage_impl
+
+    class L(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layer_id = 3
+            self.w13_weight = torch.nn.Parameter(torch.zeros(6, 2, 1))
+            self.w2_weight = torch.nn.Parameter(torch.zeros(6, 1, 1))
+
+    rtm._runtime = rtm.MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=2, b2_wave_prefill=True,
+                                                          decode_overflow=True))
+    try:
+        rt = rtm._runtime
+        rt.register_layer_for_fixed_slots(L(), slot_device=torch.device("cpu"))
+        before = rt.log2phy_buffer(3).tolist()
+        for bad, phase in (([[0, 6]], PHASE_DECODE), ([[-1, 1]], PHASE_DECODE), ([[0, 1], [2, 7]], PHASE_PREFILL)):
+            with pytest.raises(RuntimeError, match="outside"):
+                _moe_offload_stage_impl(torch.tensor(bad, dtype=torch.int32), 3, 6, phase)
+        assert rt.log2phy_buffer(3).tolist() == before  # nothing staged
+        _moe_offload_stage_impl(torch.tensor([[0, 5]], dtype=torch.int32), 3, 6, PHASE_DECODE)  # in range
+    finally:
+        rtm.reset_moe_offload_runtime()

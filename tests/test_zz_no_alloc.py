@@ -55,8 +55,8 @@ def test_noalloc_decode_equals_workspace_decode(H, I, E, P, k, sizes):
 def test_noalloc_refuses_sizes_past_the_scratch_array():
     from vllm_moe_offload_amd import native
 
-    H, I, k, P = 2048, 768, 8, 8
-    T = 512  # 4096 pairs: 6.3 MB of act + 16.8 MB of y > 8 MiB
+    H, I, k, P = 7168, 2048, 8, 8
+    T = 100  # 800 pairs (within the 1024-pair limit): 3.3 MB of act + 11.5 MB of y > 8 MiB
     x = torch.zeros((T, H), dtype=torch.bfloat16, device="cuda")
     w = torch.zeros((T, k), dtype=torch.bfloat16, device="cuda")
     w13 = torch.zeros((P, 2 * I, H), dtype=torch.bfloat16, device="cuda")
@@ -64,5 +64,36 @@ def test_noalloc_refuses_sizes_past_the_scratch_array():
     perm = native.Permutation.allocate(T * k, P, "cuda")
     out = torch.zeros((T, H), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(RuntimeError, match="workspace too small"):
+        native.fused_moe_decode_noalloc(x, w, w13, w2, perm, out)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("H,I,k,t_max,err", [
+    (2048, 768, 8, 128, "unsupported shape"),      # Qwen3 shape: the 1024-pair limit binds
+    (7168, 2048, 9, 50, "workspace too small"),    # DeepSeek-V3 expert shape + shared pair: the array binds
+])
+def test_noalloc_limit_boundary(H, I, k, t_max, err):
+    """The largest batch the entry point takes runs (bit for bit equal to
+    the workspace form); one token more is refused before any device work."""
+    from vllm_moe_offload_amd import native
+
+    E = P = 64
+    g = torch.Generator(device="cuda").manual_seed(H + 3 * k)
+    w13 = (torch.randn((P, 2 * I, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn((P, H, I), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    print(f"case noalloc boundary H={H} T={t_max}", flush=True)
+    x, w, perm = _case(native, 900 + k, t_max, k, E, P, H, I)
+    act = torch.empty((t_max * k, I), dtype=torch.bfloat16, device="cuda")
+    y = torch.empty((t_max * k, H), dtype=torch.bfloat16, device="cuda")
+    ref = torch.empty((t_max, H), dtype=torch.bfloat16, device="cuda")
+    native.fused_moe_decode(x, w, w13, w2, perm, act, ref, y=y)
+    out = torch.full((t_max, H), float("nan"), dtype=torch.bfloat16, device="cuda")
+    native.fused_moe_decode_noalloc(x, w, w13, w2, perm, out)
+    torch.cuda.synchronize()
+    assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
+    print(f"case noalloc boundary H={H} T={t_max + 1} (refused)", flush=True)
+    x, w, perm = _case(native, 901 + k, t_max + 1, k, E, P, H, I)
+    out = torch.zeros((t_max + 1, H), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(RuntimeError, match=err):
         native.fused_moe_decode_noalloc(x, w, w13, w2, perm, out)
     torch.cuda.synchronize()

@@ -12,6 +12,32 @@ namespace lmoe {
 constexpr int kWave = 64;
 
 // ---------------------------------------------------------------------------
+// device status words (lmoe_device_flags)
+// ---------------------------------------------------------------------------
+// Each translation unit holds its own copy per GPU (the build has no
+// relocatable device code): [LMOE_FLAG_UNPLACED] pairs a masked combine
+// dropped because no pass placed them, [LMOE_FLAG_ROUTER_TIMEOUT] one-launch
+// router waits that gave up.  Kernels only add to them (vector atomics);
+// lmoe_device_flags sums every unit's words and clears them.  Unused copies
+// cost 16 bytes.
+static __device__ __attribute__((aligned(16))) int32_t g_lmoe_flags[LMOE_FLAG_COUNT];
+
+__device__ __forceinline__ void add_device_flag(int f, int v) {
+  __hip_atomic_fetch_add(&g_lmoe_flags[f], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The device address of this unit's words on the current device (nullptr
+// on failure); defined once per unit by LMOE_FLAGS_UNIT(name).
+#define LMOE_FLAGS_UNIT(name)                                                    \
+  namespace lmoe {                                                               \
+  void* flags_address_##name() {                                                 \
+    void* p = nullptr;                                                           \
+    return hipGetSymbolAddress(&p, HIP_SYMBOL(g_lmoe_flags)) == hipSuccess ? p \
+                                                                           : nullptr; \
+  }                                                                              \
+  }
+
+// ---------------------------------------------------------------------------
 // bf16 <-> f32
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf16lo(uint32_t packed) {

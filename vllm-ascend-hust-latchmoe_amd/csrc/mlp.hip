@@ -235,6 +235,7 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     const int p = tid + u * 256;
     pre_pos[u] = p < NP ? row_idx[p] : -1;
     pre_w[u] = p < NP ? bf16_to_f32(wts[p]) : 0.0f;
+    if (blockIdx.x == 0 && p < NP && pre_pos[u] < 0) add_device_flag(LMOE_FLAG_UNPLACED, 1);
   }
   // add term of this thread's first output (T * R <= 256 covers decode)
   const float pre_add = (add != nullptr && tid < T * R && h0 + tid % R < H)
@@ -422,6 +423,9 @@ __global__ __launch_bounds__(256) void combine_kernel(
       const int p = t * topk + j;
       const bool in = j < topk;
       use[jj] = in && (row_idx == nullptr || row_idx[p] >= 0);
+      // a pair no pass placed: counted once (first column block of the token)
+      if (in && !use[jj] && blockIdx.y == 0 && threadIdx.x == 0)
+        add_device_flag(LMOE_FLAG_UNPLACED, 1);
       wj[jj] = in ? bf16_to_f32(w[p]) : 0.0f;
       const uint4 yv =
           *reinterpret_cast<const uint4*>(y + (in ? static_cast<size_t>(p) * H + h : 0));
@@ -600,6 +604,8 @@ static int launch_grouped_mfma(GemmArgs g, int n_pairs, int max_active, int bloc
 }
 
 }  // namespace lmoe
+
+LMOE_FLAGS_UNIT(mlp)
 
 using namespace lmoe;
 

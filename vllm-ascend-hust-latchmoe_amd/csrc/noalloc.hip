@@ -22,6 +22,7 @@ namespace {
 
 constexpr size_t kScratchBytes = static_cast<size_t>(LMOE_NOALLOC_SCRATCH_BYTES);
 constexpr int kMaxDevices = 64;
+constexpr int kDecodeMaxPairs = 1024;  // lmoe_fused_moe_decode: T * k <= 1024
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -60,6 +61,9 @@ extern "C" int lmoe_fused_moe_decode_noalloc(const void* x, int T, int H, int I,
                                              int distinct_slots, hipStream_t stream) {
   if (T < 0 || H <= 0 || I <= 0 || k <= 0) return LMOE_ERR_ARG;
   const size_t n_pairs = static_cast<size_t>(T) * static_cast<size_t>(k);
+  // the decode body's own pair limit, checked here too so that no call past
+  // it reaches the array-size check below with a misleading status
+  if (n_pairs > static_cast<size_t>(kDecodeMaxPairs)) return LMOE_ERR_SHAPE;
   const size_t act_bytes = align256(n_pairs * static_cast<size_t>(I) * 2);
   const size_t y_bytes = align256(n_pairs * static_cast<size_t>(H) * 2);
   if (act_bytes + y_bytes > kScratchBytes) return LMOE_ERR_WORKSPACE;

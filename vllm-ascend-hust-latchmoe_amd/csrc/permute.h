@@ -20,6 +20,10 @@ namespace lmoe {
 
 constexpr int kChunk = 1024;       // pairs per block
 constexpr int kMaxSlots = 8192;    // LDS histogram bound
+// skip mode 2: as mode 1, and a pair this build leaves out keeps the row_idx
+// an earlier pass of the same layer wrote, so that after the passes row_idx
+// is >= 0 exactly for the pairs some pass placed (the combine's row mask)
+constexpr int kSkipKeepRows = 2;
 
 // slot of pair p: >= 0 placed, -1 skipped silently, -2 error
 __device__ __forceinline__ int map_pair(const int32_t* ids, int p,
@@ -40,17 +44,10 @@ __device__ __forceinline__ int map_pair(const int32_t* ids, int p,
 }
 
 // Per-build state past the four counts: the build counter advances (the
-// one thread that publishes meta) and the one-token decode body's hand-off
-// counters start from zero (every thread t of n takes words t, t + n, ...).
+// one thread that publishes meta).
 __device__ __forceinline__ void publish_build(int32_t* meta) {
   // no-return atomic: the publishing thread does not wait for the old value
   __hip_atomic_fetch_add(meta + LMOE_META_GEN, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// the one-launch decode body's timeout flag and hand-off counters
-__device__ __forceinline__ void clear_decode_handoff(int32_t* meta, int t, int n) {
-  for (int c = t; c <= LMOE_META_DECODE_COUNTERS; c += n)
-    meta[c == 0 ? LMOE_META_DECODE_TIMEOUT
-                : LMOE_META_DECODE_HINT + (c - 1) * LMOE_META_DECODE_STRIDE] = 0;
 }
 
 __device__ __forceinline__ uint64_t match_key(int key, int nbits) {
@@ -126,7 +123,6 @@ __device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
   // active[a] = -1 past the active slots: kernels that serve "the a-th
   // active slot" read one value (no dependent load of meta first)
   for (int a = atot + threadIdx.x; a < P; a += blockDim.x) active[a] = -1;
-  clear_decode_handoff(meta, threadIdx.x, blockDim.x);
   if (threadIdx.x == 0) {
     offsets[P] = ctot;
     tile_off[P] = ttot;
@@ -206,7 +202,7 @@ __device__ __forceinline__ void permute_block(
       const int s = sl[c] >= 0 ? sl[c] : -1;
       const int pos = chunk_positions(s, nb, hist);  // chunks in pair order: stable
       if (p < N) {
-        row_idx[p] = pos;
+        if (pos >= 0 || skip != kSkipKeepRows) row_idx[p] = pos;
         if (pos >= 0) sorted_pairs[pos] = p;
       }
     }
@@ -308,7 +304,6 @@ __device__ __forceinline__ void permute_wave(
   }
   // active[a] = -1 past the active slots (see scan_slots)
   for (int a = atot + lane; a < P; a += kWave) active[a] = -1;
-  clear_decode_handoff(meta, lane, kWave);
   if (lane == 0) {
     offsets[P] = ctot;
     tile_off[P] = ttot;
@@ -331,7 +326,7 @@ __device__ __forceinline__ void permute_wave(
       if (placed && rank[g] == 0) lds[s[g]] = pos + cnt[g];
     }
     if (p < N) {
-      row_idx[p] = pos;
+      if (pos >= 0 || skip != kSkipKeepRows) row_idx[p] = pos;
       if (pos >= 0) sorted_pairs[pos] = p;
     }
   }

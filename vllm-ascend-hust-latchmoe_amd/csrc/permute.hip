@@ -104,7 +104,7 @@ __global__ __launch_bounds__(1024) void permute_scan_kernel(
 
 // Step 3: stable scatter of each chunk from its per-slot bases.
 __global__ __launch_bounds__(1024) void permute_scatter_kernel(
-    int N, int P, const int32_t* __restrict__ slot_of,
+    int N, int P, int skip, const int32_t* __restrict__ slot_of,
     const int32_t* __restrict__ chunk_cnt, int32_t* __restrict__ sorted_pairs,
     int32_t* __restrict__ row_idx) {
   extern __shared__ int run_base[];
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(1024) void permute_scatter_kernel(
   const int s = p < N ? slot_of[p] : -1;
   const int pos = chunk_positions(s >= 0 ? s : -1, key_bits(P), run_base);
   if (p < N) {
-    row_idx[p] = pos;
+    if (pos >= 0 || skip != kSkipKeepRows) row_idx[p] = pos;
     if (pos >= 0) sorted_pairs[pos] = p;
   }
 }
@@ -161,7 +161,8 @@ extern "C" int lmoe_permute(const int32_t* ids, int n_pairs,
     return LMOE_ERR_ARG;
   if (log2phy != nullptr && n_log2phy <= 0) return LMOE_ERR_ARG;
   if (n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
-  const int skip = skip_unmapped ? 1 : 0;
+  if (skip_unmapped < 0 || skip_unmapped > kSkipKeepRows) return LMOE_ERR_ARG;
+  const int skip = skip_unmapped;
   const size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
   if (wave_perm_fits(n_pairs, n_slots)) {
     // decode sizes: one wave, no block barriers
@@ -214,7 +215,7 @@ extern "C" int lmoe_permute(const int32_t* ids, int n_pairs,
                        tile_off, meta);
   }
   hipLaunchKernelGGL(permute_scatter_kernel, dim3(nchunks), dim3(kChunk), lds,
-                     stream, n_pairs, n_slots, slot_of, chunk_cnt, sorted_pairs,
+                     stream, n_pairs, n_slots, skip, slot_of, chunk_cnt, sorted_pairs,
                      row_idx);
   LMOE_RETURN_LAUNCH();
 }

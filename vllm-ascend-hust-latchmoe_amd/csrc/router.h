@@ -145,9 +145,11 @@ __device__ __forceinline__ void load_logits_tagged(const uint64_t* words, uint32
   }
   for (int spin = 0; __builtin_amdgcn_ballot_w64(!ok) != 0; ++spin) {
     if (spin == kRouterSpinLimit) {
-      if (lane == 0)
+      if (lane == 0) {
         __hip_atomic_store(meta + LMOE_META_ROUTER_TIMEOUT, 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+        add_device_flag(LMOE_FLAG_ROUTER_TIMEOUT, 1);
+      }
       break;
     }
     __builtin_amdgcn_s_sleep(1);

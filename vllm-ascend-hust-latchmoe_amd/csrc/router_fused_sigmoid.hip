@@ -10,3 +10,5 @@ template int launch_topk_permute<LMOE_SCORING_SIGMOID>(const RouterPermuteArgs&,
 template int launch_gate_topk_permute<LMOE_SCORING_SIGMOID>(const RouterPermuteArgs&, hipStream_t);
 
 }  // namespace lmoe
+
+LMOE_FLAGS_UNIT(router_sigmoid)

@@ -132,6 +132,41 @@ bool gpu_accessible_range(const void* p, size_t bytes, const void** dev) {
 
 extern "C" int lmoe_abi_version(void) { return LMOE_ABI_VERSION; }
 
+namespace lmoe {
+void* flags_address_mlp();
+void* flags_address_router_softmax();
+void* flags_address_router_sigmoid();
+}  // namespace lmoe
+
+extern "C" int lmoe_device_flags(int32_t* flags, int clear, hipStream_t stream) {
+  if (flags == nullptr) return LMOE_ERR_ARG;
+  // the units whose kernels add to their status words
+  static void* (*const units[])() = {lmoe::flags_address_mlp, lmoe::flags_address_router_softmax,
+                                     lmoe::flags_address_router_sigmoid};
+  constexpr int kUnits = sizeof(units) / sizeof(units[0]);
+  static const int32_t zeros[LMOE_FLAG_COUNT] = {0};
+  for (int f = 0; f < LMOE_FLAG_COUNT; ++f) flags[f] = 0;
+  for (int u = 0; u < kUnits; ++u) {
+    void* p = units[u]();
+    if (p == nullptr) return LMOE_ERR_ARG;
+    int32_t w[LMOE_FLAG_COUNT];
+    hipError_t e = hipMemcpyAsync(w, p, sizeof(w), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return static_cast<int>(e);
+    bool any = false;
+    for (int f = 0; f < LMOE_FLAG_COUNT; ++f) {
+      flags[f] += w[f];
+      any = any || w[f] != 0;
+    }
+    if (clear && any) {
+      e = hipMemcpyAsync(p, zeros, sizeof(zeros), hipMemcpyHostToDevice, stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return static_cast<int>(e);
+    }
+  }
+  return LMOE_OK;
+}
+
 extern "C" const char* lmoe_status_string(int status) {
   switch (status) {
     case LMOE_OK: return "ok";

@@ -167,7 +167,10 @@ def _overflow_pass(hidden, topk_ids, k: int, overflow: PreparedSlotWeights, ws: 
     I = int(overflow.w1.shape[1]) // 2
     perm = ws.overflow_perm(T * k, P2, hidden.device)
     bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P2, H, I, hidden.device, n_pairs=T * k)
-    native.permute(topk_ids, perm, log2phy=overflow.log2phy, skip_unmapped=True, block_m=bm)
+    # the bank pass's row_idx marks the pairs placed by either pass: the
+    # combine's row mask
+    native.permute(topk_ids, perm, log2phy=overflow.log2phy, keep_rows=True, row_idx=ws.perm.row_idx,
+                   block_m=bm)
     native.grouped_mlp(hidden, k, overflow.w1, overflow.w2, perm, ws.act[: T * k], ws.y[: T * k],
                        path=native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA)
 
@@ -200,7 +203,7 @@ def _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2p
         _overflow_pass(hidden, topk_ids, k, overflow, ws, decode=decode)
         if events:
             events[2].record()
-        native.combine(ws.y[: T * k], topk_weights, dst, add=add)
+        native.combine(ws.y[: T * k], topk_weights, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
         return dst, ws
     if decode:
         if events:  # the decode body fuses GMM2 with the combine
@@ -282,7 +285,7 @@ def decode_layer(
         native.grouped_mlp(hidden, kw, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], ws.y[: T * kw],
                            path=native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA)
         _overflow_pass(hidden, ids, kw, overflow, ws, decode=decode)
-        native.combine(ws.y[: T * kw], w, dst, add=add)
+        native.combine(ws.y[: T * kw], w, dst, row_mask=ws.perm.row_idx[: T * kw], add=add)
         return dst, w, ids
     if T * kw <= native.FUSED_DECODE_MAX_PAIRS and I <= native.GEMV_MAX_I:
         # router-fed ids: distinct experts per token, in distinct slots
@@ -573,9 +576,17 @@ def run_wave_prefill(
     report = WaveRunReport(plan.waves, sched.compute_order)
     staged: dict[int, tuple] = {}
     total_logical = runtime.total_logical_expert_count_for_layer(layer_id=layer_id, fallback=num_logical_experts)
-    # pairs of a pinned shared suffix (ids >= routed) run with the first
-    # computed wave only; later waves' tables stop at the routed ids
-    shared_pairs = int((topk_ids >= routed).sum().item()) if total_logical > routed else 0
+    # pairs of a pinned shared suffix (ids in [routed, total)) run with the
+    # first computed wave only; later waves' tables stop at the routed ids
+    shared_pairs = phase_split.count_shared_suffix_pairs(topk_ids, routed, total_logical)
+    # fail closed before any wave runs: the waves must cover every pair
+    # exactly once (phase_split.py:1808-1812); an id outside [0, total) is
+    # in no wave, and the caller falls back to the full layer
+    if plan.total_pairs + shared_pairs != T * k:
+        raise phase_split.B2WaveFallback(
+            "B2 wave pair coverage does not match the original top-k routing: "
+            f"covered={plan.total_pairs + shared_pairs} expected={T * k}"
+        )
     first = True
     t_loop = perf_counter()
     computed: set[int] = set()
@@ -610,7 +621,7 @@ def run_wave_prefill(
             t_mlp = perf_counter()
             handle = runtime.begin_slot_compute(prepared)
             try:
-                native.permute(topk_ids, ws.perm, log2phy=prepared.log2phy, skip_unmapped=True,
+                native.permute(topk_ids, ws.perm, log2phy=prepared.log2phy, skip_unmapped=True, keep_rows=not first,
                                table_len=total_logical if first else routed,
                                block_m=native.prefill_block_m(len(plan.waves[w]), H, I, hidden.device, n_pairs=T * k))
                 first = False
@@ -627,14 +638,9 @@ def run_wave_prefill(
                 wp["stage_wait_ms"] = round((t_mlp - t_wait) * 1000.0, 3)
                 wp["mlp_ms"] = round((perf_counter() - t_mlp) * 1000.0, 3)  # host issue time
                 wp["issue_end_to_compute_ms"] = round((t_wait - wp.pop("_issue_end")) * 1000.0, 3)
-    if plan.total_pairs + shared_pairs != T * k:
-        raise phase_split.B2WaveFallback(
-            "B2 wave pair coverage does not match the original top-k routing: "
-            f"covered={plan.total_pairs + shared_pairs} expected={T * k}"
-        )
     t_scatter = perf_counter()
     dst = out if out is not None else ws.out[:T]
-    native.combine(ws.y[: T * k], topk_weights, dst, add=add)
+    native.combine(ws.y[: T * k], topk_weights, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
     t_end = perf_counter()
     report.seconds = t_end - t0
     if profiling:
@@ -770,6 +776,15 @@ def run_device_waves(
     compute = torch.cuda.current_stream(dev)
     tx = runtime.transfer_engine._transfer_stream(dev)
     native.wave_plan(topk_ids, plan, n_total=total)
+    if not capturing:
+        # fail closed before any copy: a pair whose id lies outside
+        # [0, total) is in no wave (phase_split.py:1808-1812).  Under capture
+        # nothing is read back: the plan header's invalid count (word 2)
+        # stays on the device, and the combine's row mask drops such pairs
+        invalid = int(plan.buf[2].item())
+        if invalid:
+            raise phase_split.B2WaveFallback(
+                f"device wave plan left {invalid} pairs with ids outside [0, {total}) in no wave")
     planned = torch.cuda.Event()
     planned.record(compute)
     tx.wait_event(planned)
@@ -795,7 +810,7 @@ def run_device_waves(
         ready = torch.cuda.Event()
         ready.record(tx)
         compute.wait_event(ready)
-        native.permute(topk_ids, ws.perm, log2phy=table, skip_unmapped=True, block_m=bm)
+        native.permute(topk_ids, ws.perm, log2phy=table, skip_unmapped=True, keep_rows=w > 0, block_m=bm)
         native.grouped_mlp(hidden, k, stage.w13_slots, stage.w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k],
                            path=path)
         done = torch.cuda.Event()
@@ -811,7 +826,7 @@ def run_device_waves(
     else:
         compute.wait_stream(tx)  # the forked transfer stream rejoins the capture
     dst = out if out is not None else ws.out[:T]
-    native.combine(ws.y[: T * k], topk_weights, dst, add=add)
+    native.combine(ws.y[: T * k], topk_weights, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
     return dst
 
 
@@ -827,12 +842,56 @@ def run_full_layer(
     out: torch.Tensor | None = None,
     path: int = native.LMOE_PATH_AUTO,
 ) -> torch.Tensor:
-    """Blocking fallback: stage the whole layer, one pass, one combine."""
+    """Blocking fallback: stage the whole layer, one pass, one combine.
+    Eager calls fail closed (RuntimeError) when a pair maps to no slot of
+    the full layer, as the reference's remap does (slot_mapping.py:116-140)."""
     prepared, _ = runtime.prepare_full_layer_prefill_plan(
         layer_id=layer_id, num_logical_experts=num_logical_experts, device=hidden.device,
     )
     T, H = hidden.shape
     k = int(topk_ids.shape[1])
     ws = get_workspace(T, k, prepared.physical_expert_count, H, int(prepared.w1.shape[1]) // 2, hidden.device, tag="full")
-    return fused_experts(hidden, topk_weights, topk_ids, prepared.w1, prepared.w2, prepared.log2phy,
-                         add=add, out=out, path=path, workspace=ws)
+    dst = fused_experts(hidden, topk_weights, topk_ids, prepared.w1, prepared.w2, prepared.log2phy,
+                        add=add, out=out, path=path, workspace=ws)
+    if not _is_current_graph_capturing():
+        check_placed(ws)
+    return dst
+
+
+def run_overflow_prefill(
+    runtime: MoeOffloadRuntime,
+    *,
+    layer_id: int,
+    hidden: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    num_logical_experts: int,
+    device_planned: bool,
+    add: torch.Tensor | None = None,
+    token_counts_by_expert: dict[int, int] | None = None,
+) -> torch.Tensor:
+    """Capacity waves (device- or host-planned) with the reference's one
+    recoverable error: a B2WaveFallback runs the blocking full layer instead
+    (patches/patch_fused_moe.py:2281-2298 -> _run_b2_full_layer_reference
+    :3472-3650), and the reason goes to the profile evidence."""
+    t0 = perf_counter()
+    try:
+        if device_planned:
+            return run_device_waves(runtime, layer_id=layer_id, hidden=hidden, topk_weights=topk_weights,
+                                    topk_ids=topk_ids, num_logical_experts=num_logical_experts, add=add)
+        out, _ = run_wave_prefill(runtime, layer_id=layer_id, hidden=hidden, topk_weights=topk_weights,
+                                  topk_ids=topk_ids, num_logical_experts=num_logical_experts, add=add,
+                                  token_counts_by_expert=token_counts_by_expert)
+        return out
+    except phase_split.B2WaveFallback as exc:
+        reason = f"{type(exc).__name__}: {exc}"
+        if os.environ.get("SEW_B2_PROBE") or os.environ.get("SEW_OFFLOAD_PROBE"):
+            print(f"SEW_B2 branch=FALLBACK_FULL_LAYER layer={layer_id} reason={reason}", flush=True)
+        total = runtime.total_logical_expert_count_for_layer(layer_id=layer_id, fallback=num_logical_experts)
+        out = run_full_layer(runtime, layer_id=layer_id, hidden=hidden, topk_weights=topk_weights,
+                             topk_ids=topk_ids, num_logical_experts=total, add=add)
+        if runtime.profile_path:
+            runtime._record_profile_event("b2_full_layer_fallback", layer_id=int(layer_id), start=t0,
+                                          payload={"fallback_reason": reason, "n_tokens": int(hidden.shape[0]),
+                                                   "device_planned": bool(device_planned)})
+        return out

@@ -29,8 +29,7 @@ from vllm_moe_offload_amd.fused_moe import (
     fused_experts,
     get_workspace,
     route,
-    run_device_waves,
-    run_wave_prefill,
+    run_overflow_prefill,
 )
 from vllm_moe_offload_amd.moe_offload.cpu_first_loader import (
     CPU_FIRST_MARKER,
@@ -190,17 +189,16 @@ class SlotMoELayer(torch.nn.Module):
             add = self.shared_expert_forward(shared_experts_input if shared_experts_input is not None else hidden)
         rt = self.runtime
         if rt.consume_device_waves(layer_id=self.layer_id, topk_ids=ids):
-            return run_device_waves(rt, layer_id=self.layer_id, hidden=hidden, topk_weights=w, topk_ids=ids,
-                                    num_logical_experts=self.num_logical_experts, add=add)
+            return run_overflow_prefill(rt, layer_id=self.layer_id, hidden=hidden, topk_weights=w, topk_ids=ids,
+                                        num_logical_experts=self.num_logical_experts, device_planned=True, add=add)
         if not _is_current_graph_capturing():
             stats = rt.consume_prefill_route_stats_record(layer_id=self.layer_id, topk_ids=ids)
             if stats is not None:
-                out, _ = run_wave_prefill(
+                return run_overflow_prefill(
                     rt, layer_id=self.layer_id, hidden=hidden, topk_weights=w, topk_ids=ids,
-                    num_logical_experts=self.num_logical_experts, add=add,
+                    num_logical_experts=self.num_logical_experts, device_planned=False, add=add,
                     token_counts_by_expert=_with_shared(stats.token_counts_by_expert, self),
                 )
-                return out
         comm = MoECommMethod(rt)
         res = comm.fused_experts(
             MoEFusedExpertsInput(

@@ -159,6 +159,15 @@ def count_routed_tokens_by_expert(topk_ids: torch.Tensor) -> dict[int, int]:
     return {int(e): int(c) for e, c in zip(ids.tolist(), counts.tolist()) if int(e) >= 0 and int(c) > 0}
 
 
+def count_shared_suffix_pairs(topk_ids: torch.Tensor, routed: int, total: int) -> int:
+    """Pairs of a pinned shared suffix: ids in [routed, total).  An id at or
+    past total belongs to no expert, so it is not counted and the layer's
+    coverage check (waves + shared pairs == T * k) fails closed on it."""
+    if int(total) <= int(routed) or topk_ids.numel() == 0:
+        return 0
+    return int(((topk_ids >= int(routed)) & (topk_ids < int(total))).sum().item())
+
+
 def plan_balanced_b2_waves(
     token_counts_by_expert: dict[int, int],
     num_slots: int,

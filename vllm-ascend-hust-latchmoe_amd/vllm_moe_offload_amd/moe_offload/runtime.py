@@ -368,6 +368,28 @@ class MoeOffloadRuntime:
     def is_layer_registered(self, layer_id: int) -> bool:
         return int(layer_id) in self._slot_banks
 
+    def check_device_flags(self, *, layer_id: int | None = None) -> None:
+        """Fail closed on the device status words of the native library
+        (pairs a masked combine dropped because no pass placed them, one-launch
+        router waits that gave up): either means an output since the last
+        check is invalid.  The words are read and cleared with one small
+        synchronizing copy per kernel unit, so callers make this check where
+        the host already waits; with layer_id given it runs only for the
+        lowest registered layer, i.e. once per forward pass."""
+        if layer_id is not None and self._slot_banks and int(layer_id) != min(self._slot_banks):
+            return
+        if not torch.cuda.is_available():
+            return
+        from vllm_moe_offload_amd import native
+
+        flags = native.device_flags(clear=True)
+        unplaced, timeouts = flags[native.FLAG_UNPLACED], flags[native.FLAG_ROUTER_TIMEOUT]
+        if unplaced or timeouts:
+            raise RuntimeError(
+                "MoE outputs since the last device check are invalid: "
+                f"{unplaced} routed pairs were placed in no slot or wave, "
+                f"{timeouts} one-launch router waits gave up")
+
     def fused_shared_lane_layout(self, layer_id: int) -> FusedSharedLaneLayout | None:
         return self._fused_shared_lane_layouts.get(int(layer_id))
 
@@ -1002,7 +1024,13 @@ class MoeOffloadRuntime:
         buf = self.decode_overflow_buffer_index(layer_id)
         stage = self._get_prefill_stage_bank(layer_id=layer_id, buffer_index=buf, template_bank=src)
         table = self._overflow_table(layer_id, total, src.w13_slots.device)
-        wait = self.prefill_stage_buffer_release_event(layer_id=layer_id, buffer_index=buf)
+        # the buffer's last reader recorded its release when its Python ran
+        # (end_overflow_compute); a replayed graph piece records none, so the
+        # copies also wait for everything queued on the compute stream so far,
+        # which holds every earlier reader of this buffer (an earlier layer's
+        # piece is queued before this layer's staging runs)
+        wait = tuple(ev for ev in (self.prefill_stage_buffer_release_event(layer_id=layer_id, buffer_index=buf),
+                                   self._record_current_stream_event_or_none()) if ev is not None)
         loads = [(self._host_store.get(layer_id, e), stage.assign_transient_slot(i, ExpertKey(layer_id, e), step_id=step_id))
                  for i, e in enumerate(experts)]
         for sid in range(len(experts), stage.num_dynamic_slots):
@@ -1015,8 +1043,8 @@ class MoeOffloadRuntime:
                     loads, wait_event=wait, record_event=True, validate_layout=False,
                     table_update=(table, tuple(experts), tuple(range(len(experts))), True))
             else:
-                if wait is not None:
-                    _synchronize_event(getattr(wait, "event", wait))
+                for ev in wait:
+                    _synchronize_event(getattr(ev, "event", ev))
                 self._transfer_engine.load_many_sync(loads, validate_layout=False)
                 values = np.full(int(table.numel()), -1, dtype=np.int32)
                 values[list(experts)] = np.arange(len(experts), dtype=np.int32)

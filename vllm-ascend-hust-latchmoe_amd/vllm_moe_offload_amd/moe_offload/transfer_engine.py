@@ -151,7 +151,8 @@ class TransferEngine:
 
     def load_many_async(self, loads: list[Load], *, wait_event=None, record_event: bool = True,
                         validate_layout: bool = True, table_update=None):
-        """Queue the loads on the transfer stream; returns a TransferReadyEvent
+        """Queue the loads on the transfer stream after wait_event (an event
+        or a sequence of events); returns a TransferReadyEvent
         (None when the copy completed synchronously).  table_update =
         (device int32 table, indices, values[, fill]) is written by the same
         batch, before its ready event (device slots only); fill=True writes
@@ -170,7 +171,7 @@ class TransferEngine:
             slot.state = SlotState.LOADING
         done = torch.cuda.Event() if record_event else None
         ranges = copy_ranges(loads)
-        self._issue(ranges, stream, _torch_event(wait_event), done, table_update,
+        self._issue(ranges, stream, _torch_events(wait_event), done, table_update,
                     direct=all(b.host_pinned or b.w13.device.type == "cuda" for b, _ in loads))
         self.copies_issued += len(ranges)
         self.bytes_issued += sum(r[2] for r in ranges)
@@ -184,11 +185,11 @@ class TransferEngine:
         self._in_flight.append(ready)
         return ready
 
-    def _issue(self, ranges, stream, wait_event, done, table_update, *, direct: bool) -> None:
+    def _issue(self, ranges, stream, wait_events, done, table_update, *, direct: bool) -> None:
         from vllm_moe_offload_amd import native
 
-        if wait_event is not None:
-            stream.wait_event(wait_event)
+        for ev in wait_events:
+            stream.wait_event(ev)
         if direct and self.copy_engine == "gather" and native.stage_gather(ranges, stream, table_update=table_update):
             self.batches_gathered += 1
         else:
@@ -214,13 +215,22 @@ class TransferEngine:
         return self._stream
 
 
+def _waits(wait_event) -> tuple:
+    """wait_event as a tuple: one event (or TransferReadyEvent), a sequence
+    of them, or None."""
+    if wait_event is None:
+        return ()
+    return tuple(wait_event) if isinstance(wait_event, (tuple, list)) else (wait_event,)
+
+
 def _host_wait(wait_event) -> None:
-    ev = getattr(wait_event, "event", wait_event)
-    sync = getattr(ev, "synchronize", None)
-    if callable(sync):
-        sync()
+    for w in _waits(wait_event):
+        ev = getattr(w, "event", w)
+        sync = getattr(ev, "synchronize", None)
+        if callable(sync):
+            sync()
 
 
-def _torch_event(wait_event):
-    ev = getattr(wait_event, "event", wait_event)
-    return ev if isinstance(ev, torch.cuda.Event) else None
+def _torch_events(wait_event) -> tuple:
+    return tuple(ev for ev in (getattr(w, "event", w) for w in _waits(wait_event))
+                 if isinstance(ev, torch.cuda.Event))

@@ -27,17 +27,20 @@ LMOE_PATH_MFMA = 2
 LMOE_ERR_ARG = 1000
 LMOE_ERR_SHAPE = 1001
 META_ACTIVE, META_PAIRS, META_ERRORS, META_TILES = 0, 1, 2, 3
-META_GEN, META_DECODE_TIMEOUT, META_ROUTER_TIMEOUT = 4, 5, 6
+META_GEN, META_ROUTER_TIMEOUT = 4, 6
 ROUTER_SYNC_WORDS = 64 + 2 * 16 * 256  # LMOE_ROUTER_SYNC_WORDS: arrival count, then the tagged logit words
-META_COUNT = 64 + 137 * 64  # LMOE_META_COUNT: the decode hand-off counters sit 256 bytes apart
+META_COUNT = 64  # LMOE_META_COUNT
+FLAG_UNPLACED, FLAG_ROUTER_TIMEOUT, FLAG_COUNT = 0, 1, 4  # lmoe_device_flags words
 MFMA_BLOCK_M = 256  # row-tile height of the prefill MFMA GEMM (tile table of lmoe_permute)
 PART_BLOCK_M = 320  # row tiles of the one-workgroup-per-CU prefill GEMM (lmoe_grouped_mlp)
 FUSED_DECODE_MAX_PAIRS = 1024
+SKIP_KEEP_ROWS = 2  # LMOE_SKIP_KEEP_ROWS: lmoe_permute mode of the later passes of a multi-pass layer
 GEMV_MAX_I = 4096  # the decode GEMV kernels hold at most 16 chunks of 256 act columns
 
 EXPORTED_SYMBOLS = (
     "lmoe_status_string",
     "lmoe_abi_version",
+    "lmoe_device_flags",
     "lmoe_router_gate",
     "lmoe_router_topk",
     "lmoe_router_topk_permute",
@@ -56,7 +59,6 @@ EXPORTED_SYMBOLS = (
     "lmoe_stage_gather",
     "lmoe_table_update",
     "lmoe_slot_plan",
-    "lmoe_decode_one",
     "lmoe_wave_plan_bytes",
     "lmoe_wave_plan",
     "lmoe_wave_stage",
@@ -70,6 +72,7 @@ _sz = ctypes.c_size_t
 _SIGNATURES = {
     "lmoe_status_string": (ctypes.c_char_p, [_i]),
     "lmoe_abi_version": (_i, []),
+    "lmoe_device_flags": (_i, [_vp, _i, _vp]),
     "lmoe_router_gate": (_i, [_vp, _vp, _i, _i, _i, _vp, _i, _vp]),
     "lmoe_router_topk": (
         _i,
@@ -115,7 +118,6 @@ _SIGNATURES = {
     "lmoe_stage_gather": (_i, [_vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp]),
     "lmoe_slot_plan": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _i, ctypes.c_int64, _vp, _vp]),
     "lmoe_table_update": (_i, [_vp, _i, _vp, _vp, _i, _vp]),
-    "lmoe_decode_one": (_i, [_vp, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "lmoe_wave_plan_bytes": (ctypes.c_longlong, [_i, _i, _i]),
     "lmoe_wave_plan": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp]),
     "lmoe_wave_stage": (
@@ -162,6 +164,17 @@ def _check(status: int, fn: str) -> None:
     if status != 0:
         msg = load_library().lmoe_status_string(int(status))
         raise RuntimeError(f"{fn} failed with status {status}: {msg.decode()}")
+
+
+def device_flags(*, clear: bool = True, stream=None) -> list[int]:
+    """The current device's status words (lmoe_device_flags: pairs a masked
+    combine dropped, one-launch router waits that gave up), summed over the
+    library's kernels since the last clear.  Synchronizes the stream."""
+    lib = load_library()
+    buf = (ctypes.c_int32 * FLAG_COUNT)()
+    _check(lib.lmoe_device_flags(ctypes.cast(buf, ctypes.c_void_p), int(bool(clear)), _stream(stream)),
+           "lmoe_device_flags")
+    return [int(v) for v in buf]
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -488,17 +501,7 @@ class Permutation:
     workspace: torch.Tensor     # int8 scratch for the multi-block path
     sync: torch.Tensor          # [ROUTER_SYNC_WORDS] i32: the one-launch router's arrival count (kept at 0) and tagged logit words
     block_m: int = MFMA_BLOCK_M  # tile height tile_off was last built with
-    # the one-launch one-token decode body: its tagged act words ([8, I]
-    # u32 for the I it last ran with; the counters live in meta), and which
-    # build it last ran on (one launch per build)
-    decode_words: torch.Tensor | None = None
-    builds: int = 0
-    decoded_build: int = -1
-
-    def decode_words_for(self, I: int, device) -> torch.Tensor:
-        if self.decode_words is None or int(self.decode_words.shape[1]) != int(I):
-            self.decode_words = torch.zeros((8, int(I)), dtype=torch.int32, device=device)
-        return self.decode_words
+    builds: int = 0  # lmoe_permute builds issued on these buffers
 
     @classmethod
     def allocate(cls, n_pairs: int, n_slots: int, device) -> "Permutation":
@@ -526,6 +529,8 @@ def permute(
     *,
     log2phy: torch.Tensor | None = None,
     skip_unmapped: bool = False,
+    keep_rows: bool = False,
+    row_idx: torch.Tensor | None = None,
     table_len: int | None = None,
     block_m: int = MFMA_BLOCK_M,
     stream=None,
@@ -533,12 +538,23 @@ def permute(
     """Remap ids through log2phy and stable-sort the flat pairs by slot.
 
     table_len (<= log2phy.numel()) limits the ids the table covers; with
-    skip_unmapped, ids past it are left to another pass."""
+    skip_unmapped, ids past it are left to another pass.  keep_rows (a later
+    pass of a multi-pass layer; implies skip_unmapped) leaves the row_idx of
+    the pairs this pass does not place as an earlier pass wrote it, so the
+    layer's single combine masks exactly the pairs no pass placed.  row_idx
+    replaces perm.row_idx as the output (the first pass's permutation when
+    the passes build separate permutations)."""
     lib = load_library()
     _need(ids, "topk_ids", torch.int32)
     n = int(ids.numel())
     if n != perm.n_pairs:
         raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {n}")
+    rows = perm.row_idx if row_idx is None else row_idx
+    if row_idx is not None:
+        _need(row_idx, "row_idx", torch.int32)
+        if int(row_idx.numel()) < max(1, n):
+            raise ValueError("row_idx has fewer entries than pairs")
+    mode = SKIP_KEEP_ROWS if keep_rows else int(bool(skip_unmapped))
     n_table = 0
     if log2phy is not None:
         _need(log2phy, "log2phy", torch.int32)
@@ -546,9 +562,9 @@ def permute(
     _check(
         lib.lmoe_permute(
             _ptr(ids), n, _ptr(log2phy), n_table,
-            perm.n_slots, int(bool(skip_unmapped)), int(block_m),
+            perm.n_slots, mode, int(block_m),
             _ptr(perm.counts), _ptr(perm.offsets), _ptr(perm.sorted_pairs),
-            _ptr(perm.row_idx), _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta),
+            _ptr(rows), _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta),
             _ptr(perm.workspace), int(perm.workspace.numel()), _stream(stream),
         ),
         "lmoe_permute",
@@ -736,18 +752,6 @@ def fused_moe_decode(
         _need(add, "add", torch.bfloat16, (T, H))
     if y is not None:
         _need(y, "y", torch.bfloat16, (perm.n_pairs, H))
-    if distinct_slots and T == 1 and decode_one_supported(H, I, k) and perm.decoded_build != perm.builds:
-        # one launch: the down weights stream in while gate_up runs (at most
-        # once per permutation build: the build starts its hand-off state)
-        words = perm.decode_words_for(I, x.device)
-        _check(
-            lib.lmoe_decode_one(_ptr(x), H, I, k, _ptr(w13_slots), _ptr(w2_slots), P, _ptr(topk_weights),
-                                _ptr(perm.row_idx), _ptr(perm.active), _ptr(add), _ptr(words), _ptr(out),
-                                _ptr(perm.meta), _stream(stream)),
-            "lmoe_decode_one",
-        )
-        perm.decoded_build = perm.builds
-        return out
     _check(
         lib.lmoe_fused_moe_decode(
             _ptr(x), T, H, I, k, _ptr(w13_slots), _ptr(w2_slots), P, _ptr(topk_weights),
@@ -758,17 +762,6 @@ def fused_moe_decode(
         "lmoe_fused_moe_decode",
     )
     return out
-
-
-def decode_one_supported(H: int, I: int, k: int) -> bool:
-    """lmoe_decode_one is switched on (LATCHMOE_DECODE_ONE=1; off by
-    default: on the Qwen3-shaped layer it measured 24.9 us per layer in the
-    48-layer decode graph against 23.8 us for the two-kernel body: its
-    108 registers per lane halve gate_up's occupancy) and takes the shape
-    (the others run the two-kernel body)."""
-    if os.environ.get("LATCHMOE_DECODE_ONE", "0") != "1":
-        return False
-    return k <= 8 and H % 8 == 0 and I % 64 == 0 and (H + 511) // 512 <= 8 and (I + 255) // 256 <= 4
 
 
 NOALLOC_SCRATCH_BYTES = 8 << 20  # LMOE_NOALLOC_SCRATCH_BYTES

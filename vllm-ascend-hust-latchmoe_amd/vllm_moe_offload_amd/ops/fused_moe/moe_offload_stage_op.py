@@ -119,6 +119,13 @@ def stage_topk_for_layer(runtime, topk_ids: torch.Tensor, layer_id: int, num_log
             print(f"LATCHMOE_SEAM branch=device_waves layer={layer_id}", flush=True)
         return
     flat = topk_ids.detach().reshape(-1).to("cpu", non_blocking=False)  # the seam's D2H
+    bad = int(((flat < 0) | (flat >= total)).sum()) if flat.numel() else 0
+    if bad:
+        # no slot, stage buffer or wave serves such a pair: fail closed here,
+        # as the reference's remap does (slot_mapping.py:116-140), rather than
+        # let a pass skip it
+        raise RuntimeError(f"layer {layer_id}: topk_ids hold {bad} pairs with expert ids outside [0, {total})")
+    runtime.check_device_flags(layer_id=layer_id)
     counts, _ = count_active_experts_from_cpu_topk(flat, num_logical_experts=routed)
     active = tuple(sorted(counts))
     n_active = len(active)

@@ -137,11 +137,11 @@ def _patch_moe_comm_method_runtime_hooks(_comm) -> bool:
             # the seam left this overflow to the device planner: no host step
             fused_moe.check_supported_input(fused_experts_input)
             w = fused_experts_input.topk_weights
-            out = fused_moe.run_device_waves(
+            out = fused_moe.run_overflow_prefill(
                 runtime, layer_id=layer_id, hidden=fused_experts_input.hidden_states,
                 topk_weights=w if w.dtype == torch.bfloat16 else w.to(torch.bfloat16),
                 topk_ids=fused_experts_input.topk_ids.to(torch.int32).contiguous(),
-                num_logical_experts=int(off.num_logical_experts),
+                num_logical_experts=int(off.num_logical_experts), device_planned=True,
                 add=getattr(fused_experts_input, "shared_output", None),
             )
             return result_cls(routed_out=out, before_dispatch_evt=None, before_gmm2_evt=None,
@@ -151,10 +151,10 @@ def _patch_moe_comm_method_runtime_hooks(_comm) -> bool:
         if stats is not None:
             # the stage op deferred an overflow: capacity waves, one combine
             fused_moe.check_supported_input(fused_experts_input)
-            out, _ = fused_moe.run_wave_prefill(
+            out = fused_moe.run_overflow_prefill(
                 runtime, layer_id=layer_id, hidden=fused_experts_input.hidden_states,
                 topk_weights=fused_experts_input.topk_weights, topk_ids=fused_experts_input.topk_ids,
-                num_logical_experts=int(off.num_logical_experts),
+                num_logical_experts=int(off.num_logical_experts), device_planned=False,
                 add=getattr(fused_experts_input, "shared_output", None),
                 token_counts_by_expert=dict(stats.token_counts_by_expert),
             )
