@@ -20,8 +20,10 @@ after the step's eager staging has made every routed expert resident.  Also repo
   staging     forced k misses per layer per step (k in 1, 4, 8): H2D GB/s on
               the transfer stream and the fraction of compute overlapped,
               with per-layer graph replays and stable slot addresses
-  deepseek    DeepSeek-V3-style layer (H 7168, E 256, I 2048, grouped
-              sigmoid router, pinned shared expert): decode us/token
+  deepseek    DeepSeek-V3-style layer (H 7168, E 256 + 1 shared, I 2048,
+              grouped sigmoid router): every expert resident (kernels on the
+              real working set), and staged through a 64-slot bank and a
+              page-locked host store (decode B 1/8/32, 2048-token prefill)
   cpu_baseline  the numpy oracle of the same layer on the host cores
 
 Synthetic data: weights N(0, 0.02) bf16 and hidden states N(0, 1) from fixed
@@ -797,51 +799,53 @@ def bench_staging(model: DecodeModel, ks=(1, 4, 8), steps: int = 16, seed: int =
 # ---------------------------------------------------------------------------
 # C5: DeepSeek-V3-style layer (compute, resident slots)
 # ---------------------------------------------------------------------------
-def bench_deepseek(batches=(1, 8, 32), prefill_tokens: int = 2048, reps: int = 20) -> dict:
-    """DeepSeek-V3-style layer with every routed expert resident: 64 slots
-    hold the 256 routed ids round-robin (the weights are synthetic, so the
-    bytes and flops are those of a real layer) plus the shared expert as a
-    pinned suffix slot, appended to every token's top-8 with weight 1."""
+def bench_deepseek(batches=(1, 8, 32), prefill_tokens: int = 2048, reps: int = 20,
+                   staged_steps=(12, 6, 3), prefill_steps: int = 2) -> dict:
+    """DeepSeek-V3-style layer (C5) at its own working set: 256 routed
+    experts and one shared expert (H 7168, I 2048, grouped sigmoid router,
+    bias for selection only, scale 2.5; the shared expert appended to every
+    token's top-8 as a pinned suffix id with weight 1).
+
+    resident   all 257 experts in one 257-slot bank (identity table): the
+               kernels on the bytes and flops of the real working set
+               (distinct experts per step reported), graph-replayed
+    staged     the configuration's 64-slot bank, the 256 routed experts in a
+               page-locked host store, the shared expert pinned in the bank:
+               every step goes through the staging op (vllm::moe_offload_stage)
+               -- an LRU bank (plus one overflow pass) up to 128 experts,
+               device-planned waves with their H2D inside past that and for
+               the prefill -- and is timed whole (eager, copies included);
+               H2D bytes and the resident leg's compute time for the same
+               batch are reported beside it, and every staged output is
+               compared with the resident bank on the same routing
+    """
     import torch
 
     from vllm_moe_offload_amd import fused_moe, native
+    from vllm_moe_offload_amd.moe_offload.config import MoeOffloadConfig
+    from vllm_moe_offload_amd.moe_offload.runtime import MoeOffloadRuntime
+    from vllm_moe_offload_amd.ops.fused_moe.moe_offload_stage_op import (PHASE_DECODE, PHASE_PREFILL,
+                                                                         stage_topk_for_layer)
 
     dev = torch.device("cuda")
     Hd, Ed, Id, Kd, P = 7168, 256, 2048, 8, 64
+    NT = Ed + 1  # routed + the shared expert
     g = torch.Generator(device=dev)
     g.manual_seed(7168)
-    w13 = (torch.randn((P + 1, 2 * Id, Hd), generator=g, device=dev) * 0.02).to(torch.bfloat16)
-    w2 = (torch.randn((P + 1, Hd, Id), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    t0 = time.perf_counter()
+    w13 = torch.empty((NT, 2 * Id, Hd), dtype=torch.bfloat16, device=dev)
+    w2 = torch.empty((NT, Hd, Id), dtype=torch.bfloat16, device=dev)
+    for e in range(NT):
+        w13[e].copy_(torch.randn((2 * Id, Hd), generator=g, device=dev) * 0.02)
+        w2[e].copy_(torch.randn((Hd, Id), generator=g, device=dev) * 0.02)
     gate = (torch.randn((Ed, Hd), generator=g, device=dev) * 0.02).to(torch.bfloat16)
     bias = (torch.randn((Ed,), generator=g, device=dev) * 0.01).float()
-    l2p = torch.cat([torch.arange(Ed, dtype=torch.int32, device=dev) % P,
-                     torch.tensor([P], dtype=torch.int32, device=dev)])
-    res: dict = {}
+    l2p = torch.arange(NT, dtype=torch.int32, device=dev)
     per_expert = 3 * Hd * Id * 2
-    # the router appends the shared expert (id Ed -> slot P, weight 1)
     spec = fused_moe.RouterSpec(top_k=Kd, scoring_func="sigmoid", use_grouped_topk=True, num_expert_group=8,
                                 topk_group=4, routed_scaling_factor=2.5, e_score_correction_bias=bias, n_shared=1)
-
-    def make_step(B, path):
-        x = torch.randn((B, Hd), generator=g, device=dev).to(torch.bfloat16)
-        logits = torch.empty((B, Ed), dtype=torch.bfloat16, device=dev)
-        wv = torch.empty((B, Kd + 1), dtype=torch.bfloat16, device=dev)
-        idv = torch.empty((B, Kd + 1), dtype=torch.int32, device=dev)
-        ws = fused_moe.get_workspace(B, Kd + 1, P + 1, Hd, Id, dev, tag=f"ds{B}")
-        out = torch.empty((B, Hd), dtype=torch.bfloat16, device=dev)
-
-        if path == native.LMOE_PATH_AUTO:
-            # decode: gate, selection and permutation (one launch for one
-            # token), then the GEMV body
-            def step():
-                fused_moe.decode_layer(x, gate, spec, w13, w2, l2p, workspace=ws, out=out, logits_out=logits,
-                                       w_out=wv, ids_out=idv)
-        else:
-            def step():
-                w, ids, _ = fused_moe.route(x, gate, spec, logits_out=logits, w_out=wv, ids_out=idv)
-                fused_moe.fused_experts(x, w, ids, w13, w2, l2p, out=out, workspace=ws, path=path)
-
-        return step, ws
+    res: dict = {"experts": {"routed": Ed, "shared": 1, "slots": P, "bytes_per_expert": per_expert}}
+    log(f"deepseek: weights {time.perf_counter() - t0:.1f}s")
 
     def timed(step, n):
         step()
@@ -860,22 +864,128 @@ def bench_deepseek(batches=(1, 8, 32), prefill_tokens: int = 2048, reps: int = 2
                 graph.replay()
         return t.ms() / n
 
+    # ---- resident: every expert in HBM, graph-replayed ----
+    resident: dict = {}
     for B in batches:
-        step, ws = make_step(B, native.LMOE_PATH_AUTO)
+        x = torch.randn((B, Hd), generator=g, device=dev).to(torch.bfloat16)
+        logits = torch.empty((B, Ed), dtype=torch.bfloat16, device=dev)
+        wv = torch.empty((B, Kd + 1), dtype=torch.bfloat16, device=dev)
+        idv = torch.empty((B, Kd + 1), dtype=torch.int32, device=dev)
+        ws = fused_moe.get_workspace(B, Kd + 1, NT, Hd, Id, dev, tag=f"ds{B}")
+        out = torch.empty((B, Hd), dtype=torch.bfloat16, device=dev)
+
+        def step():
+            fused_moe.decode_layer(x, gate, spec, w13, w2, l2p, workspace=ws, out=out, logits_out=logits,
+                                   w_out=wv, ids_out=idv)
+
         ms = timed(step, reps)
         U = int(ws.perm.meta[native.META_ACTIVE].item())
         byts = U * per_expert + Ed * Hd * 2 + 2 * B * Hd * 2
-        res[f"decode_B{B}"] = {"us_per_layer": round(ms * 1000, 2), "us_per_token": round(ms * 1000 / B, 2),
-                               "distinct_slots": U, "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1),
-                               "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        resident[f"decode_B{B}"] = {
+            "us_per_layer": round(ms * 1000, 2), "us_per_token": round(ms * 1000 / B, 2),
+            "distinct_experts": U, "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     T = prefill_tokens
-    step, ws = make_step(T, native.LMOE_PATH_MFMA)
-    ms = timed(step, 5)
+    x = torch.randn((T, Hd), generator=g, device=dev).to(torch.bfloat16)
+    logits = torch.empty((T, Ed), dtype=torch.bfloat16, device=dev)
+    wv = torch.empty((T, Kd + 1), dtype=torch.bfloat16, device=dev)
+    idv = torch.empty((T, Kd + 1), dtype=torch.int32, device=dev)
+    ws = fused_moe.get_workspace(T, Kd + 1, NT, Hd, Id, dev, tag=f"ds{T}")
+    out = torch.empty((T, Hd), dtype=torch.bfloat16, device=dev)
+
+    def pstep():
+        w, ids, _ = fused_moe.route(x, gate, spec, logits_out=logits, w_out=wv, ids_out=idv)
+        fused_moe.fused_experts(x, w, ids, w13, w2, l2p, out=out, workspace=ws, path=native.LMOE_PATH_MFMA)
+
+    ms = timed(pstep, 5)
+    U = int(ws.perm.meta[native.META_ACTIVE].item())
     flops = 2.0 * T * (Kd + 1) * 3 * Hd * Id + 2.0 * T * Hd * Ed
+    byts = U * per_expert + Ed * Hd * 2 + T * Hd * 2 * 2 + T * (Kd + 1) * Hd * 2 * 2
     tf = flops / (ms * 1e-3) / 1e12
-    res[f"prefill_T{T}"] = {"ms": round(ms, 3), "tflops": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)}
-    del w13, w2
+    resident[f"prefill_T{T}"] = {"ms": round(ms, 3), "tflops": round(tf, 1),
+                                 "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4), "distinct_experts": U,
+                                 "weight_bytes": U * per_expert,
+                                 "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    res["resident"] = resident
     fused_moe.clear_workspaces()
+    log(f"deepseek resident: {resident}")
+
+    # ---- staged: 64 slots, the routed experts in page-locked host memory ----
+    t0 = time.perf_counter()
+    h13 = torch.empty((Ed, 2 * Id, Hd), dtype=torch.bfloat16, pin_memory=True)
+    h2 = torch.empty((Ed, Hd, Id), dtype=torch.bfloat16, pin_memory=True)
+    for e in range(Ed):
+        h13[e].copy_(w13[e])
+        h2[e].copy_(w2[e])
+    rt = MoeOffloadRuntime(MoeOffloadConfig(enabled=True, num_slots=P, async_load=True, pin_host_memory=True,
+                                            graph_compatible_offload=True, decode_overflow=True,
+                                            b2_wave_prefill=True, device_wave_prefill=True))
+    rt.register_host_buffers(layer_id=0, w13_host=h13, w2_host=h2, slot_device=dev,
+                             shared_w13=w13[Ed:], shared_w2=w2[Ed:])
+    bank = rt.slot_bank(0)
+    log(f"deepseek: pinned host store {time.perf_counter() - t0:.1f}s")
+
+    def staged_step(x, phase):
+        """One layer step through the seam: route, stage op, experts; returns
+        (out, w, ids, branch, h2d bytes, distinct routed experts)."""
+        w, ids, _ = fused_moe.route(x, gate, spec)
+        owner = set(int(o) for o in rt.slot_owner_buffer(0).tolist())
+        bytes0 = rt.transfer_engine.bytes_issued
+        stage_topk_for_layer(rt, ids, 0, NT, phase)
+        routed = set(int(e) for e in ids[:, :Kd].unique().tolist())
+        if rt.consume_device_waves(layer_id=0, topk_ids=ids):
+            out = fused_moe.run_device_waves(rt, layer_id=0, hidden=x, topk_weights=w, topk_ids=ids,
+                                             num_logical_experts=NT)
+            branch, h2d = "device_waves", len(routed - owner) * per_expert
+        else:
+            ovf = rt.decode_overflow_slot_weights(layer_id=0, n_pairs=int(ids.numel()))
+            out, _ = fused_moe._fused_experts_ws(x, w, ids, bank.w13_slots, bank.w2_slots, rt.log2phy_buffer(0),
+                                                 overflow=ovf)
+            rt.record_layer_compute(0)
+            branch = "bank+overflow" if ovf is not None else "bank"
+            h2d = rt.transfer_engine.bytes_issued - bytes0
+        return out, w, ids, branch, h2d, len(routed)
+
+    def check(out, x, w, ids):
+        ref = fused_moe.fused_experts(x, w, ids, w13, w2, l2p)
+        d = (out.float() - ref.float()).abs().max().item()
+        rms = ref.float().pow(2).mean().sqrt().item()
+        return bool(torch.equal(out.view(torch.int16), ref.view(torch.int16))), d / max(rms, 1e-30)
+
+    staged: dict = {}
+    legs = [(f"decode_B{B}", B, PHASE_DECODE, n) for B, n in zip(batches, staged_steps)]
+    legs.append((f"prefill_T{T}", T, PHASE_PREFILL, prefill_steps))
+    for name, B, phase, n in legs:
+        x = torch.randn((B, Hd), generator=g, device=dev).to(torch.bfloat16)
+        staged_step(x, phase)  # warm: the bank fills, workspaces and stage buffers exist
+        torch.cuda.synchronize()
+        ms, h2d, distinct, branches, exact, err = [], 0, [], set(), True, 0.0
+        for i in range(n):
+            x = torch.randn((B, Hd), generator=g, device=dev).to(torch.bfloat16)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            out, w, ids, branch, hb, nd = staged_step(x, phase)
+            torch.cuda.synchronize()
+            ms.append((time.perf_counter() - t1) * 1000.0)
+            h2d += hb
+            distinct.append(nd)
+            branches.add(branch)
+            same, e = check(out, x, w, ids)
+            exact, err = exact and same, max(err, e)
+        mean_ms = sum(ms) / len(ms)
+        comp = resident.get(name, {})
+        comp_ms = comp.get("ms", comp.get("us_per_layer", 0.0) / 1000.0)
+        staged[name] = {
+            "ms_per_step": round(mean_ms, 3), "steps": n, "branches": sorted(branches),
+            "distinct_routed_experts_mean": round(sum(distinct) / len(distinct), 1),
+            "h2d_bytes_per_step": int(h2d / n), "h2d_gbs": round(h2d / n / (mean_ms * 1e-3) / 1e9, 1),
+            "resident_compute_ms": round(comp_ms, 3),
+            "bitwise_equal_to_resident": exact, "max_abs_err_over_rms_vs_resident": round(err, 6)}
+        log(f"deepseek staged {name}: {staged[name]}")
+    res["staged"] = staged
+    del rt, bank, h13, h2, w13, w2
+    fused_moe.clear_workspaces()
+    torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return res
 
@@ -884,13 +994,20 @@ def bench_deepseek(batches=(1, 8, 32), prefill_tokens: int = 2048, reps: int = 2
 # CPU baseline: the oracle of one layer on the host cores
 # ---------------------------------------------------------------------------
 def _cpu_model() -> str:
+    """The host CPU: model name plus family / model / stepping (a virtual
+    machine may report only a generic name), and the logical CPUs."""
+    fields: dict[str, str] = {}
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.lower().startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = line.split(":", 1)
+                fields.setdefault(k.strip().lower(), v.strip())
     except OSError:
         pass
-    return "unknown"
+    name = fields.get("model name", "unknown")
+    ident = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    extra = f"{ident}, " if ident else ""
+    return f"{name} ({extra}{os.cpu_count()} logical CPUs)"
 
 
 def bench_cpu_baseline(budget_s: float = 8.0) -> dict:
@@ -1093,6 +1210,12 @@ def main() -> int:
                             "bytes_per_launch": gu["bytes_per_launch"],
                             "distinct_slots_per_launch": roof["distinct_slots_per_launch"],
                             "down_combine_gemv_kernel": roof["down_combine_gemv_kernel"]}
+        if b1.get("layer_hbm_gbs"):
+            # the headline's own fraction: the whole layer's algorithmic
+            # bytes over its graph-replayed time (value)
+            line["roofline"]["layer"] = {"bytes": b1.get("algorithmic_bytes_per_layer"),
+                                         "us": b1.get("us_per_layer"), "achieved": b1["layer_hbm_gbs"],
+                                         "frac": b1.get("layer_hbm_frac")}
         traffic_file = ROOT / "profiles" / "gateup_gemv_decode_b1_traffic.json"
         if traffic_file.exists():
             try:

@@ -158,6 +158,17 @@ def fused_experts(
                              path=path, workspace=workspace)[0]
 
 
+def _pass_path(n_pairs: int, I: int, path: int) -> int:
+    """The MLP path of one pass of a multi-pass layer, by the rule the
+    single-pass layer uses (fused_experts): the decode GEMVs up to
+    FUSED_DECODE_MAX_PAIRS pairs (and I <= GEMV_MAX_I), MFMA tiles past
+    that, so a split layer gives the unsplit layer's bits."""
+    if path != native.LMOE_PATH_AUTO:
+        return path
+    return native.LMOE_PATH_GEMV if n_pairs <= native.FUSED_DECODE_MAX_PAIRS and I <= native.GEMV_MAX_I \
+        else native.LMOE_PATH_MFMA
+
+
 def _overflow_pass(hidden, topk_ids, k: int, overflow: PreparedSlotWeights, ws: MoEWorkspace, *, decode: bool):
     """Second pass of a decode step whose routed experts exceed the bank:
     the pairs the overflow table maps (every other pair is skipped) run from
@@ -625,7 +636,8 @@ def run_wave_prefill(
                                table_len=total_logical if first else routed,
                                block_m=native.prefill_block_m(len(plan.waves[w]), H, I, hidden.device, n_pairs=T * k))
                 first = False
-                native.grouped_mlp(hidden, k, prepared.w1, prepared.w2, ws.perm, ws.act[: T * k], ws.y[: T * k], path=path)
+                native.grouped_mlp(hidden, k, prepared.w1, prepared.w2, ws.perm, ws.act[: T * k], ws.y[: T * k],
+                                   path=_pass_path(T * k, I, path))
             finally:
                 runtime.end_slot_compute(handle)
             if buf is not None:
@@ -812,7 +824,7 @@ def run_device_waves(
         compute.wait_event(ready)
         native.permute(topk_ids, ws.perm, log2phy=table, skip_unmapped=True, keep_rows=w > 0, block_m=bm)
         native.grouped_mlp(hidden, k, stage.w13_slots, stage.w2_slots, ws.perm, ws.act[: T * k], ws.y[: T * k],
-                           path=path)
+                           path=_pass_path(T * k, I, path))
         done = torch.cuda.Event()
         done.record(compute)
         released[b] = done

@@ -480,29 +480,49 @@ class MoeOffloadRuntime:
         )
 
     def register_host_buffers(self, *, layer_id: int, w13_host: torch.Tensor, w2_host: torch.Tensor,
-                              slot_device: torch.device) -> None:
+                              slot_device: torch.device, shared_w13: torch.Tensor | None = None,
+                              shared_w2: torch.Tensor | None = None) -> None:
         """Register a layer whose routed experts already sit in host buffers
         ([E, 2I, H] / [E, H, I], ideally page-locked): no device copy of the
         full layer is ever made, the buffers become the host store as they are
-        (the CPU-first loading path, cpu_first_loader.py:40-177)."""
+        (the CPU-first loading path, cpu_first_loader.py:40-177).  shared_w13 /
+        shared_w2 ([S, 2I, H] / [S, H, I], any device) are fused shared
+        experts: pinned suffix rows of the slot bank with logical ids
+        E .. E+S-1, as a mix-placement layer registers them
+        (slot_bank.py:98-115)."""
         layer_id = int(layer_id)
         if layer_id in self._graph_slot_address_fingerprints:
             raise RuntimeError(f"layer {layer_id} fixed-slot addresses are already captured")
+        if (shared_w13 is None) != (shared_w2 is None):
+            raise ValueError("shared_w13 and shared_w2 go together")
         holder = torch.nn.Module()
         holder.layer_id = layer_id
         holder.w13_weight = w13_host
         holder.w2_weight = w2_host
         setattr(holder, CPU_FIRST_MARKER, True)
         E = int(w13_host.shape[0])
+        S = 0 if shared_w13 is None else int(shared_w13.shape[0])
+        if S and (tuple(shared_w13.shape[1:]) != tuple(w13_host.shape[1:]) or
+                  tuple(shared_w2.shape[1:]) != tuple(w2_host.shape[1:]) or int(shared_w2.shape[0]) != S):
+            raise ValueError("fused shared experts must have the routed experts' shape")
         self._host_store.register_layer(holder, pin_memory=False, clone_tensors=False, routed_expert_count=E)
         self._original_expert_weight_bytes_by_layer[layer_id] = 0
         self._released_original_weight_layers.discard(layer_id)
         self._expert_weight_bytes_by_layer[layer_id] = _nbytes(w13_host[0]) + _nbytes(w2_host[0])
+        pinned_ids = tuple(range(E, E + S))
         bank = ExpertSlotBank(self.config.num_slots, tuple(int(d) for d in w13_host.shape[1:]),
-                              tuple(int(d) for d in w2_host.shape[1:]), dtype=w13_host.dtype, device=slot_device)
+                              tuple(int(d) for d in w2_host.shape[1:]), dtype=w13_host.dtype, device=slot_device,
+                              pinned_logical_ids=pinned_ids)
         self._slot_banks[layer_id] = bank
-        self._fused_shared_lane_layouts.pop(layer_id, None)
-        self._new_log2phy(layer_id, E, bank.num_dynamic_slots, slot_device)
+        if pinned_ids:
+            bank.install_pinned_weights(shared_w13, shared_w2)
+            self._fused_shared_lane_layouts[layer_id] = FusedSharedLaneLayout(E, S, pinned_ids)
+        else:
+            self._fused_shared_lane_layouts.pop(layer_id, None)
+        self._prefill_stage_banks.pop(layer_id, None)
+        table = self._new_log2phy(layer_id, E + S, bank.num_dynamic_slots, slot_device)
+        if pinned_ids:
+            bank.install_pinned_log2phy(table)
         self._log2phy_slot_by_expert[layer_id] = {}
         self._full_residency_layers.discard(layer_id)
         self._memory_ledger_cache = None

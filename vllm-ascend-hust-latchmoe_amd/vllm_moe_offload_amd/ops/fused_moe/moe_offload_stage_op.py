@@ -6,8 +6,10 @@ counts the active experts, and either stages them into the fixed slots
 (runtime.stage_fixed_slot_plan: H2D on the transfer stream, consumer wait,
 in-place log2phy), or, for a decode-sized batch whose union exceeds the slots
 by at most the slot count (with decode_overflow on), stages the bank plus one
-overflow pass, or, when the union exceeds the slot capacity otherwise in a
-known phase, defers to the wave executor and caches the histogram for it.  It
+overflow pass; a decode-sized union past that goes to the device-planned
+waves when the layer has them; when the union exceeds the slot capacity
+otherwise in a known phase, it defers to the wave executor and caches the
+histogram for it.  It
 returns nothing and declares topk_ids mutated so the MLP piece reads the
 router's tensor at its captured address.
 
@@ -139,6 +141,14 @@ def stage_topk_for_layer(runtime, topk_ids: torch.Tensor, layer_id: int, num_log
                                       token_counts=counts)
         if os.environ.get("LATCHMOE_SEAM_PROBE"):
             print(f"LATCHMOE_SEAM branch=decode_overflow layer={layer_id} n_active={n_active}", flush=True)
+        return
+    if over and decode_sized and not is_moe_offload_adaptive_wave_context() and runtime.can_run_device_waves(layer_id):
+        # past what one overflow pass holds: the device-planned waves, a
+        # fixed number of launches with no host step, so the decode MLP piece
+        # stays capturable
+        runtime.mark_device_waves(layer_id=layer_id, topk_ids=topk_ids)
+        if os.environ.get("LATCHMOE_SEAM_PROBE"):
+            print(f"LATCHMOE_SEAM branch=decode_device_waves layer={layer_id} n_active={n_active}", flush=True)
         return
     defer = (known and runtime.should_use_b2_pair_waves(layer_id=layer_id, active_expert_count=n_active)) or (
         runtime.config.b2_wave_prefill and phase == PHASE_UNKNOWN and hint > 0 and tokens > hint and over
