@@ -1227,17 +1227,17 @@ def main() -> int:
     if args.out:
         Path(args.out).write_text(text + "\n")
     log(f"decode phase {t_decode:.1f}s total")
-    # free page-locked and device memory while the runtime is still up (a
-    # profiler that shuts the runtime down first must not see it freed later)
-    import gc
-
-    from vllm_moe_offload_amd import fused_moe
-
+    # return page-locked and device memory while the runtime is fully up: a
+    # page-locked block left in torch's host cache would be freed by the
+    # allocator's destructor in static teardown, after a profiler attached to
+    # the runtime may have shut down
     del host_w13, host_w2
-    fused_moe.clear_workspaces()
-    gc.collect()
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
+    before = dict(torch.cuda.host_memory_stats()) if hasattr(torch.cuda, "host_memory_stats") else {}
+    after = native.release_device_resources()
+    log("page-locked host cache: reserved "
+        f"{before.get('reserved_bytes.current', before.get('segment.current', 'n/a'))} -> "
+        f"{after.get('reserved_bytes.current', after.get('segment.current', 'n/a'))} "
+        f"(keys {sorted(k for k in after if 'current' in k)[:6]})")
     return 0
 
 

@@ -230,6 +230,12 @@ def _with_shared(counts: dict[int, int], layer: SlotMoELayer) -> dict[int, int]:
 _CONST: dict[tuple, torch.Tensor] = {}
 
 
+def clear_constants() -> None:
+    """Drop the cached constant tensors (ones / zeros of the separate shared
+    expert pass)."""
+    _CONST.clear()
+
+
 def _ones_bf16(T: int, device) -> torch.Tensor:
     key = ("ones", T, str(device))
     if key not in _CONST:

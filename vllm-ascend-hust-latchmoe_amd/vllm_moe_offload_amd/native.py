@@ -10,6 +10,7 @@ The C declarations live in include/latchmoe.h; `EXPORTED_SYMBOLS` lists them.
 
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
 from dataclasses import dataclass
@@ -157,7 +158,44 @@ def load_library() -> ctypes.CDLL:
         fn.restype = restype
         fn.argtypes = argtypes
     _LIB = lib
+    atexit.register(release_device_resources)
     return lib
+
+
+def release_device_resources() -> dict:
+    """Drop every device and page-locked buffer this package holds and
+    return them to the HIP runtime while it is fully up: the workspace and
+    constant caches, the runtime singleton (slot banks, stage banks, host
+    store, events), then torch's device cache and its page-locked host cache.
+    Registered with atexit when the library loads, so it runs at the start of
+    interpreter shutdown: a page-locked block still cached there would be
+    freed only by torch's allocator destructor during C++ static teardown,
+    after tools attached to the runtime (a profiler's memory-copy tracing) may
+    already have shut down.  Returns torch's host-allocator statistics after
+    the release (empty when unavailable).  Safe to call more than once."""
+    import gc
+
+    from vllm_moe_offload_amd import fused_moe, layer
+    from vllm_moe_offload_amd.moe_offload import runtime
+
+    fused_moe.clear_workspaces()
+    layer.clear_constants()
+    runtime.reset_moe_offload_runtime()
+    gc.collect()
+    stats: dict = {}
+    try:
+        if torch.cuda.is_available() and torch.cuda.is_initialized():
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            empty_host = getattr(torch._C, "_host_emptyCache", None)
+            if empty_host is not None:
+                empty_host()
+            host_stats = getattr(torch.cuda, "host_memory_stats", None)
+            if host_stats is not None:
+                stats = dict(host_stats())
+    except RuntimeError:
+        pass  # a device that already failed has nothing left to return
+    return stats
 
 
 def _check(status: int, fn: str) -> None:
