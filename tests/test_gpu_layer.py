@@ -675,3 +675,84 @@ def test_decode_overflow_buffers_shared_by_layers_under_seam_replays():
                                           rt_b.log2phy_buffer(200 + l))
             torch.cuda.synchronize()
             assert torch.equal(out_a[l].view(torch.int16), ref.view(torch.int16)), (step, l)
+
+
+def test_c2_b64_qwen_shape_overflow_pass_equals_full_bank_eager_and_replayed():
+    """The C2 batch of 64 tokens at the Qwen3 shape (E 128, H 2048, I 768,
+    top-8) with a Zipf-skewed router, on the configuration's 64-slot bank:
+    a step runs the bank pass plus the overflow pass (stage buffer) when its
+    union passes 64 experts.  Eager and replayed from a graph captured once,
+    every step equals a 128-slot bank bit for bit, and the first step matches
+    the oracle within 2e-2 x RMS."""
+    fused_moe, SlotMoELayer, Cfg, Runtime = _mods()
+    rng = np.random.default_rng(64)
+    E, H, I, k, T = 128, 2048, 768, 8, 64
+    w13, w2, wg = _weights(rng, E, H, I)
+    t13 = torch.from_numpy(w13.view(np.int16)).view(torch.bfloat16)
+    t2 = torch.from_numpy(w2.view(np.int16)).view(torch.bfloat16)
+    gate = to_dev_bf16(wg)
+    ranks = rng.permutation(E) + 1
+    logp = -1.1 * np.log(ranks.astype(np.float64))
+    lo = -1.1 * np.log(E)
+    bias = torch.tensor((-2.0 + 4.0 * (logp - lo) / (0.0 - lo)).astype(np.float32), device="cuda")
+    common = dict(enabled=True, async_load=True, pin_host_memory=True, graph_compatible_offload=True)
+    rt_a = Runtime(Cfg(num_slots=64, decode_overflow=True, **common))
+    rt_b = Runtime(Cfg(num_slots=128, **common))
+    la = SlotMoELayer(layer_id=110, runtime=rt_a, gate_weight=gate, w13_weight=t13, w2_weight=t2, top_k=k,
+                      gate_bias=bias)
+    lb = SlotMoELayer(layer_id=111, runtime=rt_b, gate_weight=gate, w13_weight=t13, w2_weight=t2, top_k=k,
+                      gate_bias=bias)
+    la.register()
+    lb.register()
+    spec = la.router_spec
+    dev = torch.device("cuda")
+    ws_a = fused_moe.get_workspace(T, k, 64, H, I, dev, tag="b64_a")
+    ws_b = fused_moe.get_workspace(T, k, 128, H, I, dev, tag="b64_b")
+    static_x = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    out_a = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+
+    def stage(rt, layer_id, x):
+        w, ids, _ = fused_moe.route(x, gate, spec)
+        flat = ids.cpu().flatten().tolist()
+        counts = {e: flat.count(e) for e in set(flat)}
+        rt.stage_fixed_slot_plan(layer_id=layer_id, active_experts=tuple(sorted(counts)), num_logical_experts=E,
+                                 token_counts=counts)
+        return len(counts)
+
+    def run_a():
+        ovf = rt_a.decode_overflow_slot_weights(layer_id=110, n_pairs=T * k)
+        fused_moe.decode_layer(static_x, gate, spec, rt_a.slot_bank(110).w13_slots, rt_a.slot_bank(110).w2_slots,
+                               rt_a.log2phy_buffer(110), workspace=ws_a, out=out_a, overflow=ovf)
+
+    graph = None
+    n_active = []
+    for step in range(5):
+        x = normal_bf16(rng, (T, H), 1.0)
+        dx = to_dev_bf16(x)
+        static_x.copy_(dx)
+        n_active.append(stage(rt_a, 110, dx))
+        print(f"case C2 B=64 step {step}: {n_active[-1]} experts", flush=True)
+        if graph is None:
+            run_a()
+        else:
+            graph.replay()
+        rt_a.record_layer_compute(110)
+        stage(rt_b, 111, dx)
+        out_b, w_b, ids_b = fused_moe.decode_layer(dx, gate, spec, rt_b.slot_bank(111).w13_slots,
+                                                   rt_b.slot_bank(111).w2_slots, rt_b.log2phy_buffer(111),
+                                                   workspace=ws_b)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)), step
+        if step == 0:
+            ref = _oracle_layer(x, ids_b.cpu().numpy(), from_dev_bf16(w_b), w13, w2)
+            assert rel_max_err(bf16_to_f32(from_dev_bf16(out_a)), ref) <= OUT_TOL
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                run_a()
+            torch.cuda.current_stream().wait_stream(s)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                run_a()
+            rt_a.record_layer_compute(110)
+    assert max(n_active) > 64, n_active  # steps past the bank ran the overflow pass
