@@ -184,7 +184,8 @@ int lmoe_router_topk_permute(const void* logits, int logits_f32, int T, int E,
  * LMOE_ROUTER_SYNC_WORDS int32, 8-byte aligned, zero before the first call;
  * it serves one permutation (one meta), and calls that may run concurrently
  * need separate sync buffers.
- * Returns LMOE_ERR_SHAPE when T > 16, E > 256, n_slots > 8192, H % 8 != 0,
+ * Returns LMOE_ERR_SHAPE when T > 16, T > 1 with H > 2048 (long rows: one
+ * token only), E > 256, n_slots > 8192, H % 8 != 0,
  * H > 8192, x / wg are not 16-byte aligned or sync is not 8-byte aligned
  * (then use the separate calls). */
 int lmoe_router_gate_topk_permute(const void* x, const void* wg, int T, int H,

@@ -164,7 +164,8 @@ def test_decode_layer_equals_route_then_fused_experts(T):
     (4, 128, 8, 64, 2048, "softmax", True),
     (16, 128, 8, 128, 2048, "softmax", False),   # 1024-thread blocks, block permutation
     (3, 60, 4, 16, 512, "softmax", False),       # E not a multiple of the waves per block
-    (8, 256, 8, 128, 7168, "sigmoid", False),    # grouped sigmoid, long rows
+    (1, 256, 8, 128, 7168, "sigmoid", False),    # grouped sigmoid, long rows (one token only)
+    (8, 256, 8, 128, 2048, "sigmoid", False),    # grouped sigmoid, several tokens
 ])
 def test_gate_select_permute_one_launch_equals_separate_calls(T, E, k, P, H, scoring, f32):
     """lmoe_router_gate_topk_permute == lmoe_router_gate then

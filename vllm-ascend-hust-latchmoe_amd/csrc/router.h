@@ -18,6 +18,10 @@
 namespace lmoe {
 
 constexpr int kGateMaxChunks = 16;  // H <= 16 * 512 = 8192 in the GEMV path
+constexpr int kGateShortChunks = 4;  // the one-launch router's short-row gate: H <= 2048
+// threads of every one-token one-launch router: the gate form's eight gate
+// rows per block, which also covers the slot scan up to kMaxSlots / 16
+constexpr int kOneTokenRouterThreads = 512;
 // router gate at large T: 64-row x 128-expert tiles, 2 waves, 4-stage ring
 using DenseGateTile = SmallTile;
 constexpr int kGateTok = 4;         // tokens per reduction in the gate GEMV
@@ -251,7 +255,7 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
 // concurrently need separate sync buffers, and a sync buffer serves one
 // permutation (one meta).  ONE: T == 1.
 template <int NC, int EPL, int PPL, int SCORE, bool ONE>
-__global__ __launch_bounds__(1024) void gate_topk_permute_kernel(
+__global__ __launch_bounds__(ONE ? kOneTokenRouterThreads : 1024) void gate_topk_permute_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T, int H,
     void* __restrict__ logits, int logits_f32, SelectParams sp, float* __restrict__ w_f32,
     uint16_t* __restrict__ w_bf16, int32_t* __restrict__ ids,
@@ -447,8 +451,22 @@ int launch_gate_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
     if (a.sp.E <= 128) LMOE_GTP_Q(NC, 2); \
     else LMOE_GTP_Q(NC, 4);             \
   } while (0)
-  if (a.H <= 4 * 512) LMOE_GTP_E(4);
-  else LMOE_GTP_E(16);
+  // one-token launches run kOneTokenRouterThreads threads (the launch bound
+  // that gives the long-row gate its registers)
+  if (a.T == 1 && threads != kOneTokenRouterThreads) return LMOE_ERR_UNSUPPORTED;
+  if (a.H <= kGateShortChunks * 512) {
+    LMOE_GTP_E(4);
+  } else {
+    // long rows: one token only (the entry point refuses more)
+    if (a.T != 1) return LMOE_ERR_SHAPE;
+    if (a.sp.E <= 128) {
+      if (ppl == 1) LMOE_GTP(16, 2, 1, true);
+      else LMOE_GTP(16, 2, 0, true);
+    } else {
+      if (ppl == 1) LMOE_GTP(16, 4, 1, true);
+      else LMOE_GTP(16, 4, 0, true);
+    }
+  }
 #undef LMOE_GTP_E
 #undef LMOE_GTP_Q
 #undef LMOE_GTP

@@ -214,6 +214,10 @@ extern "C" int lmoe_router_gate_topk_permute(
     return LMOE_ERR_SHAPE;
   // the last block holds the whole selection and permutation
   if (T > kFusedTopkTokens || E > 256 || n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
+  // rows past 2048 columns: one token only (the several-token forms of the
+  // long-row gate spill ~810 bytes per lane, and two launches are faster
+  // above one token anyway)
+  if (T > 1 && H > kGateShortChunks * 512) return LMOE_ERR_SHAPE;
   // an empty batch still builds its (empty) permutation
   if (T == 0)
     return lmoe_permute(nullptr, 0, log2phy, n_log2phy, n_slots, skip_unmapped, block_m, counts,
