@@ -393,20 +393,30 @@ def test_mfma_tile_heights_agree_bitwise(T, k, E, P, H, I, skip):
     assert frac <= 1e-3 * max(1.0, H / 2048) and max_ulps <= 2.0
 
 
-@pytest.mark.parametrize("T,E,P", [
-    (2048, 64, 64),    # 384 gate-up units on 256 CUs: one or two per workgroup
-    (4096, 128, 128),  # the full Qwen3-shaped layer: three units per workgroup
-    (1400, 128, 42),   # a 42-slot wave: one unit per workgroup, some idle
+@pytest.mark.parametrize("T,E,P,skew", [
+    (2048, 64, 64, False),    # 384 gate-up units on 256 CUs: one or two per workgroup
+    (4096, 128, 128, False),  # the full Qwen3-shaped layer: three units per workgroup
+    (1400, 128, 42, False),   # a 42-slot wave: one unit per workgroup, some idle
+    (2048, 128, 128, True),   # skewed routing: slots of < 128 pairs (three-stage units) beside wide ones
 ])
-def test_block_range_kernel_equals_tile_grid_at_prefill_sizes(T, E, P):
+def test_block_range_kernel_equals_tile_grid_at_prefill_sizes(T, E, P, skew):
     """The 320-row block-range GEMM over several rounds of units against the
     256-row tile grid, bit for bit (the 256-row kernel is held to the oracle
-    above; an oracle pass at these sizes would take minutes)."""
+    above; an oracle pass at these sizes would take minutes).  Row tiles of
+    at most 128 rows run the three-stage geometry, larger ones the 320-row
+    one; the skewed case mixes both in one launch."""
     native = _native()
     k, H, I = 8, 2048, 768
-    print(f"case block-range T={T} E={E} P={P}", flush=True)
+    print(f"case block-range T={T} E={E} P={P} skew={skew}", flush=True)
     rng = np.random.default_rng(T + P)
-    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    if skew:
+        pz = 1.0 / np.arange(1, E + 1) ** 0.9
+        pz = pz / pz.sum()
+        ids = np.stack([rng.choice(E, size=k, replace=False, p=pz) for _ in range(T)]).astype(np.int32)
+        counts = np.bincount(ids.reshape(-1), minlength=E)
+        assert (counts[counts > 0] <= 128).any() and (counts > 128).any() and (counts > 320).any()
+    else:
+        ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
     l2p = np.full(E, -1, dtype=np.int32)
     l2p[rng.permutation(E)[:P]] = np.arange(P, dtype=np.int32)
     g = torch.Generator(device="cuda").manual_seed(T)
