@@ -375,12 +375,11 @@ __device__ __forceinline__ float exp_nonpos(float x) {
 
 __device__ __forceinline__ float sigmoid_det(float x) {
 #pragma clang fp contract(off)
-  if (x >= 0.0f) {
-    const float e = exp_nonpos(-x);
-    return 1.0f / (1.0f + e);
-  }
-  const float e = exp_nonpos(x);
-  return e / (1.0f + e);
+  // 1 / (1 + exp(-x)) for x >= 0, exp(x) / (1 + exp(x)) below, without a
+  // branch: one exp and one division per value whichever side each lane is on
+  const bool pos = x >= 0.0f;
+  const float e = exp_nonpos(pos ? -x : x);
+  return (pos ? 1.0f : e) / (1.0f + e);
 }
 
 __device__ __forceinline__ float silu_f32(float g) {

@@ -50,6 +50,17 @@ struct SelectLds {
   float gsc[kWave];
 };
 
+// Largest v over the aligned block of 2^lg2 lanes that holds this lane
+// (every lane of the block ends with it); lg2 in [1, 6].
+__device__ __forceinline__ float block_max_lanes(float v, int lg2) {
+  if (lg2 >= 6) v = xor_step<32>(v, MaxOp{});
+  if (lg2 >= 5) v = xor_step<16>(v, MaxOp{});
+  if (lg2 >= 4) v = xor_step<8>(v, MaxOp{});
+  if (lg2 >= 3) v = xor_step<4>(v, MaxOp{});
+  if (lg2 >= 2) v = xor_step<2>(v, MaxOp{});
+  return xor_step<1>(v, MaxOp{});
+}
+
 // (value desc, id asc) ordering used by every selection step.  Written
 // without short-circuit evaluation: as `a || (b && c)` the compiler emits a
 // divergent branch (and a separate LDS read and wait) per comparison, which
@@ -122,42 +133,63 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
     if (sp.n_group > 1) {
       const int ng = sp.n_group;
       const int gs = E / ng;
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) {
-        const int e = j * kWave + lane;
-        if (e < E) L.c_s[e] = sel[j];
-      }
-      wave_lds_sync();
       // group score = best + second best selection score of the group
       float gscore = -INFINITY;
-      if (lane < ng) {
-        float m1 = -INFINITY, m2 = -INFINITY;
-        int i = 0;
-        for (; i + 4 <= gs; i += 4) {
-          float q[4];
+      if (gs <= kWave && (gs & (gs - 1)) == 0) {
+        // groups of 2..64 experts are aligned lane blocks of one register:
+        // their two best scores by butterfly maxima in the block (a second
+        // copy of the best value is the second best), no table in LDS
+        const int lg2 = 31 - __builtin_clz(gs);
 #pragma unroll
-          for (int u = 0; u < 4; ++u) q[u] = L.c_s[lane * gs + i + u];
+        for (int j = 0; j < EPL; ++j) {
+          const float v = sel[j];
+          const float m1 = block_max_lanes(v, lg2);
+          const uint64_t first = static_cast<uint64_t>(lane & ~(gs - 1));
+          const uint64_t blk = (gs == kWave ? ~0ull : ((1ull << gs) - 1ull)) << first;
+          const int n_best = __popcll(__ballot(v == m1) & blk);
+          const float m2x = block_max_lanes(v == m1 ? -INFINITY : v, lg2);
+          const float gsum = m1 + (n_best >= 2 ? m1 : m2x);
+          const int g = (j * kWave + lane) >> lg2;
+          if ((lane & (gs - 1)) == 0 && g < ng) L.gsc[g] = gsum;
+        }
+        wave_lds_sync();
+        if (lane < ng) gscore = L.gsc[lane];
+      } else {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            if (q[u] > m1) {
-              m2 = m1;
-              m1 = q[u];
-            } else if (q[u] > m2) {
-              m2 = q[u];
+        for (int j = 0; j < EPL; ++j) {
+          const int e = j * kWave + lane;
+          if (e < E) L.c_s[e] = sel[j];
+        }
+        wave_lds_sync();
+        if (lane < ng) {
+          float m1 = -INFINITY, m2 = -INFINITY;
+          int i = 0;
+          for (; i + 4 <= gs; i += 4) {
+            float q[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) q[u] = L.c_s[lane * gs + i + u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              if (q[u] > m1) {
+                m2 = m1;
+                m1 = q[u];
+              } else if (q[u] > m2) {
+                m2 = q[u];
+              }
             }
           }
-        }
-        for (; i < gs; ++i) {
-          const float v = L.c_s[lane * gs + i];
-          if (v > m1) {
-            m2 = m1;
-            m1 = v;
-          } else if (v > m2) {
-            m2 = v;
+          for (; i < gs; ++i) {
+            const float v = L.c_s[lane * gs + i];
+            if (v > m1) {
+              m2 = m1;
+              m1 = v;
+            } else if (v > m2) {
+              m2 = v;
+            }
           }
+          gscore = m1 + m2;
+          L.gsc[lane] = gscore;
         }
-        gscore = m1 + m2;
-        L.gsc[lane] = gscore;
       }
       wave_lds_sync();
       // keep the topk_group best groups (ties to the lower group id)
@@ -165,10 +197,14 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
 #pragma unroll 8
       for (int g = 0; g < ng; ++g) r += better(L.gsc[g], g, gscore, lane) ? 1 : 0;
       const uint64_t kept = __ballot(lane < ng && r < sp.topk_group);
+      // group of expert e: e / gs (a shift for the power-of-two sizes)
+      const bool pow2 = (gs & (gs - 1)) == 0;
+      const int sh = pow2 ? 31 - __builtin_clz(gs) : 0;
 #pragma unroll
       for (int j = 0; j < EPL; ++j) {
         const int e = j * kWave + lane;
-        elig[j] = (e < E) && ((kept >> (e / gs)) & 1ull);
+        const int g = pow2 ? (e >> sh) : e / gs;
+        elig[j] = (e < E) && ((kept >> g) & 1ull);
       }
       wave_lds_sync();  // the scratch may be reused by the next token
     }
