@@ -50,15 +50,48 @@ struct SelectLds {
   float gsc[kWave];
 };
 
-// Largest v over the aligned block of 2^lg2 lanes that holds this lane
-// (every lane of the block ends with it); lg2 in [1, 6].
-__device__ __forceinline__ float block_max_lanes(float v, int lg2) {
-  if (lg2 >= 6) v = xor_step<32>(v, MaxOp{});
-  if (lg2 >= 5) v = xor_step<16>(v, MaxOp{});
-  if (lg2 >= 4) v = xor_step<8>(v, MaxOp{});
-  if (lg2 >= 3) v = xor_step<4>(v, MaxOp{});
-  if (lg2 >= 2) v = xor_step<2>(v, MaxOp{});
-  return xor_step<1>(v, MaxOp{});
+// Order-preserving 32-bit key of a score: key(a) > key(b) <=> a > b, -0
+// made +0 first (so equal scores have equal keys); score_of_key inverts it.
+__device__ __forceinline__ uint32_t score_key(float v) {
+  const uint32_t u = __float_as_uint(v + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float score_of_key(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+// Largest key over the aligned block of 2^LG lanes that holds this lane
+// (every lane of the block ends with it).
+template <int LG>
+__device__ __forceinline__ uint32_t block_max_key(uint32_t v) {
+  if constexpr (LG >= 6) v = umax32(v, __float_as_uint(lane_xor<32>(__uint_as_float(v))));
+  if constexpr (LG >= 5) v = umax32(v, __float_as_uint(lane_xor<16>(__uint_as_float(v))));
+  if constexpr (LG >= 4) v = umax32(v, __float_as_uint(lane_xor<8>(__uint_as_float(v))));
+  if constexpr (LG >= 3) v = umax32(v, __float_as_uint(lane_xor<4>(__uint_as_float(v))));
+  if constexpr (LG >= 2) v = umax32(v, __float_as_uint(lane_xor<2>(__uint_as_float(v))));
+  return umax32(v, __float_as_uint(lane_xor<1>(__uint_as_float(v))));
+}
+
+// Group scores (best + second best selection score) of groups of 2^LG
+// experts, which are aligned lane blocks of one register: butterfly maxima
+// over the blocks' keys, a second copy of the best counting as the second
+// best.  The score of group g goes to gsc[g] (g < ng).
+template <int LG, int EPL>
+__device__ __forceinline__ void group_scores_pow2(const float (&sel)[EPL], int ng, float* gsc) {
+  constexpr int GS = 1 << LG;
+  const int lane = threadIdx.x & 63;
+  const uint64_t blk = (GS == kWave ? ~0ull : ((1ull << GS) - 1ull)) << (lane & ~(GS - 1));
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const uint32_t key = score_key(sel[j]);
+    const uint32_t k1 = block_max_key<LG>(key);
+    const int n_best = __popcll(__ballot(key == k1) & blk);
+    const uint32_t k2 = block_max_key<LG>(key == k1 ? 0u : key);
+    const float m1 = score_of_key(k1);
+    const float gsum = m1 + (n_best >= 2 ? m1 : score_of_key(k2));
+    const int g = (j * kWave + lane) >> LG;
+    if ((lane & (GS - 1)) == 0 && g < ng) gsc[g] = gsum;
+  }
 }
 
 // (value desc, id asc) ordering used by every selection step.  Written
@@ -135,23 +168,13 @@ __device__ __forceinline__ void select_token(const SelectParams& sp,
       const int gs = E / ng;
       // group score = best + second best selection score of the group
       float gscore = -INFINITY;
-      if (gs <= kWave && (gs & (gs - 1)) == 0) {
-        // groups of 2..64 experts are aligned lane blocks of one register:
-        // their two best scores by butterfly maxima in the block (a second
-        // copy of the best value is the second best), no table in LDS
-        const int lg2 = 31 - __builtin_clz(gs);
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-          const float v = sel[j];
-          const float m1 = block_max_lanes(v, lg2);
-          const uint64_t first = static_cast<uint64_t>(lane & ~(gs - 1));
-          const uint64_t blk = (gs == kWave ? ~0ull : ((1ull << gs) - 1ull)) << first;
-          const int n_best = __popcll(__ballot(v == m1) & blk);
-          const float m2x = block_max_lanes(v == m1 ? -INFINITY : v, lg2);
-          const float gsum = m1 + (n_best >= 2 ? m1 : m2x);
-          const int g = (j * kWave + lane) >> lg2;
-          if ((lane & (gs - 1)) == 0 && g < ng) L.gsc[g] = gsum;
-        }
+      const int lg2 = 31 - __builtin_clz(gs);
+      if (gs == (1 << lg2) && lg2 >= 4 && lg2 <= 6) {
+        // groups of 16, 32 or 64 experts (DeepSeek-V3: 256 experts in 8
+        // groups of 32) are aligned lane blocks of one register
+        if (lg2 == 5) group_scores_pow2<5>(sel, ng, L.gsc);
+        else if (lg2 == 4) group_scores_pow2<4>(sel, ng, L.gsc);
+        else group_scores_pow2<6>(sel, ng, L.gsc);
         wave_lds_sync();
         if (lane < ng) gscore = L.gsc[lane];
       } else {
