@@ -60,35 +60,43 @@ __device__ __forceinline__ float score_of_key(uint32_t o) {
   return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
 }
 
-// Largest key over the aligned block of 2^LG lanes that holds this lane
-// (every lane of the block ends with it).
+// One top-two merge step with the lane M apart: (a1 >= a2) and the
+// partner's (b1 >= b2) become the two largest of the four.
+template <int M>
+__device__ __forceinline__ void top2_step(uint32_t& a1, uint32_t& a2) {
+  const uint32_t b1 = __float_as_uint(lane_xor<M>(__uint_as_float(a1)));
+  const uint32_t b2 = __float_as_uint(lane_xor<M>(__uint_as_float(a2)));
+  const uint32_t lo = a1 < b1 ? a1 : b1;
+  a1 = umax32(a1, b1);
+  a2 = umax32(lo, umax32(a2, b2));
+}
+
+// The two largest keys (a copy of the largest counts as the second) over
+// the aligned block of 2^LG lanes holding this lane; every lane of the block
+// ends with them.
 template <int LG>
-__device__ __forceinline__ uint32_t block_max_key(uint32_t v) {
-  if constexpr (LG >= 6) v = umax32(v, __float_as_uint(lane_xor<32>(__uint_as_float(v))));
-  if constexpr (LG >= 5) v = umax32(v, __float_as_uint(lane_xor<16>(__uint_as_float(v))));
-  if constexpr (LG >= 4) v = umax32(v, __float_as_uint(lane_xor<8>(__uint_as_float(v))));
-  if constexpr (LG >= 3) v = umax32(v, __float_as_uint(lane_xor<4>(__uint_as_float(v))));
-  if constexpr (LG >= 2) v = umax32(v, __float_as_uint(lane_xor<2>(__uint_as_float(v))));
-  return umax32(v, __float_as_uint(lane_xor<1>(__uint_as_float(v))));
+__device__ __forceinline__ void block_top2_key(uint32_t& a1, uint32_t& a2) {
+  if constexpr (LG >= 6) top2_step<32>(a1, a2);
+  if constexpr (LG >= 5) top2_step<16>(a1, a2);
+  if constexpr (LG >= 4) top2_step<8>(a1, a2);
+  if constexpr (LG >= 3) top2_step<4>(a1, a2);
+  if constexpr (LG >= 2) top2_step<2>(a1, a2);
+  top2_step<1>(a1, a2);
 }
 
 // Group scores (best + second best selection score) of groups of 2^LG
-// experts, which are aligned lane blocks of one register: butterfly maxima
-// over the blocks' keys, a second copy of the best counting as the second
-// best.  The score of group g goes to gsc[g] (g < ng).
+// experts, which are aligned lane blocks of one register: a top-two
+// butterfly over the blocks' keys.  The score of group g goes to gsc[g]
+// (g < ng).
 template <int LG, int EPL>
 __device__ __forceinline__ void group_scores_pow2(const float (&sel)[EPL], int ng, float* gsc) {
   constexpr int GS = 1 << LG;
   const int lane = threadIdx.x & 63;
-  const uint64_t blk = (GS == kWave ? ~0ull : ((1ull << GS) - 1ull)) << (lane & ~(GS - 1));
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    const uint32_t key = score_key(sel[j]);
-    const uint32_t k1 = block_max_key<LG>(key);
-    const int n_best = __popcll(__ballot(key == k1) & blk);
-    const uint32_t k2 = block_max_key<LG>(key == k1 ? 0u : key);
-    const float m1 = score_of_key(k1);
-    const float gsum = m1 + (n_best >= 2 ? m1 : score_of_key(k2));
+    uint32_t k1 = score_key(sel[j]), k2 = 0u;
+    block_top2_key<LG>(k1, k2);
+    const float gsum = score_of_key(k1) + score_of_key(k2);
     const int g = (j * kWave + lane) >> LG;
     if ((lane & (GS - 1)) == 0 && g < ng) gsc[g] = gsum;
   }
