@@ -271,10 +271,13 @@ __global__ __launch_bounds__(ONE ? kOneTokenRouterThreads : 1024) void gate_topk
   const int nw = blockDim.x >> 6;
   const int e = blockIdx.x * nw + (threadIdx.x >> 6);
   // every block copies the slot table while its gate rows load, so that the
-  // last one remaps the selected ids from LDS
-  const bool l2p_in_lds = log2phy != nullptr && n_log2phy <= kMaxE;
-  if (l2p_in_lds)
-    for (int i = threadIdx.x; i < n_log2phy; i += blockDim.x) l2p_lds[i] = log2phy[i];
+  // last one remaps the selected ids from LDS (no table: the identity).  The
+  // selected ids are below E + n_shared <= kMaxE, so the first kMaxE entries
+  // cover them; the permutation then reads the table with LDS loads only,
+  // not with generic loads that would also wait for the global stores of
+  // the selection
+  const int n_tab = log2phy != nullptr ? min(n_log2phy, kMaxE) : min(sp.E + sp.n_shared, kMaxE);
+  for (int i = threadIdx.x; i < n_tab; i += blockDim.x) l2p_lds[i] = log2phy != nullptr ? log2phy[i] : i;
   // this launch's tag: the build it makes (every block reads the count
   // before it counts in, and the count advances only after the last one has)
   const uint32_t tag = static_cast<uint32_t>(__hip_atomic_load(
@@ -298,10 +301,9 @@ __global__ __launch_bounds__(ONE ? kOneTokenRouterThreads : 1024) void gate_topk
   }
   __syncthreads();
   if (!last) return;
-  select_and_permute<EPL, PPL, SCORE>(logits, logits_f32, T, sp, w_f32, w_bf16, ids,
-                                      l2p_in_lds ? l2p_lds : log2phy, n_log2phy, P, skip,
-                                      block_m, counts, offsets, sorted_pairs, row_idx, active,
-                                      tile_off, meta, hist, L, words, tag);
+  select_and_permute<EPL, PPL, SCORE>(logits, logits_f32, T, sp, w_f32, w_bf16, ids, l2p_lds,
+                                      n_tab, P, skip, block_m, counts, offsets, sorted_pairs,
+                                      row_idx, active, tile_off, meta, hist, L, words, tag);
 }
 
 inline int check_select(int T, int E, int k, int n_shared, int scoring, int n_group,
