@@ -66,12 +66,14 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     if (lane == 0) act[static_cast<size_t>(a) * I + i] = swiglu_bf16(tot, up);
     return;
   }
+  __shared__ uint16_t s_act[2][4];
   const int s = active[a];
-  if (s < 0) return;
+  if (s < 0) return;  // uniform over the block
   const int p0 = offsets[s];
   const int n = offsets[s + 1] - p0;
+  // I % 64 == 0 (the entry points check it), so every wave's row is < I and
+  // all four waves meet the barrier of every pair
   const int i = blockIdx.x * 4 + wave;
-  if (i >= I) return;
   const uint16_t* grow = w13 + (static_cast<size_t>(s) * 2 * I + i) * H;
   const uint16_t* urow = grow + static_cast<size_t>(I) * H;
   uint4 wg[NC], wu[NC];
@@ -95,7 +97,19 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     // lanes 0..31 end with the gate total, 32..63 with the up total
     const float tot = reduce_scatter<2, 5, 0>(v, lane);
     const float up = read_lane(tot, 32);  // lane 32 holds the up total
-    if (lane == 0) act[static_cast<size_t>(p0 + r) * I + i] = swiglu_bf16(tot, up);
+    // the block's four act values of this pair leave in one 8-byte store
+    // (B=16 80.7 -> 79.3, B=64 209 -> 204 us per layer against a 2-byte
+    // store per wave); s_act is double-buffered, so one barrier per pair
+    if (lane == 0) s_act[r & 1][wave] = swiglu_bf16(tot, up);
+    __syncthreads();
+    if (wave == 0 && lane == 0) {
+      const uint16_t* a4 = s_act[r & 1];
+      const uint32_t lo = a4[0] | (static_cast<uint32_t>(a4[1]) << 16);
+      const uint32_t hi = a4[2] | (static_cast<uint32_t>(a4[3]) << 16);
+      // I % 64 == 0: the four columns blockIdx.x * 4 .. + 3 are all < I
+      *reinterpret_cast<uint2*>(act + static_cast<size_t>(p0 + r) * I + blockIdx.x * 4) =
+          make_uint2(lo, hi);
+    }
   }
 }
 
