@@ -219,7 +219,12 @@ size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);
  * Outputs: counts[s]; offsets[s] = exclusive prefix of counts (offsets[P] =
  * placed pairs); sorted_pairs[offsets[s] + r] = the r-th pair of slot s in
  * flat order; row_idx[p] = sorted position of pair p or -1; active[a] = a-th
- * slot with count > 0 (ascending), -1 for a >= meta[LMOE_META_ACTIVE];
+ * slot with count > 0 in launch order, -1 for a >= meta[LMOE_META_ACTIVE]:
+ * first the heavy slots (count >= 16 and 16 * count >= placed pairs; at most
+ * 16) by descending count, ties by ascending slot, then the other slots with
+ * count > 0 in ascending slot order (the decode kernels give active rank a
+ * grid row a, so a hot slot starts first instead of ending the kernel late;
+ * no output depends on the order);
  * tile_off[s] = sum over s' < s of
  * ceil(counts[s'] / block_m); meta[LMOE_META_COUNT] (ACTIVE, PAIRS, ERRORS,
  * TILES; GEN advanced; the other words are not written).

@@ -18,6 +18,12 @@ microbatch vectors of tests/test_phase_split_b2.py:325-365 (restore tokens
 brute-force insertion sort over random small inputs; invariants
 (sorted_pairs is a permutation, row_idx its inverse, slots non-decreasing,
 flat order kept inside each slot).
+
+The active-slot list is this build's own launch order (the reference has
+no such list): a heavy slot (count >= 16 and 16 * count >= placed pairs)
+first, by descending count then ascending slot, then every other slot
+with count > 0 in ascending slot order.  Pinned by a brute-force pairwise
+check over random skewed counts (tests/test_oracle_core.py).
 """
 
 from __future__ import annotations
@@ -34,7 +40,7 @@ class OraclePermutation:
     offsets: np.ndarray       # [P+1]
     sorted_pairs: np.ndarray  # [placed]
     row_idx: np.ndarray       # [N] sorted position or -1
-    active: np.ndarray        # [num_active] ascending slots with count > 0
+    active: np.ndarray        # [num_active] slots with count > 0, launch order (active_order)
     tile_off: np.ndarray      # [P+1]
     errors: int
 
@@ -57,6 +63,22 @@ def remap(ids: np.ndarray, log2phy: np.ndarray | None, n_slots: int, *, skip_unm
     if skip_unmapped:
         out = np.where(s == -1, -1, out)
     return out.astype(np.int64)
+
+
+HEAVY_MIN_PAIRS = 16
+
+
+def active_order(counts: np.ndarray) -> np.ndarray:
+    """Slots with count > 0 in launch order: heavy slots (count >= 16 and
+    16 * count >= total) by descending count, ties ascending slot, then the
+    rest in ascending slot order."""
+    c = np.asarray(counts, dtype=np.int64)
+    placed = int(c.sum())
+    heavy = (c >= HEAVY_MIN_PAIRS) & (16 * c >= placed)
+    hs = np.nonzero(heavy)[0]
+    hs = hs[np.lexsort((hs, -c[hs]))]
+    light = np.nonzero((c > 0) & ~heavy)[0]
+    return np.concatenate([hs, light]).astype(np.int64)
 
 
 def init_routing(
@@ -86,7 +108,7 @@ def init_routing(
         offsets=offsets,
         sorted_pairs=order.astype(np.int64),
         row_idx=row_idx,
-        active=np.nonzero(counts > 0)[0].astype(np.int64),
+        active=active_order(counts),
         tile_off=tile_off,
         errors=int(np.count_nonzero(slot_of == -2)),
     )

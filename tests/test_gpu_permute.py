@@ -66,6 +66,34 @@ def test_permute_matches_oracle(T, k, E, P, use_map, block_m):
     _check(perm, orc.init_routing(ids, P, log2phy=log2phy, block_m=block_m), T * k)
 
 
+@pytest.mark.parametrize("N,P,s", [
+    (128, 128, 1.2),    # one wave
+    (256, 1024, 1.5),   # one wave, 16 slots per lane
+    (512, 128, 1.1),    # one block
+    (1024, 256, 1.3),   # one block, full chunk
+    (8192, 64, 1.3),    # multi-block
+    (16000, 1024, 1.0), # multi-block, scan over the table in global memory
+])
+def test_permute_heavy_first_order_matches_oracle(N, P, s):
+    """Zipf-skewed slots (plus a run of equal heavy counts): the active list
+    leads with the heavy slots, ties by slot, as the oracle orders them."""
+    native = _native()
+    print(f"case permute heavy-first N={N} P={P} s={s}", flush=True)
+    rng = np.random.default_rng(N + P)
+    pz = 1.0 / (rng.permutation(P) + 1.0) ** s
+    ids = rng.choice(P, size=N, p=pz / pz.sum()).astype(np.int32)
+    # four slots with the same heavy count: equal counts are ordered by slot
+    tie = max(8, N // 12)
+    ids[: 4 * tie] = np.repeat(rng.permutation(P)[:4], tie)
+    ids = ids.reshape(-1, 1)
+    for block_m in (128, 320):
+        perm = native.Permutation.allocate(N, P, "cuda")
+        native.permute(to_dev_i32(ids), perm, block_m=block_m)
+        ref = orc.init_routing(ids, P, block_m=block_m)
+        assert ((ref.counts >= orc.HEAVY_MIN_PAIRS) & (16 * ref.counts >= ref.placed)).sum() >= 2
+        _check(perm, ref, N)
+
+
 @pytest.mark.parametrize("N,P", [(64, 16), (200, 16), (5000, 40)])
 def test_permute_skip_unmapped_wave_filter(N, P):
     native = _native()

@@ -41,20 +41,27 @@ def _check_perm(native, perm, ref, n_pairs):
     assert meta[native.META_GEN] == perm.builds  # one per build
 
 
-@pytest.mark.parametrize("T,E,k,P,skip", [
-    (1, 128, 8, 64, False),
-    (4, 128, 8, 64, False),
-    (16, 128, 8, 64, False),
-    (16, 128, 8, 32, True),    # a wave table: ids outside it are left to another pass
-    (17, 128, 8, 128, False),  # past the one-block limit: the two-launch path
-    (3, 60, 4, 16, False),
+@pytest.mark.parametrize("T,E,k,P,skip,skew", [
+    (1, 128, 8, 64, False, False),
+    (4, 128, 8, 64, False, False),
+    (16, 128, 8, 64, False, False),
+    (16, 128, 8, 32, True, False),    # a wave table: ids outside it are left to another pass
+    (17, 128, 8, 128, False, False),  # past the one-block limit: the two-launch path
+    (3, 60, 4, 16, False, False),
+    # skewed gate bias: heavy slots lead the active list (one wave, one
+    # block of 512 and of 1024 pairs)
+    (16, 128, 8, 128, False, True),
+    (64, 128, 8, 128, False, True),
+    (128, 128, 8, 128, False, True),
 ])
-def test_softmax_select_and_permute_bit_exact(T, E, k, P, skip):
+def test_softmax_select_and_permute_bit_exact(T, E, k, P, skip, skew):
     native = _native()
-    print(f"case topk-permute softmax T={T} E={E} k={k} P={P} skip={skip}", flush=True)
+    print(f"case topk-permute softmax T={T} E={E} k={k} P={P} skip={skip} skew={skew}", flush=True)
     rng = np.random.default_rng(500 + T * 13 + P)
     bits = _tied_logits(rng, T, E)
     lbias = (rng.standard_normal(E) * 0.7).astype(np.float32)
+    if skew:  # Zipf-like: expert of rank r gets -1.5 log r
+        lbias = (-1.5 * np.log(rng.permutation(E) + 1.0)).astype(np.float32)
     cbias = (rng.standard_normal(E) * 0.004).astype(np.float32)
     r_ids, r_w, r_wb = orc.softmax_topk(bf16_to_f32(bits), k, bias=cbias, logit_bias=lbias)
     # slot table: every selected expert mapped (skip: only a subset)
@@ -73,6 +80,8 @@ def test_softmax_select_and_permute_bit_exact(T, E, k, P, skip):
     np.testing.assert_array_equal(from_dev_bf16(w), r_wb)
     np.testing.assert_array_equal(w_f32.cpu().numpy().view(np.uint32), r_w.view(np.uint32))
     ref = operm.init_routing(r_ids, P, log2phy=l2p, skip_unmapped=skip, block_m=native.MFMA_BLOCK_M)
+    if skew:  # the case exercises the heavy-first order
+        assert ((ref.counts >= operm.HEAVY_MIN_PAIRS) & (16 * ref.counts >= ref.placed)).sum() >= 2
     _check_perm(native, perm, ref, T * k)
     assert perm.block_m == native.MFMA_BLOCK_M
 

@@ -184,6 +184,53 @@ def test_wave_filter_golden_vector_of_reference():
     assert p.errors == 0
 
 
+def _check_launch_order(active, counts):
+    """Every listed pair of slots is in launch order, by a pairwise
+    comparator: heavy (>= 16 pairs and >= 1/16 of all) before light, heavy by
+    descending count then slot, light by slot."""
+    total = sum(counts)
+
+    def heavy(s):
+        return counts[s] >= 16 and 16 * counts[s] >= total
+
+    for i in range(len(active)):
+        for j in range(i + 1, len(active)):
+            a, b = active[i], active[j]
+            if heavy(a) != heavy(b):
+                assert heavy(a), (active, counts)
+            elif heavy(a):
+                assert counts[a] > counts[b] or (counts[a] == counts[b] and a < b), (active, counts)
+            else:
+                assert a < b, (active, counts)
+
+
+def test_active_launch_order_hand_vectors():
+    # 84 pairs: the 1/16 bound is 5.25, so count >= 16 decides
+    ids = np.repeat(np.arange(7), [0, 17, 3, 20, 17, 15, 12]).reshape(-1, 1)
+    assert operm.init_routing(ids, 7).active.tolist() == [3, 1, 4, 2, 5, 6]
+    # 400 pairs: 20 pairs are under 1/16 of them, 80 and 300 are not
+    ids = np.repeat(np.arange(3), [20, 300, 80]).reshape(-1, 1)
+    assert operm.init_routing(ids, 3).active.tolist() == [1, 2, 0]
+    # 200 pairs: 8 pairs are under the 16-pair bound, 42 and 150 are not
+    ids = np.repeat(np.arange(3), [8, 150, 42]).reshape(-1, 1)
+    assert operm.init_routing(ids, 3).active.tolist() == [1, 2, 0]
+    # one token, distinct slots: slot order (the one-token kernels use rank = position)
+    assert operm.init_routing(np.array([[5, 1, 7, 2]]), 8).active.tolist() == [1, 2, 5, 7]
+
+
+def test_active_launch_order_skewed_counts():
+    rng = np.random.default_rng(11)
+    for _ in range(200):
+        P = int(rng.integers(1, 200))
+        n = int(rng.integers(0, 600))
+        pz = 1.0 / np.arange(1, P + 1) ** rng.uniform(0.0, 2.0)
+        ids = rng.choice(P, size=n, p=pz / pz.sum()).reshape(-1, 1)
+        p = operm.init_routing(ids, P)
+        assert sorted(p.active.tolist()) == [s for s in range(P) if p.counts[s] > 0]
+        assert sum(1 for s in range(P) if p.counts[s] >= 16 and 16 * p.counts[s] >= n) <= 16
+        _check_launch_order(p.active.tolist(), p.counts.tolist())
+
+
 def test_init_routing_brute_force_and_invariants():
     rng = np.random.default_rng(6)
     for _ in range(300):
@@ -201,7 +248,8 @@ def test_init_routing_brute_force_and_invariants():
             else:
                 assert p.row_idx[i] == -1
         assert p.offsets[-1] == len(want)
-        assert p.active.tolist() == [s for s in range(P) if p.counts[s] > 0]
+        assert sorted(p.active.tolist()) == [s for s in range(P) if p.counts[s] > 0]
+        _check_launch_order(p.active.tolist(), p.counts.tolist())
         tiles = [math.ceil(c / 2) for c in p.counts]
         q = operm.init_routing(ids, P, block_m=2)
         assert q.tile_off.tolist() == [0] + list(itertools.accumulate(tiles))

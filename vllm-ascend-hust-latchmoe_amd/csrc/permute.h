@@ -85,27 +85,92 @@ __device__ int block_exclusive_scan(int v, int* scan_lds, int* total) {
   return excl;
 }
 
+// Launch order of the active-slot list.  The decode GEMVs give the a-th
+// active slot the a-th row of their grid, and the hardware dispatches rows in
+// order; a workgroup's time grows with its slot's pair count, so one hot slot
+// dispatched late ends the kernel long after the rest (one slot of 60 of 512
+// pairs: 35 us past the others).  A heavy slot, one holding at least 1/16 of
+// the placed pairs and at least kHeavyMinPairs of them, therefore comes
+// first, heaviest first (ties: ascending slot); every other active slot
+// follows in ascending slot order, which keeps light and moderately loaded
+// slots mixed (moving those forward as well measured 1-4% slower, and a
+// bound of 8 pairs cost the 16-token decode layer 1%).  The 1/16 bound
+// admits at most 16 heavy slots.  The order changes no output bits: every
+// kernel writes by sorted position, never by active rank.
+constexpr int kHeavyMinPairs = 16;
+constexpr int kMaxHeavy = 16;
+
+__device__ __forceinline__ bool heavy_slot(int count, int placed) {
+  return count >= kHeavyMinPairs && 16 * count >= placed;
+}
+
+// Order key of a heavy slot: a larger key is listed first (higher count,
+// then lower slot); never 0, the value of an empty entry of a key list.
+__device__ __forceinline__ uint64_t heavy_key(int count, int s) {
+  return (static_cast<uint64_t>(count) << 32) | (0xffffffffu - static_cast<uint32_t>(s));
+}
+
+// The same order in 32 bits, for count < 65536 and s < 65536.
+__device__ __forceinline__ uint32_t heavy_key16(int count, int s) {
+  return (static_cast<uint32_t>(count) << 16) | (0xffffu - static_cast<uint32_t>(s));
+}
+
+// Rank of key among the kMaxHeavy entries of an LDS key list (empty entries
+// 0): the reads are independent, so all of them are in flight at once.
+template <typename K>
+__device__ __forceinline__ int heavy_rank(const K* keys, K key) {
+  int rank = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxHeavy; ++j) rank += keys[j] > key;
+  return rank;
+}
+
 // Scan counts[0..P) held in LDS (hist) into offsets/active/tile_off; writes
-// counts, offsets, active, tile_off and meta[ACTIVE, PAIRS, TILES], and
-// replaces hist[s] by offsets[s] in place (each s is owned by one thread).
+// counts, offsets, active (in the launch order above), tile_off and
+// meta[ACTIVE, PAIRS, TILES], and replaces hist[s] by offsets[s] in place
+// (each s is owned by one thread).
 __device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
                            int32_t* counts, int32_t* offsets, int32_t* active,
                            int32_t* tile_off, int32_t* meta) {
+  // keys of the heavy slots in slot order, empty entries 0
+  __shared__ uint64_t heavy_keys[kMaxHeavy];
   const int per = (P + blockDim.x - 1) / blockDim.x;
   const int s0 = threadIdx.x * per;
-  int csum = 0, asum = 0, tsum = 0;
+  if (threadIdx.x < kMaxHeavy) heavy_keys[threadIdx.x] = 0;
+  int csum = 0, tsum = 0;
   for (int i = 0; i < per; ++i) {
     const int s = s0 + i;
     if (s < P) {
       const int c = hist[s];
       csum += c;
-      asum += c > 0;
       tsum += (c + block_m - 1) / block_m;
     }
   }
-  int ctot, atot, ttot;
+  int ctot, hltot, ttot;
   int cpre = block_exclusive_scan(csum, scan_lds, &ctot);
-  int apre = block_exclusive_scan(asum, scan_lds, &atot);
+  // heavy slots (high half) and light active slots (low half: at most
+  // kMaxSlots < 65536) in one scan
+  int hl = 0;
+  for (int i = 0; i < per; ++i) {
+    const int s = s0 + i;
+    if (s < P) {
+      const int c = hist[s];
+      hl += heavy_slot(c, ctot) ? (1 << 16) : (c > 0);
+    }
+  }
+  const int hlpre = block_exclusive_scan(hl, scan_lds, &hltot);
+  const int nh = hltot >> 16;
+  const int atot = nh + (hltot & 0xffff);
+  int lpre = nh + (hlpre & 0xffff);
+  if (__builtin_expect(hl >> 16, 0)) {
+    int h = hlpre >> 16;
+    for (int i = 0; i < per; ++i) {
+      const int s = s0 + i;
+      if (s < P && heavy_slot(hist[s], ctot)) heavy_keys[h++] = heavy_key(hist[s], s);
+    }
+  }
+  // the scan's barriers also publish the keys (and, in the one before,
+  // order their clearing before the writes)
   int tpre = block_exclusive_scan(tsum, scan_lds, &ttot);
   for (int i = 0; i < per; ++i) {
     const int s = s0 + i;
@@ -114,7 +179,8 @@ __device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
       counts[s] = c;
       offsets[s] = cpre;
       tile_off[s] = tpre;
-      if (c > 0) active[apre++] = s;
+      if (__builtin_expect(heavy_slot(c, ctot), 0)) active[heavy_rank(heavy_keys, heavy_key(c, s))] = s;
+      else if (c > 0) active[lpre++] = s;
       hist[s] = cpre;
       cpre += c;
       tpre += (c + block_m - 1) / block_m;
@@ -213,10 +279,37 @@ __device__ __forceinline__ void permute_block(
 // decode sizes) with ballots, shuffles and LDS, but no block barrier: pair
 // p = 64 g + lane belongs to group g of lane `lane`, slot s is owned by lane
 // s / SPL.  Groups are ranked in order, so pairs of one slot keep their flat
-// order.  Same outputs as permute_block.  lds: at least 64 * SPL ints of the
-// calling wave's own LDS.
+// order.  Same outputs as permute_block.  lds: wave_perm_lds_ints(P) ints of
+// the calling wave's own LDS.
 constexpr int kWavePermMaxSlotsPerLane = 16;
 constexpr int kWavePermMaxPairsPerLane = 4;
+
+// Per-slot outputs of one lane's slots s0 .. s0 + SPL - 1 (counts c, running
+// pair and tile prefixes cpre / tpre): counts, offsets, tile_off, the slot's
+// running base in lds, and the active entry of each slot with pairs at
+// positions lpos, lpos + 1, ...; with SKIP_HEAVY the heavy slots are left out
+// (the caller lists them).
+template <int SPL, bool SKIP_HEAVY>
+__device__ __forceinline__ void wave_slot_outputs(const int (&c)[SPL], int s0, int P, int block_m,
+                                                  int ctot, int cpre, int tpre, int lpos,
+                                                  int32_t* __restrict__ counts,
+                                                  int32_t* __restrict__ offsets,
+                                                  int32_t* __restrict__ tile_off,
+                                                  int32_t* __restrict__ active, int* lds) {
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) {
+    const int sl = s0 + i;
+    if (sl < P) {
+      counts[sl] = c[i];
+      offsets[sl] = cpre;
+      tile_off[sl] = tpre;
+      if (c[i] > 0 && !(SKIP_HEAVY && heavy_slot(c[i], ctot))) active[lpos++] = sl;
+      lds[sl] = cpre;  // running base of the slot
+      cpre += c[i];
+      tpre += (c[i] + block_m - 1) / block_m;
+    }
+  }
+}
 
 template <int SPL, int PPL>
 __device__ __forceinline__ void permute_wave(
@@ -268,6 +361,12 @@ __device__ __forceinline__ void permute_wave(
   const int cinc = wave_inclusive_sum(csum);
   int cpre = cinc - csum;
   const int ctot = read_lane_i32(cinc, 63);
+  // launch order (heavy_slot): whether the wave holds a heavy slot (one
+  // ballot; the rare heavy case counts them again)
+  bool lane_heavy = false;
+#pragma unroll
+  for (int i = 0; i < SPL; ++i) lane_heavy |= heavy_slot(c[i], ctot);
+  const bool any_heavy = __builtin_amdgcn_ballot_w64(lane_heavy) != 0ull;
   int apre, atot, tpre, ttot;
   if constexpr (SPL == 1) {
     // one slot per lane: the active prefix is a ballot count
@@ -280,7 +379,8 @@ __device__ __forceinline__ void permute_wave(
     atot = read_lane_i32(ainc, 63);
   }
   if (SPL == 1 && N <= block_m) {
-    // no slot holds more than block_m pairs: one tile per active slot
+    // no slot holds more than block_m pairs: one tile per active slot, so
+    // the tile prefix is the active prefix in slot order
     tpre = apre;
     ttot = atot;
   } else {
@@ -288,19 +388,38 @@ __device__ __forceinline__ void permute_wave(
     tpre = tinc - tsum;
     ttot = read_lane_i32(tinc, 63);
   }
-  wave_lds_sync();  // every lane has read its counts before lds is reused
+  // uniform; marked unlikely so that the branch is laid out after the
+  // kernel's straight-line path
+  if (__builtin_expect(any_heavy, 0)) {
+    // heavy keys in lds[64 SPL .. + kMaxHeavy) (slot order, empty entries
+    // 0); lane j < nh ranks key j against all of them and lists its slot.
+    // Light slots follow the nh heavy ones: active slots before this lane's,
+    // less the heavy ones.  (counts <= N <= 256 and slots < 1024 here:
+    // 32-bit keys)
+    int hsum = 0;
 #pragma unroll
-  for (int i = 0; i < SPL; ++i) {
-    const int sl = s0 + i;
-    if (sl < P) {
-      counts[sl] = c[i];
-      offsets[sl] = cpre;
-      tile_off[sl] = tpre;
-      if (c[i] > 0) active[apre++] = sl;
-      lds[sl] = cpre;  // running base of the slot
-      cpre += c[i];
-      tpre += (c[i] + block_m - 1) / block_m;
+    for (int i = 0; i < SPL; ++i) hsum += heavy_slot(c[i], ctot);
+    const int hinc = wave_inclusive_sum(hsum);
+    const int hpre = hinc - hsum;
+    const int nh = read_lane_i32(hinc, 63);
+    uint32_t* keys = reinterpret_cast<uint32_t*>(lds + kWave * SPL);
+    if (lane < kMaxHeavy && lane >= nh) keys[lane] = 0;
+    int h = hpre;
+#pragma unroll
+    for (int i = 0; i < SPL; ++i)
+      if (heavy_slot(c[i], ctot)) keys[h++] = heavy_key16(c[i], s0 + i);
+    wave_lds_sync();
+    if (lane < nh) {
+      const uint32_t key = keys[lane];
+      active[heavy_rank(keys, key)] = static_cast<int>(0xffffu - (key & 0xffffu));
     }
+    wave_lds_sync();  // every lane has read its counts and the keys before lds is reused
+    wave_slot_outputs<SPL, true>(c, s0, P, block_m, ctot, cpre, tpre, apre + nh - hpre, counts,
+                                 offsets, tile_off, active, lds);
+  } else {
+    wave_lds_sync();  // every lane has read its counts before lds is reused
+    wave_slot_outputs<SPL, false>(c, s0, P, block_m, ctot, cpre, tpre, apre, counts, offsets,
+                                  tile_off, active, lds);
   }
   // active[a] = -1 past the active slots (see scan_slots)
   for (int a = atot + lane; a < P; a += kWave) active[a] = -1;
@@ -345,13 +464,19 @@ __host__ __device__ inline int wave_perm_ppl(int N) {
   return N <= kWave ? 1 : N <= 2 * kWave ? 2 : N <= 4 * kWave ? 4 : 0;
 }
 
+// LDS ints permute_wave needs for P slots: the count table of 64 slots per
+// lane and the heavy-slot key list.
+__host__ __device__ inline int wave_perm_lds_ints(int P) {
+  return kWave * wave_perm_spl(P) + kMaxHeavy;
+}
+
 // Whether one wave permutes N pairs over P slots.
 __host__ __device__ inline bool wave_perm_fits(int N, int P) {
   return wave_perm_ppl(N) > 0 && wave_perm_spl(P) > 0;
 }
 
 // permute_wave with PPL pairs per lane for any P <= 64 *
-// kWavePermMaxSlotsPerLane (lds: 64 * wave_perm_spl(P) ints).  PPL is a
+// kWavePermMaxSlotsPerLane (lds: wave_perm_lds_ints(P) ints).  PPL is a
 // template parameter of the callers' kernels: one pair layout per kernel
 // keeps the latency-bound routers' code (and registers) small.
 template <int PPL>

@@ -25,7 +25,7 @@ __global__ __launch_bounds__(64) void permute_wave_kernel(
     int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
     int32_t* __restrict__ row_idx, int32_t* __restrict__ active,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
-  extern __shared__ int lds[];  // [64 * wave_perm_spl(P)]
+  extern __shared__ int lds[];  // [wave_perm_lds_ints(P)]
   permute_wave_any<PPL>(ids, N, log2phy, n_log2phy, P, skip, block_m, counts, offsets,
                         sorted_pairs, row_idx, active, tile_off, meta, lds);
 }
@@ -166,7 +166,7 @@ extern "C" int lmoe_permute(const int32_t* ids, int n_pairs,
   const size_t lds = sizeof(int) * static_cast<size_t>(n_slots);
   if (wave_perm_fits(n_pairs, n_slots)) {
     // decode sizes: one wave, no block barriers
-    const size_t wlds = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(n_slots));
+    const size_t wlds = sizeof(int) * static_cast<size_t>(wave_perm_lds_ints(n_slots));
 #define LMOE_PWK(Q)                                                                           \
   hipLaunchKernelGGL(permute_wave_kernel<Q>, dim3(1), dim3(kWave), wlds, stream, ids, n_pairs, \
                      log2phy, n_log2phy, n_slots, skip, block_m, counts, offsets, sorted_pairs,  \

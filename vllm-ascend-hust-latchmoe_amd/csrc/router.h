@@ -235,7 +235,7 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
     int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta) {
-  extern __shared__ int hist[];  // [max(P, 64 * wave_perm_spl(P))]
+  extern __shared__ int hist[];  // [max(P, wave_perm_lds_ints(P))]
   __shared__ TopkPermuteLds<EPL> L;
   select_and_permute<EPL, PPL, SCORE>(logits, logits_f32, T, sp, w_f32, w_bf16, ids, log2phy,
                                       n_log2phy, P, skip, block_m, counts, offsets,
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(ONE ? kOneTokenRouterThreads : 1024) void gate_topk
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
     int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
     int32_t* __restrict__ sync) {
-  extern __shared__ int hist[];  // [max(P, 64 * wave_perm_spl(P))]
+  extern __shared__ int hist[];  // [max(P, wave_perm_lds_ints(P))]
   __shared__ TopkPermuteLds<EPL> L;
   __shared__ int32_t l2p_lds[kMaxE];
   __shared__ int last;
@@ -381,7 +381,7 @@ inline void router_launch_shape(const RouterPermuteArgs& a, bool gate, int* thre
   *threads = t;
   size_t l = sizeof(int) * static_cast<size_t>(a.n_slots);
   if (wave_perm_fits(n_pairs, a.n_slots)) {
-    const size_t w = sizeof(int) * kWave * static_cast<size_t>(wave_perm_spl(a.n_slots));
+    const size_t w = sizeof(int) * static_cast<size_t>(wave_perm_lds_ints(a.n_slots));
     l = w > l ? w : l;
   }
   *lds = l;

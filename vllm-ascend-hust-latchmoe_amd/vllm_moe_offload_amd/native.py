@@ -533,7 +533,7 @@ class Permutation:
     offsets: torch.Tensor       # [P+1] i32
     sorted_pairs: torch.Tensor  # [N] i32 flat pair at each sorted position
     row_idx: torch.Tensor       # [N] i32 sorted position of each pair (expanded_row_idx) or -1
-    active: torch.Tensor        # [P] i32 slots with count > 0, ascending
+    active: torch.Tensor        # [P] i32 slots with count > 0: heavy slots first (by count), then ascending
     tile_off: torch.Tensor      # [P+1] i32 MFMA tile prefix
     meta: torch.Tensor          # [4] i32
     workspace: torch.Tensor     # int8 scratch for the multi-block path
