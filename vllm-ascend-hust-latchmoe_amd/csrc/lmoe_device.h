@@ -335,6 +335,21 @@ __device__ __forceinline__ uint4 load16_if(const uint16_t* p, int off, bool ok) 
   return ok ? v : make_uint4(0u, 0u, 0u, 0u);
 }
 
+// The two guarded loads with the guard dropped when the caller knows it holds
+// (CHECK false: the chunks tile the row exactly).  A guarded load costs its
+// lanes a zeroed register set and an exec-masked load per chunk; in the
+// multi-token GEMV loops that is a quarter of the instructions per token.
+template <bool CHECK>
+__device__ __forceinline__ uint4 load16_g(const uint16_t* p, int off, bool ok) {
+  if constexpr (CHECK) return load16_if(p, off, ok);
+  else return *reinterpret_cast<const uint4*>(p + off);
+}
+template <bool CHECK>
+__device__ __forceinline__ uint4 load_stream16_g(const uint16_t* p, int off, bool ok) {
+  if constexpr (CHECK) return load_stream16_if(p, off, ok);
+  else return load_stream16(p + off);
+}
+
 // Order LDS traffic of one wave: stores before the fence are seen by every
 // lane's loads after it.
 __device__ __forceinline__ void wave_lds_sync() {

@@ -31,7 +31,7 @@ namespace lmoe {
 // several tokens per step needs twice the registers, and the lost occupancy
 // costs more than the shorter chain saves: measured slower at B = 4 and 16.)
 // ---------------------------------------------------------------------------
-template <int NC, bool ONE>
+template <int NC, bool ONE, bool FULL>
 __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, int H, int I, int topk,
     const uint16_t* __restrict__ w13, const int32_t* __restrict__ offsets,
@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      xv[c] = load16_if(x, h, h < H);
+      xv[c] = load16_g<!FULL>(x, h, h < H);
     }
     const int s = active[a];
     const int i = blockIdx.x * 4 + wave;
@@ -58,15 +58,16 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      v[0] = dot8(xv[c], load_stream16_if(grow, h, h < H), v[0]);
-      v[1] = dot8(xv[c], load_stream16_if(urow, h, h < H), v[1]);
+      v[0] = dot8(xv[c], load_stream16_g<!FULL>(grow, h, h < H), v[0]);
+      v[1] = dot8(xv[c], load_stream16_g<!FULL>(urow, h, h < H), v[1]);
     }
     const float tot = reduce_scatter<2, 5, 0>(v, lane);
     const float up = read_lane(tot, 32);  // lane 32 holds the up total
     if (lane == 0) act[static_cast<size_t>(a) * I + i] = swiglu_bf16(tot, up);
     return;
   }
-  __shared__ uint16_t s_act[2][4];
+  // [token parity][wave][gate total, up total]
+  __shared__ __attribute__((aligned(16))) float s_gu[2][4][2];
   const int s = active[a];
   if (s < 0) return;  // uniform over the block
   const int p0 = offsets[s];
@@ -80,8 +81,8 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int h = c * 512 + lane * 8;
-    wg[c] = load_stream16_if(grow, h, h < H);
-    wu[c] = load_stream16_if(urow, h, h < H);
+    wg[c] = load_stream16_g<!FULL>(grow, h, h < H);
+    wu[c] = load_stream16_g<!FULL>(urow, h, h < H);
   }
   for (int r = 0; r < n; ++r) {
     const int t = sorted_pairs[p0 + r] / topk;
@@ -90,25 +91,24 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      const uint4 xv = load16_if(xr, h, h < H);
+      const uint4 xv = load16_g<!FULL>(xr, h, h < H);
       v[0] = dot8(xv, wg[c], v[0]);
       v[1] = dot8(xv, wu[c], v[1]);
     }
-    // lanes 0..31 end with the gate total, 32..63 with the up total
+    // lanes 0..31 end with the gate total, 32..63 with the up total; lanes
+    // 0 and 32 leave them in LDS (double-buffered by pair parity, one
+    // barrier per pair), and wave 0's lanes 0 and 1 form the block's four
+    // act values, two per lane, and store them as one 8-byte piece: one
+    // SwiGLU sequence per block and pair instead of one per wave (the
+    // paired form gives each value the bits of the single one)
     const float tot = reduce_scatter<2, 5, 0>(v, lane);
-    const float up = read_lane(tot, 32);  // lane 32 holds the up total
-    // the block's four act values of this pair leave in one 8-byte store
-    // (B=16 80.7 -> 79.3, B=64 209 -> 204 us per layer against a 2-byte
-    // store per wave); s_act is double-buffered, so one barrier per pair
-    if (lane == 0) s_act[r & 1][wave] = swiglu_bf16(tot, up);
+    if ((lane & 31) == 0) s_gu[r & 1][wave][lane >> 5] = tot;
     __syncthreads();
-    if (wave == 0 && lane == 0) {
-      const uint16_t* a4 = s_act[r & 1];
-      const uint32_t lo = a4[0] | (static_cast<uint32_t>(a4[1]) << 16);
-      const uint32_t hi = a4[2] | (static_cast<uint32_t>(a4[3]) << 16);
+    if (wave == 0 && lane < 2) {
+      const float4 gu = *reinterpret_cast<const float4*>(&s_gu[r & 1][2 * lane][0]);
       // I % 64 == 0: the four columns blockIdx.x * 4 .. + 3 are all < I
-      *reinterpret_cast<uint2*>(act + static_cast<size_t>(p0 + r) * I + blockIdx.x * 4) =
-          make_uint2(lo, hi);
+      *reinterpret_cast<uint32_t*>(act + static_cast<size_t>(p0 + r) * I + blockIdx.x * 4 + 2 * lane) =
+          swiglu_bf16x2(gu.x, gu.y, gu.z, gu.w);
     }
   }
 }
@@ -355,7 +355,8 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
 // lane-pair tree of down_combine_gemv_kernel, so y equals its LDS values bit
 // for bit.
 // ---------------------------------------------------------------------------
-template <int DNC, int R>
+// FULL: I == DNC * 256 and H % (8 R) == 0, so no chunk or row is guarded.
+template <int DNC, int R, bool FULL>
 __global__ __launch_bounds__(256) void down_rows_kernel(
     const uint16_t* __restrict__ act, int I, int H,
     const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(256) void down_rows_kernel(
 #pragma unroll
     for (int c = 0; c < DNC; ++c) {
       const int col = c * 256 + l5 * 8;
-      w[r][c] = load_stream16_if(base2, h * I + col, h < H && col < I);
+      w[r][c] = load_stream16_g<!FULL>(base2, h * I + col, h < H && col < I);
     }
   }
   for (int q = 0; q < n; ++q) {
@@ -393,14 +394,14 @@ __global__ __launch_bounds__(256) void down_rows_kernel(
 #pragma unroll
     for (int c = 0; c < DNC; ++c) {
       const int col = c * 256 + l5 * 8;
-      const uint4 av = load16_if(ar, col, col < I);
+      const uint4 av = load16_g<!FULL>(ar, col, col < I);
 #pragma unroll
       for (int r = 0; r < R; ++r) v[r] = dot8(av, w[r][c], v[r]);
     }
     // reduce over the 32 lanes of each half wave: lane holds row r
     const float tot = reduce_scatter<R, 4, 0>(v, lane);
     const int r = scatter_index<4, 0, LV>(lane);
-    if ((l5 & ((1 << (5 - LV)) - 1)) == 0 && h0 + r < H)
+    if ((l5 & ((1 << (5 - LV)) - 1)) == 0 && (FULL || h0 + r < H))
       y[static_cast<size_t>(dst) * H + h0 + r] = static_cast<uint16_t>(f32_to_bf16_bits(tot));
   }
 }
@@ -494,14 +495,20 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
   // faster at 16 tokens but 0.7 us slower at one token, and one layout must
   // serve every batch size, so the row-per-wave kernels stay there.)
   const bool cols = nc > 8;
-#define LMOE_GU(NC)                                                                           \
-  do {                                                                                        \
-    if (one)                                                                                  \
-      hipLaunchKernelGGL((gateup_gemv_kernel<NC, true>), g4, dim3(256), 0, stream, x, H, I,    \
-                         topk, w13, offsets, sorted_pairs, active, meta, act);                \
-    else                                                                                      \
-      hipLaunchKernelGGL((gateup_gemv_kernel<NC, false>), g4, dim3(256), 0, stream, x, H, I,   \
-                         topk, w13, offsets, sorted_pairs, active, meta, act);                \
+  // rows of exactly NC chunks of 512 columns load without guards
+#define LMOE_GU1(NC, ONE)                                                                      \
+  do {                                                                                         \
+    if (H == (NC)*512)                                                                         \
+      hipLaunchKernelGGL((gateup_gemv_kernel<NC, ONE, true>), g4, dim3(256), 0, stream, x, H,   \
+                         I, topk, w13, offsets, sorted_pairs, active, meta, act);              \
+    else                                                                                       \
+      hipLaunchKernelGGL((gateup_gemv_kernel<NC, ONE, false>), g4, dim3(256), 0, stream, x, H,  \
+                         I, topk, w13, offsets, sorted_pairs, active, meta, act);              \
+  } while (0)
+#define LMOE_GU(NC)              \
+  do {                           \
+    if (one) LMOE_GU1(NC, true); \
+    else LMOE_GU1(NC, false);    \
   } while (0)
 #define LMOE_GC(NC, RP)                                                                      \
   hipLaunchKernelGGL((gateup_gemv_cols_kernel<NC, RP>), dim3((I + (RP)-1) / (RP), max_active),  \
@@ -518,6 +525,7 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
   else if (nc <= 4) LMOE_GU(4);
   else LMOE_GU(8);
 #undef LMOE_GU
+#undef LMOE_GU1
   return LMOE_OK;
 }
 
@@ -529,9 +537,15 @@ static int launch_down_rows(const uint16_t* act, int H, int I, const uint16_t* w
                             const int32_t* active, int max_active, uint16_t* y,
                             hipStream_t stream) {
   const int dnc = (I + 255) / 256;
-#define LMOE_DR(DNC, R)                                                                         \
-  hipLaunchKernelGGL((down_rows_kernel<DNC, R>), dim3((H + 8 * (R)-1) / (8 * (R)), max_active), \
-                     dim3(256), 0, stream, act, I, H, w2, offsets, sorted_pairs, active, y)
+#define LMOE_DR1(DNC, R, FULL)                                                               \
+  hipLaunchKernelGGL((down_rows_kernel<DNC, R, FULL>), dim3((H + 8 * (R)-1) / (8 * (R)),       \
+                     max_active), dim3(256), 0, stream, act, I, H, w2, offsets, sorted_pairs,   \
+                     active, y)
+#define LMOE_DR(DNC, R)                                                   \
+  do {                                                                    \
+    if (I == (DNC)*256 && H % (8 * (R)) == 0) LMOE_DR1(DNC, R, true);     \
+    else LMOE_DR1(DNC, R, false);                                         \
+  } while (0)
   if (dnc <= 2) LMOE_DR(2, 2);
   else if (dnc <= 3) LMOE_DR(3, 2);
   else if (dnc <= 4) LMOE_DR(4, 2);
@@ -539,6 +553,7 @@ static int launch_down_rows(const uint16_t* act, int H, int I, const uint16_t* w
   else if (dnc <= 16) LMOE_DR(16, 2);
   else return LMOE_ERR_SHAPE;
 #undef LMOE_DR
+#undef LMOE_DR1
   return LMOE_OK;
 }
 
