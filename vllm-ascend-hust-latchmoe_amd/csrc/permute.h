@@ -69,14 +69,13 @@ __device__ int block_exclusive_scan(int v, int* scan_lds, int* total) {
   const int inc = wave_inclusive_sum(v);
   if (lane == 63) scan_lds[wave] = inc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int w = 0; w < nw; ++w) {
-      const int c = scan_lds[w];
-      scan_lds[w] = run;
-      run += c;
-    }
-    scan_lds[nw] = run;
+  if (wave == 0) {
+    // the wave totals scanned by one wave (nw <= 16 lanes) instead of one
+    // thread walking them through LDS
+    const int t = lane < nw ? scan_lds[lane] : 0;
+    const int tinc = wave_inclusive_sum(t);
+    if (lane < nw) scan_lds[lane] = tinc - t;
+    if (lane == 63) scan_lds[nw] = tinc;
   }
   __syncthreads();
   const int excl = scan_lds[wave] + inc - v;
@@ -128,7 +127,10 @@ __device__ __forceinline__ int heavy_rank(const K* keys, K key) {
 // Scan counts[0..P) held in LDS (hist) into offsets/active/tile_off; writes
 // counts, offsets, active (in the launch order above), tile_off and
 // meta[ACTIVE, PAIRS, TILES], and replaces hist[s] by offsets[s] in place
-// (each s is owned by one thread).
+// (each s is owned by one thread).  PUBLISH false: only the in-place
+// conversion (a workgroup that needs the offsets but is not the one that
+// writes the outputs).
+template <bool PUBLISH = true>
 __device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
                            int32_t* counts, int32_t* offsets, int32_t* active,
                            int32_t* tile_off, int32_t* meta) {
@@ -176,16 +178,19 @@ __device__ void scan_slots(int* hist, int P, int block_m, int* scan_lds,
     const int s = s0 + i;
     if (s < P) {
       const int c = hist[s];
-      counts[s] = c;
-      offsets[s] = cpre;
-      tile_off[s] = tpre;
-      if (__builtin_expect(heavy_slot(c, ctot), 0)) active[heavy_rank(heavy_keys, heavy_key(c, s))] = s;
-      else if (c > 0) active[lpre++] = s;
+      if (PUBLISH) {
+        counts[s] = c;
+        offsets[s] = cpre;
+        tile_off[s] = tpre;
+        if (__builtin_expect(heavy_slot(c, ctot), 0)) active[heavy_rank(heavy_keys, heavy_key(c, s))] = s;
+        else if (c > 0) active[lpre++] = s;
+      }
       hist[s] = cpre;
       cpre += c;
       tpre += (c + block_m - 1) / block_m;
     }
   }
+  if (!PUBLISH) return;
   // active[a] = -1 past the active slots: kernels that serve "the a-th
   // active slot" read one value (no dependent load of meta first)
   for (int a = atot + threadIdx.x; a < P; a += blockDim.x) active[a] = -1;
