@@ -204,7 +204,8 @@ __global__ __launch_bounds__(256) void gateup_gemv_cols_kernel(
 constexpr int kFusedMaxPairs = 1024;
 constexpr int kDnMaxRows = 4;
 
-template <int DNC, int R, bool PF, bool ONE>
+// FULL: I == DNC * 256 and H % R == 0 (W2 rows and act chunks unguarded).
+template <int DNC, int R, bool PF, bool ONE, bool FULL = false>
 __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
     const uint16_t* __restrict__ act, int I, int H, int T, int topk,
     const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
@@ -231,7 +232,7 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
 #pragma unroll
       for (int c = 0; c < DNC; ++c) {
         const int col = c * 256 + l5 * 8;
-        w[r][c] = load_stream16_if(base2, h * I + col, h < H && col < I);
+        w[r][c] = load_stream16_g<!FULL>(base2, h * I + col, h < H && col < I);
       }
     }
   };
@@ -278,7 +279,7 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
 #pragma unroll
         for (int c = 0; c < DNC; ++c) {
           const int col = c * 256 + l5 * 8;
-          const uint4 av = load16_if(ar, col, q < n && col < I);
+          const uint4 av = load16_if(ar, col, q < n && (FULL || col < I));
 #pragma unroll
           for (int r = 0; r < R; ++r) v[r] = dot8(av, wcur[r][c], v[r]);
         }
@@ -782,8 +783,12 @@ static int down_combine_impl(const void* act, int T, int H, int I, int k,
     const uint16_t* w2_ = static_cast<const uint16_t*>(w2_slots);                              \
     const uint16_t* add_ = static_cast<const uint16_t*>(add);                                  \
     uint16_t* out_ = static_cast<uint16_t*>(out);                                              \
-    if (one && k <= 8)                                                                         \
-      /* one slot per half wave (ranks < k <= 8): no next-slot prefetch */                     \
+    if (one && k <= 8 && I == (DNC)*256 && H % (R) == 0)                                       \
+      /* one slot per half wave (ranks < k <= 8): no next-slot prefetch; rows of whole chunks */ \
+      hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, false, true, true>), grid, dim3(256), \
+                         0, stream, a_, I, H, T, k, w2_, offsets, active, n_slots, row_idx, w,  \
+                         add_, out_);                                                          \
+    else if (one && k <= 8)                                                                    \
       hipLaunchKernelGGL((down_combine_gemv_kernel<DNC, R, false, true>), grid, dim3(256), 0,   \
                          stream, a_, I, H, T, k, w2_, offsets, active, n_slots, row_idx, w,     \
                          add_, out_);                                                          \

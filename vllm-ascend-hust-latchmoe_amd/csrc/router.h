@@ -56,8 +56,10 @@ __device__ __forceinline__ void store_logit(void* __restrict__ logits, int logit
 // logits[t][e] of one expert e for tokens [t0, t1), by the calling wave.
 // The expert row stays in registers (one 16-byte chunk per 512 columns per
 // lane) while the token rows stream through L1.  ONE: t1 == t0 + 1 (the
-// kernel holds only the single-token code).  words: see store_logit.
-template <int NC, bool ONE>
+// kernel holds only the single-token code).  words: see store_logit.  FULL:
+// H == NC * 512, so the chunk loads need no guards (the guards' zeroed
+// registers and exec-masked loads come before the first load issues).
+template <int NC, bool ONE, bool FULL = false>
 __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
                                          const uint16_t* __restrict__ wg, int t0, int t1,
                                          int H, int E, int e, void* __restrict__ logits,
@@ -70,7 +72,7 @@ __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int h = c * 512 + lane * 8;
-    w[c] = load16_if(wrow, h, h < H);
+    w[c] = load16_g<!FULL>(wrow, h, h < H);
   }
   // kGateTok tokens per reduction (x rows in flight together; the same
   // lane-pair tree per token as a lone wave_sum, so the logits do not depend
@@ -81,7 +83,7 @@ __device__ __forceinline__ void gate_row(const uint16_t* __restrict__ x,
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int h = c * 512 + lane * 8;
-      acc = dot8(load16_if(xr, h, h < H), w[c], acc);
+      acc = dot8(load16_g<!FULL>(xr, h, h < H), w[c], acc);
     }
     acc = wave_sum(acc);
     if (lane == 0) store_logit(logits, logits_f32, static_cast<size_t>(t0) * E + e, acc, words, tag);
@@ -253,8 +255,8 @@ __global__ __launch_bounds__(1024) void topk_permute_kernel(
 // any whose tag is not yet this launch's.  Only that last block ever waits,
 // for stores that every other block has already issued.  Calls that may run
 // concurrently need separate sync buffers, and a sync buffer serves one
-// permutation (one meta).  ONE: T == 1.
-template <int NC, int EPL, int PPL, int SCORE, bool ONE>
+// permutation (one meta).  ONE: T == 1.  FULL: H == NC * 512 (see gate_row).
+template <int NC, int EPL, int PPL, int SCORE, bool ONE, bool FULL = false>
 __global__ __launch_bounds__(ONE ? kOneTokenRouterThreads : 1024) void gate_topk_permute_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T, int H,
     void* __restrict__ logits, int logits_f32, SelectParams sp, float* __restrict__ w_f32,
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(ONE ? kOneTokenRouterThreads : 1024) void gate_topk
   const int t0 = ONE ? 0 : static_cast<int>(blockIdx.y) * kGateTok;
   const int t1 = ONE ? T : min(T, t0 + kGateTok);
   if (e < sp.E && t0 < t1)
-    gate_row<NC, ONE>(x, wg, t0, t1, H, sp.E, e, logits, logits_f32, words, tag);
+    gate_row<NC, ONE, FULL>(x, wg, t0, t1, H, sp.E, e, logits, logits_f32, words, tag);
   // every wave's logits are issued before thread 0 counts the block in (not
   // waited for: waiting for the stores to complete cost 0.35 us per layer,
   // more than the last block's occasional second read)
@@ -430,15 +432,21 @@ int launch_gate_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
   const int ppl = router_perm_ppl(a.T * (a.sp.k + a.sp.n_shared), a.n_slots);
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const uint16_t* wg = static_cast<const uint16_t*>(a.wg);
-#define LMOE_GTP(NC, EPL, Q, ONE)                                                                 \
-  hipLaunchKernelGGL((gate_topk_permute_kernel<NC, EPL, Q, SCORE, ONE>), dim3(blocks, tgroups), \
+#define LMOE_GTP_F(NC, EPL, Q, ONE, FULL)                                                        \
+  hipLaunchKernelGGL((gate_topk_permute_kernel<NC, EPL, Q, SCORE, ONE, FULL>),                   \
+                     dim3(blocks, tgroups), \
                      dim3(threads), lds, stream, x, wg, a.T, a.H, a.logits, a.logits_f32, a.sp, \
                      a.w_f32, a.w_bf16, a.ids, a.log2phy, a.n_log2phy, a.n_slots, a.skip,       \
                      a.block_m, a.counts, a.offsets, a.sorted_pairs, a.row_idx, a.active,       \
                      a.tile_off, a.meta, a.sync)
+#define LMOE_GTP(NC, EPL, Q, ONE) LMOE_GTP_F(NC, EPL, Q, ONE, false)
+  // one token, rows of exactly NC chunks: the gate loads without guards
 #define LMOE_GTP_Q(NC, EPL)                          \
   do {                                               \
-    if (a.T == 1) {                                  \
+    if (a.T == 1 && a.H == (NC)*512) {               \
+      if (ppl == 1) LMOE_GTP_F(NC, EPL, 1, true, true); \
+      else LMOE_GTP_F(NC, EPL, 0, true, true);       \
+    } else if (a.T == 1) {                           \
       if (ppl == 1) LMOE_GTP(NC, EPL, 1, true);      \
       else LMOE_GTP(NC, EPL, 0, true);               \
     } else {                                         \
@@ -472,6 +480,7 @@ int launch_gate_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
 #undef LMOE_GTP_E
 #undef LMOE_GTP_Q
 #undef LMOE_GTP
+#undef LMOE_GTP_F
   LMOE_RETURN_LAUNCH();
 }
 

@@ -10,7 +10,8 @@
 namespace lmoe {
 
 // logits[t][e] for e = 4*blockIdx.x + wave, tokens of block row blockIdx.y.
-template <int NC>
+// FULL: H == NC * 512 (unguarded chunk loads, see gate_row).
+template <int NC, bool FULL>
 __global__ __launch_bounds__(256) void gate_gemv_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int T,
     int H, int E, int tokens_per_block, void* __restrict__ logits,
@@ -19,8 +20,8 @@ __global__ __launch_bounds__(256) void gate_gemv_kernel(
   if (e >= E) return;
   const int t0 = blockIdx.y * tokens_per_block;
   const int t1 = min(T, t0 + tokens_per_block);
-  if (t1 - t0 == 1) gate_row<NC, true>(x, wg, t0, t1, H, E, e, logits, logits_f32);
-  else gate_row<NC, false>(x, wg, t0, t1, H, E, e, logits, logits_f32);
+  if (t1 - t0 == 1) gate_row<NC, true, FULL>(x, wg, t0, t1, H, E, e, logits, logits_f32);
+  else gate_row<NC, false, FULL>(x, wg, t0, t1, H, E, e, logits, logits_f32);
 }
 
 // One wave per token; EPL experts per lane (EPL*64 >= E).
@@ -107,14 +108,20 @@ extern "C" int lmoe_router_gate(const void* x, const void* wg, int T, int H,
   const int tpb = kGateTok;
   dim3 grid((E + 3) / 4, (T + tpb - 1) / tpb);
   const int nc = (H + 511) / 512;
-#define LMOE_GATE(NC)                                                              \
-  hipLaunchKernelGGL(gate_gemv_kernel<NC>, grid, dim3(256), 0, stream,             \
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(wg), \
-                     T, H, E, tpb, logits, logits_f32)
+#define LMOE_GATE1(NC, FULL)                                                                \
+  hipLaunchKernelGGL((gate_gemv_kernel<NC, FULL>), grid, dim3(256), 0, stream,                \
+                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(wg), T, H, E, \
+                     tpb, logits, logits_f32)
+#define LMOE_GATE(NC)                              \
+  do {                                             \
+    if (H == (NC)*512) LMOE_GATE1(NC, true);       \
+    else LMOE_GATE1(NC, false);                    \
+  } while (0)
   if (nc <= 4) LMOE_GATE(4);
   else if (nc <= 8) LMOE_GATE(8);
   else LMOE_GATE(16);
 #undef LMOE_GATE
+#undef LMOE_GATE1
   LMOE_RETURN_LAUNCH();
 }
 
