@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define LMOE_ABI_VERSION 7
+#define LMOE_ABI_VERSION 8
 
 enum { LMOE_SKIP_KEEP_ROWS = 2 }; /* lmoe_permute skip_unmapped mode */
 
@@ -238,6 +238,25 @@ int lmoe_permute(const int32_t* ids, int n_pairs, const int32_t* log2phy,
                  int32_t* meta, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);
 
+/* The two builds of a decode layer whose routed experts exceed its bank, in
+ * one launch: table a (the bank, skip_unmapped = 1) and table b (the
+ * overflow stage buffer, LMOE_SKIP_KEEP_ROWS) over the same ids, each into
+ * its own outputs (counts_x .. meta_x, as lmoe_permute writes them), row_idx
+ * shared.  Every output equals lmoe_permute(a, 1) followed by
+ * lmoe_permute(b, 2) on the same row_idx.  Both tables required; n_pairs <=
+ * 1024 (one workgroup per table; larger builds: LMOE_ERR_SHAPE, run the two
+ * lmoe_permute calls).  No workspace.  No single counterpart in the
+ * reference, which remaps and routes one expert table per pass
+ * (slot_mapping.py:116-140 + patch_fused_moe.py:668-701 per wave). */
+int lmoe_permute_two_tables(
+    const int32_t* ids, int n_pairs, int block_m, int32_t* row_idx,
+    const int32_t* log2phy_a, int n_log2phy_a, int n_slots_a, int32_t* counts_a,
+    int32_t* offsets_a, int32_t* sorted_pairs_a, int32_t* active_a,
+    int32_t* tile_off_a, int32_t* meta_a, const int32_t* log2phy_b,
+    int n_log2phy_b, int n_slots_b, int32_t* counts_b, int32_t* offsets_b,
+    int32_t* sorted_pairs_b, int32_t* active_b, int32_t* tile_off_b,
+    int32_t* meta_b, hipStream_t stream);
+
 /* expanded_x: x_sorted[pos] = x[sorted_pairs[pos] / k] for pos < n_pairs
  * (positions past meta[LMOE_META_PAIRS] are left untouched). */
 int lmoe_gather_rows(const void* x, int H, int k, const int32_t* sorted_pairs,
@@ -278,6 +297,32 @@ int lmoe_down(const void* act, int H, int I, const void* w2_slots, int n_slots,
               const int32_t* active, const int32_t* tile_off,
               const int32_t* meta, int n_pairs, int block_m, int path, void* y,
               hipStream_t stream);
+
+/* Both decode passes of a layer whose routed experts exceed its bank, in one
+ * gate_up and one down launch (the GEMV path): pass a is the bank (w13_a,
+ * w2_a, n_slots_a and its permutation, built with skip_unmapped), pass b the
+ * overflow stage buffer (w13_b, w2_b, n_slots_b and its permutation, built
+ * with skip mode 2 over the same ids).  act is one [n_pairs, I] bf16
+ * workspace: pass a's rows at its sorted positions, pass b's after pass a's
+ * meta_a[LMOE_META_PAIRS] placed pairs.  y is [T*k, H] indexed by flat pair,
+ * as lmoe_grouped_mlp writes it; every value has the bits of
+ * lmoe_grouped_mlp(path GEMV) over each pass.  The two tables must map
+ * disjoint experts (an overflow expert maps to -1 in the bank table): a pair
+ * both place is written by both passes in no set order, and pass b's rows
+ * that would fall past act's n_pairs rows are not computed.  Rows up to 4096
+ * columns (H <= 4096, I <= 4096), act and w2 16-byte aligned; else
+ * LMOE_ERR_SHAPE (run the passes one by one).  No counterpart in the reference, which executes a
+ * working set past the slot count as bounded pair waves one after the other
+ * (moe_offload/runtime.py:1215-1232); here the decode overflow's two passes
+ * share their launches. */
+int lmoe_decode_mlp_two_passes(const void* x, int T, int H, int I, int k,
+                               const void* w13_a, const void* w2_a, int n_slots_a,
+                               const int32_t* offsets_a, const int32_t* sorted_pairs_a,
+                               const int32_t* active_a, const int32_t* meta_a,
+                               const void* w13_b, const void* w2_b, int n_slots_b,
+                               const int32_t* offsets_b, const int32_t* sorted_pairs_b,
+                               const int32_t* active_b, int n_pairs, void* act, void* y,
+                               hipStream_t stream);
 
 /* Weighted combine: out[t] = sum_{j<k} w[t][j] * y[t*k+j], f32 accumulation
  * in j order, one rounding to bf16.  y is [T*k, H] bf16 indexed by flat pair

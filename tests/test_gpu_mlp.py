@@ -438,3 +438,102 @@ def test_block_range_kernel_equals_tile_grid_at_prefill_sizes(T, E, P, skew):
     assert torch.equal(outs[256][0].view(torch.int16), outs[320][0].view(torch.int16))
     assert torch.equal(outs[256][1].view(torch.int16), outs[320][1].view(torch.int16))
     assert torch.isfinite(outs[320][1].float()).all()
+
+
+def _two_pass_tables(rng, ids, E, Pa, Pb, overlap):
+    """Bank table (a) and overflow table (b) over the routed experts: a
+    random subset in the bank, the rest split between the overflow buffer
+    and no table (pairs no pass places); with overlap, both tables map every
+    routed expert."""
+    used = rng.permutation(np.unique(ids))
+    la = np.full(E, -1, dtype=np.int32)
+    lb = np.full(E, -1, dtype=np.int32)
+    if overlap:
+        la[used] = rng.permutation(Pa)[: used.size]
+        lb[used] = rng.permutation(Pb)[: used.size]
+        return la, lb
+    na = min(Pa, used.size * 3 // 5)
+    nb = min(Pb, used.size - na - 1)
+    la[used[:na]] = rng.permutation(Pa)[:na]
+    lb[used[na:na + nb]] = rng.permutation(Pb)[:nb]
+    return la, lb
+
+
+@pytest.mark.parametrize("T,k,E,Pa,Pb,H,I,overlap", [
+    (64, 8, 128, 32, 32, 2048, 768, False),  # the B=64 decode shape: both kernels unguarded
+    (16, 8, 64, 32, 32, 1536, 320, False),   # guarded chunks in both kernels
+    (1, 8, 64, 4, 8, 512, 128, False),       # one token
+    (8, 4, 32, 12, 16, 4096, 256, False),    # 8 chunks of 512 columns
+    (4, 2, 16, 6, 8, 512, 4096, False),      # 16 chunks of 256 act columns
+    (16, 8, 64, 64, 64, 1024, 256, True),    # tables that overlap: pass b computes nothing
+])
+def test_two_passes_in_shared_launches_equal_passes_one_by_one(T, k, E, Pa, Pb, H, I, overlap):
+    """lmoe_decode_mlp_two_passes (bank + overflow stage buffer, one gate_up
+    and one down launch) writes every y row with the bits of two
+    grouped_mlp(GEMV) passes run one after the other, and leaves the rows of
+    pairs neither table maps untouched.  With overlapping tables every pair
+    is placed by the bank pass, the overflow pass's act rows would fall past
+    the buffer, and it computes nothing: y equals the bank pass alone."""
+    native = _native()
+    rng = np.random.default_rng(1000 + T * 7 + H + I)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    la, lb = _two_pass_tables(rng, ids, E, Pa, Pb, overlap)
+    x = normal_bf16(rng, (T, H), 1.0)
+    w13a, w2a = normal_bf16(rng, (Pa, 2 * I, H), 0.02), normal_bf16(rng, (Pa, H, I), 0.02)
+    if overlap:  # both tables hold the same weights for an expert
+        w13b = np.zeros((Pb, 2 * I, H), dtype=np.uint16)
+        w2b = np.zeros((Pb, H, I), dtype=np.uint16)
+        for e in np.unique(ids):
+            w13b[lb[e]], w2b[lb[e]] = w13a[la[e]], w2a[la[e]]
+    else:
+        w13b, w2b = normal_bf16(rng, (Pb, 2 * I, H), 0.02), normal_bf16(rng, (Pb, H, I), 0.02)
+    print(f"case two passes T={T} k={k} H={H} I={I} overlap={overlap}", flush=True)
+    d_ids, d_x = to_dev_i32(ids), to_dev_bf16(x)
+    d13a, d2a, d13b, d2b = (to_dev_bf16(w) for w in (w13a, w2a, w13b, w2b))
+    n = T * k
+    pa = native.Permutation.allocate(n, Pa, "cuda")
+    pb = native.Permutation.allocate(n, Pb, "cuda")
+    native.permute(d_ids, pa, log2phy=to_dev_i32(la), skip_unmapped=True)
+    native.permute(d_ids, pb, log2phy=to_dev_i32(lb), keep_rows=True, row_idx=pa.row_idx)
+    fill = torch.full((n, H), -7.0, dtype=torch.bfloat16, device="cuda")
+    act1 = torch.empty((n, I), dtype=torch.bfloat16, device="cuda")
+    y1 = fill.clone()
+    native.grouped_mlp(d_x, k, d13a, d2a, pa, act1, y1, path=native.LMOE_PATH_GEMV)
+    y_bank = y1.clone()
+    if not overlap:
+        native.grouped_mlp(d_x, k, d13b, d2b, pb, act1, y1, path=native.LMOE_PATH_GEMV)
+    act2 = torch.empty((n, I), dtype=torch.bfloat16, device="cuda")
+    y2 = fill.clone()
+    native.decode_mlp_two_passes(d_x, k, d13a, d2a, pa, d13b, d2b, pb, act2, y2)
+    # a second call on the same buffers (the replay case) writes the same bits
+    y3 = fill.clone()
+    native.decode_mlp_two_passes(d_x, k, d13a, d2a, pa, d13b, d2b, pb, act2, y3)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert torch.equal(y2.view(torch.int16), y3.view(torch.int16))
+    flat = ids.reshape(-1)
+    placed = (la[flat] >= 0) | (lb[flat] >= 0)
+    untouched = torch.from_numpy(~placed).cuda()
+    assert torch.equal(y2[untouched].view(torch.int16), fill[untouched].view(torch.int16))
+    if overlap:
+        assert placed.all() and torch.equal(y2.view(torch.int16), y_bank.view(torch.int16))
+    else:
+        assert (~placed).any() and (lb[flat] >= 0).any()
+
+
+def test_two_passes_reject_rows_past_4096_columns():
+    """Rows the row-per-wave GEMVs do not hold are refused before any launch
+    (status LMOE_ERR_SHAPE through the C ABI, ValueError in the wrapper)."""
+    native = _native()
+    lib = native.load_library()
+    T, k, H, I, P = 1, 2, 4608, 128, 4
+    z = torch.zeros(1, dtype=torch.int32, device="cuda")
+    p = z.data_ptr()
+    st = lib.lmoe_decode_mlp_two_passes(p, T, H, I, k, p, p, P, p, p, p, p, p, p, P, p, p, p, T * k, p, p, None)
+    assert st == native.LMOE_ERR_SHAPE
+    st = lib.lmoe_decode_mlp_two_passes(p, T, 512, 4160, k, p, p, P, p, p, p, p, p, p, P, p, p, p, T * k, p, p,
+                                        None)
+    assert st == native.LMOE_ERR_SHAPE
+    st = lib.lmoe_decode_mlp_two_passes(p, T, 512, 128, k, p, p, P, p, p, p, p, p, p, 0, p, p, p, T * k, p, p,
+                                        None)
+    assert st == native.LMOE_ERR_ARG

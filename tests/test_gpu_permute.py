@@ -164,3 +164,113 @@ def test_table_update_writes_exactly_the_pairs(n_table, n):
     ref = init.copy()
     ref[idx] = val
     np.testing.assert_array_equal(table.cpu().numpy(), ref)
+
+
+def _perm_arrays(perm, n):
+    torch.cuda.synchronize()
+    return {name: getattr(perm, name).cpu().numpy()[: (n if name in ("sorted_pairs", "row_idx") else None)]
+            for name in ("counts", "offsets", "sorted_pairs", "row_idx", "active", "tile_off")} | \
+        {"meta": perm.meta.cpu().numpy()[:4]}
+
+
+@pytest.mark.parametrize("N,Pa,Pb,E,overlap,bad", [
+    (128, 64, 64, 128, False, False),    # one wave per table
+    (512, 64, 64, 128, False, False),    # the B=64 decode build: one workgroup per table
+    (1024, 64, 300, 600, False, True),   # the largest one-launch build, ids outside both tables
+    (200, 40, 1500, 3000, False, False),  # a table past the wave form: workgroups
+    (256, 64, 64, 100, True, False),     # overlapping tables: the later build's rows win
+    (0, 8, 8, 16, False, False),         # empty batch
+])
+def test_permute_two_tables_equals_two_builds(N, Pa, Pb, E, overlap, bad):
+    """lmoe_permute_two_tables (bank table in skip mode 1, overflow table in
+    skip mode 2, one launch) writes every output as lmoe_permute(a, 1) then
+    lmoe_permute(b, 2) on the same row_idx, and both match the oracle."""
+    native = _native()
+    rng = np.random.default_rng(N + Pb)
+    ids = rng.integers(0, E, size=N).astype(np.int32)
+    if bad and N:  # ids past the tables: skipped silently by both builds
+        ids[rng.integers(0, N, size=7)] = E + 5
+        ids[3] = -2
+    experts = rng.permutation(E)
+    la = np.full(E, -1, dtype=np.int32)
+    lb = np.full(E, -1, dtype=np.int32)
+    na = min(Pa, E // 2)
+    la[experts[:na]] = rng.permutation(Pa)[:na]
+    if overlap:
+        lb[experts[:Pb]] = rng.permutation(Pb)[: min(Pb, E)]
+    else:
+        nb = min(Pb, E - na - 3)
+        lb[experts[na:na + nb]] = rng.permutation(Pb)[:nb]
+        if bad:  # entries that are no slot of their table: errors of each build
+            la[experts[-1]] = Pa + 5
+            lb[experts[-2]] = -7
+            ids[5], ids[6] = experts[-1], experts[-2]
+    print(f"case two tables N={N} Pa={Pa} Pb={Pb} overlap={overlap} bad={bad}", flush=True)
+    d_ids, d_la, d_lb = to_dev_i32(ids.reshape(-1, 1) if N else ids), to_dev_i32(la), to_dev_i32(lb)
+    seq_a, seq_b = native.Permutation.allocate(N, Pa, "cuda"), native.Permutation.allocate(N, Pb, "cuda")
+    one_a, one_b = native.Permutation.allocate(N, Pa, "cuda"), native.Permutation.allocate(N, Pb, "cuda")
+    for p in (seq_a, seq_b, one_a, one_b):  # stale contents the builds must overwrite
+        for t in (p.counts, p.offsets, p.sorted_pairs, p.row_idx, p.active, p.tile_off):
+            t.fill_(7)
+    native.permute(d_ids, seq_a, log2phy=d_la, skip_unmapped=True)
+    native.permute(d_ids, seq_b, log2phy=d_lb, keep_rows=True, row_idx=seq_a.row_idx)
+    lib = native.load_library()
+    st = lib.lmoe_permute_two_tables(
+        native._ptr(d_ids), N, native.MFMA_BLOCK_M, native._ptr(one_a.row_idx),
+        native._ptr(d_la), E, Pa, native._ptr(one_a.counts), native._ptr(one_a.offsets),
+        native._ptr(one_a.sorted_pairs), native._ptr(one_a.active), native._ptr(one_a.tile_off),
+        native._ptr(one_a.meta), native._ptr(d_lb), E, Pb, native._ptr(one_b.counts), native._ptr(one_b.offsets),
+        native._ptr(one_b.sorted_pairs), native._ptr(one_b.active), native._ptr(one_b.tile_off),
+        native._ptr(one_b.meta), None)
+    assert st == 0
+    got_a, got_b = _perm_arrays(one_a, N), _perm_arrays(one_b, N)
+    want_a, want_b = _perm_arrays(seq_a, N), _perm_arrays(seq_b, N)
+    for name in got_a:
+        if name == "sorted_pairs":  # positions past the placed pairs are not written
+            pa, pb = int(want_a["meta"][1]), int(want_b["meta"][1])
+            np.testing.assert_array_equal(got_a[name][:pa], want_a[name][:pa])
+            np.testing.assert_array_equal(got_b[name][:pb], want_b[name][:pb])
+            continue
+        np.testing.assert_array_equal(got_a[name], want_a[name], err_msg=name)
+        if name != "row_idx":  # the second build's row_idx lives in the first's buffer
+            np.testing.assert_array_equal(got_b[name], want_b[name], err_msg=name)
+    # the oracle: each table's build, row_idx from the later build where it places
+    ra = orc.init_routing(ids, Pa, log2phy=la, skip_unmapped=True, block_m=native.MFMA_BLOCK_M)
+    rb = orc.init_routing(ids, Pb, log2phy=lb, skip_unmapped=True, block_m=native.MFMA_BLOCK_M)
+    np.testing.assert_array_equal(got_a["counts"], ra.counts)
+    np.testing.assert_array_equal(got_b["counts"], rb.counts)
+    np.testing.assert_array_equal(got_a["sorted_pairs"][: ra.placed], ra.sorted_pairs)
+    np.testing.assert_array_equal(got_b["sorted_pairs"][: rb.placed], rb.sorted_pairs)
+    np.testing.assert_array_equal(got_a["active"][: ra.active.size], ra.active)
+    np.testing.assert_array_equal(got_b["active"][: rb.active.size], rb.active)
+    rows = np.where(rb.row_idx >= 0, rb.row_idx, ra.row_idx)
+    np.testing.assert_array_equal(got_a["row_idx"], rows)
+    assert got_a["meta"][2] == ra.errors and got_b["meta"][2] == rb.errors
+    if bad and N:
+        assert ra.errors > 0 and rb.errors > 0
+    if overlap:
+        assert ((ra.row_idx >= 0) & (rb.row_idx >= 0)).any()
+
+
+def test_permute_two_tables_refuses_builds_past_one_workgroup():
+    """More than 1024 pairs: LMOE_ERR_SHAPE before any launch (the wrapper
+    then runs the two builds one after the other)."""
+    native = _native()
+    lib = native.load_library()
+    z = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    p = z.data_ptr()
+    st = lib.lmoe_permute_two_tables(p, 1025, 256, p, p, 8, 8, p, p, p, p, p, p, p, 8, 8, p, p, p, p, p, p, None)
+    assert st == native.LMOE_ERR_SHAPE
+    st = lib.lmoe_permute_two_tables(p, 16, 256, p, None, 8, 8, p, p, p, p, p, p, p, 8, 8, p, p, p, p, p, p, None)
+    assert st == native.LMOE_ERR_ARG
+    # the wrapper's fallback: the two builds
+    N, P = 2048, 16
+    rng = np.random.default_rng(5)
+    ids = to_dev_i32(rng.integers(0, 32, size=N).astype(np.int32))
+    la = np.full(32, -1, dtype=np.int32)
+    lb = np.full(32, -1, dtype=np.int32)
+    la[:16], lb[16:] = np.arange(16), np.arange(16)
+    a, b = native.Permutation.allocate(N, P, "cuda"), native.Permutation.allocate(N, P, "cuda")
+    native.permute_two_tables(ids, a, to_dev_i32(la), b, to_dev_i32(lb))
+    torch.cuda.synchronize()
+    assert int(a.meta[1]) + int(b.meta[1]) == N and (a.row_idx >= 0).all()

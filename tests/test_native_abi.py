@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = native.load_library()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.lmoe_abi_version() == 7
+    assert lib.lmoe_abi_version() == 8
     assert lib.lmoe_status_string(1001) == b"unsupported shape"
 
 

@@ -21,6 +21,60 @@
 
 namespace lmoe {
 
+// Several tokens: block (bx, slot s) of the gate_up GEMV, the slot's pairs
+// p0 .. p0 + n - 1 (act rows p0 + r of act).  Each wave holds its row pair's
+// weights in registers and the slot's tokens stream past one at a time.
+template <int NC, bool FULL>
+__device__ __forceinline__ void gateup_tokens(const uint16_t* __restrict__ x, int H, int I,
+                                              int topk, const uint16_t* __restrict__ w13, int s,
+                                              int p0, int n,
+                                              const int32_t* __restrict__ sorted_pairs,
+                                              uint16_t* __restrict__ act) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // [token parity][wave][gate total, up total]
+  __shared__ __attribute__((aligned(16))) float s_gu[2][4][2];
+  // I % 64 == 0 (the entry points check it), so every wave's row is < I and
+  // all four waves meet the barrier of every pair
+  const int i = blockIdx.x * 4 + wave;
+  const uint16_t* grow = w13 + (static_cast<size_t>(s) * 2 * I + i) * H;
+  const uint16_t* urow = grow + static_cast<size_t>(I) * H;
+  uint4 wg[NC], wu[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int h = c * 512 + lane * 8;
+    wg[c] = load_stream16_g<!FULL>(grow, h, h < H);
+    wu[c] = load_stream16_g<!FULL>(urow, h, h < H);
+  }
+  for (int r = 0; r < n; ++r) {
+    const int t = sorted_pairs[p0 + r] / topk;
+    const uint16_t* xr = x + static_cast<size_t>(t) * H;
+    float v[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int h = c * 512 + lane * 8;
+      const uint4 xv = load16_g<!FULL>(xr, h, h < H);
+      v[0] = dot8(xv, wg[c], v[0]);
+      v[1] = dot8(xv, wu[c], v[1]);
+    }
+    // lanes 0..31 end with the gate total, 32..63 with the up total; lanes
+    // 0 and 32 leave them in LDS (double-buffered by pair parity, one
+    // barrier per pair), and wave 0's lanes 0 and 1 form the block's four
+    // act values, two per lane, and store them as one 8-byte piece: one
+    // SwiGLU sequence per block and pair instead of one per wave (the
+    // paired form gives each value the bits of the single one)
+    const float tot = reduce_scatter<2, 5, 0>(v, lane);
+    if ((lane & 31) == 0) s_gu[r & 1][wave][lane >> 5] = tot;
+    __syncthreads();
+    if (wave == 0 && lane < 2) {
+      const float4 gu = *reinterpret_cast<const float4*>(&s_gu[r & 1][2 * lane][0]);
+      // I % 64 == 0: the four columns blockIdx.x * 4 .. + 3 are all < I
+      *reinterpret_cast<uint32_t*>(act + static_cast<size_t>(p0 + r) * I + blockIdx.x * 4 + 2 * lane) =
+          swiglu_bf16x2(gu.x, gu.y, gu.z, gu.w);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // gate_up GEMV + SiLU*mul, rows up to 4096 columns.  grid (ceil(I/4),
 // max_active), 4 waves.  Block (bx, a) serves the a-th active slot (active[] /
@@ -66,51 +120,47 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     if (lane == 0) act[static_cast<size_t>(a) * I + i] = swiglu_bf16(tot, up);
     return;
   }
-  // [token parity][wave][gate total, up total]
-  __shared__ __attribute__((aligned(16))) float s_gu[2][4][2];
   const int s = active[a];
   if (s < 0) return;  // uniform over the block
   const int p0 = offsets[s];
-  const int n = offsets[s + 1] - p0;
-  // I % 64 == 0 (the entry points check it), so every wave's row is < I and
-  // all four waves meet the barrier of every pair
-  const int i = blockIdx.x * 4 + wave;
-  const uint16_t* grow = w13 + (static_cast<size_t>(s) * 2 * I + i) * H;
-  const uint16_t* urow = grow + static_cast<size_t>(I) * H;
-  uint4 wg[NC], wu[NC];
-#pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int h = c * 512 + lane * 8;
-    wg[c] = load_stream16_g<!FULL>(grow, h, h < H);
-    wu[c] = load_stream16_g<!FULL>(urow, h, h < H);
-  }
-  for (int r = 0; r < n; ++r) {
-    const int t = sorted_pairs[p0 + r] / topk;
-    const uint16_t* xr = x + static_cast<size_t>(t) * H;
-    float v[2] = {0.0f, 0.0f};
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int h = c * 512 + lane * 8;
-      const uint4 xv = load16_g<!FULL>(xr, h, h < H);
-      v[0] = dot8(xv, wg[c], v[0]);
-      v[1] = dot8(xv, wu[c], v[1]);
-    }
-    // lanes 0..31 end with the gate total, 32..63 with the up total; lanes
-    // 0 and 32 leave them in LDS (double-buffered by pair parity, one
-    // barrier per pair), and wave 0's lanes 0 and 1 form the block's four
-    // act values, two per lane, and store them as one 8-byte piece: one
-    // SwiGLU sequence per block and pair instead of one per wave (the
-    // paired form gives each value the bits of the single one)
-    const float tot = reduce_scatter<2, 5, 0>(v, lane);
-    if ((lane & 31) == 0) s_gu[r & 1][wave][lane >> 5] = tot;
-    __syncthreads();
-    if (wave == 0 && lane < 2) {
-      const float4 gu = *reinterpret_cast<const float4*>(&s_gu[r & 1][2 * lane][0]);
-      // I % 64 == 0: the four columns blockIdx.x * 4 .. + 3 are all < I
-      *reinterpret_cast<uint32_t*>(act + static_cast<size_t>(p0 + r) * I + blockIdx.x * 4 + 2 * lane) =
-          swiglu_bf16x2(gu.x, gu.y, gu.z, gu.w);
-    }
-  }
+  gateup_tokens<NC, FULL>(x, H, I, topk, w13, s, p0, offsets[s + 1] - p0, sorted_pairs, act);
+}
+
+// Both passes of a decode layer whose working set exceeds its bank (the
+// bank and the overflow stage buffer, each with its own permutation) in one
+// gate_up launch: grid rows below max_active_a serve the bank's active
+// slots, the rest the overflow's.  The overflow pass's act rows follow the
+// bank pass's placed pairs (meta_a[LMOE_META_PAIRS]), so one act buffer of
+// n_pairs rows holds both when the two tables map disjoint experts (each
+// pair placed by at most one pass); second_rows keeps an overflow slot's
+// rows inside the buffer otherwise.  Each block runs gateup_tokens as the
+// one-pass kernel does: the same bits.
+__device__ __forceinline__ int second_rows(int base, int p0, int n, int n_pairs) {
+  const int room = n_pairs - base - p0;
+  return n < room ? n : room;
+}
+
+template <int NC, bool FULL>
+__global__ __launch_bounds__(256) void gateup_gemv_two_kernel(
+    const uint16_t* __restrict__ x, int H, int I, int topk, int n_pairs, int max_active_a,
+    const uint16_t* __restrict__ w13_a, const int32_t* __restrict__ offsets_a,
+    const int32_t* __restrict__ sorted_pairs_a, const int32_t* __restrict__ active_a,
+    const int32_t* __restrict__ meta_a, const uint16_t* __restrict__ w13_b,
+    const int32_t* __restrict__ offsets_b, const int32_t* __restrict__ sorted_pairs_b,
+    const int32_t* __restrict__ active_b, uint16_t* __restrict__ act) {
+  const bool second = static_cast<int>(blockIdx.y) >= max_active_a;
+  const int a = second ? blockIdx.y - max_active_a : blockIdx.y;
+  const int32_t* offsets = second ? offsets_b : offsets_a;
+  const int s = (second ? active_b : active_a)[a];
+  if (s < 0) return;  // uniform over the block
+  const int p0 = offsets[s];
+  const int base = second ? meta_a[LMOE_META_PAIRS] : 0;
+  int n = offsets[s + 1] - p0;
+  if (second) n = second_rows(base, p0, n, n_pairs);  // uniform over the block
+  if (n <= 0) return;
+  gateup_tokens<NC, FULL>(x, H, I, topk, second ? w13_b : w13_a, s, p0, n,
+                          second ? sorted_pairs_b : sorted_pairs_a,
+                          act + static_cast<size_t>(base) * I);
 }
 
 // ---------------------------------------------------------------------------
@@ -357,22 +407,18 @@ __global__ __launch_bounds__(256) void down_combine_gemv_kernel(
 // for bit.
 // ---------------------------------------------------------------------------
 // FULL: I == DNC * 256 and H % (8 R) == 0, so no chunk or row is guarded.
+// Block (bx, slot s) of the down GEMV: the slot's pairs p0 .. p0 + n - 1,
+// act row pos read at act + pos * I (act already offset for a second pass).
 template <int DNC, int R, bool FULL>
-__global__ __launch_bounds__(256) void down_rows_kernel(
-    const uint16_t* __restrict__ act, int I, int H,
-    const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ active,
-    uint16_t* __restrict__ y) {
+__device__ __forceinline__ void down_rows_body(const uint16_t* __restrict__ act, int I, int H,
+                                               const uint16_t* __restrict__ w2, int s, int p0,
+                                               int n, const int32_t* __restrict__ sorted_pairs,
+                                               uint16_t* __restrict__ y) {
   constexpr int LV = (R >= 4) ? 2 : 1;
-  const int a = blockIdx.y;  // < n_slots: active[] has an entry (-1 past the active slots)
-  const int s = active[a];
-  if (s < 0) return;
   const int lane = threadIdx.x & 63;
   const int l5 = lane & 31;
   const int hw = (threadIdx.x >> 6) * 2 + (lane >> 5);
   const int h0 = (blockIdx.x * 8 + hw) * R;
-  const int p0 = offsets[s];
-  const int n = offsets[s + 1] - p0;
   // both halves of a wave serve the same slot: loop bounds are wave-uniform
   const uint16_t* base2 = w2 + static_cast<size_t>(s) * H * I;
   uint4 w[R][DNC];
@@ -405,6 +451,45 @@ __global__ __launch_bounds__(256) void down_rows_kernel(
     if ((l5 & ((1 << (5 - LV)) - 1)) == 0 && (FULL || h0 + r < H))
       y[static_cast<size_t>(dst) * H + h0 + r] = static_cast<uint16_t>(f32_to_bf16_bits(tot));
   }
+}
+
+template <int DNC, int R, bool FULL>
+__global__ __launch_bounds__(256) void down_rows_kernel(
+    const uint16_t* __restrict__ act, int I, int H,
+    const uint16_t* __restrict__ w2, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ sorted_pairs, const int32_t* __restrict__ active,
+    uint16_t* __restrict__ y) {
+  const int a = blockIdx.y;  // < n_slots: active[] has an entry (-1 past the active slots)
+  const int s = active[a];
+  if (s < 0) return;
+  const int p0 = offsets[s];
+  down_rows_body<DNC, R, FULL>(act, I, H, w2, s, p0, offsets[s + 1] - p0, sorted_pairs, y);
+}
+
+// The down GEMV of both passes (see gateup_gemv_two_kernel): grid rows below
+// max_active_a serve the bank's active slots, the rest the overflow's, whose
+// act rows follow the bank pass's placed pairs.  y is indexed by flat pair,
+// which each pair has in at most one pass.
+template <int DNC, int R, bool FULL>
+__global__ __launch_bounds__(256) void down_rows_two_kernel(
+    const uint16_t* __restrict__ act, int I, int H, int n_pairs, int max_active_a,
+    const uint16_t* __restrict__ w2_a, const int32_t* __restrict__ offsets_a,
+    const int32_t* __restrict__ sorted_pairs_a, const int32_t* __restrict__ active_a,
+    const int32_t* __restrict__ meta_a, const uint16_t* __restrict__ w2_b,
+    const int32_t* __restrict__ offsets_b, const int32_t* __restrict__ sorted_pairs_b,
+    const int32_t* __restrict__ active_b, uint16_t* __restrict__ y) {
+  const bool second = static_cast<int>(blockIdx.y) >= max_active_a;
+  const int a = second ? blockIdx.y - max_active_a : blockIdx.y;
+  const int32_t* offsets = second ? offsets_b : offsets_a;
+  const int s = (second ? active_b : active_a)[a];
+  if (s < 0) return;
+  const int p0 = offsets[s];
+  const int base = second ? meta_a[LMOE_META_PAIRS] : 0;
+  int n = offsets[s + 1] - p0;
+  if (second) n = second_rows(base, p0, n, n_pairs);  // the rows gate_up wrote
+  if (n <= 0) return;
+  down_rows_body<DNC, R, FULL>(act + static_cast<size_t>(base) * I, I, H, second ? w2_b : w2_a, s,
+                               p0, n, second ? sorted_pairs_b : sorted_pairs_a, y);
 }
 
 // ---------------------------------------------------------------------------
@@ -757,6 +842,72 @@ extern "C" int lmoe_grouped_mlp(const void* x, int T, int H, int I, int k,
   if (st != LMOE_OK) return st;
   return lmoe_down(act, H, I, w2_slots, n_slots, offsets, sorted_pairs, active, tile_off, meta,
                    n_pairs, block_m, path, y, stream);
+}
+
+extern "C" int lmoe_decode_mlp_two_passes(
+    const void* x, int T, int H, int I, int k, const void* w13_a, const void* w2_a, int n_slots_a,
+    const int32_t* offsets_a, const int32_t* sorted_pairs_a, const int32_t* active_a,
+    const int32_t* meta_a, const void* w13_b, const void* w2_b, int n_slots_b,
+    const int32_t* offsets_b, const int32_t* sorted_pairs_b, const int32_t* active_b,
+    int n_pairs, void* act, void* y, hipStream_t stream) {
+  int st = check_mlp_args(T, H, I, k, n_slots_a, n_pairs);
+  if (st != LMOE_OK) return st;
+  if (n_slots_b <= 0) return LMOE_ERR_ARG;
+  if (n_pairs == 0) return LMOE_OK;  // an empty batch: nothing read or written
+  if (x == nullptr || w13_a == nullptr || w2_a == nullptr || offsets_a == nullptr ||
+      sorted_pairs_a == nullptr || active_a == nullptr || meta_a == nullptr ||
+      w13_b == nullptr || w2_b == nullptr || offsets_b == nullptr || sorted_pairs_b == nullptr ||
+      active_b == nullptr || act == nullptr || y == nullptr)
+    return LMOE_ERR_ARG;
+  // the row-per-wave GEMVs only (rows up to 4096 columns)
+  const int nc = (H + 511) / 512;
+  const int dnc = (I + 255) / 256;
+  if (nc > 8 || dnc > 16) return LMOE_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(act) | reinterpret_cast<uintptr_t>(w2_a) |
+       reinterpret_cast<uintptr_t>(w2_b)) & 15u)
+    return LMOE_ERR_SHAPE;
+  const int max_a = n_pairs < n_slots_a ? n_pairs : n_slots_a;
+  const int max_b = n_pairs < n_slots_b ? n_pairs : n_slots_b;
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint16_t* w13a = static_cast<const uint16_t*>(w13_a);
+  const uint16_t* w13b = static_cast<const uint16_t*>(w13_b);
+  uint16_t* actb = static_cast<uint16_t*>(act);
+  const dim3 g4((I + 3) / 4, max_a + max_b);
+#define LMOE_GU2(NC, FULL)                                                                     \
+  hipLaunchKernelGGL((gateup_gemv_two_kernel<NC, FULL>), g4, dim3(256), 0, stream, xb, H, I, k, \
+                     n_pairs, max_a, w13a, offsets_a, sorted_pairs_a, active_a, meta_a, w13b,   \
+                     offsets_b, sorted_pairs_b, active_b, actb)
+#define LMOE_GU2N(NC)                     \
+  do {                                    \
+    if (H == (NC)*512) LMOE_GU2(NC, true); \
+    else LMOE_GU2(NC, false);             \
+  } while (0)
+  if (nc <= 2) LMOE_GU2N(2);
+  else if (nc <= 4) LMOE_GU2N(4);
+  else LMOE_GU2N(8);
+#undef LMOE_GU2N
+#undef LMOE_GU2
+  const uint16_t* w2a = static_cast<const uint16_t*>(w2_a);
+  const uint16_t* w2b = static_cast<const uint16_t*>(w2_b);
+  uint16_t* yb = static_cast<uint16_t*>(y);
+  // R = 2 rows per half wave, as launch_down_rows
+#define LMOE_DR2(DNC, FULL)                                                                       \
+  hipLaunchKernelGGL((down_rows_two_kernel<DNC, 2, FULL>), dim3((H + 15) / 16, max_a + max_b),    \
+                     dim3(256), 0, stream, actb, I, H, n_pairs, max_a, w2a, offsets_a, sorted_pairs_a,    \
+                     active_a, meta_a, w2b, offsets_b, sorted_pairs_b, active_b, yb)
+#define LMOE_DR2N(DNC)                                          \
+  do {                                                          \
+    if (I == (DNC)*256 && H % 16 == 0) LMOE_DR2(DNC, true);     \
+    else LMOE_DR2(DNC, false);                                  \
+  } while (0)
+  if (dnc <= 2) LMOE_DR2N(2);
+  else if (dnc <= 3) LMOE_DR2N(3);
+  else if (dnc <= 4) LMOE_DR2N(4);
+  else if (dnc <= 8) LMOE_DR2N(8);
+  else LMOE_DR2N(16);
+#undef LMOE_DR2N
+#undef LMOE_DR2
+  LMOE_RETURN_LAUNCH();
 }
 
 // one: a single token whose pairs sit in distinct slots (active rank a is

@@ -43,6 +43,21 @@ __device__ __forceinline__ int map_pair(const int32_t* ids, int p,
   return -2;
 }
 
+// A later pass's table whose pairs keep the row_idx that pass writes: a
+// build given one leaves those entries alone, so that two builds of one
+// layer (the bank, then the overflow table in skip mode 2) can run at the
+// same time and give the row_idx of the two run one after the other.  A null
+// table (the default) keeps nothing.
+struct RowKeep {
+  const int32_t* log2phy = nullptr;
+  int n_log2phy = 0;
+  int P = 0;
+};
+
+__device__ __forceinline__ bool kept_row(const RowKeep& keep, const int32_t* ids, int p) {
+  return keep.log2phy != nullptr && map_pair(ids, p, keep.log2phy, keep.n_log2phy, keep.P, 1) >= 0;
+}
+
 // Per-build state past the four counts: the build counter advances (the
 // one thread that publishes meta).
 __device__ __forceinline__ void publish_build(int32_t* meta) {
@@ -244,7 +259,7 @@ __device__ __forceinline__ void permute_block(
     int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_pairs,
     int32_t* __restrict__ row_idx, int32_t* __restrict__ active,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ meta, int* hist,
-    int* scan_lds, int* err_lds) {
+    int* scan_lds, int* err_lds, RowKeep keep = {}) {
   for (int s = threadIdx.x; s < P; s += blockDim.x) hist[s] = 0;
   if (threadIdx.x == 0) *err_lds = 0;
   __syncthreads();
@@ -273,7 +288,7 @@ __device__ __forceinline__ void permute_block(
       const int s = sl[c] >= 0 ? sl[c] : -1;
       const int pos = chunk_positions(s, nb, hist);  // chunks in pair order: stable
       if (p < N) {
-        if (pos >= 0 || skip != kSkipKeepRows) row_idx[p] = pos;
+        if ((pos >= 0 || skip != kSkipKeepRows) && !kept_row(keep, ids, p)) row_idx[p] = pos;
         if (pos >= 0) sorted_pairs[pos] = p;
       }
     }
@@ -322,7 +337,7 @@ __device__ __forceinline__ void permute_wave(
     int skip, int block_m, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
     int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
-    int* lds) {
+    int* lds, RowKeep keep = {}) {
   const int lane = threadIdx.x & 63;
   const int nbits = key_bits(P);
   int s[PPL], rank[PPL], cnt[PPL];
@@ -450,7 +465,7 @@ __device__ __forceinline__ void permute_wave(
       if (placed && rank[g] == 0) lds[s[g]] = pos + cnt[g];
     }
     if (p < N) {
-      if (pos >= 0 || skip != kSkipKeepRows) row_idx[p] = pos;
+      if ((pos >= 0 || skip != kSkipKeepRows) && !kept_row(keep, ids, p)) row_idx[p] = pos;
       if (pos >= 0) sorted_pairs[pos] = p;
     }
   }
@@ -490,11 +505,11 @@ __device__ __forceinline__ void permute_wave_any(
     int skip, int block_m, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ row_idx,
     int32_t* __restrict__ active, int32_t* __restrict__ tile_off, int32_t* __restrict__ meta,
-    int* lds) {
+    int* lds, RowKeep keep = {}) {
   const int spl = wave_perm_spl(P);
 #define LMOE_PW(S)                                                                                  \
   permute_wave<S, PPL>(ids, N, log2phy, n_log2phy, P, skip, block_m, counts, offsets, sorted_pairs, \
-                       row_idx, active, tile_off, meta, lds)
+                       row_idx, active, tile_off, meta, lds, keep)
   if (spl <= 1) LMOE_PW(1);
   else if (spl == 2) LMOE_PW(2);
   else if (spl == 4) LMOE_PW(4);

@@ -30,6 +30,58 @@ __global__ __launch_bounds__(64) void permute_wave_kernel(
                         sorted_pairs, row_idx, active, tile_off, meta, lds);
 }
 
+// Two builds over the same pairs in one launch, one per block: block 0
+// the bank table in skip mode 1, block 1 a later pass's table (the decode
+// overflow stage buffer) in skip mode 2.  Block 0 leaves the row_idx of the
+// pairs block 1 places (RowKeep), so the outputs are those of the two builds
+// one after the other.
+struct PermBuild {
+  const int32_t* log2phy;
+  int n_log2phy;
+  int P;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* sorted_pairs;
+  int32_t* active;
+  int32_t* tile_off;
+  int32_t* meta;
+};
+
+__device__ __forceinline__ RowKeep keep_of(bool second, const PermBuild& b) {
+  RowKeep k;
+  if (!second) {
+    k.log2phy = b.log2phy;
+    k.n_log2phy = b.n_log2phy;
+    k.P = b.P;
+  }
+  return k;
+}
+
+__global__ __launch_bounds__(1024) void permute_small_two_kernel(
+    const int32_t* __restrict__ ids, int N, int block_m, PermBuild a, PermBuild b,
+    int32_t* __restrict__ row_idx) {
+  extern __shared__ int hist[];  // [max(P_a, P_b)]
+  __shared__ int scan_lds[33];
+  __shared__ int err_lds;
+  const bool second = blockIdx.x != 0;
+  const PermBuild o = second ? b : a;
+  permute_block(ids, N, o.log2phy, o.n_log2phy, o.P, second ? kSkipKeepRows : 1, block_m,
+                o.counts, o.offsets, o.sorted_pairs, row_idx, o.active, o.tile_off, o.meta, hist,
+                scan_lds, &err_lds, keep_of(second, b));
+}
+
+template <int PPL>
+__global__ __launch_bounds__(64) void permute_wave_two_kernel(
+    const int32_t* __restrict__ ids, int N, int block_m, PermBuild a, PermBuild b,
+    int32_t* __restrict__ row_idx) {
+  extern __shared__ int lds[];  // [max(wave_perm_lds_ints(P_a), wave_perm_lds_ints(P_b))]
+  const bool second = blockIdx.x != 0;
+  const PermBuild o = second ? b : a;
+  permute_wave_any<PPL>(ids, N, o.log2phy, o.n_log2phy, o.P, second ? kSkipKeepRows : 1, block_m,
+                        o.counts, o.offsets, o.sorted_pairs, row_idx, o.active, o.tile_off,
+                        o.meta, lds, keep_of(second, b));
+}
+
 // Multi-block path, step 1: per-chunk histograms.
 __global__ __launch_bounds__(1024) void permute_hist_kernel(
     const int32_t* __restrict__ ids, int N, const int32_t* __restrict__ log2phy,
@@ -192,6 +244,56 @@ extern "C" int lmoe_permute(const int32_t* ids, int n_pairs,
   hipLaunchKernelGGL(permute_scan_scatter_kernel, dim3(nchunks), dim3(kChunk), 2 * lds, stream,
                      n_pairs, n_slots, nchunks, skip, block_m, slot_of, chunk_cnt, chunk_err,
                      counts, offsets, active, tile_off, meta, sorted_pairs, row_idx);
+  LMOE_RETURN_LAUNCH();
+}
+
+extern "C" int lmoe_permute_two_tables(
+    const int32_t* ids, int n_pairs, int block_m, int32_t* row_idx, const int32_t* log2phy_a,
+    int n_log2phy_a, int n_slots_a, int32_t* counts_a, int32_t* offsets_a, int32_t* sorted_pairs_a,
+    int32_t* active_a, int32_t* tile_off_a, int32_t* meta_a, const int32_t* log2phy_b,
+    int n_log2phy_b, int n_slots_b, int32_t* counts_b, int32_t* offsets_b,
+    int32_t* sorted_pairs_b, int32_t* active_b, int32_t* tile_off_b, int32_t* meta_b,
+    hipStream_t stream) {
+  if (n_pairs < 0 || n_slots_a <= 0 || n_slots_b <= 0 || block_m <= 0) return LMOE_ERR_ARG;
+  if (n_log2phy_a <= 0 || n_log2phy_b <= 0) return LMOE_ERR_ARG;
+  if ((n_pairs > 0 && ids == nullptr) || row_idx == nullptr || log2phy_a == nullptr ||
+      log2phy_b == nullptr)
+    return LMOE_ERR_ARG;
+  if (counts_a == nullptr || offsets_a == nullptr || sorted_pairs_a == nullptr ||
+      active_a == nullptr || tile_off_a == nullptr || meta_a == nullptr || counts_b == nullptr ||
+      offsets_b == nullptr || sorted_pairs_b == nullptr || active_b == nullptr ||
+      tile_off_b == nullptr || meta_b == nullptr)
+    return LMOE_ERR_ARG;
+  if (n_slots_a > kMaxSlots || n_slots_b > kMaxSlots) return LMOE_ERR_SHAPE;
+  // one block per table: the multi-block builds are left to lmoe_permute
+  if (n_pairs > kChunk) return LMOE_ERR_SHAPE;
+  const PermBuild a{log2phy_a, n_log2phy_a, n_slots_a, counts_a, offsets_a, sorted_pairs_a,
+                    active_a, tile_off_a, meta_a};
+  const PermBuild b{log2phy_b, n_log2phy_b, n_slots_b, counts_b, offsets_b, sorted_pairs_b,
+                    active_b, tile_off_b, meta_b};
+  if (wave_perm_fits(n_pairs, n_slots_a) && wave_perm_fits(n_pairs, n_slots_b)) {
+    const int ints_a = wave_perm_lds_ints(n_slots_a);
+    const int ints_b = wave_perm_lds_ints(n_slots_b);
+    const size_t wlds = sizeof(int) * static_cast<size_t>(ints_a > ints_b ? ints_a : ints_b);
+#define LMOE_PW2(Q)                                                                             \
+  hipLaunchKernelGGL(permute_wave_two_kernel<Q>, dim3(2), dim3(kWave), wlds, stream, ids,        \
+                     n_pairs, block_m, a, b, row_idx)
+    const int ppl = wave_perm_ppl(n_pairs);
+    if (ppl == 1) LMOE_PW2(1);
+    else if (ppl == 2) LMOE_PW2(2);
+    else LMOE_PW2(4);
+#undef LMOE_PW2
+    LMOE_RETURN_LAUNCH();
+  }
+  // the larger table sets the block's threads and LDS (as lmoe_permute's
+  // one-block path sizes them for one table)
+  const int P = n_slots_a > n_slots_b ? n_slots_a : n_slots_b;
+  int threads = n_pairs > P / 16 ? n_pairs : P / 16;
+  threads = ((threads + 63) / 64) * 64;
+  threads = threads < 64 ? 64 : (threads > kChunk ? kChunk : threads);
+  hipLaunchKernelGGL(permute_small_two_kernel, dim3(2), dim3(threads),
+                     sizeof(int) * static_cast<size_t>(P), stream, ids, n_pairs, block_m, a, b,
+                     row_idx);
   LMOE_RETURN_LAUNCH();
 }
 

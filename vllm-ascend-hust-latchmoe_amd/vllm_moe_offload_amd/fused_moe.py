@@ -169,21 +169,57 @@ def _pass_path(n_pairs: int, I: int, path: int) -> int:
         else native.LMOE_PATH_MFMA
 
 
-def _overflow_pass(hidden, topk_ids, k: int, overflow: PreparedSlotWeights, ws: MoEWorkspace, *, decode: bool):
-    """Second pass of a decode step whose routed experts exceed the bank:
-    the pairs the overflow table maps (every other pair is skipped) run from
-    the stage buffer into their rows of y."""
+def _overflow_perm(hidden, k: int, overflow: PreparedSlotWeights, ws: MoEWorkspace) -> native.Permutation:
+    """The workspace's permutation buffers of the overflow table."""
+    return ws.overflow_perm(hidden.shape[0] * k, int(overflow.physical_expert_count), hidden.device)
+
+
+def _overflow_permute(hidden, topk_ids, k: int, overflow: PreparedSlotWeights, ws: MoEWorkspace, *,
+                      decode: bool) -> native.Permutation:
+    """The second pass's permutation: the pairs the overflow table maps
+    (every other pair is skipped).  The bank pass's row_idx then marks the
+    pairs placed by either pass: the combine's row mask."""
     T, H = hidden.shape
     P2 = int(overflow.physical_expert_count)
     I = int(overflow.w1.shape[1]) // 2
-    perm = ws.overflow_perm(T * k, P2, hidden.device)
+    perm = _overflow_perm(hidden, k, overflow, ws)
     bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P2, H, I, hidden.device, n_pairs=T * k)
-    # the bank pass's row_idx marks the pairs placed by either pass: the
-    # combine's row mask
     native.permute(topk_ids, perm, log2phy=overflow.log2phy, keep_rows=True, row_idx=ws.perm.row_idx,
                    block_m=bm)
+    return perm
+
+
+def _overflow_pass(hidden, topk_ids, k: int, overflow: PreparedSlotWeights, ws: MoEWorkspace, *, decode: bool):
+    """Second pass of a decode step whose routed experts exceed the bank:
+    the pairs the overflow table maps run from the stage buffer into their
+    rows of y."""
+    T = hidden.shape[0]
+    perm = _overflow_permute(hidden, topk_ids, k, overflow, ws, decode=decode)
     native.grouped_mlp(hidden, k, overflow.w1, overflow.w2, perm, ws.act[: T * k], ws.y[: T * k],
                        path=native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA)
+
+
+def _merged_passes(hidden, I: int, decode: bool) -> bool:
+    """Whether a decode overflow layer runs both passes' GEMVs in shared
+    launches (decode_mlp_two_passes): the decode GEMV path with rows of at
+    most TWO_PASS_MAX_COLS columns.  In the 48-layer B=64 decode graph
+    (Qwen3-30B-A3B shapes, ~33 of 48 layers with an overflow pass) shared
+    launches took the layer from 186.0 to 180.2 us, and both tables' builds
+    in one permutation launch on top of them to 176.0 us (same box)."""
+    return decode and hidden.shape[1] <= native.TWO_PASS_MAX_COLS and I <= native.TWO_PASS_MAX_COLS
+
+
+def _two_passes(hidden, topk_ids, k: int, w13_slots, w2_slots, overflow: PreparedSlotWeights,
+                ws: MoEWorkspace, perm: native.Permutation | None = None) -> None:
+    """Both passes of a decode overflow layer after the bank permutation
+    (skip_unmapped): the overflow permutation (unless perm already holds
+    it), then one gate_up and one down launch serve both; y[pair] has the
+    bits of the passes run one by one."""
+    T = hidden.shape[0]
+    if perm is None:
+        perm = _overflow_permute(hidden, topk_ids, k, overflow, ws, decode=True)
+    native.decode_mlp_two_passes(hidden, k, w13_slots, w2_slots, ws.perm, overflow.w1, overflow.w2, perm,
+                                 ws.act[: T * k], ws.y[: T * k])
 
 
 def _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2phy, *, add=None, out=None,
@@ -202,18 +238,27 @@ def _fused_experts_ws(hidden, topk_weights, topk_ids, w13_slots, w2_slots, log2p
         path = native.LMOE_PATH_MFMA
     decode = T * k <= native.FUSED_DECODE_MAX_PAIRS and path != native.LMOE_PATH_MFMA
     bm = native.MFMA_BLOCK_M if decode else native.prefill_block_m(P, H, I, hidden.device, n_pairs=T * k)
+    merged = overflow is not None and log2phy is not None and _merged_passes(hidden, I, decode) and not events
     if events:
         events[0].record()
-    native.permute(topk_ids, ws.perm, log2phy=log2phy, skip_unmapped=overflow is not None, block_m=bm)
+    perm_b = None
+    if merged:  # both tables' builds in one launch
+        perm_b = _overflow_perm(hidden, k, overflow, ws)
+        native.permute_two_tables(topk_ids, ws.perm, log2phy, perm_b, overflow.log2phy, block_m=bm)
+    else:
+        native.permute(topk_ids, ws.perm, log2phy=log2phy, skip_unmapped=overflow is not None, block_m=bm)
     if overflow is not None:
-        mlp_path = native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA
-        native.gateup_silu(hidden, k, w13_slots, ws.perm, ws.act[: T * k], path=mlp_path)
-        if events:
-            events[1].record()
-        native.down(ws.act[: T * k], w2_slots, ws.perm, ws.y[: T * k], path=mlp_path)
-        _overflow_pass(hidden, topk_ids, k, overflow, ws, decode=decode)
-        if events:
-            events[2].record()
+        if merged:
+            _two_passes(hidden, topk_ids, k, w13_slots, w2_slots, overflow, ws, perm_b)
+        else:
+            mlp_path = native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA
+            native.gateup_silu(hidden, k, w13_slots, ws.perm, ws.act[: T * k], path=mlp_path)
+            if events:
+                events[1].record()
+            native.down(ws.act[: T * k], w2_slots, ws.perm, ws.y[: T * k], path=mlp_path)
+            _overflow_pass(hidden, topk_ids, k, overflow, ws, decode=decode)
+            if events:
+                events[2].record()
         native.combine(ws.y[: T * k], topk_weights, dst, row_mask=ws.perm.row_idx[: T * k], add=add)
         return dst, ws
     if decode:
@@ -284,18 +329,26 @@ def decode_layer(
         renormalize=bool(spec.renormalize), routed_scaling_factor=float(spec.routed_scaling_factor),
         n_shared=int(spec.n_shared), w_bf16=w_out, ids=ids_out, skip_unmapped=overflow is not None,
     )
+    I = int(w13_slots.shape[1]) // 2
+    decode = T * kw <= native.FUSED_DECODE_MAX_PAIRS and I <= native.GEMV_MAX_I
+    merged = overflow is not None and log2phy is not None and _merged_passes(hidden, I, decode)
+    perm_b = None
     if T <= ONE_LAUNCH_ROUTER_MAX_TOKENS:
         w, ids, _ = native.router_gate_topk_permute(hidden, gate_weight, logits_out, k, ws.perm, **sel)
     else:
         logits = native.router_gate(hidden, gate_weight, logits_out)
+        if merged:  # the overflow table's build rides with the bank's
+            perm_b = _overflow_perm(hidden, kw, overflow, ws)
+            sel["second"] = (perm_b, overflow.log2phy)
         w, ids, _ = native.router_topk_permute(logits, k, ws.perm, **sel)
     dst = out if out is not None else ws.out[:T]
-    I = int(w13_slots.shape[1]) // 2
     if overflow is not None:
-        decode = T * kw <= native.FUSED_DECODE_MAX_PAIRS and I <= native.GEMV_MAX_I
-        native.grouped_mlp(hidden, kw, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], ws.y[: T * kw],
-                           path=native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA)
-        _overflow_pass(hidden, ids, kw, overflow, ws, decode=decode)
+        if merged:
+            _two_passes(hidden, ids, kw, w13_slots, w2_slots, overflow, ws, perm_b)
+        else:
+            native.grouped_mlp(hidden, kw, w13_slots, w2_slots, ws.perm, ws.act[: T * kw], ws.y[: T * kw],
+                               path=native.LMOE_PATH_GEMV if decode else native.LMOE_PATH_MFMA)
+            _overflow_pass(hidden, ids, kw, overflow, ws, decode=decode)
         native.combine(ws.y[: T * kw], w, dst, row_mask=ws.perm.row_idx[: T * kw], add=add)
         return dst, w, ids
     if T * kw <= native.FUSED_DECODE_MAX_PAIRS and I <= native.GEMV_MAX_I:

@@ -37,6 +37,8 @@ PART_BLOCK_M = 320  # row tiles of the one-workgroup-per-CU prefill GEMM (lmoe_g
 FUSED_DECODE_MAX_PAIRS = 1024
 SKIP_KEEP_ROWS = 2  # LMOE_SKIP_KEEP_ROWS: lmoe_permute mode of the later passes of a multi-pass layer
 GEMV_MAX_I = 4096  # the decode GEMV kernels hold at most 16 chunks of 256 act columns
+TWO_PASS_MAX_COLS = 4096  # lmoe_decode_mlp_two_passes: the row-per-wave GEMVs only
+PERMUTE_TWO_MAX_PAIRS = 1024  # lmoe_permute_two_tables: one workgroup per table
 
 EXPORTED_SYMBOLS = (
     "lmoe_status_string",
@@ -48,10 +50,12 @@ EXPORTED_SYMBOLS = (
     "lmoe_router_gate_topk_permute",
     "lmoe_permute_workspace_bytes",
     "lmoe_permute",
+    "lmoe_permute_two_tables",
     "lmoe_gather_rows",
     "lmoe_grouped_mlp",
     "lmoe_gateup_silu",
     "lmoe_down",
+    "lmoe_decode_mlp_two_passes",
     "lmoe_combine",
     "lmoe_fused_moe_decode",
     "lmoe_fused_moe_decode_noalloc",
@@ -94,6 +98,11 @@ _SIGNATURES = {
         _i,
         [_vp, _i, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
+    "lmoe_permute_two_tables": (
+        _i,
+        [_vp, _i, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp,
+         _vp, _vp],
+    ),
     "lmoe_gather_rows": (_i, [_vp, _i, _i, _vp, _vp, _i, _vp, _vp]),
     "lmoe_grouped_mlp": (
         _i,
@@ -104,6 +113,11 @@ _SIGNATURES = {
         [_vp, _i, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp],
     ),
     "lmoe_down": (_i, [_vp, _i, _i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
+    "lmoe_decode_mlp_two_passes": (
+        _i,
+        [_vp, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _i, _vp,
+         _vp, _vp],
+    ),
     "lmoe_combine": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "lmoe_fused_moe_decode": (
         _i,
@@ -340,11 +354,16 @@ def router_topk_permute(
     w_bf16: torch.Tensor | None = None,
     ids: torch.Tensor | None = None,
     w_f32: torch.Tensor | None = None,
+    second: "tuple[Permutation, torch.Tensor] | None" = None,
     stream=None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
     """router_topk then permute into perm, in one launch when the shape allows
     it (T <= 16, E <= 256); otherwise the two launches.  For a slot table
-    (log2phy) that is final before the router runs."""
+    (log2phy) that is final before the router runs.  second = (permutation,
+    table) of a later pass over the same ids (the decode overflow stage
+    buffer; perm is then built with skip_unmapped): built after perm in skip
+    mode 2 on perm.row_idx, in the same launch as perm when the selection
+    runs on its own (permute_two_tables)."""
     lib = load_library()
     if logits.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("logits must be bf16 or f32")
@@ -370,6 +389,8 @@ def router_topk_permute(
     if log2phy is not None:
         _need(log2phy, "log2phy", torch.int32)
         n_table = int(log2phy.numel())
+    if second is not None and (log2phy is None or not skip_unmapped):
+        raise ValueError("a second pass needs the first pass's table with skip_unmapped")
     bm = MFMA_BLOCK_M if block_m is None else int(block_m)
     status = lib.lmoe_router_topk_permute(
         _ptr(logits), int(logits.dtype == torch.float32), T, E, int(top_k), int(n_shared), mode,
@@ -386,11 +407,17 @@ def router_topk_permute(
                     topk_group=topk_group, renormalize=renormalize,
                     routed_scaling_factor=routed_scaling_factor, n_shared=n_shared, w_bf16=w_bf16, ids=ids,
                     w_f32=w_f32, stream=stream)
-        permute(ids, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, block_m=bm, stream=stream)
+        if second is not None:
+            permute_two_tables(ids, perm, log2phy, second[0], second[1], block_m=bm, stream=stream)
+        else:
+            permute(ids, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, block_m=bm, stream=stream)
         return w_bf16, ids, w_f32
     _check(status, "lmoe_router_topk_permute")
     perm.builds += 1
     perm.block_m = bm
+    if second is not None:
+        permute(ids, second[0], log2phy=second[1], keep_rows=True, row_idx=perm.row_idx, block_m=bm,
+                stream=stream)
     return w_bf16, ids, w_f32
 
 
@@ -612,6 +639,49 @@ def permute(
     return perm
 
 
+def permute_two_tables(
+    ids: torch.Tensor,
+    perm: Permutation,
+    log2phy: torch.Tensor,
+    second: Permutation,
+    second_log2phy: torch.Tensor,
+    *,
+    block_m: int = MFMA_BLOCK_M,
+    stream=None,
+) -> tuple[Permutation, Permutation]:
+    """permute(ids, perm, log2phy, skip_unmapped=True) followed by
+    permute(ids, second, second_log2phy, keep_rows=True, row_idx=perm.row_idx)
+    (the bank and overflow-table builds of a decode overflow layer), in one
+    launch up to PERMUTE_TWO_MAX_PAIRS pairs, as the two calls past that."""
+    lib = load_library()
+    _need(ids, "topk_ids", torch.int32)
+    _need(log2phy, "log2phy", torch.int32)
+    _need(second_log2phy, "second_log2phy", torch.int32)
+    n = int(ids.numel())
+    if n != perm.n_pairs or n != second.n_pairs:
+        raise ValueError(f"permutation buffers sized for {perm.n_pairs} / {second.n_pairs} pairs, got {n}")
+    if n > PERMUTE_TWO_MAX_PAIRS:
+        permute(ids, perm, log2phy=log2phy, skip_unmapped=True, block_m=block_m, stream=stream)
+        permute(ids, second, log2phy=second_log2phy, keep_rows=True, row_idx=perm.row_idx, block_m=block_m,
+                stream=stream)
+        return perm, second
+    _check(
+        lib.lmoe_permute_two_tables(
+            _ptr(ids), n, int(block_m), _ptr(perm.row_idx),
+            _ptr(log2phy), int(log2phy.numel()), perm.n_slots, _ptr(perm.counts), _ptr(perm.offsets),
+            _ptr(perm.sorted_pairs), _ptr(perm.active), _ptr(perm.tile_off), _ptr(perm.meta),
+            _ptr(second_log2phy), int(second_log2phy.numel()), second.n_slots, _ptr(second.counts),
+            _ptr(second.offsets), _ptr(second.sorted_pairs), _ptr(second.active), _ptr(second.tile_off),
+            _ptr(second.meta), _stream(stream),
+        ),
+        "lmoe_permute_two_tables",
+    )
+    for p in (perm, second):
+        p.block_m = int(block_m)
+        p.builds += 1
+    return perm, second
+
+
 def gather_rows(x: torch.Tensor, top_k: int, perm: Permutation, out: torch.Tensor | None = None,
                 *, stream=None) -> torch.Tensor:
     """expanded_x: out[pos] = x[sorted_pairs[pos] // top_k]."""
@@ -720,6 +790,53 @@ def down(act: torch.Tensor, w2_slots: torch.Tensor, perm: Permutation, y: torch.
             _ptr(perm.tile_off), _ptr(perm.meta), perm.n_pairs, perm.block_m, int(path), _ptr(y), _stream(stream),
         ),
         "lmoe_down",
+    )
+    return y
+
+
+def decode_mlp_two_passes(
+    x: torch.Tensor,
+    top_k: int,
+    w13_a: torch.Tensor,
+    w2_a: torch.Tensor,
+    perm_a: Permutation,
+    w13_b: torch.Tensor,
+    w2_b: torch.Tensor,
+    perm_b: Permutation,
+    act: torch.Tensor,
+    y: torch.Tensor,
+    *,
+    stream=None,
+) -> torch.Tensor:
+    """The decode GEMVs of both passes of an overflow layer (bank a, overflow
+    stage buffer b, each with its own permutation over the same ids) in one
+    gate_up and one down launch; y[pair] as grouped_mlp(path=GEMV) writes it
+    for either pass.  The tables must map disjoint experts.  Rows up to
+    TWO_PASS_MAX_COLS columns (H and I): past that, run the passes one by
+    one (grouped_mlp)."""
+    lib = load_library()
+    _need(x, "x", torch.bfloat16)
+    T, H = x.shape
+    Pa, I = _check_bank(w13_a, w2_a, H)
+    Pb, Ib = _check_bank(w13_b, w2_b, H)
+    if Ib != I:
+        raise ValueError("the two passes' banks have different intermediate sizes")
+    if H > TWO_PASS_MAX_COLS or I > TWO_PASS_MAX_COLS:
+        raise ValueError(f"rows past {TWO_PASS_MAX_COLS} columns: run the passes one by one")
+    if Pa != perm_a.n_slots or Pb != perm_b.n_slots:
+        raise ValueError("a slot bank does not match its permutation")
+    if perm_a.n_pairs != T * top_k or perm_b.n_pairs != T * top_k:
+        raise ValueError("permutations do not match T * top_k pairs")
+    _need(act, "act", torch.bfloat16, (perm_a.n_pairs, I))
+    _need(y, "y", torch.bfloat16, (perm_a.n_pairs, H))
+    _check(
+        lib.lmoe_decode_mlp_two_passes(
+            _ptr(x), T, H, I, int(top_k), _ptr(w13_a), _ptr(w2_a), Pa, _ptr(perm_a.offsets),
+            _ptr(perm_a.sorted_pairs), _ptr(perm_a.active), _ptr(perm_a.meta), _ptr(w13_b), _ptr(w2_b), Pb,
+            _ptr(perm_b.offsets), _ptr(perm_b.sorted_pairs), _ptr(perm_b.active), perm_a.n_pairs, _ptr(act),
+            _ptr(y), _stream(stream),
+        ),
+        "lmoe_decode_mlp_two_passes",
     )
     return y
 
