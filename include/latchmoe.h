@@ -203,6 +203,37 @@ int lmoe_router_gate_topk_permute(const void* x, const void* wg, int T, int H,
                                   int32_t* meta, int32_t* sync,
                                   hipStream_t stream);
 
+/* One token (T == 1): lmoe_router_gate_topk_permute's gate and selection
+ * (the same logits, w_f32, w_bf16 and ids, bit for bit, and the same sync
+ * and meta protocol), then the token's pairs in pair order instead of the
+ * slot-sorted permutation: the placed pairs take positions 0, 1, ... in
+ * pair order, active[pos] = the slot of the pos-th placed pair,
+ * sorted_pairs[pos] = that pair, row_idx[j] = pair j's position or -1, and
+ * active[a] = -1 for a from the placed count to n_slots - 1; meta[ACTIVE]
+ * = meta[PAIRS] = the placed pairs, meta[ERRORS] as lmoe_permute counts
+ * them, GEN advanced; counts, offsets and tile_off are not touched.  A pair
+ * whose id maps to no slot is placed nowhere (skip_unmapped as in
+ * lmoe_permute).  With distinct slots (a router-fed token) this is a
+ * permutation of the one-token kernels' form (every slot serves one pair,
+ * position a is active rank a): lmoe_fused_moe_decode with distinct_slots
+ * gives the same bits from it as from the sorted permutation.  It saves the
+ * sort at the end of the router's dependent chain.  No counterpart in the
+ * reference, whose permutation is always slot-sorted
+ * (patch_fused_moe.py:668-701); the gate and selection replace
+ * moe_router_op.py:108-124, 228-231.  LMOE_ERR_SHAPE as
+ * lmoe_router_gate_topk_permute with T = 1. */
+int lmoe_router_gate_topk_pairs(const void* x, const void* wg, int H, int E,
+                                void* logits, int logits_f32, int k,
+                                int n_shared, int scoring, const float* bias,
+                                const float* logit_bias, int n_group,
+                                int topk_group, int renorm, float routed_scale,
+                                float* w_f32, uint16_t* w_bf16, int32_t* ids,
+                                const int32_t* log2phy, int n_log2phy,
+                                int n_slots, int skip_unmapped,
+                                int32_t* sorted_pairs, int32_t* row_idx,
+                                int32_t* active, int32_t* meta, int32_t* sync,
+                                hipStream_t stream);
+
 /* Bytes of device workspace lmoe_permute needs for n_pairs pairs, n_slots. */
 size_t lmoe_permute_workspace_bytes(int n_pairs, int n_slots);
 

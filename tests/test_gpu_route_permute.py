@@ -161,6 +161,9 @@ def test_decode_layer_equals_route_then_fused_experts(T):
     assert torch.equal(ids1, ids2)
     assert torch.equal(w1.view(torch.int16), w2_.view(torch.int16))
     assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    if T == 1:  # one token: the layer's router leaves the pairs in pair order
+        _check_pair_order(native, ws_b.perm, ids2.cpu().numpy(), l2p, P, False)
+        return
     for name in ("counts", "offsets", "sorted_pairs", "row_idx", "active", "tile_off", "meta"):
         a, b = getattr(ws_a.perm, name), getattr(ws_b.perm, name)
         # meta: the four counts (past them, build count and decode hand-off state)
@@ -346,3 +349,131 @@ def test_one_token_one_launch_router_with_ties_equals_separate_calls_and_oracle(
             # the steered step really selects tied experts
             vals = lg[0, r_ids[0]]
             assert np.unique(vals).size < k, "no tie among the selected experts"
+
+
+def _check_pair_order(native, perm, ids, l2p, P, skip, n_shared_ids=()):
+    """The one-token pair-order outputs against the oracle's remap: the
+    placed pairs at positions 0, 1, ... in pair order."""
+    flat = ids.reshape(-1)
+    slot = operm.remap(flat, l2p, P, skip_unmapped=skip)
+    placed = np.flatnonzero(slot >= 0)
+    n = placed.size
+    row_idx = perm.row_idx.cpu().numpy()[: flat.size]
+    want_rows = np.full(flat.size, -1)
+    want_rows[placed] = np.arange(n)
+    np.testing.assert_array_equal(row_idx, want_rows)
+    np.testing.assert_array_equal(perm.sorted_pairs.cpu().numpy()[:n], placed)
+    active = perm.active.cpu().numpy()
+    np.testing.assert_array_equal(active[:n], slot[placed])
+    assert (active[n:P] == -1).all()
+    meta = perm.meta.cpu().numpy()
+    assert list(meta[:3]) == [n, n, int((slot == -2).sum())]
+    assert meta[native.META_GEN] == perm.builds
+    return n
+
+
+@pytest.mark.parametrize("E,k,S,P,H,scoring,table", [
+    (128, 8, 0, 64, 2048, "softmax", "map"),      # the Qwen3-shaped decode replay
+    (128, 8, 0, 128, 2048, "softmax", "none"),    # no table: ids are slots
+    (128, 8, 0, 64, 1536, "softmax", "skip"),     # guarded gate rows; two pairs left to another pass
+    (128, 8, 0, 64, 2048, "softmax", "error"),    # a selected expert in no slot: an error
+    (256, 8, 1, 300, 7168, "sigmoid", "map"),     # grouped sigmoid, long rows, a shared expert
+])
+def test_pair_order_router_equals_one_launch_router(E, k, S, P, H, scoring, table):
+    """lmoe_router_gate_topk_pairs gives lmoe_router_gate_topk_permute's
+    logits, ids and weights bit for bit (three calls in a row: the arrival
+    counter is back at zero after each), and the pairs in pair order against
+    the oracle's remap."""
+    native = _native()
+    print(f"case pair-order router E={E} k={k} S={S} P={P} H={H} {scoring} table={table}", flush=True)
+    rng = np.random.default_rng(300 + E + H)
+    grouped = scoring == "sigmoid"
+    kw = dict(scoring=scoring, num_expert_group=8 if grouped else 1, topk_group=4 if grouped else 1,
+              routed_scaling_factor=2.5 if grouped else 1.0, n_shared=S)
+    bias = torch.from_numpy((rng.standard_normal(E) * 0.01).astype(np.float32)).cuda()
+    wg = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
+    kwp = k + S
+    perm_a = native.Permutation.allocate(kwp, P, "cuda")
+    perm_b = native.Permutation.allocate(kwp, P, "cuda")
+    perm_b.active.fill_(77)  # stale entries the call must overwrite
+    for it in range(3):
+        x = to_dev_bf16(normal_bf16(rng, (1, H), 1.0))
+        lg0 = torch.empty((1, E), dtype=torch.bfloat16, device="cuda")
+        native.router_gate(x, wg, lg0)
+        _, ids0, _ = native.router_topk(lg0, k, bias=bias, **kw)
+        used = np.unique(ids0.cpu().numpy())
+        skip = table == "skip"
+        if table == "none":
+            l2p, d_l2p = None, None
+        else:
+            l2p = np.full(E + S, -1, dtype=np.int32)
+            l2p[used] = rng.permutation(P)[: used.size]
+            if table in ("skip", "error"):
+                l2p[used[:2]] = -1  # in no slot of this table
+            d_l2p = to_dev_i32(l2p)
+        lg_a = torch.empty((1, E), dtype=torch.bfloat16, device="cuda")
+        wa, ida, wfa = native.router_gate_topk_permute(x, wg, lg_a, k, perm_a, log2phy=d_l2p, bias=bias,
+                                                       skip_unmapped=skip, w_f32=torch.empty((1, kwp), device="cuda"),
+                                                       **kw)
+        lg_b = torch.empty((1, E), dtype=torch.bfloat16, device="cuda")
+        wb, idb, wfb = native.router_gate_topk_pairs(x, wg, lg_b, k, perm_b, log2phy=d_l2p, bias=bias,
+                                                     skip_unmapped=skip, w_f32=torch.empty((1, kwp), device="cuda"),
+                                                     **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(lg_a.view(torch.int16), lg_b.view(torch.int16)), it
+        assert torch.equal(ida, idb), it
+        assert torch.equal(wa.view(torch.int16), wb.view(torch.int16)), it
+        assert torch.equal(wfa.view(torch.int32), wfb.view(torch.int32)), it
+        ids_np = idb.cpu().numpy()
+        n = _check_pair_order(native, perm_b, ids_np, l2p, P, skip)
+        assert n == (kwp - 2 if table in ("skip", "error") else kwp)
+        assert perm_b.sync[0].item() == 0
+        assert perm_b.meta[native.META_ROUTER_TIMEOUT].item() == 0
+
+
+@pytest.mark.parametrize("E,k,S,P,H,I,scoring", [
+    (128, 8, 0, 64, 2048, 768, "softmax"),
+    (256, 8, 1, 64, 7168, 2048, "sigmoid"),   # nine pairs: a half wave takes two slots
+])
+def test_one_token_body_from_pair_order_equals_sorted(E, k, S, P, H, I, scoring):
+    """fused_moe_decode(distinct_slots=True) from the pair-order router's
+    outputs gives the bits it gives from the sorted permutation (with an add
+    term), and decode_layer at one token (which takes the pair order) equals
+    route() + fused_experts()."""
+    native = _native()
+    from vllm_moe_offload_amd import fused_moe
+
+    print(f"case one-token body pair order E={E} H={H} I={I}", flush=True)
+    rng = np.random.default_rng(900 + E)
+    grouped = scoring == "sigmoid"
+    kw = dict(scoring=scoring, num_expert_group=8 if grouped else 1, topk_group=4 if grouped else 1,
+              routed_scaling_factor=2.5 if grouped else 1.0, n_shared=S)
+    kwp = k + S
+    wg = to_dev_bf16(normal_bf16(rng, (E, H), 0.02))
+    w13 = to_dev_bf16(normal_bf16(rng, (P, 2 * I, H), 0.02))
+    w2 = to_dev_bf16(normal_bf16(rng, (P, H, I), 0.02))
+    x = to_dev_bf16(normal_bf16(rng, (1, H), 1.0))
+    add = to_dev_bf16(normal_bf16(rng, (1, H), 0.5))
+    l2p = np.full(E + S, -1, dtype=np.int32)
+    l2p[rng.permutation(E + S)[:P]] = rng.permutation(P)
+    # make sure the selected experts are in slots: route once, then map them
+    lg0 = torch.empty((1, E), dtype=torch.bfloat16, device="cuda")
+    native.router_gate(x, wg, lg0)
+    _, ids0, _ = native.router_topk(lg0, k, **kw)
+    used = np.unique(ids0.cpu().numpy())
+    l2p[:] = -1
+    l2p[used] = rng.permutation(P)[: used.size]
+    d_l2p = to_dev_i32(l2p)
+    outs = []
+    for form in ("sorted", "pairs"):
+        perm = native.Permutation.allocate(kwp, P, "cuda")
+        lg = torch.empty((1, E), dtype=torch.bfloat16, device="cuda")
+        router = native.router_gate_topk_permute if form == "sorted" else native.router_gate_topk_pairs
+        w, ids, _ = router(x, wg, lg, k, perm, log2phy=d_l2p, **kw)
+        act = torch.empty((kwp, I), dtype=torch.bfloat16, device="cuda")
+        y = torch.empty((kwp, H), dtype=torch.bfloat16, device="cuda")
+        out = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
+        native.fused_moe_decode(x, w, w13, w2, perm, act, out, add=add, y=y, distinct_slots=True)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

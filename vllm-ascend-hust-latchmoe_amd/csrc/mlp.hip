@@ -173,9 +173,11 @@ __global__ __launch_bounds__(256) void gateup_gemv_two_kernel(
 // pair.  The four waves' partial sums meet in LDS (double-buffered by token
 // parity, one barrier per token) and wave 0 adds them in wave order.  Every
 // token's act is computed the same way whatever the batch, so one token
-// alone gives the bits it gets in a batch.
+// alone gives the bits it gets in a batch.  ONE: T == 1 with every slot
+// serving one pair (active rank a is position a, the x row is row 0), as in
+// gateup_gemv_kernel: offsets and sorted_pairs are not read.
 // ---------------------------------------------------------------------------
-template <int NC, int RP>
+template <int NC, int RP, bool ONE>
 __global__ __launch_bounds__(256) void gateup_gemv_cols_kernel(
     const uint16_t* __restrict__ x, int H, int I, int topk,
     const uint16_t* __restrict__ w13, const int32_t* __restrict__ offsets,
@@ -207,12 +209,12 @@ __global__ __launch_bounds__(256) void gateup_gemv_cols_kernel(
       }
     }
   }
-  const int p0 = offsets[s];
-  const int n = offsets[s + 1] - p0;
-  int t_next = n > 0 ? sorted_pairs[p0] / topk : 0;
+  const int p0 = ONE ? a : offsets[s];
+  const int n = ONE ? 1 : offsets[s + 1] - p0;
+  int t_next = (!ONE && n > 0) ? sorted_pairs[p0] / topk : 0;
   for (int r = 0; r < n; ++r) {
     const int t = t_next;
-    if (r + 1 < n) t_next = sorted_pairs[p0 + r + 1] / topk;
+    if (!ONE && r + 1 < n) t_next = sorted_pairs[p0 + r + 1] / topk;
     const uint16_t* xr = x + static_cast<size_t>(t) * H;
     float v[NR];
 #pragma unroll
@@ -596,14 +598,16 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
     if (one) LMOE_GU1(NC, true); \
     else LMOE_GU1(NC, false);    \
   } while (0)
-#define LMOE_GC(NC, RP)                                                                      \
-  hipLaunchKernelGGL((gateup_gemv_cols_kernel<NC, RP>), dim3((I + (RP)-1) / (RP), max_active),  \
-                     dim3(256), 0, stream, x, H, I, topk, w13, offsets, sorted_pairs, active, act)
+#define LMOE_GC(NC, RP, ONE)                                                                 \
+  hipLaunchKernelGGL((gateup_gemv_cols_kernel<NC, RP, ONE>), dim3((I + (RP)-1) / (RP),         \
+                     max_active), dim3(256), 0, stream, x, H, I, topk, w13, offsets,              \
+                     sorted_pairs, active, act)
   if (cols) {
     // the four waves split each row's columns and share every x row (for
     // one token too, so that a token's act does not depend on its batch)
-    if (nc <= 16) LMOE_GC(16, 2);
-    else return LMOE_ERR_SHAPE;
+    if (nc > 16) return LMOE_ERR_SHAPE;
+    if (one) LMOE_GC(16, 2, true);
+    else LMOE_GC(16, 2, false);
     return LMOE_OK;
   }
 #undef LMOE_GC

@@ -25,11 +25,9 @@ constexpr int kMaxSlots = 8192;    // LDS histogram bound
 // is >= 0 exactly for the pairs some pass placed (the combine's row mask)
 constexpr int kSkipKeepRows = 2;
 
-// slot of pair p: >= 0 placed, -1 skipped silently, -2 error
-__device__ __forceinline__ int map_pair(const int32_t* ids, int p,
-                                        const int32_t* __restrict__ log2phy,
-                                        int n_log2phy, int P, int skip) {
-  const int id = ids[p];
+// slot of expert id `id`: >= 0 placed, -1 skipped silently, -2 error
+__device__ __forceinline__ int map_id(int id, const int32_t* __restrict__ log2phy, int n_log2phy,
+                                      int P, int skip) {
   int s;
   if (log2phy != nullptr) {
     // in wave mode an id the table does not cover belongs to another pass
@@ -41,6 +39,13 @@ __device__ __forceinline__ int map_pair(const int32_t* ids, int p,
   if (s >= 0 && s < P) return s;
   if (skip && s == -1) return -1;
   return -2;
+}
+
+// slot of pair p, as map_id
+__device__ __forceinline__ int map_pair(const int32_t* ids, int p,
+                                        const int32_t* __restrict__ log2phy,
+                                        int n_log2phy, int P, int skip) {
+  return map_id(ids[p], log2phy, n_log2phy, P, skip);
 }
 
 // A later pass's table whose pairs keep the row_idx that pass writes: a

@@ -174,10 +174,52 @@ __device__ __forceinline__ void load_logits_tagged(const uint64_t* words, uint32
     lg[j] = j * kWave + lane < E ? __uint_as_float(static_cast<uint32_t>(wv[j])) : -INFINITY;
 }
 
+// One token's pairs in pair order, for the one-token MLP kernels (which read
+// active[a] as the slot of position a, a pair of its own, and row_idx[p] as
+// pair p's position): lane j < kw holds pair j's expert e.  The placed pairs
+// take positions 0, 1, ... in pair order (a pair whose id maps to no slot
+// of the table is left out, and counted in meta[LMOE_META_ERRORS] unless
+// skip allows it, as map_id decides): active[pos] = its slot,
+// sorted_pairs[pos] = j, row_idx[j] = pos or -1, active[a] = -1 from the
+// placed count on (every a < P).  meta ACTIVE and PAIRS = the placed pairs,
+// ERRORS, and the build count advances; counts, offsets, tile_off and
+// meta[TILES] are not written.  With distinct slots this is the sorted
+// permutation with the slots in pair order: the one-token kernels compute
+// every value as from it.
+__device__ __forceinline__ void pair_order_outputs(int e, int lane, int kw,
+                                                   const int32_t* __restrict__ log2phy,
+                                                   int n_log2phy, int P, int skip,
+                                                   int32_t* __restrict__ sorted_pairs,
+                                                   int32_t* __restrict__ row_idx,
+                                                   int32_t* __restrict__ active,
+                                                   int32_t* __restrict__ meta) {
+  const int s = lane < kw ? map_id(e, log2phy, n_log2phy, P, skip) : -1;
+  const bool placed = s >= 0;
+  const uint64_t pm = __ballot(placed);
+  const int pos = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(pm >> 32),
+                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(pm), 0));
+  const int n_placed = __popcll(pm);
+  const int n_err = __popcll(__ballot(s == -2));
+  if (lane < kw) row_idx[lane] = placed ? pos : -1;
+  if (placed) {
+    sorted_pairs[pos] = lane;
+    active[pos] = s;
+  }
+  for (int a = n_placed + lane; a < P; a += kWave) active[a] = -1;
+  if (lane == 0) {
+    meta[LMOE_META_ACTIVE] = n_placed;
+    meta[LMOE_META_PAIRS] = n_placed;
+    meta[LMOE_META_ERRORS] = n_err;
+    publish_build(meta);
+  }
+}
+
 // PPL > 0: one wave permutes with PPL pairs per lane; PPL == 0: the block
 // permutation (more pairs or slots than one wave takes).  SCORE: the
 // scoring (LMOE_SCORING_*), sp.scoring must agree.  words (the one-launch
 // router): the logits come from its tagged words, see load_logits_tagged.
+// PPL < 0: one token in pair order (pair_order_outputs) instead of the
+// permutation.
 template <int EPL, int PPL, int SCORE>
 __device__ __forceinline__ void select_and_permute(
     const void* __restrict__ logits, int logits_f32, int T, const SelectParams& sp,
@@ -210,7 +252,13 @@ __device__ __forceinline__ void select_and_permute(
       w_bf16[o] = static_cast<uint16_t>(f32_to_bf16_bits(w));
       if (w_f32 != nullptr) w_f32[o] = w;
     }
+    if constexpr (PPL < 0) {
+      pair_order_outputs(e, lane, kw, log2phy, n_log2phy, P, skip, sorted_pairs, row_idx, active,
+                         meta);
+      return;
+    }
   }
+  if constexpr (PPL < 0) return;  // one token: wave 0 wrote everything
   __syncthreads();
   const int n_pairs = T * (sp.k + sp.n_shared);
   if constexpr (PPL > 0) {
@@ -365,6 +413,7 @@ struct RouterPermuteArgs {
   int32_t* active;
   int32_t* tile_off;
   int32_t* meta;
+  bool pairs;  // one token: pair-order outputs instead of the permutation
 };
 
 // Block size and dynamic LDS of the one-launch routers: enough waves for
@@ -429,7 +478,9 @@ int launch_gate_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
   // several tokens: one block row per kGateTok tokens, so no wave walks
   // the token groups in turn
   const int tgroups = a.T == 1 ? 1 : (a.T + kGateTok - 1) / kGateTok;
-  const int ppl = router_perm_ppl(a.T * (a.sp.k + a.sp.n_shared), a.n_slots);
+  // -1: the one-token pair-order outputs (pair_order_outputs)
+  const int ppl = a.pairs ? -1 : router_perm_ppl(a.T * (a.sp.k + a.sp.n_shared), a.n_slots);
+  if (a.pairs && a.T != 1) return LMOE_ERR_SHAPE;
   const uint16_t* x = static_cast<const uint16_t*>(a.x);
   const uint16_t* wg = static_cast<const uint16_t*>(a.wg);
 #define LMOE_GTP_F(NC, EPL, Q, ONE, FULL)                                                        \
@@ -444,10 +495,12 @@ int launch_gate_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
 #define LMOE_GTP_Q(NC, EPL)                          \
   do {                                               \
     if (a.T == 1 && a.H == (NC)*512) {               \
-      if (ppl == 1) LMOE_GTP_F(NC, EPL, 1, true, true); \
+      if (ppl < 0) LMOE_GTP_F(NC, EPL, -1, true, true); \
+      else if (ppl == 1) LMOE_GTP_F(NC, EPL, 1, true, true); \
       else LMOE_GTP_F(NC, EPL, 0, true, true);       \
     } else if (a.T == 1) {                           \
-      if (ppl == 1) LMOE_GTP(NC, EPL, 1, true);      \
+      if (ppl < 0) LMOE_GTP(NC, EPL, -1, true);      \
+      else if (ppl == 1) LMOE_GTP(NC, EPL, 1, true); \
       else LMOE_GTP(NC, EPL, 0, true);               \
     } else {                                         \
       if (ppl == 1) LMOE_GTP(NC, EPL, 1, false);     \
@@ -470,10 +523,12 @@ int launch_gate_topk_permute(const RouterPermuteArgs& a, hipStream_t stream) {
     // long rows: one token only (the entry point refuses more)
     if (a.T != 1) return LMOE_ERR_SHAPE;
     if (a.sp.E <= 128) {
-      if (ppl == 1) LMOE_GTP(16, 2, 1, true);
+      if (ppl < 0) LMOE_GTP(16, 2, -1, true);
+      else if (ppl == 1) LMOE_GTP(16, 2, 1, true);
       else LMOE_GTP(16, 2, 0, true);
     } else {
-      if (ppl == 1) LMOE_GTP(16, 4, 1, true);
+      if (ppl < 0) LMOE_GTP(16, 4, -1, true);
+      else if (ppl == 1) LMOE_GTP(16, 4, 1, true);
       else LMOE_GTP(16, 4, 0, true);
     }
   }

@@ -203,6 +203,54 @@ extern "C" int lmoe_router_topk_permute(
                                          : launch_topk_permute<LMOE_SCORING_SIGMOID>(ra, stream);
 }
 
+extern "C" int lmoe_router_gate_topk_pairs(
+    const void* x, const void* wg, int H, int E, void* logits, int logits_f32, int k,
+    int n_shared, int scoring, const float* bias, const float* logit_bias, int n_group,
+    int topk_group, int renorm, float routed_scale, float* w_f32, uint16_t* w_bf16, int32_t* ids,
+    const int32_t* log2phy, int n_log2phy, int n_slots, int skip_unmapped, int32_t* sorted_pairs,
+    int32_t* row_idx, int32_t* active, int32_t* meta, int32_t* sync, hipStream_t stream) {
+  if (H <= 0) return LMOE_ERR_ARG;
+  int st = check_select(1, E, k, n_shared, scoring, n_group, topk_group);
+  if (st != LMOE_OK) return st;
+  if (n_slots <= 0) return LMOE_ERR_ARG;
+  if (log2phy != nullptr && n_log2phy <= 0) return LMOE_ERR_ARG;
+  if (H % 8 != 0 || H > kGateMaxChunks * 512) return LMOE_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(wg)) & 15u)
+    return LMOE_ERR_SHAPE;
+  if (E > 256 || n_slots > kMaxSlots) return LMOE_ERR_SHAPE;
+  if (x == nullptr || wg == nullptr || logits == nullptr || w_bf16 == nullptr || ids == nullptr ||
+      sorted_pairs == nullptr || row_idx == nullptr || active == nullptr || meta == nullptr ||
+      sync == nullptr)
+    return LMOE_ERR_ARG;
+  if (reinterpret_cast<uintptr_t>(sync) & 7u) return LMOE_ERR_SHAPE;  // u64 tagged words
+  RouterPermuteArgs ra{};
+  ra.x = x;
+  ra.wg = wg;
+  ra.H = H;
+  ra.sync = sync;
+  ra.T = 1;
+  ra.logits = logits;
+  ra.logits_f32 = logits_f32;
+  ra.sp = make_select(E, k, n_shared, scoring, bias, logit_bias, n_group, topk_group, renorm,
+                      routed_scale);
+  ra.w_f32 = w_f32;
+  ra.w_bf16 = w_bf16;
+  ra.ids = ids;
+  ra.log2phy = log2phy;
+  ra.n_log2phy = n_log2phy;
+  ra.n_slots = n_slots;
+  ra.skip = skip_unmapped ? 1 : 0;
+  ra.block_m = 1;  // no tile table
+  ra.sorted_pairs = sorted_pairs;
+  ra.row_idx = row_idx;
+  ra.active = active;
+  ra.meta = meta;
+  ra.pairs = true;
+  return scoring == LMOE_SCORING_SOFTMAX
+             ? launch_gate_topk_permute<LMOE_SCORING_SOFTMAX>(ra, stream)
+             : launch_gate_topk_permute<LMOE_SCORING_SIGMOID>(ra, stream);
+}
+
 extern "C" int lmoe_router_gate_topk_permute(
     const void* x, const void* wg, int T, int H, int E, void* logits, int logits_f32, int k,
     int n_shared, int scoring, const float* bias, const float* logit_bias, int n_group,

@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "lmoe_router_topk",
     "lmoe_router_topk_permute",
     "lmoe_router_gate_topk_permute",
+    "lmoe_router_gate_topk_pairs",
     "lmoe_permute_workspace_bytes",
     "lmoe_permute",
     "lmoe_permute_two_tables",
@@ -92,6 +93,11 @@ _SIGNATURES = {
         _i,
         [_vp, _vp, _i, _i, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp,
          _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
+    "lmoe_router_gate_topk_pairs": (
+        _i,
+        [_vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _i, _i, _i,
+         _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "lmoe_permute_workspace_bytes": (_sz, [_i, _i]),
     "lmoe_permute": (
@@ -500,6 +506,85 @@ def router_gate_topk_permute(
     _check(status, "lmoe_router_gate_topk_permute")
     perm.builds += 1
     perm.block_m = bm
+    return w_bf16, ids, w_f32
+
+
+def router_gate_topk_pairs(
+    x: torch.Tensor,
+    wg: torch.Tensor,
+    logits: torch.Tensor,
+    top_k: int,
+    perm: "Permutation",
+    *,
+    log2phy: torch.Tensor | None = None,
+    skip_unmapped: bool = False,
+    scoring: str = "softmax",
+    bias: torch.Tensor | None = None,
+    logit_bias: torch.Tensor | None = None,
+    num_expert_group: int = 1,
+    topk_group: int = 1,
+    renormalize: bool = True,
+    routed_scaling_factor: float = 1.0,
+    n_shared: int = 0,
+    w_bf16: torch.Tensor | None = None,
+    ids: torch.Tensor | None = None,
+    w_f32: torch.Tensor | None = None,
+    stream=None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """One token: router_gate_topk_permute's gate and selection (the same
+    bits) with perm in the one-token pair order (lmoe_router_gate_topk_pairs:
+    the placed pairs at positions 0, 1, ... in pair order, active[pos] their
+    slots; counts, offsets and tile_off are not written), the form
+    fused_moe_decode(distinct_slots=True) reads.  Falls back to
+    router_gate_topk_permute (the sorted permutation, which that call reads
+    the same way) where the one launch does not take the shape."""
+    lib = load_library()
+    T, H = x.shape
+    E = wg.shape[0]
+    if T != 1:
+        raise ValueError("the pair-order router serves one token")
+    _need(x, "x", torch.bfloat16)
+    _need(wg, "wg", torch.bfloat16, (E, H))
+    if logits.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("logits must be bf16 or f32")
+    _need(logits, "logits", logits.dtype, (T, E))
+    mode = {"softmax": LMOE_SCORING_SOFTMAX, "sigmoid": LMOE_SCORING_SIGMOID}.get(scoring)
+    if mode is None:
+        raise ValueError(f"unsupported scoring function {scoring!r}")
+    _check_biases(bias, logit_bias, E)
+    dev = x.device
+    kw = int(top_k) + int(n_shared)
+    if w_bf16 is None:
+        w_bf16 = torch.empty((T, kw), dtype=torch.bfloat16, device=dev)
+    if ids is None:
+        ids = torch.empty((T, kw), dtype=torch.int32, device=dev)
+    _need(w_bf16, "topk_weights", torch.bfloat16, (T, kw))
+    _need(ids, "topk_ids", torch.int32, (T, kw))
+    if w_f32 is not None:
+        _need(w_f32, "w_f32", torch.float32, (T, kw))
+    if kw != perm.n_pairs:
+        raise ValueError(f"permutation buffers sized for {perm.n_pairs} pairs, got {kw}")
+    n_table = 0
+    if log2phy is not None:
+        _need(log2phy, "log2phy", torch.int32)
+        n_table = int(log2phy.numel())
+    status = lib.lmoe_router_gate_topk_pairs(
+        _ptr(x), _ptr(wg), H, E, _ptr(logits), int(logits.dtype == torch.float32), int(top_k),
+        int(n_shared), mode, _ptr(bias), _ptr(logit_bias), int(num_expert_group or 1), int(topk_group or 1),
+        int(bool(renormalize)), float(routed_scaling_factor), _ptr(w_f32), _ptr(w_bf16), _ptr(ids),
+        _ptr(log2phy), n_table, perm.n_slots, int(bool(skip_unmapped)),
+        _ptr(perm.sorted_pairs), _ptr(perm.row_idx), _ptr(perm.active), _ptr(perm.meta), _ptr(perm.sync),
+        _stream(stream),
+    )
+    if status == LMOE_ERR_SHAPE:
+        return router_gate_topk_permute(
+            x, wg, logits, top_k, perm, log2phy=log2phy, skip_unmapped=skip_unmapped, scoring=scoring,
+            bias=bias, logit_bias=logit_bias, num_expert_group=num_expert_group, topk_group=topk_group,
+            renormalize=renormalize, routed_scaling_factor=routed_scaling_factor, n_shared=n_shared,
+            w_bf16=w_bf16, ids=ids, w_f32=w_f32, stream=stream,
+        )
+    _check(status, "lmoe_router_gate_topk_pairs")
+    perm.builds += 1
     return w_bf16, ids, w_f32
 
 
