@@ -392,7 +392,10 @@ int lmoe_down_combine(const void* act, int T, int H, int I, int k,
  * Ids from elsewhere pass 0 (the general kernels; same bits when the
  * promise holds).  Needs T*k <= 1024, H % 8 == 0, I % 64 == 0, I <= 4096,
  * H <= 8192; x, slot banks, act and y 16-byte aligned.  Permutation arrays
- * as produced by lmoe_permute. */
+ * as produced by lmoe_permute; with one token and distinct_slots, also the
+ * pair-order form of lmoe_router_gate_topk_pairs (its one-token kernels
+ * read only active[] and row_idx[], not offsets or sorted_pairs), with the
+ * same out bit for bit. */
 int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
                           const void* w13_slots, const void* w2_slots,
                           int n_slots, const uint16_t* w,
