@@ -62,6 +62,18 @@ def test_empty_batch_through_router_permutation_mlp_and_combine(H, E, I, k, P):
     native.router_gate_topk_permute(x0, gate, logits0, k, perm, log2phy=l2p)
     _assert_empty(native, perm, P)
 
+    # a decode overflow layer's two tables in one build, and both passes'
+    # GEMVs in shared launches
+    perm2 = native.Permutation.allocate(0, P, dev)
+    _stale(perm)
+    _stale(perm2)
+    native.permute_two_tables(ids0, perm, l2p, perm2, l2p)
+    _assert_empty(native, perm, P)
+    _assert_empty(native, perm2, P)
+    act0 = torch.empty((0, I), dtype=torch.bfloat16, device=dev)
+    y2 = torch.empty((0, H), dtype=torch.bfloat16, device=dev)
+    native.decode_mlp_two_passes(x0, k, w13, w2, perm, w13, w2, perm2, act0, y2)
+
     # the layer body on both paths, and the combine alone
     for path in (native.LMOE_PATH_AUTO, native.LMOE_PATH_MFMA):
         out = fused_moe.fused_experts(x0, w0, ids0, w13, w2, l2p, path=path)
