@@ -244,6 +244,8 @@ def test_fused_decode_more_shapes(T, k, E, P, H, I):
     (13, 6, 8, 2048, 768),   # ~10 tokens per slot: groups of 4 and a ragged tail
     (7, 3, 4, 7168, 2048),   # column-split gate_up waves; down rows in groups of 2 pairs
     (9, 2, 3, 768, 4096),    # widest I: one pair per down reduction
+    (40, 8, 16, 2048, 768),  # past 256 pairs: gate_up takes tokens two at a time
+    (35, 8, 11, 1536, 256),  # the same with guarded chunks and odd slot counts (a one-token tail)
 ])
 def test_batched_tokens_equal_one_token_at_a_time(T, k, E, H, I):
     """Slots serving several tokens reduce them in groups; every token's

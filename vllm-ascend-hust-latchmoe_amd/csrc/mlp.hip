@@ -23,8 +23,11 @@ namespace lmoe {
 
 // Several tokens: block (bx, slot s) of the gate_up GEMV, the slot's pairs
 // p0 .. p0 + n - 1 (act rows p0 + r of act).  Each wave holds its row pair's
-// weights in registers and the slot's tokens stream past one at a time.
-template <int NC, bool FULL>
+// weights in registers and the slot's tokens stream past one at a time; with
+// TWO, two at a time (one reduction of four values and one barrier per two
+// tokens; the reduction pairs lanes 32, 16, 8, 4, 2, 1 apart for every
+// value as the two-value one does, so each act value has the same bits).
+template <int NC, bool FULL, bool TWO = false>
 __device__ __forceinline__ void gateup_tokens(const uint16_t* __restrict__ x, int H, int I,
                                               int topk, const uint16_t* __restrict__ w13, int s,
                                               int p0, int n,
@@ -46,7 +49,38 @@ __device__ __forceinline__ void gateup_tokens(const uint16_t* __restrict__ x, in
     wg[c] = load_stream16_g<!FULL>(grow, h, h < H);
     wu[c] = load_stream16_g<!FULL>(urow, h, h < H);
   }
-  for (int r = 0; r < n; ++r) {
+  int r = 0;
+  if constexpr (TWO) {
+    // [step parity][token][wave][gate total, up total]
+    __shared__ __attribute__((aligned(16))) float s_gu2[2][2][4][2];
+    for (int it = 0; r + 1 < n; r += 2, ++it) {
+      const uint16_t* xr0 = x + static_cast<size_t>(sorted_pairs[p0 + r] / topk) * H;
+      const uint16_t* xr1 = x + static_cast<size_t>(sorted_pairs[p0 + r + 1] / topk) * H;
+      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int h = c * 512 + lane * 8;
+        const uint4 xv0 = load16_g<!FULL>(xr0, h, h < H);
+        const uint4 xv1 = load16_g<!FULL>(xr1, h, h < H);
+        v[0] = dot8(xv0, wg[c], v[0]);
+        v[1] = dot8(xv0, wu[c], v[1]);
+        v[2] = dot8(xv1, wg[c], v[2]);
+        v[3] = dot8(xv1, wu[c], v[3]);
+      }
+      // lanes 0..15 end with token r's gate total, 16..31 its up total,
+      // 32..47 and 48..63 token r + 1's
+      const float tot = reduce_scatter<4, 5, 0>(v, lane);
+      if ((lane & 15) == 0) s_gu2[it & 1][lane >> 5][wave][(lane >> 4) & 1] = tot;
+      __syncthreads();
+      if (wave == 0 && lane < 4) {
+        const int tk = lane >> 1;
+        const float4 gu = *reinterpret_cast<const float4*>(&s_gu2[it & 1][tk][2 * (lane & 1)][0]);
+        *reinterpret_cast<uint32_t*>(act + static_cast<size_t>(p0 + r + tk) * I + blockIdx.x * 4 +
+                                     2 * (lane & 1)) = swiglu_bf16x2(gu.x, gu.y, gu.z, gu.w);
+      }
+    }
+  }
+  for (; r < n; ++r) {
     const int t = sorted_pairs[p0 + r] / topk;
     const uint16_t* xr = x + static_cast<size_t>(t) * H;
     float v[2] = {0.0f, 0.0f};
@@ -85,7 +119,7 @@ __device__ __forceinline__ void gateup_tokens(const uint16_t* __restrict__ x, in
 // several tokens per step needs twice the registers, and the lost occupancy
 // costs more than the shorter chain saves: measured slower at B = 4 and 16.)
 // ---------------------------------------------------------------------------
-template <int NC, bool ONE, bool FULL>
+template <int NC, bool ONE, bool FULL, bool TWO = false>
 __global__ __launch_bounds__(256) void gateup_gemv_kernel(
     const uint16_t* __restrict__ x, int H, int I, int topk,
     const uint16_t* __restrict__ w13, const int32_t* __restrict__ offsets,
@@ -123,7 +157,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_kernel(
   const int s = active[a];
   if (s < 0) return;  // uniform over the block
   const int p0 = offsets[s];
-  gateup_tokens<NC, FULL>(x, H, I, topk, w13, s, p0, offsets[s + 1] - p0, sorted_pairs, act);
+  gateup_tokens<NC, FULL, TWO>(x, H, I, topk, w13, s, p0, offsets[s + 1] - p0, sorted_pairs, act);
 }
 
 // Both passes of a decode layer whose working set exceeds its bank (the
@@ -140,7 +174,7 @@ __device__ __forceinline__ int second_rows(int base, int p0, int n, int n_pairs)
   return n < room ? n : room;
 }
 
-template <int NC, bool FULL>
+template <int NC, bool FULL, bool TWO>
 __global__ __launch_bounds__(256) void gateup_gemv_two_kernel(
     const uint16_t* __restrict__ x, int H, int I, int topk, int n_pairs, int max_active_a,
     const uint16_t* __restrict__ w13_a, const int32_t* __restrict__ offsets_a,
@@ -158,7 +192,7 @@ __global__ __launch_bounds__(256) void gateup_gemv_two_kernel(
   int n = offsets[s + 1] - p0;
   if (second) n = second_rows(base, p0, n, n_pairs);  // uniform over the block
   if (n <= 0) return;
-  gateup_tokens<NC, FULL>(x, H, I, topk, second ? w13_b : w13_a, s, p0, n,
+  gateup_tokens<NC, FULL, TWO>(x, H, I, topk, second ? w13_b : w13_a, s, p0, n,
                           second ? sorted_pairs_b : sorted_pairs_a,
                           act + static_cast<size_t>(base) * I);
 }
@@ -571,12 +605,16 @@ __global__ __launch_bounds__(256) void combine_kernel(
 // launch helpers
 // ---------------------------------------------------------------------------
 // one: T == 1 (every slot serves at most one pair; log2phy maps distinct
-// experts to distinct slots).
+// experts to distinct slots).  Past kTwoTokenMinPairs pairs the several-token
+// form takes its tokens two at a time.
+constexpr int kTwoTokenMinPairs = 256;
+
 static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
                               const uint16_t* w13, const int32_t* offsets,
                               const int32_t* sorted_pairs, const int32_t* active,
-                              const int32_t* meta, int max_active, bool one, uint16_t* act,
-                              hipStream_t stream) {
+                              const int32_t* meta, int max_active, bool one, int n_pairs,
+                              uint16_t* act, hipStream_t stream) {
+  const bool two = !one && n_pairs > kTwoTokenMinPairs;
   const int nc = (H + 511) / 512;
   const dim3 g4((I + 3) / 4, max_active);
   // long rows: the column-split kernel.  (For H <= 4096 it measured 3%
@@ -584,19 +622,19 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
   // serve every batch size, so the row-per-wave kernels stay there.)
   const bool cols = nc > 8;
   // rows of exactly NC chunks of 512 columns load without guards
-#define LMOE_GU1(NC, ONE)                                                                      \
-  do {                                                                                         \
-    if (H == (NC)*512)                                                                         \
-      hipLaunchKernelGGL((gateup_gemv_kernel<NC, ONE, true>), g4, dim3(256), 0, stream, x, H,   \
-                         I, topk, w13, offsets, sorted_pairs, active, meta, act);              \
-    else                                                                                       \
-      hipLaunchKernelGGL((gateup_gemv_kernel<NC, ONE, false>), g4, dim3(256), 0, stream, x, H,  \
-                         I, topk, w13, offsets, sorted_pairs, active, meta, act);              \
+#define LMOE_GU0(NC, ONE, FULL, TWO)                                                          \
+  hipLaunchKernelGGL((gateup_gemv_kernel<NC, ONE, FULL, TWO>), g4, dim3(256), 0, stream, x, H, \
+                     I, topk, w13, offsets, sorted_pairs, active, meta, act)
+#define LMOE_GU1(NC, ONE, TWO)                     \
+  do {                                             \
+    if (H == (NC)*512) LMOE_GU0(NC, ONE, true, TWO); \
+    else LMOE_GU0(NC, ONE, false, TWO);            \
   } while (0)
-#define LMOE_GU(NC)              \
-  do {                           \
-    if (one) LMOE_GU1(NC, true); \
-    else LMOE_GU1(NC, false);    \
+#define LMOE_GU(NC)                     \
+  do {                                  \
+    if (one) LMOE_GU1(NC, true, false); \
+    else if (two) LMOE_GU1(NC, false, true); \
+    else LMOE_GU1(NC, false, false);    \
   } while (0)
 #define LMOE_GC(NC, RP, ONE)                                                                 \
   hipLaunchKernelGGL((gateup_gemv_cols_kernel<NC, RP, ONE>), dim3((I + (RP)-1) / (RP),         \
@@ -616,6 +654,7 @@ static int launch_gateup_gemv(const uint16_t* x, int H, int I, int topk,
   else LMOE_GU(8);
 #undef LMOE_GU
 #undef LMOE_GU1
+#undef LMOE_GU0
   return LMOE_OK;
 }
 
@@ -760,8 +799,8 @@ extern "C" int lmoe_gateup_silu(const void* x, int T, int H, int I, int k,
     // of the one token
     st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
                             static_cast<const uint16_t*>(w13_slots), offsets, sorted_pairs,
-                            active, meta, max_active, false, static_cast<uint16_t*>(act),
-                            stream);
+                            active, meta, max_active, false, n_pairs,
+                            static_cast<uint16_t*>(act), stream);
     if (st != LMOE_OK) return st;
     LMOE_RETURN_LAUNCH();
   }
@@ -877,10 +916,15 @@ extern "C" int lmoe_decode_mlp_two_passes(
   const uint16_t* w13b = static_cast<const uint16_t*>(w13_b);
   uint16_t* actb = static_cast<uint16_t*>(act);
   const dim3 g4((I + 3) / 4, max_a + max_b);
-#define LMOE_GU2(NC, FULL)                                                                     \
-  hipLaunchKernelGGL((gateup_gemv_two_kernel<NC, FULL>), g4, dim3(256), 0, stream, xb, H, I, k, \
-                     n_pairs, max_a, w13a, offsets_a, sorted_pairs_a, active_a, meta_a, w13b,   \
+#define LMOE_GU3(NC, FULL, TWO)                                                                \
+  hipLaunchKernelGGL((gateup_gemv_two_kernel<NC, FULL, TWO>), g4, dim3(256), 0, stream, xb, H, I, \
+                     k, n_pairs, max_a, w13a, offsets_a, sorted_pairs_a, active_a, meta_a, w13b,    \
                      offsets_b, sorted_pairs_b, active_b, actb)
+#define LMOE_GU2(NC, FULL)                                   \
+  do {                                                       \
+    if (n_pairs > kTwoTokenMinPairs) LMOE_GU3(NC, FULL, true); \
+    else LMOE_GU3(NC, FULL, false);                          \
+  } while (0)
 #define LMOE_GU2N(NC)                     \
   do {                                    \
     if (H == (NC)*512) LMOE_GU2(NC, true); \
@@ -891,6 +935,7 @@ extern "C" int lmoe_decode_mlp_two_passes(
   else LMOE_GU2N(8);
 #undef LMOE_GU2N
 #undef LMOE_GU2
+#undef LMOE_GU3
   const uint16_t* w2a = static_cast<const uint16_t*>(w2_a);
   const uint16_t* w2b = static_cast<const uint16_t*>(w2_b);
   uint16_t* yb = static_cast<uint16_t*>(y);
@@ -1004,7 +1049,7 @@ extern "C" int lmoe_fused_moe_decode(const void* x, int T, int H, int I, int k,
   const bool one = T == 1 && distinct_slots != 0;
   int st = launch_gateup_gemv(static_cast<const uint16_t*>(x), H, I, k,
                               static_cast<const uint16_t*>(w13_slots), offsets,
-                              sorted_pairs, active, meta, max_active, one,
+                              sorted_pairs, active, meta, max_active, one, n_pairs,
                               static_cast<uint16_t*>(act), stream);
   if (st != LMOE_OK) return st;
   if (y != nullptr && T > 1 && n_pairs > 16) {
